@@ -1,0 +1,222 @@
+"""Benchmark: SparseAttention forward tokens/s on one MI355X.
+
+Workload (default): bf16 GQA SparseAttention, d_model=4096, 32 query heads /
+8 kv heads (d_head=128), batch 1, N=4096, K=128, window 16, 2 global tokens,
+8 hash rounds, causal.  Weights: seeded construction, Wq/Wk/Wv/Wo re-drawn
+with xavier_uniform_ in that order, parameters cast to bf16 (the hyperplanes
+stay fp32); x = 0.02 * N(0, 1) in bf16 from a generator seeded 1000.
+
+One "step" = one SparseAttention.forward (projections, graph build, gather
+attention, output projection) on inputs already resident in HBM.
+
+Also reported:
+* roofline of the gather-attention kernel: algorithmic bytes per launch
+  B*H*N*(2*K_out*d + 2*d)*2 (K and V row gathers, q read, out write) over the
+  kernel's average duration measured with events on the launch stream;
+* recall@32 of the graph against exact dense top-32 (head 0 and all heads);
+* cpu_baseline: the reference's torch op sequence (oracle/torch_port.py) on
+  the host cores, on one kv-head group (4 of 32 query heads) of the same
+  workload, scaled to whole-workload tokens/s.
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+import warnings
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_HBM = 8.0e12
+
+
+def build_module(dev):
+    import torch
+    from ssa_amd import SSAConfig, SparseAttention
+    cfg = SSAConfig(d_model=4096, num_heads=32, num_kv_heads=8, num_neighbors=128,
+                    window_size=16, num_global_tokens=2, num_hash_rounds=8, max_num_hashes=12,
+                    lsh_num_probes=0, causal=True)
+    torch.manual_seed(0)
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")
+        attn = SparseAttention(cfg)
+    for W in (attn.Wq, attn.Wk, attn.Wv, attn.Wo):
+        torch.nn.init.xavier_uniform_(W.weight)
+    attn = attn.to(dev)
+    for p in attn.parameters():
+        p.data = p.data.to(torch.bfloat16)
+    attn.eval()
+    g = torch.Generator().manual_seed(1000)
+    x = (torch.randn(1, 4096, 4096, generator=g) * 0.02).to(torch.bfloat16).to(dev)
+    return cfg, attn, x
+
+
+def recall_at_32(q, k, nb, va, rep, causal_variant=False):
+    """Reference method (tests/test_quality_and_scaling.py:80-95): dense unscaled
+    top-32 per query vs the valid neighbours; returns (head 0, all-head mean)."""
+    import torch
+    B, H, N, d = q.shape
+    res = []
+    for h in range(H):
+        qs = q[0, h].float()
+        ks = k[0, h // rep].float()
+        s = qs @ ks.T
+        if causal_variant:
+            s = s.masked_fill(torch.ones_like(s, dtype=torch.bool).triu(1), float("-inf"))
+        top = s.topk(32, dim=-1).indices
+        hit = ((nb[0, h].unsqueeze(-1) == top.unsqueeze(1)) & va[0, h].unsqueeze(-1)).any(1)
+        if causal_variant:
+            tk = torch.clamp(torch.arange(N, device=q.device) + 1, max=32).float()
+            valid_top = torch.isfinite(torch.gather(s, 1, top))
+            r = (hit & valid_top).sum(-1).float() / tk
+        else:
+            r = hit.sum(-1).float() / 32.0
+        res.append(r.mean().item())
+    return res[0], sum(res) / len(res)
+
+
+def cpu_baseline(attn_gpu):
+    """Time the reference's CPU op sequence on one kv group of the workload."""
+    import torch
+    from oracle import torch_port
+    cfg = attn_gpu.config
+    nthreads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    torch.set_num_threads(nthreads)
+    rep = attn_gpu.kv_rep
+    d = attn_gpu.d_head
+    Wq = attn_gpu.Wq.weight[: rep * d].detach().cpu()
+    Wk = attn_gpu.Wk.weight[:d].detach().cpu()
+    Wv = attn_gpu.Wv.weight[:d].detach().cpu()
+    Wo = attn_gpu.Wo.weight[:, : rep * d].detach().cpu()
+    rp = attn_gpu.lsh_builder.rand_proj.detach().cpu()
+    g = torch.Generator().manual_seed(1000)
+    x = (torch.randn(1, 4096, 4096, generator=g) * 0.02).to(torch.bfloat16)
+    kw = dict(H=rep, n_kv=1, K=cfg.num_neighbors, window=cfg.window_size,
+              glob_n=cfg.num_global_tokens, R=cfg.num_hash_rounds, max_p=cfg.max_num_hashes,
+              T=cfg.lsh_num_probes, causal=cfg.causal)
+    times = []
+    for i in range(2):
+        t0 = time.perf_counter()
+        with torch.no_grad():
+            torch_port.forward(x, Wq, Wk, Wv, Wo, rp, **kw)
+        times.append(time.perf_counter() - t0)
+        print(f"# cpu sample run {i}: {times[-1]:.2f} s", file=sys.stderr, flush=True)
+    t = min(times[1:]) if len(times) > 1 else times[0]
+    groups = cfg.num_heads // rep
+    tok_s = 4096 / (t * groups)
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": tok_s, "unit": "tokens/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"1 of {groups} kv-head groups ({rep} query heads, 1 kv head) of the same "
+                      f"workload through the reference's torch CPU op sequence "
+                      f"(oracle/torch_port.py), {t:.2f} s, scaled x{groups}; "
+                      f"1 warm-up + 1 timed run; CPU: {model}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-recall", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the sparse forward shards by kv-head group with no exchange inside attention; "
+              "see the sharding note of the design document).", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    dev = "cuda:0"
+    cfg, attn, x = build_module(dev)
+    B, N = x.shape[0], x.shape[1]
+    H, d, K = attn.H, attn.d_head, attn.K
+    print("# workload built", file=sys.stderr, flush=True)
+
+    with torch.no_grad():
+        for _ in range(args.warmup):
+            attn(x)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            attn(x)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+    ms = (t1 - t0) * 1000.0 / args.steps
+    value = B * N / ((t1 - t0) / args.steps)
+    print(f"# forward {ms:.3f} ms/step", file=sys.stderr, flush=True)
+
+    # per-stage timing with events on the launch stream (torch's current stream)
+    with torch.no_grad():
+        q = attn._split_q(attn.Wq(x))
+        k = attn._split_kv_compact(attn.Wk(x))
+        v = attn._split_kv_compact(attn.Wv(x))
+        st = torch.cuda.current_stream()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+        reps = max(args.steps, 10)
+        ev[0].record(st)
+        for _ in range(reps):
+            nb, va = attn.build_graph(q, k, N, N, B, x.device, True, False)
+        ev[1].record(st)
+        ev[2].record(st)
+        for _ in range(reps):
+            out = attn.apply_graph(q, k, v, nb, va)
+        ev[3].record(st)
+        torch.cuda.synchronize()
+    t_build = ev[0].elapsed_time(ev[1]) / reps
+    t_apply = ev[2].elapsed_time(ev[3]) / reps
+    K_out = nb.shape[-1]
+    bytes_apply = B * H * N * (2 * K_out * d + 2 * d) * 2
+    achieved = bytes_apply / (t_apply / 1000.0)
+    traffic = None
+    tf = os.path.join(ROOT, "profiles", "apply_traffic_bf16_gqa_n4096.json")
+    if os.path.exists(tf):
+        with open(tf) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+    print(f"# build {t_build:.3f} ms, apply {t_apply:.3f} ms", file=sys.stderr, flush=True)
+
+    rec = None
+    if not args.no_recall:
+        with torch.no_grad():
+            r0, rall = recall_at_32(q, k, nb, va, attn.kv_rep)
+            c0, call = recall_at_32(q, k, nb, va, attn.kv_rep, causal_variant=True)
+        rec = {"head0": r0, "all_heads": rall, "causal_head0": c0, "causal_all_heads": call}
+
+    line = {
+        "metric": "sparse-attn fwd tokens/sec at N=4096,K=128; % HBM roofline; recall@32",
+        "value": value, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "SparseAttention bf16 GQA forward, d_model=4096, 32 q heads / "
+                               "8 kv heads (d_head=128), B=1, N=4096, K=128, window=16, "
+                               "2 global tokens, R=8, causal",
+                   "global_batch": B, "seq_len": N, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": achieved / 1e9, "peak": PEAK_HBM / 1e9,
+                     "unit": "GB/s", "frac": achieved / PEAK_HBM, "traffic": traffic,
+                     "kernel": "apply_fwd_kernel", "bytes_per_launch": bytes_apply,
+                     "ms_per_launch": t_apply},
+        "t_build_ms": t_build, "t_apply_ms": t_apply, "k_out": K_out,
+        "recall_at_32": rec,
+    }
+    if not args.no_cpu:
+        cb = cpu_baseline(attn)
+        line["cpu_baseline"] = cb
+        line["speedup_vs_cpu"] = value / cb["value"]
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,176 @@
+/*
+ * ssa_amd.h -- C ABI of the MI355X (gfx950) SparseAttention forward hot path.
+ *
+ * One shared library, libssa_amd.so, exports the functions below.  Every entry
+ * point takes plain pointers, element strides and sizes; nothing here knows
+ * about torch.  Device pointers are HIP device addresses; `stream` is a
+ * hipStream_t passed as void* (NULL = the default stream).  All work is
+ * enqueued on `stream`; no entry point synchronises the host, allocates device
+ * memory or frees caller memory.  Callers own every buffer (inputs, outputs,
+ * workspace).  Every function returns 0 on success and a negative SSA_E_*
+ * code otherwise; ssa_last_error() returns a message for the calling thread's
+ * last failure.
+ *
+ * The entry points replace the reference's Python functions (daedalus/SSA,
+ * sparse_attention.py) cited on each declaration.
+ */
+#ifndef SSA_AMD_H
+#define SSA_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element types of q / k / v / out */
+#define SSA_F32  0
+#define SSA_BF16 1
+#define SSA_F16  2
+
+/* status codes */
+#define SSA_OK          0
+#define SSA_E_ARG      -1   /* invalid argument (shape, stride, dtype)        */
+#define SSA_E_UNSUP    -2   /* unsupported size (head dim, bucket bits, ...)  */
+#define SSA_E_WORKSPACE -3  /* workspace too small                           */
+#define SSA_E_HIP      -4   /* a HIP runtime call failed                      */
+
+/* A (B, Hx, L, d) tensor view with the last dimension contiguous.  Strides are
+ * in elements.  Head h of a query tensor reads kv head h / (Hq / Hkv). */
+typedef struct {
+    const void *ptr;
+    int32_t dtype;           /* SSA_F32 / SSA_BF16 / SSA_F16 */
+    int64_t sb, sh, sn;      /* strides of B, head, position */
+} ssa_tensor4;
+
+/* ---------------------------------------------------------------------------
+ * Neighbor-graph build.
+ *
+ * mode SSA_GRAPH_FULL replaces SparseAttention.build_graph
+ *   (sparse_attention.py:1325-1390: window + global + LSH + self, merged by
+ *   merge_neighbors :966-1089).  Outputs neighbors (B,Hq,N,k_out) int64 and
+ *   valid (B,Hq,N,k_out) uint8 with k_out = ssa_graph_out_width().
+ * mode SSA_GRAPH_LSH replaces LSHGraphBuilder.forward
+ *   (sparse_attention.py:814-959).  Outputs lsh_idx (B,Hq,N,kk) int64,
+ *   kk = min(top_k, R*(1+min(T,P))*C), ordered by descending score; slots
+ *   without a candidate hold glob[t] (t < G) or 0, as the reference does.
+ *
+ * k may be the un-expanded (B, Hkv, M, d) tensor: query head h uses kv head
+ * h / (Hq / Hkv).  Passing an already expanded k (Hkv = Hq) is also valid.
+ * --------------------------------------------------------------------------- */
+#define SSA_GRAPH_FULL 0
+#define SSA_GRAPH_LSH  1
+
+typedef struct {
+    int32_t mode;            /* SSA_GRAPH_FULL / SSA_GRAPH_LSH                       */
+    int32_t B, Hq, Hkv;      /* batch, query heads, kv heads (Hq % Hkv == 0)         */
+    int32_t N, M, d;         /* query length, key length, head dim                   */
+    ssa_tensor4 q;           /* (B, Hq, N, d)                                        */
+    ssa_tensor4 k;           /* (B, Hkv, M, d)                                       */
+    const float *rand_proj;  /* (R, max_p, d) fp32 hyperplanes, contiguous           */
+    int32_t R, max_p;        /* rounds, planes registered per round                  */
+    int32_t P;               /* effective planes this call (1..12)                   */
+    int32_t T;               /* requested probes (clamped to P internally)            */
+    int32_t C;               /* candidates per bucket list (lsh_candidates)          */
+    int32_t top_k;           /* LSH top-k (lsh_k)                                    */
+    int32_t window;          /* window half width w (FULL, self-attention only)      */
+    int32_t causal;          /* future candidates -> self, causal window             */
+    int32_t is_cross;        /* cross-attention: no window, no self slot             */
+    int32_t total_k;         /* num_neighbors K (FULL)                               */
+    const int64_t *glob;     /* (G,) global key ids, already clamped to [0, M-1]     */
+    int32_t G;
+    /* Optional injected fp32 projections (parity testing):                          */
+    const float *q_proj;     /* (B*Hq, R, N, P) or NULL                              */
+    const float *k_proj;     /* (B*Hkv, R, M, P) or NULL                             */
+    /* outputs */
+    int64_t *out_idx;        /* FULL: neighbors (B,Hq,N,k_out); LSH: (B,Hq,N,kk)     */
+    uint8_t *out_valid;      /* FULL: (B,Hq,N,k_out); LSH: unused (may be NULL)      */
+    int32_t *out_ties;       /* optional single counter: queries whose k-th LSH score */
+                             /* is tied (selection resolved by stream order)          */
+} ssa_graph_args;
+
+/* Output width of the FULL graph: self-attention 1 + min(K-1, 2w+1+G+kk),
+ * cross-attention min(K, G+kk) (sparse_attention.py:1062-1072). */
+int64_t ssa_graph_out_width(const ssa_graph_args *a);
+
+/* Bytes of device workspace ssa_build_graph needs for these arguments. */
+int64_t ssa_graph_workspace_bytes(const ssa_graph_args *a);
+
+/* Replaces SparseAttention.build_graph (:1325-1390) and, in SSA_GRAPH_LSH
+ * mode, LSHGraphBuilder.forward (:814-959). */
+int ssa_build_graph(const ssa_graph_args *a, void *workspace, int64_t workspace_bytes,
+                    void *stream);
+
+/* ---------------------------------------------------------------------------
+ * Bucket permutation: for each of `rows` rows of `n` bucket ids (uint16, values
+ * < 2^P), the permutation torch.sort(ids, dim=-1) returns on the CPU (an
+ * unstable introsort; sparse_attention.py:781), plus bucket start / size
+ * tables (:785-792).  Bucket starts of empty buckets hold the next bucket's
+ * start.  Exposed for testing the sort stage on its own.
+ * --------------------------------------------------------------------------- */
+int64_t ssa_bucket_sort_workspace_bytes(int32_t rows, int32_t n);
+int ssa_bucket_sort(const uint16_t *ids, int32_t rows, int32_t n, int32_t P,
+                    int32_t *perm, int32_t *bstart, int32_t *bsize,
+                    void *workspace, int64_t workspace_bytes, void *stream);
+
+/* ---------------------------------------------------------------------------
+ * Merge of arbitrary window / global / LSH index lists.
+ * Replaces merge_neighbors (sparse_attention.py:966-1089).
+ *   win (N, Kw) int64 contiguous (Kw may be 0), glob (G,), lsh (BH, N, Kl)
+ *   contiguous.  has_self: self-attention (slot 0 = n, n removed from pool).
+ *   Outputs (BH, N, k_out) int64 + uint8 valid, k_out = has_self ?
+ *   1 + min(K-1, Kw+G+Kl) : min(K, Kw+G+Kl).  workspace: 16 bytes.
+ * --------------------------------------------------------------------------- */
+int ssa_merge_neighbors(const int64_t *win, int32_t Kw, const int64_t *glob, int32_t G,
+                        const int64_t *lsh, int32_t Kl, int32_t BH, int32_t N,
+                        int32_t has_self, int32_t total_k, int64_t *out, uint8_t *valid,
+                        void *workspace, void *stream);
+
+/* ---------------------------------------------------------------------------
+ * Gather attention.  Replaces sparse_gather_attention
+ * (sparse_attention.py:1096-1199).
+ *   q (B,Hq,N,d), k/v (B,Hkv,M,d) views; neighbors (B,Hq,N,K) int64 and
+ *   valid (B,Hq,N,K) uint8 (or NULL = all valid), both contiguous.
+ *   out: (B,Hq,N,d) in q's dtype written through the given strides.
+ *   scores = fp32(q.k) * scale, masked to -inf where !valid, fp32 softmax;
+ *   16-bit models round p to the value dtype before P.V unless fp32_weights;
+ *   P.V accumulates in fp32 and rounds once.
+ *   dropout_p > 0 applies inverted dropout to p with a counter-based hash of
+ *   (seed, query row, slot).
+ * --------------------------------------------------------------------------- */
+typedef struct {
+    int32_t B, Hq, Hkv, N, M, d, K;
+    ssa_tensor4 q, k, v;
+    const int64_t *neighbors;
+    const uint8_t *valid;
+    float scale;
+    int32_t fp32_weights;
+    float dropout_p;
+    uint64_t seed;
+    void *out;               /* dtype of q */
+    int64_t out_sb, out_sh, out_sn;
+} ssa_apply_args;
+
+int ssa_sparse_gather_attention(const ssa_apply_args *a, void *stream);
+
+/* Backward of ssa_sparse_gather_attention (the graph is not differentiable,
+ * sparse_attention.py:157-159): given dout (B,Hq,N,d) contiguous fp32 (the
+ * upstream gradient), writes dq (B,Hq,N,d) fp32 and ACCUMULATES dk, dv
+ * (B,Hkv,M,d) fp32 (the caller zeroes them).  Uses the same dropout seed. */
+typedef struct {
+    ssa_apply_args fwd;
+    const float *dout;
+    float *dq, *dk, *dv;
+} ssa_apply_bwd_args;
+
+int ssa_sparse_gather_attention_bwd(const ssa_apply_bwd_args *a, void *stream);
+
+/* Library identification and error text. */
+const char *ssa_version(void);
+const char *ssa_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SSA_AMD_H */

@@ -1,0 +1,278 @@
+"""ctypes binding of libssa_amd.so (the C ABI declared in include/ssa_amd.h).
+
+torch is imported first so that the HIP runtime torch ships
+(libamdhip64.so.7) is the one the library binds to: device pointers and
+stream handles then come from the same runtime instance.
+
+Every wrapper raises RuntimeError when the library is missing or a call
+fails; there is no CPU or torch fallback for the hot path.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libssa_amd.so")
+
+SSA_F32, SSA_BF16, SSA_F16 = 0, 1, 2
+GRAPH_FULL, GRAPH_LSH = 0, 1
+
+_DTYPES = {torch.float32: SSA_F32, torch.bfloat16: SSA_BF16, torch.float16: SSA_F16}
+
+c_i32 = ctypes.c_int32
+c_i64 = ctypes.c_int64
+c_vp = ctypes.c_void_p
+
+
+class Tensor4(ctypes.Structure):
+    _fields_ = [("ptr", c_vp), ("dtype", c_i32), ("sb", c_i64), ("sh", c_i64), ("sn", c_i64)]
+
+
+class GraphArgs(ctypes.Structure):
+    _fields_ = [
+        ("mode", c_i32), ("B", c_i32), ("Hq", c_i32), ("Hkv", c_i32),
+        ("N", c_i32), ("M", c_i32), ("d", c_i32),
+        ("q", Tensor4), ("k", Tensor4),
+        ("rand_proj", c_vp), ("R", c_i32), ("max_p", c_i32), ("P", c_i32), ("T", c_i32),
+        ("C", c_i32), ("top_k", c_i32), ("window", c_i32), ("causal", c_i32),
+        ("is_cross", c_i32), ("total_k", c_i32),
+        ("glob", c_vp), ("G", c_i32),
+        ("q_proj", c_vp), ("k_proj", c_vp),
+        ("out_idx", c_vp), ("out_valid", c_vp), ("out_ties", c_vp),
+    ]
+
+
+class ApplyArgs(ctypes.Structure):
+    _fields_ = [
+        ("B", c_i32), ("Hq", c_i32), ("Hkv", c_i32), ("N", c_i32), ("M", c_i32), ("d", c_i32),
+        ("K", c_i32),
+        ("q", Tensor4), ("k", Tensor4), ("v", Tensor4),
+        ("neighbors", c_vp), ("valid", c_vp),
+        ("scale", ctypes.c_float), ("fp32_weights", c_i32), ("dropout_p", ctypes.c_float),
+        ("seed", ctypes.c_uint64),
+        ("out", c_vp), ("out_sb", c_i64), ("out_sh", c_i64), ("out_sn", c_i64),
+    ]
+
+
+class ApplyBwdArgs(ctypes.Structure):
+    _fields_ = [("fwd", ApplyArgs), ("dout", c_vp), ("dq", c_vp), ("dk", c_vp), ("dv", c_vp)]
+
+
+_lib = None
+
+
+def lib():
+    """Load libssa_amd.so once; raise if it is not built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"ssa_amd: {LIB_PATH} is not built; run `make -C ssa_amd/csrc` "
+                "(or __graft_entry__.build()).  There is no fallback path.")
+        L = ctypes.CDLL(LIB_PATH)
+        L.ssa_version.restype = ctypes.c_char_p
+        L.ssa_last_error.restype = ctypes.c_char_p
+        L.ssa_graph_out_width.restype = c_i64
+        L.ssa_graph_out_width.argtypes = [ctypes.POINTER(GraphArgs)]
+        L.ssa_graph_workspace_bytes.restype = c_i64
+        L.ssa_graph_workspace_bytes.argtypes = [ctypes.POINTER(GraphArgs)]
+        L.ssa_build_graph.restype = ctypes.c_int
+        L.ssa_build_graph.argtypes = [ctypes.POINTER(GraphArgs), c_vp, c_i64, c_vp]
+        L.ssa_bucket_sort_workspace_bytes.restype = c_i64
+        L.ssa_bucket_sort_workspace_bytes.argtypes = [c_i32, c_i32]
+        L.ssa_bucket_sort.restype = ctypes.c_int
+        L.ssa_bucket_sort.argtypes = [c_vp, c_i32, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp, c_i64,
+                                      c_vp]
+        L.ssa_merge_neighbors.restype = ctypes.c_int
+        L.ssa_merge_neighbors.argtypes = [c_vp, c_i32, c_vp, c_i32, c_vp, c_i32, c_i32, c_i32,
+                                          c_i32, c_i32, c_vp, c_vp, c_vp, c_vp]
+        L.ssa_sparse_gather_attention.restype = ctypes.c_int
+        L.ssa_sparse_gather_attention.argtypes = [ctypes.POINTER(ApplyArgs), c_vp]
+        L.ssa_sparse_gather_attention_bwd.restype = ctypes.c_int
+        L.ssa_sparse_gather_attention_bwd.argtypes = [ctypes.POINTER(ApplyBwdArgs), c_vp]
+        _lib = L
+    return _lib
+
+
+def version() -> str:
+    return lib().ssa_version().decode()
+
+
+def _check(rc: int, what: str):
+    if rc != 0:
+        msg = lib().ssa_last_error().decode()
+        raise RuntimeError(f"ssa_amd.{what} failed ({rc}): {msg}")
+
+
+def require_device(*tensors):
+    for t in tensors:
+        if t is not None and t.device.type != "cuda":
+            raise RuntimeError(
+                "ssa_amd runs the SparseAttention hot path on ROCm devices only "
+                f"(got a tensor on {t.device}); move the module and inputs to 'cuda'.")
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    try:
+        return _DTYPES[dt]
+    except KeyError:
+        raise RuntimeError(f"ssa_amd: dtype {dt} unsupported (float32, bfloat16, float16)")
+
+
+def view4(t: torch.Tensor):
+    """(B, H, L, d) tensor -> (Tensor4, keep-alive tensor) with a unit last stride."""
+    if t.dim() != 4:
+        raise RuntimeError(f"ssa_amd: expected a 4-D (B, H, L, d) tensor, got {tuple(t.shape)}")
+    if t.stride(-1) != 1:
+        t = t.contiguous()
+    sb, sh, sn, _ = t.stride()
+    return Tensor4(t.data_ptr(), dtype_code(t.dtype), sb, sh, sn), t
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+# --------------------------------------------------------------------------- graph build
+def build_graph(q, k, rand_proj, *, P, T, C, top_k, window, causal, is_cross, total_k, glob,
+                mode=GRAPH_FULL, q_proj=None, k_proj=None, count_ties=False):
+    """Run ssa_build_graph.  q (B,Hq,N,d), k (B,Hkv,M,d) views on one device.
+
+    Returns (out_idx, out_valid or None, ties or None)."""
+    require_device(q, k, rand_proj, glob)
+    B, Hq, N, d = q.shape
+    Bk, Hkv, M, dk = k.shape
+    if Bk != B or dk != d:
+        raise RuntimeError(f"ssa_amd.build_graph: q {tuple(q.shape)} / k {tuple(k.shape)} mismatch")
+    if q.dtype != k.dtype:
+        raise RuntimeError("ssa_amd.build_graph: q and k dtypes differ")
+    qa, qk = view4(q)
+    ka, kk_ = view4(k)
+    rp = rand_proj.detach().to(torch.float32).contiguous()
+    g = glob.detach().to(device=q.device, dtype=torch.int64).contiguous()
+    qp = q_proj.detach().to(torch.float32).contiguous() if q_proj is not None else None
+    kp = k_proj.detach().to(torch.float32).contiguous() if k_proj is not None else None
+    a = GraphArgs()
+    a.mode = mode
+    a.B, a.Hq, a.Hkv, a.N, a.M, a.d = B, Hq, Hkv, N, M, d
+    a.q, a.k = qa, ka
+    a.rand_proj = rp.data_ptr()
+    a.R, a.max_p = rp.shape[0], rp.shape[1]
+    a.P, a.T, a.C, a.top_k = P, T, C, top_k
+    a.window, a.causal, a.is_cross, a.total_k = window, int(causal), int(is_cross), total_k
+    a.glob, a.G = (g.data_ptr() if g.numel() else None), g.numel()
+    a.q_proj, a.k_proj = _ptr(qp), _ptr(kp)
+    L = lib()
+    width = L.ssa_graph_out_width(ctypes.byref(a))
+    if width < 0:
+        _check(-1, "build_graph")
+    wsb = L.ssa_graph_workspace_bytes(ctypes.byref(a))
+    if wsb < 0:
+        _check(-1, "build_graph")
+    out = torch.empty((B, Hq, N, width), dtype=torch.int64, device=q.device)
+    valid = (torch.empty((B, Hq, N, width), dtype=torch.bool, device=q.device)
+             if mode == GRAPH_FULL else None)
+    ties = torch.zeros(1, dtype=torch.int32, device=q.device) if count_ties else None
+    ws = torch.empty(max(int(wsb), 1), dtype=torch.uint8, device=q.device)
+    a.out_idx, a.out_valid, a.out_ties = out.data_ptr(), _ptr(valid), _ptr(ties)
+    _check(L.ssa_build_graph(ctypes.byref(a), ws.data_ptr(), int(wsb), _stream(q)), "build_graph")
+    # keep inputs alive until the stream has consumed them
+    _keep = (qk, kk_, rp, g, qp, kp, ws)
+    del _keep
+    return out, valid, ties
+
+
+def bucket_sort(ids: torch.Tensor, P: int):
+    """ssa_bucket_sort on (rows, n) uint16-valued ids -> (perm int32, bstart, bsize)."""
+    require_device(ids)
+    ids16 = ids.to(torch.int32).to(torch.int16).contiguous()   # same bits as uint16 for < 2^15
+    rows, n = ids16.shape
+    perm = torch.empty((rows, n), dtype=torch.int32, device=ids.device)
+    bstart = torch.empty((rows, 1 << P), dtype=torch.int32, device=ids.device)
+    bsize = torch.empty((rows, 1 << P), dtype=torch.int32, device=ids.device)
+    L = lib()
+    wsb = max(int(L.ssa_bucket_sort_workspace_bytes(rows, n)), 1)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=ids.device)
+    _check(L.ssa_bucket_sort(ids16.data_ptr(), rows, n, P, perm.data_ptr(), bstart.data_ptr(),
+                             bsize.data_ptr(), ws.data_ptr(), wsb, _stream(ids)), "bucket_sort")
+    return perm, bstart, bsize
+
+
+def merge_neighbors(win, glob, lsh, has_self: bool, total_k: int):
+    require_device(win, glob, lsh)
+    B, H, N, Kl = lsh.shape
+    w = win.to(torch.int64).contiguous()
+    Kw = w.shape[1] if w.dim() == 2 else 0
+    g = glob.to(torch.int64).contiguous()
+    l = lsh.to(torch.int64).contiguous()
+    Kall = Kw + g.numel() + Kl
+    ks = min(total_k - 1, Kall) if has_self else min(total_k, Kall)
+    Kout = (1 if has_self else 0) + ks
+    out = torch.empty((B, H, N, Kout), dtype=torch.int64, device=lsh.device)
+    valid = torch.empty((B, H, N, Kout), dtype=torch.bool, device=lsh.device)
+    ws = torch.empty(16, dtype=torch.uint8, device=lsh.device)
+    _check(lib().ssa_merge_neighbors(
+        _ptr(w) if Kw else None, Kw, _ptr(g) if g.numel() else None, g.numel(),
+        _ptr(l) if Kl else None, Kl, B * H, N, int(has_self), total_k, out.data_ptr(),
+        valid.data_ptr(), ws.data_ptr(), _stream(lsh)), "merge_neighbors")
+    return out, valid
+
+
+# --------------------------------------------------------------------------- apply
+def _apply_args(q, k, v, neighbors, valid, scale, fp32w, dropout_p, seed, out):
+    B, Hq, N, d = q.shape
+    _, Hkv, M, _ = k.shape
+    K = neighbors.shape[-1]
+    qa, qk = view4(q)
+    ka, kk_ = view4(k)
+    va, vk = view4(v)
+    nb = neighbors.to(torch.int64).contiguous()
+    vl = valid.to(torch.bool).contiguous() if valid is not None else None
+    a = ApplyArgs()
+    a.B, a.Hq, a.Hkv, a.N, a.M, a.d, a.K = B, Hq, Hkv, N, M, d, K
+    a.q, a.k, a.v = qa, ka, va
+    a.neighbors, a.valid = nb.data_ptr(), _ptr(vl)
+    a.scale, a.fp32_weights, a.dropout_p, a.seed = float(scale), int(fp32w), float(dropout_p), seed
+    a.out = out.data_ptr()
+    a.out_sb, a.out_sh, a.out_sn = out.stride(0), out.stride(1), out.stride(2)
+    return a, (qk, kk_, vk, nb, vl)
+
+
+def gather_attention_fwd(q, k, v, neighbors, valid, scale, fp32w=False, dropout_p=0.0, seed=0,
+                         out=None):
+    require_device(q, k, v, neighbors, valid)
+    if not (q.dtype == k.dtype == v.dtype):
+        raise RuntimeError("ssa_amd.sparse_gather_attention: q, k, v dtypes differ")
+    if out is None:
+        B, Hq, N, d = q.shape
+        out = torch.empty((B, N, Hq, d), dtype=q.dtype, device=q.device).transpose(1, 2)
+    a, keep = _apply_args(q, k, v, neighbors, valid, scale, fp32w, dropout_p, seed, out)
+    _check(lib().ssa_sparse_gather_attention(ctypes.byref(a), _stream(q)),
+           "sparse_gather_attention")
+    del keep
+    return out
+
+
+def gather_attention_bwd(q, k, v, neighbors, valid, scale, fp32w, dropout_p, seed, dout):
+    B, Hq, N, d = q.shape
+    _, Hkv, M, _ = k.shape
+    do = dout.to(torch.float32).contiguous()
+    dq = torch.empty((B, Hq, N, d), dtype=torch.float32, device=q.device)
+    dk = torch.zeros((B, Hkv, M, d), dtype=torch.float32, device=q.device)
+    dv = torch.zeros((B, Hkv, M, d), dtype=torch.float32, device=q.device)
+    dummy = torch.empty((B, N, Hq, d), dtype=q.dtype, device=q.device).transpose(1, 2)
+    a, keep = _apply_args(q, k, v, neighbors, valid, scale, fp32w, dropout_p, seed, dummy)
+    b = ApplyBwdArgs()
+    b.fwd = a
+    b.dout, b.dq, b.dk, b.dv = do.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr()
+    _check(lib().ssa_sparse_gather_attention_bwd(ctypes.byref(b), _stream(q)),
+           "sparse_gather_attention_bwd")
+    del keep
+    return dq, dk, dv

@@ -1,0 +1,413 @@
+// ssa_apply.hip -- gather attention over a fixed neighbor graph (gfx950).
+//
+// Replaces sparse_gather_attention (sparse_attention.py:1096-1199).
+//
+// One wavefront per query row (b, h, n).  A row of d elements is covered by
+// LPR lanes with 16-byte loads, so one load instruction brings RPI = 64/LPR
+// whole K (or V) rows; with U rows in flight per lane the wave keeps
+// U*RPI*row_bytes of gathers outstanding.  Scores go to LDS (K floats per
+// wave), the fp32 softmax is a wave reduction, and P.V accumulates in fp32
+// registers, reduced across the RPI row groups at the end.
+//
+// Numerics follow the reference: s = fp32(q.k) * fp32(scale); -inf where
+// !valid; p = exp(s - max) / sum in fp32; 16-bit models round p to the value
+// dtype before P.V (fp32_attn_weights keeps it fp32); P.V accumulates in fp32
+// and is rounded once to the output dtype.
+#include "ssa_common.h"
+
+namespace {
+
+struct ApplyP {
+    int32_t B, Hq, Hkv, N, M, K, rep;
+    const void *q, *k, *v;
+    int64_t qsb, qsh, qsn, ksb, ksh, ksn, vsb, vsh, vsn;
+    const int64_t *nb;
+    const uint8_t *valid;
+    float scale;
+    int32_t fp32w;
+    float drop_p;
+    float drop_scale;
+    uint64_t seed;
+    void *out;
+    int64_t osb, osh, osn;
+    int64_t rows;          // B*Hq*N
+    int64_t nblocks;       // logical blocks
+    // backward
+    const float *dout;
+    float *dq, *dk, *dv;
+};
+
+constexpr int WAVES = 4;   // waves per workgroup
+
+template <typename T> struct VecOf;
+template <> struct VecOf<float> { static constexpr int n = 4; };
+template <> struct VecOf<bf16_t> { static constexpr int n = 8; };
+template <> struct VecOf<f16_t> { static constexpr int n = 8; };
+
+template <typename T, int D> struct Geo {
+    static constexpr int VEC = (VecOf<T>::n < D) ? VecOf<T>::n : D;   // elements per lane
+    static constexpr int LPR = D / VEC;                                // lanes per row
+    static constexpr int RPI = SSA_WAVE / LPR;                         // rows per wave load
+    static_assert(D % VEC == 0, "head dim must be a multiple of the vector width");
+    static_assert(LPR <= SSA_WAVE, "row wider than a wave");
+};
+
+template <typename T, int VEC>
+__device__ __forceinline__ void load_vec(const T *p, float (&f)[VEC]) {
+    if constexpr (sizeof(T) * VEC == 16) {
+        uint4 u = *reinterpret_cast<const uint4 *>(p);
+        const T *e = reinterpret_cast<const T *>(&u);
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) f[i] = to_f32(e[i]);
+    } else if constexpr (sizeof(T) * VEC == 8) {
+        uint2 u = *reinterpret_cast<const uint2 *>(p);
+        const T *e = reinterpret_cast<const T *>(&u);
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) f[i] = to_f32(e[i]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) f[i] = to_f32(p[i]);
+    }
+}
+
+// counter-based uniform in [0, 1): 64-bit mix of (seed, row, slot)
+__device__ __forceinline__ float drop_uniform(uint64_t seed, int64_t row, int j) {
+    uint64_t x = seed ^ (uint64_t)row * 0x9E3779B97F4A7C15ull ^ ((uint64_t)j << 32);
+    x ^= x >> 33; x *= 0xff51afd7ed558ccdull;
+    x ^= x >> 33; x *= 0xc4ceb9fe1a85ec53ull;
+    x ^= x >> 33;
+    return (float)(x >> 40) * (1.0f / 16777216.0f);
+}
+
+template <typename T, int D, int U>
+__global__ void __launch_bounds__(WAVES * SSA_WAVE)
+apply_fwd_kernel(ApplyP p) {
+    using G = Geo<T, D>;
+    constexpr int VEC = G::VEC, LPR = G::LPR, RPI = G::RPI;
+    extern __shared__ float smem[];
+    const int64_t blk = xcd_logical_block(blockIdx.x, p.nblocks);
+    if (blk >= p.nblocks) return;
+    const int wid = threadIdx.x / SSA_WAVE;
+    const int64_t row = blk * WAVES + wid;
+    if (row >= p.rows) return;
+    const int lane = lane_id();
+    const int sub = lane / LPR, li = lane % LPR;
+    float *sc = smem + wid * p.K;
+
+    const int n = (int)(row % p.N);
+    const int64_t bh = row / p.N;
+    const int h = (int)(bh % p.Hq);
+    const int b = (int)(bh / p.Hq);
+    const int g = h / p.rep;
+
+    const T *qrow = (const T *)p.q + b * p.qsb + h * p.qsh + (int64_t)n * p.qsn;
+    const T *kb = (const T *)p.k + b * p.ksb + g * p.ksh;
+    const T *vb = (const T *)p.v + b * p.vsb + g * p.vsh;
+    const int64_t *nb = p.nb + row * p.K;
+    const uint8_t *va = p.valid ? p.valid + row * p.K : nullptr;
+
+    float qf[VEC];
+    load_vec<T, VEC>(qrow + li * VEC, qf);
+
+    // ---- scores
+    for (int j0 = 0; j0 < p.K; j0 += RPI * U) {
+        int64_t idx[U];
+        bool ok[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int j = j0 + u * RPI + sub;
+            int64_t x = 0;
+            bool o = false;
+            if (j < p.K) {
+                x = nb[j];
+                o = va ? (va[j] != 0) : true;
+            }
+            if (x < 0 || x >= p.M) { x = 0; o = false; }   // never read out of bounds
+            idx[u] = x;
+            ok[u] = o;
+        }
+        float kf[U][VEC];
+#pragma unroll
+        for (int u = 0; u < U; ++u) load_vec<T, VEC>(kb + idx[u] * p.ksn + li * VEC, kf[u]);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            float part = 0.f;
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) part = fmaf(qf[e], kf[u][e], part);
+#pragma unroll
+            for (int o = LPR / 2; o > 0; o >>= 1) part += __shfl_xor(part, o, SSA_WAVE);
+            const int j = j0 + u * RPI + sub;
+            if (li == 0 && j < p.K) sc[j] = ok[u] ? part * p.scale : -INFINITY;
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // ---- fp32 softmax statistics
+    float m = -INFINITY;
+    for (int j = lane; j < p.K; j += SSA_WAVE) m = fmaxf(m, sc[j]);
+    m = wave_max(m);
+    float l = 0.f;
+    for (int j = lane; j < p.K; j += SSA_WAVE) l += expf(sc[j] - m);
+    l = wave_sum(l);
+
+    // ---- P.V
+    float acc[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
+    for (int j0 = 0; j0 < p.K; j0 += RPI * U) {
+        int64_t idx[U];
+        float pj[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int j = j0 + u * RPI + sub;
+            float w = 0.f;
+            int64_t x = 0;
+            if (j < p.K) {
+                w = expf(sc[j] - m) / l;
+                x = nb[j];
+                if (x < 0 || x >= p.M) { x = 0; w = 0.f; }
+                if (!p.fp32w) w = Cvt<T>::round(w);
+                if (p.drop_p > 0.f) {
+                    w = (drop_uniform(p.seed, row, j) < p.drop_p) ? 0.f
+                                                                   : w * p.drop_scale;
+                    if (!p.fp32w) w = Cvt<T>::round(w);
+                }
+            }
+            idx[u] = x;
+            pj[u] = w;
+        }
+        float vf[U][VEC];
+#pragma unroll
+        for (int u = 0; u < U; ++u) load_vec<T, VEC>(vb + idx[u] * p.vsn + li * VEC, vf[u]);
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) acc[e] = fmaf(pj[u], vf[u][e], acc[e]);
+    }
+#pragma unroll
+    for (int o = LPR; o < SSA_WAVE; o <<= 1)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[e] += __shfl_xor(acc[e], o, SSA_WAVE);
+    if (sub == 0) {
+        T *orow = (T *)p.out + b * p.osb + h * p.osh + (int64_t)n * p.osn + li * VEC;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) Cvt<T>::store(orow + e, acc[e]);
+    }
+}
+
+// Backward: recompute p, then dp = dO.v, ds = p (dp - sum p dp), draw = ds*scale,
+// dq = sum draw k (direct store), dk += draw q, dv += p' dO (fp32 atomics).
+template <typename T, int D>
+__global__ void __launch_bounds__(WAVES * SSA_WAVE)
+apply_bwd_kernel(ApplyP p) {
+    using G = Geo<T, D>;
+    constexpr int VEC = G::VEC, LPR = G::LPR, RPI = G::RPI;
+    extern __shared__ float smem[];
+    const int64_t blk = xcd_logical_block(blockIdx.x, p.nblocks);
+    if (blk >= p.nblocks) return;
+    const int wid = threadIdx.x / SSA_WAVE;
+    const int64_t row = blk * WAVES + wid;
+    if (row >= p.rows) return;
+    const int lane = lane_id();
+    const int sub = lane / LPR, li = lane % LPR;
+    float *sc = smem + wid * 2 * p.K;     // scores, then p'
+    float *dpv = sc + p.K;                // dp per slot
+
+    const int n = (int)(row % p.N);
+    const int64_t bh = row / p.N;
+    const int h = (int)(bh % p.Hq);
+    const int b = (int)(bh / p.Hq);
+    const int g = h / p.rep;
+    const T *qrow = (const T *)p.q + b * p.qsb + h * p.qsh + (int64_t)n * p.qsn;
+    const T *kb = (const T *)p.k + b * p.ksb + g * p.ksh;
+    const T *vb = (const T *)p.v + b * p.vsb + g * p.vsh;
+    const int64_t *nb = p.nb + row * p.K;
+    const uint8_t *va = p.valid ? p.valid + row * p.K : nullptr;
+    const float *dorow = p.dout + row * D + li * VEC;
+
+    float qf[VEC], dof[VEC];
+    load_vec<T, VEC>(qrow + li * VEC, qf);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) dof[e] = dorow[e];
+
+    for (int j0 = 0; j0 < p.K; j0 += RPI) {
+        const int j = j0 + sub;
+        int64_t x = 0;
+        bool o = false;
+        if (j < p.K) { x = nb[j]; o = va ? (va[j] != 0) : true; }
+        if (x < 0 || x >= p.M) { x = 0; o = false; }
+        float kf[VEC], vf[VEC];
+        load_vec<T, VEC>(kb + x * p.ksn + li * VEC, kf);
+        load_vec<T, VEC>(vb + x * p.vsn + li * VEC, vf);
+        float s = 0.f, dp = 0.f;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) { s = fmaf(qf[e], kf[e], s); dp = fmaf(dof[e], vf[e], dp); }
+#pragma unroll
+        for (int off = LPR / 2; off > 0; off >>= 1) {
+            s += __shfl_xor(s, off, SSA_WAVE);
+            dp += __shfl_xor(dp, off, SSA_WAVE);
+        }
+        if (li == 0 && j < p.K) { sc[j] = o ? s * p.scale : -INFINITY; dpv[j] = dp; }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float m = -INFINITY;
+    for (int j = lane; j < p.K; j += SSA_WAVE) m = fmaxf(m, sc[j]);
+    m = wave_max(m);
+    float l = 0.f;
+    for (int j = lane; j < p.K; j += SSA_WAVE) l += expf(sc[j] - m);
+    l = wave_sum(l);
+    // dp w.r.t. softmax output includes the dropout mask/scale
+    float pdp = 0.f;
+    for (int j = lane; j < p.K; j += SSA_WAVE) {
+        float pj = expf(sc[j] - m) / l;
+        float mask = 1.f;
+        if (p.drop_p > 0.f) mask = (drop_uniform(p.seed, row, j) < p.drop_p) ? 0.f : p.drop_scale;
+        float dpj = dpv[j] * mask;
+        pdp += pj * dpj;
+        sc[j] = pj;          // keep p
+        dpv[j] = dpj;        // keep dp (softmax-output side)
+    }
+    pdp = wave_sum(pdp);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    float dqa[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) dqa[e] = 0.f;
+    for (int j0 = 0; j0 < p.K; j0 += RPI) {
+        const int j = j0 + sub;
+        if (j >= p.K) continue;
+        int64_t x = nb[j];
+        if (x < 0 || x >= p.M) continue;
+        const float pj = sc[j];
+        const float draw = pj * (dpv[j] - pdp) * p.scale;
+        float mask = 1.f;
+        if (p.drop_p > 0.f) mask = (drop_uniform(p.seed, row, j) < p.drop_p) ? 0.f : p.drop_scale;
+        const float pw = pj * mask;
+        float kf[VEC];
+        load_vec<T, VEC>(kb + x * p.ksn + li * VEC, kf);
+        float *dkr = p.dk + (((int64_t)b * p.Hkv + g) * p.M + x) * D + li * VEC;
+        float *dvr = p.dv + (((int64_t)b * p.Hkv + g) * p.M + x) * D + li * VEC;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+            dqa[e] = fmaf(draw, kf[e], dqa[e]);
+            if (draw != 0.f) unsafeAtomicAdd(dkr + e, draw * qf[e]);
+            if (pw != 0.f) unsafeAtomicAdd(dvr + e, pw * dof[e]);
+        }
+    }
+#pragma unroll
+    for (int o = LPR; o < SSA_WAVE; o <<= 1)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) dqa[e] += __shfl_xor(dqa[e], o, SSA_WAVE);
+    if (sub == 0) {
+        float *dqr = p.dq + row * D + li * VEC;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) dqr[e] = dqa[e];
+    }
+}
+
+template <typename T, int D>
+int launch_apply(const ApplyP &p, hipStream_t st, bool bwd) {
+    const int64_t grid = 8 * ceil_div(p.nblocks, 8);
+    if (bwd) {
+        const size_t lds = (size_t)WAVES * 2 * p.K * sizeof(float);
+        hipLaunchKernelGGL((apply_bwd_kernel<T, D>), dim3((unsigned)grid), dim3(WAVES * SSA_WAVE),
+                           lds, st, p);
+    } else {
+        const size_t lds = (size_t)WAVES * p.K * sizeof(float);
+        constexpr int U = (Geo<T, D>::RPI >= 8) ? 4 : 8;
+        hipLaunchKernelGGL((apply_fwd_kernel<T, D, U>), dim3((unsigned)grid),
+                           dim3(WAVES * SSA_WAVE), lds, st, p);
+    }
+    SSA_CHECK_LAUNCH();
+    return SSA_OK;
+}
+
+template <typename T>
+int dispatch_d(const ApplyP &p, int d, hipStream_t st, bool bwd) {
+    switch (d) {
+        case 4: return launch_apply<T, 4>(p, st, bwd);
+        case 8: return launch_apply<T, 8>(p, st, bwd);
+        case 16: return launch_apply<T, 16>(p, st, bwd);
+        case 32: return launch_apply<T, 32>(p, st, bwd);
+        case 64: return launch_apply<T, 64>(p, st, bwd);
+        case 128: return launch_apply<T, 128>(p, st, bwd);
+        case 256: return launch_apply<T, 256>(p, st, bwd);
+        default:
+            ssa_set_error("sparse_gather_attention: head dim %d unsupported (4..256, power of 2)", d);
+            return SSA_E_UNSUP;
+    }
+}
+
+int check_view(const ssa_tensor4 &t, int dtype, const char *name) {
+    if (!t.ptr) { ssa_set_error("%s: null pointer", name); return SSA_E_ARG; }
+    if (t.dtype != dtype) { ssa_set_error("%s: dtype mismatch", name); return SSA_E_ARG; }
+    return SSA_OK;
+}
+
+int apply_common(const ssa_apply_args *a, ApplyP &p) {
+    SSA_CHECK_ARG(a != nullptr, "sparse_gather_attention: null args");
+    SSA_CHECK_ARG(a->B >= 0 && a->Hq > 0 && a->Hkv > 0 && a->N >= 0 && a->M > 0 && a->K >= 0,
+                  "sparse_gather_attention: bad sizes B=%d Hq=%d Hkv=%d N=%d M=%d K=%d", a->B,
+                  a->Hq, a->Hkv, a->N, a->M, a->K);
+    SSA_CHECK_ARG(a->Hq % a->Hkv == 0, "sparse_gather_attention: Hq %% Hkv != 0");
+    SSA_CHECK_ARG(a->K <= 4096, "sparse_gather_attention: K=%d above 4096", a->K);
+    SSA_CHECK_ARG(a->q.dtype >= 0 && a->q.dtype <= 2, "sparse_gather_attention: bad dtype");
+    int rc;
+    if ((rc = check_view(a->q, a->q.dtype, "q"))) return rc;
+    if ((rc = check_view(a->k, a->q.dtype, "k"))) return rc;
+    if ((rc = check_view(a->v, a->q.dtype, "v"))) return rc;
+    SSA_CHECK_ARG(a->neighbors != nullptr && a->out != nullptr, "sparse_gather_attention: null");
+    SSA_CHECK_ARG(a->dropout_p >= 0.f && a->dropout_p < 1.f, "dropout p must be in [0, 1)");
+    p = ApplyP{};
+    p.B = a->B; p.Hq = a->Hq; p.Hkv = a->Hkv; p.N = a->N; p.M = a->M; p.K = a->K;
+    p.rep = a->Hq / a->Hkv;
+    p.q = a->q.ptr; p.k = a->k.ptr; p.v = a->v.ptr;
+    p.qsb = a->q.sb; p.qsh = a->q.sh; p.qsn = a->q.sn;
+    p.ksb = a->k.sb; p.ksh = a->k.sh; p.ksn = a->k.sn;
+    p.vsb = a->v.sb; p.vsh = a->v.sh; p.vsn = a->v.sn;
+    p.nb = a->neighbors; p.valid = a->valid;
+    p.scale = a->scale; p.fp32w = a->fp32_weights;
+    p.drop_p = a->dropout_p;
+    p.drop_scale = a->dropout_p > 0.f ? 1.f / (1.f - a->dropout_p) : 1.f;
+    p.seed = a->seed;
+    p.out = a->out; p.osb = a->out_sb; p.osh = a->out_sh; p.osn = a->out_sn;
+    p.rows = (int64_t)a->B * a->Hq * a->N;
+    p.nblocks = ceil_div(p.rows, WAVES);
+    return SSA_OK;
+}
+
+int run_apply(const ApplyP &p, int dtype, int d, hipStream_t st, bool bwd) {
+    if (p.rows == 0) return SSA_OK;
+    switch (dtype) {
+        case SSA_F32: return dispatch_d<float>(p, d, st, bwd);
+        case SSA_BF16: return dispatch_d<bf16_t>(p, d, st, bwd);
+        case SSA_F16: return dispatch_d<f16_t>(p, d, st, bwd);
+    }
+    ssa_set_error("sparse_gather_attention: bad dtype %d", dtype);
+    return SSA_E_ARG;
+}
+
+}  // namespace
+
+extern "C" int ssa_sparse_gather_attention(const ssa_apply_args *a, void *stream) {
+    ApplyP p;
+    int rc = apply_common(a, p);
+    if (rc) return rc;
+    return run_apply(p, a->q.dtype, a->d, (hipStream_t)stream, false);
+}
+
+extern "C" int ssa_sparse_gather_attention_bwd(const ssa_apply_bwd_args *a, void *stream) {
+    SSA_CHECK_ARG(a != nullptr, "sparse_gather_attention_bwd: null args");
+    ApplyP p;
+    int rc = apply_common(&a->fwd, p);
+    if (rc) return rc;
+    SSA_CHECK_ARG(a->dout && a->dq && a->dk && a->dv, "sparse_gather_attention_bwd: null grad");
+    p.dout = a->dout; p.dq = a->dq; p.dk = a->dk; p.dv = a->dv;
+    return run_apply(p, a->fwd.q.dtype, a->fwd.d, (hipStream_t)stream, true);
+}

@@ -1,0 +1,124 @@
+// ssa_common.h -- shared device helpers for the gfx950 SparseAttention kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/ssa_amd.h"
+
+#define SSA_WAVE 64
+
+// ---------------------------------------------------------------- error text
+void ssa_set_error(const char *fmt, ...);
+
+#define SSA_CHECK_ARG(cond, ...)                 \
+    do {                                         \
+        if (!(cond)) {                           \
+            ssa_set_error(__VA_ARGS__);          \
+            return SSA_E_ARG;                    \
+        }                                        \
+    } while (0)
+
+#define SSA_CHECK_HIP(expr)                                                        \
+    do {                                                                           \
+        hipError_t e_ = (expr);                                                    \
+        if (e_ != hipSuccess) {                                                    \
+            ssa_set_error("%s failed: %s", #expr, hipGetErrorString(e_));          \
+            return SSA_E_HIP;                                                      \
+        }                                                                          \
+    } while (0)
+
+#define SSA_CHECK_LAUNCH() SSA_CHECK_HIP(hipGetLastError())
+
+// ---------------------------------------------------------------- dtypes
+// 16-bit storage types as raw bits: bf16 = upper half of an fp32, fp16 = IEEE
+// binary16.  Conversions are written out so the numerics are explicit.
+struct bf16_t { uint16_t x; };
+struct f16_t  { uint16_t x; };
+
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(bf16_t v) {
+    return __uint_as_float(((uint32_t)v.x) << 16);
+}
+__device__ __forceinline__ float to_f32(f16_t v) {
+    _Float16 h;
+    __builtin_memcpy(&h, &v.x, 2);
+    return (float)h;
+}
+
+// round-to-nearest-even fp32 -> bf16 (NaN kept quiet)
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7f800000u) == 0x7f800000u) return (uint16_t)((u >> 16) | ((u & 0xffff) ? 0x40 : 0));
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+template <typename T> struct Cvt;
+template <> struct Cvt<float> {
+    static __device__ __forceinline__ float round(float v) { return v; }
+    static __device__ __forceinline__ void store(float *p, float v) { *p = v; }
+};
+template <> struct Cvt<bf16_t> {
+    static __device__ __forceinline__ float round(float v) {
+        return __uint_as_float(((uint32_t)f32_to_bf16_bits(v)) << 16);
+    }
+    static __device__ __forceinline__ void store(bf16_t *p, float v) { p->x = f32_to_bf16_bits(v); }
+};
+template <> struct Cvt<f16_t> {
+    static __device__ __forceinline__ float round(float v) { return (float)(_Float16)v; }
+    static __device__ __forceinline__ void store(f16_t *p, float v) {
+        _Float16 h = (_Float16)v;
+        __builtin_memcpy(&p->x, &h, 2);
+    }
+};
+
+// ---------------------------------------------------------------- wave ops
+__device__ __forceinline__ int lane_id() { return (int)__lane_id(); }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, SSA_WAVE);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, SSA_WAVE));
+    return v;
+}
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, SSA_WAVE);
+    return v;
+}
+
+// ballot over the 64-lane wave
+__device__ __forceinline__ uint64_t wave_ballot(bool p) { return __ballot(p); }
+
+// number of set bits of m in lanes below this one
+__device__ __forceinline__ int lanes_below(uint64_t m) {
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                     __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
+}
+
+// order-preserving map fp32 -> uint32 (larger float -> larger key); all
+// finite values and +/-inf map above 0, so 0 can mark "no score".
+__device__ __forceinline__ uint32_t score_key(float f) {
+    uint32_t u = __float_as_uint(f);
+    uint32_t k = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return k == 0 ? 1u : k;
+}
+__device__ __forceinline__ float key_score(uint32_t k) {
+    uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
+    return __uint_as_float(u);
+}
+
+__host__ __device__ __forceinline__ int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// XCD-aware block order: the dispatcher sends workgroup i to XCD i % 8.  Map
+// physical block id -> logical id so that each XCD walks one contiguous range
+// of logical blocks (consecutive logical blocks share K/V rows in L2).
+__device__ __forceinline__ int64_t xcd_logical_block(int64_t phys, int64_t nlogical) {
+    const int64_t per = (nlogical + 7) / 8;
+    return (phys % 8) * per + phys / 8;
+}

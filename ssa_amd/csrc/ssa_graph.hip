@@ -1,0 +1,882 @@
+// ssa_graph.hip -- neighbor-graph build for SparseAttention on gfx950.
+//
+// Replaces SparseAttention.build_graph (sparse_attention.py:1325-1390) and
+// LSHGraphBuilder.forward (:814-959).  Pipeline per call:
+//
+//  1. hash_kernel      fp32 projections of every q row (B*Hq*N) and every
+//                      UN-expanded k row (B*Hkv*M) on the first P planes of
+//                      each round; bit j = (proj_j > 0) (+0, -0, NaN -> 0),
+//                      plane j = bit j; probe t flips the t-th least |proj|
+//                      bit of the base id (ties by plane order) (:575-646).
+//  2. bucket sort      introsort-exact permutation per (kv head, round), see
+//                      ssa_sort.hip (:781-792).  Shared by the kv_rep query
+//                      heads of a GQA group.
+//  3. query bucketing  counting sort of the N queries of each (head, round,
+//                      id set) by bucket id, and a tile list of up to 64
+//                      queries that share one bucket.
+//  4. rescore_kernel   a query's candidate list depends only on its bucket
+//                      (:668-696): the C candidate rows of bucket u are staged
+//                      in LDS once per tile and scored against every query of
+//                      the tile (fp32 dot, q.k unscaled, :909-916).  Scores go
+//                      to S[row][slot], slot = stream position.
+//  5. select_kernel    one wavefront per query walks its candidate stream in
+//                      the reference's concatenation order (round, id set,
+//                      slot, :869-877) with a seen-bitmap of M bits in LDS:
+//                      a slot is kept iff valid and its key was not met at an
+//                      earlier stream position, valid or not (:884-890);
+//                      causal future keys become the query itself (:698-709);
+//                      empty buckets read glob ++ 0 (:711-737).  Kept scores
+//                      are held in registers and the exact top-kk is found by
+//                      a 32-step bitwise search of the order-preserving score
+//                      keys.  Slots without a candidate take glob[t] / 0 by
+//                      position (:948-957).  FULL mode then merges window,
+//                      globals and the LSH set into a key bitmap and reads it
+//                      out in ascending order (:966-1089).
+//
+// Tie rule: when the kk-th and (kk+1)-th kept scores are exactly equal the
+// reference's choice follows its chunked introselect replay; here the tied
+// slots earlier in the stream win.  Such queries are counted in out_ties.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "ssa_common.h"
+#include "ssa_graph_internal.h"
+
+namespace {
+
+constexpr int TQ = 64;         // queries per rescore tile
+constexpr int TC = 64;         // candidates per rescore sub-tile
+constexpr int SEL_WAVES = 4;   // waves per select workgroup
+
+struct Dims {
+    int B, Hq, Hkv, rep, N, M, d, R, maxP, P, Tp, NS, NB, C, CPL, nlists, G, kk, Kw, Kout;
+    int64_t Call, BH, BK;
+    int nbh_chunk;
+};
+
+// ------------------------------------------------------------------ hashing
+struct HashP {
+    const void *x;
+    int64_t sb, sh, sn;
+    int nh, L, d;
+    const float *planes;
+    int R, maxP, P, Tp, NS;
+    const float *inj;
+    uint16_t *out;
+    int key_layout;
+    int64_t rows;
+};
+
+template <typename T>
+__global__ void __launch_bounds__(256) hash_kernel(HashP p) {
+    const int64_t row = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (row >= p.rows) return;
+    const int i = (int)(row % p.L);
+    const int64_t bh = row / p.L;
+    const int h = (int)(bh % p.nh);
+    const int64_t b = bh / p.nh;
+    const T *x = (const T *)p.x + b * p.sb + h * p.sh + (int64_t)i * p.sn;
+    for (int r = 0; r < p.R; ++r) {
+        float pr[12];
+#pragma unroll
+        for (int j = 0; j < 12; ++j) pr[j] = 0.f;
+        if (p.inj) {
+            const float *ip = p.inj + ((bh * p.R + r) * p.L + i) * p.P;
+            for (int j = 0; j < p.P; ++j) pr[j] = ip[j];
+        } else {
+            const float *pl = p.planes + (int64_t)r * p.maxP * p.d;
+            for (int e = 0; e < p.d; ++e) {
+                const float xv = to_f32(x[e]);
+#pragma unroll
+                for (int j = 0; j < 12; ++j)
+                    if (j < p.P) pr[j] = fmaf(xv, pl[j * p.d + e], pr[j]);
+            }
+        }
+        int id = 0;
+#pragma unroll
+        for (int j = 0; j < 12; ++j)
+            if (j < p.P && pr[j] > 0.f) id |= 1 << j;
+        if (p.key_layout) {
+            p.out[(bh * p.R + r) * p.L + i] = (uint16_t)id;
+        } else {
+            uint16_t *o = p.out + ((bh * p.L + i) * p.R + r) * p.NS;
+            o[0] = (uint16_t)id;
+            if (p.Tp > 0) {
+                int ord[12];
+#pragma unroll
+                for (int j = 0; j < 12; ++j) ord[j] = 0;
+                for (int j = 0; j < p.P; ++j) {       // stable rank of |proj_j|
+                    const float aj = fabsf(pr[j]);
+                    int rank = 0;
+                    for (int q = 0; q < p.P; ++q) {
+                        const float aq = fabsf(pr[q]);
+                        rank += (aq < aj) || (aq == aj && q < j);
+                    }
+                    for (int t = 0; t < 12; ++t)
+                        if (t == rank) ord[t] = j;
+                }
+                for (int t = 0; t < p.Tp; ++t) {
+                    int pos = 0;
+#pragma unroll
+                    for (int q = 0; q < 12; ++q)
+                        if (q == t) pos = ord[q];
+                    o[1 + t] = (uint16_t)(id ^ (1 << pos));
+                }
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------ small utilities
+__global__ void fill_i32_kernel(int32_t *p, int64_t n, int32_t v) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = v;
+}
+
+// ------------------------------------------------------------------ query bucketing
+struct QbP {
+    const uint16_t *qid;
+    const int32_t *bsize;   // key bucket sizes (BK*R, NB)
+    int32_t *cnt, *off, *cur, *qlist, *tiles, *ntiles;
+    int N, R, NS, NB, Hq, Hkv, rep, bh0, ninst;
+};
+
+__device__ __forceinline__ void inst_decode(const QbP &p, int inst, int &bh, int &r, int &t) {
+    t = inst % p.NS;
+    r = (inst / p.NS) % p.R;
+    bh = p.bh0 + inst / (p.NS * p.R);
+}
+
+__global__ void __launch_bounds__(256) qb_hist_kernel(QbP p) {
+    extern __shared__ int32_t hist[];
+    const int inst = blockIdx.y;
+    int bh, r, t;
+    inst_decode(p, inst, bh, r, t);
+    for (int u = threadIdx.x; u < p.NB; u += blockDim.x) hist[u] = 0;
+    __syncthreads();
+    const int n = blockIdx.x * blockDim.x + threadIdx.x;
+    if (n < p.N) {
+        const int u = p.qid[(((int64_t)bh * p.N + n) * p.R + r) * p.NS + t];
+        atomicAdd(&hist[u], 1);
+    }
+    __syncthreads();
+    for (int u = threadIdx.x; u < p.NB; u += blockDim.x)
+        if (hist[u]) atomicAdd(&p.cnt[(int64_t)inst * p.NB + u], hist[u]);
+}
+
+// one block per instance: bucket offsets and the tile list
+__global__ void __launch_bounds__(256) qb_scan_kernel(QbP p) {
+    __shared__ int32_t part_q[256], part_t[256];
+    __shared__ int32_t tbase;
+    const int inst = blockIdx.x;
+    int bh, r, t;
+    inst_decode(p, inst, bh, r, t);
+    const int b = bh / p.Hq, h = bh % p.Hq, g = h / p.rep;
+    const int64_t krow = ((int64_t)b * p.Hkv + g) * p.R + r;
+    const int per = (p.NB + 255) / 256;
+    const int u0 = threadIdx.x * per;
+    int sq = 0, st = 0;
+    for (int u = u0; u < u0 + per && u < p.NB; ++u) {
+        const int c = p.cnt[(int64_t)inst * p.NB + u];
+        sq += c;
+        if (c > 0 && p.bsize[krow * p.NB + u] > 0) st += (c + TQ - 1) / TQ;
+    }
+    part_q[threadIdx.x] = sq;
+    part_t[threadIdx.x] = st;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int aq = 0, at = 0;
+        for (int i = 0; i < 256; ++i) {
+            const int vq = part_q[i], vt = part_t[i];
+            part_q[i] = aq;
+            part_t[i] = at;
+            aq += vq;
+            at += vt;
+        }
+        tbase = atomicAdd(p.ntiles, at);
+    }
+    __syncthreads();
+    int aq = part_q[threadIdx.x], at = tbase + part_t[threadIdx.x];
+    for (int u = u0; u < u0 + per && u < p.NB; ++u) {
+        const int c = p.cnt[(int64_t)inst * p.NB + u];
+        p.off[(int64_t)inst * p.NB + u] = aq;
+        p.cur[(int64_t)inst * p.NB + u] = aq;
+        if (c > 0 && p.bsize[krow * p.NB + u] > 0) {
+            for (int k = 0; k * TQ < c; ++k) {
+                int32_t *e = p.tiles + (int64_t)at * 4;
+                e[0] = inst;
+                e[1] = u;
+                e[2] = aq + k * TQ;
+                e[3] = min(TQ, c - k * TQ);
+                ++at;
+            }
+        }
+        aq += c;
+    }
+}
+
+__global__ void __launch_bounds__(256) qb_scatter_kernel(QbP p) {
+    const int inst = blockIdx.y;
+    int bh, r, t;
+    inst_decode(p, inst, bh, r, t);
+    const int n = blockIdx.x * blockDim.x + threadIdx.x;
+    if (n >= p.N) return;
+    const int u = p.qid[(((int64_t)bh * p.N + n) * p.R + r) * p.NS + t];
+    const int pos = atomicAdd(&p.cur[(int64_t)inst * p.NB + u], 1);
+    p.qlist[(int64_t)inst * p.N + pos] = n;
+}
+
+// ------------------------------------------------------------------ rescore
+struct RsP {
+    const int32_t *tiles, *ntiles, *qlist, *perm, *bstart, *bsize;
+    const void *q, *k;
+    int64_t qsb, qsh, qsn, ksb, ksh, ksn;
+    float *S;
+    int N, M, R, NS, NB, C, Hq, Hkv, rep, bh0;
+    int64_t Call;
+};
+
+template <typename T, int D>
+__global__ void __launch_bounds__(256) rescore_kernel(RsP p) {
+    constexpr int LD = D + 1;
+    extern __shared__ float rs_smem[];
+    float *Qs = rs_smem;                // [TQ][LD]
+    float *Ks = Qs + TQ * LD;           // [TC][LD]
+    int *nidx = (int *)(Ks + TC * LD);  // [TQ]
+    int *kidx = nidx + TQ;              // [TC]
+    if ((int)blockIdx.x >= *p.ntiles) return;
+    const int32_t *e = p.tiles + (int64_t)blockIdx.x * 4;
+    const int inst = e[0], u = e[1], qb = e[2], qc = e[3];
+    const int t = inst % p.NS, r = (inst / p.NS) % p.R, bhl = inst / (p.NS * p.R);
+    const int bh = p.bh0 + bhl;
+    const int b = bh / p.Hq, h = bh % p.Hq, g = h / p.rep;
+    const int64_t prow = ((int64_t)b * p.Hkv + g) * p.R + r;
+    const int st = p.bstart[prow * p.NB + u];
+    const int nv = min(p.bsize[prow * p.NB + u], p.C);
+    const int tid = threadIdx.x;
+    const T *qbase = (const T *)p.q + b * p.qsb + h * p.qsh;
+    const T *kbase = (const T *)p.k + b * p.ksb + g * p.ksh;
+
+    if (tid < TQ) nidx[tid] = tid < qc ? p.qlist[(int64_t)inst * p.N + qb + tid] : 0;
+    __syncthreads();
+    for (int x = tid; x < TQ * D; x += 256) {
+        const int i = x / D, c = x % D;
+        Qs[i * LD + c] = i < qc ? to_f32(qbase[(int64_t)nidx[i] * p.qsn + c]) : 0.f;
+    }
+    const int64_t slotbase = (int64_t)(r * p.NS + t) * p.C;
+    const int ty = tid / 16, tx = tid % 16;
+    for (int c0 = 0; c0 < nv; c0 += TC) {
+        __syncthreads();
+        if (tid < TC) kidx[tid] = (c0 + tid < nv) ? p.perm[prow * p.M + st + c0 + tid] : 0;
+        __syncthreads();
+        for (int x = tid; x < TC * D; x += 256) {
+            const int j = x / D, c = x % D;
+            Ks[j * LD + c] = (c0 + j < nv) ? to_f32(kbase[(int64_t)kidx[j] * p.ksn + c]) : 0.f;
+        }
+        __syncthreads();
+        float acc[4][4];
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int bb = 0; bb < 4; ++bb) acc[a][bb] = 0.f;
+        for (int c = 0; c < D; ++c) {
+            float qa[4], kb[4];
+#pragma unroll
+            for (int a = 0; a < 4; ++a) qa[a] = Qs[(ty * 4 + a) * LD + c];
+#pragma unroll
+            for (int bb = 0; bb < 4; ++bb) kb[bb] = Ks[(tx + 16 * bb) * LD + c];
+#pragma unroll
+            for (int a = 0; a < 4; ++a)
+#pragma unroll
+                for (int bb = 0; bb < 4; ++bb) acc[a][bb] = fmaf(qa[a], kb[bb], acc[a][bb]);
+        }
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+            const int i = ty * 4 + a;
+            if (i >= qc) continue;
+            float *srow = p.S + ((int64_t)bhl * p.N + nidx[i]) * p.Call + slotbase + c0;
+#pragma unroll
+            for (int bb = 0; bb < 4; ++bb) {
+                const int cc = tx + 16 * bb;
+                if (c0 + cc < nv) srow[cc] = acc[a][bb];
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------ select + merge
+struct SelP {
+    const uint16_t *qid;
+    const int32_t *perm, *bstart, *bsize;
+    const float *S;
+    const void *q, *k;
+    int64_t qsb, qsh, qsn, ksb, ksh, ksn;
+    const int64_t *glob;
+    int N, M, d, R, NS, NB, C, CPL, nlists, Hq, Hkv, rep, G, kk, window, causal, cross, mode,
+        total_k, Kw, Kout, bh0, words;
+    int64_t Call, rows;
+    int64_t *out_idx;
+    uint8_t *out_valid;
+    int32_t *ties;
+    int64_t nblocks;
+};
+
+__device__ __forceinline__ bool bm_test(const uint32_t *bm, int v) {
+    return (bm[v >> 5] >> (v & 31)) & 1u;
+}
+__device__ __forceinline__ void bm_set(uint32_t *bm, int v) { atomicOr(&bm[v >> 5], 1u << (v & 31)); }
+
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ int wave_excl_scan(int v) {
+    const int lane = lane_id();
+    int x = v;
+#pragma unroll
+    for (int o = 1; o < SSA_WAVE; o <<= 1) {
+        const int y = __shfl_up(x, o, SSA_WAVE);
+        if (lane >= o) x += y;
+    }
+    return x - v;
+}
+
+template <typename T>
+struct SelCtx {
+    const SelP &p;
+    int n, bh, bk;
+    int64_t row;
+    float qv[4];
+    const T *kbase;
+    __device__ SelCtx(const SelP &pp) : p(pp) {}
+    __device__ float dotk(int v) const {
+        const int lane = lane_id();
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = lane + 64 * i;
+            if (e < p.d) s = fmaf(qv[i], to_f32(kbase[(int64_t)v * p.ksn + e]), s);
+        }
+        return wave_sum(s);
+    }
+    // key id held by stream slot (list, c)
+    __device__ int slot_value(int list, int c) const {
+        const int r = list / p.NS, t = list % p.NS;
+        const int u = p.qid[((int64_t)bh * p.N + n) * p.R * p.NS + r * p.NS + t];
+        const int64_t prow = (int64_t)bk * p.R + r;
+        const int sz = p.bsize[prow * p.NB + u];
+        if (sz == 0) return c < p.G ? (int)p.glob[c] : 0;
+        const int st = p.bstart[prow * p.NB + u];
+        const int nv = min(sz, p.C);
+        const int raw = p.perm[prow * p.M + (c < nv ? st + c : p.M - 1)];
+        return (p.causal && raw > n) ? n : raw;
+    }
+};
+
+template <typename T, int MAXCH>
+__global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
+    extern __shared__ uint32_t sel_smem[];
+    const int64_t blk = xcd_logical_block(blockIdx.x, p.nblocks);
+    if (blk >= p.nblocks) return;
+    const int wid = threadIdx.x / SSA_WAVE;
+    const int64_t rloc = blk * SEL_WAVES + wid;
+    if (rloc >= p.rows) return;
+    const int lane = lane_id();
+    const int per_wave = p.words + 3 * p.kk;
+    uint32_t *bm = sel_smem + (int64_t)wid * per_wave;
+    uint32_t *ekey = bm + p.words;
+    uint32_t *eval = ekey + p.kk;
+    uint32_t *eslot = eval + p.kk;
+
+    SelCtx<T> cx(p);
+    cx.n = (int)(rloc % p.N);
+    const int bhl = (int)(rloc / p.N);
+    cx.bh = p.bh0 + bhl;
+    const int b = cx.bh / p.Hq, h = cx.bh % p.Hq, g = h / p.rep;
+    cx.bk = b * p.Hkv + g;
+    cx.row = (int64_t)cx.bh * p.N + cx.n;
+    const int n = cx.n;
+    const T *qrow = (const T *)p.q + b * p.qsb + h * p.qsh + (int64_t)n * p.qsn;
+    cx.kbase = (const T *)p.k + b * p.ksb + g * p.ksh;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int e = lane + 64 * i;
+        cx.qv[i] = e < p.d ? to_f32(qrow[e]) : 0.f;
+    }
+    const float selfscore = p.causal ? cx.dotk(n) : 0.f;
+    for (int w = lane; w < p.words; w += SSA_WAVE) bm[w] = 0u;
+    wave_lds_sync();
+
+    const float *srow = p.S + ((int64_t)bhl * p.N + n) * p.Call;
+    const uint16_t *qids = p.qid + cx.row * p.R * p.NS;
+    uint32_t key[MAXCH];
+    int st = 0, sz = 0, nv = 0;
+    int64_t prow = 0;
+#pragma unroll
+    for (int ci = 0; ci < MAXCH; ++ci) {
+        key[ci] = 0u;
+        const int list = ci / p.CPL;
+        if (list < p.nlists) {
+            const int cj = ci - list * p.CPL;
+            if (cj == 0) {
+                const int r = list / p.NS;
+                const int u = qids[list];
+                prow = (int64_t)cx.bk * p.R + r;
+                st = p.bstart[prow * p.NB + u];
+                sz = p.bsize[prow * p.NB + u];
+                nv = min(sz, p.C);
+            }
+            const int c = cj * SSA_WAVE + lane;
+            const bool in_list = c < p.C;
+            if (sz == 0) {
+                if (cj == 0) {
+                    const int lim = min(p.C, p.G + 1);
+                    for (int cc = 0; cc < lim; ++cc) {
+                        const int v = cc < p.G ? (int)p.glob[cc] : 0;
+                        const bool seen = bm_test(bm, v);
+                        wave_lds_sync();
+                        if (!seen) {
+                            if (lane == 0) bm_set(bm, v);
+                            const float sc = cx.dotk(v);
+                            if (lane == cc) key[ci] = score_key(sc);
+                        }
+                        wave_lds_sync();
+                    }
+                }
+            } else {
+                const bool real = in_list && c < nv;
+                const int raw = in_list ? p.perm[prow * p.M + (real ? st + c : p.M - 1)] : 0;
+                const int v = (p.causal && raw > n) ? n : raw;
+                const bool seen = in_list ? bm_test(bm, v) : true;
+                const bool ck = real && !seen;
+                const uint64_t selfm = wave_ballot(ck && v == n);
+                const bool keep = ck && (v != n || lanes_below(selfm) == 0);
+                wave_lds_sync();
+                if (in_list) bm_set(bm, v);
+                wave_lds_sync();
+                if (keep) {
+                    const float sc = (p.causal && v == n) ? selfscore
+                                                          : srow[(int64_t)list * p.C + c];
+                    key[ci] = score_key(sc);
+                }
+            }
+        }
+    }
+
+    // ---- exact top-kk threshold over the kept keys
+    int nk = 0;
+#pragma unroll
+    for (int ci = 0; ci < MAXCH; ++ci) nk += key[ci] != 0u;
+    nk = wave_sum_i(nk);
+    const int kk = p.kk;
+    uint32_t thr = 0u;
+    int need = 0;
+    if (nk > kk) {
+#pragma unroll 1
+        for (int bit = 31; bit >= 0; --bit) {
+            const uint32_t cand = thr | (1u << bit);
+            int cnt = 0;
+#pragma unroll
+            for (int ci = 0; ci < MAXCH; ++ci) cnt += key[ci] >= cand;
+            if (wave_sum_i(cnt) >= kk) thr = cand;
+        }
+        int gt = 0, eq = 0;
+#pragma unroll
+        for (int ci = 0; ci < MAXCH; ++ci) { gt += key[ci] > thr; eq += key[ci] == thr; }
+        gt = wave_sum_i(gt);
+        eq = wave_sum_i(eq);
+        need = kk - gt;
+        if (eq > need && lane == 0 && p.ties) atomicAdd(p.ties, 1);
+    }
+    const int f = nk < kk ? nk : kk;
+
+    // ---- emit the selected slots
+    if (p.mode == SSA_GRAPH_FULL) {
+        for (int w = lane; w < p.words; w += SSA_WAVE) bm[w] = 0u;
+        wave_lds_sync();
+    }
+    int eq_before = 0, nsel = 0;
+#pragma unroll
+    for (int ci = 0; ci < MAXCH; ++ci) {
+        const uint32_t kv = key[ci];
+        const bool is_eq = (nk > kk) && kv == thr;
+        const uint64_t eqm = wave_ballot(is_eq);
+        bool sel = kv > thr || (is_eq && eq_before + lanes_below(eqm) < need);
+        if (kv == 0u) sel = false;
+        eq_before += __popcll(eqm);
+        const uint64_t sm = wave_ballot(sel);
+        if (sm) {
+            const int list = ci / p.CPL;
+            const int c = (ci - list * p.CPL) * SSA_WAVE + lane;
+            if (sel) {
+                const int v = cx.slot_value(list, c);
+                if (p.mode == SSA_GRAPH_FULL) {
+                    bm_set(bm, v);
+                } else {
+                    const int pos = nsel + lanes_below(sm);
+                    ekey[pos] = kv;
+                    eval[pos] = (uint32_t)v;
+                    eslot[pos] = (uint32_t)(list * p.C + c);
+                }
+            }
+            nsel += __popcll(sm);
+        }
+    }
+    wave_lds_sync();
+
+    if (p.mode == SSA_GRAPH_LSH) {
+        int64_t *orow = p.out_idx + cx.row * kk;
+        for (int e = lane; e < f; e += SSA_WAVE) {
+            const uint32_t k0 = ekey[e], s0 = eslot[e];
+            int rank = 0;
+            for (int e2 = 0; e2 < f; ++e2) {
+                const uint32_t k2 = ekey[e2];
+                rank += (k2 > k0) || (k2 == k0 && eslot[e2] < s0);
+            }
+            orow[rank] = (int64_t)eval[e];
+        }
+        for (int t = f + lane; t < kk; t += SSA_WAVE) orow[t] = t < p.G ? p.glob[t] : 0;
+        return;
+    }
+
+    // ---- FULL: pool = window + globals + LSH (+ fallback 0), minus self
+    if (!p.cross) {
+        for (int o = -p.window + lane; o <= p.window; o += SSA_WAVE) {
+            int x = n + o;
+            if (p.causal && o > 0) x = n;
+            x = x < 0 ? 0 : (x > p.M - 1 ? p.M - 1 : x);
+            bm_set(bm, x);
+        }
+    }
+    for (int j = lane; j < p.G; j += SSA_WAVE) bm_set(bm, (int)p.glob[j]);
+    if (lane == 0 && (f > p.G ? f : p.G) < kk) bm_set(bm, 0);
+    wave_lds_sync();
+    if (!p.cross && lane == 0) atomicAnd(&bm[n >> 5], ~(1u << (n & 31)));
+    wave_lds_sync();
+
+    const int self = p.cross ? 0 : 1;
+    const int ks = p.Kout - self;
+    int64_t *orow = p.out_idx + cx.row * p.Kout;
+    uint8_t *vrow = p.out_valid + cx.row * p.Kout;
+    const int wpl = (p.words + SSA_WAVE - 1) / SSA_WAVE;
+    const int w0 = lane * wpl;
+    int cnt = 0;
+    for (int w = w0; w < w0 + wpl && w < p.words; ++w) cnt += __popc(bm[w]);
+    int pos = wave_excl_scan(cnt);
+    const int total = wave_sum_i(cnt);
+    for (int w = w0; w < w0 + wpl && w < p.words && pos < ks; ++w) {
+        uint32_t word = bm[w];
+        while (word && pos < ks) {
+            const int bit = __ffs(word) - 1;
+            word &= word - 1;
+            orow[self + pos] = (int64_t)(w * 32 + bit);
+            vrow[self + pos] = 1;
+            ++pos;
+        }
+    }
+    const int filled = total < ks ? total : ks;
+    for (int i = self + filled + lane; i < p.Kout; i += SSA_WAVE) {
+        orow[i] = 0;
+        vrow[i] = 0;
+    }
+    if (self && lane == 0) {
+        orow[0] = n;
+        vrow[0] = 1;
+    }
+}
+
+// ------------------------------------------------------------------ host side
+int supported_d(int d) { return d >= 4 && d <= 256 && (d & (d - 1)) == 0; }
+
+int maxch_for(int nch) {
+    static const int opts[] = {8, 16, 32, 48, 64, 96, 128};
+    for (int o : opts)
+        if (nch <= o) return o;
+    return 0;
+}
+
+struct Layout {
+    int64_t kid, qid, perm, bstart, bsize, sorttmp, cnt, off, cur, qlist, tiles, ntiles, S, total;
+};
+
+int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
+
+Layout plan(const Dims &D) {
+    Layout L{};
+    int64_t o = 0;
+    auto take = [&](int64_t bytes) { int64_t at = o; o += align256(bytes); return at; };
+    const int64_t nbh = D.nbh_chunk;
+    const int64_t ninst = nbh * D.R * D.NS;
+    L.kid = take(D.BK * D.R * D.M * 2);
+    L.qid = take(D.BH * D.N * D.R * D.NS * 2);
+    L.perm = take(D.BK * D.R * D.M * 4);
+    L.bstart = take(D.BK * D.R * D.NB * 4);
+    L.bsize = take(D.BK * D.R * D.NB * 4);
+    L.sorttmp = take(ssa_sort_tmp_bytes((int)(D.BK * D.R), D.M));
+    L.cnt = take(ninst * D.NB * 4);
+    L.off = take(ninst * D.NB * 4);
+    L.cur = take(ninst * D.NB * 4);
+    L.qlist = take(ninst * D.N * 4);
+    L.tiles = take(ninst * (ceil_div(D.N, TQ) + D.NB) * 16);
+    L.ntiles = take(4);
+    L.S = take(nbh * D.N * D.Call * 4);
+    L.total = o;
+    return L;
+}
+
+int make_dims(const ssa_graph_args *a, Dims &D) {
+    SSA_CHECK_ARG(a != nullptr, "build_graph: null args");
+    SSA_CHECK_ARG(a->mode == SSA_GRAPH_FULL || a->mode == SSA_GRAPH_LSH, "build_graph: bad mode");
+    SSA_CHECK_ARG(a->B >= 1 && a->Hq >= 1 && a->Hkv >= 1 && a->N >= 1 && a->M >= 1,
+                  "build_graph: bad sizes B=%d Hq=%d Hkv=%d N=%d M=%d", a->B, a->Hq, a->Hkv,
+                  a->N, a->M);
+    SSA_CHECK_ARG(a->Hq % a->Hkv == 0, "build_graph: Hq %% Hkv != 0");
+    SSA_CHECK_ARG(a->P >= 1 && a->P <= 12 && a->P <= a->max_p, "build_graph: P=%d", a->P);
+    SSA_CHECK_ARG(a->R >= 1 && a->C >= 1 && a->top_k >= 1 && a->T >= 0, "build_graph: R/C/top_k/T");
+    SSA_CHECK_ARG(a->G >= 0 && a->G <= 63, "build_graph: G=%d outside 0..63", a->G);
+    SSA_CHECK_ARG(a->rand_proj || (a->q_proj && a->k_proj), "build_graph: no hyperplanes");
+    SSA_CHECK_ARG(a->q.ptr && a->k.ptr && a->out_idx, "build_graph: null tensor");
+    SSA_CHECK_ARG(a->q.dtype == a->k.dtype && a->q.dtype >= 0 && a->q.dtype <= 2,
+                  "build_graph: q/k dtype");
+    SSA_CHECK_ARG(a->G == 0 || a->glob, "build_graph: glob is null");
+    if (!supported_d(a->d)) {
+        ssa_set_error("build_graph: head dim %d unsupported (4..256, power of 2)", a->d);
+        return SSA_E_UNSUP;
+    }
+    if (!ssa_sort_supported(a->M)) {
+        ssa_set_error("build_graph: key length %d unsupported (1..32768)", a->M);
+        return SSA_E_UNSUP;
+    }
+    D.B = a->B; D.Hq = a->Hq; D.Hkv = a->Hkv; D.rep = a->Hq / a->Hkv;
+    D.N = a->N; D.M = a->M; D.d = a->d; D.R = a->R; D.maxP = a->max_p; D.P = a->P;
+    D.Tp = a->T < a->P ? a->T : a->P;
+    D.NS = 1 + D.Tp;
+    D.NB = 1 << a->P;
+    D.C = a->C;
+    D.CPL = (int)ceil_div(a->C, SSA_WAVE);
+    D.nlists = a->R * D.NS;
+    D.G = a->G;
+    D.Call = (int64_t)a->R * D.NS * a->C;
+    D.kk = (int)(a->top_k < D.Call ? a->top_k : D.Call);
+    D.BH = (int64_t)a->B * a->Hq;
+    D.BK = (int64_t)a->B * a->Hkv;
+    const int self = a->is_cross ? 0 : 1;
+    D.Kw = a->is_cross ? 0 : 2 * a->window + 1;
+    const int64_t Kall = (int64_t)D.Kw + a->G + D.kk;
+    if (a->mode == SSA_GRAPH_FULL) {
+        SSA_CHECK_ARG(a->total_k >= 1, "build_graph: total_k");
+        SSA_CHECK_ARG(a->out_valid, "build_graph: out_valid is null");
+        SSA_CHECK_ARG(a->is_cross || a->N == a->M, "build_graph: self-attention needs N == M");
+        SSA_CHECK_ARG(a->window >= 0, "build_graph: window");
+        const int64_t ks = self ? (a->total_k - 1 < Kall ? a->total_k - 1 : Kall)
+                                : (a->total_k < Kall ? a->total_k : Kall);
+        D.Kout = (int)(self + ks);
+    } else {
+        D.Kout = D.kk;
+    }
+    SSA_CHECK_ARG(!a->causal || a->N <= a->M, "build_graph: causal needs N <= M");
+    const int nch = D.nlists * D.CPL;
+    if (!maxch_for(nch)) {
+        ssa_set_error("build_graph: candidate stream of %lld slots (%d chunks) above the "
+                      "register-resident limit of 128 chunks of 64",
+                      (long long)D.Call, nch);
+        return SSA_E_UNSUP;
+    }
+    // chunk the query heads so the score buffer stays near 2 GiB
+    const int64_t per_bh = (int64_t)a->N * D.Call * 4;
+    int64_t nbh = ((int64_t)2 << 30) / (per_bh > 0 ? per_bh : 1);
+    if (nbh < 1) nbh = 1;
+    if (nbh > D.BH) nbh = D.BH;
+    D.nbh_chunk = (int)nbh;
+    return SSA_OK;
+}
+
+template <typename T>
+int launch_hash(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws,
+                hipStream_t st) {
+    HashP hp{};
+    hp.planes = a->rand_proj;
+    hp.R = D.R; hp.maxP = D.maxP; hp.P = D.P; hp.Tp = D.Tp; hp.NS = D.NS; hp.d = D.d;
+    // keys
+    hp.x = a->k.ptr; hp.sb = a->k.sb; hp.sh = a->k.sh; hp.sn = a->k.sn;
+    hp.nh = D.Hkv; hp.L = D.M; hp.inj = a->k_proj; hp.key_layout = 1;
+    hp.out = (uint16_t *)(ws + L.kid);
+    hp.rows = D.BK * D.M;
+    hipLaunchKernelGGL(hash_kernel<T>, dim3((unsigned)ceil_div(hp.rows, 256)), dim3(256), 0, st, hp);
+    SSA_CHECK_LAUNCH();
+    // queries
+    hp.x = a->q.ptr; hp.sb = a->q.sb; hp.sh = a->q.sh; hp.sn = a->q.sn;
+    hp.nh = D.Hq; hp.L = D.N; hp.inj = a->q_proj; hp.key_layout = 0;
+    hp.out = (uint16_t *)(ws + L.qid);
+    hp.rows = D.BH * D.N;
+    hipLaunchKernelGGL(hash_kernel<T>, dim3((unsigned)ceil_div(hp.rows, 256)), dim3(256), 0, st, hp);
+    SSA_CHECK_LAUNCH();
+    return SSA_OK;
+}
+
+template <typename T, int Dh>
+int launch_rescore(const RsP &rp, int64_t grid, hipStream_t st) {
+    const size_t lds = (size_t)(TQ + TC) * (Dh + 1) * 4 + (TQ + TC) * 4;
+    SSA_CHECK_HIP(hipFuncSetAttribute((const void *)rescore_kernel<T, Dh>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    hipLaunchKernelGGL((rescore_kernel<T, Dh>), dim3((unsigned)grid), dim3(256), lds, st, rp);
+    SSA_CHECK_LAUNCH();
+    return SSA_OK;
+}
+
+template <typename T>
+int rescore_dispatch(int d, const RsP &rp, int64_t grid, hipStream_t st) {
+    switch (d) {
+        case 4: return launch_rescore<T, 4>(rp, grid, st);
+        case 8: return launch_rescore<T, 8>(rp, grid, st);
+        case 16: return launch_rescore<T, 16>(rp, grid, st);
+        case 32: return launch_rescore<T, 32>(rp, grid, st);
+        case 64: return launch_rescore<T, 64>(rp, grid, st);
+        case 128: return launch_rescore<T, 128>(rp, grid, st);
+        case 256: return launch_rescore<T, 256>(rp, grid, st);
+    }
+    ssa_set_error("rescore: head dim %d", d);
+    return SSA_E_UNSUP;
+}
+
+template <typename T, int MC>
+int launch_select_mc(const SelP &sp, hipStream_t st) {
+    const size_t lds = (size_t)SEL_WAVES * (sp.words + 3 * sp.kk) * 4;
+    SSA_CHECK_HIP(hipFuncSetAttribute((const void *)select_kernel<T, MC>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    const int64_t grid = 8 * ceil_div(sp.nblocks, 8);
+    hipLaunchKernelGGL((select_kernel<T, MC>), dim3((unsigned)grid), dim3(SEL_WAVES * SSA_WAVE),
+                       lds, st, sp);
+    SSA_CHECK_LAUNCH();
+    return SSA_OK;
+}
+
+template <typename T>
+int select_dispatch(int mc, const SelP &sp, hipStream_t st) {
+    switch (mc) {
+        case 8: return launch_select_mc<T, 8>(sp, st);
+        case 16: return launch_select_mc<T, 16>(sp, st);
+        case 32: return launch_select_mc<T, 32>(sp, st);
+        case 48: return launch_select_mc<T, 48>(sp, st);
+        case 64: return launch_select_mc<T, 64>(sp, st);
+        case 96: return launch_select_mc<T, 96>(sp, st);
+        case 128: return launch_select_mc<T, 128>(sp, st);
+    }
+    ssa_set_error("select: chunk count %d", mc);
+    return SSA_E_UNSUP;
+}
+
+template <typename T>
+int build_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws,
+                hipStream_t st) {
+    int rc = launch_hash<T>(D, a, L, ws, st);
+    if (rc) return rc;
+    rc = ssa_launch_bucket_sort((const uint16_t *)(ws + L.kid), (int)(D.BK * D.R), D.M, D.P,
+                                (int32_t *)(ws + L.perm), (int32_t *)(ws + L.bstart),
+                                (int32_t *)(ws + L.bsize), (uint16_t *)(ws + L.sorttmp), st);
+    if (rc) return rc;
+    const size_t sel_lds = (size_t)SEL_WAVES * ((D.M + 31) / 32 + 1 + 3 * D.kk) * 4;
+    if (sel_lds > SSA_LDS_BYTES) {
+        ssa_set_error("build_graph: select needs %zu bytes of LDS", sel_lds);
+        return SSA_E_UNSUP;
+    }
+    for (int64_t bh0 = 0; bh0 < D.BH; bh0 += D.nbh_chunk) {
+        const int nbh = (int)((D.BH - bh0) < D.nbh_chunk ? (D.BH - bh0) : D.nbh_chunk);
+        const int ninst = nbh * D.R * D.NS;
+        QbP qp{};
+        qp.qid = (const uint16_t *)(ws + L.qid);
+        qp.bsize = (const int32_t *)(ws + L.bsize);
+        qp.cnt = (int32_t *)(ws + L.cnt);
+        qp.off = (int32_t *)(ws + L.off);
+        qp.cur = (int32_t *)(ws + L.cur);
+        qp.qlist = (int32_t *)(ws + L.qlist);
+        qp.tiles = (int32_t *)(ws + L.tiles);
+        qp.ntiles = (int32_t *)(ws + L.ntiles);
+        qp.N = D.N; qp.R = D.R; qp.NS = D.NS; qp.NB = D.NB; qp.Hq = D.Hq; qp.Hkv = D.Hkv;
+        qp.rep = D.rep; qp.bh0 = (int)bh0; qp.ninst = ninst;
+        const int64_t ncnt = (int64_t)ninst * D.NB;
+        hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(ncnt, 256), 4096)),
+                           dim3(256), 0, st, qp.cnt, ncnt, 0);
+        SSA_CHECK_LAUNCH();
+        hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(64), 0, st, qp.ntiles, (int64_t)1, 0);
+        SSA_CHECK_LAUNCH();
+        const dim3 gq((unsigned)ceil_div(D.N, 256), (unsigned)ninst);
+        hipLaunchKernelGGL(qb_hist_kernel, gq, dim3(256), (size_t)D.NB * 4, st, qp);
+        SSA_CHECK_LAUNCH();
+        hipLaunchKernelGGL(qb_scan_kernel, dim3((unsigned)ninst), dim3(256), 0, st, qp);
+        SSA_CHECK_LAUNCH();
+        hipLaunchKernelGGL(qb_scatter_kernel, gq, dim3(256), 0, st, qp);
+        SSA_CHECK_LAUNCH();
+
+        RsP rp{};
+        rp.tiles = qp.tiles; rp.ntiles = qp.ntiles; rp.qlist = qp.qlist;
+        rp.perm = (const int32_t *)(ws + L.perm);
+        rp.bstart = (const int32_t *)(ws + L.bstart);
+        rp.bsize = (const int32_t *)(ws + L.bsize);
+        rp.q = a->q.ptr; rp.k = a->k.ptr;
+        rp.qsb = a->q.sb; rp.qsh = a->q.sh; rp.qsn = a->q.sn;
+        rp.ksb = a->k.sb; rp.ksh = a->k.sh; rp.ksn = a->k.sn;
+        rp.S = (float *)(ws + L.S);
+        rp.N = D.N; rp.M = D.M; rp.R = D.R; rp.NS = D.NS; rp.NB = D.NB; rp.C = D.C;
+        rp.Hq = D.Hq; rp.Hkv = D.Hkv; rp.rep = D.rep; rp.bh0 = (int)bh0; rp.Call = D.Call;
+        const int64_t grid = (int64_t)ninst * (ceil_div(D.N, TQ) + D.NB);
+        rc = rescore_dispatch<T>(D.d, rp, grid, st);
+        if (rc) return rc;
+
+        SelP sp{};
+        sp.qid = qp.qid; sp.perm = rp.perm; sp.bstart = rp.bstart; sp.bsize = rp.bsize;
+        sp.S = rp.S; sp.q = a->q.ptr; sp.k = a->k.ptr;
+        sp.qsb = a->q.sb; sp.qsh = a->q.sh; sp.qsn = a->q.sn;
+        sp.ksb = a->k.sb; sp.ksh = a->k.sh; sp.ksn = a->k.sn;
+        sp.glob = a->glob;
+        sp.N = D.N; sp.M = D.M; sp.d = D.d; sp.R = D.R; sp.NS = D.NS; sp.NB = D.NB; sp.C = D.C;
+        sp.CPL = D.CPL; sp.nlists = D.nlists; sp.Hq = D.Hq; sp.Hkv = D.Hkv; sp.rep = D.rep;
+        sp.G = D.G; sp.kk = D.kk; sp.window = a->window; sp.causal = a->causal;
+        sp.cross = a->is_cross; sp.mode = a->mode; sp.total_k = a->total_k; sp.Kw = D.Kw;
+        sp.Kout = D.Kout; sp.bh0 = (int)bh0; sp.words = (D.M + 31) / 32 + 1;
+        sp.Call = D.Call; sp.rows = (int64_t)nbh * D.N;
+        sp.out_idx = a->out_idx; sp.out_valid = a->out_valid; sp.ties = a->out_ties;
+        sp.nblocks = ceil_div(sp.rows, SEL_WAVES);
+        rc = select_dispatch<T>(maxch_for(D.nlists * D.CPL), sp, st);
+        if (rc) return rc;
+    }
+    return SSA_OK;
+}
+
+}  // namespace
+
+extern "C" int64_t ssa_graph_out_width(const ssa_graph_args *a) {
+    Dims D;
+    if (make_dims(a, D)) return -1;
+    return D.Kout;
+}
+
+extern "C" int64_t ssa_graph_workspace_bytes(const ssa_graph_args *a) {
+    Dims D;
+    if (make_dims(a, D)) return -1;
+    return plan(D).total;
+}
+
+extern "C" int ssa_build_graph(const ssa_graph_args *a, void *workspace, int64_t workspace_bytes,
+                               void *stream) {
+    Dims D;
+    int rc = make_dims(a, D);
+    if (rc) return rc;
+    const Layout L = plan(D);
+    if (workspace_bytes < L.total || !workspace) {
+        ssa_set_error("build_graph: workspace %lld < %lld bytes", (long long)workspace_bytes,
+                      (long long)L.total);
+        return SSA_E_WORKSPACE;
+    }
+    hipStream_t st = (hipStream_t)stream;
+    char *ws = (char *)workspace;
+    switch (a->q.dtype) {
+        case SSA_F32: return build_typed<float>(D, a, L, ws, st);
+        case SSA_BF16: return build_typed<bf16_t>(D, a, L, ws, st);
+        case SSA_F16: return build_typed<f16_t>(D, a, L, ws, st);
+    }
+    return SSA_E_ARG;
+}

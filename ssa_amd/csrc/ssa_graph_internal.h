@@ -1,0 +1,12 @@
+// ssa_graph_internal.h -- launchers shared between the graph-build sources.
+#pragma once
+
+#include "ssa_common.h"
+
+// LDS a workgroup may use on gfx950 (160 KiB), minus room for static shared data
+#define SSA_LDS_BYTES (160 * 1024 - 512)
+
+int ssa_sort_supported(int n);
+int64_t ssa_sort_tmp_bytes(int rows, int n);
+int ssa_launch_bucket_sort(const uint16_t *ids, int rows, int n, int P, int32_t *perm,
+                           int32_t *bstart, int32_t *bsize, uint16_t *tmp, hipStream_t st);

@@ -1,0 +1,161 @@
+"""Host-side contract of the drop-in API (CPU only, no kernels).
+
+Seeded construction must reproduce the reference's weights and hyperplanes
+bit-for-bit (same RNG consumption order), so checkpoints and seeds carry over.
+"""
+import warnings
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import golden_files, load_golden
+from ssa_amd import (GlobalGraphBuilder, LSHGraphBuilder, SparseAttention, SparseTransformer,
+                     SSAConfig, SubquadraticRegimeTracker, WindowGraphBuilder)
+
+
+@pytest.mark.parametrize("path", golden_files()[::2], ids=lambda p: p.split("/")[-1])
+def test_seeded_construction_matches_reference_state_dict(path):
+    z, m = load_golden(path)
+    cfg = SSAConfig(**m["config"])
+    torch.manual_seed(m["seed"])
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")
+        attn = SparseAttention(cfg)
+    sd = attn.state_dict()
+    ref_keys = sorted(k[3:] for k in z.files if k.startswith("sd_"))
+    assert sorted(sd.keys()) == ref_keys
+    for key in ref_keys:
+        np.testing.assert_array_equal(sd[key].numpy(), z["sd_" + key])
+
+
+def test_config_defaults_match_reference():
+    c = SSAConfig()
+    assert (c.d_model, c.num_heads, c.num_kv_heads, c.num_neighbors, c.max_num_hashes,
+            c.num_hash_rounds, c.lsh_num_probes, c.window_size, c.num_global_tokens,
+            c.global_token_indices, c.dropout, c.causal, c.fp32_attn_weights) == (
+        512, 8, None, 128, 12, 8, 0, 8, 2, None, 0.0, False, False)
+
+
+@pytest.mark.parametrize("M,C,maxp,exp", [(1024, 432, 12, 1), (4096, 368, 12, 3),
+                                          (32768, 748, 12, 5), (512, 208, 12, 1),
+                                          (8192, 368, 12, 4), (1, 10, 12, 1), (100, 0, 12, 1),
+                                          (10 ** 7, 1, 12, 12), (181, 64, 12, 1),
+                                          (182, 64, 12, 2)])
+def test_effective_p_closed_form(M, C, maxp, exp):
+    assert LSHGraphBuilder.compute_effective_p(M, C, maxp) == exp
+
+
+def test_effective_p_uses_python_round_half_even():
+    # log2(M / C) = 2.5 exactly -> round half to even -> 2
+    M, C = int(64 * 2 ** 0.5 * 100), 100
+    p = LSHGraphBuilder.compute_effective_p(M, C, 12)
+    assert p == round(np.log2(M / C))
+
+
+def test_lsh_k_and_candidates():
+    attn = SparseAttention(SSAConfig(d_model=4096, num_heads=32, num_kv_heads=8,
+                                     num_neighbors=128, window_size=16, num_global_tokens=2,
+                                     num_hash_rounds=8, causal=True))
+    assert attn.lsh_k == 128 - (33 + 2 + 1) == 92
+    assert attn.lsh_builder.C == 368
+    assert attn.kv_rep == 4 and attn.d_head == 128
+
+
+def test_window_builder_closed_form():
+    w = WindowGraphBuilder(3, causal=True)(10, 10, "cpu")
+    for n in range(10):
+        exp = [min(max(n + o, 0), 9) if o <= 0 else n for o in range(-3, 4)]
+        assert w[n].tolist() == exp
+    w2 = WindowGraphBuilder(2)(5, 5, "cpu")
+    assert w2[4].tolist() == [2, 3, 4, 4, 4]
+
+
+def test_global_builder():
+    assert GlobalGraphBuilder(2, [0, 5, 17])(32, "cpu").tolist() == [0, 5, 17]
+    assert GlobalGraphBuilder(2, [0, 100, 200])(32, "cpu").tolist() == [0, 31, 31]
+    assert GlobalGraphBuilder(3)(32, "cpu").tolist() == [0, 1, 2]
+    assert GlobalGraphBuilder(3)(2, "cpu").tolist() == [0, 1]
+
+
+def test_probe_helper_matches_reference_vectors():
+    for path in golden_files():
+        z, m = load_golden(path)
+        if m["config"]["lsh_num_probes"] == 0:
+            continue
+        torch.manual_seed(0)
+        lsh = LSHGraphBuilder(d_head=m["d_head"], lsh_candidates=m["C"], num_rounds=1,
+                              max_num_hashes=m["config"]["max_num_hashes"],
+                              num_probes=m["config"]["lsh_num_probes"])
+        proj = torch.from_numpy(z["qproj"][:, 0])
+        got = lsh._probe_ids(proj, m["p_eff"], m["config"]["lsh_num_probes"])
+        got = torch.stack(got, -1).numpy() if got else np.zeros(proj.shape[:2] + (0,))
+        np.testing.assert_array_equal(got, z["probes0"])
+
+
+def test_assertions_and_warnings():
+    with pytest.raises(AssertionError):
+        SparseAttention(SSAConfig(d_model=64, num_heads=5, num_kv_heads=2))
+    with pytest.raises(AssertionError):
+        SparseAttention(SSAConfig(d_model=66, num_heads=4))
+    with pytest.raises(AssertionError):
+        LSHGraphBuilder(8, 8, max_num_hashes=13)
+    with pytest.raises(AssertionError):
+        LSHGraphBuilder(8, 8, num_probes=-1)
+    with pytest.warns(UserWarning, match="exceeds"):
+        SparseAttention(SSAConfig(d_model=32, num_heads=2, num_neighbors=16, window_size=16))
+
+
+def test_attention_mask_guard_raises_value_error():
+    attn = SparseAttention(SSAConfig(d_model=32, num_heads=2, num_neighbors=16))
+    with pytest.raises(ValueError, match="attention_mask"):
+        attn(torch.randn(1, 8, 32), attention_mask=torch.ones(1, 8))
+
+
+def test_cpu_tensors_raise_instead_of_falling_back():
+    attn = SparseAttention(SSAConfig(d_model=32, num_heads=2, num_neighbors=16,
+                                     max_num_hashes=2, window_size=2))
+    with pytest.raises(RuntimeError, match="ROCm"):
+        attn(torch.randn(1, 8, 32))
+
+
+def test_kv_param_counts_scale_with_kv_heads():
+    def kvp(n_kv):
+        a = SparseAttention(SSAConfig(d_model=64, num_heads=4, num_kv_heads=n_kv,
+                                      num_neighbors=16, window_size=4, max_num_hashes=3))
+        return a.Wk.weight.numel() + a.Wv.weight.numel()
+    assert kvp(1) * 4 == kvp(4) and kvp(2) * 2 == kvp(4)
+
+
+def test_split_helpers():
+    attn = SparseAttention(SSAConfig(d_model=64, num_heads=4, num_kv_heads=2))
+    x = torch.randn(2, 5, 64)
+    assert torch.equal(attn._split(x), attn._split_q(x))
+    kv = torch.randn(2, 5, 32)
+    e = attn._split_kv(kv)
+    c = attn._split_kv_compact(kv)
+    assert e.shape == (2, 4, 5, 16) and c.shape == (2, 2, 5, 16)
+    for h in range(4):
+        assert torch.equal(e[:, h], c[:, h // 2])
+
+
+def test_regime_tracker():
+    t = SubquadraticRegimeTracker()
+    t.record(128, 32, 4, 128)
+    t.record(512, 32, 4, 128)
+    assert t.check(warn=False)
+    t.record(1024, 64, 4, 128)
+    with pytest.warns(UserWarning, match="SubquadraticRegimeTracker"):
+        assert t.check() is False
+
+
+def test_transformer_structure_and_state_keys():
+    cfg = SSAConfig(d_model=32, num_heads=2, num_neighbors=12, max_num_hashes=2, window_size=3,
+                    num_global_tokens=1)
+    m = SparseTransformer(cfg, num_layers=2, vocab_size=50)
+    keys = set(m.state_dict().keys())
+    for k in ["embed.weight", "layers.0.attn.Wq.weight", "layers.1.attn.lsh_builder.rand_proj",
+              "layers.0.ff.0.weight", "layers.0.ff.3.bias", "layers.0.norm1.weight",
+              "norm.bias"]:
+        assert k in keys
+    assert SparseTransformer(cfg, num_layers=1).embed is None
