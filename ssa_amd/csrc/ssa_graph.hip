@@ -638,7 +638,7 @@ int make_dims(const ssa_graph_args *a, Dims &D) {
     SSA_CHECK_ARG(a->R >= 1 && a->C >= 1 && a->top_k >= 1 && a->T >= 0, "build_graph: R/C/top_k/T");
     SSA_CHECK_ARG(a->G >= 0 && a->G <= 63, "build_graph: G=%d outside 0..63", a->G);
     SSA_CHECK_ARG(a->rand_proj || (a->q_proj && a->k_proj), "build_graph: no hyperplanes");
-    SSA_CHECK_ARG(a->q.ptr && a->k.ptr && a->out_idx, "build_graph: null tensor");
+    SSA_CHECK_ARG(a->q.ptr && a->k.ptr, "build_graph: null q/k");
     SSA_CHECK_ARG(a->q.dtype == a->k.dtype && a->q.dtype >= 0 && a->q.dtype <= 2,
                   "build_graph: q/k dtype");
     SSA_CHECK_ARG(a->G == 0 || a->glob, "build_graph: glob is null");
@@ -668,7 +668,6 @@ int make_dims(const ssa_graph_args *a, Dims &D) {
     const int64_t Kall = (int64_t)D.Kw + a->G + D.kk;
     if (a->mode == SSA_GRAPH_FULL) {
         SSA_CHECK_ARG(a->total_k >= 1, "build_graph: total_k");
-        SSA_CHECK_ARG(a->out_valid, "build_graph: out_valid is null");
         SSA_CHECK_ARG(a->is_cross || a->N == a->M, "build_graph: self-attention needs N == M");
         SSA_CHECK_ARG(a->window >= 0, "build_graph: window");
         const int64_t ks = self ? (a->total_k - 1 < Kall ? a->total_k - 1 : Kall)
@@ -865,6 +864,8 @@ extern "C" int ssa_build_graph(const ssa_graph_args *a, void *workspace, int64_t
     Dims D;
     int rc = make_dims(a, D);
     if (rc) return rc;
+    SSA_CHECK_ARG(a->out_idx, "build_graph: out_idx is null");
+    SSA_CHECK_ARG(a->mode != SSA_GRAPH_FULL || a->out_valid, "build_graph: out_valid is null");
     const Layout L = plan(D);
     if (workspace_bytes < L.total || !workspace) {
         ssa_set_error("build_graph: workspace %lld < %lld bytes", (long long)workspace_bytes,
