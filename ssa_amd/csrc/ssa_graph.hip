@@ -39,6 +39,9 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <algorithm>
+#include <type_traits>
+
 #include "ssa_common.h"
 #include "ssa_graph_internal.h"
 
@@ -54,6 +57,10 @@ struct Dims {
     int nbh_chunk;
 };
 
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
 // ------------------------------------------------------------------ hashing
 struct HashP {
     const void *x;
@@ -64,6 +71,7 @@ struct HashP {
     const float *inj;
     uint16_t *out;
     int key_layout;
+    int vec16;          // rows 16-byte aligned: quarter rows load with 16-byte loads
     int64_t rows;
 };
 
@@ -122,6 +130,115 @@ __global__ void __launch_bounds__(256) hash_kernel(HashP p) {
                         if (q == t) pos = ord[q];
                     o[1 + t] = (uint16_t)(id ^ (1 << pos));
                 }
+            }
+        }
+    }
+}
+
+// bucket id and probe ids of one row from its P projections (plane j = bit j)
+__device__ __forceinline__ void write_ids(const float *pr, int P, int Tp, uint16_t *o) {
+    int id = 0;
+    for (int j = 0; j < P; ++j)
+        if (pr[j] > 0.f) id |= 1 << j;
+    o[0] = (uint16_t)id;
+    for (int t = 0; t < Tp; ++t) {
+        // plane whose stable rank of |proj| is t
+        int pos = 0;
+        for (int j = 0; j < P; ++j) {
+            const float aj = fabsf(pr[j]);
+            int rank = 0;
+            for (int q = 0; q < P; ++q) {
+                const float aq = fabsf(pr[q]);
+                rank += (aq < aj) || (aq == aj && q < j);
+            }
+            if (rank == t) pos = j;
+        }
+        o[1 + t] = (uint16_t)(id ^ (1 << pos));
+    }
+}
+
+// Projection on the matrix cores: v_mfma_f32_16x16x4f32 computes a 16 x 16 block
+// of rows x planes, lane l feeding row (l % 16) and plane (l % 16) with the
+// element k = l / 16 of the step.  The reduction over the head dim is split so
+// that lane group g = l / 16 walks the contiguous quarter [g*d/4, (g+1)*d/4):
+// every lane loads its quarter row once with wide loads.  One wavefront handles
+// 16 rows against all R*P planes (staged in LDS, fp32, row stride d+1).
+template <typename T, int D>
+__global__ void __launch_bounds__(256) hash_mfma_kernel(HashP p) {
+    constexpr int DQ = D / 4;
+    extern __shared__ float hs[];
+    const int NP = p.R * p.P;
+    const int NT = (NP + 15) / 16;
+    float *W = hs;                                    // [NT*16][D+1]
+    float *proj = W + NT * 16 * (D + 1);              // [4 waves][16][NT*16 + 1]
+    const int pst = NT * 16 + 1;
+    for (int x = threadIdx.x; x < NT * 16 * D; x += blockDim.x) {
+        const int j = x / D, e = x % D;
+        float w = 0.f;
+        if (j < NP) w = p.planes[((int64_t)(j / p.P) * p.maxP + (j % p.P)) * D + e];
+        W[j * (D + 1) + e] = w;
+    }
+    __syncthreads();
+    const int wid = threadIdx.x / SSA_WAVE;
+    const int lane = lane_id();
+    const int li = lane % 16, lg = lane / 16;
+    const int64_t row0 = ((int64_t)blockIdx.x * 4 + wid) * 16;
+    if (row0 >= p.rows) return;
+    const int64_t row = row0 + li;
+    float xs[DQ];
+    if (row < p.rows) {
+        const int i = (int)(row % p.L);
+        const int64_t bh = row / p.L;
+        const T *x = (const T *)p.x + (bh / p.nh) * p.sb + (bh % p.nh) * p.sh + (int64_t)i * p.sn +
+                     lg * DQ;
+        constexpr int PER16 = 16 / (int)sizeof(T);
+        if constexpr (DQ % PER16 == 0) {
+            if (p.vec16) {
+#pragma unroll
+                for (int e0 = 0; e0 < DQ; e0 += PER16) {
+                    const uint4 w = *reinterpret_cast<const uint4 *>(x + e0);
+                    const T *tv = reinterpret_cast<const T *>(&w);
+#pragma unroll
+                    for (int e = 0; e < PER16; ++e) xs[e0 + e] = to_f32(tv[e]);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < DQ; ++e) xs[e] = to_f32(x[e]);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < DQ; ++e) xs[e] = to_f32(x[e]);
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < DQ; ++e) xs[e] = 0.f;
+    }
+    float *pw = proj + wid * 16 * pst;
+    for (int t = 0; t < NT; ++t) {
+        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+        const float *wr = W + (t * 16 + li) * (D + 1) + lg * DQ;
+#pragma unroll
+        for (int s = 0; s < DQ; ++s)
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xs[s], wr[s], acc, 0, 0, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pw[(4 * lg + r) * pst + t * 16 + li] = acc[r];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane < 16 && row0 + lane < p.rows) {
+        const int64_t rw = row0 + lane;
+        const int i = (int)(rw % p.L);
+        const int64_t bh = rw / p.L;
+        for (int r = 0; r < p.R; ++r) {
+            const float *pr = pw + lane * pst + r * p.P;
+            if (p.key_layout) {
+                int id = 0;
+                for (int j = 0; j < p.P; ++j)
+                    if (pr[j] > 0.f) id |= 1 << j;
+                p.out[(bh * p.R + r) * p.L + i] = (uint16_t)id;
+            } else {
+                write_ids(pr, p.P, p.Tp, p.out + ((bh * p.L + i) * p.R + r) * p.NS);
             }
         }
     }
@@ -217,14 +334,26 @@ __global__ void __launch_bounds__(256) qb_scan_kernel(QbP p) {
 }
 
 __global__ void __launch_bounds__(256) qb_scatter_kernel(QbP p) {
+    // block-local ranks first, then one global reservation per (block, bucket)
+    extern __shared__ int32_t sc_smem[];
+    int32_t *hist = sc_smem;          // [NB]
+    int32_t *base = sc_smem + p.NB;   // [NB]
     const int inst = blockIdx.y;
     int bh, r, t;
     inst_decode(p, inst, bh, r, t);
+    for (int u = threadIdx.x; u < p.NB; u += blockDim.x) hist[u] = 0;
+    __syncthreads();
     const int n = blockIdx.x * blockDim.x + threadIdx.x;
-    if (n >= p.N) return;
-    const int u = p.qid[(((int64_t)bh * p.N + n) * p.R + r) * p.NS + t];
-    const int pos = atomicAdd(&p.cur[(int64_t)inst * p.NB + u], 1);
-    p.qlist[(int64_t)inst * p.N + pos] = n;
+    int u = 0, local = 0;
+    if (n < p.N) {
+        u = p.qid[(((int64_t)bh * p.N + n) * p.R + r) * p.NS + t];
+        local = atomicAdd(&hist[u], 1);
+    }
+    __syncthreads();
+    for (int b = threadIdx.x; b < p.NB; b += blockDim.x)
+        if (hist[b]) base[b] = atomicAdd(&p.cur[(int64_t)inst * p.NB + b], hist[b]);
+    __syncthreads();
+    if (n < p.N) p.qlist[(int64_t)inst * p.N + base[u] + local] = n;
 }
 
 // ------------------------------------------------------------------ rescore
@@ -305,11 +434,122 @@ __global__ void __launch_bounds__(256) rescore_kernel(RsP p) {
     }
 }
 
+// Matrix-core rescore for 16-bit q/k.  v_mfma_f32_16x16x32_{bf16,f16}: lane l
+// supplies row (l % 16) of A and column (l % 16) of B, each with the 8
+// elements k = 8*(l/16) .. +7; result element (4*(l/16) + r, l % 16) lands in
+// accumulator r.  Products of 16-bit values are exact in fp32 and accumulate
+// in fp32, so a score equals an fp32 dot product up to summation order.
+// Each wave keeps the fragments of the tile's 64 queries in registers and
+// streams slices of 64 candidate rows (4 x 4 blocks of 16 x 16).
+
+template <typename T> struct Mfma16;
+template <> struct Mfma16<bf16_t> {
+    typedef bf16x8_t vec;
+    static __device__ __forceinline__ f32x4_t mma(vec a, vec b, f32x4_t c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+};
+template <> struct Mfma16<f16_t> {
+    typedef f16x8_t vec;
+    static __device__ __forceinline__ f32x4_t mma(vec a, vec b, f32x4_t c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    }
+};
+
+template <typename T, int D>
+__global__ void __launch_bounds__(256) rescore_mfma_kernel(RsP p) {
+    using V = typename Mfma16<T>::vec;
+    constexpr int KS = (D + 31) / 32;   // k steps of 32
+    __shared__ int nidx[TQ];
+    if ((int)blockIdx.x >= *p.ntiles) return;
+    const int32_t *e = p.tiles + (int64_t)blockIdx.x * 4;
+    const int inst = e[0], u = e[1], qb = e[2], qc = e[3];
+    const int t = inst % p.NS, r = (inst / p.NS) % p.R, bhl = inst / (p.NS * p.R);
+    const int bh = p.bh0 + bhl;
+    const int b = bh / p.Hq, h = bh % p.Hq, g = h / p.rep;
+    const int64_t prow = ((int64_t)b * p.Hkv + g) * p.R + r;
+    const int st = p.bstart[prow * p.NB + u];
+    const int nv = min(p.bsize[prow * p.NB + u], p.C);
+    const int tid = threadIdx.x;
+    const int wid = tid / SSA_WAVE;
+    const int lane = lane_id();
+    const int li = lane % 16, lg = lane / 16;
+    const T *qbase = (const T *)p.q + b * p.qsb + h * p.qsh;
+    const T *kbase = (const T *)p.k + b * p.ksb + g * p.ksh;
+    if (tid < TQ) nidx[tid] = tid < qc ? p.qlist[(int64_t)inst * p.N + qb + tid] : 0;
+    __syncthreads();
+
+    V qa[4][KS];
+#pragma unroll
+    for (int qt = 0; qt < 4; ++qt) {
+        const int row = qt * 16 + li;
+        const bool ok = row < qc;
+        const T *src = qbase + (int64_t)nidx[ok ? row : 0] * p.qsn;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            const int e0 = 32 * s + 8 * lg;
+            if (ok && e0 < D) {
+                const uint4 w = *reinterpret_cast<const uint4 *>(src + e0);
+                qa[qt][s] = __builtin_bit_cast(V, w);
+            } else {
+                qa[qt][s] = __builtin_bit_cast(V, make_uint4(0, 0, 0, 0));
+            }
+        }
+    }
+    const int64_t slotbase = (int64_t)(r * p.NS + t) * p.C;
+    const int32_t *pr = p.perm + prow * p.M + st;
+    for (int c0 = wid * 64; c0 < nv; c0 += 4 * 64) {
+        V kb[4][KS];
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) {
+            const int cand = c0 + ct * 16 + li;
+            const bool ok = cand < nv;
+            const T *src = kbase + (int64_t)(ok ? pr[cand] : 0) * p.ksn;
+#pragma unroll
+            for (int s = 0; s < KS; ++s) {
+                const int e0 = 32 * s + 8 * lg;
+                if (ok && e0 < D) {
+                    const uint4 w = *reinterpret_cast<const uint4 *>(src + e0);
+                    kb[ct][s] = __builtin_bit_cast(V, w);
+                } else {
+                    kb[ct][s] = __builtin_bit_cast(V, make_uint4(0, 0, 0, 0));
+                }
+            }
+        }
+        f32x4_t acc[4][4];
+#pragma unroll
+        for (int qt = 0; qt < 4; ++qt)
+#pragma unroll
+            for (int ct = 0; ct < 4; ++ct) acc[qt][ct] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < KS; ++s)
+#pragma unroll
+            for (int qt = 0; qt < 4; ++qt)
+#pragma unroll
+                for (int ct = 0; ct < 4; ++ct)
+                    acc[qt][ct] = Mfma16<T>::mma(qa[qt][s], kb[ct][s], acc[qt][ct]);
+#pragma unroll
+        for (int qt = 0; qt < 4; ++qt) {
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const int row = qt * 16 + 4 * lg + rr;
+                if (row >= qc) continue;
+                float *srow = p.S + ((int64_t)bhl * p.N + nidx[row]) * p.Call + slotbase;
+#pragma unroll
+                for (int ct = 0; ct < 4; ++ct) {
+                    const int cand = c0 + ct * 16 + li;
+                    if (cand < nv) srow[cand] = acc[qt][ct][rr];
+                }
+            }
+        }
+    }
+}
+
 // ------------------------------------------------------------------ select + merge
 struct SelP {
     const uint16_t *qid;
     const int32_t *perm, *bstart, *bsize;
-    const float *S;
+    float *S;
     const void *q, *k;
     int64_t qsb, qsh, qsn, ksb, ksh, ksn;
     const int64_t *glob;
@@ -345,38 +585,86 @@ __device__ __forceinline__ int wave_excl_scan(int v) {
 }
 
 template <typename T>
-struct SelCtx {
-    const SelP &p;
-    int n, bh, bk;
-    int64_t row;
-    float qv[4];
-    const T *kbase;
-    __device__ SelCtx(const SelP &pp) : p(pp) {}
-    __device__ float dotk(int v) const {
-        const int lane = lane_id();
-        float s = 0.f;
+__device__ __forceinline__ float dot_row(const float (&qv)[4], const T *krow, int d) {
+    const int lane = lane_id();
+    float s = 0.f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int e = lane + 64 * i;
-            if (e < p.d) s = fmaf(qv[i], to_f32(kbase[(int64_t)v * p.ksn + e]), s);
+    for (int i = 0; i < 4; ++i) {
+        const int e = lane + 64 * i;
+        if (e < d) s = fmaf(qv[i], to_f32(krow[e]), s);
+    }
+    return wave_sum(s);
+}
+
+__device__ __forceinline__ void wave_compiler_fence() {
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+}
+
+// sum over the wave of per-lane counts c in [0, 2^NB): one ballot per bit
+template <int NB>
+__device__ __forceinline__ int wave_count(int c) {
+    int s = 0;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) s += __popcll(wave_ballot((c >> b) & 1)) << b;
+    return s;
+}
+
+constexpr int SEL_CAP = 512;   // keys kept in LDS for the exact threshold search
+
+// Per-wave LDS of the select kernel, in 32-bit words:
+//   bm    [words]     seen bitmap, later the merge bitmap
+//   kmask [2*nch]     per 64-slot chunk, the ballot of kept slots
+//   ckey  [SEL_CAP]   sample of kept keys, then kept keys >= the lower bound
+//   cslot [SEL_CAP]   stream slot of each compacted key
+//   gsc   [64]        scores of glob[0..G-1] and key 0 (empty buckets)
+//   LSH mode: ekey/eval/eslot [kk] the selected entries
+__host__ __device__ inline int sel_lds_words(int nch, int words, int kk, bool lsh) {
+    return (words + 2 * nch + 2 * SEL_CAP + 64 + (lsh ? 3 * kk : 0) + 1) & ~1;
+}
+
+// bitwise search for the largest t (over the top bits hi..lo_bit) with at
+// least kk of the wave's keys >= t; stops early once exactly kk keys are >= t.
+// Keys come from k[0..NK) per lane (0 = absent).
+template <int NK>
+__device__ __forceinline__ uint32_t kth_search(const uint32_t (&k)[NK], int kk, int lo_bit) {
+    uint32_t thr = 0u;
+#pragma unroll 1
+    for (int bit = 31; bit >= lo_bit; --bit) {
+        const uint32_t cand = thr | (1u << bit);
+        int c = 0;
+#pragma unroll
+        for (int i = 0; i < NK; ++i) c += k[i] >= cand;
+        const int tot = wave_count<4>(c);
+        if (tot >= kk) {
+            thr = cand;
+            if (tot == kk) break;
         }
-        return wave_sum(s);
     }
-    // key id held by stream slot (list, c)
-    __device__ int slot_value(int list, int c) const {
-        const int r = list / p.NS, t = list % p.NS;
-        const int u = p.qid[((int64_t)bh * p.N + n) * p.R * p.NS + r * p.NS + t];
-        const int64_t prow = (int64_t)bk * p.R + r;
-        const int sz = p.bsize[prow * p.NB + u];
-        if (sz == 0) return c < p.G ? (int)p.glob[c] : 0;
-        const int st = p.bstart[prow * p.NB + u];
-        const int nv = min(sz, p.C);
-        const int raw = p.perm[prow * p.M + (c < nv ? st + c : p.M - 1)];
-        return (p.causal && raw > n) ? n : raw;
-    }
+    return thr;
+}
+
+struct SelList {
+    int st, sz, nv;
+    const int32_t *pr;
 };
 
-template <typename T, int MAXCH>
+// One wavefront per query row, streaming over the query's candidate stream in
+// the reference's concatenation order (round, id set, slot):
+//  pass 1  key id and score of every slot; first occurrence in stream order,
+//          valid or not (:884-890), by test-and-set of the key's bit in LDS (a
+//          wave's LDS atomics complete in program order); the kept slots of
+//          each 64-slot chunk as one ballot; the first SEL_CAP kept keys as a
+//          sample.  Slots of a chunk holding the same key (the query itself
+//          after causal substitution, repeated zeros of an empty bucket) carry
+//          the same score, so whichever one wins gives the same selection.
+//  bound   the kk-th largest sample key over the top 16 bits bounds the
+//          threshold from below (the sample is a subset of the stream);
+//  pass 2  the kept keys >= the bound are compacted (key, slot) into LDS;
+//  search  exact kk-th largest over the compacted keys (bitwise, early exit);
+//  emit    selected = key > thr, or key == thr for the first `need` in stream
+//          order; LSH mode writes them by descending score, FULL mode merges
+//          them with the window and the globals through a key bitmap.
+template <typename T, bool LSH_MODE>
 __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     extern __shared__ uint32_t sel_smem[];
     const int64_t blk = xcd_logical_block(blockIdx.x, p.nblocks);
@@ -385,150 +673,240 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     const int64_t rloc = blk * SEL_WAVES + wid;
     if (rloc >= p.rows) return;
     const int lane = lane_id();
-    const int per_wave = p.words + 3 * p.kk;
-    uint32_t *bm = sel_smem + (int64_t)wid * per_wave;
-    uint32_t *ekey = bm + p.words;
+    const int nch = p.nlists * p.CPL;
+    uint32_t *bm = sel_smem + (int64_t)wid * sel_lds_words(nch, p.words, p.kk, LSH_MODE);
+    uint64_t *kmask = (uint64_t *)(bm + p.words);
+    uint32_t *ckey = (uint32_t *)(kmask + nch);
+    uint32_t *cslot = ckey + SEL_CAP;
+    float *gsc = (float *)(cslot + SEL_CAP);
+    uint32_t *ekey = (uint32_t *)(gsc + 64);
     uint32_t *eval = ekey + p.kk;
     uint32_t *eslot = eval + p.kk;
 
-    SelCtx<T> cx(p);
-    cx.n = (int)(rloc % p.N);
+    const int n = (int)(rloc % p.N);
     const int bhl = (int)(rloc / p.N);
-    cx.bh = p.bh0 + bhl;
-    const int b = cx.bh / p.Hq, h = cx.bh % p.Hq, g = h / p.rep;
-    cx.bk = b * p.Hkv + g;
-    cx.row = (int64_t)cx.bh * p.N + cx.n;
-    const int n = cx.n;
+    const int bh = p.bh0 + bhl;
+    const int b = bh / p.Hq, h = bh % p.Hq, g = h / p.rep;
+    const int bk = b * p.Hkv + g;
+    const int64_t row = (int64_t)bh * p.N + n;
     const T *qrow = (const T *)p.q + b * p.qsb + h * p.qsh + (int64_t)n * p.qsn;
-    cx.kbase = (const T *)p.k + b * p.ksb + g * p.ksh;
+    const T *kbase = (const T *)p.k + b * p.ksb + g * p.ksh;
+    float qv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int e = lane + 64 * i;
-        cx.qv[i] = e < p.d ? to_f32(qrow[e]) : 0.f;
+        qv[i] = e < p.d ? to_f32(qrow[e]) : 0.f;
     }
-    const float selfscore = p.causal ? cx.dotk(n) : 0.f;
+    const uint32_t kself =
+        p.causal ? score_key(dot_row<T>(qv, kbase + (int64_t)n * p.ksn, p.d)) : 0u;
+    const uint16_t *qids = p.qid + row * p.R * p.NS;
+    const float *srow = p.S + ((int64_t)bhl * p.N + n) * p.Call;
+    const int ng = min(p.G + 1, SSA_WAVE);
     for (int w = lane; w < p.words; w += SSA_WAVE) bm[w] = 0u;
+    bool gsc_ready = false;
     wave_lds_sync();
 
-    const float *srow = p.S + ((int64_t)bhl * p.N + n) * p.Call;
-    const uint16_t *qids = p.qid + cx.row * p.R * p.NS;
-    uint32_t key[MAXCH];
-    int st = 0, sz = 0, nv = 0;
-    int64_t prow = 0;
-#pragma unroll
-    for (int ci = 0; ci < MAXCH; ++ci) {
-        key[ci] = 0u;
-        const int list = ci / p.CPL;
-        if (list < p.nlists) {
-            const int cj = ci - list * p.CPL;
-            if (cj == 0) {
-                const int r = list / p.NS;
-                const int u = qids[list];
-                prow = (int64_t)cx.bk * p.R + r;
-                st = p.bstart[prow * p.NB + u];
-                sz = p.bsize[prow * p.NB + u];
-                nv = min(sz, p.C);
+    auto list_info = [&](int list) {
+        SelList L;
+        const int u = qids[list];
+        const int64_t prow = (int64_t)bk * p.R + list / p.NS;
+        L.sz = p.bsize[prow * p.NB + u];
+        L.st = p.bstart[prow * p.NB + u];
+        L.nv = min(L.sz, p.C);
+        L.pr = p.perm + prow * p.M;
+        return L;
+    };
+    // key id and score key of slot c of a list (c < C)
+    auto slot_kv = [&](const SelList &L, int list, int c, int &v, uint32_t &kv, bool &real) {
+        if (L.sz > 0) {
+            real = c < L.nv;
+            const int raw = L.pr[real ? L.st + c : p.M - 1];
+            v = (p.causal && raw > n) ? n : raw;
+            const float sc = srow[real ? (int64_t)list * p.C + c : 0];
+            kv = (p.causal && v == n) ? kself : score_key(sc);
+        } else {                                     // empty bucket: glob ++ 0
+            real = true;
+            const int j = c < ng - 1 ? c : ng - 1;
+            v = (c < p.G) ? (int)p.glob[j] : 0;
+            kv = score_key(gsc[j]);
+        }
+    };
+
+    // ---- pass 1
+    int nk = 0, nsamp = 0;
+    for (int list = 0; list < p.nlists; ++list) {
+        const SelList L = list_info(list);
+        if (L.sz == 0 && !gsc_ready) {               // scores of glob[0..G-1] and key 0
+            for (int j = 0; j < ng; ++j) {
+                const int v = j < p.G ? (int)p.glob[j] : 0;
+                const float sc = dot_row<T>(qv, kbase + (int64_t)v * p.ksn, p.d);
+                if (lane == 0) gsc[j] = sc;
             }
+            gsc_ready = true;
+            wave_lds_sync();
+        }
+        for (int cj = 0; cj < p.CPL; ++cj) {
             const int c = cj * SSA_WAVE + lane;
             const bool in_list = c < p.C;
-            if (sz == 0) {
-                if (cj == 0) {
-                    const int lim = min(p.C, p.G + 1);
-                    for (int cc = 0; cc < lim; ++cc) {
-                        const int v = cc < p.G ? (int)p.glob[cc] : 0;
-                        const bool seen = bm_test(bm, v);
-                        wave_lds_sync();
-                        if (!seen) {
-                            if (lane == 0) bm_set(bm, v);
-                            const float sc = cx.dotk(v);
-                            if (lane == cc) key[ci] = score_key(sc);
-                        }
-                        wave_lds_sync();
-                    }
-                }
-            } else {
-                const bool real = in_list && c < nv;
-                const int raw = in_list ? p.perm[prow * p.M + (real ? st + c : p.M - 1)] : 0;
-                const int v = (p.causal && raw > n) ? n : raw;
-                const bool seen = in_list ? bm_test(bm, v) : true;
-                const bool ck = real && !seen;
-                const uint64_t selfm = wave_ballot(ck && v == n);
-                const bool keep = ck && (v != n || lanes_below(selfm) == 0);
-                wave_lds_sync();
-                if (in_list) bm_set(bm, v);
-                wave_lds_sync();
-                if (keep) {
-                    const float sc = (p.causal && v == n) ? selfscore
-                                                          : srow[(int64_t)list * p.C + c];
-                    key[ci] = score_key(sc);
-                }
+            int v = 0;
+            uint32_t kv = 0u;
+            bool real = false;
+            if (in_list) slot_kv(L, list, c, v, kv, real);
+            const uint32_t bit = 1u << (v & 31);
+            const uint32_t old = atomicOr(&bm[v >> 5], (in_list & real) ? bit : 0u);
+            atomicOr(&bm[v >> 5], (in_list & !real) ? bit : 0u);   // fillers after the reals
+            const bool keep = in_list & real & ((old & bit) == 0u);
+            const uint64_t km = wave_ballot(keep);
+            if (lane == 0) kmask[list * p.CPL + cj] = km;
+            if (nsamp < SEL_CAP) {
+                const int pos = nsamp + lanes_below(km);
+                if (keep && pos < SEL_CAP) ckey[pos] = kv;
             }
+            nsamp += __popcll(km);
+            nk += __popcll(km);
         }
     }
+    wave_lds_sync();
 
-    // ---- exact top-kk threshold over the kept keys
-    int nk = 0;
-#pragma unroll
-    for (int ci = 0; ci < MAXCH; ++ci) nk += key[ci] != 0u;
-    nk = wave_sum_i(nk);
-    const int kk = p.kk;
-    uint32_t thr = 0u;
-    int need = 0;
-    if (nk > kk) {
-#pragma unroll 1
-        for (int bit = 31; bit >= 0; --bit) {
-            const uint32_t cand = thr | (1u << bit);
-            int cnt = 0;
-#pragma unroll
-            for (int ci = 0; ci < MAXCH; ++ci) cnt += key[ci] >= cand;
-            if (wave_sum_i(cnt) >= kk) thr = cand;
+    // re-walk the kept slots of the stream in order
+    auto walk_kept = [&](auto &&fn) {
+        for (int list = 0; list < p.nlists; ++list) {
+            const SelList L = list_info(list);
+            for (int cj = 0; cj < p.CPL; ++cj) {
+                const uint64_t km = kmask[list * p.CPL + cj];
+                if (km == 0ull) continue;
+                const int c = cj * SSA_WAVE + lane;
+                const bool keep = (km >> lane) & 1ull;
+                int v = 0;
+                uint32_t kv = 0u;
+                bool real = false;
+                if (keep) slot_kv(L, list, c, v, kv, real);
+                fn(keep, kv, v, list * p.C + c);
+            }
         }
-        int gt = 0, eq = 0;
+    };
+
+    // ---- threshold
+    const int kk = p.kk;
+    uint32_t thr = 0u;                 // 0: every kept key is selected
+    int need = 0;
+    int cnt = 0;
+    bool compacted = false;
+    if (nk > kk) {
+        uint32_t lo = 1u;
+        const int ns = nsamp < SEL_CAP ? nsamp : SEL_CAP;
+        if (ns >= kk) {
+            uint32_t sv[SEL_CAP / SSA_WAVE];
 #pragma unroll
-        for (int ci = 0; ci < MAXCH; ++ci) { gt += key[ci] > thr; eq += key[ci] == thr; }
-        gt = wave_sum_i(gt);
-        eq = wave_sum_i(eq);
-        need = kk - gt;
-        if (eq > need && lane == 0 && p.ties) atomicAdd(p.ties, 1);
+            for (int i = 0; i < SEL_CAP / SSA_WAVE; ++i) {
+                const int e = lane + SSA_WAVE * i;
+                sv[i] = e < ns ? ckey[e] : 0u;
+            }
+            lo = kth_search(sv, kk, 16);
+            if (lo == 0u) lo = 1u;
+        }
+        wave_lds_sync();
+        // pass 2: compact the kept keys >= lo with their stream slot
+        walk_kept([&](bool keep, uint32_t kv, int, int slot) {
+            const bool t = keep & (kv >= lo);
+            const uint64_t m = wave_ballot(t);
+            const int pos = cnt + lanes_below(m);
+            if (t && pos < SEL_CAP) { ckey[pos] = kv; cslot[pos] = (uint32_t)slot; }
+            cnt += __popcll(m);
+        });
+        wave_lds_sync();
+        if (cnt <= SEL_CAP) {
+            compacted = true;
+            uint32_t cv[SEL_CAP / SSA_WAVE];
+#pragma unroll
+            for (int i = 0; i < SEL_CAP / SSA_WAVE; ++i) {
+                const int e = lane + SSA_WAVE * i;
+                cv[i] = e < cnt ? ckey[e] : 0u;
+            }
+            thr = kth_search(cv, kk, 0);
+            int ge = 0, gt = 0;
+#pragma unroll
+            for (int i = 0; i < SEL_CAP / SSA_WAVE; ++i) { ge += cv[i] >= thr; gt += cv[i] > thr; }
+            ge = wave_count<4>(ge);
+            gt = wave_count<4>(gt);
+            need = kk - gt;
+            if (ge - gt > need && lane == 0 && p.ties) atomicAdd(p.ties, 1);
+        } else {
+            // rare: exact search over the whole kept stream (one walk per bit)
+            uint32_t t0 = 0u;
+            for (int bit = 31; bit >= 0; --bit) {
+                const uint32_t cand = t0 | (1u << bit);
+                int c = 0;
+                walk_kept([&](bool keep, uint32_t kv, int, int) {
+                    c += __popcll(wave_ballot(keep & (kv >= cand)));
+                });
+                if (c >= kk) t0 = cand;
+            }
+            thr = t0;
+            int ge = 0, gt = 0;
+            walk_kept([&](bool keep, uint32_t kv, int, int) {
+                ge += __popcll(wave_ballot(keep & (kv >= thr)));
+                gt += __popcll(wave_ballot(keep & (kv > thr)));
+            });
+            need = kk - gt;
+            if (ge - gt > need && lane == 0 && p.ties) atomicAdd(p.ties, 1);
+        }
     }
     const int f = nk < kk ? nk : kk;
 
     // ---- emit the selected slots
-    if (p.mode == SSA_GRAPH_FULL) {
+    if (!LSH_MODE) {
         for (int w = lane; w < p.words; w += SSA_WAVE) bm[w] = 0u;
         wave_lds_sync();
     }
-    int eq_before = 0, nsel = 0;
-#pragma unroll
-    for (int ci = 0; ci < MAXCH; ++ci) {
-        const uint32_t kv = key[ci];
-        const bool is_eq = (nk > kk) && kv == thr;
-        const uint64_t eqm = wave_ballot(is_eq);
-        bool sel = kv > thr || (is_eq && eq_before + lanes_below(eqm) < need);
-        if (kv == 0u) sel = false;
-        eq_before += __popcll(eqm);
-        const uint64_t sm = wave_ballot(sel);
-        if (sm) {
-            const int list = ci / p.CPL;
-            const int c = (ci - list * p.CPL) * SSA_WAVE + lane;
+    int nsel = 0, eq_before = 0;
+    auto take = [&](bool sel, uint32_t kv, int v, int slot) {
+        if (!LSH_MODE) {
+            atomicOr(&bm[v >> 5], sel ? (1u << (v & 31)) : 0u);
+        } else {
+            const uint64_t sm = wave_ballot(sel);
             if (sel) {
-                const int v = cx.slot_value(list, c);
-                if (p.mode == SSA_GRAPH_FULL) {
-                    bm_set(bm, v);
-                } else {
-                    const int pos = nsel + lanes_below(sm);
-                    ekey[pos] = kv;
-                    eval[pos] = (uint32_t)v;
-                    eslot[pos] = (uint32_t)(list * p.C + c);
-                }
+                const int pos = nsel + lanes_below(sm);
+                ekey[pos] = kv;
+                eval[pos] = (uint32_t)v;
+                eslot[pos] = (uint32_t)slot;
             }
             nsel += __popcll(sm);
         }
+    };
+    auto decide = [&](bool keep, uint32_t kv) {
+        const bool is_eq = keep & (kv == thr) & (thr != 0u);
+        const uint64_t eqm = wave_ballot(is_eq);
+        const bool sel = keep & ((kv > thr) | (is_eq & (eq_before + lanes_below(eqm) < need)));
+        eq_before += __popcll(eqm);
+        return sel;
+    };
+    if (compacted) {
+        for (int e0 = 0; e0 < cnt; e0 += SSA_WAVE) {
+            const int e = e0 + lane;
+            const bool in = e < cnt;
+            const uint32_t kv = in ? ckey[e] : 0u;
+            const bool sel = decide(in, kv);
+            int v = 0;
+            const int slot = in ? (int)cslot[e] : 0;
+            if (sel) {
+                const int list = slot / p.C, c = slot - list * p.C;
+                const SelList L = list_info(list);
+                uint32_t k2;
+                bool r2;
+                slot_kv(L, list, c, v, k2, r2);
+            }
+            take(sel, kv, v, slot);
+        }
+    } else {
+        walk_kept([&](bool keep, uint32_t kv, int v, int slot) {
+            take(decide(keep, kv), kv, v, slot);
+        });
     }
     wave_lds_sync();
 
-    if (p.mode == SSA_GRAPH_LSH) {
-        int64_t *orow = p.out_idx + cx.row * kk;
+    if (LSH_MODE) {
+        int64_t *orow = p.out_idx + row * kk;
         for (int e = lane; e < f; e += SSA_WAVE) {
             const uint32_t k0 = ekey[e], s0 = eslot[e];
             int rank = 0;
@@ -542,7 +920,7 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
         return;
     }
 
-    // ---- FULL: pool = window + globals + LSH (+ fallback 0), minus self
+    // FULL: pool = window + globals + LSH (+ fallback 0), minus self
     if (!p.cross) {
         for (int o = -p.window + lane; o <= p.window; o += SSA_WAVE) {
             int x = n + o;
@@ -559,20 +937,20 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
 
     const int self = p.cross ? 0 : 1;
     const int ks = p.Kout - self;
-    int64_t *orow = p.out_idx + cx.row * p.Kout;
-    uint8_t *vrow = p.out_valid + cx.row * p.Kout;
+    int64_t *orow = p.out_idx + row * p.Kout;
+    uint8_t *vrow = p.out_valid + row * p.Kout;
     const int wpl = (p.words + SSA_WAVE - 1) / SSA_WAVE;
     const int w0 = lane * wpl;
-    int cnt = 0;
-    for (int w = w0; w < w0 + wpl && w < p.words; ++w) cnt += __popc(bm[w]);
-    int pos = wave_excl_scan(cnt);
-    const int total = wave_sum_i(cnt);
+    int cntb = 0;
+    for (int w = w0; w < w0 + wpl && w < p.words; ++w) cntb += __popc(bm[w]);
+    int pos = wave_excl_scan(cntb);
+    const int total = wave_sum_i(cntb);
     for (int w = w0; w < w0 + wpl && w < p.words && pos < ks; ++w) {
         uint32_t word = bm[w];
         while (word && pos < ks) {
-            const int bit = __ffs(word) - 1;
+            const int bitp = __ffs(word) - 1;
             word &= word - 1;
-            orow[self + pos] = (int64_t)(w * 32 + bit);
+            orow[self + pos] = (int64_t)(w * 32 + bitp);
             vrow[self + pos] = 1;
             ++pos;
         }
@@ -590,13 +968,6 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
 
 // ------------------------------------------------------------------ host side
 int supported_d(int d) { return d >= 4 && d <= 256 && (d & (d - 1)) == 0; }
-
-int maxch_for(int nch) {
-    static const int opts[] = {8, 16, 32, 48, 64, 96, 128};
-    for (int o : opts)
-        if (nch <= o) return o;
-    return 0;
-}
 
 struct Layout {
     int64_t kid, qid, perm, bstart, bsize, sorttmp, cnt, off, cur, qlist, tiles, ntiles, S, total;
@@ -677,13 +1048,6 @@ int make_dims(const ssa_graph_args *a, Dims &D) {
         D.Kout = D.kk;
     }
     SSA_CHECK_ARG(!a->causal || a->N <= a->M, "build_graph: causal needs N <= M");
-    const int nch = D.nlists * D.CPL;
-    if (!maxch_for(nch)) {
-        ssa_set_error("build_graph: candidate stream of %lld slots (%d chunks) above the "
-                      "register-resident limit of 128 chunks of 64",
-                      (long long)D.Call, nch);
-        return SSA_E_UNSUP;
-    }
     // chunk the query heads so the score buffer stays near 2 GiB
     const int64_t per_bh = (int64_t)a->N * D.Call * 4;
     int64_t nbh = ((int64_t)2 << 30) / (per_bh > 0 ? per_bh : 1);
@@ -691,6 +1055,49 @@ int make_dims(const ssa_graph_args *a, Dims &D) {
     if (nbh > D.BH) nbh = D.BH;
     D.nbh_chunk = (int)nbh;
     return SSA_OK;
+}
+
+template <typename T, int Dh>
+int launch_hash_mfma(const HashP &hp, hipStream_t st) {
+    const int NT = (hp.R * hp.P + 15) / 16;
+    const size_t lds = ((size_t)NT * 16 * (Dh + 1) + (size_t)4 * 16 * (NT * 16 + 1)) * 4;
+    if (lds > SSA_LDS_BYTES) {
+        ssa_set_error("hash: %d planes x d=%d need %zu bytes of LDS", hp.R * hp.P, Dh, lds);
+        return SSA_E_UNSUP;
+    }
+    SSA_CHECK_HIP(hipFuncSetAttribute((const void *)hash_mfma_kernel<T, Dh>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    hipLaunchKernelGGL((hash_mfma_kernel<T, Dh>), dim3((unsigned)ceil_div(hp.rows, 64)), dim3(256),
+                       lds, st, hp);
+    SSA_CHECK_LAUNCH();
+    return SSA_OK;
+}
+
+template <typename T>
+int launch_hash_one(const HashP &hp, int d, hipStream_t st) {
+    if (hp.rows == 0) return SSA_OK;
+    if (hp.inj) {
+        hipLaunchKernelGGL(hash_kernel<T>, dim3((unsigned)ceil_div(hp.rows, 256)), dim3(256), 0,
+                           st, hp);
+        SSA_CHECK_LAUNCH();
+        return SSA_OK;
+    }
+    switch (d) {
+        case 4: return launch_hash_mfma<T, 4>(hp, st);
+        case 8: return launch_hash_mfma<T, 8>(hp, st);
+        case 16: return launch_hash_mfma<T, 16>(hp, st);
+        case 32: return launch_hash_mfma<T, 32>(hp, st);
+        case 64: return launch_hash_mfma<T, 64>(hp, st);
+        case 128: return launch_hash_mfma<T, 128>(hp, st);
+        case 256: return launch_hash_mfma<T, 256>(hp, st);
+    }
+    ssa_set_error("hash: head dim %d", d);
+    return SSA_E_UNSUP;
+}
+
+bool view_aligned16(const ssa_tensor4 &t, int elem) {
+    const int64_t v = 16 / elem;
+    return (uintptr_t)t.ptr % 16 == 0 && t.sb % v == 0 && t.sh % v == 0 && t.sn % v == 0;
 }
 
 template <typename T>
@@ -702,18 +1109,18 @@ int launch_hash(const Dims &D, const ssa_graph_args *a, const Layout &L, char *w
     // keys
     hp.x = a->k.ptr; hp.sb = a->k.sb; hp.sh = a->k.sh; hp.sn = a->k.sn;
     hp.nh = D.Hkv; hp.L = D.M; hp.inj = a->k_proj; hp.key_layout = 1;
+    hp.vec16 = view_aligned16(a->k, (int)sizeof(T)) ? 1 : 0;
     hp.out = (uint16_t *)(ws + L.kid);
     hp.rows = D.BK * D.M;
-    hipLaunchKernelGGL(hash_kernel<T>, dim3((unsigned)ceil_div(hp.rows, 256)), dim3(256), 0, st, hp);
-    SSA_CHECK_LAUNCH();
+    int rc = launch_hash_one<T>(hp, D.d, st);
+    if (rc) return rc;
     // queries
     hp.x = a->q.ptr; hp.sb = a->q.sb; hp.sh = a->q.sh; hp.sn = a->q.sn;
     hp.nh = D.Hq; hp.L = D.N; hp.inj = a->q_proj; hp.key_layout = 0;
+    hp.vec16 = view_aligned16(a->q, (int)sizeof(T)) ? 1 : 0;
     hp.out = (uint16_t *)(ws + L.qid);
     hp.rows = D.BH * D.N;
-    hipLaunchKernelGGL(hash_kernel<T>, dim3((unsigned)ceil_div(hp.rows, 256)), dim3(256), 0, st, hp);
-    SSA_CHECK_LAUNCH();
-    return SSA_OK;
+    return launch_hash_one<T>(hp, D.d, st);
 }
 
 template <typename T, int Dh>
@@ -726,8 +1133,34 @@ int launch_rescore(const RsP &rp, int64_t grid, hipStream_t st) {
     return SSA_OK;
 }
 
+template <typename T, int Dh>
+int launch_rescore_mfma(const RsP &rp, int64_t grid, hipStream_t st) {
+    hipLaunchKernelGGL((rescore_mfma_kernel<T, Dh>), dim3((unsigned)grid), dim3(256), 0, st, rp);
+    SSA_CHECK_LAUNCH();
+    return SSA_OK;
+}
+
+// 16-byte fragment loads need 16-byte aligned rows
+bool rows_aligned16(const RsP &rp, int elem) {
+    const int64_t v = 16 / elem;
+    return ((uintptr_t)rp.q % 16 == 0) && ((uintptr_t)rp.k % 16 == 0) && rp.qsb % v == 0 &&
+           rp.qsh % v == 0 && rp.qsn % v == 0 && rp.ksb % v == 0 && rp.ksh % v == 0 &&
+           rp.ksn % v == 0;
+}
+
 template <typename T>
 int rescore_dispatch(int d, const RsP &rp, int64_t grid, hipStream_t st) {
+    if constexpr (!std::is_same<T, float>::value) {
+        if (d >= 8 && d <= 128 && rows_aligned16(rp, 2)) {
+            switch (d) {
+                case 8: return launch_rescore_mfma<T, 8>(rp, grid, st);
+                case 16: return launch_rescore_mfma<T, 16>(rp, grid, st);
+                case 32: return launch_rescore_mfma<T, 32>(rp, grid, st);
+                case 64: return launch_rescore_mfma<T, 64>(rp, grid, st);
+                case 128: return launch_rescore_mfma<T, 128>(rp, grid, st);
+            }
+        }
+    }
     switch (d) {
         case 4: return launch_rescore<T, 4>(rp, grid, st);
         case 8: return launch_rescore<T, 8>(rp, grid, st);
@@ -741,31 +1174,27 @@ int rescore_dispatch(int d, const RsP &rp, int64_t grid, hipStream_t st) {
     return SSA_E_UNSUP;
 }
 
-template <typename T, int MC>
-int launch_select_mc(const SelP &sp, hipStream_t st) {
-    const size_t lds = (size_t)SEL_WAVES * (sp.words + 3 * sp.kk) * 4;
-    SSA_CHECK_HIP(hipFuncSetAttribute((const void *)select_kernel<T, MC>,
+template <typename T, bool LSH>
+int launch_select(const SelP &sp, hipStream_t st) {
+    const size_t lds =
+        (size_t)SEL_WAVES * sel_lds_words(sp.nlists * sp.CPL, sp.words, sp.kk, LSH) * 4;
+    if (lds > SSA_LDS_BYTES) {
+        ssa_set_error("build_graph: select needs %zu bytes of LDS", lds);
+        return SSA_E_UNSUP;
+    }
+    SSA_CHECK_HIP(hipFuncSetAttribute((const void *)select_kernel<T, LSH>,
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     const int64_t grid = 8 * ceil_div(sp.nblocks, 8);
-    hipLaunchKernelGGL((select_kernel<T, MC>), dim3((unsigned)grid), dim3(SEL_WAVES * SSA_WAVE),
+    hipLaunchKernelGGL((select_kernel<T, LSH>), dim3((unsigned)grid), dim3(SEL_WAVES * SSA_WAVE),
                        lds, st, sp);
     SSA_CHECK_LAUNCH();
     return SSA_OK;
 }
 
 template <typename T>
-int select_dispatch(int mc, const SelP &sp, hipStream_t st) {
-    switch (mc) {
-        case 8: return launch_select_mc<T, 8>(sp, st);
-        case 16: return launch_select_mc<T, 16>(sp, st);
-        case 32: return launch_select_mc<T, 32>(sp, st);
-        case 48: return launch_select_mc<T, 48>(sp, st);
-        case 64: return launch_select_mc<T, 64>(sp, st);
-        case 96: return launch_select_mc<T, 96>(sp, st);
-        case 128: return launch_select_mc<T, 128>(sp, st);
-    }
-    ssa_set_error("select: chunk count %d", mc);
-    return SSA_E_UNSUP;
+int select_dispatch(const SelP &sp, hipStream_t st) {
+    return sp.mode == SSA_GRAPH_LSH ? launch_select<T, true>(sp, st)
+                                    : launch_select<T, false>(sp, st);
 }
 
 template <typename T>
@@ -777,11 +1206,6 @@ int build_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *w
                                 (int32_t *)(ws + L.perm), (int32_t *)(ws + L.bstart),
                                 (int32_t *)(ws + L.bsize), (uint16_t *)(ws + L.sorttmp), st);
     if (rc) return rc;
-    const size_t sel_lds = (size_t)SEL_WAVES * ((D.M + 31) / 32 + 1 + 3 * D.kk) * 4;
-    if (sel_lds > SSA_LDS_BYTES) {
-        ssa_set_error("build_graph: select needs %zu bytes of LDS", sel_lds);
-        return SSA_E_UNSUP;
-    }
     for (int64_t bh0 = 0; bh0 < D.BH; bh0 += D.nbh_chunk) {
         const int nbh = (int)((D.BH - bh0) < D.nbh_chunk ? (D.BH - bh0) : D.nbh_chunk);
         const int ninst = nbh * D.R * D.NS;
@@ -807,7 +1231,7 @@ int build_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *w
         SSA_CHECK_LAUNCH();
         hipLaunchKernelGGL(qb_scan_kernel, dim3((unsigned)ninst), dim3(256), 0, st, qp);
         SSA_CHECK_LAUNCH();
-        hipLaunchKernelGGL(qb_scatter_kernel, gq, dim3(256), 0, st, qp);
+        hipLaunchKernelGGL(qb_scatter_kernel, gq, dim3(256), (size_t)D.NB * 8, st, qp);
         SSA_CHECK_LAUNCH();
 
         RsP rp{};
@@ -835,11 +1259,11 @@ int build_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *w
         sp.CPL = D.CPL; sp.nlists = D.nlists; sp.Hq = D.Hq; sp.Hkv = D.Hkv; sp.rep = D.rep;
         sp.G = D.G; sp.kk = D.kk; sp.window = a->window; sp.causal = a->causal;
         sp.cross = a->is_cross; sp.mode = a->mode; sp.total_k = a->total_k; sp.Kw = D.Kw;
-        sp.Kout = D.Kout; sp.bh0 = (int)bh0; sp.words = (D.M + 31) / 32 + 1;
+        sp.Kout = D.Kout; sp.bh0 = (int)bh0; sp.words = ((D.M + 31) / 32 + 2) & ~1;
         sp.Call = D.Call; sp.rows = (int64_t)nbh * D.N;
         sp.out_idx = a->out_idx; sp.out_valid = a->out_valid; sp.ties = a->out_ties;
         sp.nblocks = ceil_div(sp.rows, SEL_WAVES);
-        rc = select_dispatch<T>(maxch_for(D.nlists * D.CPL), sp, st);
+        rc = select_dispatch<T>(sp, st);
         if (rc) return rc;
     }
     return SSA_OK;
