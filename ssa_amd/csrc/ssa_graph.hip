@@ -732,8 +732,15 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
         }
     };
 
-    // ---- pass 1
-    int nk = 0, nsamp = 0;
+    // ---- pass 1: dedup, and the kept keys >= lo in stream order into LDS.  lo
+    // is a lower bound of the final threshold: whenever the buffer nears its
+    // capacity, lo is raised to (a 24-bit floor of) the kk-th largest key in the
+    // buffer -- a subset of the stream -- and the buffer is filtered in place.
+    const int kk = p.kk;
+    const int fill = SEL_CAP - SSA_WAVE;
+    int nk = 0, cnt = 0;
+    uint32_t lo = 0u;
+    bool overflow = false;
     for (int list = 0; list < p.nlists; ++list) {
         const SelList L = list_info(list);
         if (L.sz == 0 && !gsc_ready) {               // scores of glob[0..G-1] and key 0
@@ -754,21 +761,52 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
             if (in_list) slot_kv(L, list, c, v, kv, real);
             const uint32_t bit = 1u << (v & 31);
             const uint32_t old = atomicOr(&bm[v >> 5], (in_list & real) ? bit : 0u);
-            atomicOr(&bm[v >> 5], (in_list & !real) ? bit : 0u);   // fillers after the reals
+            if (wave_ballot(in_list & !real)) atomicOr(&bm[v >> 5], (in_list & !real) ? bit : 0u);
             const bool keep = in_list & real & ((old & bit) == 0u);
             const uint64_t km = wave_ballot(keep);
             if (lane == 0) kmask[list * p.CPL + cj] = km;
-            if (nsamp < SEL_CAP) {
-                const int pos = nsamp + lanes_below(km);
-                if (keep && pos < SEL_CAP) ckey[pos] = kv;
-            }
-            nsamp += __popcll(km);
             nk += __popcll(km);
+            const bool app = keep & (kv >= lo);
+            const uint64_t am = wave_ballot(app);
+            const int pos = cnt + lanes_below(am);
+            if (app && pos < SEL_CAP) { ckey[pos] = kv; cslot[pos] = (uint32_t)(list * p.C + c); }
+            cnt += __popcll(am);
+            if (cnt >= fill && cnt >= kk && !overflow) {
+                wave_lds_sync();
+                const int m0 = cnt < SEL_CAP ? cnt : SEL_CAP;
+                uint32_t sv[SEL_CAP / SSA_WAVE];
+#pragma unroll
+                for (int i = 0; i < SEL_CAP / SSA_WAVE; ++i) {
+                    const int e = lane + SSA_WAVE * i;
+                    sv[i] = e < m0 ? ckey[e] : 0u;
+                }
+                const uint32_t nlo = kth_search(sv, kk, 8);
+                lo = nlo > lo ? nlo : (lo ? lo : 1u);
+                uint32_t sl[SEL_CAP / SSA_WAVE];
+#pragma unroll
+                for (int i = 0; i < SEL_CAP / SSA_WAVE; ++i) {
+                    const int e = lane + SSA_WAVE * i;
+                    sl[i] = e < m0 ? cslot[e] : 0u;
+                }
+                wave_lds_sync();
+                int nc = 0;
+#pragma unroll
+                for (int i = 0; i < SEL_CAP / SSA_WAVE; ++i) {
+                    const bool t = sv[i] >= lo && sv[i] != 0u;
+                    const uint64_t m = wave_ballot(t);
+                    if (t) { ckey[nc + lanes_below(m)] = sv[i]; cslot[nc + lanes_below(m)] = sl[i]; }
+                    nc += __popcll(m);
+                }
+                overflow = cnt > SEL_CAP;
+                cnt = nc;
+                wave_lds_sync();
+            }
         }
     }
+    overflow = overflow || cnt > SEL_CAP;
     wave_lds_sync();
 
-    // re-walk the kept slots of the stream in order
+    // re-walk the kept slots of the stream in order (rare paths only)
     auto walk_kept = [&](auto &&fn) {
         for (int list = 0; list < p.nlists; ++list) {
             const SelList L = list_info(list);
@@ -787,36 +825,11 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     };
 
     // ---- threshold
-    const int kk = p.kk;
     uint32_t thr = 0u;                 // 0: every kept key is selected
     int need = 0;
-    int cnt = 0;
-    bool compacted = false;
+    const bool compacted = !overflow;  // every key >= the threshold is in ckey
     if (nk > kk) {
-        uint32_t lo = 1u;
-        const int ns = nsamp < SEL_CAP ? nsamp : SEL_CAP;
-        if (ns >= kk) {
-            uint32_t sv[SEL_CAP / SSA_WAVE];
-#pragma unroll
-            for (int i = 0; i < SEL_CAP / SSA_WAVE; ++i) {
-                const int e = lane + SSA_WAVE * i;
-                sv[i] = e < ns ? ckey[e] : 0u;
-            }
-            lo = kth_search(sv, kk, 16);
-            if (lo == 0u) lo = 1u;
-        }
-        wave_lds_sync();
-        // pass 2: compact the kept keys >= lo with their stream slot
-        walk_kept([&](bool keep, uint32_t kv, int, int slot) {
-            const bool t = keep & (kv >= lo);
-            const uint64_t m = wave_ballot(t);
-            const int pos = cnt + lanes_below(m);
-            if (t && pos < SEL_CAP) { ckey[pos] = kv; cslot[pos] = (uint32_t)slot; }
-            cnt += __popcll(m);
-        });
-        wave_lds_sync();
-        if (cnt <= SEL_CAP) {
-            compacted = true;
+        if (compacted) {
             uint32_t cv[SEL_CAP / SSA_WAVE];
 #pragma unroll
             for (int i = 0; i < SEL_CAP / SSA_WAVE; ++i) {
