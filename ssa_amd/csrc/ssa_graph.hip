@@ -612,6 +612,8 @@ __device__ __forceinline__ int wave_count(int c) {
 constexpr int SEL_CAP = 512;   // keys kept in LDS for the exact threshold search
 
 // Per-wave LDS of the select kernel, in 32-bit words:
+//   tab   [4*nch]     per 64-slot chunk: perm offset of lane 0, flags, stream
+//                     slot of lane 0, perm offset of the overflow filler
 //   bm    [words]     seen bitmap, later the merge bitmap
 //   kmask [2*nch]     per 64-slot chunk, the ballot of kept slots
 //   ckey  [SEL_CAP]   sample of kept keys, then kept keys >= the lower bound
@@ -619,17 +621,21 @@ constexpr int SEL_CAP = 512;   // keys kept in LDS for the exact threshold searc
 //   gsc   [64]        scores of glob[0..G-1] and key 0 (empty buckets)
 //   LSH mode: ekey/eval/eslot [kk] the selected entries
 __host__ __device__ inline int sel_lds_words(int nch, int words, int kk, bool lsh) {
-    return (words + 2 * nch + 2 * SEL_CAP + 64 + (lsh ? 3 * kk : 0) + 1) & ~1;
+    return (4 * nch + words + 2 * nch + 2 * SEL_CAP + 64 + (lsh ? 3 * kk : 0) + 1) & ~1;
 }
 
-// bitwise search for the largest t (over the top bits hi..lo_bit) with at
-// least kk of the wave's keys >= t; stops early once exactly kk keys are >= t.
-// Keys come from k[0..NK) per lane (0 = absent).
+// Largest t (resolved down to bit lo_bit) such that at least kk of the wave's
+// keys k[0..NK) per lane are >= t, given base <= answer <= top: the answer shares
+// the bit prefix of base and top, so only the bits below their highest
+// difference are searched.  Stops early once exactly kk keys are >= t.
 template <int NK>
-__device__ __forceinline__ uint32_t kth_search(const uint32_t (&k)[NK], int kk, int lo_bit) {
-    uint32_t thr = 0u;
+__device__ __forceinline__ uint32_t kth_search(const uint32_t (&k)[NK], int kk, uint32_t base,
+                                               uint32_t top, int lo_bit) {
+    if (base >= top) return base;
+    const int hb = 31 - __clz(base ^ top);
+    uint32_t thr = hb >= 31 ? 0u : (base & ~((2u << hb) - 1u));
 #pragma unroll 1
-    for (int bit = 31; bit >= lo_bit; --bit) {
+    for (int bit = hb; bit >= lo_bit; --bit) {
         const uint32_t cand = thr | (1u << bit);
         int c = 0;
 #pragma unroll
@@ -643,10 +649,33 @@ __device__ __forceinline__ uint32_t kth_search(const uint32_t (&k)[NK], int kk, 
     return thr;
 }
 
+__device__ __forceinline__ uint32_t wave_max_u(uint32_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const uint32_t y = (uint32_t)__shfl_xor((int)v, o, SSA_WAVE);
+        v = y > v ? y : v;
+    }
+    return v;
+}
+__device__ __forceinline__ uint32_t wave_min_u(uint32_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const uint32_t y = (uint32_t)__shfl_xor((int)v, o, SSA_WAVE);
+        v = y < v ? y : v;
+    }
+    return v;
+}
+
 struct SelList {
     int st, sz, nv;
     const int32_t *pr;
 };
+
+// chunk descriptor flags word: lanes in the list | real slots << 7 | flags
+constexpr int CH_EMPTY = 1 << 14;      // the list's bucket is empty (glob ++ 0)
+constexpr int CH_FIRST = 1 << 15;      // first chunk of its list
+__device__ __forceinline__ int CH_LANES(int y) { return y & 127; }
+__device__ __forceinline__ int CH_REAL(int y) { return (y >> 7) & 127; }
 
 // One wavefront per query row, streaming over the query's candidate stream in
 // the reference's concatenation order (round, id set, slot):
@@ -674,7 +703,8 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     if (rloc >= p.rows) return;
     const int lane = lane_id();
     const int nch = p.nlists * p.CPL;
-    uint32_t *bm = sel_smem + (int64_t)wid * sel_lds_words(nch, p.words, p.kk, LSH_MODE);
+    int4 *tab = (int4 *)(sel_smem + (int64_t)wid * sel_lds_words(nch, p.words, p.kk, LSH_MODE));
+    uint32_t *bm = (uint32_t *)(tab + nch);
     uint64_t *kmask = (uint64_t *)(bm + p.words);
     uint32_t *ckey = (uint32_t *)(kmask + nch);
     uint32_t *cslot = ckey + SEL_CAP;
@@ -703,7 +733,31 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     const float *srow = p.S + ((int64_t)bhl * p.N + n) * p.Call;
     const int ng = min(p.G + 1, SSA_WAVE);
     for (int w = lane; w < p.words; w += SSA_WAVE) bm[w] = 0u;
-    bool gsc_ready = false;
+    bool any_empty = false;
+    for (int ci = lane; ci < nch; ci += SSA_WAVE) {
+        const int list = ci / p.CPL, cj = ci - list * p.CPL;
+        const int u = qids[list];
+        const int64_t prow = (int64_t)bk * p.R + list / p.NS;
+        const int st = p.bstart[prow * p.NB + u];
+        const int sz = p.bsize[prow * p.NB + u];
+        const int c0 = cj * SSA_WAVE;
+        const int lanes = min(p.C - c0, SSA_WAVE);
+        const int realn = sz == 0 ? lanes : max(0, min(min(sz, p.C) - c0, SSA_WAVE));
+        int4 d4;
+        d4.x = st + c0;
+        d4.y = lanes | (realn << 7) | (sz == 0 ? CH_EMPTY : 0) | (cj == 0 ? CH_FIRST : 0);
+        d4.z = list * p.C + c0;
+        d4.w = (int)prow;
+        tab[ci] = d4;
+        any_empty |= sz == 0;
+    }
+    if (wave_ballot(any_empty)) {          // scores of glob[0..G-1] and key 0 (:711-737)
+        for (int j = 0; j < ng; ++j) {
+            const int v = j < p.G ? (int)p.glob[j] : 0;
+            const float sc = dot_row<T>(qv, kbase + (int64_t)v * p.ksn, p.d);
+            if (lane == 0) gsc[j] = sc;
+        }
+    }
     wave_lds_sync();
 
     auto list_info = [&](int list) {
@@ -741,35 +795,46 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     int nk = 0, cnt = 0;
     uint32_t lo = 0u;
     bool overflow = false;
-    for (int list = 0; list < p.nlists; ++list) {
-        const SelList L = list_info(list);
-        if (L.sz == 0 && !gsc_ready) {               // scores of glob[0..G-1] and key 0
-            for (int j = 0; j < ng; ++j) {
-                const int v = j < p.G ? (int)p.glob[j] : 0;
-                const float sc = dot_row<T>(qv, kbase + (int64_t)v * p.ksn, p.d);
-                if (lane == 0) gsc[j] = sc;
-            }
-            gsc_ready = true;
-            wave_lds_sync();
+    constexpr int PIPE = 4;            // chunks whose loads are in flight together
+    for (int ci0 = 0; ci0 < nch; ci0 += PIPE) {
+        int4 d4[PIPE];
+        int raw[PIPE];
+        float sc[PIPE];
+#pragma unroll
+        for (int u = 0; u < PIPE; ++u) {
+            d4[u] = ci0 + u < nch ? tab[ci0 + u] : make_int4(0, 0, 0, 0);
+            const bool real = (lane < CH_REAL(d4[u].y)) & ((d4[u].y & CH_EMPTY) == 0);
+            raw[u] = p.perm[(int64_t)d4[u].w * p.M + (real ? d4[u].x + lane : p.M - 1)];
+            sc[u] = srow[real ? d4[u].z + lane : 0];
         }
-        for (int cj = 0; cj < p.CPL; ++cj) {
-            const int c = cj * SSA_WAVE + lane;
-            const bool in_list = c < p.C;
-            int v = 0;
-            uint32_t kv = 0u;
-            bool real = false;
-            if (in_list) slot_kv(L, list, c, v, kv, real);
+#pragma unroll
+        for (int u = 0; u < PIPE; ++u) {
+            const int y = d4[u].y;
+            const bool in_list = lane < CH_LANES(y);
+            const bool empty = (y & CH_EMPTY) != 0;
+            const bool real = in_list & (lane < CH_REAL(y));
+            int v;
+            uint32_t kv;
+            if (!empty) {
+                v = (p.causal && raw[u] > n) ? n : raw[u];
+                kv = (p.causal && v == n) ? kself : score_key(sc[u]);
+            } else {                                   // empty bucket: glob ++ 0
+                const int c = ((y & CH_FIRST) ? 0 : SSA_WAVE) + lane;
+                const int j = c < ng - 1 ? c : ng - 1;
+                v = (c < p.G) ? (int)p.glob[j] : 0;
+                kv = score_key(gsc[j]);
+            }
             const uint32_t bit = 1u << (v & 31);
-            const uint32_t old = atomicOr(&bm[v >> 5], (in_list & real) ? bit : 0u);
+            const uint32_t old = atomicOr(&bm[v >> 5], real ? bit : 0u);
             if (wave_ballot(in_list & !real)) atomicOr(&bm[v >> 5], (in_list & !real) ? bit : 0u);
-            const bool keep = in_list & real & ((old & bit) == 0u);
+            const bool keep = real & ((old & bit) == 0u);
             const uint64_t km = wave_ballot(keep);
-            if (lane == 0) kmask[list * p.CPL + cj] = km;
+            if (lane == 0 && ci0 + u < nch) kmask[ci0 + u] = km;
             nk += __popcll(km);
             const bool app = keep & (kv >= lo);
             const uint64_t am = wave_ballot(app);
             const int pos = cnt + lanes_below(am);
-            if (app && pos < SEL_CAP) { ckey[pos] = kv; cslot[pos] = (uint32_t)(list * p.C + c); }
+            if (app && pos < SEL_CAP) { ckey[pos] = kv; cslot[pos] = (uint32_t)(d4[u].z + lane); }
             cnt += __popcll(am);
             if (cnt >= fill && cnt >= kk && !overflow) {
                 wave_lds_sync();
@@ -780,8 +845,17 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
                     const int e = lane + SSA_WAVE * i;
                     sv[i] = e < m0 ? ckey[e] : 0u;
                 }
-                const uint32_t nlo = kth_search(sv, kk, 8);
-                lo = nlo > lo ? nlo : (lo ? lo : 1u);
+                uint32_t mx = 0u, mn = 0xffffffffu;
+#pragma unroll
+                for (int i = 0; i < SEL_CAP / SSA_WAVE; ++i) {
+                    mx = sv[i] > mx ? sv[i] : mx;
+                    mn = (sv[i] != 0u && sv[i] < mn) ? sv[i] : mn;
+                }
+                mx = wave_max_u(mx);
+                mn = wave_min_u(mn);
+                const uint32_t base0 = lo > mn ? lo : mn;     // every buffered key >= lo
+                const uint32_t nlo = kth_search(sv, kk, base0, mx, 16);
+                lo = nlo > lo ? nlo : lo;
                 uint32_t sl[SEL_CAP / SSA_WAVE];
 #pragma unroll
                 for (int i = 0; i < SEL_CAP / SSA_WAVE; ++i) {
@@ -836,7 +910,15 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
                 const int e = lane + SSA_WAVE * i;
                 cv[i] = e < cnt ? ckey[e] : 0u;
             }
-            thr = kth_search(cv, kk, 0);
+            uint32_t mx = 0u, mn = 0xffffffffu;
+#pragma unroll
+            for (int i = 0; i < SEL_CAP / SSA_WAVE; ++i) {
+                mx = cv[i] > mx ? cv[i] : mx;
+                mn = (cv[i] != 0u && cv[i] < mn) ? cv[i] : mn;
+            }
+            mx = wave_max_u(mx);
+            mn = wave_min_u(mn);
+            thr = kth_search(cv, kk, lo > mn ? lo : mn, mx, 0);
             int ge = 0, gt = 0;
 #pragma unroll
             for (int i = 0; i < SEL_CAP / SSA_WAVE; ++i) { ge += cv[i] >= thr; gt += cv[i] > thr; }
