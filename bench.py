@@ -15,8 +15,10 @@ Also reported:
   kernel's average duration measured with events on the launch stream;
 * recall@32 of the graph against exact dense top-32 (head 0 and all heads);
 * cpu_baseline: the reference's torch op sequence (oracle/torch_port.py) on
-  the host cores, on one kv-head group (4 of 32 query heads) of the same
-  workload, scaled to whole-workload tokens/s.
+  the host cores, on two kv-head groups (8 of 32 query heads) of the same
+  workload, scaled to whole-workload tokens/s;
+* roofline.traffic: HBM bytes per apply launch from the committed rocprofv3
+  FETCH_SIZE/WRITE_SIZE summary (profiles/hbm_traffic_bf16_gqa_n4096.md).
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu]
 """
@@ -78,6 +80,21 @@ def recall_at_32(q, k, nb, va, rep, causal_variant=False):
     return res[0], sum(res) / len(res)
 
 
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (a line `traffic <kernel> <bytes>`), or None."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic_bf16_gqa_n4096.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                parts = line.strip().strip("`").split()
+                if len(parts) == 3 and parts[0] == "traffic" and parts[1] == kernel:
+                    return int(parts[2])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(attn_gpu):
     """Time the reference's CPU op sequence on one kv group of the workload."""
     import torch
@@ -87,26 +104,27 @@ def cpu_baseline(attn_gpu):
     torch.set_num_threads(nthreads)
     rep = attn_gpu.kv_rep
     d = attn_gpu.d_head
-    Wq = attn_gpu.Wq.weight[: rep * d].detach().cpu()
-    Wk = attn_gpu.Wk.weight[:d].detach().cpu()
-    Wv = attn_gpu.Wv.weight[:d].detach().cpu()
-    Wo = attn_gpu.Wo.weight[:, : rep * d].detach().cpu()
+    ng = 2                                      # kv-head groups in the sample
+    Wq = attn_gpu.Wq.weight[: ng * rep * d].detach().cpu()
+    Wk = attn_gpu.Wk.weight[: ng * d].detach().cpu()
+    Wv = attn_gpu.Wv.weight[: ng * d].detach().cpu()
+    Wo = attn_gpu.Wo.weight[:, : ng * rep * d].detach().cpu()
     rp = attn_gpu.lsh_builder.rand_proj.detach().cpu()
     g = torch.Generator().manual_seed(1000)
     x = (torch.randn(1, 4096, 4096, generator=g) * 0.02).to(torch.bfloat16)
-    kw = dict(H=rep, n_kv=1, K=cfg.num_neighbors, window=cfg.window_size,
+    kw = dict(H=ng * rep, n_kv=ng, K=cfg.num_neighbors, window=cfg.window_size,
               glob_n=cfg.num_global_tokens, R=cfg.num_hash_rounds, max_p=cfg.max_num_hashes,
               T=cfg.lsh_num_probes, causal=cfg.causal)
     times = []
-    for i in range(2):
+    for i in range(4):
         t0 = time.perf_counter()
         with torch.no_grad():
             torch_port.forward(x, Wq, Wk, Wv, Wo, rp, **kw)
         times.append(time.perf_counter() - t0)
         print(f"# cpu sample run {i}: {times[-1]:.2f} s", file=sys.stderr, flush=True)
-    t = min(times[1:]) if len(times) > 1 else times[0]
+    t = sorted(times[1:])[1]
     groups = cfg.num_heads // rep
-    tok_s = 4096 / (t * groups)
+    tok_s = 4096 / (t * groups / ng)
     model = ""
     try:
         with open("/proc/cpuinfo") as f:
@@ -118,10 +136,10 @@ def cpu_baseline(attn_gpu):
         pass
     return {"value": tok_s, "unit": "tokens/s", "cores": torch.get_num_threads(),
             "kind": "port",
-            "sample": f"1 of {groups} kv-head groups ({rep} query heads, 1 kv head) of the same "
-                      f"workload through the reference's torch CPU op sequence "
-                      f"(oracle/torch_port.py), {t:.2f} s, scaled x{groups}; "
-                      f"1 warm-up + 1 timed run; CPU: {model}"}
+            "sample": f"{ng} of {groups} kv-head groups ({ng * rep} query heads, {ng} kv heads) "
+                      f"of the same workload through the reference's torch CPU op sequence "
+                      f"(oracle/torch_port.py), median {t:.2f} s, scaled x{groups // ng}; "
+                      f"1 warm-up + 3 timed runs; CPU: {model}"}
 
 
 def main():
@@ -131,6 +149,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-recall", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="first run a plain bf16 copy kernel (x*1, 256 MiB in, 256 MiB out) "
+                         "5 times, as the reference point for rocprofv3 FETCH_SIZE/WRITE_SIZE")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -139,6 +160,16 @@ def main():
         sys.exit(2)
     import torch
     dev = "cuda:0"
+    if args.calibrate_copy:
+        n = 128 << 20
+        src = torch.ones(n, dtype=torch.bfloat16, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            torch.mul(src, 1, out=dst)
+        torch.cuda.synchronize()
+        print(f"# copy calibration: 5 x (read {2 * n} B, write {2 * n} B)", file=sys.stderr,
+              flush=True)
+        del src, dst
     cfg, attn, x = build_module(dev)
     B, N = x.shape[0], x.shape[1]
     H, d, K = attn.H, attn.d_head, attn.K
@@ -157,33 +188,29 @@ def main():
     value = B * N / ((t1 - t0) / args.steps)
     print(f"# forward {ms:.3f} ms/step", file=sys.stderr, flush=True)
 
-    # per-stage timing with events on the launch stream (torch's current stream)
+    # per-stage timing with events on the launch stream (torch's current stream):
+    # build then apply, as inside forward, with each stage bracketed by its own
+    # events so that the apply launches see the same cache state as in forward
     with torch.no_grad():
         q = attn._split_q(attn.Wq(x))
         k = attn._split_kv_compact(attn.Wk(x))
         v = attn._split_kv_compact(attn.Wv(x))
         st = torch.cuda.current_stream()
-        ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
         reps = max(args.steps, 10)
-        ev[0].record(st)
-        for _ in range(reps):
+        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(reps)]
+        for e in evs:
+            e[0].record(st)
             nb, va = attn.build_graph(q, k, N, N, B, x.device, True, False)
-        ev[1].record(st)
-        ev[2].record(st)
-        for _ in range(reps):
+            e[1].record(st)
             out = attn.apply_graph(q, k, v, nb, va)
-        ev[3].record(st)
+            e[2].record(st)
         torch.cuda.synchronize()
-    t_build = ev[0].elapsed_time(ev[1]) / reps
-    t_apply = ev[2].elapsed_time(ev[3]) / reps
+    t_build = sum(e[0].elapsed_time(e[1]) for e in evs) / reps
+    t_apply = sum(e[1].elapsed_time(e[2]) for e in evs) / reps
     K_out = nb.shape[-1]
     bytes_apply = B * H * N * (2 * K_out * d + 2 * d) * 2
     achieved = bytes_apply / (t_apply / 1000.0)
-    traffic = None
-    tf = os.path.join(ROOT, "profiles", "apply_traffic_bf16_gqa_n4096.json")
-    if os.path.exists(tf):
-        with open(tf) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+    traffic = measured_traffic("apply_fwd_kernel")
     print(f"# build {t_build:.3f} ms, apply {t_apply:.3f} ms", file=sys.stderr, flush=True)
 
     rec = None
