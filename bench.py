@@ -213,6 +213,17 @@ def main():
     traffic = measured_traffic("apply_fwd_kernel")
     print(f"# build {t_build:.3f} ms, apply {t_apply:.3f} ms", file=sys.stderr, flush=True)
 
+    # rows whose k-th LSH score is tied (selection decided by the tie rule)
+    from ssa_amd import _lib
+    with torch.no_grad():
+        lb = attn.lsh_builder
+        p_eff = lb.compute_effective_p(N, lb.C, lb.max_P)
+        _, _, ties = _lib.build_graph(q, k, lb.rand_proj, P=p_eff, T=lb.T, C=lb.C,
+                                      top_k=attn.lsh_k, window=cfg.window_size, causal=True,
+                                      is_cross=False, total_k=K, glob=attn.glob_builder(N, dev),
+                                      count_ties=True)
+        tie_rows = int(ties.item())
+
     rec = None
     if not args.no_recall:
         with torch.no_grad():
@@ -234,6 +245,7 @@ def main():
                      "kernel": "apply_fwd_kernel", "bytes_per_launch": bytes_apply,
                      "ms_per_launch": t_apply},
         "t_build_ms": t_build, "t_apply_ms": t_apply, "k_out": K_out,
+        "tie_rows": tie_rows, "query_rows": B * H * N,
         "recall_at_32": rec,
     }
     if not args.no_cpu:

@@ -64,9 +64,26 @@ def lib():
                                        ctypes.c_long, ctypes.c_long, ctypes.c_int,
                                        ctypes.c_long, ctypes.c_float, ctypes.c_int,
                                        ctypes.c_int, P]
+        L.ssa_oracle_set_mutation.argtypes = [ctypes.c_int]
         del I64
         _lib = L
     return _lib
+
+
+class mutation:
+    """Context manager that plants mistake `m` in the C oracle (see the MUT_*
+    list in ssa_oracle.c) so a test can show that a pinning check catches it."""
+
+    def __init__(self, m: int):
+        self.m = m
+
+    def __enter__(self):
+        lib().ssa_oracle_set_mutation(self.m)
+        return self
+
+    def __exit__(self, *exc):
+        lib().ssa_oracle_set_mutation(0)
+        return False
 
 
 def _p(a: np.ndarray):

@@ -41,6 +41,22 @@ typedef struct {
 
 typedef int (*less_fn)(const elem_t *a, const elem_t *b);
 
+/* Planted mistakes, for the tests that show each pinning check catches one
+ * (0 = the faithful restatement).  Never set outside those tests. */
+static int g_mut = 0;
+void ssa_oracle_set_mutation(int m) { g_mut = m; }
+enum {
+    MUT_STABLE_SORT = 1,     /* stable sort instead of introsort               */
+    MUT_FILLER_NO_MARK = 2,  /* invalid slots do not mark their key as seen    */
+    MUT_SIGN_GE = 3,         /* bit = proj >= 0                                */
+    MUT_NO_CAUSAL = 4,       /* no causal substitution of future keys          */
+    MUT_NO_EMPTY_FB = 5,     /* no glob ++ 0 list for an empty bucket          */
+    MUT_NEGINF_ZERO = 6,     /* -inf slots become 0 instead of glob[t]         */
+    MUT_PROBE_CUMUL = 7,     /* probe t flips bits cumulatively                */
+    MUT_ONE_TOPK = 8,        /* one top-k over the whole row, not chunked      */
+    MUT_MERGE_SELF = 9       /* merge keeps the query itself in the pool       */
+};
+
 /* key-only '<' : torch.sort(int64) ascending, sparse_attention.py:781 */
 static int less_key(const elem_t *a, const elem_t *b) { return a->key < b->key; }
 
@@ -234,7 +250,8 @@ static void partial_sort(elem_t *f, elem_t *mid, elem_t *l, less_fn lt) {
 void ssa_oracle_sort_perm(const int64_t *keys, long n, int64_t *perm) {
     elem_t *e = (elem_t *)malloc((size_t)(n > 0 ? n : 1) * sizeof(elem_t));
     for (long i = 0; i < n; ++i) { e[i].key = keys[i]; e[i].val = 0.f; e[i].pos = i; }
-    intro_sort(e, e + n, less_key);
+    if (g_mut == MUT_STABLE_SORT) insertion_sort(e, e + n, less_key);
+    else intro_sort(e, e + n, less_key);
     for (long i = 0; i < n; ++i) perm[i] = e[i].pos;
     free(e);
 }
@@ -272,7 +289,8 @@ static float dot_f32(const float *a, const float *b, int d) {
 /* bucket id: bit j = (proj_j > 0), plane j is bit j (sparse_attention.py:589-591) */
 static int64_t bucket_of(const float *proj, int P) {
     int64_t id = 0;
-    for (int j = 0; j < P; ++j) if (proj[j] > 0.f) id |= (int64_t)1 << j;
+    for (int j = 0; j < P; ++j)
+        if (g_mut == MUT_SIGN_GE ? proj[j] >= 0.f : proj[j] > 0.f) id |= (int64_t)1 << j;
     return id;
 }
 
@@ -291,6 +309,7 @@ static void probe_ids(const float *proj, int P, int T, int64_t base, int64_t *ou
         int pos = ord[t];
         int bit = (int)((base >> pos) & 1);
         out[t] = base + ((int64_t)1 << pos) * (1 - 2 * bit);
+        if (g_mut == MUT_PROBE_CUMUL) base = out[t];
     }
 }
 
@@ -380,8 +399,8 @@ long ssa_oracle_lsh_forward(const float *q, const float *k, long BH, long kv_rep
     int64_t *ti = (int64_t *)malloc(sizeof(int64_t) * (size_t)(kk + 1));
     float *bestv = (float *)malloc(sizeof(float) * (size_t)(kk + 1));
     int64_t *besti = (int64_t *)malloc(sizeof(int64_t) * (size_t)(kk + 1));
-    float *mv = (float *)malloc(sizeof(float) * (size_t)(kk + chunk + 1));
-    int64_t *mi = (int64_t *)malloc(sizeof(int64_t) * (size_t)(kk + chunk + 1));
+    float *mv = (float *)malloc(sizeof(float) * (size_t)(kk + Call + 1));
+    int64_t *mi = (int64_t *)malloc(sizeof(int64_t) * (size_t)(kk + Call + 1));
     float *scores = (float *)malloc(sizeof(float) * (size_t)(Call > 0 ? Call : 1));
     long n_ties = 0;
 
@@ -418,8 +437,8 @@ long ssa_oracle_lsh_forward(const float *q, const float *k, long BH, long kv_rep
                         int v = p <= bend;                                         /* :690 */
                         int64_t gp = v ? p : M; if (gp > M - 1) gp = M - 1;        /* :691-696 */
                         int64_t cv = pm[gp];
-                        if (causal && cv > n) cv = n;                              /* :698-709 */
-                        if (sz == 0) {                                             /* :711-737 */
+                        if (causal && cv > n && g_mut != MUT_NO_CAUSAL) cv = n;    /* :698-709 */
+                        if (sz == 0 && g_mut != MUT_NO_EMPTY_FB) {                 /* :711-737 */
                             cv = (c < G) ? glob[c] : 0;
                             v = 1;
                         }
@@ -432,14 +451,15 @@ long ssa_oracle_lsh_forward(const float *q, const float *k, long BH, long kv_rep
             for (long jj = 0; jj < Call; ++jj) {
                 int64_t cv = cand[jj];
                 int first = stamp[cv] != tag;
-                stamp[cv] = tag;
+                if (valid[jj] || g_mut != MUT_FILLER_NO_MARK) stamp[cv] = tag;
                 int keep = valid[jj] && first;
                 scores[jj] = keep ? dot_f32(qn, kg + cv * d, d) : -INFINITY;      /* :909-916 */
             }
             /* chunked running top-k (:904-922) */
             for (long t = 0; t < kk; ++t) { bestv[t] = -INFINITY; besti[t] = 0; }
-            for (long s0 = 0; s0 < Call; s0 += chunk) {
-                long s1 = s0 + chunk < Call ? s0 + chunk : Call;
+            const long step = g_mut == MUT_ONE_TOPK ? Call : chunk;
+            for (long s0 = 0; s0 < Call; s0 += step) {
+                long s1 = s0 + step < Call ? s0 + step : Call;
                 long w = kk + (s1 - s0);
                 for (long t = 0; t < kk; ++t) { mv[t] = bestv[t]; mi[t] = besti[t]; }
                 for (long t = s0; t < s1; ++t) { mv[kk + t - s0] = scores[t]; mi[kk + t - s0] = cand[t]; }
@@ -464,7 +484,8 @@ long ssa_oracle_lsh_forward(const float *q, const float *k, long BH, long kv_rep
             /* -inf slots -> glob[t] or 0 by slot position (:948-957) */
             int64_t *oi = out_idx + (bh * N + n) * kk;
             for (long t = 0; t < kk; ++t) {
-                if (isinf(bestv[t]) && bestv[t] < 0) oi[t] = (t < G) ? glob[t] : 0;
+                if (isinf(bestv[t]) && bestv[t] < 0)
+                    oi[t] = (t < G && g_mut != MUT_NEGINF_ZERO) ? glob[t] : 0;
                 else oi[t] = besti[t];
             }
             if (out_val) memcpy(out_val + (bh * N + n) * kk, bestv, sizeof(float) * (size_t)kk);
@@ -509,7 +530,7 @@ void ssa_oracle_merge(const int64_t *win, long Kw, const int64_t *glob, long G, 
             for (long i = 0; i < Kw; ++i) row[c++] = win[n * Kw + i];
             for (long i = 0; i < G; ++i) row[c++] = glob[i];
             for (long i = 0; i < Kl; ++i) row[c++] = lsh[(bh * N + n) * Kl + i];
-            if (has_self)                                                    /* :1043-1049 */
+            if (has_self && g_mut != MUT_MERGE_SELF)                         /* :1043-1049 */
                 for (long i = 0; i < Kall; ++i) if (row[i] == n) row[i] = sentinel;
             qsort(row, (size_t)Kall, sizeof(int64_t), cmp_i64);              /* :1052 */
             for (long i = Kall - 1; i >= 1; --i)                             /* :1053-1059 */

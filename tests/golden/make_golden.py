@@ -14,7 +14,7 @@ fallback, chunked top-k, -inf fallback), merge_neighbors, build_graph,
 sparse_gather_attention, SparseAttention.forward with its stats, and the RNG
 consumption order of seeded construction.
 
-Usage:  python tests/golden/make_golden.py
+Usage:  python tests/golden/make_golden.py [--only-empty-ranked]
 """
 from __future__ import annotations
 
@@ -169,10 +169,37 @@ def lsh_empty_bucket_case(sa):
                 rand_proj=_np(lsh.rand_proj)), dict(C=4, top_k=2, max_P=1, R=1)
 
 
+def lsh_empty_bucket_ranked_case(sa):
+    """Empty bucket whose glob ++ 0 list must compete on score: query 0 meets
+    an empty bucket in round 0 (every key has a negative first coordinate) and
+    a populated one in round 1; keys 5 (the global token) and 0 score above
+    every round-1 candidate, so they are selected only if the empty-bucket
+    list is built.  Hyperplanes are set to unit vectors after construction."""
+    torch.manual_seed(7)
+    lsh = sa.LSHGraphBuilder(d_head=4, max_num_hashes=1, lsh_candidates=4, num_rounds=2)
+    with torch.no_grad():
+        lsh.rand_proj.zero_()
+        lsh.rand_proj[0, 0, 0] = 1.0
+        lsh.rand_proj[1, 0, 1] = 1.0
+    k = torch.tensor([[-1., -1, 0, 4], [-1, 1, 0, 0], [-1, 1, 0, 0], [-1, 1, 0, 0],
+                      [-1, 1, 0, 0], [-1, -1, 0, 5], [-1, 1, 0, 0], [-1, 1, 0, 0]])
+    q = torch.tensor([[1., 1, 0, 1], [-1, 1, 0, 1]])
+    glob = torch.tensor([5])
+    out = lsh(q.view(1, 1, 2, 4), k.view(1, 1, 8, 4), top_k=2, causal=False, glob_fallback=glob)
+    return dict(q=_np(q), k=_np(k), glob=_np(glob), out=_np(out),
+                rand_proj=_np(lsh.rand_proj)), dict(C=4, top_k=2, max_P=1, R=2)
+
+
 def main():
     sys.path.insert(0, REF)
     import sparse_attention as sa  # the reference module (read-only checkout)
 
+    if "--only-empty-ranked" in sys.argv:
+        rec, meta = lsh_empty_bucket_ranked_case(sa)
+        np.savez_compressed(os.path.join(HERE, "lsh_empty_bucket_ranked.npz"),
+                            meta=json.dumps(meta), **rec)
+        print("wrote lsh_empty_bucket_ranked.npz", rec["out"].tolist())
+        return
     index = []
     for name, cfg_kw, shape, dtype, extra in CASES:
         for seed in SEEDS:
@@ -184,6 +211,10 @@ def main():
     rec, meta = lsh_empty_bucket_case(sa)
     np.savez_compressed(os.path.join(HERE, "lsh_empty_bucket.npz"), meta=json.dumps(meta), **rec)
     index.append("lsh_empty_bucket.npz")
+    rec, meta = lsh_empty_bucket_ranked_case(sa)
+    np.savez_compressed(os.path.join(HERE, "lsh_empty_bucket_ranked.npz"), meta=json.dumps(meta),
+                        **rec)
+    index.append("lsh_empty_bucket_ranked.npz")
     with open(os.path.join(HERE, "index.json"), "w") as f:
         json.dump(index, f, indent=1)
 

@@ -98,6 +98,26 @@ def test_empty_bucket_fallback_uses_global_tokens():
     assert set(nb[0, 0, 0].tolist()) <= {0, 1}
 
 
+def test_empty_bucket_list_competes_on_score_reference_vector():
+    """Reference vector: the glob ++ 0 list of an empty bucket outscores the
+    populated round (query 0 -> [5, 0]).  Query 1 has a k-th place tie among
+    keys 1, 2, 3 (equal scores): any of them is a correct top-2 member."""
+    import os
+    import numpy as np
+    from ssa_amd import LSHGraphBuilder
+    z = np.load(os.path.join(os.path.dirname(__file__), "golden", "lsh_empty_bucket_ranked.npz"))
+    lsh = LSHGraphBuilder(d_head=4, max_num_hashes=1, lsh_candidates=4, num_rounds=2).to(DEV)
+    with torch.no_grad():
+        lsh.rand_proj.copy_(torch.from_numpy(z["rand_proj"]))
+    q = torch.from_numpy(z["q"]).view(1, 1, 2, 4).to(DEV)
+    k = torch.from_numpy(z["k"]).view(1, 1, 8, 4).to(DEV)
+    nb = lsh(q, k, top_k=2, causal=False, glob_fallback=torch.from_numpy(z["glob"]).to(DEV))
+    got = nb.cpu().view(2, 2).tolist()
+    ref = z["out"].reshape(2, 2).tolist()
+    assert got[0] == ref[0]
+    assert got[1][0] == ref[1][0] and got[1][1] in (1, 2, 3)
+
+
 def test_cross_attention_more_queries_than_keys():
     a = _attn(d_model=16, num_heads=1, num_neighbors=4, max_num_hashes=1, window_size=1,
               num_global_tokens=1)

@@ -153,6 +153,16 @@ def test_oracle_empty_bucket_vector():
     np.testing.assert_array_equal(res["idx"], z["out"].reshape(1, 4, 2))
 
 
+def test_oracle_empty_bucket_list_competes_on_score():
+    """Reference vector where the glob ++ 0 list of an empty bucket outscores
+    the populated round: query 0 selects [5, 0]; query 1 has a tie at the
+    k-th place among keys 1..3 that the reference resolves to key 2."""
+    z = np.load(os.path.join(os.path.dirname(__file__), "golden", "lsh_empty_bucket_ranked.npz"))
+    res = oracle.lsh_forward(z["q"].reshape(1, 2, 4), z["k"].reshape(1, 8, 4), z["rand_proj"],
+                             kv_rep=1, P=1, T=0, C=4, top_k=2, causal=False, glob=z["glob"])
+    np.testing.assert_array_equal(res["idx"], z["out"].reshape(1, 2, 2))
+
+
 def test_oracle_projection_path_matches_injected_on_exact_inputs():
     """With exact-arithmetic inputs (small integers) the oracle's own fp32
     projections equal any summation order, so computed == injected."""
@@ -207,3 +217,63 @@ def test_apply_equals_dense_attention_when_graph_is_complete(mode):
     ref = torch.softmax(s, -1) @ torch.from_numpy(v).double()
     tol = 1e-12 if mode == 0 else 2e-2
     assert np.abs(out - ref.numpy()).max() <= tol * np.abs(ref.numpy()).max()
+
+
+# --------------------------------------------------------------------------- planted mistakes
+def _golden_graph_matches(path) -> bool:
+    z, m = load_golden(path)
+    B, N, M, H, d = m["B"], m["N"], m["M"], m["H"], m["d_head"]
+    cfg = m["config"]
+    rp = z["sd_lsh_builder.rand_proj"]
+    R, P = rp.shape[0], m["p_eff"]
+    res = oracle.lsh_forward(z["q"].reshape(B * H, N, d), z["k"].reshape(B * H, M, d), rp,
+                             kv_rep=1, P=P, T=cfg["lsh_num_probes"], C=m["C"],
+                             top_k=m["lsh_k"], causal=m["causal"], glob=z["glob"],
+                             q_proj=z["qproj"].reshape(B * H, R, N, P),
+                             k_proj=z["kproj"].reshape(B * H, R, M, P))
+    nb, va = oracle.merge(z["win"], z["glob"], res["idx"], has_self=not m["cross"],
+                          total_k=cfg["num_neighbors"])
+    return (np.array_equal(res["idx"], z["lsh"].reshape(B * H, N, -1))
+            and np.array_equal(nb, z["neighbors"].reshape(B * H, N, -1))
+            and np.array_equal(va, z["valid"].reshape(B * H, N, -1)))
+
+
+def _pinning_failures():
+    """Names of the oracle's pinning checks that fail (golden vectors, library
+    routines, closed forms)."""
+    failed = []
+    checks = [("sign rule", test_hash_sign_rule_and_bit_order),
+              ("probe flips", test_probe_ids_flip_least_confident_bits_of_base),
+              ("probe ties", test_probe_ties_keep_plane_order),
+              ("empty bucket vector", test_oracle_empty_bucket_vector),
+              ("ranked empty bucket vector", test_oracle_empty_bucket_list_competes_on_score),
+              ("merge closed form", test_merge_closed_form),
+              ("sort vs torch.sort", lambda: test_sort_perm_matches_torch_sort(2, 4096, 3,
+                                                                              "uniform"))]
+    for name, fn in checks:
+        try:
+            fn()
+        except AssertionError:
+            failed.append(name)
+    for path in golden_files():
+        if not _golden_graph_matches(path):
+            failed.append(os.path.basename(path))
+    return failed
+
+
+MUTATIONS = {1: "stable sort", 2: "fillers do not mark their key", 3: "sign rule >= 0",
+             4: "no causal substitution", 5: "no empty-bucket list", 6: "-inf slots -> 0",
+             7: "cumulative probe flips", 8: "one unchunked top-k", 9: "self kept in merge pool"}
+
+
+def test_faithful_oracle_passes_every_pinning_check():
+    assert _pinning_failures() == []
+
+
+@pytest.mark.parametrize("mut", sorted(MUTATIONS), ids=lambda m: MUTATIONS[m])
+def test_planted_mistake_fails_a_pinning_check(mut):
+    """Each plausible mistake in the restatement is caught by at least one of
+    the checks that pin the oracle."""
+    with oracle.mutation(mut):
+        failed = _pinning_failures()
+    assert failed, f"planted mistake '{MUTATIONS[mut]}' passes every pinning check"
