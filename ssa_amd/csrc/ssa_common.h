@@ -104,8 +104,11 @@ __device__ __forceinline__ int lanes_below(uint64_t m) {
 // order-preserving map fp32 -> uint32 (larger float -> larger key); all
 // finite values and +/-inf map above 0, so 0 can mark "no score".
 __device__ __forceinline__ uint32_t score_key(float f) {
-    uint32_t u = __float_as_uint(f);
-    uint32_t k = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    // -0 and +0 compare equal (one key); every NaN ranks above +inf, as the
+    // top-k comparator "NaN first, then >" orders them
+    if (f != f) return 0xffffffffu;
+    const uint32_t u = __float_as_uint(f == 0.f ? 0.f : f);
+    const uint32_t k = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
     return k == 0 ? 1u : k;
 }
 __device__ __forceinline__ float key_score(uint32_t k) {
