@@ -56,7 +56,7 @@ def lib():
         L.ssa_oracle_lsh_forward.argtypes = [
             P, P, ctypes.c_long, ctypes.c_long, ctypes.c_long, ctypes.c_long, ctypes.c_int,
             P, P, P, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
-            ctypes.c_int, ctypes.c_int, P, ctypes.c_int, P, P, P, P]
+            ctypes.c_int, ctypes.c_int, P, ctypes.c_int, P, P, P, P, ctypes.c_long]
         L.ssa_oracle_merge.argtypes = [P, ctypes.c_long, P, ctypes.c_long, P, ctypes.c_long,
                                        ctypes.c_long, ctypes.c_long, ctypes.c_int,
                                        ctypes.c_long, P, P]
@@ -140,13 +140,15 @@ def hash_rows(x, planes, T: int = 0):
 
 
 def lsh_forward(q, k, planes, *, kv_rep: int, P: int, T: int, C: int, top_k: int,
-                causal: bool, glob, q_proj=None, k_proj=None, want_perm: bool = False):
+                causal: bool, glob, q_proj=None, k_proj=None, want_perm: bool = False,
+                q_step: int = 1):
     """LSHGraphBuilder.forward (sparse_attention.py:814-959).
 
     q: (BH, N, d), k: (BK, M, d) with BH = BK * kv_rep, planes: (R, maxP, d).
     Optional injected projections q_proj (BH, R, N, P) / k_proj (BK, R, M, P).
     Returns dict(idx (BH,N,kk) int64, val (BH,N,kk) f32, tie (BH,N) bool,
-    n_ties, perm (BK,R,M) if want_perm).
+    n_ties, perm (BK,R,M) if want_perm).  q_step > 1 computes only the query
+    rows n % q_step == 0; the other rows of idx / val / tie are zero.
 
     Pinned by golden fixtures generated from the reference (tests/golden).
     """
@@ -160,9 +162,9 @@ def lsh_forward(q, k, planes, *, kv_rep: int, P: int, T: int, C: int, top_k: int
     Call = R * (1 + Tp) * C
     kk = min(top_k, Call)
     g = _i64(glob)
-    idx = np.empty((BH, N, kk), np.int64)
-    val = np.empty((BH, N, kk), np.float32)
-    tie = np.empty((BH, N), np.uint8)
+    idx = np.zeros((BH, N, kk), np.int64)
+    val = np.zeros((BH, N, kk), np.float32)
+    tie = np.zeros((BH, N), np.uint8)
     perm = np.empty((BK, R, M), np.int64) if want_perm else None
     qp = _f32(q_proj) if q_proj is not None else None
     kp = _f32(k_proj) if k_proj is not None else None
@@ -170,7 +172,7 @@ def lsh_forward(q, k, planes, *, kv_rep: int, P: int, T: int, C: int, top_k: int
         _p(q), _p(k), BH, kv_rep, N, M, d,
         _p(qp) if qp is not None else None, _p(kp) if kp is not None else None,
         _p(pl), R, maxP, P, T, C, top_k, int(causal), _p(g), g.size,
-        _p(idx), _p(val), _p(tie), _p(perm) if perm is not None else None)
+        _p(idx), _p(val), _p(tie), _p(perm) if perm is not None else None, int(q_step))
     out = dict(idx=idx, val=val, tie=tie.astype(bool), n_ties=int(n_ties))
     if want_perm:
         out["perm"] = perm

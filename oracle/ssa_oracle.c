@@ -353,7 +353,10 @@ long ssa_oracle_lsh_forward(const float *q, const float *k, long BH, long kv_rep
                             int d, const float *q_proj, const float *k_proj, const float *planes,
                             int R, int maxP, int P, int T, int C, int top_k, int causal,
                             const int64_t *glob, int G, int64_t *out_idx, float *out_val,
-                            uint8_t *out_tie, int64_t *out_perm) {
+                            uint8_t *out_tie, int64_t *out_perm, long q_step) {
+    /* q_step > 1 computes only the query rows n % q_step == 0 (the others are
+     * left untouched), for checks at full sizes */
+    if (q_step < 1) q_step = 1;
     const int Tp = T < P ? T : P;                        /* :617 min(num_probes, p_eff) */
     const int nsets = 1 + Tp;
     const long Call = (long)R * nsets * C;
@@ -408,7 +411,7 @@ long ssa_oracle_lsh_forward(const float *q, const float *k, long BH, long kv_rep
         const long g = bh / kv_rep;
         const float *kg = k + g * M * d;
         for (long m = 0; m < M; ++m) stamp[m] = -1;
-        for (long n = 0; n < N; ++n) {
+        for (long n = 0; n < N; n += q_step) {
             const float *qn = q + (bh * N + n) * d;
             /* id sets per round: primary then probes (:793-795) */
             for (int r = 0; r < R; ++r) {
