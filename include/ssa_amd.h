@@ -86,8 +86,9 @@ typedef struct {
     /* outputs */
     int64_t *out_idx;        /* FULL: neighbors (B,Hq,N,k_out); LSH: (B,Hq,N,kk)     */
     uint8_t *out_valid;      /* FULL: (B,Hq,N,k_out); LSH: unused (may be NULL)      */
-    int32_t *out_ties;       /* optional single counter: queries whose k-th LSH score */
-                             /* is tied (selection resolved by stream order)          */
+    int32_t *out_ties;       /* optional single counter (caller zeroes it): queries   */
+                             /* whose kk-th LSH score is tied; their selection is     */
+                             /* replayed with the reference's top-k tie order         */
 } ssa_graph_args;
 
 /* Output width of the FULL graph: self-attention 1 + min(K-1, 2w+1+G+kk),

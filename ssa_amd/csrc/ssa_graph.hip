@@ -14,28 +14,32 @@
 //  3. query bucketing  counting sort of the N queries of each (head, round,
 //                      id set) by bucket id, and a tile list of up to 64
 //                      queries that share one bucket.
-//  4. rescore_kernel   a query's candidate list depends only on its bucket
-//                      (:668-696): the C candidate rows of bucket u are staged
-//                      in LDS once per tile and scored against every query of
-//                      the tile (fp32 dot, q.k unscaled, :909-916).  Scores go
-//                      to S[row][slot], slot = stream position.
+//  4. rescore          a query's candidate list depends only on its bucket
+//                      (:668-696): the C candidate rows of bucket u are scored
+//                      against up to 64 queries of the bucket per tile (MFMA
+//                      for 16-bit inputs, fp32 fma chains otherwise; q.k
+//                      unscaled, :909-916).  Scores go to S[row][slot], slot =
+//                      stream position.  aux_*_kernel scores, with the same
+//                      arithmetic, the keys the lists do not carry: the query
+//                      itself (causal substitution) and glob ++ 0.
 //  5. select_kernel    one wavefront per query walks its candidate stream in
 //                      the reference's concatenation order (round, id set,
 //                      slot, :869-877) with a seen-bitmap of M bits in LDS:
 //                      a slot is kept iff valid and its key was not met at an
 //                      earlier stream position, valid or not (:884-890);
 //                      causal future keys become the query itself (:698-709);
-//                      empty buckets read glob ++ 0 (:711-737).  Kept scores
-//                      are held in registers and the exact top-kk is found by
-//                      a 32-step bitwise search of the order-preserving score
-//                      keys.  Slots without a candidate take glob[t] / 0 by
-//                      position (:948-957).  FULL mode then merges window,
-//                      globals and the LSH set into a key bitmap and reads it
-//                      out in ascending order (:966-1089).
-//
-// Tie rule: when the kk-th and (kk+1)-th kept scores are exactly equal the
-// reference's choice follows its chunked introselect replay; here the tied
-// slots earlier in the stream win.  Such queries are counted in out_ties.
+//                      empty buckets read glob ++ 0 (:711-737).  The kept
+//                      scores above a running lower bound are buffered in LDS
+//                      and the exact kk-th is found by a bitwise search of
+//                      the order-preserving score keys.  Slots without a
+//                      candidate take glob[t] / 0 by position (:948-957).
+//                      FULL mode then merges window, globals and the LSH set
+//                      into a key bitmap and reads it out in ascending order
+//                      (:966-1089).
+//  6. topk_replay      rows whose result depends on the order of equal scores
+//                      (a tied kk-th score; in LSH mode any equal selected
+//                      scores) are rebuilt and run through an exact replay of
+//                      the reference's chunked nth_element + sort (:904-922).
 #include <stdarg.h>
 #include <stdio.h>
 
@@ -55,6 +59,7 @@ struct Dims {
     int B, Hq, Hkv, rep, N, M, d, R, maxP, P, Tp, NS, NB, C, CPL, nlists, G, kk, Kw, Kout;
     int64_t Call, BH, BK;
     int nbh_chunk;
+    int chunk;         // width of the reference's running top-k chunks (:903)
 };
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -545,6 +550,96 @@ __global__ void __launch_bounds__(256) rescore_mfma_kernel(RsP p) {
     }
 }
 
+// ------------------------------------------------------------------ extra scores
+// Per query row: q.k_n (the key that replaces future candidates when causal,
+// :698-709) and q.k_glob[j], q.k_0 (the empty-bucket list, :711-737).  They
+// are computed with exactly the arithmetic of the rescore kernel the same
+// call uses (MFMA k-steps of 32, or one fmaf chain over d), so a key scores
+// the same wherever it appears -- the reference's single einsum gives equal
+// keys equal scores, and ties among them must survive.
+struct AuxP {
+    const void *q, *k;
+    int64_t qsb, qsh, qsn, ksb, ksh, ksn;
+    const int64_t *glob;
+    int N, Hq, Hkv, rep, bh0, nbh, G, NA, causal;
+    float *out;        // (nbh * N, NA)
+};
+
+template <typename T, int D>
+__global__ void __launch_bounds__(256) aux_mfma_kernel(AuxP p) {
+    using V = typename Mfma16<T>::vec;
+    constexpr int KS = (D + 31) / 32;
+    const int wid = threadIdx.x / SSA_WAVE;
+    const int lane = lane_id();
+    const int li = lane % 16, lg = lane / 16;
+    const int nblk = (p.N + 15) / 16;
+    const int64_t wg = (int64_t)blockIdx.x * 4 + wid;
+    if (wg >= (int64_t)p.nbh * nblk) return;
+    const int bhl = (int)(wg / nblk);
+    const int n0 = (int)(wg % nblk) * 16;
+    const int bh = p.bh0 + bhl;
+    const int b = bh / p.Hq, h = bh % p.Hq, g = h / p.rep;
+    const T *qbase = (const T *)p.q + b * p.qsb + h * p.qsh;
+    const T *kbase = (const T *)p.k + b * p.ksb + g * p.ksh;
+    auto frag = [&](const T *src, bool ok, int s) {
+        const int e0 = 32 * s + 8 * lg;
+        if (ok && e0 < D) return __builtin_bit_cast(V, *reinterpret_cast<const uint4 *>(src + e0));
+        return __builtin_bit_cast(V, make_uint4(0, 0, 0, 0));
+    };
+    const int nq = n0 + li;
+    const bool okq = nq < p.N;
+    V qa[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) qa[s] = frag(qbase + (int64_t)(okq ? nq : 0) * p.qsn, okq, s);
+    float *orow = p.out + ((int64_t)bhl * p.N + n0) * p.NA;
+    if (p.causal) {            // column li holds key n0 + li: the diagonal is q_n . k_n
+        V kb[KS];
+#pragma unroll
+        for (int s = 0; s < KS; ++s) kb[s] = frag(kbase + (int64_t)(okq ? nq : 0) * p.ksn, okq, s);
+        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) acc = Mfma16<T>::mma(qa[s], kb[s], acc);
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            const int row = 4 * lg + rr;
+            if (row == li && n0 + row < p.N) orow[(int64_t)row * p.NA] = acc[rr];
+        }
+    }
+    for (int j0 = 0; j0 <= p.G; j0 += 16) {       // columns: glob[0..G-1], then key 0
+        const int j = j0 + li;
+        const int key = j < p.G ? (int)p.glob[j] : 0;
+        V kb[KS];
+#pragma unroll
+        for (int s = 0; s < KS; ++s) kb[s] = frag(kbase + (int64_t)key * p.ksn, true, s);
+        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) acc = Mfma16<T>::mma(qa[s], kb[s], acc);
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            const int row = 4 * lg + rr;
+            if (n0 + row < p.N && j <= p.G) orow[(int64_t)row * p.NA + 1 + j] = acc[rr];
+        }
+    }
+}
+
+template <typename T, int D>
+__global__ void __launch_bounds__(256) aux_valu_kernel(AuxP p) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (int64_t)p.nbh * p.N * p.NA) return;
+    const int a = (int)(idx % p.NA);
+    const int64_t rloc = idx / p.NA;
+    const int n = (int)(rloc % p.N);
+    const int bh = p.bh0 + (int)(rloc / p.N);
+    const int b = bh / p.Hq, h = bh % p.Hq, g = h / p.rep;
+    if (a == 0 && !p.causal) return;
+    const int key = a == 0 ? n : (a - 1 < p.G ? (int)p.glob[a - 1] : 0);
+    const T *qr = (const T *)p.q + b * p.qsb + h * p.qsh + (int64_t)n * p.qsn;
+    const T *kr = (const T *)p.k + b * p.ksb + g * p.ksh + (int64_t)key * p.ksn;
+    float acc = 0.f;
+    for (int c = 0; c < D; ++c) acc = fmaf(to_f32(qr[c]), to_f32(kr[c]), acc);
+    p.out[idx] = acc;
+}
+
 // ------------------------------------------------------------------ select + merge
 struct SelP {
     const uint16_t *qid;
@@ -559,6 +654,10 @@ struct SelP {
     int64_t *out_idx;
     uint8_t *out_valid;
     int32_t *ties;
+    int32_t *tie_list;     // rows (within the chunk) handed to the exact top-k replay
+    int32_t *tie_count;
+    const float *aux;      // per row: q.k_n, then q.k_glob[j] (j < G), then q.k_0
+    int NA;
     int64_t nblocks;
 };
 
@@ -677,6 +776,58 @@ constexpr int CH_FIRST = 1 << 15;      // first chunk of its list
 __device__ __forceinline__ int CH_LANES(int y) { return y & 127; }
 __device__ __forceinline__ int CH_REAL(int y) { return (y >> 7) & 127; }
 
+// FULL mode tail (merge_neighbors, sparse_attention.py:966-1089): `bm` holds
+// the selected LSH keys; adds the window (:368-376), the globals, key 0 when a
+// -inf slot at or past G falls back to it (:948-957), removes the query itself
+// and writes [self] ++ the ascending union, zero-padded and marked invalid.
+__device__ void full_merge_emit(uint32_t *bm, const SelP &p, int n, int64_t row, int f) {
+    const int lane = lane_id();
+    const int kk = p.kk;
+    if (!p.cross) {
+        for (int o = -p.window + lane; o <= p.window; o += SSA_WAVE) {
+            int x = n + o;
+            if (p.causal && o > 0) x = n;
+            x = x < 0 ? 0 : (x > p.M - 1 ? p.M - 1 : x);
+            bm_set(bm, x);
+        }
+    }
+    for (int j = lane; j < p.G; j += SSA_WAVE) bm_set(bm, (int)p.glob[j]);
+    if (lane == 0 && (f > p.G ? f : p.G) < kk) bm_set(bm, 0);
+    wave_lds_sync();
+    if (!p.cross && lane == 0) atomicAnd(&bm[n >> 5], ~(1u << (n & 31)));
+    wave_lds_sync();
+
+    const int self = p.cross ? 0 : 1;
+    const int ks = p.Kout - self;
+    int64_t *orow = p.out_idx + row * p.Kout;
+    uint8_t *vrow = p.out_valid + row * p.Kout;
+    const int wpl = (p.words + SSA_WAVE - 1) / SSA_WAVE;
+    const int w0 = lane * wpl;
+    int cntb = 0;
+    for (int w = w0; w < w0 + wpl && w < p.words; ++w) cntb += __popc(bm[w]);
+    int pos = wave_excl_scan(cntb);
+    const int total = wave_sum_i(cntb);
+    for (int w = w0; w < w0 + wpl && w < p.words && pos < ks; ++w) {
+        uint32_t word = bm[w];
+        while (word && pos < ks) {
+            const int bitp = __ffs(word) - 1;
+            word &= word - 1;
+            orow[self + pos] = (int64_t)(w * 32 + bitp);
+            vrow[self + pos] = 1;
+            ++pos;
+        }
+    }
+    const int filled = total < ks ? total : ks;
+    for (int i = self + filled + lane; i < p.Kout; i += SSA_WAVE) {
+        orow[i] = 0;
+        vrow[i] = 0;
+    }
+    if (self && lane == 0) {
+        orow[0] = n;
+        vrow[0] = 1;
+    }
+}
+
 // One wavefront per query row, streaming over the query's candidate stream in
 // the reference's concatenation order (round, id set, slot):
 //  pass 1  key id and score of every slot; first occurrence in stream order,
@@ -719,16 +870,11 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     const int b = bh / p.Hq, h = bh % p.Hq, g = h / p.rep;
     const int bk = b * p.Hkv + g;
     const int64_t row = (int64_t)bh * p.N + n;
-    const T *qrow = (const T *)p.q + b * p.qsb + h * p.qsh + (int64_t)n * p.qsn;
-    const T *kbase = (const T *)p.k + b * p.ksb + g * p.ksh;
-    float qv[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int e = lane + 64 * i;
-        qv[i] = e < p.d ? to_f32(qrow[e]) : 0.f;
-    }
-    const uint32_t kself =
-        p.causal ? score_key(dot_row<T>(qv, kbase + (int64_t)n * p.ksn, p.d)) : 0u;
+    // scores the candidate lists do not carry (computed with the rescore's
+    // arithmetic, so equal keys get equal scores): the query's own key, which
+    // replaces future candidates, and the empty-bucket list glob ++ 0
+    const float *arow = p.aux + rloc * p.NA;
+    const uint32_t kself = p.causal ? score_key(arow[0]) : 0u;
     const uint16_t *qids = p.qid + row * p.R * p.NS;
     const float *srow = p.S + ((int64_t)bhl * p.N + n) * p.Call;
     const int ng = min(p.G + 1, SSA_WAVE);
@@ -751,13 +897,7 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
         tab[ci] = d4;
         any_empty |= sz == 0;
     }
-    if (wave_ballot(any_empty)) {          // scores of glob[0..G-1] and key 0 (:711-737)
-        for (int j = 0; j < ng; ++j) {
-            const int v = j < p.G ? (int)p.glob[j] : 0;
-            const float sc = dot_row<T>(qv, kbase + (int64_t)v * p.ksn, p.d);
-            if (lane == 0) gsc[j] = sc;
-        }
-    }
+    if (wave_ballot(any_empty) && lane < ng) gsc[lane] = arow[1 + lane];   // (:711-737)
     wave_lds_sync();
 
     auto list_info = [&](int list) {
@@ -901,6 +1041,7 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     // ---- threshold
     uint32_t thr = 0u;                 // 0: every kept key is selected
     int need = 0;
+    bool btie = false;                 // several kept keys equal the kk-th one
     const bool compacted = !overflow;  // every key >= the threshold is in ckey
     if (nk > kk) {
         if (compacted) {
@@ -925,7 +1066,7 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
             ge = wave_count<4>(ge);
             gt = wave_count<4>(gt);
             need = kk - gt;
-            if (ge - gt > need && lane == 0 && p.ties) atomicAdd(p.ties, 1);
+            btie = ge - gt > need;
         } else {
             // rare: exact search over the whole kept stream (one walk per bit)
             uint32_t t0 = 0u;
@@ -944,9 +1085,10 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
                 gt += __popcll(wave_ballot(keep & (kv > thr)));
             });
             need = kk - gt;
-            if (ge - gt > need && lane == 0 && p.ties) atomicAdd(p.ties, 1);
+            btie = ge - gt > need;
         }
     }
+    if (btie && lane == 0 && p.ties) atomicAdd(p.ties, 1);
     const int f = nk < kk ? nk : kk;
 
     // ---- emit the selected slots
@@ -1002,62 +1144,410 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
 
     if (LSH_MODE) {
         int64_t *orow = p.out_idx + row * kk;
+        bool dup = false;
         for (int e = lane; e < f; e += SSA_WAVE) {
             const uint32_t k0 = ekey[e], s0 = eslot[e];
             int rank = 0;
             for (int e2 = 0; e2 < f; ++e2) {
                 const uint32_t k2 = ekey[e2];
                 rank += (k2 > k0) || (k2 == k0 && eslot[e2] < s0);
+                dup |= (k2 == k0) && (e2 != e);
             }
             orow[rank] = (int64_t)eval[e];
         }
         for (int t = f + lane; t < kk; t += SSA_WAVE) orow[t] = t < p.G ? p.glob[t] : 0;
+        // the order among equal scores (and a tied kk-th place) follows the
+        // reference's nth_element / sort internals: replayed exactly later
+        if ((btie || wave_ballot(dup)) && lane == 0 && p.tie_list)
+            p.tie_list[atomicAdd(p.tie_count, 1)] = (int)rloc;
         return;
     }
+    if (btie && lane == 0 && p.tie_list) p.tie_list[atomicAdd(p.tie_count, 1)] = (int)rloc;
 
-    // FULL: pool = window + globals + LSH (+ fallback 0), minus self
-    if (!p.cross) {
-        for (int o = -p.window + lane; o <= p.window; o += SSA_WAVE) {
-            int x = n + o;
-            if (p.causal && o > 0) x = n;
-            x = x < 0 ? 0 : (x > p.M - 1 ? p.M - 1 : x);
-            bm_set(bm, x);
+    full_merge_emit(bm, p, n, row, f);
+}
+
+// ------------------------------------------------------------------ exact top-k replay
+// A row whose kk-th kept score is tied, or (LSH mode) whose selected scores are
+// not all distinct, depends on how the reference's running top-k orders equal
+// scores: torch.topk on the CPU is std::nth_element(kk-1) followed by
+// std::sort of the first kk-1, over best ++ chunk, chunk by chunk (:904-922).
+// Such rows are replayed here, one wavefront per row: the candidate stream is
+// rebuilt chunk by chunk (same keys, scores and first-occurrence rule as the
+// select kernel), and every nth_element / sort runs as libstdc++ runs it:
+// median-of-three Hoare partitions (data-parallel, as in the bucket sort),
+// heap fallbacks at the depth limit and final insertion sorts, all on keys
+// ordered by the top-k comparator ("NaN first, then >").
+constexpr int RP_WAVES = 2;
+constexpr uint32_t RP_NEGINF = 0xff800000u;   // rank key of -inf: ~score_key(-inf)
+constexpr int RP_STACK = 64;
+
+__host__ __device__ inline int rp_lds_words(int W, int words) {
+    return (3 * W + (W + 31) / 32 + 1 + 3 * RP_STACK + words + 64 + 1) & ~1;
+}
+
+__device__ __forceinline__ void rp_sync() {
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+struct RpArr {
+    uint32_t *key;     // rank keys: smaller = earlier in top-k order
+    int32_t *cand;     // key ids carried along
+};
+
+__device__ __forceinline__ void rp_swap(const RpArr &a, int i, int j) {
+    const uint32_t tk = a.key[i];
+    const int32_t tc = a.cand[i];
+    a.key[i] = a.key[j]; a.cand[i] = a.cand[j];
+    a.key[j] = tk; a.cand[j] = tc;
+}
+
+// ---- single-lane heap routines (depth-limit fallbacks, partial_sort)
+__device__ void rp_push_up(const RpArr &a, int base, int hole, int top, uint32_t vk, int32_t vc) {
+    int parent = (hole - 1) / 2;
+    while (hole > top && a.key[base + parent] < vk) {
+        a.key[base + hole] = a.key[base + parent];
+        a.cand[base + hole] = a.cand[base + parent];
+        hole = parent;
+        parent = (hole - 1) / 2;
+    }
+    a.key[base + hole] = vk;
+    a.cand[base + hole] = vc;
+}
+
+__device__ void rp_adjust(const RpArr &a, int base, int hole, int len, uint32_t vk, int32_t vc) {
+    const int top = hole;
+    int child = hole;
+    while (child < (len - 1) / 2) {
+        child = 2 * (child + 1);
+        if (a.key[base + child] < a.key[base + child - 1]) child--;
+        a.key[base + hole] = a.key[base + child];
+        a.cand[base + hole] = a.cand[base + child];
+        hole = child;
+    }
+    if ((len & 1) == 0 && child == (len - 2) / 2) {
+        child = 2 * (child + 1);
+        a.key[base + hole] = a.key[base + child - 1];
+        a.cand[base + hole] = a.cand[base + child - 1];
+        hole = child - 1;
+    }
+    rp_push_up(a, base, hole, top, vk, vc);
+}
+
+// heap_select(f, mid, l): [f, mid) becomes a max-heap of the mid-f smallest
+__device__ void rp_heap_select(const RpArr &a, int f, int mid, int l) {
+    const int len = mid - f;
+    if (len >= 2) {
+        for (int parent = (len - 2) / 2;; --parent) {
+            rp_adjust(a, f, parent, len, a.key[f + parent], a.cand[f + parent]);
+            if (parent == 0) break;
         }
     }
-    for (int j = lane; j < p.G; j += SSA_WAVE) bm_set(bm, (int)p.glob[j]);
-    if (lane == 0 && (f > p.G ? f : p.G) < kk) bm_set(bm, 0);
-    wave_lds_sync();
-    if (!p.cross && lane == 0) atomicAnd(&bm[n >> 5], ~(1u << (n & 31)));
-    wave_lds_sync();
-
-    const int self = p.cross ? 0 : 1;
-    const int ks = p.Kout - self;
-    int64_t *orow = p.out_idx + row * p.Kout;
-    uint8_t *vrow = p.out_valid + row * p.Kout;
-    const int wpl = (p.words + SSA_WAVE - 1) / SSA_WAVE;
-    const int w0 = lane * wpl;
-    int cntb = 0;
-    for (int w = w0; w < w0 + wpl && w < p.words; ++w) cntb += __popc(bm[w]);
-    int pos = wave_excl_scan(cntb);
-    const int total = wave_sum_i(cntb);
-    for (int w = w0; w < w0 + wpl && w < p.words && pos < ks; ++w) {
-        uint32_t word = bm[w];
-        while (word && pos < ks) {
-            const int bitp = __ffs(word) - 1;
-            word &= word - 1;
-            orow[self + pos] = (int64_t)(w * 32 + bitp);
-            vrow[self + pos] = 1;
-            ++pos;
+    for (int i = mid; i < l; ++i) {
+        if (a.key[i] < a.key[f]) {
+            const uint32_t vk = a.key[i];
+            const int32_t vc = a.cand[i];
+            a.key[i] = a.key[f];
+            a.cand[i] = a.cand[f];
+            rp_adjust(a, f, 0, len, vk, vc);
         }
     }
-    const int filled = total < ks ? total : ks;
-    for (int i = self + filled + lane; i < p.Kout; i += SSA_WAVE) {
-        orow[i] = 0;
-        vrow[i] = 0;
+}
+
+__device__ void rp_heap_sort(const RpArr &a, int f, int l) {
+    while (l - f > 1) {
+        --l;
+        const uint32_t vk = a.key[l];
+        const int32_t vc = a.cand[l];
+        a.key[l] = a.key[f];
+        a.cand[l] = a.cand[f];
+        rp_adjust(a, f, 0, l - f, vk, vc);
     }
-    if (self && lane == 0) {
-        orow[0] = n;
-        vrow[0] = 1;
+}
+
+__device__ void rp_insertion(const RpArr &a, int f, int l) {
+    for (int i = f + 1; i < l; ++i) {
+        const uint32_t vk = a.key[i];
+        const int32_t vc = a.cand[i];
+        int j = i;
+        while (j > f && vk < a.key[j - 1]) {
+            a.key[j] = a.key[j - 1];
+            a.cand[j] = a.cand[j - 1];
+            --j;
+        }
+        a.key[j] = vk;
+        a.cand[j] = vc;
+    }
+}
+
+// ---- one wavefront partitions [f, l) (median of f+1, middle, l-1 moved to f,
+// then the unguarded Hoare scan, done from the stopper lists); returns the cut
+__device__ int rp_partition(const RpArr &a, uint16_t *TL, uint16_t *TR, int f, int l) {
+    const int lane = lane_id();
+    const int n = l - f;
+    const int ia = f + 1, ib = f + n / 2, ic = l - 1;
+    const uint32_t ka = a.key[ia], kb = a.key[ib], kc = a.key[ic];
+    int x;
+    if (ka < kb) {
+        if (kb < kc) x = ib;
+        else if (ka < kc) x = ic;
+        else x = ia;
+    } else if (ka < kc) x = ia;
+    else if (kb < kc) x = ic;
+    else x = ib;
+    const uint32_t pv = a.key[x];
+    rp_sync();
+    if (lane == 0) rp_swap(a, f, x);
+    rp_sync();
+    int numL = 0, numR = 0;
+    for (int base = f; base < l; base += SSA_WAVE) {
+        const int i = base + lane;
+        const bool in = i < l;
+        const uint32_t kv = in ? a.key[i] : 0u;
+        const bool isL = in && i > f && kv >= pv;
+        const bool isR = in && kv <= pv;
+        const uint64_t bL = wave_ballot(isL), bR = wave_ballot(isR);
+        if (isL) TL[f + numL + lanes_below(bL)] = (uint16_t)i;
+        if (isR) TR[f + numR + lanes_below(bR)] = (uint16_t)i;
+        numL += __popcll(bL);
+        numR += __popcll(bR);
+    }
+    rp_sync();
+    int lo = 0, hi = numL < numR ? numL : numR;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if ((int)TL[f + mid - 1] < (int)TR[f + numR - mid]) lo = mid; else hi = mid - 1;
+    }
+    const int sw = lo;
+    for (int k0 = 0; k0 < sw; k0 += SSA_WAVE) {
+        const int k = k0 + lane;
+        if (k < sw) rp_swap(a, TL[f + k], TR[f + numR - 1 - k]);
+    }
+    int cut = 0x7fffffff;
+    if (sw < numL) cut = TL[f + sw];
+    if (sw > 0) { const int r = TR[f + numR - sw]; cut = r < cut ? r : cut; }
+    rp_sync();
+    return cut;
+}
+
+__device__ __forceinline__ int rp_log2(int n) { return 31 - __clz(n); }
+
+// std::nth_element(f, nth, l)
+__device__ void rp_nth_element(const RpArr &a, uint16_t *TL, uint16_t *TR, int f, int nth, int l) {
+    if (f == l || nth == l) return;
+    int depth = 2 * rp_log2(l - f);
+    while (l - f > 3) {
+        if (depth == 0) {
+            if (lane_id() == 0) {
+                rp_heap_select(a, f, nth + 1, l);
+                rp_swap(a, f, nth);
+            }
+            rp_sync();
+            return;
+        }
+        --depth;
+        const int cut = rp_partition(a, TL, TR, f, l);
+        if (cut <= nth) f = cut; else l = cut;
+    }
+    if (lane_id() == 0) rp_insertion(a, f, l);
+    rp_sync();
+}
+
+// std::sort(f, l): introsort loop over an explicit stack, then the final
+// insertion sort, which stops at every partition cut, so it runs per leaf
+__device__ void rp_sort(const RpArr &a, uint16_t *TL, uint16_t *TR, uint32_t *lbits,
+                        int32_t *stk, int f, int l) {
+    const int lane = lane_id();
+    if (l - f < 2) return;
+    for (int w = lane; w < (l + 31) / 32 + 1; w += SSA_WAVE) lbits[w] = 0u;
+    rp_sync();
+    if (lane == 0) atomicOr(&lbits[f >> 5], 1u << (f & 31));
+    int top = 0;
+    if (l - f > 16) {
+        if (lane == 0) { stk[0] = f; stk[RP_STACK] = l; stk[2 * RP_STACK] = 2 * rp_log2(l - f); }
+        top = 1;
+    }
+    rp_sync();
+    while (top > 0) {
+        --top;
+        const int sf = stk[top], sl = stk[RP_STACK + top], sd = stk[2 * RP_STACK + top];
+        rp_sync();
+        if (sd == 0) {
+            if (lane == 0) {
+                rp_heap_select(a, sf, sl, sl);
+                rp_heap_sort(a, sf, sl);
+            }
+            rp_sync();
+            continue;
+        }
+        const int cut = rp_partition(a, TL, TR, sf, sl);
+        if (lane == 0) {
+            atomicOr(&lbits[cut >> 5], 1u << (cut & 31));
+            int t = top;
+            if (sl - cut > 16) { stk[t] = cut; stk[RP_STACK + t] = sl; stk[2 * RP_STACK + t] = sd - 1; ++t; }
+            if (cut - sf > 16) { stk[t] = sf; stk[RP_STACK + t] = cut; stk[2 * RP_STACK + t] = sd - 1; ++t; }
+        }
+        top += (sl - cut > 16) + (cut - sf > 16);
+        rp_sync();
+    }
+    // leaf starts in order, then one leaf per lane
+    int nl = 0;
+    for (int base = f; base < l; base += SSA_WAVE) {
+        const int i = base + lane;
+        const bool st = i < l && ((lbits[i >> 5] >> (i & 31)) & 1u);
+        const uint64_t m = wave_ballot(st);
+        if (st) TL[nl + lanes_below(m)] = (uint16_t)i;
+        nl += __popcll(m);
+    }
+    rp_sync();
+    for (int i = lane; i < nl; i += SSA_WAVE) {
+        const int s0 = TL[i];
+        const int e = i + 1 < nl ? (int)TL[i + 1] : l;
+        rp_insertion(a, s0, e);
+    }
+    rp_sync();
+}
+
+template <typename T, bool LSH_MODE>
+__global__ void __launch_bounds__(RP_WAVES * SSA_WAVE)
+topk_replay_kernel(SelP p, int chunk, int W) {
+    extern __shared__ uint32_t rp_smem[];
+    const int wid = threadIdx.x / SSA_WAVE;
+    const int lane = lane_id();
+    uint32_t *base = rp_smem + (int64_t)wid * rp_lds_words(W, p.words);
+    RpArr A;
+    A.key = base;
+    A.cand = (int32_t *)(base + W);
+    uint16_t *TL = (uint16_t *)(base + 2 * W);
+    uint16_t *TR = TL + W;
+    uint32_t *lbits = base + 3 * W;
+    int32_t *stk = (int32_t *)(lbits + (W + 31) / 32 + 1);
+    uint32_t *bm = (uint32_t *)(stk + 3 * RP_STACK);
+    float *gsc = (float *)(bm + p.words);
+
+    const int total = (int)gridDim.x * RP_WAVES;
+    const int cnt = *p.tie_count;
+    const int kk = p.kk;
+    for (int it = (int)blockIdx.x * RP_WAVES + wid; it < cnt; it += total) {
+        const int64_t rloc = p.tie_list[it];
+        const int n = (int)(rloc % p.N);
+        const int bhl = (int)(rloc / p.N);
+        const int bh = p.bh0 + bhl;
+        const int b = bh / p.Hq, h = bh % p.Hq, g = h / p.rep;
+        const int bk = b * p.Hkv + g;
+        const int64_t row = (int64_t)bh * p.N + n;
+        const float *arow = p.aux + rloc * p.NA;
+        const float kself = p.causal ? arow[0] : 0.f;
+        const int ng = min(p.G + 1, SSA_WAVE);
+        if (lane < ng) gsc[lane] = arow[1 + lane];
+        for (int w = lane; w < p.words; w += SSA_WAVE) bm[w] = 0u;
+        for (int t = lane; t < kk; t += SSA_WAVE) { A.key[t] = RP_NEGINF; A.cand[t] = 0; }
+        const uint16_t *qids = p.qid + row * p.R * p.NS;
+        const float *srow = p.S + ((int64_t)bhl * p.N + n) * p.Call;
+        rp_sync();
+
+        for (int64_t s0 = 0; s0 < p.Call; s0 += chunk) {
+            const int64_t s1 = s0 + chunk < p.Call ? s0 + chunk : p.Call;
+            // rebuild the stream slots [s0, s1) in groups that stay inside one list
+            for (int64_t j0 = s0; j0 < s1;) {
+                const int list = (int)(j0 / p.C);
+                const int c0 = (int)(j0 - (int64_t)list * p.C);
+                int nl = p.C - c0;
+                nl = nl < SSA_WAVE ? nl : SSA_WAVE;
+                nl = (int64_t)nl < s1 - j0 ? nl : (int)(s1 - j0);
+                const int u = qids[list];
+                const int64_t prow = (int64_t)bk * p.R + list / p.NS;
+                const int st = p.bstart[prow * p.NB + u];
+                const int sz = p.bsize[prow * p.NB + u];
+                const int c = c0 + lane;
+                const bool in = lane < nl;
+                int v = 0;
+                bool keep = false;
+                float sc = 0.f;
+                if (sz > 0) {
+                    const bool real = in && c < min(sz, p.C);
+                    const int raw = in ? p.perm[prow * p.M + (real ? st + c : p.M - 1)] : 0;
+                    v = (p.causal && raw > n) ? n : raw;
+                    const uint32_t bit = 1u << (v & 31);
+                    const uint32_t old = atomicOr(&bm[v >> 5], real ? bit : 0u);
+                    const bool fill = in && !real;
+                    if (wave_ballot(fill)) atomicOr(&bm[v >> 5], fill ? bit : 0u);
+                    keep = real && !(old & bit);
+                    if (p.causal) {
+                        // several slots of this group became the query itself:
+                        // the earliest one is the first occurrence
+                        const uint64_t nm = wave_ballot(real && v == n);
+                        if (__popcll(nm) > 1) {
+                            const bool clr = real && v == n && !(old & bit);
+                            const bool seen = wave_ballot(clr) == 0ull;
+                            if (real && v == n)
+                                keep = !seen && lane == (int)(__ffsll((long long)nm) - 1);
+                        }
+                    }
+                    if (keep) sc = (p.causal && v == n) ? kself : srow[j0 + lane];
+                } else {
+                    // empty bucket: glob ++ 0, all valid; duplicates resolved in slot order
+                    const int jg = c < ng - 1 ? c : ng - 1;
+                    v = (c < p.G) ? (int)p.glob[c < p.G ? c : 0] : 0;
+                    bool pending = in;
+                    uint64_t pm = wave_ballot(pending);
+                    while (pm) {
+                        const int leader = (int)(__ffsll((long long)pm) - 1);
+                        const int vl = __shfl(v, leader, SSA_WAVE);
+                        const bool same = pending && v == vl;
+                        if (lane == leader) {
+                            const uint32_t bit = 1u << (v & 31);
+                            const uint32_t old = atomicOr(&bm[v >> 5], bit);
+                            keep = !(old & bit);
+                        }
+                        pending = pending && !same;
+                        pm = wave_ballot(pending);
+                    }
+                    if (keep) sc = gsc[jg];
+                }
+                if (in) {
+                    const int at = kk + (int)(j0 - s0) + lane;
+                    A.key[at] = keep ? ~score_key(sc) : RP_NEGINF;
+                    A.cand[at] = v;
+                }
+                rp_sync();
+                j0 += nl;
+            }
+            // torch.topk(best ++ chunk, kk): partial_sort when 64*kk <= width,
+            // else nth_element(kk-1) + sort(kk-1)
+            const int w = kk + (int)(s1 - s0);
+            if ((int64_t)kk * 64 <= w) {
+                if (lane == 0) {
+                    rp_heap_select(A, 0, kk, w);
+                    rp_heap_sort(A, 0, kk);
+                }
+                rp_sync();
+            } else {
+                rp_nth_element(A, TL, TR, 0, kk - 1, w);
+                rp_sort(A, TL, TR, lbits, stk, 0, kk - 1);
+            }
+        }
+        // A[0, kk) is the reference's best list: finite entries first
+        int fcount = 0;
+        for (int t0 = 0; t0 < kk; t0 += SSA_WAVE) {
+            const int t = t0 + lane;
+            fcount += __popcll(wave_ballot(t < kk && A.key[t] != RP_NEGINF));
+        }
+        if (LSH_MODE) {
+            int64_t *orow = p.out_idx + row * kk;
+            for (int t = lane; t < kk; t += SSA_WAVE)
+                orow[t] = t < fcount ? (int64_t)A.cand[t] : (t < p.G ? p.glob[t] : 0);
+        } else {
+            for (int w = lane; w < p.words; w += SSA_WAVE) bm[w] = 0u;
+            rp_sync();
+            for (int t = lane; t < fcount; t += SSA_WAVE) bm_set(bm, A.cand[t]);
+            rp_sync();
+            full_merge_emit(bm, p, n, row, fcount);
+        }
+        rp_sync();
     }
 }
 
@@ -1065,7 +1555,8 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
 int supported_d(int d) { return d >= 4 && d <= 256 && (d & (d - 1)) == 0; }
 
 struct Layout {
-    int64_t kid, qid, perm, bstart, bsize, sorttmp, cnt, off, cur, qlist, tiles, ntiles, S, total;
+    int64_t kid, qid, perm, bstart, bsize, sorttmp, cnt, off, cur, qlist, tiles, ntiles, S,
+        tie_list, tie_count, aux, total;
 };
 
 int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
@@ -1089,6 +1580,9 @@ Layout plan(const Dims &D) {
     L.tiles = take(ninst * (ceil_div(D.N, TQ) + D.NB) * 16);
     L.ntiles = take(4);
     L.S = take(nbh * D.N * D.Call * 4);
+    L.tie_list = take(nbh * D.N * 4);
+    L.tie_count = take(4);
+    L.aux = take(nbh * D.N * (D.G + 2) * 4);
     L.total = o;
     return L;
 }
@@ -1127,6 +1621,12 @@ int make_dims(const ssa_graph_args *a, Dims &D) {
     D.G = a->G;
     D.Call = (int64_t)a->R * D.NS * a->C;
     D.kk = (int)(a->top_k < D.Call ? a->top_k : D.Call);
+    {
+        int64_t ch = 4 * (int64_t)D.kk;
+        if (ch < 256) ch = 256;
+        if (ch > D.Call) ch = D.Call;
+        D.chunk = (int)ch;
+    }
     D.BH = (int64_t)a->B * a->Hq;
     D.BK = (int64_t)a->B * a->Hkv;
     const int self = a->is_cross ? 0 : 1;
@@ -1244,9 +1744,14 @@ bool rows_aligned16(const RsP &rp, int elem) {
 }
 
 template <typename T>
+bool rescore_uses_mfma(int d, const RsP &rp) {
+    return !std::is_same<T, float>::value && d >= 8 && d <= 128 && rows_aligned16(rp, 2);
+}
+
+template <typename T>
 int rescore_dispatch(int d, const RsP &rp, int64_t grid, hipStream_t st) {
     if constexpr (!std::is_same<T, float>::value) {
-        if (d >= 8 && d <= 128 && rows_aligned16(rp, 2)) {
+        if (rescore_uses_mfma<T>(d, rp)) {
             switch (d) {
                 case 8: return launch_rescore_mfma<T, 8>(rp, grid, st);
                 case 16: return launch_rescore_mfma<T, 16>(rp, grid, st);
@@ -1282,6 +1787,55 @@ int launch_select(const SelP &sp, hipStream_t st) {
     const int64_t grid = 8 * ceil_div(sp.nblocks, 8);
     hipLaunchKernelGGL((select_kernel<T, LSH>), dim3((unsigned)grid), dim3(SEL_WAVES * SSA_WAVE),
                        lds, st, sp);
+    SSA_CHECK_LAUNCH();
+    return SSA_OK;
+}
+
+// Extra scores with the arithmetic of the rescore kernel rescore_dispatch picks
+template <typename T>
+int aux_dispatch(int d, bool mfma, const AuxP &ap, hipStream_t st) {
+    const int64_t rows = (int64_t)ap.nbh * ap.N;
+    if constexpr (!std::is_same<T, float>::value) {
+        if (mfma) {
+            const int64_t waves = (int64_t)ap.nbh * ((ap.N + 15) / 16);
+            const dim3 grid((unsigned)ceil_div(waves, 4));
+#define SSA_AUX_MFMA(DD) \
+    case DD: hipLaunchKernelGGL((aux_mfma_kernel<T, DD>), grid, dim3(256), 0, st, ap); break;
+            switch (d) {
+                SSA_AUX_MFMA(8) SSA_AUX_MFMA(16) SSA_AUX_MFMA(32) SSA_AUX_MFMA(64)
+                SSA_AUX_MFMA(128)
+                default: ssa_set_error("aux scores: head dim %d", d); return SSA_E_UNSUP;
+            }
+#undef SSA_AUX_MFMA
+            SSA_CHECK_LAUNCH();
+            return SSA_OK;
+        }
+    }
+    const dim3 grid((unsigned)ceil_div(rows * ap.NA, 256));
+#define SSA_AUX_VALU(DD) \
+    case DD: hipLaunchKernelGGL((aux_valu_kernel<T, DD>), grid, dim3(256), 0, st, ap); break;
+    switch (d) {
+        SSA_AUX_VALU(4) SSA_AUX_VALU(8) SSA_AUX_VALU(16) SSA_AUX_VALU(32) SSA_AUX_VALU(64)
+        SSA_AUX_VALU(128) SSA_AUX_VALU(256)
+        default: ssa_set_error("aux scores: head dim %d", d); return SSA_E_UNSUP;
+    }
+#undef SSA_AUX_VALU
+    SSA_CHECK_LAUNCH();
+    return SSA_OK;
+}
+
+// Exact top-k replay of the rows select flagged.  Rows whose replay does not
+// fit LDS (kk + chunk above ~12k slots) keep the select kernel's rule.
+template <typename T, bool LSH>
+int launch_replay(const SelP &sp, int chunk, hipStream_t st) {
+    const int W = sp.kk + chunk;
+    const size_t lds = (size_t)RP_WAVES * rp_lds_words(W, sp.words) * 4;
+    if (lds > SSA_LDS_BYTES || W > 65535) return SSA_OK;
+    SSA_CHECK_HIP(hipFuncSetAttribute((const void *)topk_replay_kernel<T, LSH>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    const int64_t blocks = std::min<int64_t>(ceil_div(sp.rows, RP_WAVES), 1024);
+    hipLaunchKernelGGL((topk_replay_kernel<T, LSH>), dim3((unsigned)blocks),
+                       dim3(RP_WAVES * SSA_WAVE), lds, st, sp, chunk, W);
     SSA_CHECK_LAUNCH();
     return SSA_OK;
 }
@@ -1343,6 +1897,16 @@ int build_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *w
         const int64_t grid = (int64_t)ninst * (ceil_div(D.N, TQ) + D.NB);
         rc = rescore_dispatch<T>(D.d, rp, grid, st);
         if (rc) return rc;
+        AuxP ap{};
+        ap.q = a->q.ptr; ap.k = a->k.ptr;
+        ap.qsb = a->q.sb; ap.qsh = a->q.sh; ap.qsn = a->q.sn;
+        ap.ksb = a->k.sb; ap.ksh = a->k.sh; ap.ksn = a->k.sn;
+        ap.glob = a->glob;
+        ap.N = D.N; ap.Hq = D.Hq; ap.Hkv = D.Hkv; ap.rep = D.rep; ap.bh0 = (int)bh0;
+        ap.nbh = nbh; ap.G = D.G; ap.NA = D.G + 2; ap.causal = a->causal;
+        ap.out = (float *)(ws + L.aux);
+        rc = aux_dispatch<T>(D.d, rescore_uses_mfma<T>(D.d, rp), ap, st);
+        if (rc) return rc;
 
         SelP sp{};
         sp.qid = qp.qid; sp.perm = rp.perm; sp.bstart = rp.bstart; sp.bsize = rp.bsize;
@@ -1357,8 +1921,17 @@ int build_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *w
         sp.Kout = D.Kout; sp.bh0 = (int)bh0; sp.words = ((D.M + 31) / 32 + 2) & ~1;
         sp.Call = D.Call; sp.rows = (int64_t)nbh * D.N;
         sp.out_idx = a->out_idx; sp.out_valid = a->out_valid; sp.ties = a->out_ties;
+        sp.tie_list = (int32_t *)(ws + L.tie_list);
+        sp.tie_count = (int32_t *)(ws + L.tie_count);
+        sp.aux = ap.out;
+        sp.NA = ap.NA;
         sp.nblocks = ceil_div(sp.rows, SEL_WAVES);
+        hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(64), 0, st, sp.tie_count, (int64_t)1, 0);
+        SSA_CHECK_LAUNCH();
         rc = select_dispatch<T>(sp, st);
+        if (rc) return rc;
+        rc = sp.mode == SSA_GRAPH_LSH ? launch_replay<T, true>(sp, D.chunk, st)
+                                      : launch_replay<T, false>(sp, D.chunk, st);
         if (rc) return rc;
     }
     return SSA_OK;

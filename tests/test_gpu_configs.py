@@ -9,10 +9,12 @@ transformer) the module runs on the GPU at the real shape and:
   window and the globals present, causal rows free of future keys apart from
   the global tokens, the output width rule);
 * a deterministic sample of query rows is checked against the oracle with the
-  same fp32 hash projections injected into both: LSH neighbour sets equal,
-  except where the two fp32 summation orders of a score straddle the k-th
-  score (a near tie, bounded by the fp32 error of the two dot products); rows
-  whose LSH sets agree must have identical merged neighbours and valid masks;
+  same fp32 hash projections injected into both: LSH neighbour sets equal
+  (rows with a tied kk-th score included: the GPU replays the reference's
+  top-k on them), except where the two fp32 summation orders of a score
+  straddle the k-th score (a near tie, bounded by the fp32 error of the two
+  dot products); rows whose LSH sets agree must have identical merged
+  neighbours and valid masks;
 * the gathered attention of the sampled rows matches the oracle's float64
   apply (1e-5 relative in fp32, 2e-2 in bf16).
 """
@@ -150,9 +152,7 @@ def _check_against_oracle(attn, q, k, v, nb, va, causal, cross, q_step, heads=No
                                 total_k=attn.K)
         for n in range(0, N, q_step):
             n_rows += 1
-            if ref["tie"][0, n]:
-                n_tie += 1
-                continue
+            n_tie += int(ref["tie"][0, n])
             a = set(lsh_gpu[h0, n].tolist())
             b = set(ref["idx"][0, n].tolist())
             if a == b:
@@ -164,8 +164,9 @@ def _check_against_oracle(attn, q, k, v, nb, va, causal, cross, q_step, heads=No
                 assert _near_tie_ok(qf[h0, n].astype(np.float64), kf[g].astype(np.float64),
                                     a, b, kth), f"unexplained LSH difference head {h0} row {n}"
                 n_near += 1
-    assert n_exact >= 0.95 * (n_rows - n_tie), (n_rows, n_exact, n_tie, n_near)
-    print(f"  sampled rows {n_rows}: exact {n_exact}, near-tie {n_near}, tie {n_tie}", flush=True)
+    assert n_exact >= 0.95 * n_rows, (n_rows, n_exact, n_tie, n_near)
+    print(f"  sampled rows {n_rows} (tied kk-th score: {n_tie}): exact {n_exact}, "
+          f"near-tie {n_near}", flush=True)
 
     # apply on the sampled rows of the module's own graph
     with torch.no_grad():

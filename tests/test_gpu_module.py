@@ -101,7 +101,7 @@ def test_empty_bucket_fallback_uses_global_tokens():
 def test_empty_bucket_list_competes_on_score_reference_vector():
     """Reference vector: the glob ++ 0 list of an empty bucket outscores the
     populated round (query 0 -> [5, 0]).  Query 1 has a k-th place tie among
-    keys 1, 2, 3 (equal scores): any of them is a correct top-2 member."""
+    keys 1, 2, 3 (equal scores) that the reference's top-k resolves to key 2."""
     import os
     import numpy as np
     from ssa_amd import LSHGraphBuilder
@@ -112,10 +112,7 @@ def test_empty_bucket_list_competes_on_score_reference_vector():
     q = torch.from_numpy(z["q"]).view(1, 1, 2, 4).to(DEV)
     k = torch.from_numpy(z["k"]).view(1, 1, 8, 4).to(DEV)
     nb = lsh(q, k, top_k=2, causal=False, glob_fallback=torch.from_numpy(z["glob"]).to(DEV))
-    got = nb.cpu().view(2, 2).tolist()
-    ref = z["out"].reshape(2, 2).tolist()
-    assert got[0] == ref[0]
-    assert got[1][0] == ref[1][0] and got[1][1] in (1, 2, 3)
+    assert nb.cpu().view(2, 2).tolist() == z["out"].reshape(2, 2).tolist()
 
 
 def test_cross_attention_more_queries_than_keys():

@@ -6,10 +6,11 @@ within 1e-5 relative (fp32) and 2e-2 (bf16/fp16), relative to max |ref|.
 Two input tiers (sparse_attention.py cannot fix fp32 summation order):
 * exact-arithmetic inputs (small integers): every fp32 projection and score is
   exact in any order, so the whole graph must match the oracle bit for bit,
-  except queries whose kk-th LSH score is exactly tied (the oracle flags them;
-  the selection among equal scores is algorithm-defined);
+  including the many rows whose kk-th LSH score is tied (small integers tie
+  often): those are resolved by the GPU's replay of the reference's
+  nth_element / sort, and the LSH lists must come out in the same order;
 * the reference's own vectors with the reference's fp32 projections injected:
-  neighbor sets must match the reference's.
+  neighbor lists must match the reference's.
 """
 import os
 
@@ -128,11 +129,8 @@ def test_full_graph_exact_tier_matches_oracle(case, seed):
     g_nb = got.cpu().numpy().reshape(B * H, N, -1)
     g_va = got_v.cpu().numpy().reshape(B * H, N, -1)
     assert g_nb.shape == rnb.shape
-    ok = ~ref["tie"]
-    np.testing.assert_array_equal(g_nb[ok], rnb[ok])
-    np.testing.assert_array_equal(g_va[ok], rva[ok])
-    # tie rows: the part of the set strictly above the tied score must agree
-    assert ok.mean() > 0.5
+    np.testing.assert_array_equal(g_nb, rnb)
+    np.testing.assert_array_equal(g_va, rva)
 
 
 @pytest.mark.parametrize("case", GRAPH_CASES[:5], ids=lambda c: c[0])
@@ -142,13 +140,9 @@ def test_lsh_builder_exact_tier_matches_oracle(case):
     g = got.cpu().numpy().reshape(B * H, N, -1)
     r = ref["idx"]
     assert g.shape == r.shape
-    ok = ~ref["tie"]
-    for a, b in zip(g[ok], r[ok]):
-        assert sorted(a.tolist()) == sorted(b.tolist())
-    # order: descending score; identical wherever the oracle's scores are distinct
-    vals = ref["val"][ok]
-    distinct = np.array([len(set(v.tolist())) == len(v) for v in vals])
-    np.testing.assert_array_equal(g[ok][distinct], r[ok][distinct])
+    # same lists in the same order, tied rows included
+    print(f"  {case[0]}: {ref['n_ties']} rows with a tied kk-th score", flush=True)
+    np.testing.assert_array_equal(g, r)
 
 
 def test_graph_bf16_inputs_exact_tier():
@@ -158,8 +152,7 @@ def test_graph_bf16_inputs_exact_tier():
         case, 5, dtype=torch.bfloat16)
     win = attn.win_builder(N, M, "cpu").numpy()
     rnb, rva = oracle.merge(win, glob.numpy(), ref["idx"], has_self=True, total_k=K)
-    ok = ~ref["tie"]
-    np.testing.assert_array_equal(got.cpu().numpy().reshape(B * H, N, -1)[ok], rnb[ok])
+    np.testing.assert_array_equal(got.cpu().numpy().reshape(B * H, N, -1), rnb)
 
 
 # ------------------------------------------------------------------ graph, reference vectors
@@ -185,25 +178,15 @@ def test_graph_on_reference_vectors_with_injected_projections(path):
         nb, va = attn.build_graph(q, k_exp, N, M, B, DEV, m["causal"], m["cross"],
                                   _proj=(qp, kp))
     torch.cuda.synchronize()
-    # sets: the reference breaks score ties by its introselect replay; rows the
-    # oracle marks as tied are compared above the tied score only
-    r = oracle.lsh_forward(z["q"].reshape(B * H, N, d), z["k"].reshape(B * H, M, d),
-                           z["sd_lsh_builder.rand_proj"], kv_rep=1, P=P,
-                           T=m["config"]["lsh_num_probes"], C=m["C"], top_k=m["lsh_k"],
-                           causal=m["causal"], glob=z["glob"],
-                           q_proj=z["qproj"].reshape(B * H, R, N, P),
-                           k_proj=z["kproj"].reshape(B * H, R, M, P))
-    ok = ~r["tie"]
+    # the reference's lists, in its order (ties resolved by the replay)
     g_l = lsh.cpu().numpy().reshape(B * H, N, -1)
     z_l = z["lsh"].reshape(B * H, N, -1)
-    for a, b in zip(g_l[ok], z_l[ok]):
-        assert sorted(a.tolist()) == sorted(b.tolist())
+    np.testing.assert_array_equal(g_l, z_l)
     g_nb = nb.cpu().numpy().reshape(B * H, N, -1)
     z_nb = z["neighbors"].reshape(B * H, N, -1)
-    np.testing.assert_array_equal(g_nb[ok], z_nb[ok])
-    np.testing.assert_array_equal(va.cpu().numpy().reshape(B * H, N, -1)[ok],
-                                  z["valid"].reshape(B * H, N, -1)[ok])
-    assert ok.mean() > 0.5
+    np.testing.assert_array_equal(g_nb, z_nb)
+    np.testing.assert_array_equal(va.cpu().numpy().reshape(B * H, N, -1),
+                                  z["valid"].reshape(B * H, N, -1))
 
 
 # ------------------------------------------------------------------ apply
