@@ -366,7 +366,7 @@ struct RsP {
     const int32_t *tiles, *ntiles, *qlist, *perm, *bstart, *bsize;
     const void *q, *k;
     int64_t qsb, qsh, qsn, ksb, ksh, ksn;
-    float *S;
+    uint32_t *S;       // order-preserving score keys (score_key), slot = stream position
     int N, M, R, NS, NB, C, Hq, Hkv, rep, bh0;
     int64_t Call;
 };
@@ -429,11 +429,11 @@ __global__ void __launch_bounds__(256) rescore_kernel(RsP p) {
         for (int a = 0; a < 4; ++a) {
             const int i = ty * 4 + a;
             if (i >= qc) continue;
-            float *srow = p.S + ((int64_t)bhl * p.N + nidx[i]) * p.Call + slotbase + c0;
+            uint32_t *srow = p.S + ((int64_t)bhl * p.N + nidx[i]) * p.Call + slotbase + c0;
 #pragma unroll
             for (int bb = 0; bb < 4; ++bb) {
                 const int cc = tx + 16 * bb;
-                if (c0 + cc < nv) srow[cc] = acc[a][bb];
+                if (c0 + cc < nv) srow[cc] = score_key(acc[a][bb]);
             }
         }
     }
@@ -539,11 +539,11 @@ __global__ void __launch_bounds__(256) rescore_mfma_kernel(RsP p) {
             for (int rr = 0; rr < 4; ++rr) {
                 const int row = qt * 16 + 4 * lg + rr;
                 if (row >= qc) continue;
-                float *srow = p.S + ((int64_t)bhl * p.N + nidx[row]) * p.Call + slotbase;
+                uint32_t *srow = p.S + ((int64_t)bhl * p.N + nidx[row]) * p.Call + slotbase;
 #pragma unroll
                 for (int ct = 0; ct < 4; ++ct) {
                     const int cand = c0 + ct * 16 + li;
-                    if (cand < nv) srow[cand] = acc[qt][ct][rr];
+                    if (cand < nv) srow[cand] = score_key(acc[qt][ct][rr]);
                 }
             }
         }
@@ -644,7 +644,7 @@ __global__ void __launch_bounds__(256) aux_valu_kernel(AuxP p) {
 struct SelP {
     const uint16_t *qid;
     const int32_t *perm, *bstart, *bsize;
-    float *S;
+    const uint32_t *S;     // score keys (score_key), row-major (rows, Call)
     const void *q, *k;
     int64_t qsb, qsh, qsn, ksb, ksh, ksn;
     const int64_t *glob;
@@ -711,16 +711,17 @@ __device__ __forceinline__ int wave_count(int c) {
 constexpr int SEL_CAP = 512;   // keys kept in LDS for the exact threshold search
 
 // Per-wave LDS of the select kernel, in 32-bit words:
-//   tab   [4*nch]     per 64-slot chunk: perm offset of lane 0, flags, stream
-//                     slot of lane 0, perm offset of the overflow filler
+//   tab   [4*nch]     per 64-slot chunk: perm index of lane 0, flags, stream
+//                     slot of lane 0, key id of the overflow filler slots
 //   bm    [words]     seen bitmap, later the merge bitmap
 //   kmask [2*nch]     per 64-slot chunk, the ballot of kept slots
 //   ckey  [SEL_CAP]   sample of kept keys, then kept keys >= the lower bound
-//   cslot [SEL_CAP]   stream slot of each compacted key
-//   gsc   [64]        scores of glob[0..G-1] and key 0 (empty buckets)
+//   cval  [SEL_CAP]   key id of each compacted key (entries stay in stream order)
+//   gsc   [64]        score keys of glob[0..G-1] and key 0 (empty buckets)
+//   gid   [64]        the ids glob[0..G-1], 0
 //   LSH mode: ekey/eval/eslot [kk] the selected entries
 __host__ __device__ inline int sel_lds_words(int nch, int words, int kk, bool lsh) {
-    return (4 * nch + words + 2 * nch + 2 * SEL_CAP + 64 + (lsh ? 3 * kk : 0) + 1) & ~1;
+    return (4 * nch + words + 2 * nch + 2 * SEL_CAP + 128 + (lsh ? 3 * kk : 0) + 1) & ~1;
 }
 
 // Largest t (resolved down to bit lo_bit) such that at least kk of the wave's
@@ -858,9 +859,10 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     uint32_t *bm = (uint32_t *)(tab + nch);
     uint64_t *kmask = (uint64_t *)(bm + p.words);
     uint32_t *ckey = (uint32_t *)(kmask + nch);
-    uint32_t *cslot = ckey + SEL_CAP;
-    float *gsc = (float *)(cslot + SEL_CAP);
-    uint32_t *ekey = (uint32_t *)(gsc + 64);
+    uint32_t *cval = ckey + SEL_CAP;
+    uint32_t *gsc = cval + SEL_CAP;
+    int32_t *gid = (int32_t *)(gsc + 64);
+    uint32_t *ekey = (uint32_t *)(gid + 64);
     uint32_t *eval = ekey + p.kk;
     uint32_t *eslot = eval + p.kk;
 
@@ -876,7 +878,7 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     const float *arow = p.aux + rloc * p.NA;
     const uint32_t kself = p.causal ? score_key(arow[0]) : 0u;
     const uint16_t *qids = p.qid + row * p.R * p.NS;
-    const float *srow = p.S + ((int64_t)bhl * p.N + n) * p.Call;
+    const uint32_t *srow = p.S + ((int64_t)bhl * p.N + n) * p.Call;
     const int ng = min(p.G + 1, SSA_WAVE);
     for (int w = lane; w < p.words; w += SSA_WAVE) bm[w] = 0u;
     bool any_empty = false;
@@ -890,14 +892,23 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
         const int lanes = min(p.C - c0, SSA_WAVE);
         const int realn = sz == 0 ? lanes : max(0, min(min(sz, p.C) - c0, SSA_WAVE));
         int4 d4;
-        d4.x = st + c0;
+        d4.x = (int)(prow * p.M) + min(st + c0, p.M - 1);   // perm index of lane 0 (clamped)
         d4.y = lanes | (realn << 7) | (sz == 0 ? CH_EMPTY : 0) | (cj == 0 ? CH_FIRST : 0);
         d4.z = list * p.C + c0;
-        d4.w = (int)prow;
+        d4.w = p.perm[prow * p.M + p.M - 1];      // key of the overflow filler slots
         tab[ci] = d4;
         any_empty |= sz == 0;
     }
-    if (wave_ballot(any_empty) && lane < ng) gsc[lane] = arow[1 + lane];   // (:711-737)
+    // glob ++ 0 (:711-737): ids and score keys, lane j holding entry j (also
+    // in LDS for the rare re-walk paths)
+    int greg_id = 0;
+    uint32_t greg_sc = 0u;
+    if (wave_ballot(any_empty) && lane < ng) {
+        greg_sc = score_key(arow[1 + lane]);
+        greg_id = lane < p.G ? (int)p.glob[lane] : 0;
+        gsc[lane] = greg_sc;
+        gid[lane] = greg_id;
+    }
     wave_lds_sync();
 
     auto list_info = [&](int list) {
@@ -916,13 +927,13 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
             real = c < L.nv;
             const int raw = L.pr[real ? L.st + c : p.M - 1];
             v = (p.causal && raw > n) ? n : raw;
-            const float sc = srow[real ? (int64_t)list * p.C + c : 0];
-            kv = (p.causal && v == n) ? kself : score_key(sc);
+            const uint32_t sk = srow[real ? (int64_t)list * p.C + c : 0];
+            kv = (p.causal && v == n) ? kself : sk;
         } else {                                     // empty bucket: glob ++ 0
             real = true;
             const int j = c < ng - 1 ? c : ng - 1;
-            v = (c < p.G) ? (int)p.glob[j] : 0;
-            kv = score_key(gsc[j]);
+            v = gid[j];
+            kv = gsc[j];
         }
     };
 
@@ -931,90 +942,136 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     // capacity, lo is raised to (a 24-bit floor of) the kk-th largest key in the
     // buffer -- a subset of the stream -- and the buffer is filtered in place.
     const int kk = p.kk;
-    const int fill = SEL_CAP - SSA_WAVE;
+    const int fill = SEL_CAP / 2;      // checked once per group of 4 chunks (<= 256 keys)
     int nk = 0, cnt = 0;
     uint32_t lo = 0u;
     bool overflow = false;
-    constexpr int PIPE = 4;            // chunks whose loads are in flight together
-    for (int ci0 = 0; ci0 < nch; ci0 += PIPE) {
-        int4 d4[PIPE];
-        int raw[PIPE];
-        float sc[PIPE];
+    bool nseen = false;                // the query's own key has occurred
+    // Chunks are processed PIPE at a time; the loads of the next group are
+    // issued before the current group is deduplicated, so a wave always has
+    // one group of candidate ids and scores in flight.
+    // Loads are unconditional (inactive lanes read an in-range slot), so no
+    // register written by a pending load is rewritten before it lands.
+    constexpr int PIPE = 4;
+    int cy[PIPE], cw[PIPE], craw[PIPE];
+    uint32_t csk[PIPE];
 #pragma unroll
-        for (int u = 0; u < PIPE; ++u) {
-            d4[u] = ci0 + u < nch ? tab[ci0 + u] : make_int4(0, 0, 0, 0);
-            const bool real = (lane < CH_REAL(d4[u].y)) & ((d4[u].y & CH_EMPTY) == 0);
-            raw[u] = p.perm[(int64_t)d4[u].w * p.M + (real ? d4[u].x + lane : p.M - 1)];
-            sc[u] = srow[real ? d4[u].z + lane : 0];
+    for (int u = 0; u < PIPE; ++u) {
+        const int4 d = u < nch ? tab[u] : make_int4(0, 0, 0, 0);
+        cy[u] = __builtin_amdgcn_readfirstlane(d.y);
+        cw[u] = __builtin_amdgcn_readfirstlane(d.w);
+        const int x = __builtin_amdgcn_readfirstlane(d.x);
+        const int z = __builtin_amdgcn_readfirstlane(d.z);
+        const bool real = (lane < CH_REAL(cy[u])) & ((cy[u] & CH_EMPTY) == 0);
+        craw[u] = p.perm[real ? x + lane : x];
+        csk[u] = srow[real ? z + lane : z];
+    }
+    for (int ci0 = 0; ci0 < nch; ci0 += PIPE) {
+        int ny[PIPE], nw[PIPE], nraw[PIPE];
+        uint32_t nsk[PIPE];
+        if (ci0 + PIPE < nch) {
+#pragma unroll
+            for (int u = 0; u < PIPE; ++u) {
+                const int ci = ci0 + PIPE + u;
+                const int4 d = ci < nch ? tab[ci] : make_int4(0, 0, 0, 0);
+                ny[u] = __builtin_amdgcn_readfirstlane(d.y);
+                nw[u] = __builtin_amdgcn_readfirstlane(d.w);
+                const int x = __builtin_amdgcn_readfirstlane(d.x);
+                const int z = __builtin_amdgcn_readfirstlane(d.z);
+                const bool real = (lane < CH_REAL(ny[u])) & ((ny[u] & CH_EMPTY) == 0);
+                nraw[u] = p.perm[real ? x + lane : x];
+                nsk[u] = srow[real ? z + lane : z];
+            }
         }
 #pragma unroll
         for (int u = 0; u < PIPE; ++u) {
-            const int y = d4[u].y;
+            const int y = cy[u];
             const bool in_list = lane < CH_LANES(y);
             const bool empty = (y & CH_EMPTY) != 0;
             const bool real = in_list & (lane < CH_REAL(y));
-            int v;
-            uint32_t kv;
-            if (!empty) {
-                v = (p.causal && raw[u] > n) ? n : raw[u];
-                kv = (p.causal && v == n) ? kself : score_key(sc[u]);
-            } else {                                   // empty bucket: glob ++ 0
+            const int raw = lane < CH_REAL(y) ? craw[u] : cw[u];   // fillers: perm[M-1]
+            int v = (p.causal && raw > n) ? n : raw;
+            uint32_t kv = (p.causal && v == n) ? kself : csk[u];
+            if (empty) {                               // empty bucket: glob ++ 0
                 const int c = ((y & CH_FIRST) ? 0 : SSA_WAVE) + lane;
                 const int j = c < ng - 1 ? c : ng - 1;
-                v = (c < p.G) ? (int)p.glob[j] : 0;
-                kv = score_key(gsc[j]);
+                v = __shfl(greg_id, j, SSA_WAVE);
+                kv = (uint32_t)__shfl((int)greg_sc, j, SSA_WAVE);
+            }
+            // The query's own key (every future candidate when causal) is
+            // tracked by a wave-uniform flag instead of the bitmap: its first
+            // occurrence in stream order decides, valid or not.
+            const bool isn = p.causal && in_list && v == n;
+            bool keepn = false;
+            if (p.causal) {
+                const uint64_t nm = wave_ballot(isn);
+                if (nm != 0ull && !nseen) {
+                    keepn = real && lane == (int)__ffsll((long long)nm) - 1;
+                    nseen = true;
+                }
             }
             const uint32_t bit = 1u << (v & 31);
-            const uint32_t old = atomicOr(&bm[v >> 5], real ? bit : 0u);
-            if (wave_ballot(in_list & !real)) atomicOr(&bm[v >> 5], (in_list & !real) ? bit : 0u);
-            const bool keep = real & ((old & bit) == 0u);
+            const bool doat = real && !isn;
+            uint32_t old = 0u;
+            if (doat) old = atomicOr(&bm[v >> 5], bit);
+            // fillers (all perm[M-1]) mark their key once, after the real slots
+            const uint64_t fm = wave_ballot(in_list && !real && !isn);
+            if (fm != 0ull && lane == (int)__ffsll((long long)fm) - 1) atomicOr(&bm[v >> 5], bit);
+            const bool keep = (doat && (old & bit) == 0u) || keepn;
             const uint64_t km = wave_ballot(keep);
             if (lane == 0 && ci0 + u < nch) kmask[ci0 + u] = km;
             nk += __popcll(km);
             const bool app = keep & (kv >= lo);
             const uint64_t am = wave_ballot(app);
             const int pos = cnt + lanes_below(am);
-            if (app && pos < SEL_CAP) { ckey[pos] = kv; cslot[pos] = (uint32_t)(d4[u].z + lane); }
+            if (app && pos < SEL_CAP) { ckey[pos] = kv; cval[pos] = (uint32_t)v; }
             cnt += __popcll(am);
-            if (cnt >= fill && cnt >= kk && !overflow) {
-                wave_lds_sync();
-                const int m0 = cnt < SEL_CAP ? cnt : SEL_CAP;
-                uint32_t sv[SEL_CAP / SSA_WAVE];
+        }
+        if (cnt >= fill && cnt >= kk && !overflow) {
+            wave_lds_sync();
+            const int m0 = cnt < SEL_CAP ? cnt : SEL_CAP;
+            uint32_t sv[SEL_CAP / SSA_WAVE];
 #pragma unroll
-                for (int i = 0; i < SEL_CAP / SSA_WAVE; ++i) {
-                    const int e = lane + SSA_WAVE * i;
-                    sv[i] = e < m0 ? ckey[e] : 0u;
-                }
-                uint32_t mx = 0u, mn = 0xffffffffu;
-#pragma unroll
-                for (int i = 0; i < SEL_CAP / SSA_WAVE; ++i) {
-                    mx = sv[i] > mx ? sv[i] : mx;
-                    mn = (sv[i] != 0u && sv[i] < mn) ? sv[i] : mn;
-                }
-                mx = wave_max_u(mx);
-                mn = wave_min_u(mn);
-                const uint32_t base0 = lo > mn ? lo : mn;     // every buffered key >= lo
-                const uint32_t nlo = kth_search(sv, kk, base0, mx, 16);
-                lo = nlo > lo ? nlo : lo;
-                uint32_t sl[SEL_CAP / SSA_WAVE];
-#pragma unroll
-                for (int i = 0; i < SEL_CAP / SSA_WAVE; ++i) {
-                    const int e = lane + SSA_WAVE * i;
-                    sl[i] = e < m0 ? cslot[e] : 0u;
-                }
-                wave_lds_sync();
-                int nc = 0;
-#pragma unroll
-                for (int i = 0; i < SEL_CAP / SSA_WAVE; ++i) {
-                    const bool t = sv[i] >= lo && sv[i] != 0u;
-                    const uint64_t m = wave_ballot(t);
-                    if (t) { ckey[nc + lanes_below(m)] = sv[i]; cslot[nc + lanes_below(m)] = sl[i]; }
-                    nc += __popcll(m);
-                }
-                overflow = cnt > SEL_CAP;
-                cnt = nc;
-                wave_lds_sync();
+            for (int i = 0; i < SEL_CAP / SSA_WAVE; ++i) {
+                const int e = lane + SSA_WAVE * i;
+                sv[i] = e < m0 ? ckey[e] : 0u;
             }
+            uint32_t mx = 0u, mn = 0xffffffffu;
+#pragma unroll
+            for (int i = 0; i < SEL_CAP / SSA_WAVE; ++i) {
+                mx = sv[i] > mx ? sv[i] : mx;
+                mn = (sv[i] != 0u && sv[i] < mn) ? sv[i] : mn;
+            }
+            mx = wave_max_u(mx);
+            mn = wave_min_u(mn);
+            const uint32_t base0 = lo > mn ? lo : mn;     // every buffered key >= lo
+            const uint32_t nlo = kth_search(sv, kk, base0, mx, 16);
+            lo = nlo > lo ? nlo : lo;
+            uint32_t sl[SEL_CAP / SSA_WAVE];
+#pragma unroll
+            for (int i = 0; i < SEL_CAP / SSA_WAVE; ++i) {
+                const int e = lane + SSA_WAVE * i;
+                sl[i] = e < m0 ? cval[e] : 0u;
+            }
+            wave_lds_sync();
+            int nc = 0;
+#pragma unroll
+            for (int i = 0; i < SEL_CAP / SSA_WAVE; ++i) {
+                const bool t = sv[i] >= lo && sv[i] != 0u;
+                const uint64_t m = wave_ballot(t);
+                if (t) { ckey[nc + lanes_below(m)] = sv[i]; cval[nc + lanes_below(m)] = sl[i]; }
+                nc += __popcll(m);
+            }
+            overflow = cnt > SEL_CAP;
+            cnt = nc;
+            wave_lds_sync();
+        }
+#pragma unroll
+        for (int u = 0; u < PIPE; ++u) {
+            cy[u] = ny[u];
+            cw[u] = nw[u];
+            craw[u] = nraw[u];
+            csk[u] = nsk[u];
         }
     }
     overflow = overflow || cnt > SEL_CAP;
@@ -1124,16 +1181,8 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
             const bool in = e < cnt;
             const uint32_t kv = in ? ckey[e] : 0u;
             const bool sel = decide(in, kv);
-            int v = 0;
-            const int slot = in ? (int)cslot[e] : 0;
-            if (sel) {
-                const int list = slot / p.C, c = slot - list * p.C;
-                const SelList L = list_info(list);
-                uint32_t k2;
-                bool r2;
-                slot_kv(L, list, c, v, k2, r2);
-            }
-            take(sel, kv, v, slot);
+            const int v = in ? (int)cval[e] : 0;
+            take(sel, kv, v, e);           // compacted index: increasing in stream order
         }
     } else {
         walk_kept([&](bool keep, uint32_t kv, int v, int slot) {
@@ -1426,7 +1475,7 @@ topk_replay_kernel(SelP p, int chunk, int W) {
     uint32_t *lbits = base + 3 * W;
     int32_t *stk = (int32_t *)(lbits + (W + 31) / 32 + 1);
     uint32_t *bm = (uint32_t *)(stk + 3 * RP_STACK);
-    float *gsc = (float *)(bm + p.words);
+    uint32_t *gsc = bm + p.words;
 
     const int total = (int)gridDim.x * RP_WAVES;
     const int cnt = *p.tie_count;
@@ -1440,13 +1489,13 @@ topk_replay_kernel(SelP p, int chunk, int W) {
         const int bk = b * p.Hkv + g;
         const int64_t row = (int64_t)bh * p.N + n;
         const float *arow = p.aux + rloc * p.NA;
-        const float kself = p.causal ? arow[0] : 0.f;
+        const uint32_t kself = p.causal ? score_key(arow[0]) : 0u;
         const int ng = min(p.G + 1, SSA_WAVE);
-        if (lane < ng) gsc[lane] = arow[1 + lane];
+        if (lane < ng) gsc[lane] = score_key(arow[1 + lane]);
         for (int w = lane; w < p.words; w += SSA_WAVE) bm[w] = 0u;
         for (int t = lane; t < kk; t += SSA_WAVE) { A.key[t] = RP_NEGINF; A.cand[t] = 0; }
         const uint16_t *qids = p.qid + row * p.R * p.NS;
-        const float *srow = p.S + ((int64_t)bhl * p.N + n) * p.Call;
+        const uint32_t *srow = p.S + ((int64_t)bhl * p.N + n) * p.Call;
         rp_sync();
 
         for (int64_t s0 = 0; s0 < p.Call; s0 += chunk) {
@@ -1466,7 +1515,7 @@ topk_replay_kernel(SelP p, int chunk, int W) {
                 const bool in = lane < nl;
                 int v = 0;
                 bool keep = false;
-                float sc = 0.f;
+                uint32_t sk = 0u;
                 if (sz > 0) {
                     const bool real = in && c < min(sz, p.C);
                     const int raw = in ? p.perm[prow * p.M + (real ? st + c : p.M - 1)] : 0;
@@ -1487,7 +1536,7 @@ topk_replay_kernel(SelP p, int chunk, int W) {
                                 keep = !seen && lane == (int)(__ffsll((long long)nm) - 1);
                         }
                     }
-                    if (keep) sc = (p.causal && v == n) ? kself : srow[j0 + lane];
+                    if (keep) sk = (p.causal && v == n) ? kself : srow[j0 + lane];
                 } else {
                     // empty bucket: glob ++ 0, all valid; duplicates resolved in slot order
                     const int jg = c < ng - 1 ? c : ng - 1;
@@ -1506,11 +1555,11 @@ topk_replay_kernel(SelP p, int chunk, int W) {
                         pending = pending && !same;
                         pm = wave_ballot(pending);
                     }
-                    if (keep) sc = gsc[jg];
+                    if (keep) sk = gsc[jg];
                 }
                 if (in) {
                     const int at = kk + (int)(j0 - s0) + lane;
-                    A.key[at] = keep ? ~score_key(sc) : RP_NEGINF;
+                    A.key[at] = keep ? ~sk : RP_NEGINF;
                     A.cand[at] = v;
                 }
                 rp_sync();
@@ -1610,6 +1659,8 @@ int make_dims(const ssa_graph_args *a, Dims &D) {
         ssa_set_error("build_graph: key length %d unsupported (1..32768)", a->M);
         return SSA_E_UNSUP;
     }
+    SSA_CHECK_ARG((int64_t)a->B * a->Hkv * a->R * a->M < ((int64_t)1 << 31),
+                  "build_graph: B*Hkv*R*M must stay below 2^31 (bucket permutation index)");
     D.B = a->B; D.Hq = a->Hq; D.Hkv = a->Hkv; D.rep = a->Hq / a->Hkv;
     D.N = a->N; D.M = a->M; D.d = a->d; D.R = a->R; D.maxP = a->max_p; D.P = a->P;
     D.Tp = a->T < a->P ? a->T : a->P;
@@ -1891,7 +1942,7 @@ int build_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *w
         rp.q = a->q.ptr; rp.k = a->k.ptr;
         rp.qsb = a->q.sb; rp.qsh = a->q.sh; rp.qsn = a->q.sn;
         rp.ksb = a->k.sb; rp.ksh = a->k.sh; rp.ksn = a->k.sn;
-        rp.S = (float *)(ws + L.S);
+        rp.S = (uint32_t *)(ws + L.S);
         rp.N = D.N; rp.M = D.M; rp.R = D.R; rp.NS = D.NS; rp.NB = D.NB; rp.C = D.C;
         rp.Hq = D.Hq; rp.Hkv = D.Hkv; rp.rep = D.rep; rp.bh0 = (int)bh0; rp.Call = D.Call;
         const int64_t grid = (int64_t)ninst * (ceil_div(D.N, TQ) + D.NB);
