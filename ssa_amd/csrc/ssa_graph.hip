@@ -737,10 +737,9 @@ __device__ __forceinline__ uint32_t kth_search(const uint32_t (&k)[NK], int kk, 
 #pragma unroll 1
     for (int bit = hb; bit >= lo_bit; --bit) {
         const uint32_t cand = thr | (1u << bit);
-        int c = 0;
+        int tot = 0;                   // one compare-to-mask + scalar popcount per slot
 #pragma unroll
-        for (int i = 0; i < NK; ++i) c += k[i] >= cand;
-        const int tot = wave_count<4>(c);
+        for (int i = 0; i < NK; ++i) tot += __popcll(wave_ballot(k[i] >= cand));
         if (tot >= kk) {
             thr = cand;
             if (tot == kk) break;
@@ -1119,9 +1118,10 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
             thr = kth_search(cv, kk, lo > mn ? lo : mn, mx, 0);
             int ge = 0, gt = 0;
 #pragma unroll
-            for (int i = 0; i < SEL_CAP / SSA_WAVE; ++i) { ge += cv[i] >= thr; gt += cv[i] > thr; }
-            ge = wave_count<4>(ge);
-            gt = wave_count<4>(gt);
+            for (int i = 0; i < SEL_CAP / SSA_WAVE; ++i) {
+                ge += __popcll(wave_ballot(cv[i] >= thr));
+                gt += __popcll(wave_ballot(cv[i] > thr));
+            }
             need = kk - gt;
             btie = ge - gt > need;
         } else {
