@@ -368,6 +368,7 @@ struct RsP {
     int64_t qsb, qsh, qsn, ksb, ksh, ksn;
     uint32_t *S;       // order-preserving score keys (score_key), slot = stream position
     int N, M, R, NS, NB, C, Hq, Hkv, rep, bh0;
+    int vec4;          // rows and list starts of S are 16-byte aligned (C % 4 == 0)
     int64_t Call;
 };
 
@@ -461,11 +462,25 @@ template <> struct Mfma16<f16_t> {
     }
 };
 
+// MFMA rescore of one tile (up to 64 queries of one bucket x the bucket's nv
+// candidates).  The block stages each 64-candidate slice of K rows in LDS once
+// (double-buffered, rows padded by 16 bytes so the fragment reads are free of
+// bank conflicts); wave w scores queries 16w..16w+15 against the slice as
+// K . Q^T, so each lane holds 4 consecutive candidates of one query and writes
+// their score keys with one 16-byte store.
+constexpr int RS_ROWB_PAD = 16;
+
+template <int D>
+__host__ __device__ constexpr int rs_row_bytes() { return D * 2 + RS_ROWB_PAD; }
+
 template <typename T, int D>
 __global__ void __launch_bounds__(256) rescore_mfma_kernel(RsP p) {
     using V = typename Mfma16<T>::vec;
-    constexpr int KS = (D + 31) / 32;   // k steps of 32
+    constexpr int KS = (D + 31) / 32;          // k steps of 32
+    constexpr int RB = rs_row_bytes<D>();      // LDS bytes per staged row
+    constexpr int SEGS = D / 8;                // 16-byte segments per row
     __shared__ int nidx[TQ];
+    extern __shared__ __align__(16) unsigned char rs_lds[];   // [2][64][RB]
     if ((int)blockIdx.x >= *p.ntiles) return;
     const int32_t *e = p.tiles + (int64_t)blockIdx.x * 4;
     const int inst = e[0], u = e[1], qb = e[2], qc = e[3];
@@ -481,72 +496,98 @@ __global__ void __launch_bounds__(256) rescore_mfma_kernel(RsP p) {
     const int li = lane % 16, lg = lane / 16;
     const T *qbase = (const T *)p.q + b * p.qsb + h * p.qsh;
     const T *kbase = (const T *)p.k + b * p.ksb + g * p.ksh;
+    const int32_t *pr = p.perm + prow * p.M + st;
     if (tid < TQ) nidx[tid] = tid < qc ? p.qlist[(int64_t)inst * p.N + qb + tid] : 0;
     __syncthreads();
 
-    V qa[4][KS];
-#pragma unroll
-    for (int qt = 0; qt < 4; ++qt) {
-        const int row = qt * 16 + li;
-        const bool ok = row < qc;
-        const T *src = qbase + (int64_t)nidx[ok ? row : 0] * p.qsn;
+    // this wave's 16 queries as the B operand (column li = query 16*wid + li)
+    const int qrow = 16 * wid + li;
+    const bool qok = qrow < qc;
+    V qf[KS];
+    {
+        const T *src = qbase + (int64_t)nidx[qok ? qrow : 0] * p.qsn;
 #pragma unroll
         for (int s = 0; s < KS; ++s) {
             const int e0 = 32 * s + 8 * lg;
-            if (ok && e0 < D) {
-                const uint4 w = *reinterpret_cast<const uint4 *>(src + e0);
-                qa[qt][s] = __builtin_bit_cast(V, w);
-            } else {
-                qa[qt][s] = __builtin_bit_cast(V, make_uint4(0, 0, 0, 0));
-            }
+            qf[s] = (qok && e0 < D) ? __builtin_bit_cast(V, *reinterpret_cast<const uint4 *>(src + e0))
+                                    : __builtin_bit_cast(V, make_uint4(0, 0, 0, 0));
         }
     }
-    const int64_t slotbase = (int64_t)(r * p.NS + t) * p.C;
-    const int32_t *pr = p.perm + prow * p.M + st;
-    for (int c0 = wid * 64; c0 < nv; c0 += 4 * 64) {
-        V kb[4][KS];
+    const bool active = 16 * wid < qc;
+
+    // cooperative copy of candidate rows [c0, c0 + 64) into registers, then LDS
+    constexpr int PER = (64 * SEGS + 255) / 256;
+    uint4 stage[PER];
+    auto fetch = [&](int c0) {
 #pragma unroll
-        for (int ct = 0; ct < 4; ++ct) {
-            const int cand = c0 + ct * 16 + li;
-            const bool ok = cand < nv;
-            const T *src = kbase + (int64_t)(ok ? pr[cand] : 0) * p.ksn;
+        for (int i = 0; i < PER; ++i) {
+            const int x = tid + 256 * i;
+            const int row = x / SEGS, seg = x % SEGS;
+            const bool ok = x < 64 * SEGS && c0 + row < nv;
+            const T *src = kbase + (int64_t)(ok ? pr[c0 + row] : 0) * p.ksn + seg * 8;
+            stage[i] = ok ? *reinterpret_cast<const uint4 *>(src) : make_uint4(0, 0, 0, 0);
+        }
+    };
+    auto commit = [&](int buf) {
+        unsigned char *dst = rs_lds + buf * (64 * RB);
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int x = tid + 256 * i;
+            if (x < 64 * SEGS) {
+                const int row = x / SEGS, seg = x % SEGS;
+                *reinterpret_cast<uint4 *>(dst + row * RB + seg * 16) = stage[i];
+            }
+        }
+    };
+    const int64_t slotbase = (int64_t)(r * p.NS + t) * p.C;
+    uint32_t *srow = p.S + ((int64_t)bhl * p.N + nidx[qok ? qrow : 0]) * p.Call + slotbase;
+    const int nsl = (nv + 63) / 64;
+    fetch(0);
+    commit(0);
+    __syncthreads();
+    for (int j = 0; j < nsl; ++j) {
+        const int c0 = 64 * j;
+        if (j + 1 < nsl) fetch(c0 + 64);
+        if (active) {
+            const unsigned char *kl = rs_lds + (j & 1) * (64 * RB);
+            f32x4_t acc[4];
+#pragma unroll
+            for (int ct = 0; ct < 4; ++ct) acc[ct] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int s = 0; s < KS; ++s) {
                 const int e0 = 32 * s + 8 * lg;
-                if (ok && e0 < D) {
-                    const uint4 w = *reinterpret_cast<const uint4 *>(src + e0);
-                    kb[ct][s] = __builtin_bit_cast(V, w);
-                } else {
-                    kb[ct][s] = __builtin_bit_cast(V, make_uint4(0, 0, 0, 0));
-                }
-            }
-        }
-        f32x4_t acc[4][4];
-#pragma unroll
-        for (int qt = 0; qt < 4; ++qt)
-#pragma unroll
-            for (int ct = 0; ct < 4; ++ct) acc[qt][ct] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s = 0; s < KS; ++s)
-#pragma unroll
-            for (int qt = 0; qt < 4; ++qt)
-#pragma unroll
-                for (int ct = 0; ct < 4; ++ct)
-                    acc[qt][ct] = Mfma16<T>::mma(qa[qt][s], kb[ct][s], acc[qt][ct]);
-#pragma unroll
-        for (int qt = 0; qt < 4; ++qt) {
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr) {
-                const int row = qt * 16 + 4 * lg + rr;
-                if (row >= qc) continue;
-                uint32_t *srow = p.S + ((int64_t)bhl * p.N + nidx[row]) * p.Call + slotbase;
 #pragma unroll
                 for (int ct = 0; ct < 4; ++ct) {
-                    const int cand = c0 + ct * 16 + li;
-                    if (cand < nv) srow[cand] = score_key(acc[qt][ct][rr]);
+                    const V kf = e0 < D ? __builtin_bit_cast(
+                                              V, *reinterpret_cast<const uint4 *>(
+                                                     kl + (ct * 16 + li) * RB + e0 * 2))
+                                        : __builtin_bit_cast(V, make_uint4(0, 0, 0, 0));
+                    acc[ct] = Mfma16<T>::mma(kf, qf[s], acc[ct]);
+                }
+            }
+            // lane (li, lg) holds candidates c0 + 16 ct + 4 lg + rr of query li
+            if (qok) {
+#pragma unroll
+                for (int ct = 0; ct < 4; ++ct) {
+                    const int cc = c0 + ct * 16 + 4 * lg;
+                    uint4 kv;
+                    kv.x = score_key(acc[ct][0]);
+                    kv.y = score_key(acc[ct][1]);
+                    kv.z = score_key(acc[ct][2]);
+                    kv.w = score_key(acc[ct][3]);
+                    if (cc + 3 < nv && p.vec4) {
+                        *reinterpret_cast<uint4 *>(srow + cc) = kv;
+                    } else {
+                        if (cc < nv) srow[cc] = kv.x;
+                        if (cc + 1 < nv) srow[cc + 1] = kv.y;
+                        if (cc + 2 < nv) srow[cc + 2] = kv.z;
+                        if (cc + 3 < nv) srow[cc + 3] = kv.w;
+                    }
                 }
             }
         }
+        if (j + 1 < nsl) commit((j + 1) & 1);
+        __syncthreads();
     }
 }
 
@@ -591,21 +632,21 @@ __global__ void __launch_bounds__(256) aux_mfma_kernel(AuxP p) {
     V qa[KS];
 #pragma unroll
     for (int s = 0; s < KS; ++s) qa[s] = frag(qbase + (int64_t)(okq ? nq : 0) * p.qsn, okq, s);
-    float *orow = p.out + ((int64_t)bhl * p.N + n0) * p.NA;
-    if (p.causal) {            // column li holds key n0 + li: the diagonal is q_n . k_n
+    // operand roles as in the rescore (keys as A, queries as B): lane (li, lg)
+    // receives C[4 lg + rr][li] = score of key row 4 lg + rr for query n0 + li
+    float *ob = p.out + ((int64_t)bhl * p.N + n0) * p.NA;
+    if (p.causal) {            // key row li is key n0 + li: the diagonal is q_n . k_n
         V kb[KS];
 #pragma unroll
         for (int s = 0; s < KS; ++s) kb[s] = frag(kbase + (int64_t)(okq ? nq : 0) * p.ksn, okq, s);
         f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s = 0; s < KS; ++s) acc = Mfma16<T>::mma(qa[s], kb[s], acc);
+        for (int s = 0; s < KS; ++s) acc = Mfma16<T>::mma(kb[s], qa[s], acc);
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-            const int row = 4 * lg + rr;
-            if (row == li && n0 + row < p.N) orow[(int64_t)row * p.NA] = acc[rr];
-        }
+        for (int rr = 0; rr < 4; ++rr)
+            if (4 * lg + rr == li && okq) ob[(int64_t)li * p.NA] = acc[rr];
     }
-    for (int j0 = 0; j0 <= p.G; j0 += 16) {       // columns: glob[0..G-1], then key 0
+    for (int j0 = 0; j0 <= p.G; j0 += 16) {       // key rows: glob[0..G-1], then key 0
         const int j = j0 + li;
         const int key = j < p.G ? (int)p.glob[j] : 0;
         V kb[KS];
@@ -613,11 +654,11 @@ __global__ void __launch_bounds__(256) aux_mfma_kernel(AuxP p) {
         for (int s = 0; s < KS; ++s) kb[s] = frag(kbase + (int64_t)key * p.ksn, true, s);
         f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s = 0; s < KS; ++s) acc = Mfma16<T>::mma(qa[s], kb[s], acc);
+        for (int s = 0; s < KS; ++s) acc = Mfma16<T>::mma(kb[s], qa[s], acc);
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
-            const int row = 4 * lg + rr;
-            if (n0 + row < p.N && j <= p.G) orow[(int64_t)row * p.NA + 1 + j] = acc[rr];
+            const int jj = j0 + 4 * lg + rr;
+            if (okq && jj <= p.G) ob[(int64_t)li * p.NA + 1 + jj] = acc[rr];
         }
     }
 }
@@ -1781,7 +1822,10 @@ int launch_rescore(const RsP &rp, int64_t grid, hipStream_t st) {
 
 template <typename T, int Dh>
 int launch_rescore_mfma(const RsP &rp, int64_t grid, hipStream_t st) {
-    hipLaunchKernelGGL((rescore_mfma_kernel<T, Dh>), dim3((unsigned)grid), dim3(256), 0, st, rp);
+    const size_t lds = (size_t)2 * 64 * rs_row_bytes<Dh>();
+    SSA_CHECK_HIP(hipFuncSetAttribute((const void *)rescore_mfma_kernel<T, Dh>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    hipLaunchKernelGGL((rescore_mfma_kernel<T, Dh>), dim3((unsigned)grid), dim3(256), lds, st, rp);
     SSA_CHECK_LAUNCH();
     return SSA_OK;
 }
@@ -1945,6 +1989,7 @@ int build_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *w
         rp.S = (uint32_t *)(ws + L.S);
         rp.N = D.N; rp.M = D.M; rp.R = D.R; rp.NS = D.NS; rp.NB = D.NB; rp.C = D.C;
         rp.Hq = D.Hq; rp.Hkv = D.Hkv; rp.rep = D.rep; rp.bh0 = (int)bh0; rp.Call = D.Call;
+        rp.vec4 = (D.C % 4 == 0) ? 1 : 0;
         const int64_t grid = (int64_t)ninst * (ceil_div(D.N, TQ) + D.NB);
         rc = rescore_dispatch<T>(D.d, rp, grid, st);
         if (rc) return rc;
