@@ -261,6 +261,8 @@ struct QbP {
     const uint16_t *qid;
     const int32_t *bsize;   // key bucket sizes (BK*R, NB)
     int32_t *cnt, *off, *cur, *qlist, *tiles, *ntiles;
+    int32_t *tcnt;          // tiles per instance
+    int32_t *kbase;         // first tile of each order key
     int N, R, NS, NB, Hq, Hkv, rep, bh0, ninst;
 };
 
@@ -287,10 +289,9 @@ __global__ void __launch_bounds__(256) qb_hist_kernel(QbP p) {
         if (hist[u]) atomicAdd(&p.cnt[(int64_t)inst * p.NB + u], hist[u]);
 }
 
-// one block per instance: bucket offsets and the tile list
+// one block per instance: bucket offsets and the instance's tile count
 __global__ void __launch_bounds__(256) qb_scan_kernel(QbP p) {
     __shared__ int32_t part_q[256], part_t[256];
-    __shared__ int32_t tbase;
     const int inst = blockIdx.x;
     int bh, r, t;
     inst_decode(p, inst, bh, r, t);
@@ -310,21 +311,73 @@ __global__ void __launch_bounds__(256) qb_scan_kernel(QbP p) {
     if (threadIdx.x == 0) {
         int aq = 0, at = 0;
         for (int i = 0; i < 256; ++i) {
-            const int vq = part_q[i], vt = part_t[i];
+            const int vq = part_q[i];
             part_q[i] = aq;
-            part_t[i] = at;
             aq += vq;
-            at += vt;
+            at += part_t[i];
         }
-        tbase = atomicAdd(p.ntiles, at);
+        p.tcnt[inst] = at;
     }
     __syncthreads();
-    int aq = part_q[threadIdx.x], at = tbase + part_t[threadIdx.x];
+    int aq = part_q[threadIdx.x];
     for (int u = u0; u < u0 + per && u < p.NB; ++u) {
         const int c = p.cnt[(int64_t)inst * p.NB + u];
         p.off[(int64_t)inst * p.NB + u] = aq;
         p.cur[(int64_t)inst * p.NB + u] = aq;
-        if (c > 0 && p.bsize[krow * p.NB + u] > 0) {
+        aq += c;
+    }
+}
+
+// Position of an instance in the tile list: ordered by (kv head, round, id
+// set, query head within the GQA group), so the tiles that read one round's
+// candidate rows of one kv head are adjacent.
+__device__ __forceinline__ int64_t qb_order_key(const QbP &p, int inst, int64_t bk_first) {
+    int bh, r, t;
+    inst_decode(p, inst, bh, r, t);
+    const int b = bh / p.Hq, h = bh % p.Hq;
+    const int64_t bk = (int64_t)b * p.Hkv + h / p.rep - bk_first;
+    return ((bk * p.R + r) * p.NS + t) * p.rep + h % p.rep;
+}
+
+// one block: tile list in that order, and the tile count
+__global__ void __launch_bounds__(256) qb_order_kernel(QbP p, int64_t nkeys) {
+    __shared__ int32_t part[256];
+    const int64_t bk_first = (int64_t)(p.bh0 / p.Hq) * p.Hkv + (p.bh0 % p.Hq) / p.rep;
+    // dense per-key tile counts, then an exclusive scan over keys
+    for (int64_t k = threadIdx.x; k < nkeys; k += 256) p.kbase[k] = 0;
+    __syncthreads();
+    for (int inst = threadIdx.x; inst < p.ninst; inst += 256)
+        p.kbase[qb_order_key(p, inst, bk_first)] = p.tcnt[inst];
+    __syncthreads();
+    const int64_t per = (nkeys + 255) / 256;
+    const int64_t k0 = threadIdx.x * per;
+    int sum = 0;
+    for (int64_t k = k0; k < k0 + per && k < nkeys; ++k) sum += p.kbase[k];
+    part[threadIdx.x] = sum;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int acc = 0;
+        for (int i = 0; i < 256; ++i) { const int v = part[i]; part[i] = acc; acc += v; }
+        p.ntiles[0] = acc;
+    }
+    __syncthreads();
+    int acc = part[threadIdx.x];
+    for (int64_t k = k0; k < k0 + per && k < nkeys; ++k) {
+        const int v = p.kbase[k];
+        p.kbase[k] = acc;
+        acc += v;
+    }
+    __syncthreads();
+    for (int inst = threadIdx.x; inst < p.ninst; inst += 256) {
+        int bh, r, t;
+        inst_decode(p, inst, bh, r, t);
+        const int b = bh / p.Hq, h = bh % p.Hq, g = h / p.rep;
+        const int64_t krow = ((int64_t)b * p.Hkv + g) * p.R + r;
+        int at = p.kbase[qb_order_key(p, inst, bk_first)];
+        for (int u = 0; u < p.NB; ++u) {
+            const int c = p.cnt[(int64_t)inst * p.NB + u];
+            if (c == 0 || p.bsize[krow * p.NB + u] == 0) continue;
+            const int aq = p.off[(int64_t)inst * p.NB + u];
             for (int k = 0; k * TQ < c; ++k) {
                 int32_t *e = p.tiles + (int64_t)at * 4;
                 e[0] = inst;
@@ -334,7 +387,6 @@ __global__ void __launch_bounds__(256) qb_scan_kernel(QbP p) {
                 ++at;
             }
         }
-        aq += c;
     }
 }
 
@@ -372,6 +424,16 @@ struct RsP {
     int64_t Call;
 };
 
+// Tile of this block: the dispatcher sends block i to XCD i % 8, so XCD x
+// takes the contiguous tile range [x * per, (x + 1) * per) in order and its L2
+// keeps the candidate rows those adjacent tiles share.  -1: no tile.
+__device__ __forceinline__ int rs_tile_of_block(int ntiles) {
+    const int per = (ntiles + 7) / 8;
+    const int x = (int)(blockIdx.x % 8), k = (int)(blockIdx.x / 8);
+    const int tile = x * per + k;
+    return (k < per && tile < ntiles) ? tile : -1;
+}
+
 template <typename T, int D>
 __global__ void __launch_bounds__(256) rescore_kernel(RsP p) {
     constexpr int LD = D + 1;
@@ -380,8 +442,9 @@ __global__ void __launch_bounds__(256) rescore_kernel(RsP p) {
     float *Ks = Qs + TQ * LD;           // [TC][LD]
     int *nidx = (int *)(Ks + TC * LD);  // [TQ]
     int *kidx = nidx + TQ;              // [TC]
-    if ((int)blockIdx.x >= *p.ntiles) return;
-    const int32_t *e = p.tiles + (int64_t)blockIdx.x * 4;
+    const int tile = rs_tile_of_block(*p.ntiles);
+    if (tile < 0) return;
+    const int32_t *e = p.tiles + (int64_t)tile * 4;
     const int inst = e[0], u = e[1], qb = e[2], qc = e[3];
     const int t = inst % p.NS, r = (inst / p.NS) % p.R, bhl = inst / (p.NS * p.R);
     const int bh = p.bh0 + bhl;
@@ -481,8 +544,9 @@ __global__ void __launch_bounds__(256) rescore_mfma_kernel(RsP p) {
     constexpr int SEGS = D / 8;                // 16-byte segments per row
     __shared__ int nidx[TQ];
     extern __shared__ __align__(16) unsigned char rs_lds[];   // [2][64][RB]
-    if ((int)blockIdx.x >= *p.ntiles) return;
-    const int32_t *e = p.tiles + (int64_t)blockIdx.x * 4;
+    const int tile = rs_tile_of_block(*p.ntiles);
+    if (tile < 0) return;
+    const int32_t *e = p.tiles + (int64_t)tile * 4;
     const int inst = e[0], u = e[1], qb = e[2], qc = e[3];
     const int t = inst % p.NS, r = (inst / p.NS) % p.R, bhl = inst / (p.NS * p.R);
     const int bh = p.bh0 + bhl;
@@ -1645,7 +1709,8 @@ topk_replay_kernel(SelP p, int chunk, int W) {
 int supported_d(int d) { return d >= 4 && d <= 256 && (d & (d - 1)) == 0; }
 
 struct Layout {
-    int64_t kid, qid, perm, bstart, bsize, sorttmp, cnt, off, cur, qlist, tiles, ntiles, S,
+    int64_t kid, qid, perm, bstart, bsize, sorttmp, cnt, off, cur, qlist, tiles, ntiles, tcnt,
+        kbase, S,
         tie_list, tie_count, aux, total;
 };
 
@@ -1669,6 +1734,8 @@ Layout plan(const Dims &D) {
     L.qlist = take(ninst * D.N * 4);
     L.tiles = take(ninst * (ceil_div(D.N, TQ) + D.NB) * 16);
     L.ntiles = take(4);
+    L.tcnt = take(ninst * 4);
+    L.kbase = take((nbh / D.rep + 2) * D.R * D.NS * D.rep * 4);
     L.S = take(nbh * D.N * D.Call * 4);
     L.tie_list = take(nbh * D.N * 4);
     L.tie_count = take(4);
@@ -1962,19 +2029,25 @@ int build_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *w
         qp.qlist = (int32_t *)(ws + L.qlist);
         qp.tiles = (int32_t *)(ws + L.tiles);
         qp.ntiles = (int32_t *)(ws + L.ntiles);
+        qp.tcnt = (int32_t *)(ws + L.tcnt);
+        qp.kbase = (int32_t *)(ws + L.kbase);
         qp.N = D.N; qp.R = D.R; qp.NS = D.NS; qp.NB = D.NB; qp.Hq = D.Hq; qp.Hkv = D.Hkv;
         qp.rep = D.rep; qp.bh0 = (int)bh0; qp.ninst = ninst;
         const int64_t ncnt = (int64_t)ninst * D.NB;
         hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(ncnt, 256), 4096)),
                            dim3(256), 0, st, qp.cnt, ncnt, 0);
         SSA_CHECK_LAUNCH();
-        hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(64), 0, st, qp.ntiles, (int64_t)1, 0);
-        SSA_CHECK_LAUNCH();
         const dim3 gq((unsigned)ceil_div(D.N, 256), (unsigned)ninst);
         hipLaunchKernelGGL(qb_hist_kernel, gq, dim3(256), (size_t)D.NB * 4, st, qp);
         SSA_CHECK_LAUNCH();
         hipLaunchKernelGGL(qb_scan_kernel, dim3((unsigned)ninst), dim3(256), 0, st, qp);
         SSA_CHECK_LAUNCH();
+        {
+            auto bk_of = [&](int64_t bh) { return (bh / D.Hq) * D.Hkv + (bh % D.Hq) / D.rep; };
+            const int64_t nkeys = (bk_of(bh0 + nbh - 1) - bk_of(bh0) + 1) * D.R * D.NS * D.rep;
+            hipLaunchKernelGGL(qb_order_kernel, dim3(1), dim3(256), 0, st, qp, nkeys);
+            SSA_CHECK_LAUNCH();
+        }
         hipLaunchKernelGGL(qb_scatter_kernel, gq, dim3(256), (size_t)D.NB * 8, st, qp);
         SSA_CHECK_LAUNCH();
 
@@ -1990,7 +2063,7 @@ int build_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *w
         rp.N = D.N; rp.M = D.M; rp.R = D.R; rp.NS = D.NS; rp.NB = D.NB; rp.C = D.C;
         rp.Hq = D.Hq; rp.Hkv = D.Hkv; rp.rep = D.rep; rp.bh0 = (int)bh0; rp.Call = D.Call;
         rp.vec4 = (D.C % 4 == 0) ? 1 : 0;
-        const int64_t grid = (int64_t)ninst * (ceil_div(D.N, TQ) + D.NB);
+        const int64_t grid = 8 * ceil_div((int64_t)ninst * (ceil_div(D.N, TQ) + D.NB), 8);
         rc = rescore_dispatch<T>(D.d, rp, grid, st);
         if (rc) return rc;
         AuxP ap{};
