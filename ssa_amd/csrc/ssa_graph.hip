@@ -579,20 +579,24 @@ __global__ void __launch_bounds__(256) rescore_mfma_kernel(RsP p) {
     }
     const bool active = 16 * wid < qc;
 
-    // cooperative copy of candidate rows [c0, c0 + 64) into registers, then LDS
+    // the tile's candidate ids, then candidate rows [c0, c0 + 64) copied
+    // through registers into LDS two slices ahead of their use
+    int32_t *prl = reinterpret_cast<int32_t *>(rs_lds + 2 * (64 * RB));
+    for (int c = tid; c < nv; c += 256) prl[c] = pr[c];
+    __syncthreads();
     constexpr int PER = (64 * SEGS + 255) / 256;
-    uint4 stage[PER];
-    auto fetch = [&](int c0) {
+    uint4 sa[PER], sb[PER];
+    auto fetch = [&](int c0, uint4 (&stage)[PER]) {
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             const int x = tid + 256 * i;
             const int row = x / SEGS, seg = x % SEGS;
             const bool ok = x < 64 * SEGS && c0 + row < nv;
-            const T *src = kbase + (int64_t)(ok ? pr[c0 + row] : 0) * p.ksn + seg * 8;
+            const T *src = kbase + (int64_t)(ok ? prl[c0 + row] : 0) * p.ksn + seg * 8;
             stage[i] = ok ? *reinterpret_cast<const uint4 *>(src) : make_uint4(0, 0, 0, 0);
         }
     };
-    auto commit = [&](int buf) {
+    auto commit = [&](int buf, const uint4 (&stage)[PER]) {
         unsigned char *dst = rs_lds + buf * (64 * RB);
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
@@ -606,12 +610,13 @@ __global__ void __launch_bounds__(256) rescore_mfma_kernel(RsP p) {
     const int64_t slotbase = (int64_t)(r * p.NS + t) * p.C;
     uint32_t *srow = p.S + ((int64_t)bhl * p.N + nidx[qok ? qrow : 0]) * p.Call + slotbase;
     const int nsl = (nv + 63) / 64;
-    fetch(0);
-    commit(0);
+    fetch(0, sa);
+    commit(0, sa);
+    if (nsl > 1) fetch(64, sa);
+    if (nsl > 2) fetch(128, sb);
     __syncthreads();
     for (int j = 0; j < nsl; ++j) {
         const int c0 = 64 * j;
-        if (j + 1 < nsl) fetch(c0 + 64);
         if (active) {
             const unsigned char *kl = rs_lds + (j & 1) * (64 * RB);
             f32x4_t acc[4];
@@ -650,8 +655,13 @@ __global__ void __launch_bounds__(256) rescore_mfma_kernel(RsP p) {
                 }
             }
         }
-        if (j + 1 < nsl) commit((j + 1) & 1);
+        // slice j + 1 was fetched a full iteration ago; every wave is done
+        // with the buffer it replaces (last read in iteration j - 1)
+        if (j + 1 < nsl) commit((j + 1) & 1, sa);
         __syncthreads();
+#pragma unroll
+        for (int i = 0; i < PER; ++i) sa[i] = sb[i];
+        if (j + 3 < nsl) fetch(c0 + 192, sb);
     }
 }
 
@@ -1889,7 +1899,7 @@ int launch_rescore(const RsP &rp, int64_t grid, hipStream_t st) {
 
 template <typename T, int Dh>
 int launch_rescore_mfma(const RsP &rp, int64_t grid, hipStream_t st) {
-    const size_t lds = (size_t)2 * 64 * rs_row_bytes<Dh>();
+    const size_t lds = (size_t)2 * 64 * rs_row_bytes<Dh>() + (size_t)rp.C * 4;
     SSA_CHECK_HIP(hipFuncSetAttribute((const void *)rescore_mfma_kernel<T, Dh>,
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     hipLaunchKernelGGL((rescore_mfma_kernel<T, Dh>), dim3((unsigned)grid), dim3(256), lds, st, rp);
