@@ -2,12 +2,14 @@
 //
 // Replaces sparse_gather_attention (sparse_attention.py:1096-1199).
 //
-// One wavefront per query row (b, h, n).  A row of d elements is covered by
-// LPR lanes with 16-byte loads, so one load instruction brings RPI = 64/LPR
-// whole K (or V) rows; with U rows in flight per lane the wave keeps
-// U*RPI*row_bytes of gathers outstanding.  Scores go to LDS (K floats per
-// wave), the fp32 softmax is a wave reduction, and P.V accumulates in fp32
-// registers, reduced across the RPI row groups at the end.
+// One wavefront per query row (b, h, n).  The row's neighbour ids are staged
+// once in LDS as int32.  A row of d elements is covered by LPR lanes with
+// 16-byte loads, so one load instruction brings RPI = 64/LPR whole K (or V)
+// rows; with U rows in flight per lane the wave keeps U*RPI*row_bytes of
+// gathers outstanding.  Scores go to LDS, the fp32 softmax is a wave
+// reduction that turns them into the weights p in place (one exp per slot),
+// and P.V accumulates in fp32 registers, reduced across the RPI row groups at
+// the end.
 //
 // Numerics follow the reference: s = fp32(q.k) * fp32(scale); -inf where
 // !valid; p = exp(s - max) / sum in fp32; 16-bit models round p to the value
@@ -92,7 +94,8 @@ apply_fwd_kernel(ApplyP p) {
     if (row >= p.rows) return;
     const int lane = lane_id();
     const int sub = lane / LPR, li = lane % LPR;
-    float *sc = smem + wid * p.K;
+    int32_t *ix = reinterpret_cast<int32_t *>(smem) + (int64_t)wid * 2 * p.K;   // key ids, -1 = masked
+    float *sc = reinterpret_cast<float *>(ix + p.K);                          // scores, then p
 
     const int n = (int)(row % p.N);
     const int64_t bh = row / p.N;
@@ -106,29 +109,30 @@ apply_fwd_kernel(ApplyP p) {
     const int64_t *nb = p.nb + row * p.K;
     const uint8_t *va = p.valid ? p.valid + row * p.K : nullptr;
 
+    // neighbour ids once, as int32 in LDS; masked or out-of-range slots -> -1
+    for (int j = lane; j < p.K; j += SSA_WAVE) {
+        const int64_t x = nb[j];
+        const bool o = (va ? va[j] != 0 : true) && x >= 0 && x < p.M;
+        ix[j] = o ? (int)x : -1;
+    }
     float qf[VEC];
     load_vec<T, VEC>(qrow + li * VEC, qf);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
     // ---- scores
     for (int j0 = 0; j0 < p.K; j0 += RPI * U) {
-        int64_t idx[U];
-        bool ok[U];
+        int xi[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int j = j0 + u * RPI + sub;
-            int64_t x = 0;
-            bool o = false;
-            if (j < p.K) {
-                x = nb[j];
-                o = va ? (va[j] != 0) : true;
-            }
-            if (x < 0 || x >= p.M) { x = 0; o = false; }   // never read out of bounds
-            idx[u] = x;
-            ok[u] = o;
+            xi[u] = j < p.K ? ix[j] : -1;
         }
         float kf[U][VEC];
 #pragma unroll
-        for (int u = 0; u < U; ++u) load_vec<T, VEC>(kb + idx[u] * p.ksn + li * VEC, kf[u]);
+        for (int u = 0; u < U; ++u)
+            load_vec<T, VEC>(kb + (int64_t)(xi[u] < 0 ? 0 : xi[u]) * p.ksn + li * VEC, kf[u]);
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             float part = 0.f;
@@ -137,50 +141,53 @@ apply_fwd_kernel(ApplyP p) {
 #pragma unroll
             for (int o = LPR / 2; o > 0; o >>= 1) part += __shfl_xor(part, o, SSA_WAVE);
             const int j = j0 + u * RPI + sub;
-            if (li == 0 && j < p.K) sc[j] = ok[u] ? part * p.scale : -INFINITY;
+            if (li == 0 && j < p.K) sc[j] = xi[u] >= 0 ? part * p.scale : -INFINITY;
         }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    // ---- fp32 softmax statistics
+    // ---- fp32 softmax, p computed once per slot (rounded to the value dtype
+    // unless fp32_attn_weights; inverted dropout applied to p)
     float m = -INFINITY;
     for (int j = lane; j < p.K; j += SSA_WAVE) m = fmaxf(m, sc[j]);
     m = wave_max(m);
     float l = 0.f;
     for (int j = lane; j < p.K; j += SSA_WAVE) l += expf(sc[j] - m);
     l = wave_sum(l);
+    const float inv = 1.f / l;
+    for (int j = lane; j < p.K; j += SSA_WAVE) {
+        float w = expf(sc[j] - m) * inv;
+        if (!p.fp32w) w = Cvt<T>::round(w);
+        if (p.drop_p > 0.f) {
+            w = (drop_uniform(p.seed, row, j) < p.drop_p) ? 0.f : w * p.drop_scale;
+            if (!p.fp32w) w = Cvt<T>::round(w);
+        }
+        sc[j] = w;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
     // ---- P.V
     float acc[VEC];
 #pragma unroll
     for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
     for (int j0 = 0; j0 < p.K; j0 += RPI * U) {
-        int64_t idx[U];
+        int xi[U];
         float pj[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int j = j0 + u * RPI + sub;
-            float w = 0.f;
-            int64_t x = 0;
-            if (j < p.K) {
-                w = expf(sc[j] - m) / l;
-                x = nb[j];
-                if (x < 0 || x >= p.M) { x = 0; w = 0.f; }
-                if (!p.fp32w) w = Cvt<T>::round(w);
-                if (p.drop_p > 0.f) {
-                    w = (drop_uniform(p.seed, row, j) < p.drop_p) ? 0.f
-                                                                   : w * p.drop_scale;
-                    if (!p.fp32w) w = Cvt<T>::round(w);
-                }
-            }
-            idx[u] = x;
-            pj[u] = w;
+            const bool in = j < p.K;
+            xi[u] = in ? ix[j] : -1;
+            pj[u] = in ? sc[j] : 0.f;
         }
         float vf[U][VEC];
 #pragma unroll
-        for (int u = 0; u < U; ++u) load_vec<T, VEC>(vb + idx[u] * p.vsn + li * VEC, vf[u]);
+        for (int u = 0; u < U; ++u)
+            load_vec<T, VEC>(vb + (int64_t)(xi[u] < 0 ? 0 : xi[u]) * p.vsn + li * VEC, vf[u]);
 #pragma unroll
         for (int u = 0; u < U; ++u)
 #pragma unroll
@@ -319,7 +326,7 @@ int launch_apply(const ApplyP &p, hipStream_t st, bool bwd) {
         hipLaunchKernelGGL((apply_bwd_kernel<T, D>), dim3((unsigned)grid), dim3(WAVES * SSA_WAVE),
                            lds, st, p);
     } else {
-        const size_t lds = (size_t)WAVES * p.K * sizeof(float);
+        const size_t lds = (size_t)WAVES * 2 * p.K * sizeof(float);
         constexpr int U = (Geo<T, D>::RPI >= 8) ? 4 : 8;
         hipLaunchKernelGGL((apply_fwd_kernel<T, D, U>), dim3((unsigned)grid),
                            dim3(WAVES * SSA_WAVE), lds, st, p);
