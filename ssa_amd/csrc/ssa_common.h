@@ -95,6 +95,14 @@ __device__ __forceinline__ int wave_sum_i(int v) {
 // ballot over the 64-lane wave
 __device__ __forceinline__ uint64_t wave_ballot(bool p) { return __ballot(p); }
 
+// lane predicate from a wave-uniform lane mask (becomes the exec mask itself)
+__device__ __forceinline__ bool in_mask(uint64_t m) { return __builtin_amdgcn_inverse_ballot_w64(m); }
+
+// wave-uniform mask of lanes [0, L)
+__device__ __forceinline__ uint64_t lanes_mask(int L) {
+    return L >= 64 ? ~0ull : (L <= 0 ? 0ull : ((1ull << L) - 1ull));
+}
+
 // number of set bits of m in lanes below this one
 __device__ __forceinline__ int lanes_below(uint64_t m) {
     return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),

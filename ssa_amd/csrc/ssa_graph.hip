@@ -885,9 +885,12 @@ struct SelList {
     const int32_t *pr;
 };
 
-// chunk descriptor flags word: lanes in the list | real slots << 7 | flags
+// chunk descriptor flags word: lanes in the list (bits 0-6) | real slots << 7
+// (bits 7-13) | flags (bits 14-17)
 constexpr int CH_EMPTY = 1 << 14;      // the list's bucket is empty (glob ++ 0)
 constexpr int CH_FIRST = 1 << 15;      // first chunk of its list
+constexpr int CH_FULL = 1 << 16;       // 64 real slots (no fillers, not empty)
+constexpr int CH_NOFILL = 1 << 17;     // every slot of the chunk in the list is real
 __device__ __forceinline__ int CH_LANES(int y) { return y & 127; }
 __device__ __forceinline__ int CH_REAL(int y) { return (y >> 7) & 127; }
 
@@ -1007,7 +1010,9 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
         const int realn = sz == 0 ? lanes : max(0, min(min(sz, p.C) - c0, SSA_WAVE));
         int4 d4;
         d4.x = (int)(prow * p.M) + min(st + c0, p.M - 1);   // perm index of lane 0 (clamped)
-        d4.y = lanes | (realn << 7) | (sz == 0 ? CH_EMPTY : 0) | (cj == 0 ? CH_FIRST : 0);
+        d4.y = lanes | (realn << 7) | (sz == 0 ? CH_EMPTY : 0) | (cj == 0 ? CH_FIRST : 0) |
+               (sz > 0 && realn == SSA_WAVE ? CH_FULL : 0) |
+               (sz > 0 && realn == lanes ? CH_NOFILL : 0);
         d4.z = list * p.C + c0;
         d4.w = p.perm[prow * p.M + p.M - 1];      // key of the overflow filler slots
         tab[ci] = d4;
@@ -1061,6 +1066,7 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     uint32_t lo = 0u;
     bool overflow = false;
     bool nseen = false;                // the query's own key has occurred
+    int kml = 0, kmh = 0;              // keep masks of the current 64 chunks, lane = chunk
     // Chunks are processed PIPE at a time; the loads of the next group are
     // issued before the current group is deduplicated, so a wave always has
     // one group of candidate ids and scores in flight.
@@ -1100,13 +1106,55 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
 #pragma unroll
         for (int u = 0; u < PIPE; ++u) {
             const int y = cy[u];
-            const bool in_list = lane < CH_LANES(y);
+            const int ci = ci0 + u;
+            if ((y & CH_NOFILL) && (nseen || !p.causal)) {
+                // fast path: every slot of the chunk is real and the query's own
+                // key has already occurred -- no fillers, no first-occurrence logic
+                const uint64_t Min = (y & CH_FULL) ? ~0ull : lanes_mask(CH_LANES(y));
+                const int v = p.causal ? min(craw[u], n) : craw[u];
+                uint64_t Mvn = 0ull;
+                uint32_t kv = csk[u];
+                if (p.causal) {
+                    Mvn = wave_ballot(v == n);
+                    kv = in_mask(Mvn) ? kself : kv;
+                }
+                const uint64_t Mdo = Min & ~Mvn;
+                const uint32_t bit = 1u << (v & 31);
+                uint32_t old = 0u;
+                if (in_mask(Mdo)) old = atomicOr(&bm[v >> 5], bit);
+                const uint64_t km = Mdo & wave_ballot((old & bit) == 0u);
+                if (lane == (ci & 63)) {
+                    kml = (int)(uint32_t)km;
+                    kmh = (int)(uint32_t)(km >> 32);
+                }
+                nk += __popcll(km);
+                const uint64_t am = km & wave_ballot(kv >= lo);
+                const int pos = cnt + lanes_below(am);
+                const int na = __popcll(am);
+                if (cnt + na <= SEL_CAP) {
+                    if (in_mask(am)) { ckey[pos] = kv; cval[pos] = (uint32_t)v; }
+                } else if (in_mask(am) && pos < SEL_CAP) {
+                    ckey[pos] = kv;
+                    cval[pos] = (uint32_t)v;
+                }
+                cnt += na;
+                continue;
+            }
+            // general path: lane masks of the chunk (slots in the list, real slots)
+            const bool full = (y & CH_FULL) != 0;
             const bool empty = (y & CH_EMPTY) != 0;
-            const bool real = in_list & (lane < CH_REAL(y));
-            const int raw = lane < CH_REAL(y) ? craw[u] : cw[u];   // fillers: perm[M-1]
-            int v = (p.causal && raw > n) ? n : raw;
-            uint32_t kv = (p.causal && v == n) ? kself : csk[u];
-            if (empty) {                               // empty bucket: glob ++ 0
+            uint64_t Min = ~0ull, Mreal = ~0ull;
+            if (!full) {
+                Min = lanes_mask(CH_LANES(y));
+                Mreal = empty ? Min : lanes_mask(CH_REAL(y));
+            }
+            int v;
+            uint32_t kv;
+            if (!empty) {
+                const int raw = full ? craw[u] : (in_mask(Mreal) ? craw[u] : cw[u]);   // fillers: perm[M-1]
+                v = p.causal ? min(raw, n) : raw;                  // future keys -> the query
+                kv = csk[u];
+            } else {                                   // empty bucket: glob ++ 0
                 const int c = ((y & CH_FIRST) ? 0 : SSA_WAVE) + lane;
                 const int j = c < ng - 1 ? c : ng - 1;
                 v = __shfl(greg_id, j, SSA_WAVE);
@@ -1115,31 +1163,48 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
             // The query's own key (every future candidate when causal) is
             // tracked by a wave-uniform flag instead of the bitmap: its first
             // occurrence in stream order decides, valid or not.
-            const bool isn = p.causal && in_list && v == n;
-            bool keepn = false;
+            uint64_t Mvn = 0ull, Mkeepn = 0ull;
             if (p.causal) {
-                const uint64_t nm = wave_ballot(isn);
-                if (nm != 0ull && !nseen) {
-                    keepn = real && lane == (int)__ffsll((long long)nm) - 1;
+                Mvn = wave_ballot(v == n) & Min;
+                if (!empty) kv = in_mask(Mvn) ? kself : kv;
+                if (!nseen && Mvn != 0ull) {
+                    Mkeepn = (1ull << (__ffsll((long long)Mvn) - 1)) & Mreal;
                     nseen = true;
                 }
             }
             const uint32_t bit = 1u << (v & 31);
-            const bool doat = real && !isn;
+            uint32_t *wp = &bm[v >> 5];
+            const uint64_t Mdo = Mreal & ~Mvn;
             uint32_t old = 0u;
-            if (doat) old = atomicOr(&bm[v >> 5], bit);
-            // fillers (all perm[M-1]) mark their key once, after the real slots
-            const uint64_t fm = wave_ballot(in_list && !real && !isn);
-            if (fm != 0ull && lane == (int)__ffsll((long long)fm) - 1) atomicOr(&bm[v >> 5], bit);
-            const bool keep = (doat && (old & bit) == 0u) || keepn;
-            const uint64_t km = wave_ballot(keep);
-            if (lane == 0 && ci0 + u < nch) kmask[ci0 + u] = km;
+            if (in_mask(Mdo)) old = atomicOr(wp, bit);
+            if (!full) {
+                // fillers (all perm[M-1]) mark their key once, after the real slots
+                const uint64_t Mfill = Min & ~Mreal & ~Mvn;
+                if (Mfill != 0ull && in_mask(1ull << (__ffsll((long long)Mfill) - 1)))
+                    atomicOr(wp, bit);
+            }
+            const uint64_t km = (Mdo & wave_ballot((old & bit) == 0u)) | Mkeepn;
+            // keep masks, one chunk per lane, stored to LDS every 64 chunks
+            if (lane == (ci & 63)) {
+                kml = (int)(uint32_t)km;
+                kmh = (int)(uint32_t)(km >> 32);
+            }
             nk += __popcll(km);
-            const bool app = keep & (kv >= lo);
-            const uint64_t am = wave_ballot(app);
+            const uint64_t am = km & wave_ballot(kv >= lo);
             const int pos = cnt + lanes_below(am);
-            if (app && pos < SEL_CAP) { ckey[pos] = kv; cval[pos] = (uint32_t)v; }
-            cnt += __popcll(am);
+            const int na = __popcll(am);
+            if (cnt + na <= SEL_CAP) {
+                if (in_mask(am)) { ckey[pos] = kv; cval[pos] = (uint32_t)v; }
+            } else if (in_mask(am) && pos < SEL_CAP) {
+                ckey[pos] = kv;
+                cval[pos] = (uint32_t)v;
+            }
+            cnt += na;
+        }
+        if (((ci0 + PIPE) & 63) == 0 || ci0 + PIPE >= nch) {
+            const int base = (ci0 + PIPE - 1) & ~63;
+            if (base + lane < nch)
+                kmask[base + lane] = ((uint64_t)(uint32_t)kmh << 32) | (uint32_t)kml;
         }
         if (cnt >= fill && cnt >= kk && !overflow) {
             wave_lds_sync();
