@@ -98,6 +98,10 @@ __device__ __forceinline__ uint64_t wave_ballot(bool p) { return __ballot(p); }
 // lane predicate from a wave-uniform lane mask (becomes the exec mask itself)
 __device__ __forceinline__ bool in_mask(uint64_t m) { return __builtin_amdgcn_inverse_ballot_w64(m); }
 
+// word 3 of a raw buffer resource on gfx950: 32-bit data format, reads past
+// num_records return 0
+#define SSA_BUF_FLAGS 0x00020000
+
 // wave-uniform mask of lanes [0, L)
 __device__ __forceinline__ uint64_t lanes_mask(int L) {
     return L >= 64 ? ~0ull : (L <= 0 ? 0ull : ((1ull << L) - 1ull));

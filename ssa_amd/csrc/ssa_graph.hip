@@ -773,6 +773,7 @@ struct SelP {
     int32_t *tie_count;
     const float *aux;      // per row: q.k_n, then q.k_glob[j] (j < G), then q.k_0
     int NA;
+    int perm_bytes;        // size of the permutation array (B*Hkv*R*M*4 < 2^31)
     int64_t nblocks;
 };
 
@@ -967,7 +968,7 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     extern __shared__ uint32_t sel_smem[];
     const int64_t blk = xcd_logical_block(blockIdx.x, p.nblocks);
     if (blk >= p.nblocks) return;
-    const int wid = threadIdx.x / SSA_WAVE;
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / SSA_WAVE);   // wave-uniform
     const int64_t rloc = blk * SEL_WAVES + wid;
     if (rloc >= p.rows) return;
     const int lane = lane_id();
@@ -1073,6 +1074,14 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     // Loads are unconditional (inactive lanes read an in-range slot), so no
     // register written by a pending load is rewritten before it lands.
     constexpr int PIPE = 4;
+    // Raw buffer loads: the chunk's offset is a scalar, the lane's a constant,
+    // and lanes past the end of the list read in-range data or 0 (the
+    // descriptors bound the permutation and this query's score row).
+    const __amdgpu_buffer_rsrc_t prs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)p.perm, (short)0, p.perm_bytes, SSA_BUF_FLAGS);
+    const __amdgpu_buffer_rsrc_t srs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)srow, (short)0, (int)(p.Call * 4), SSA_BUF_FLAGS);
+    const int lane4 = lane * 4;
     int cy[PIPE], cw[PIPE], craw[PIPE];
     uint32_t csk[PIPE];
 #pragma unroll
@@ -1082,9 +1091,8 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
         cw[u] = __builtin_amdgcn_readfirstlane(d.w);
         const int x = __builtin_amdgcn_readfirstlane(d.x);
         const int z = __builtin_amdgcn_readfirstlane(d.z);
-        const bool real = (lane < CH_REAL(cy[u])) & ((cy[u] & CH_EMPTY) == 0);
-        craw[u] = p.perm[real ? x + lane : x];
-        csk[u] = srow[real ? z + lane : z];
+        craw[u] = __builtin_amdgcn_raw_buffer_load_b32(prs, lane4, x * 4, 0);
+        csk[u] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(srs, lane4, z * 4, 0);
     }
     for (int ci0 = 0; ci0 < nch; ci0 += PIPE) {
         int ny[PIPE], nw[PIPE], nraw[PIPE];
@@ -1098,9 +1106,8 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
                 nw[u] = __builtin_amdgcn_readfirstlane(d.w);
                 const int x = __builtin_amdgcn_readfirstlane(d.x);
                 const int z = __builtin_amdgcn_readfirstlane(d.z);
-                const bool real = (lane < CH_REAL(ny[u])) & ((ny[u] & CH_EMPTY) == 0);
-                nraw[u] = p.perm[real ? x + lane : x];
-                nsk[u] = srow[real ? z + lane : z];
+                nraw[u] = __builtin_amdgcn_raw_buffer_load_b32(prs, lane4, x * 4, 0);
+                nsk[u] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(srs, lane4, z * 4, 0);
             }
         }
 #pragma unroll
@@ -1842,8 +1849,8 @@ int make_dims(const ssa_graph_args *a, Dims &D) {
         ssa_set_error("build_graph: key length %d unsupported (1..32768)", a->M);
         return SSA_E_UNSUP;
     }
-    SSA_CHECK_ARG((int64_t)a->B * a->Hkv * a->R * a->M < ((int64_t)1 << 31),
-                  "build_graph: B*Hkv*R*M must stay below 2^31 (bucket permutation index)");
+    SSA_CHECK_ARG((int64_t)a->B * a->Hkv * a->R * a->M < ((int64_t)1 << 29),
+                  "build_graph: B*Hkv*R*M must stay below 2^29 (bucket permutation bytes)");
     D.B = a->B; D.Hq = a->Hq; D.Hkv = a->Hkv; D.rep = a->Hq / a->Hkv;
     D.N = a->N; D.M = a->M; D.d = a->d; D.R = a->R; D.maxP = a->max_p; D.P = a->P;
     D.Tp = a->T < a->P ? a->T : a->P;
@@ -2169,6 +2176,7 @@ int build_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *w
         sp.tie_count = (int32_t *)(ws + L.tie_count);
         sp.aux = ap.out;
         sp.NA = ap.NA;
+        sp.perm_bytes = (int)(D.BK * D.R * D.M * 4);
         sp.nblocks = ceil_div(sp.rows, SEL_WAVES);
         hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(64), 0, st, sp.tie_count, (int64_t)1, 0);
         SSA_CHECK_LAUNCH();
