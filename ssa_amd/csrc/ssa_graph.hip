@@ -831,7 +831,7 @@ constexpr int SEL_CAP = 512;   // keys kept in LDS for the exact threshold searc
 //                     slot of lane 0, key id of the overflow filler slots
 //   bm    [words]     seen bitmap, later the merge bitmap
 //   kmask [2*nch]     per 64-slot chunk, the ballot of kept slots
-//   ckey  [SEL_CAP]   sample of kept keys, then kept keys >= the lower bound
+//   ckey  [SEL_CAP]   kept keys >= the lower bound
 //   cval  [SEL_CAP]   key id of each compacted key (entries stay in stream order)
 //   gsc   [64]        score keys of glob[0..G-1] and key 0 (empty buckets)
 //   gid   [64]        the ids glob[0..G-1], 0
@@ -963,7 +963,7 @@ __device__ void full_merge_emit(uint32_t *bm, const SelP &p, int n, int64_t row,
 //  emit    selected = key > thr, or key == thr for the first `need` in stream
 //          order; LSH mode writes them by descending score, FULL mode merges
 //          them with the window and the globals through a key bitmap.
-template <typename T, bool LSH_MODE>
+template <typename T, bool LSH_MODE, bool CAUSAL>
 __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     extern __shared__ uint32_t sel_smem[];
     const int64_t blk = xcd_logical_block(blockIdx.x, p.nblocks);
@@ -994,7 +994,7 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     // arithmetic, so equal keys get equal scores): the query's own key, which
     // replaces future candidates, and the empty-bucket list glob ++ 0
     const float *arow = p.aux + rloc * p.NA;
-    const uint32_t kself = p.causal ? score_key(arow[0]) : 0u;
+    const uint32_t kself = CAUSAL ? score_key(arow[0]) : 0u;
     const uint16_t *qids = p.qid + row * p.R * p.NS;
     const uint32_t *srow = p.S + ((int64_t)bhl * p.N + n) * p.Call;
     const int ng = min(p.G + 1, SSA_WAVE);
@@ -1046,9 +1046,9 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
         if (L.sz > 0) {
             real = c < L.nv;
             const int raw = L.pr[real ? L.st + c : p.M - 1];
-            v = (p.causal && raw > n) ? n : raw;
+            v = (CAUSAL && raw > n) ? n : raw;
             const uint32_t sk = srow[real ? (int64_t)list * p.C + c : 0];
-            kv = (p.causal && v == n) ? kself : sk;
+            kv = (CAUSAL && v == n) ? kself : sk;
         } else {                                     // empty bucket: glob ++ 0
             real = true;
             const int j = c < ng - 1 ? c : ng - 1;
@@ -1110,18 +1110,19 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
                 nsk[u] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(srs, lane4, z * 4, 0);
             }
         }
+        const bool roomy = cnt + PIPE * SSA_WAVE <= SEL_CAP;   // no capacity check needed
 #pragma unroll
         for (int u = 0; u < PIPE; ++u) {
             const int y = cy[u];
             const int ci = ci0 + u;
-            if ((y & CH_NOFILL) && (nseen || !p.causal)) {
+            if ((y & CH_NOFILL) && (nseen || !CAUSAL)) {
                 // fast path: every slot of the chunk is real and the query's own
                 // key has already occurred -- no fillers, no first-occurrence logic
                 const uint64_t Min = (y & CH_FULL) ? ~0ull : lanes_mask(CH_LANES(y));
-                const int v = p.causal ? min(craw[u], n) : craw[u];
+                const int v = CAUSAL ? min(craw[u], n) : craw[u];
                 uint64_t Mvn = 0ull;
                 uint32_t kv = csk[u];
-                if (p.causal) {
+                if (CAUSAL) {
                     Mvn = wave_ballot(v == n);
                     kv = in_mask(Mvn) ? kself : kv;
                 }
@@ -1134,15 +1135,18 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
                     kml = (int)(uint32_t)km;
                     kmh = (int)(uint32_t)(km >> 32);
                 }
-                nk += __popcll(km);
                 const uint64_t am = km & wave_ballot(kv >= lo);
-                const int pos = cnt + lanes_below(am);
+                const int below = lanes_below(am);
                 const int na = __popcll(am);
-                if (cnt + na <= SEL_CAP) {
-                    if (in_mask(am)) { ckey[pos] = kv; cval[pos] = (uint32_t)v; }
-                } else if (in_mask(am) && pos < SEL_CAP) {
-                    ckey[pos] = kv;
-                    cval[pos] = (uint32_t)v;
+                if (roomy) {
+                    // every lane stores: appended keys at cnt.., the others just
+                    // past them (in range, never read)
+                    const int dst = in_mask(am) ? cnt + below : cnt + na + (lane - below);
+                    ckey[dst] = kv;
+                    cval[dst] = (uint32_t)v;
+                } else if (in_mask(am) && cnt + below < SEL_CAP) {
+                    ckey[cnt + below] = kv;
+                    cval[cnt + below] = (uint32_t)v;
                 }
                 cnt += na;
                 continue;
@@ -1159,7 +1163,7 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
             uint32_t kv;
             if (!empty) {
                 const int raw = full ? craw[u] : (in_mask(Mreal) ? craw[u] : cw[u]);   // fillers: perm[M-1]
-                v = p.causal ? min(raw, n) : raw;                  // future keys -> the query
+                v = CAUSAL ? min(raw, n) : raw;                  // future keys -> the query
                 kv = csk[u];
             } else {                                   // empty bucket: glob ++ 0
                 const int c = ((y & CH_FIRST) ? 0 : SSA_WAVE) + lane;
@@ -1171,7 +1175,7 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
             // tracked by a wave-uniform flag instead of the bitmap: its first
             // occurrence in stream order decides, valid or not.
             uint64_t Mvn = 0ull, Mkeepn = 0ull;
-            if (p.causal) {
+            if (CAUSAL) {
                 Mvn = wave_ballot(v == n) & Min;
                 if (!empty) kv = in_mask(Mvn) ? kself : kv;
                 if (!nseen && Mvn != 0ull) {
@@ -1196,17 +1200,10 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
                 kml = (int)(uint32_t)km;
                 kmh = (int)(uint32_t)(km >> 32);
             }
-            nk += __popcll(km);
             const uint64_t am = km & wave_ballot(kv >= lo);
             const int pos = cnt + lanes_below(am);
-            const int na = __popcll(am);
-            if (cnt + na <= SEL_CAP) {
-                if (in_mask(am)) { ckey[pos] = kv; cval[pos] = (uint32_t)v; }
-            } else if (in_mask(am) && pos < SEL_CAP) {
-                ckey[pos] = kv;
-                cval[pos] = (uint32_t)v;
-            }
-            cnt += na;
+            if (in_mask(am) && pos < SEL_CAP) { ckey[pos] = kv; cval[pos] = (uint32_t)v; }
+            cnt += __popcll(am);
         }
         if (((ci0 + PIPE) & 63) == 0 || ci0 + PIPE >= nch) {
             const int base = (ci0 + PIPE - 1) & ~63;
@@ -1262,6 +1259,12 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     }
     overflow = overflow || cnt > SEL_CAP;
     wave_lds_sync();
+    // kept slots in the whole stream
+    {
+        int c = 0;
+        for (int ci = lane; ci < nch; ci += SSA_WAVE) c += __popcll(kmask[ci]);
+        nk = wave_sum_i(c);
+    }
 
     // re-walk the kept slots of the stream in order (rare paths only)
     auto walk_kept = [&](auto &&fn) {
@@ -2018,7 +2021,7 @@ int rescore_dispatch(int d, const RsP &rp, int64_t grid, hipStream_t st) {
     return SSA_E_UNSUP;
 }
 
-template <typename T, bool LSH>
+template <typename T, bool LSH, bool CAUSAL>
 int launch_select(const SelP &sp, hipStream_t st) {
     const size_t lds =
         (size_t)SEL_WAVES * sel_lds_words(sp.nlists * sp.CPL, sp.words, sp.kk, LSH) * 4;
@@ -2026,11 +2029,11 @@ int launch_select(const SelP &sp, hipStream_t st) {
         ssa_set_error("build_graph: select needs %zu bytes of LDS", lds);
         return SSA_E_UNSUP;
     }
-    SSA_CHECK_HIP(hipFuncSetAttribute((const void *)select_kernel<T, LSH>,
+    SSA_CHECK_HIP(hipFuncSetAttribute((const void *)select_kernel<T, LSH, CAUSAL>,
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     const int64_t grid = 8 * ceil_div(sp.nblocks, 8);
-    hipLaunchKernelGGL((select_kernel<T, LSH>), dim3((unsigned)grid), dim3(SEL_WAVES * SSA_WAVE),
-                       lds, st, sp);
+    hipLaunchKernelGGL((select_kernel<T, LSH, CAUSAL>), dim3((unsigned)grid),
+                       dim3(SEL_WAVES * SSA_WAVE), lds, st, sp);
     SSA_CHECK_LAUNCH();
     return SSA_OK;
 }
@@ -2086,8 +2089,9 @@ int launch_replay(const SelP &sp, int chunk, hipStream_t st) {
 
 template <typename T>
 int select_dispatch(const SelP &sp, hipStream_t st) {
-    return sp.mode == SSA_GRAPH_LSH ? launch_select<T, true>(sp, st)
-                                    : launch_select<T, false>(sp, st);
+    if (sp.mode == SSA_GRAPH_LSH)
+        return sp.causal ? launch_select<T, true, true>(sp, st) : launch_select<T, true, false>(sp, st);
+    return sp.causal ? launch_select<T, false, true>(sp, st) : launch_select<T, false, false>(sp, st);
 }
 
 template <typename T>
