@@ -1042,7 +1042,8 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
         return L;
     };
     // key id and score key of slot c of a list (c < C)
-    auto slot_kv = [&](const SelList &L, int list, int c, int &v, uint32_t &kv, bool &real) {
+    auto slot_kv = [&, n, kself](const SelList &L, int list, int c, int &v, uint32_t &kv,
+                                 bool &real) {
         if (L.sz > 0) {
             real = c < L.nv;
             const int raw = L.pr[real ? L.st + c : p.M - 1];
