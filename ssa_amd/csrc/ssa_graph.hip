@@ -263,6 +263,7 @@ struct QbP {
     int32_t *cnt, *off, *cur, *qlist, *tiles, *ntiles;
     int32_t *tcnt;          // tiles per instance
     int32_t *kbase;         // first tile of each order key
+    int32_t *hcnt;          // per (instance, query block, bucket): count, then first position
     int N, R, NS, NB, Hq, Hkv, rep, bh0, ninst;
 };
 
@@ -285,11 +286,13 @@ __global__ void __launch_bounds__(256) qb_hist_kernel(QbP p) {
         atomicAdd(&hist[u], 1);
     }
     __syncthreads();
-    for (int u = threadIdx.x; u < p.NB; u += blockDim.x)
-        if (hist[u]) atomicAdd(&p.cnt[(int64_t)inst * p.NB + u], hist[u]);
+    int32_t *hb = p.hcnt + ((int64_t)inst * gridDim.x + blockIdx.x) * p.NB;
+    for (int u = threadIdx.x; u < p.NB; u += blockDim.x) hb[u] = hist[u];
 }
 
-// one block per instance: bucket offsets and the instance's tile count
+// one block per instance: bucket totals and offsets, the first position of
+// each query block's queries in each bucket (so queries stay in position
+// order inside a bucket), and the instance's tile count
 __global__ void __launch_bounds__(256) qb_scan_kernel(QbP p) {
     __shared__ int32_t part_q[256], part_t[256];
     const int inst = blockIdx.x;
@@ -297,11 +300,15 @@ __global__ void __launch_bounds__(256) qb_scan_kernel(QbP p) {
     inst_decode(p, inst, bh, r, t);
     const int b = bh / p.Hq, h = bh % p.Hq, g = h / p.rep;
     const int64_t krow = ((int64_t)b * p.Hkv + g) * p.R + r;
+    const int nblk = (p.N + 255) / 256;
+    int32_t *hb = p.hcnt + (int64_t)inst * nblk * p.NB;
     const int per = (p.NB + 255) / 256;
     const int u0 = threadIdx.x * per;
     int sq = 0, st = 0;
     for (int u = u0; u < u0 + per && u < p.NB; ++u) {
-        const int c = p.cnt[(int64_t)inst * p.NB + u];
+        int c = 0;
+        for (int k = 0; k < nblk; ++k) c += hb[(int64_t)k * p.NB + u];
+        p.cnt[(int64_t)inst * p.NB + u] = c;
         sq += c;
         if (c > 0 && p.bsize[krow * p.NB + u] > 0) st += (c + TQ - 1) / TQ;
     }
@@ -321,10 +328,14 @@ __global__ void __launch_bounds__(256) qb_scan_kernel(QbP p) {
     __syncthreads();
     int aq = part_q[threadIdx.x];
     for (int u = u0; u < u0 + per && u < p.NB; ++u) {
-        const int c = p.cnt[(int64_t)inst * p.NB + u];
         p.off[(int64_t)inst * p.NB + u] = aq;
-        p.cur[(int64_t)inst * p.NB + u] = aq;
-        aq += c;
+        int base = aq;
+        for (int k = 0; k < nblk; ++k) {
+            const int c = hb[(int64_t)k * p.NB + u];
+            hb[(int64_t)k * p.NB + u] = base;
+            base += c;
+        }
+        aq = base;
     }
 }
 
@@ -391,26 +402,34 @@ __global__ void __launch_bounds__(256) qb_order_kernel(QbP p, int64_t nkeys) {
 }
 
 __global__ void __launch_bounds__(256) qb_scatter_kernel(QbP p) {
-    // block-local ranks first, then one global reservation per (block, bucket)
-    extern __shared__ int32_t sc_smem[];
-    int32_t *hist = sc_smem;          // [NB]
-    int32_t *base = sc_smem + p.NB;   // [NB]
+    // rank of each query among the block's queries of its bucket, in position
+    // order: per wave one ballot per distinct bucket, then the waves in order
+    extern __shared__ int32_t sc_smem[];   // [4][NB] per-wave counts
     const int inst = blockIdx.y;
     int bh, r, t;
     inst_decode(p, inst, bh, r, t);
-    for (int u = threadIdx.x; u < p.NB; u += blockDim.x) hist[u] = 0;
+    const int wid = threadIdx.x / SSA_WAVE;
+    for (int x = threadIdx.x; x < 4 * p.NB; x += blockDim.x) sc_smem[x] = 0;
     __syncthreads();
     const int n = blockIdx.x * blockDim.x + threadIdx.x;
-    int u = 0, local = 0;
-    if (n < p.N) {
-        u = p.qid[(((int64_t)bh * p.N + n) * p.R + r) * p.NS + t];
-        local = atomicAdd(&hist[u], 1);
+    const bool in = n < p.N;
+    const int u = in ? p.qid[(((int64_t)bh * p.N + n) * p.R + r) * p.NS + t] : -1;
+    int local = 0;
+    uint64_t todo = wave_ballot(in);
+    while (todo) {
+        const int leader = (int)__ffsll((long long)todo) - 1;
+        const int ul = __shfl(u, leader, SSA_WAVE);
+        const uint64_t m = wave_ballot(in && u == ul);
+        if (in && u == ul) local = lanes_below(m);
+        if (lane_id() == leader) sc_smem[wid * p.NB + ul] = __popcll(m);
+        todo &= ~m;
     }
     __syncthreads();
-    for (int b = threadIdx.x; b < p.NB; b += blockDim.x)
-        if (hist[b]) base[b] = atomicAdd(&p.cur[(int64_t)inst * p.NB + b], hist[b]);
-    __syncthreads();
-    if (n < p.N) p.qlist[(int64_t)inst * p.N + base[u] + local] = n;
+    if (in) {
+        int pos = p.hcnt[((int64_t)inst * gridDim.x + blockIdx.x) * p.NB + u] + local;
+        for (int w = 0; w < wid; ++w) pos += sc_smem[w * p.NB + u];
+        p.qlist[(int64_t)inst * p.N + pos] = n;
+    }
 }
 
 // ------------------------------------------------------------------ rescore
@@ -1816,7 +1835,7 @@ Layout plan(const Dims &D) {
     L.sorttmp = take(ssa_sort_tmp_bytes((int)(D.BK * D.R), D.M));
     L.cnt = take(ninst * D.NB * 4);
     L.off = take(ninst * D.NB * 4);
-    L.cur = take(ninst * D.NB * 4);
+    L.cur = take(ninst * ceil_div(D.N, 256) * D.NB * 4);   // per-block counts / bases
     L.qlist = take(ninst * D.N * 4);
     L.tiles = take(ninst * (ceil_div(D.N, TQ) + D.NB) * 16);
     L.ntiles = take(4);
@@ -2112,7 +2131,8 @@ int build_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *w
         qp.bsize = (const int32_t *)(ws + L.bsize);
         qp.cnt = (int32_t *)(ws + L.cnt);
         qp.off = (int32_t *)(ws + L.off);
-        qp.cur = (int32_t *)(ws + L.cur);
+        qp.cur = nullptr;
+        qp.hcnt = (int32_t *)(ws + L.cur);
         qp.qlist = (int32_t *)(ws + L.qlist);
         qp.tiles = (int32_t *)(ws + L.tiles);
         qp.ntiles = (int32_t *)(ws + L.ntiles);
@@ -2120,10 +2140,6 @@ int build_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *w
         qp.kbase = (int32_t *)(ws + L.kbase);
         qp.N = D.N; qp.R = D.R; qp.NS = D.NS; qp.NB = D.NB; qp.Hq = D.Hq; qp.Hkv = D.Hkv;
         qp.rep = D.rep; qp.bh0 = (int)bh0; qp.ninst = ninst;
-        const int64_t ncnt = (int64_t)ninst * D.NB;
-        hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(ncnt, 256), 4096)),
-                           dim3(256), 0, st, qp.cnt, ncnt, 0);
-        SSA_CHECK_LAUNCH();
         const dim3 gq((unsigned)ceil_div(D.N, 256), (unsigned)ninst);
         hipLaunchKernelGGL(qb_hist_kernel, gq, dim3(256), (size_t)D.NB * 4, st, qp);
         SSA_CHECK_LAUNCH();
@@ -2135,7 +2151,7 @@ int build_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *w
             hipLaunchKernelGGL(qb_order_kernel, dim3(1), dim3(256), 0, st, qp, nkeys);
             SSA_CHECK_LAUNCH();
         }
-        hipLaunchKernelGGL(qb_scatter_kernel, gq, dim3(256), (size_t)D.NB * 8, st, qp);
+        hipLaunchKernelGGL(qb_scatter_kernel, gq, dim3(256), (size_t)D.NB * 16, st, qp);
         SSA_CHECK_LAUNCH();
 
         RsP rp{};
