@@ -92,6 +92,23 @@ __device__ __forceinline__ int wave_sum_i(int v) {
     return v;
 }
 
+__device__ __forceinline__ uint32_t wave_max_u(uint32_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const uint32_t y = (uint32_t)__shfl_xor((int)v, o, SSA_WAVE);
+        v = y > v ? y : v;
+    }
+    return v;
+}
+__device__ __forceinline__ uint32_t wave_min_u(uint32_t v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const uint32_t y = (uint32_t)__shfl_xor((int)v, o, SSA_WAVE);
+        v = y < v ? y : v;
+    }
+    return v;
+}
+
 // ballot over the 64-lane wave
 __device__ __forceinline__ uint64_t wave_ballot(bool p) { return __ballot(p); }
 

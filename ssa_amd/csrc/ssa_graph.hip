@@ -434,11 +434,11 @@ __global__ void __launch_bounds__(256) qb_scatter_kernel(QbP p) {
 
 // ------------------------------------------------------------------ rescore
 struct RsP {
-    const int32_t *tiles, *ntiles, *qlist, *perm, *bstart, *bsize;
+    const int32_t *tiles, *ntiles, *qlist, *sid, *bstart, *bsize;
     const void *q, *k;
     int64_t qsb, qsh, qsn, ksb, ksh, ksn;
-    uint32_t *S;       // order-preserving score keys (score_key), slot = stream position
-    int N, M, R, NS, NB, C, Hq, Hkv, rep, bh0;
+    uint32_t *S;       // score keys (score_key); slot = list * C + sorted member index
+    int N, M, R, NS, NB, C, Hq, Hkv, rep, bh0, causal;
     int vec4;          // rows and list starts of S are 16-byte aligned (C % 4 == 0)
     int64_t Call;
 };
@@ -451,6 +451,24 @@ __device__ __forceinline__ int rs_tile_of_block(int ntiles) {
     const int x = (int)(blockIdx.x % 8), k = (int)(blockIdx.x / 8);
     const int tile = x * per + k;
     return (k < per && tile < ntiles) ? tile : -1;
+}
+
+// Sorted members a tile needs: a causal query only uses members below its own
+// position, so the tile needs those below its last query (all otherwise).
+// sd: the bucket's member ids in ascending order; nq: tile queries in nidx.
+__device__ __forceinline__ int rs_tile_cutoff(const int32_t *sd, int nv, const int *nidx, int nq,
+                                              bool causal) {
+    if (!causal) return nv;
+    const int lane = lane_id();
+    const int nmax = (int)wave_max_u(lane < nq ? (uint32_t)nidx[lane] : 0u);
+    int cnt = 0;
+    for (int c0 = 0; c0 < nv; c0 += SSA_WAVE) {
+        const int c = c0 + lane;
+        const int m = __popcll(wave_ballot(c < nv && sd[c] < nmax));
+        cnt += m;
+        if (m < SSA_WAVE) break;
+    }
+    return cnt;
 }
 
 template <typename T, int D>
@@ -470,13 +488,14 @@ __global__ void __launch_bounds__(256) rescore_kernel(RsP p) {
     const int b = bh / p.Hq, h = bh % p.Hq, g = h / p.rep;
     const int64_t prow = ((int64_t)b * p.Hkv + g) * p.R + r;
     const int st = p.bstart[prow * p.NB + u];
-    const int nv = min(p.bsize[prow * p.NB + u], p.C);
     const int tid = threadIdx.x;
     const T *qbase = (const T *)p.q + b * p.qsb + h * p.qsh;
     const T *kbase = (const T *)p.k + b * p.ksb + g * p.ksh;
+    const int32_t *sd = p.sid + prow * p.M + st;
 
     if (tid < TQ) nidx[tid] = tid < qc ? p.qlist[(int64_t)inst * p.N + qb + tid] : 0;
     __syncthreads();
+    const int nv = rs_tile_cutoff(sd, min(p.bsize[prow * p.NB + u], p.C), nidx, qc, p.causal);
     for (int x = tid; x < TQ * D; x += 256) {
         const int i = x / D, c = x % D;
         Qs[i * LD + c] = i < qc ? to_f32(qbase[(int64_t)nidx[i] * p.qsn + c]) : 0.f;
@@ -485,7 +504,7 @@ __global__ void __launch_bounds__(256) rescore_kernel(RsP p) {
     const int ty = tid / 16, tx = tid % 16;
     for (int c0 = 0; c0 < nv; c0 += TC) {
         __syncthreads();
-        if (tid < TC) kidx[tid] = (c0 + tid < nv) ? p.perm[prow * p.M + st + c0 + tid] : 0;
+        if (tid < TC) kidx[tid] = (c0 + tid < nv) ? sd[c0 + tid] : 0;
         __syncthreads();
         for (int x = tid; x < TC * D; x += 256) {
             const int j = x / D, c = x % D;
@@ -544,8 +563,8 @@ template <> struct Mfma16<f16_t> {
     }
 };
 
-// MFMA rescore of one tile (up to 64 queries of one bucket x the bucket's nv
-// candidates).  The block stages each 64-candidate slice of K rows in LDS once
+// MFMA rescore of one tile (up to 64 queries of one bucket x the bucket's
+// candidates in ascending id order, up to the tile's cutoff).  The block stages each 64-candidate slice of K rows in LDS once
 // (double-buffered, rows padded by 16 bytes so the fragment reads are free of
 // bank conflicts); wave w scores queries 16w..16w+15 against the slice as
 // K . Q^T, so each lane holds 4 consecutive candidates of one query and writes
@@ -572,14 +591,14 @@ __global__ void __launch_bounds__(256) rescore_mfma_kernel(RsP p) {
     const int b = bh / p.Hq, h = bh % p.Hq, g = h / p.rep;
     const int64_t prow = ((int64_t)b * p.Hkv + g) * p.R + r;
     const int st = p.bstart[prow * p.NB + u];
-    const int nv = min(p.bsize[prow * p.NB + u], p.C);
+    const int nva = min(p.bsize[prow * p.NB + u], p.C);
     const int tid = threadIdx.x;
     const int wid = tid / SSA_WAVE;
     const int lane = lane_id();
     const int li = lane % 16, lg = lane / 16;
     const T *qbase = (const T *)p.q + b * p.qsb + h * p.qsh;
     const T *kbase = (const T *)p.k + b * p.ksb + g * p.ksh;
-    const int32_t *pr = p.perm + prow * p.M + st;
+    const int32_t *pr = p.sid + prow * p.M + st;
     if (tid < TQ) nidx[tid] = tid < qc ? p.qlist[(int64_t)inst * p.N + qb + tid] : 0;
     __syncthreads();
 
@@ -601,8 +620,9 @@ __global__ void __launch_bounds__(256) rescore_mfma_kernel(RsP p) {
     // the tile's candidate ids, then candidate rows [c0, c0 + 64) copied
     // through registers into LDS two slices ahead of their use
     int32_t *prl = reinterpret_cast<int32_t *>(rs_lds + 2 * (64 * RB));
-    for (int c = tid; c < nv; c += 256) prl[c] = pr[c];
+    for (int c = tid; c < nva; c += 256) prl[c] = pr[c];
     __syncthreads();
+    const int nv = rs_tile_cutoff(prl, nva, nidx, qc, p.causal);
     constexpr int PER = (64 * SEGS + 255) / 256;
     uint4 sa[PER], sb[PER];
     auto fetch = [&](int c0, uint4 (&stage)[PER]) {
@@ -682,6 +702,135 @@ __global__ void __launch_bounds__(256) rescore_mfma_kernel(RsP p) {
         for (int i = 0; i < PER; ++i) sa[i] = sb[i];
         if (j + 3 < nsl) fetch(c0 + 192, sb);
     }
+}
+
+// ------------------------------------------------------------------ sorted candidate lists
+// A bucket's candidate list is its first C members in permutation order
+// (:668-696).  Only the order-free parts of the stream are rescored and
+// scanned in key order: with the members of each list sorted by key id, the
+// members a causal query can use (ids below its own position) are a prefix.
+// Per (kv head, round) row of M permutation positions:
+//   sid[st + i]  i-th smallest member id of the bucket starting at st (i < nv)
+//   rnk[st + c]  sorted index of the member at list slot c
+//   smin[st + i] smallest list slot among sorted members i.. (first future slot)
+//   inv[key]     permutation position of every key
+struct LsP {
+    const int32_t *perm, *bstart, *bsize;
+    int32_t *sid, *rnk, *smin, *inv;
+    int M, NB, C;
+};
+
+__global__ void __launch_bounds__(256) list_sort_kernel(LsP p) {
+    extern __shared__ uint32_t ls_key[];
+    const int64_t prow = blockIdx.x / p.NB;
+    const int u = (int)(blockIdx.x % p.NB);
+    const int st = p.bstart[prow * p.NB + u];
+    const int sz = p.bsize[prow * p.NB + u];
+    if (sz == 0) return;
+    const int nv = min(sz, p.C);
+    int P2 = 1;
+    while (P2 < nv) P2 <<= 1;
+    const int tid = threadIdx.x;
+    const int64_t base = prow * p.M;
+    const int32_t *pr = p.perm + base;
+    for (int i = tid; i < sz; i += 256) p.inv[base + pr[st + i]] = st + i;
+    // key id << 16 | list slot: ids < 2^15, slots < 2^16
+    for (int i = tid; i < P2; i += 256)
+        ls_key[i] = i < nv ? (((uint32_t)pr[st + i] << 16) | (uint32_t)i) : 0xffffffffu;
+    __syncthreads();
+    for (int k = 2; k <= P2; k <<= 1) {            // bitonic sort, ascending
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            for (int i = tid; i < P2; i += 256) {
+                const int ixj = i ^ j;
+                if (ixj > i) {
+                    const uint32_t a = ls_key[i], b = ls_key[ixj];
+                    if ((a > b) == ((i & k) == 0)) { ls_key[i] = b; ls_key[ixj] = a; }
+                }
+            }
+            __syncthreads();
+        }
+    }
+    for (int i = tid; i < nv; i += 256) {
+        const uint32_t key = ls_key[i];
+        p.sid[base + st + i] = (int32_t)(key >> 16);
+        p.rnk[base + st + (int)(key & 0xffffu)] = i;
+    }
+    if (tid < SSA_WAVE) {                          // suffix minimum of the list slots
+        const int lane = tid;
+        int carry = p.C;
+        for (int hi = nv; hi > 0; hi -= SSA_WAVE) {
+            const int i = hi - SSA_WAVE + lane;
+            int c = i >= 0 ? (int)(ls_key[i] & 0xffffu) : p.C;
+#pragma unroll
+            for (int o = 1; o < SSA_WAVE; o <<= 1) {
+                const int y = __shfl_down(c, o, SSA_WAVE);
+                if (lane + o < SSA_WAVE) c = min(c, y);
+            }
+            c = min(c, carry);
+            if (i >= 0) p.smin[base + st + i] = c;
+            carry = __shfl(c, 0, SSA_WAVE);
+        }
+    }
+}
+
+// Per (query row, list): the number of sorted members below the query
+// (causal; all of them otherwise), and where the query's own key first occurs
+// in the list -- a member at or past the query (causal substitution, :698-709),
+// an overflow filler (invalid) when the filler key is at or past the query, or
+// an entry of glob ++ 0 for an empty bucket (:711-737) -- as
+// {bucket start, size, cutoff, first slot * 2 + (that slot is valid)}; first
+// slot C: none.
+struct CutP {
+    const uint16_t *qid;
+    const int32_t *perm, *bstart, *bsize, *sid, *smin;
+    const int64_t *glob;
+    int4 *cut;
+    int N, M, R, NS, NB, C, Hq, Hkv, rep, bh0, G, causal, nlists;
+    int64_t rows;
+};
+
+__global__ void __launch_bounds__(256) cut_kernel(CutP p) {
+    const int64_t x = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (x >= p.rows * p.nlists) return;
+    const int list = (int)(x % p.nlists);
+    const int64_t rloc = x / p.nlists;
+    const int n = (int)(rloc % p.N);
+    const int bh = p.bh0 + (int)(rloc / p.N);
+    const int b = bh / p.Hq, h = bh % p.Hq, g = h / p.rep;
+    const int64_t row = (int64_t)bh * p.N + n;
+    const int u = p.qid[row * p.R * p.NS + list];
+    const int64_t prow = ((int64_t)b * p.Hkv + g) * p.R + list / p.NS;
+    const int st = p.bstart[prow * p.NB + u];
+    const int sz = p.bsize[prow * p.NB + u];
+    int cutoff = 0, first = p.C, real = 0;
+    if (sz == 0) {
+        if (p.causal) {
+            const int gl = min(p.G, p.C);
+            for (int j = 0; j < gl; ++j)
+                if ((int)p.glob[j] == n) { first = j; break; }
+            if (first == p.C && n == 0 && p.G < p.C) first = p.G;
+            real = 1;
+        }
+    } else {
+        const int nv = min(sz, p.C);
+        if (p.causal) {
+            const int32_t *sd = p.sid + prow * p.M + st;
+            int lo = 0, hi = nv;                   // members with id < n
+            while (lo < hi) {
+                const int mid = (lo + hi) >> 1;
+                if (sd[mid] < n) lo = mid + 1; else hi = mid;
+            }
+            cutoff = lo;
+            const int a = cutoff < nv ? p.smin[prow * p.M + st + cutoff] : p.C;
+            const int f = p.perm[prow * p.M + p.M - 1];
+            const int fb = (sz < p.C && f >= n) ? sz : p.C;
+            first = min(a, fb);
+            real = a < fb ? 1 : 0;
+        } else {
+            cutoff = nv;
+        }
+    }
+    p.cut[x] = make_int4(st, sz, cutoff, first * 2 + real);
 }
 
 // ------------------------------------------------------------------ extra scores
@@ -778,6 +927,8 @@ __global__ void __launch_bounds__(256) aux_valu_kernel(AuxP p) {
 struct SelP {
     const uint16_t *qid;
     const int32_t *perm, *bstart, *bsize;
+    const int32_t *sid, *rnk, *inv;   // sorted list members, their ranks, key positions
+    const int4 *cut;       // per (row, list): {start, size, cutoff, first slot * 2 + valid}
     const uint32_t *S;     // score keys (score_key), row-major (rows, Call)
     const void *q, *k;
     int64_t qsb, qsh, qsn, ksb, ksh, ksn;
@@ -796,9 +947,6 @@ struct SelP {
     int64_t nblocks;
 };
 
-__device__ __forceinline__ bool bm_test(const uint32_t *bm, int v) {
-    return (bm[v >> 5] >> (v & 31)) & 1u;
-}
 __device__ __forceinline__ void bm_set(uint32_t *bm, int v) { atomicOr(&bm[v >> 5], 1u << (v & 31)); }
 
 __device__ __forceinline__ void wave_lds_sync() {
@@ -818,45 +966,27 @@ __device__ __forceinline__ int wave_excl_scan(int v) {
     return x - v;
 }
 
-template <typename T>
-__device__ __forceinline__ float dot_row(const float (&qv)[4], const T *krow, int d) {
-    const int lane = lane_id();
-    float s = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int e = lane + 64 * i;
-        if (e < d) s = fmaf(qv[i], to_f32(krow[e]), s);
-    }
-    return wave_sum(s);
-}
-
 __device__ __forceinline__ void wave_compiler_fence() {
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-}
-
-// sum over the wave of per-lane counts c in [0, 2^NB): one ballot per bit
-template <int NB>
-__device__ __forceinline__ int wave_count(int c) {
-    int s = 0;
-#pragma unroll
-    for (int b = 0; b < NB; ++b) s += __popcll(wave_ballot((c >> b) & 1)) << b;
-    return s;
 }
 
 constexpr int SEL_CAP = 512;   // keys kept in LDS for the exact threshold search
 
 // Per-wave LDS of the select kernel, in 32-bit words:
-//   tab   [4*nch]     per 64-slot chunk: perm index of lane 0, flags, stream
-//                     slot of lane 0, key id of the overflow filler slots
+//   tab   [4*nch]     per 64-member chunk of a sorted list prefix: index of its
+//                     first member id, flags, score slot of its first member
+//   lst   [4*nlists]  per list: bucket start, size, first slot of the query's
+//                     own key (x2 + valid), overflow filler key
 //   bm    [words]     seen bitmap, later the merge bitmap
-//   kmask [2*nch]     per 64-slot chunk, the ballot of kept slots
+//   kmask [2*nch]     per chunk, the ballot of kept members
 //   ckey  [SEL_CAP]   kept keys >= the lower bound
-//   cval  [SEL_CAP]   key id of each compacted key (entries stay in stream order)
+//   cval  [SEL_CAP]   key id of each compacted key
 //   gsc   [64]        score keys of glob[0..G-1] and key 0 (empty buckets)
 //   gid   [64]        the ids glob[0..G-1], 0
 //   LSH mode: ekey/eval/eslot [kk] the selected entries
-__host__ __device__ inline int sel_lds_words(int nch, int words, int kk, bool lsh) {
-    return (4 * nch + words + 2 * nch + 2 * SEL_CAP + 128 + (lsh ? 3 * kk : 0) + 1) & ~1;
+__host__ __device__ inline int sel_lds_words(int nch, int words, int kk, bool lsh, int nlists) {
+    return (4 * nch + 4 * nlists + words + 2 * nch + 2 * SEL_CAP + 128 + (lsh ? 3 * kk : 0) + 1) &
+           ~1;
 }
 
 // Largest t (resolved down to bit lo_bit) such that at least kk of the wave's
@@ -883,36 +1013,10 @@ __device__ __forceinline__ uint32_t kth_search(const uint32_t (&k)[NK], int kk, 
     return thr;
 }
 
-__device__ __forceinline__ uint32_t wave_max_u(uint32_t v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const uint32_t y = (uint32_t)__shfl_xor((int)v, o, SSA_WAVE);
-        v = y > v ? y : v;
-    }
-    return v;
-}
-__device__ __forceinline__ uint32_t wave_min_u(uint32_t v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const uint32_t y = (uint32_t)__shfl_xor((int)v, o, SSA_WAVE);
-        v = y < v ? y : v;
-    }
-    return v;
-}
-
-struct SelList {
-    int st, sz, nv;
-    const int32_t *pr;
-};
-
-// chunk descriptor flags word: lanes in the list (bits 0-6) | real slots << 7
-// (bits 7-13) | flags (bits 14-17)
+// chunk descriptor flags word: members in the chunk (bits 0-6) | flags
 constexpr int CH_EMPTY = 1 << 14;      // the list's bucket is empty (glob ++ 0)
-constexpr int CH_FIRST = 1 << 15;      // first chunk of its list
-constexpr int CH_FULL = 1 << 16;       // 64 real slots (no fillers, not empty)
-constexpr int CH_NOFILL = 1 << 17;     // every slot of the chunk in the list is real
+constexpr int CH_FULL = 1 << 16;       // 64 members
 __device__ __forceinline__ int CH_LANES(int y) { return y & 127; }
-__device__ __forceinline__ int CH_REAL(int y) { return (y >> 7) & 127; }
 
 // FULL mode tail (merge_neighbors, sparse_attention.py:966-1089): `bm` holds
 // the selected LSH keys; adds the window (:368-376), the globals, key 0 when a
@@ -966,22 +1070,33 @@ __device__ void full_merge_emit(uint32_t *bm, const SelP &p, int n, int64_t row,
     }
 }
 
-// One wavefront per query row, streaming over the query's candidate stream in
-// the reference's concatenation order (round, id set, slot):
-//  pass 1  key id and score of every slot; first occurrence in stream order,
-//          valid or not (:884-890), by test-and-set of the key's bit in LDS (a
-//          wave's LDS atomics complete in program order); the kept slots of
-//          each 64-slot chunk as one ballot; the first SEL_CAP kept keys as a
-//          sample.  Slots of a chunk holding the same key (the query itself
-//          after causal substitution, repeated zeros of an empty bucket) carry
-//          the same score, so whichever one wins gives the same selection.
-//  bound   the kk-th largest sample key over the top 16 bits bounds the
-//          threshold from below (the sample is a subset of the stream);
-//  pass 2  the kept keys >= the bound are compacted (key, slot) into LDS;
+// One wavefront per query row.  The reference scans the query's candidate
+// stream (round, id set, slot) and keeps each key at its first occurrence,
+// valid or not (:884-890).  Real members of a list all carry their own score,
+// so which of their occurrences comes first does not change the selection:
+// only the query's own key (every future member becomes the query when
+// causal, :698-709) and the overflow filler keys (invalid slots, :691-696)
+// depend on the stream order, and both are settled up front:
+//  query   kept with its own score when its first occurrence (from the cut
+//          table, earliest list first) is valid;
+//  filler  a filler key whose first occurrence is a filler slot is marked seen
+//          (never kept); the real occurrences before it are found through the
+//          key's permutation position in each list's round.
+// What remains is order-free, so each list contributes only its members below
+// the query (causal; all otherwise) in ascending id order, whose scores the
+// rescore wrote contiguously, plus glob ++ 0 for an empty bucket:
+//  pass 1  dedup by test-and-set of the key's bit in LDS; the kept members of
+//          each 64-member chunk as one ballot; kept keys >= a lower bound
+//          compacted (key, id) into LDS;
+//  bound   the kk-th largest buffered key over the top 16 bits raises the
+//          lower bound whenever the buffer fills (the buffer is a subset of the
+//          stream);
 //  search  exact kk-th largest over the compacted keys (bitwise, early exit);
-//  emit    selected = key > thr, or key == thr for the first `need` in stream
-//          order; LSH mode writes them by descending score, FULL mode merges
-//          them with the window and the globals through a key bitmap.
+//  emit    selected = key > thr, or key == thr for the first `need`; rows where
+//          that choice matters (a tied kk-th key, equal selected keys in LSH
+//          mode) are handed to the exact replay.  LSH mode writes the selected
+//          keys by descending score, FULL mode merges them with the window and
+//          the globals through a key bitmap.
 template <typename T, bool LSH_MODE, bool CAUSAL>
 __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     extern __shared__ uint32_t sel_smem[];
@@ -991,11 +1106,13 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     const int64_t rloc = blk * SEL_WAVES + wid;
     if (rloc >= p.rows) return;
     const int lane = lane_id();
-    const int nch = p.nlists * p.CPL;
-    int4 *tab = (int4 *)(sel_smem + (int64_t)wid * sel_lds_words(nch, p.words, p.kk, LSH_MODE));
-    uint32_t *bm = (uint32_t *)(tab + nch);
+    const int nl = p.nlists;
+    const int nchmax = nl * p.CPL;
+    int4 *tab = (int4 *)(sel_smem + (int64_t)wid * sel_lds_words(nchmax, p.words, p.kk, LSH_MODE, nl));
+    int4 *lst = tab + nchmax;
+    uint32_t *bm = (uint32_t *)(lst + nl);
     uint64_t *kmask = (uint64_t *)(bm + p.words);
-    uint32_t *ckey = (uint32_t *)(kmask + nch);
+    uint32_t *ckey = (uint32_t *)(kmask + nchmax);
     uint32_t *cval = ckey + SEL_CAP;
     uint32_t *gsc = cval + SEL_CAP;
     int32_t *gid = (int32_t *)(gsc + 64);
@@ -1010,36 +1127,59 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     const int bk = b * p.Hkv + g;
     const int64_t row = (int64_t)bh * p.N + n;
     // scores the candidate lists do not carry (computed with the rescore's
-    // arithmetic, so equal keys get equal scores): the query's own key, which
-    // replaces future candidates, and the empty-bucket list glob ++ 0
+    // arithmetic, so equal keys get equal scores): the query's own key and the
+    // empty-bucket list glob ++ 0
     const float *arow = p.aux + rloc * p.NA;
     const uint32_t kself = CAUSAL ? score_key(arow[0]) : 0u;
-    const uint16_t *qids = p.qid + row * p.R * p.NS;
     const uint32_t *srow = p.S + ((int64_t)bhl * p.N + n) * p.Call;
     const int ng = min(p.G + 1, SSA_WAVE);
     for (int w = lane; w < p.words; w += SSA_WAVE) bm[w] = 0u;
+
+    // ---- chunk table of the sorted prefixes, one lane per list
+    int nch = 0;
     bool any_empty = false;
-    for (int ci = lane; ci < nch; ci += SSA_WAVE) {
-        const int list = ci / p.CPL, cj = ci - list * p.CPL;
-        const int u = qids[list];
-        const int64_t prow = (int64_t)bk * p.R + list / p.NS;
-        const int st = p.bstart[prow * p.NB + u];
-        const int sz = p.bsize[prow * p.NB + u];
-        const int c0 = cj * SSA_WAVE;
-        const int lanes = min(p.C - c0, SSA_WAVE);
-        const int realn = sz == 0 ? lanes : max(0, min(min(sz, p.C) - c0, SSA_WAVE));
-        int4 d4;
-        d4.x = (int)(prow * p.M) + min(st + c0, p.M - 1);   // perm index of lane 0 (clamped)
-        d4.y = lanes | (realn << 7) | (sz == 0 ? CH_EMPTY : 0) | (cj == 0 ? CH_FIRST : 0) |
-               (sz > 0 && realn == SSA_WAVE ? CH_FULL : 0) |
-               (sz > 0 && realn == lanes ? CH_NOFILL : 0);
-        d4.z = list * p.C + c0;
-        d4.w = p.perm[prow * p.M + p.M - 1];      // key of the overflow filler slots
-        tab[ci] = d4;
-        any_empty |= sz == 0;
+    bool nkeep = false;                // the query's own key is kept
+    bool nfound = !CAUSAL;
+    const int4 *crow = p.cut + rloc * nl;
+    for (int l0 = 0; l0 < nl; l0 += SSA_WAVE) {
+        const int list = l0 + lane;
+        const bool in = list < nl;
+        int4 ct = make_int4(0, 0, 0, 0);
+        int64_t prow = 0;
+        if (in) {
+            prow = (int64_t)bk * p.R + list / p.NS;
+            ct = crow[list];
+            lst[list] = make_int4(ct.x, ct.y, ct.w, p.perm[prow * p.M + p.M - 1]);
+        }
+        const int st = ct.x, sz = ct.y, cutoff = ct.z;
+        const int nc = !in ? 0 : (sz == 0 ? 1 : (cutoff + SSA_WAVE - 1) / SSA_WAVE);
+        const int at = nch + wave_excl_scan(nc);
+        for (int k = 0; k < nc; ++k) {
+            const int c0 = k * SSA_WAVE;
+            int4 d;
+            if (sz == 0) {
+                d = make_int4(0, min(p.C, ng) | CH_EMPTY, 0, 0);
+            } else {
+                const int lanes = min(cutoff - c0, SSA_WAVE);
+                d = make_int4((int)(prow * p.M) + st + c0, lanes | (lanes == SSA_WAVE ? CH_FULL : 0),
+                              list * p.C + c0, 0);
+            }
+            tab[at + k] = d;
+        }
+        nch += wave_sum_i(nc);
+        any_empty |= in && sz == 0;
+        if (!nfound) {
+            // earliest list holding the query's key: its first slot decides
+            const uint64_t fm = wave_ballot(in && (ct.w >> 1) < p.C);
+            if (fm != 0ull) {
+                const int ln = (int)(__ffsll((long long)fm) - 1);
+                nkeep = (__shfl(ct.w, ln, SSA_WAVE) & 1) != 0;
+                nfound = true;
+            }
+        }
     }
-    // glob ++ 0 (:711-737): ids and score keys, lane j holding entry j (also
-    // in LDS for the rare re-walk paths)
+    nch = __builtin_amdgcn_readfirstlane(nch);
+    // glob ++ 0 (:711-737): ids and score keys, lane j holding entry j
     int greg_id = 0;
     uint32_t greg_sc = 0u;
     if (wave_ballot(any_empty) && lane < ng) {
@@ -1050,72 +1190,86 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     }
     wave_lds_sync();
 
-    auto list_info = [&](int list) {
-        SelList L;
-        const int u = qids[list];
-        const int64_t prow = (int64_t)bk * p.R + list / p.NS;
-        L.sz = p.bsize[prow * p.NB + u];
-        L.st = p.bstart[prow * p.NB + u];
-        L.nv = min(L.sz, p.C);
-        L.pr = p.perm + prow * p.M;
-        return L;
-    };
-    // key id and score key of slot c of a list (c < C)
-    auto slot_kv = [&, n, kself](const SelList &L, int list, int c, int &v, uint32_t &kv,
-                                 bool &real) {
-        if (L.sz > 0) {
-            real = c < L.nv;
-            const int raw = L.pr[real ? L.st + c : p.M - 1];
-            v = (CAUSAL && raw > n) ? n : raw;
-            const uint32_t sk = srow[real ? (int64_t)list * p.C + c : 0];
-            kv = (CAUSAL && v == n) ? kself : sk;
-        } else {                                     // empty bucket: glob ++ 0
-            real = true;
-            const int j = c < ng - 1 ? c : ng - 1;
-            v = gid[j];
-            kv = gsc[j];
+    // ---- overflow fillers: list L (0 < size < C) holds its round's filler key
+    // f at slots size..C-1, invalid.  Lane pairs (L, L2 <= L) look for a real
+    // occurrence of f in list L2 or a filler of f in an earlier list; with
+    // neither, f's first occurrence is L's filler and f is never kept.
+    {
+        uint32_t *fhit = ckey;         // per list: f occurs earlier (scratch before pass 1)
+        for (int w = lane; w < (nl + 31) / 32; w += SSA_WAVE) fhit[w] = 0u;
+        wave_lds_sync();
+        const int np = nl * nl;
+        for (int p0 = 0; p0 < np; p0 += SSA_WAVE) {
+            const int pi = p0 + lane;
+            const int L = pi / nl, L2 = pi - L * nl;
+            if (pi < np && L2 <= L) {
+                const int4 a = lst[L];
+                const int v = a.w;
+                if (a.y > 0 && a.y < p.C && (!CAUSAL || v < n)) {
+                    const int4 c2 = lst[L2];
+                    bool hit;
+                    if (c2.y == 0) {                   // glob ++ 0, all valid
+                        hit = v == 0 && p.G < p.C;
+                        const int gl = min(p.G, p.C);
+                        for (int j = 0; j < gl; ++j) hit |= gid[j] == v;
+                    } else {
+                        hit = L2 < L && c2.y < p.C && c2.w == v;
+                        if (!hit) {
+                            const int pos = p.inv[((int64_t)bk * p.R + L2 / p.NS) * p.M + v];
+                            hit = pos >= c2.x && pos < c2.x + min(c2.y, p.C);
+                        }
+                    }
+                    if (hit) atomicOr(&fhit[L >> 5], 1u << (L & 31));
+                }
+            }
         }
-    };
+        wave_lds_sync();
+        for (int L = lane; L < nl; L += SSA_WAVE) {
+            const int4 a = lst[L];
+            if (a.y > 0 && a.y < p.C && (!CAUSAL || a.w < n) && !((fhit[L >> 5] >> (L & 31)) & 1u))
+                bm_set(bm, a.w);
+        }
+        wave_lds_sync();
+    }
 
-    // ---- pass 1: dedup, and the kept keys >= lo in stream order into LDS.  lo
-    // is a lower bound of the final threshold: whenever the buffer nears its
-    // capacity, lo is raised to (a 24-bit floor of) the kk-th largest key in the
-    // buffer -- a subset of the stream -- and the buffer is filtered in place.
+    // ---- pass 1: dedup, and the kept keys >= lo into LDS.  lo is a lower
+    // bound of the final threshold: whenever the buffer nears its capacity, lo
+    // is raised to (a 16-bit floor of) the kk-th largest key in the buffer --
+    // a subset of the stream -- and the buffer is filtered in place.
     const int kk = p.kk;
     const int fill = SEL_CAP / 2;      // checked once per group of 4 chunks (<= 256 keys)
     int nk = 0, cnt = 0;
     uint32_t lo = 0u;
     bool overflow = false;
-    bool nseen = false;                // the query's own key has occurred
+    if (nkeep) {
+        if (lane == 0) { ckey[0] = kself; cval[0] = (uint32_t)n; }
+        cnt = 1;
+    }
     int kml = 0, kmh = 0;              // keep masks of the current 64 chunks, lane = chunk
     // Chunks are processed PIPE at a time; the loads of the next group are
     // issued before the current group is deduplicated, so a wave always has
-    // one group of candidate ids and scores in flight.
-    // Loads are unconditional (inactive lanes read an in-range slot), so no
-    // register written by a pending load is rewritten before it lands.
+    // one group of member ids and scores in flight.  Loads are unconditional
+    // raw buffer loads (scalar chunk offset, constant lane offset): lanes past
+    // a chunk's members read in-range data or 0.
     constexpr int PIPE = 4;
-    // Raw buffer loads: the chunk's offset is a scalar, the lane's a constant,
-    // and lanes past the end of the list read in-range data or 0 (the
-    // descriptors bound the permutation and this query's score row).
     const __amdgpu_buffer_rsrc_t prs =
-        __builtin_amdgcn_make_buffer_rsrc((void *)p.perm, (short)0, p.perm_bytes, SSA_BUF_FLAGS);
+        __builtin_amdgcn_make_buffer_rsrc((void *)p.sid, (short)0, p.perm_bytes, SSA_BUF_FLAGS);
     const __amdgpu_buffer_rsrc_t srs =
         __builtin_amdgcn_make_buffer_rsrc((void *)srow, (short)0, (int)(p.Call * 4), SSA_BUF_FLAGS);
     const int lane4 = lane * 4;
-    int cy[PIPE], cw[PIPE], craw[PIPE];
+    int cy[PIPE], craw[PIPE];
     uint32_t csk[PIPE];
 #pragma unroll
     for (int u = 0; u < PIPE; ++u) {
         const int4 d = u < nch ? tab[u] : make_int4(0, 0, 0, 0);
         cy[u] = __builtin_amdgcn_readfirstlane(d.y);
-        cw[u] = __builtin_amdgcn_readfirstlane(d.w);
         const int x = __builtin_amdgcn_readfirstlane(d.x);
         const int z = __builtin_amdgcn_readfirstlane(d.z);
         craw[u] = __builtin_amdgcn_raw_buffer_load_b32(prs, lane4, x * 4, 0);
         csk[u] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(srs, lane4, z * 4, 0);
     }
     for (int ci0 = 0; ci0 < nch; ci0 += PIPE) {
-        int ny[PIPE], nw[PIPE], nraw[PIPE];
+        int ny[PIPE], nraw[PIPE];
         uint32_t nsk[PIPE];
         if (ci0 + PIPE < nch) {
 #pragma unroll
@@ -1123,7 +1277,6 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
                 const int ci = ci0 + PIPE + u;
                 const int4 d = ci < nch ? tab[ci] : make_int4(0, 0, 0, 0);
                 ny[u] = __builtin_amdgcn_readfirstlane(d.y);
-                nw[u] = __builtin_amdgcn_readfirstlane(d.w);
                 const int x = __builtin_amdgcn_readfirstlane(d.x);
                 const int z = __builtin_amdgcn_readfirstlane(d.z);
                 nraw[u] = __builtin_amdgcn_raw_buffer_load_b32(prs, lane4, x * 4, 0);
@@ -1135,95 +1288,36 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
         for (int u = 0; u < PIPE; ++u) {
             const int y = cy[u];
             const int ci = ci0 + u;
-            if ((y & CH_NOFILL) && (nseen || !CAUSAL)) {
-                // fast path: every slot of the chunk is real and the query's own
-                // key has already occurred -- no fillers, no first-occurrence logic
-                const uint64_t Min = (y & CH_FULL) ? ~0ull : lanes_mask(CH_LANES(y));
-                const int v = CAUSAL ? min(craw[u], n) : craw[u];
-                uint64_t Mvn = 0ull;
-                uint32_t kv = csk[u];
-                if (CAUSAL) {
-                    Mvn = wave_ballot(v == n);
-                    kv = in_mask(Mvn) ? kself : kv;
-                }
-                const uint64_t Mdo = Min & ~Mvn;
-                const uint32_t bit = 1u << (v & 31);
-                uint32_t old = 0u;
-                if (in_mask(Mdo)) old = atomicOr(&bm[v >> 5], bit);
-                const uint64_t km = Mdo & wave_ballot((old & bit) == 0u);
-                if (lane == (ci & 63)) {
-                    kml = (int)(uint32_t)km;
-                    kmh = (int)(uint32_t)(km >> 32);
-                }
-                const uint64_t am = km & wave_ballot(kv >= lo);
-                const int below = lanes_below(am);
-                const int na = __popcll(am);
-                if (roomy) {
-                    // every lane stores: appended keys at cnt.., the others just
-                    // past them (in range, never read)
-                    const int dst = in_mask(am) ? cnt + below : cnt + na + (lane - below);
-                    ckey[dst] = kv;
-                    cval[dst] = (uint32_t)v;
-                } else if (in_mask(am) && cnt + below < SEL_CAP) {
-                    ckey[cnt + below] = kv;
-                    cval[cnt + below] = (uint32_t)v;
-                }
-                cnt += na;
-                continue;
-            }
-            // general path: lane masks of the chunk (slots in the list, real slots)
-            const bool full = (y & CH_FULL) != 0;
-            const bool empty = (y & CH_EMPTY) != 0;
-            uint64_t Min = ~0ull, Mreal = ~0ull;
-            if (!full) {
-                Min = lanes_mask(CH_LANES(y));
-                Mreal = empty ? Min : lanes_mask(CH_REAL(y));
-            }
-            int v;
-            uint32_t kv;
-            if (!empty) {
-                const int raw = full ? craw[u] : (in_mask(Mreal) ? craw[u] : cw[u]);   // fillers: perm[M-1]
-                v = CAUSAL ? min(raw, n) : raw;                  // future keys -> the query
-                kv = csk[u];
-            } else {                                   // empty bucket: glob ++ 0
-                const int c = ((y & CH_FIRST) ? 0 : SSA_WAVE) + lane;
-                const int j = c < ng - 1 ? c : ng - 1;
-                v = __shfl(greg_id, j, SSA_WAVE);
-                kv = (uint32_t)__shfl((int)greg_sc, j, SSA_WAVE);
-            }
-            // The query's own key (every future candidate when causal) is
-            // tracked by a wave-uniform flag instead of the bitmap: its first
-            // occurrence in stream order decides, valid or not.
-            uint64_t Mvn = 0ull, Mkeepn = 0ull;
-            if (CAUSAL) {
-                Mvn = wave_ballot(v == n) & Min;
-                if (!empty) kv = in_mask(Mvn) ? kself : kv;
-                if (!nseen && Mvn != 0ull) {
-                    Mkeepn = (1ull << (__ffsll((long long)Mvn) - 1)) & Mreal;
-                    nseen = true;
-                }
+            uint64_t Min = (y & CH_FULL) ? ~0ull : lanes_mask(CH_LANES(y));
+            int v = craw[u];
+            uint32_t kv = csk[u];
+            if (y & CH_EMPTY) {                // glob ++ 0; the query's key is settled
+                v = greg_id;
+                kv = greg_sc;
+                if (CAUSAL) Min &= ~wave_ballot(v == n);
             }
             const uint32_t bit = 1u << (v & 31);
-            uint32_t *wp = &bm[v >> 5];
-            const uint64_t Mdo = Mreal & ~Mvn;
             uint32_t old = 0u;
-            if (in_mask(Mdo)) old = atomicOr(wp, bit);
-            if (!full) {
-                // fillers (all perm[M-1]) mark their key once, after the real slots
-                const uint64_t Mfill = Min & ~Mreal & ~Mvn;
-                if (Mfill != 0ull && in_mask(1ull << (__ffsll((long long)Mfill) - 1)))
-                    atomicOr(wp, bit);
-            }
-            const uint64_t km = (Mdo & wave_ballot((old & bit) == 0u)) | Mkeepn;
-            // keep masks, one chunk per lane, stored to LDS every 64 chunks
+            if (in_mask(Min)) old = atomicOr(&bm[v >> 5], bit);
+            const uint64_t km = Min & wave_ballot((old & bit) == 0u);
             if (lane == (ci & 63)) {
                 kml = (int)(uint32_t)km;
                 kmh = (int)(uint32_t)(km >> 32);
             }
             const uint64_t am = km & wave_ballot(kv >= lo);
-            const int pos = cnt + lanes_below(am);
-            if (in_mask(am) && pos < SEL_CAP) { ckey[pos] = kv; cval[pos] = (uint32_t)v; }
-            cnt += __popcll(am);
+            const int below = lanes_below(am);
+            const int na = __popcll(am);
+            if (roomy) {
+                // every lane stores: appended keys at cnt.., the others just
+                // past them (in range, never read)
+                const int dst = in_mask(am) ? cnt + below : cnt + na + (lane - below);
+                ckey[dst] = kv;
+                cval[dst] = (uint32_t)v;
+            } else if (in_mask(am) && cnt + below < SEL_CAP) {
+                ckey[cnt + below] = kv;
+                cval[cnt + below] = (uint32_t)v;
+            }
+            cnt += na;
         }
         if (((ci0 + PIPE) & 63) == 0 || ci0 + PIPE >= nch) {
             const int base = (ci0 + PIPE - 1) & ~63;
@@ -1272,35 +1366,39 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
 #pragma unroll
         for (int u = 0; u < PIPE; ++u) {
             cy[u] = ny[u];
-            cw[u] = nw[u];
             craw[u] = nraw[u];
             csk[u] = nsk[u];
         }
     }
     overflow = overflow || cnt > SEL_CAP;
     wave_lds_sync();
-    // kept slots in the whole stream
+    // kept keys in the whole stream
     {
         int c = 0;
         for (int ci = lane; ci < nch; ci += SSA_WAVE) c += __popcll(kmask[ci]);
-        nk = wave_sum_i(c);
+        nk = wave_sum_i(c) + (nkeep ? 1 : 0);
     }
 
-    // re-walk the kept slots of the stream in order (rare paths only)
+    // re-walk the kept keys (rare path: the buffer overflowed)
     auto walk_kept = [&](auto &&fn) {
-        for (int list = 0; list < p.nlists; ++list) {
-            const SelList L = list_info(list);
-            for (int cj = 0; cj < p.CPL; ++cj) {
-                const uint64_t km = kmask[list * p.CPL + cj];
-                if (km == 0ull) continue;
-                const int c = cj * SSA_WAVE + lane;
-                const bool keep = (km >> lane) & 1ull;
-                int v = 0;
-                uint32_t kv = 0u;
-                bool real = false;
-                if (keep) slot_kv(L, list, c, v, kv, real);
-                fn(keep, kv, v, list * p.C + c);
+        if (nkeep) fn(lane == 0, kself, n, 0);
+        for (int ci = 0; ci < nch; ++ci) {
+            const uint64_t km = kmask[ci];
+            if (km == 0ull) continue;
+            const int4 d = tab[ci];
+            const bool keep = (km >> lane) & 1ull;
+            int v = 0;
+            uint32_t kv = 0u;
+            if (keep) {
+                if (d.y & CH_EMPTY) {
+                    v = gid[lane];
+                    kv = gsc[lane];
+                } else {
+                    v = p.sid[d.x + lane];
+                    kv = srow[d.z + lane];
+                }
             }
+            fn(keep, kv, v, 1 + ci * SSA_WAVE + lane);
         }
     };
 
@@ -1746,7 +1844,11 @@ topk_replay_kernel(SelP p, int chunk, int W) {
                                 keep = !seen && lane == (int)(__ffsll((long long)nm) - 1);
                         }
                     }
-                    if (keep) sk = (p.causal && v == n) ? kself : srow[j0 + lane];
+                    // scores are stored by the member's rank in the sorted list
+                    if (keep)
+                        sk = (p.causal && v == n)
+                                 ? kself
+                                 : srow[(int64_t)list * p.C + p.rnk[prow * p.M + st + c]];
                 } else {
                     // empty bucket: glob ++ 0, all valid; duplicates resolved in slot order
                     const int jg = c < ng - 1 ? c : ng - 1;
@@ -1814,8 +1916,8 @@ topk_replay_kernel(SelP p, int chunk, int W) {
 int supported_d(int d) { return d >= 4 && d <= 256 && (d & (d - 1)) == 0; }
 
 struct Layout {
-    int64_t kid, qid, perm, bstart, bsize, sorttmp, cnt, off, cur, qlist, tiles, ntiles, tcnt,
-        kbase, S,
+    int64_t kid, qid, perm, bstart, bsize, sorttmp, sid, rnk, smin, inv, cut, cnt, off, cur,
+        qlist, tiles, ntiles, tcnt, kbase, S,
         tie_list, tie_count, aux, total;
 };
 
@@ -1833,6 +1935,11 @@ Layout plan(const Dims &D) {
     L.bstart = take(D.BK * D.R * D.NB * 4);
     L.bsize = take(D.BK * D.R * D.NB * 4);
     L.sorttmp = take(ssa_sort_tmp_bytes((int)(D.BK * D.R), D.M));
+    L.sid = take(D.BK * D.R * D.M * 4);
+    L.rnk = take(D.BK * D.R * D.M * 4);
+    L.smin = take(D.BK * D.R * D.M * 4);
+    L.inv = take(D.BK * D.R * D.M * 4);
+    L.cut = take(nbh * D.N * D.nlists * 16);
     L.cnt = take(ninst * D.NB * 4);
     L.off = take(ninst * D.NB * 4);
     L.cur = take(ninst * ceil_div(D.N, 256) * D.NB * 4);   // per-block counts / bases
@@ -1858,6 +1965,7 @@ int make_dims(const ssa_graph_args *a, Dims &D) {
     SSA_CHECK_ARG(a->Hq % a->Hkv == 0, "build_graph: Hq %% Hkv != 0");
     SSA_CHECK_ARG(a->P >= 1 && a->P <= 12 && a->P <= a->max_p, "build_graph: P=%d", a->P);
     SSA_CHECK_ARG(a->R >= 1 && a->C >= 1 && a->top_k >= 1 && a->T >= 0, "build_graph: R/C/top_k/T");
+    SSA_CHECK_ARG(a->C <= (1 << 24), "build_graph: C=%d above 2^24", a->C);
     SSA_CHECK_ARG(a->G >= 0 && a->G <= 63, "build_graph: G=%d outside 0..63", a->G);
     SSA_CHECK_ARG(a->rand_proj || (a->q_proj && a->k_proj), "build_graph: no hyperplanes");
     SSA_CHECK_ARG(a->q.ptr && a->k.ptr, "build_graph: null q/k");
@@ -2044,7 +2152,7 @@ int rescore_dispatch(int d, const RsP &rp, int64_t grid, hipStream_t st) {
 template <typename T, bool LSH, bool CAUSAL>
 int launch_select(const SelP &sp, hipStream_t st) {
     const size_t lds =
-        (size_t)SEL_WAVES * sel_lds_words(sp.nlists * sp.CPL, sp.words, sp.kk, LSH) * 4;
+        (size_t)SEL_WAVES * sel_lds_words(sp.nlists * sp.CPL, sp.words, sp.kk, LSH, sp.nlists) * 4;
     if (lds > SSA_LDS_BYTES) {
         ssa_set_error("build_graph: select needs %zu bytes of LDS", lds);
         return SSA_E_UNSUP;
@@ -2123,6 +2231,25 @@ int build_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *w
                                 (int32_t *)(ws + L.perm), (int32_t *)(ws + L.bstart),
                                 (int32_t *)(ws + L.bsize), (uint16_t *)(ws + L.sorttmp), st);
     if (rc) return rc;
+    {
+        LsP lp{};
+        lp.perm = (const int32_t *)(ws + L.perm);
+        lp.bstart = (const int32_t *)(ws + L.bstart);
+        lp.bsize = (const int32_t *)(ws + L.bsize);
+        lp.sid = (int32_t *)(ws + L.sid);
+        lp.rnk = (int32_t *)(ws + L.rnk);
+        lp.smin = (int32_t *)(ws + L.smin);
+        lp.inv = (int32_t *)(ws + L.inv);
+        lp.M = D.M; lp.NB = D.NB; lp.C = D.C;
+        int p2 = 1;
+        while (p2 < std::min(D.C, D.M)) p2 <<= 1;
+        const size_t lds = (size_t)p2 * 4;
+        SSA_CHECK_HIP(hipFuncSetAttribute((const void *)list_sort_kernel,
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        hipLaunchKernelGGL(list_sort_kernel, dim3((unsigned)(D.BK * D.R * D.NB)), dim3(256), lds, st,
+                           lp);
+        SSA_CHECK_LAUNCH();
+    }
     for (int64_t bh0 = 0; bh0 < D.BH; bh0 += D.nbh_chunk) {
         const int nbh = (int)((D.BH - bh0) < D.nbh_chunk ? (D.BH - bh0) : D.nbh_chunk);
         const int ninst = nbh * D.R * D.NS;
@@ -2156,7 +2283,7 @@ int build_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *w
 
         RsP rp{};
         rp.tiles = qp.tiles; rp.ntiles = qp.ntiles; rp.qlist = qp.qlist;
-        rp.perm = (const int32_t *)(ws + L.perm);
+        rp.sid = (const int32_t *)(ws + L.sid);
         rp.bstart = (const int32_t *)(ws + L.bstart);
         rp.bsize = (const int32_t *)(ws + L.bsize);
         rp.q = a->q.ptr; rp.k = a->k.ptr;
@@ -2165,6 +2292,7 @@ int build_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *w
         rp.S = (uint32_t *)(ws + L.S);
         rp.N = D.N; rp.M = D.M; rp.R = D.R; rp.NS = D.NS; rp.NB = D.NB; rp.C = D.C;
         rp.Hq = D.Hq; rp.Hkv = D.Hkv; rp.rep = D.rep; rp.bh0 = (int)bh0; rp.Call = D.Call;
+        rp.causal = a->causal ? 1 : 0;
         rp.vec4 = (D.C % 4 == 0) ? 1 : 0;
         const int64_t grid = 8 * ceil_div((int64_t)ninst * (ceil_div(D.N, TQ) + D.NB), 8);
         rc = rescore_dispatch<T>(D.d, rp, grid, st);
@@ -2180,8 +2308,24 @@ int build_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *w
         rc = aux_dispatch<T>(D.d, rescore_uses_mfma<T>(D.d, rp), ap, st);
         if (rc) return rc;
 
+        CutP cp{};
+        cp.qid = qp.qid;
+        cp.perm = (const int32_t *)(ws + L.perm);
+        cp.bstart = rp.bstart; cp.bsize = rp.bsize; cp.sid = rp.sid;
+        cp.smin = (const int32_t *)(ws + L.smin);
+        cp.glob = a->glob;
+        cp.cut = (int4 *)(ws + L.cut);
+        cp.N = D.N; cp.M = D.M; cp.R = D.R; cp.NS = D.NS; cp.NB = D.NB; cp.C = D.C;
+        cp.Hq = D.Hq; cp.Hkv = D.Hkv; cp.rep = D.rep; cp.bh0 = (int)bh0; cp.G = D.G;
+        cp.causal = a->causal ? 1 : 0; cp.nlists = D.nlists; cp.rows = (int64_t)nbh * D.N;
+        hipLaunchKernelGGL(cut_kernel, dim3((unsigned)ceil_div(cp.rows * D.nlists, 256)), dim3(256),
+                           0, st, cp);
+        SSA_CHECK_LAUNCH();
+
         SelP sp{};
-        sp.qid = qp.qid; sp.perm = rp.perm; sp.bstart = rp.bstart; sp.bsize = rp.bsize;
+        sp.qid = qp.qid; sp.perm = cp.perm; sp.bstart = rp.bstart; sp.bsize = rp.bsize;
+        sp.sid = rp.sid; sp.rnk = (const int32_t *)(ws + L.rnk);
+        sp.inv = (const int32_t *)(ws + L.inv); sp.cut = cp.cut;
         sp.S = rp.S; sp.q = a->q.ptr; sp.k = a->k.ptr;
         sp.qsb = a->q.sb; sp.qsh = a->q.sh; sp.qsn = a->q.sn;
         sp.ksb = a->k.sb; sp.ksh = a->k.sh; sp.ksn = a->k.sn;
