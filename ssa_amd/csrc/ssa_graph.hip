@@ -974,19 +974,42 @@ constexpr int SEL_CAP = 512;   // keys kept in LDS for the exact threshold searc
 
 // Per-wave LDS of the select kernel, in 32-bit words:
 //   tab   [4*nch]     per 64-member chunk of a sorted list prefix: index of its
-//                     first member id, flags, score slot of its first member
+//                     first member id, lane mask (low), score slot of its first
+//                     member, lane mask (high)
 //   lst   [4*nlists]  per list: bucket start, size, first slot of the query's
-//                     own key (x2 + valid), overflow filler key
+//                     own key (x2 + valid), overflow filler key (after the
+//                     filler rule: the key if it is marked seen, else -1)
 //   bm    [words]     seen bitmap, later the merge bitmap
-//   kmask [2*nch]     per chunk, the ballot of kept members
-//   ckey  [SEL_CAP]   kept keys >= the lower bound
-//   cval  [SEL_CAP]   key id of each compacted key
+//   ckey  [SEL_CAP+64] kept keys >= the lower bound; the last 64 entries take
+//                     the stores of lanes that append nothing
+//   cval  [SEL_CAP+64] key id of each compacted key
 //   gsc   [64]        score keys of glob[0..G-1] and key 0 (empty buckets)
 //   gid   [64]        the ids glob[0..G-1], 0
 //   LSH mode: ekey/eval/eslot [kk] the selected entries
+constexpr int SEL_BUF = SEL_CAP + 64;
 __host__ __device__ inline int sel_lds_words(int nch, int words, int kk, bool lsh, int nlists) {
-    return (4 * nch + 4 * nlists + words + 2 * nch + 2 * SEL_CAP + 128 + (lsh ? 3 * kk : 0) + 1) &
-           ~1;
+    return (4 * nch + 4 * nlists + words + 2 * SEL_BUF + 128 + (lsh ? 3 * kk : 0) + 1) & ~1;
+}
+
+// Dedup one chunk of members (lanes in Min) against the seen bitmap, count the
+// kept ones, and append the kept keys >= lo to the compacted buffer.  Every
+// lane stores: lanes that append nothing (or would pass the capacity) write
+// to their own slot past SEL_CAP, which is never read.
+__device__ __forceinline__ void sel_absorb(uint32_t *bm, uint32_t *ckey, uint32_t *cval,
+                                           uint64_t Min, int v, uint32_t kv, uint32_t lo,
+                                           int &cnt, int &nkept) {
+    const int lane = lane_id();
+    const uint32_t bit = 1u << (v & 31);
+    uint32_t old = 0u;
+    if (in_mask(Min)) old = atomicOr(&bm[v >> 5], bit);
+    const uint64_t km = Min & wave_ballot((old & bit) == 0u);
+    nkept += __popcll(km);
+    const uint64_t am = km & wave_ballot(kv >= lo);
+    const int pos = cnt + lanes_below(am);
+    const int dst = (in_mask(am) & (pos < SEL_CAP)) ? pos : SEL_CAP + lane;
+    ckey[dst] = kv;
+    cval[dst] = (uint32_t)v;
+    cnt += __popcll(am);
 }
 
 // Largest t (resolved down to bit lo_bit) such that at least kk of the wave's
@@ -1012,11 +1035,6 @@ __device__ __forceinline__ uint32_t kth_search(const uint32_t (&k)[NK], int kk, 
     }
     return thr;
 }
-
-// chunk descriptor flags word: members in the chunk (bits 0-6) | flags
-constexpr int CH_EMPTY = 1 << 14;      // the list's bucket is empty (glob ++ 0)
-constexpr int CH_FULL = 1 << 16;       // 64 members
-__device__ __forceinline__ int CH_LANES(int y) { return y & 127; }
 
 // FULL mode tail (merge_neighbors, sparse_attention.py:966-1089): `bm` holds
 // the selected LSH keys; adds the window (:368-376), the globals, key 0 when a
@@ -1111,10 +1129,9 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     int4 *tab = (int4 *)(sel_smem + (int64_t)wid * sel_lds_words(nchmax, p.words, p.kk, LSH_MODE, nl));
     int4 *lst = tab + nchmax;
     uint32_t *bm = (uint32_t *)(lst + nl);
-    uint64_t *kmask = (uint64_t *)(bm + p.words);
-    uint32_t *ckey = (uint32_t *)(kmask + nchmax);
-    uint32_t *cval = ckey + SEL_CAP;
-    uint32_t *gsc = cval + SEL_CAP;
+    uint32_t *ckey = bm + p.words;
+    uint32_t *cval = ckey + SEL_BUF;
+    uint32_t *gsc = cval + SEL_BUF;
     int32_t *gid = (int32_t *)(gsc + 64);
     uint32_t *ekey = (uint32_t *)(gid + 64);
     uint32_t *eval = ekey + p.kk;
@@ -1137,7 +1154,7 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
 
     // ---- chunk table of the sorted prefixes, one lane per list
     int nch = 0;
-    bool any_empty = false;
+    bool any_empty = false;            // some bucket is empty: glob ++ 0 (same for all)
     bool nkeep = false;                // the query's own key is kept
     bool nfound = !CAUSAL;
     const int4 *crow = p.cut + rloc * nl;
@@ -1152,28 +1169,22 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
             lst[list] = make_int4(ct.x, ct.y, ct.w, p.perm[prow * p.M + p.M - 1]);
         }
         const int st = ct.x, sz = ct.y, cutoff = ct.z;
-        const int nc = !in ? 0 : (sz == 0 ? 1 : (cutoff + SSA_WAVE - 1) / SSA_WAVE);
+        const int nc = (in && sz > 0) ? (cutoff + SSA_WAVE - 1) / SSA_WAVE : 0;
         const int at = nch + wave_excl_scan(nc);
         for (int k = 0; k < nc; ++k) {
             const int c0 = k * SSA_WAVE;
-            int4 d;
-            if (sz == 0) {
-                d = make_int4(0, min(p.C, ng) | CH_EMPTY, 0, 0);
-            } else {
-                const int lanes = min(cutoff - c0, SSA_WAVE);
-                d = make_int4((int)(prow * p.M) + st + c0, lanes | (lanes == SSA_WAVE ? CH_FULL : 0),
-                              list * p.C + c0, 0);
-            }
-            tab[at + k] = d;
+            const uint64_t m = lanes_mask(cutoff - c0);
+            tab[at + k] = make_int4((int)(prow * p.M) + st + c0, (int)(uint32_t)m, list * p.C + c0,
+                                    (int)(uint32_t)(m >> 32));
         }
         nch += wave_sum_i(nc);
-        any_empty |= in && sz == 0;
+        any_empty = any_empty || wave_ballot(in && sz == 0) != 0ull;
         if (!nfound) {
             // earliest list holding the query's key: its first slot decides
             const uint64_t fm = wave_ballot(in && (ct.w >> 1) < p.C);
             if (fm != 0ull) {
-                const int ln = (int)(__ffsll((long long)fm) - 1);
-                nkeep = (__shfl(ct.w, ln, SSA_WAVE) & 1) != 0;
+                const uint64_t vm = wave_ballot(in && (ct.w & 1));
+                nkeep = ((vm >> (__ffsll((long long)fm) - 1)) & 1ull) != 0ull;
                 nfound = true;
             }
         }
@@ -1182,7 +1193,7 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     // glob ++ 0 (:711-737): ids and score keys, lane j holding entry j
     int greg_id = 0;
     uint32_t greg_sc = 0u;
-    if (wave_ballot(any_empty) && lane < ng) {
+    if (any_empty && lane < ng) {
         greg_sc = score_key(arow[1 + lane]);
         greg_id = lane < p.G ? (int)p.glob[lane] : 0;
         gsc[lane] = greg_sc;
@@ -1226,8 +1237,10 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
         wave_lds_sync();
         for (int L = lane; L < nl; L += SSA_WAVE) {
             const int4 a = lst[L];
-            if (a.y > 0 && a.y < p.C && (!CAUSAL || a.w < n) && !((fhit[L >> 5] >> (L & 31)) & 1u))
-                bm_set(bm, a.w);
+            const bool mark = a.y > 0 && a.y < p.C && (!CAUSAL || a.w < n) &&
+                              !((fhit[L >> 5] >> (L & 31)) & 1u);
+            if (mark) bm_set(bm, a.w);
+            lst[L].w = mark ? a.w : -1;
         }
         wave_lds_sync();
     }
@@ -1238,14 +1251,18 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     // a subset of the stream -- and the buffer is filtered in place.
     const int kk = p.kk;
     const int fill = SEL_CAP / 2;      // checked once per group of 4 chunks (<= 256 keys)
-    int nk = 0, cnt = 0;
+    int nkept = nkeep ? 1 : 0, cnt = 0;
     uint32_t lo = 0u;
     bool overflow = false;
     if (nkeep) {
         if (lane == 0) { ckey[0] = kself; cval[0] = (uint32_t)n; }
         cnt = 1;
     }
-    int kml = 0, kmh = 0;              // keep masks of the current 64 chunks, lane = chunk
+    if (any_empty) {                   // glob ++ 0; the query's own key is settled
+        uint64_t Min = lanes_mask(min(p.C, ng));
+        if (CAUSAL) Min &= ~wave_ballot(greg_id == n);
+        sel_absorb(bm, ckey, cval, Min, greg_id, greg_sc, lo, cnt, nkept);
+    }
     // Chunks are processed PIPE at a time; the loads of the next group are
     // issued before the current group is deduplicated, so a wave always has
     // one group of member ids and scores in flight.  Loads are unconditional
@@ -1257,73 +1274,39 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     const __amdgpu_buffer_rsrc_t srs =
         __builtin_amdgcn_make_buffer_rsrc((void *)srow, (short)0, (int)(p.Call * 4), SSA_BUF_FLAGS);
     const int lane4 = lane * 4;
-    int cy[PIPE], craw[PIPE];
+    uint64_t cm[PIPE];
+    int craw[PIPE];
     uint32_t csk[PIPE];
 #pragma unroll
     for (int u = 0; u < PIPE; ++u) {
         const int4 d = u < nch ? tab[u] : make_int4(0, 0, 0, 0);
-        cy[u] = __builtin_amdgcn_readfirstlane(d.y);
+        cm[u] = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane(d.w) << 32) |
+                (uint32_t)__builtin_amdgcn_readfirstlane(d.y);
         const int x = __builtin_amdgcn_readfirstlane(d.x);
         const int z = __builtin_amdgcn_readfirstlane(d.z);
         craw[u] = __builtin_amdgcn_raw_buffer_load_b32(prs, lane4, x * 4, 0);
         csk[u] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(srs, lane4, z * 4, 0);
     }
     for (int ci0 = 0; ci0 < nch; ci0 += PIPE) {
-        int ny[PIPE], nraw[PIPE];
+        uint64_t nm[PIPE];
+        int nraw[PIPE];
         uint32_t nsk[PIPE];
         if (ci0 + PIPE < nch) {
 #pragma unroll
             for (int u = 0; u < PIPE; ++u) {
                 const int ci = ci0 + PIPE + u;
                 const int4 d = ci < nch ? tab[ci] : make_int4(0, 0, 0, 0);
-                ny[u] = __builtin_amdgcn_readfirstlane(d.y);
+                nm[u] = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane(d.w) << 32) |
+                        (uint32_t)__builtin_amdgcn_readfirstlane(d.y);
                 const int x = __builtin_amdgcn_readfirstlane(d.x);
                 const int z = __builtin_amdgcn_readfirstlane(d.z);
                 nraw[u] = __builtin_amdgcn_raw_buffer_load_b32(prs, lane4, x * 4, 0);
                 nsk[u] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(srs, lane4, z * 4, 0);
             }
         }
-        const bool roomy = cnt + PIPE * SSA_WAVE <= SEL_CAP;   // no capacity check needed
 #pragma unroll
-        for (int u = 0; u < PIPE; ++u) {
-            const int y = cy[u];
-            const int ci = ci0 + u;
-            uint64_t Min = (y & CH_FULL) ? ~0ull : lanes_mask(CH_LANES(y));
-            int v = craw[u];
-            uint32_t kv = csk[u];
-            if (y & CH_EMPTY) {                // glob ++ 0; the query's key is settled
-                v = greg_id;
-                kv = greg_sc;
-                if (CAUSAL) Min &= ~wave_ballot(v == n);
-            }
-            const uint32_t bit = 1u << (v & 31);
-            uint32_t old = 0u;
-            if (in_mask(Min)) old = atomicOr(&bm[v >> 5], bit);
-            const uint64_t km = Min & wave_ballot((old & bit) == 0u);
-            if (lane == (ci & 63)) {
-                kml = (int)(uint32_t)km;
-                kmh = (int)(uint32_t)(km >> 32);
-            }
-            const uint64_t am = km & wave_ballot(kv >= lo);
-            const int below = lanes_below(am);
-            const int na = __popcll(am);
-            if (roomy) {
-                // every lane stores: appended keys at cnt.., the others just
-                // past them (in range, never read)
-                const int dst = in_mask(am) ? cnt + below : cnt + na + (lane - below);
-                ckey[dst] = kv;
-                cval[dst] = (uint32_t)v;
-            } else if (in_mask(am) && cnt + below < SEL_CAP) {
-                ckey[cnt + below] = kv;
-                cval[cnt + below] = (uint32_t)v;
-            }
-            cnt += na;
-        }
-        if (((ci0 + PIPE) & 63) == 0 || ci0 + PIPE >= nch) {
-            const int base = (ci0 + PIPE - 1) & ~63;
-            if (base + lane < nch)
-                kmask[base + lane] = ((uint64_t)(uint32_t)kmh << 32) | (uint32_t)kml;
-        }
+        for (int u = 0; u < PIPE; ++u)
+            sel_absorb(bm, ckey, cval, cm[u], craw[u], csk[u], lo, cnt, nkept);
         if (cnt >= fill && cnt >= kk && !overflow) {
             wave_lds_sync();
             const int m0 = cnt < SEL_CAP ? cnt : SEL_CAP;
@@ -1365,40 +1348,48 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
         }
 #pragma unroll
         for (int u = 0; u < PIPE; ++u) {
-            cy[u] = ny[u];
+            cm[u] = nm[u];
             craw[u] = nraw[u];
             csk[u] = nsk[u];
         }
     }
     overflow = overflow || cnt > SEL_CAP;
     wave_lds_sync();
-    // kept keys in the whole stream
-    {
-        int c = 0;
-        for (int ci = lane; ci < nch; ci += SSA_WAVE) c += __popcll(kmask[ci]);
-        nk = wave_sum_i(c) + (nkeep ? 1 : 0);
-    }
+    const int nk = nkept;
 
-    // re-walk the kept keys (rare path: the buffer overflowed)
+    // re-walk the kept keys (rare path: the buffer overflowed, so it is free
+    // to hold a fresh seen bitmap)
     auto walk_kept = [&](auto &&fn) {
+        uint32_t *bm2 = ckey;
+        wave_lds_sync();
+        for (int w = lane; w < p.words; w += SSA_WAVE) bm2[w] = 0u;
+        wave_lds_sync();
+        for (int L = lane; L < nl; L += SSA_WAVE)
+            if (lst[L].w >= 0) bm_set(bm2, lst[L].w);
+        wave_lds_sync();
         if (nkeep) fn(lane == 0, kself, n, 0);
+        auto walk_chunk = [&](uint64_t Min, int v, uint32_t kv, int slot) {
+            const uint32_t bit = 1u << (v & 31);
+            uint32_t old = 0u;
+            if (in_mask(Min)) old = atomicOr(&bm2[v >> 5], bit);
+            fn(in_mask(Min) && !(old & bit), kv, v, slot);
+        };
+        if (any_empty) {
+            uint64_t Min = lanes_mask(min(p.C, ng));
+            if (CAUSAL) Min &= ~wave_ballot(greg_id == n);
+            walk_chunk(Min, greg_id, greg_sc, 1 + lane);
+        }
         for (int ci = 0; ci < nch; ++ci) {
-            const uint64_t km = kmask[ci];
-            if (km == 0ull) continue;
             const int4 d = tab[ci];
-            const bool keep = (km >> lane) & 1ull;
+            const uint64_t Min = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane(d.w) << 32) |
+                                 (uint32_t)__builtin_amdgcn_readfirstlane(d.y);
             int v = 0;
             uint32_t kv = 0u;
-            if (keep) {
-                if (d.y & CH_EMPTY) {
-                    v = gid[lane];
-                    kv = gsc[lane];
-                } else {
-                    v = p.sid[d.x + lane];
-                    kv = srow[d.z + lane];
-                }
+            if (in_mask(Min)) {
+                v = p.sid[__builtin_amdgcn_readfirstlane(d.x) + lane];
+                kv = srow[__builtin_amdgcn_readfirstlane(d.z) + lane];
             }
-            fn(keep, kv, v, 1 + ci * SSA_WAVE + lane);
+            walk_chunk(Min, v, kv, 65 + ci * SSA_WAVE + lane);
         }
     };
 
