@@ -204,6 +204,198 @@ apply_fwd_kernel(ApplyP p) {
     }
 }
 
+// ---------------------------------------------------------------- 16-bit forward
+// Packed 16-bit arithmetic for bf16 / fp16 models whose attention weights are
+// rounded to the value dtype (fp32_attn_weights off):
+//  * q.k: four v_dot2 (pairs of 16-bit products, fp32 accumulate) per lane,
+//    then a sum over the LPR lanes of a row by DPP row permutations;
+//  * P.V: the weights are exact in the value dtype, so two neighbours j, j'
+//    go through one v_dot2 per element: {p_j, p_j'} . {v_j[e], v_j'[e]},
+//    with the element pairs gathered by v_perm;
+//  * rows are addressed by 32-bit byte offsets from a wave-uniform base.
+template <typename T> struct Dot2;
+template <> struct Dot2<bf16_t> {
+    typedef __bf16 __attribute__((ext_vector_type(2))) v2;
+    static __device__ __forceinline__ float dot(uint32_t a, uint32_t b, float c) {
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, a), __builtin_bit_cast(v2, b),
+                                               c, false);
+    }
+    // two bf16-exact fp32 values as a pair (a low, b high): their upper halves
+    static __device__ __forceinline__ uint32_t pack(float a, float b) {
+        return __builtin_amdgcn_perm(__float_as_uint(b), __float_as_uint(a), 0x07060302u);
+    }
+    static __device__ __forceinline__ uint32_t bits(float v) { return f32_to_bf16_bits(v); }
+};
+template <> struct Dot2<f16_t> {
+    typedef _Float16 __attribute__((ext_vector_type(2))) v2;
+    static __device__ __forceinline__ float dot(uint32_t a, uint32_t b, float c) {
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(v2, a), __builtin_bit_cast(v2, b), c,
+                                      false);
+    }
+    static __device__ __forceinline__ uint32_t pack(float a, float b) {
+        const v2 h = {(_Float16)a, (_Float16)b};       // exact: both are fp16 values
+        return __builtin_bit_cast(uint32_t, h);
+    }
+    static __device__ __forceinline__ uint32_t bits(float v) {
+        const _Float16 h = (_Float16)v;
+        return (uint32_t)__builtin_bit_cast(uint16_t, h);
+    }
+};
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float v) {
+    // every source lane of these patterns exists: old (0) is never used, and
+    // an identity old lets the move fold into the add as a DPP operand
+    return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF,
+                                                          false));
+}
+
+// sum over the L lanes of each aligned group (L a power of two <= 32); every
+// lane of the group gets the sum
+template <int L>
+__device__ __forceinline__ float group_sum(float v) {
+    if constexpr (L >= 16) v = dpp_add<0x140>(v);   // row mirror
+    if constexpr (L >= 8) v = dpp_add<0x141>(v);    // row half mirror
+    if constexpr (L >= 2) v = dpp_add<0xB1>(v);     // quad perm [1,0,3,2]
+    if constexpr (L >= 4) v = dpp_add<0x4E>(v);     // quad perm [2,3,0,1]
+    if constexpr (L >= 32) v += __shfl_xor(v, 16, SSA_WAVE);
+    return v;
+}
+
+template <typename T, int D, int U>
+__global__ void __launch_bounds__(WAVES * SSA_WAVE)
+apply_fwd16_kernel(ApplyP p) {
+    constexpr int LPR = D / 8;                 // lanes per row, 16 bytes each
+    constexpr int RPI = SSA_WAVE / LPR;        // rows per wave load
+    static_assert(sizeof(T) == 2 && D % 8 == 0 && LPR <= 32 && U % 2 == 0, "16-bit path");
+    extern __shared__ float smem[];
+    const int64_t blk = xcd_logical_block(blockIdx.x, p.nblocks);
+    if (blk >= p.nblocks) return;
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / SSA_WAVE);
+    const int64_t row = blk * WAVES + wid;
+    if (row >= p.rows) return;
+    const int lane = lane_id();
+    const int sub = lane / LPR, li = lane % LPR;
+    int32_t *ix = reinterpret_cast<int32_t *>(smem) + (int64_t)wid * 2 * p.K;   // key ids, -1 = masked
+    float *sc = reinterpret_cast<float *>(ix + p.K);                          // scores, then p
+
+    const int n = (int)(row % p.N);
+    const int64_t bh = row / p.N;
+    const int h = (int)(bh % p.Hq);
+    const int b = (int)(bh / p.Hq);
+    const int g = h / p.rep;
+    const T *qrow = (const T *)p.q + b * p.qsb + h * p.qsh + (int64_t)n * p.qsn;
+    const char *kb = (const char *)((const T *)p.k + b * p.ksb + g * p.ksh);
+    const char *vb = (const char *)((const T *)p.v + b * p.vsb + g * p.vsh);
+    const uint32_t krb = (uint32_t)(p.ksn * 2), vrb = (uint32_t)(p.vsn * 2);   // row bytes < 2^24
+    const uint32_t lio = (uint32_t)li * 16u;
+    const int64_t *nb = p.nb + row * p.K;
+    const uint8_t *va = p.valid ? p.valid + row * p.K : nullptr;
+
+    for (int j = lane; j < p.K; j += SSA_WAVE) {
+        const int64_t x = nb[j];
+        const bool o = (va ? va[j] != 0 : true) && x >= 0 && x < p.M;
+        ix[j] = o ? (int)x : -1;
+    }
+    const uint4 q4 = *reinterpret_cast<const uint4 *>(qrow + li * 8);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // ---- scores
+    for (int j0 = 0; j0 < p.K; j0 += RPI * U) {
+        int xi[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int j = j0 + u * RPI + sub;
+            xi[u] = j < p.K ? ix[j] : -1;
+        }
+        uint4 kv[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            kv[u] = *reinterpret_cast<const uint4 *>(
+                kb + (__umul24((uint32_t)max(xi[u], 0), krb) + lio));
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            float part = Dot2<T>::dot(q4.x, kv[u].x, 0.f);
+            part = Dot2<T>::dot(q4.y, kv[u].y, part);
+            part = Dot2<T>::dot(q4.z, kv[u].z, part);
+            part = Dot2<T>::dot(q4.w, kv[u].w, part);
+            part = group_sum<LPR>(part);
+            const int j = j0 + u * RPI + sub;
+            if (li == 0 && j < p.K) sc[j] = xi[u] >= 0 ? part * p.scale : -INFINITY;
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // ---- fp32 softmax; p rounded to the value dtype (inverted dropout on p)
+    float m = -INFINITY;
+    for (int j = lane; j < p.K; j += SSA_WAVE) m = fmaxf(m, sc[j]);
+    m = wave_max(m);
+    float l = 0.f;
+    for (int j = lane; j < p.K; j += SSA_WAVE) l += expf(sc[j] - m);
+    l = wave_sum(l);
+    const float inv = 1.f / l;
+    for (int j = lane; j < p.K; j += SSA_WAVE) {
+        float w = Cvt<T>::round(expf(sc[j] - m) * inv);
+        if (p.drop_p > 0.f)
+            w = (drop_uniform(p.seed, row, j) < p.drop_p) ? 0.f : Cvt<T>::round(w * p.drop_scale);
+        sc[j] = w;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // ---- P.V, neighbours in pairs
+    float acc[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = 0.f;
+    for (int j0 = 0; j0 < p.K; j0 += RPI * U) {
+        int xi[U];
+        float pj[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int j = j0 + u * RPI + sub;
+            const bool in = j < p.K;
+            xi[u] = in ? ix[j] : -1;
+            pj[u] = in ? sc[j] : 0.f;
+        }
+        uint4 vv[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            vv[u] = *reinterpret_cast<const uint4 *>(
+                vb + (__umul24((uint32_t)max(xi[u], 0), vrb) + lio));
+#pragma unroll
+        for (int u = 0; u < U; u += 2) {
+            const uint32_t pp = Dot2<T>::pack(pj[u], pj[u + 1]);
+            const uint32_t a[4] = {vv[u].x, vv[u].y, vv[u].z, vv[u].w};
+            const uint32_t c[4] = {vv[u + 1].x, vv[u + 1].y, vv[u + 1].z, vv[u + 1].w};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                acc[2 * r] = Dot2<T>::dot(pp, __builtin_amdgcn_perm(c[r], a[r], 0x05040100u),
+                                          acc[2 * r]);
+                acc[2 * r + 1] = Dot2<T>::dot(pp, __builtin_amdgcn_perm(c[r], a[r], 0x07060302u),
+                                              acc[2 * r + 1]);
+            }
+        }
+    }
+#pragma unroll
+    for (int o = LPR; o < SSA_WAVE; o <<= 1)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] += __shfl_xor(acc[e], o, SSA_WAVE);
+    if (sub == 0) {
+        T *orow = (T *)p.out + b * p.osb + h * p.osh + (int64_t)n * p.osn + li * 8;
+        uint4 o4;
+        o4.x = Dot2<T>::bits(acc[0]) | (Dot2<T>::bits(acc[1]) << 16);
+        o4.y = Dot2<T>::bits(acc[2]) | (Dot2<T>::bits(acc[3]) << 16);
+        o4.z = Dot2<T>::bits(acc[4]) | (Dot2<T>::bits(acc[5]) << 16);
+        o4.w = Dot2<T>::bits(acc[6]) | (Dot2<T>::bits(acc[7]) << 16);
+        *reinterpret_cast<uint4 *>(orow) = o4;
+    }
+}
+
 // Backward: recompute p, then dp = dO.v, ds = p (dp - sum p dp), draw = ds*scale,
 // dq = sum draw k (direct store), dk += draw q, dv += p' dO (fp32 atomics).
 template <typename T, int D>
@@ -318,6 +510,22 @@ apply_bwd_kernel(ApplyP p) {
     }
 }
 
+// The 16-bit path needs weights in the value dtype, 16-byte aligned rows and
+// byte offsets of every K / V row (and q row slice) within 32 bits.
+bool fwd16_ok(const ApplyP &p, int elem, int D) {
+    const int64_t v = 16 / elem;
+    const bool aligned = ((uintptr_t)p.q % 16 == 0) && ((uintptr_t)p.k % 16 == 0) &&
+                         ((uintptr_t)p.v % 16 == 0) && ((uintptr_t)p.out % 16 == 0) &&
+                         p.qsb % v == 0 && p.qsh % v == 0 && p.qsn % v == 0 && p.ksb % v == 0 &&
+                         p.ksh % v == 0 && p.ksn % v == 0 && p.vsb % v == 0 && p.vsh % v == 0 &&
+                         p.vsn % v == 0 && p.osb % v == 0 && p.osh % v == 0 && p.osn % v == 0;
+    const int64_t lim = (int64_t)1 << 24;
+    const bool small = p.ksn * elem < lim && p.vsn * elem < lim &&
+                       ((int64_t)p.M * p.ksn + D) * elem < ((int64_t)1 << 31) &&
+                       ((int64_t)p.M * p.vsn + D) * elem < ((int64_t)1 << 31);
+    return !p.fp32w && aligned && small;
+}
+
 template <typename T, int D>
 int launch_apply(const ApplyP &p, hipStream_t st, bool bwd) {
     const int64_t grid = 8 * ceil_div(p.nblocks, 8);
@@ -328,6 +536,14 @@ int launch_apply(const ApplyP &p, hipStream_t st, bool bwd) {
     } else {
         const size_t lds = (size_t)WAVES * 2 * p.K * sizeof(float);
         constexpr int U = (Geo<T, D>::RPI >= 8) ? 4 : 8;
+        if constexpr (sizeof(T) == 2 && D >= 8) {
+            if (fwd16_ok(p, (int)sizeof(T), D)) {
+                hipLaunchKernelGGL((apply_fwd16_kernel<T, D, U>), dim3((unsigned)grid),
+                                   dim3(WAVES * SSA_WAVE), lds, st, p);
+                SSA_CHECK_LAUNCH();
+                return SSA_OK;
+            }
+        }
         hipLaunchKernelGGL((apply_fwd_kernel<T, D, U>), dim3((unsigned)grid),
                            dim3(WAVES * SSA_WAVE), lds, st, p);
     }

@@ -92,22 +92,26 @@ __device__ __forceinline__ int wave_sum_i(int v) {
     return v;
 }
 
-__device__ __forceinline__ uint32_t wave_max_u(uint32_t v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const uint32_t y = (uint32_t)__shfl_xor((int)v, o, SSA_WAVE);
-        v = y > v ? y : v;
-    }
-    return v;
+// wave-wide max / min of an unsigned value through DPP row operations
+// (quad swaps, row mirrors, row broadcasts 15 and 31), read from lane 63: a
+// wave-uniform result with no LDS traffic.  Every lane must be active.
+// The moved operand's "old" value is the identity of the operation (lanes of
+// rows outside a broadcast's row mask see it), which also lets the compiler
+// fold the move into the max / min as a DPP operand.
+template <bool MAX>
+__device__ __forceinline__ uint32_t wave_reduce_dpp(uint32_t v) {
+    constexpr int id = MAX ? 0 : -1;
+    auto op = [](uint32_t a, uint32_t b) { return MAX ? (a > b ? a : b) : (a < b ? a : b); };
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v, 0xB1, 0xF, 0xF, false));
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v, 0x4E, 0xF, 0xF, false));
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v, 0x141, 0xF, 0xF, false));
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v, 0x140, 0xF, 0xF, false));
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v, 0x142, 0xA, 0xF, false));
+    v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(id, (int)v, 0x143, 0xC, 0xF, false));
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, SSA_WAVE - 1);
 }
-__device__ __forceinline__ uint32_t wave_min_u(uint32_t v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const uint32_t y = (uint32_t)__shfl_xor((int)v, o, SSA_WAVE);
-        v = y < v ? y : v;
-    }
-    return v;
-}
+__device__ __forceinline__ uint32_t wave_max_u(uint32_t v) { return wave_reduce_dpp<true>(v); }
+__device__ __forceinline__ uint32_t wave_min_u(uint32_t v) { return wave_reduce_dpp<false>(v); }
 
 // ballot over the 64-lane wave
 __device__ __forceinline__ uint64_t wave_ballot(bool p) { return __ballot(p); }

@@ -778,8 +778,9 @@ __global__ void __launch_bounds__(256) list_sort_kernel(LsP p) {
 // in the list -- a member at or past the query (causal substitution, :698-709),
 // an overflow filler (invalid) when the filler key is at or past the query, or
 // an entry of glob ++ 0 for an empty bucket (:711-737) -- as
-// {bucket start, size, cutoff, first slot * 2 + (that slot is valid)}; first
-// slot C: none.
+// {row offset of the bucket (kv-head/round row * M + start), size | filler
+// key << 16, cutoff | start << 16, first slot * 2 + (that slot is valid)};
+// first slot C: none.  Sizes, cutoffs, starts and keys stay below 2^16.
 struct CutP {
     const uint16_t *qid;
     const int32_t *perm, *bstart, *bsize, *sid, *smin;
@@ -802,6 +803,7 @@ __global__ void __launch_bounds__(256) cut_kernel(CutP p) {
     const int64_t prow = ((int64_t)b * p.Hkv + g) * p.R + list / p.NS;
     const int st = p.bstart[prow * p.NB + u];
     const int sz = p.bsize[prow * p.NB + u];
+    const int f = p.perm[prow * p.M + p.M - 1];   // key of the overflow filler slots
     int cutoff = 0, first = p.C, real = 0;
     if (sz == 0) {
         if (p.causal) {
@@ -822,7 +824,6 @@ __global__ void __launch_bounds__(256) cut_kernel(CutP p) {
             }
             cutoff = lo;
             const int a = cutoff < nv ? p.smin[prow * p.M + st + cutoff] : p.C;
-            const int f = p.perm[prow * p.M + p.M - 1];
             const int fb = (sz < p.C && f >= n) ? sz : p.C;
             first = min(a, fb);
             real = a < fb ? 1 : 0;
@@ -830,7 +831,8 @@ __global__ void __launch_bounds__(256) cut_kernel(CutP p) {
             cutoff = nv;
         }
     }
-    p.cut[x] = make_int4(st, sz, cutoff, first * 2 + real);
+    p.cut[x] = make_int4((int)(prow * p.M) + st, sz | (f << 16), cutoff | (st << 16),
+                         first * 2 + real);
 }
 
 // ------------------------------------------------------------------ extra scores
@@ -928,7 +930,8 @@ struct SelP {
     const uint16_t *qid;
     const int32_t *perm, *bstart, *bsize;
     const int32_t *sid, *rnk, *inv;   // sorted list members, their ranks, key positions
-    const int4 *cut;       // per (row, list): {start, size, cutoff, first slot * 2 + valid}
+    const int4 *cut;       // per (row, list): bucket offset, size/filler, cutoff/start, first
+    uint32_t nl_magic;     // ceil(2^32 / nlists): pair index / nlists as a high product
     const uint32_t *S;     // score keys (score_key), row-major (rows, Call)
     const void *q, *k;
     int64_t qsb, qsh, qsn, ksb, ksh, ksn;
@@ -976,9 +979,9 @@ constexpr int SEL_CAP = 512;   // keys kept in LDS for the exact threshold searc
 //   tab   [4*nch]     per 64-member chunk of a sorted list prefix: index of its
 //                     first member id, lane mask (low), score slot of its first
 //                     member, lane mask (high)
-//   lst   [4*nlists]  per list: bucket start, size, first slot of the query's
-//                     own key (x2 + valid), overflow filler key (after the
-//                     filler rule: the key if it is marked seen, else -1)
+//   lst   [4*nlists]  per list: bucket start, size, offset of its kv-head/round
+//                     row, overflow filler key (after the filler rule: the key
+//                     if it is marked seen, else -1)
 //   bm    [words]     seen bitmap, later the merge bitmap
 //   ckey  [SEL_CAP+64] kept keys >= the lower bound; the last 64 entries take
 //                     the stores of lanes that append nothing
@@ -987,8 +990,11 @@ constexpr int SEL_CAP = 512;   // keys kept in LDS for the exact threshold searc
 //   gid   [64]        the ids glob[0..G-1], 0
 //   LSH mode: ekey/eval/eslot [kk] the selected entries
 constexpr int SEL_BUF = SEL_CAP + 64;
+constexpr int SEL_PIPE = 4;            // chunks per group in pass 1
+__host__ __device__ inline int sel_tab_entries(int nch) { return nch + 2 * SEL_PIPE; }
 __host__ __device__ inline int sel_lds_words(int nch, int words, int kk, bool lsh, int nlists) {
-    return (4 * nch + 4 * nlists + words + 2 * SEL_BUF + 128 + (lsh ? 3 * kk : 0) + 1) & ~1;
+    return (4 * sel_tab_entries(nch) + 4 * nlists + words + 2 * SEL_BUF + 128 +
+            (lsh ? 3 * kk : 0) + 1) & ~1;
 }
 
 // Dedup one chunk of members (lanes in Min) against the seen bitmap, count the
@@ -1036,19 +1042,48 @@ __device__ __forceinline__ uint32_t kth_search(const uint32_t (&k)[NK], int kk, 
     return thr;
 }
 
+__device__ __forceinline__ int wave_incl_max(int v) {
+    const int lane = lane_id();
+#pragma unroll
+    for (int o = 1; o < SSA_WAVE; o <<= 1) {
+        const int y = __shfl_up(v, o, SSA_WAVE);
+        if (lane >= o) v = max(v, y);
+    }
+    return v;
+}
+
+// index of the k-th (0-based) set bit of b (k < popcount(b))
+__device__ __forceinline__ int nth_set_bit(uint32_t b, int k) {
+    int pos = 0;
+#pragma unroll
+    for (int sh = 16; sh >= 1; sh >>= 1) {
+        const int c = __popc(b & ((1u << sh) - 1u));
+        const bool up = k >= c;
+        k = up ? k - c : k;
+        b = up ? b >> sh : b;
+        pos = up ? pos + sh : pos;
+    }
+    return pos;
+}
+
 // FULL mode tail (merge_neighbors, sparse_attention.py:966-1089): `bm` holds
 // the selected LSH keys; adds the window (:368-376), the globals, key 0 when a
 // -inf slot at or past G falls back to it (:948-957), removes the query itself
 // and writes [self] ++ the ascending union, zero-padded and marked invalid.
-__device__ void full_merge_emit(uint32_t *bm, const SelP &p, int n, int64_t row, int f) {
+// scr: LDS scratch of scr_cap ints (free at this point).
+__device__ void full_merge_emit(uint32_t *bm, const SelP &p, int n, int64_t row, int f,
+                                int32_t *scr, int scr_cap) {
     const int lane = lane_id();
     const int kk = p.kk;
     if (!p.cross) {
-        for (int o = -p.window + lane; o <= p.window; o += SSA_WAVE) {
-            int x = n + o;
-            if (p.causal && o > 0) x = n;
-            x = x < 0 ? 0 : (x > p.M - 1 ? p.M - 1 : x);
-            bm_set(bm, x);
+        // the window {clamp(n + o) : |o| <= window, o <= 0 if causal} is the
+        // range [a, e]: one mask per word
+        const int a = min(max(n - p.window, 0), p.M - 1);
+        const int e = min(max(p.causal ? n : n + p.window, 0), p.M - 1);
+        for (int w = (a >> 5) + lane; w <= (e >> 5); w += SSA_WAVE) {
+            const int lo = max(a - 32 * w, 0), hi = min(e - 32 * w, 31);
+            const uint32_t m = (hi == 31 ? 0xffffffffu : ((2u << hi) - 1u)) & ~((1u << lo) - 1u);
+            atomicOr(&bm[w], m);
         }
     }
     for (int j = lane; j < p.G; j += SSA_WAVE) bm_set(bm, (int)p.glob[j]);
@@ -1065,19 +1100,48 @@ __device__ void full_merge_emit(uint32_t *bm, const SelP &p, int n, int64_t row,
     const int w0 = lane * wpl;
     int cntb = 0;
     for (int w = w0; w < w0 + wpl && w < p.words; ++w) cntb += __popc(bm[w]);
-    int pos = wave_excl_scan(cntb);
+    const int pos = wave_excl_scan(cntb);
     const int total = wave_sum_i(cntb);
-    for (int w = w0; w < w0 + wpl && w < p.words && pos < ks; ++w) {
-        uint32_t word = bm[w];
-        while (word && pos < ks) {
-            const int bitp = __ffs(word) - 1;
-            word &= word - 1;
-            orow[self + pos] = (int64_t)(w * 32 + bitp);
-            vrow[self + pos] = 1;
-            ++pos;
+    const int filled = total < ks ? total : ks;
+    if (ks <= scr_cap) {
+        // output slot t holds the (t - s)-th key of the word whose first key
+        // is at slot s, the last word start at or before t: mark word starts,
+        // then a running max over the slots finds s
+        for (int t = lane; t < ks; t += SSA_WAVE) scr[t] = -1;
+        wave_lds_sync();
+        int q = pos;
+        for (int w = w0; w < w0 + wpl && w < p.words; ++w) {
+            const int c = __popc(bm[w]);
+            if (c > 0 && q < ks) scr[q] = w;
+            q += c;
+        }
+        wave_lds_sync();
+        int carry = -1;
+        for (int t0 = 0; t0 < filled; t0 += SSA_WAVE) {
+            const int t = t0 + lane;
+            const bool in = t < filled;
+            int s = wave_incl_max((in && scr[t] >= 0) ? t : -1);
+            s = max(s, carry);
+            carry = __builtin_amdgcn_readlane(s, SSA_WAVE - 1);
+            if (in) {
+                const int w = scr[s];
+                orow[self + t] = (int64_t)(w * 32 + nth_set_bit(bm[w], t - s));
+                vrow[self + t] = 1;
+            }
+        }
+    } else {
+        int q = pos;
+        for (int w = w0; w < w0 + wpl && w < p.words && q < ks; ++w) {
+            uint32_t word = bm[w];
+            while (word && q < ks) {
+                const int bitp = __ffs(word) - 1;
+                word &= word - 1;
+                orow[self + q] = (int64_t)(w * 32 + bitp);
+                vrow[self + q] = 1;
+                ++q;
+            }
         }
     }
-    const int filled = total < ks ? total : ks;
     for (int i = self + filled + lane; i < p.Kout; i += SSA_WAVE) {
         orow[i] = 0;
         vrow[i] = 0;
@@ -1086,6 +1150,37 @@ __device__ void full_merge_emit(uint32_t *bm, const SelP &p, int n, int64_t row,
         orow[0] = n;
         vrow[0] = 1;
     }
+}
+
+// Exact kk-th largest of the cnt compacted keys (all >= lo): the threshold
+// thr, how many keys equal to it are needed (need), and whether more equal
+// keys than needed exist (btie).  NK keys per lane cover cnt.
+template <int NK>
+__device__ __forceinline__ void sel_threshold(const uint32_t *ckey, int cnt, int kk, uint32_t lo,
+                                              uint32_t &thr, int &need, bool &btie) {
+    const int lane = lane_id();
+    uint32_t cv[NK];
+#pragma unroll
+    for (int i = 0; i < NK; ++i) cv[i] = ckey[lane + SSA_WAVE * i];
+#pragma unroll
+    for (int i = 0; i < NK; ++i) cv[i] = lane + SSA_WAVE * i < cnt ? cv[i] : 0u;
+    uint32_t mx = 0u, mn = 0xffffffffu;
+#pragma unroll
+    for (int i = 0; i < NK; ++i) {
+        mx = cv[i] > mx ? cv[i] : mx;
+        mn = (cv[i] != 0u && cv[i] < mn) ? cv[i] : mn;
+    }
+    mx = wave_max_u(mx);
+    mn = wave_min_u(mn);
+    thr = kth_search(cv, kk, lo > mn ? lo : mn, mx, 0);
+    int ge = 0, gt = 0;
+#pragma unroll
+    for (int i = 0; i < NK; ++i) {
+        ge += __popcll(wave_ballot(cv[i] >= thr));
+        gt += __popcll(wave_ballot(cv[i] > thr));
+    }
+    need = kk - gt;
+    btie = ge - gt > need;
 }
 
 // One wavefront per query row.  The reference scans the query's candidate
@@ -1127,7 +1222,7 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     const int nl = p.nlists;
     const int nchmax = nl * p.CPL;
     int4 *tab = (int4 *)(sel_smem + (int64_t)wid * sel_lds_words(nchmax, p.words, p.kk, LSH_MODE, nl));
-    int4 *lst = tab + nchmax;
+    int4 *lst = tab + sel_tab_entries(nchmax);
     uint32_t *bm = (uint32_t *)(lst + nl);
     uint32_t *ckey = bm + p.words;
     uint32_t *cval = ckey + SEL_BUF;
@@ -1137,18 +1232,14 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     uint32_t *eval = ekey + p.kk;
     uint32_t *eslot = eval + p.kk;
 
-    const int n = (int)(rloc % p.N);
-    const int bhl = (int)(rloc / p.N);
-    const int bh = p.bh0 + bhl;
-    const int b = bh / p.Hq, h = bh % p.Hq, g = h / p.rep;
-    const int bk = b * p.Hkv + g;
-    const int64_t row = (int64_t)bh * p.N + n;
+    const int n = (int)((uint32_t)rloc % (uint32_t)p.N);     // rows of a chunk < 2^31
+    const int64_t row = (int64_t)p.bh0 * p.N + rloc;
     // scores the candidate lists do not carry (computed with the rescore's
     // arithmetic, so equal keys get equal scores): the query's own key and the
     // empty-bucket list glob ++ 0
     const float *arow = p.aux + rloc * p.NA;
     const uint32_t kself = CAUSAL ? score_key(arow[0]) : 0u;
-    const uint32_t *srow = p.S + ((int64_t)bhl * p.N + n) * p.Call;
+    const uint32_t *srow = p.S + rloc * p.Call;
     const int ng = min(p.G + 1, SSA_WAVE);
     for (int w = lane; w < p.words; w += SSA_WAVE) bm[w] = 0u;
 
@@ -1161,20 +1252,15 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     for (int l0 = 0; l0 < nl; l0 += SSA_WAVE) {
         const int list = l0 + lane;
         const bool in = list < nl;
-        int4 ct = make_int4(0, 0, 0, 0);
-        int64_t prow = 0;
-        if (in) {
-            prow = (int64_t)bk * p.R + list / p.NS;
-            ct = crow[list];
-            lst[list] = make_int4(ct.x, ct.y, ct.w, p.perm[prow * p.M + p.M - 1]);
-        }
-        const int st = ct.x, sz = ct.y, cutoff = ct.z;
+        const int4 ct = in ? crow[list] : make_int4(0, 0, 0, 0);
+        const int sz = ct.y & 0xffff, cutoff = ct.z & 0xffff, st = ct.z >> 16;
+        if (in) lst[list] = make_int4(st, sz, ct.x - st, ct.y >> 16);
         const int nc = (in && sz > 0) ? (cutoff + SSA_WAVE - 1) / SSA_WAVE : 0;
         const int at = nch + wave_excl_scan(nc);
         for (int k = 0; k < nc; ++k) {
             const int c0 = k * SSA_WAVE;
             const uint64_t m = lanes_mask(cutoff - c0);
-            tab[at + k] = make_int4((int)(prow * p.M) + st + c0, (int)(uint32_t)m, list * p.C + c0,
+            tab[at + k] = make_int4(ct.x + c0, (int)(uint32_t)m, list * p.C + c0,
                                     (int)(uint32_t)(m >> 32));
         }
         nch += wave_sum_i(nc);
@@ -1190,6 +1276,7 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
         }
     }
     nch = __builtin_amdgcn_readfirstlane(nch);
+    if (lane < 2 * SEL_PIPE) tab[nch + lane] = make_int4(0, 0, 0, 0);   // empty tail chunks
     // glob ++ 0 (:711-737): ids and score keys, lane j holding entry j
     int greg_id = 0;
     uint32_t greg_sc = 0u;
@@ -1212,7 +1299,8 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
         const int np = nl * nl;
         for (int p0 = 0; p0 < np; p0 += SSA_WAVE) {
             const int pi = p0 + lane;
-            const int L = pi / nl, L2 = pi - L * nl;
+            const int L = nl <= 1024 ? (int)__umulhi((uint32_t)pi, p.nl_magic) : pi / nl;
+            const int L2 = pi - L * nl;
             if (pi < np && L2 <= L) {
                 const int4 a = lst[L];
                 const int v = a.w;
@@ -1226,7 +1314,7 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
                     } else {
                         hit = L2 < L && c2.y < p.C && c2.w == v;
                         if (!hit) {
-                            const int pos = p.inv[((int64_t)bk * p.R + L2 / p.NS) * p.M + v];
+                            const int pos = p.inv[c2.z + v];
                             hit = pos >= c2.x && pos < c2.x + min(c2.y, p.C);
                         }
                     }
@@ -1265,57 +1353,66 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     }
     // Chunks are processed PIPE at a time; the loads of the next group are
     // issued before the current group is deduplicated, so a wave always has
-    // one group of member ids and scores in flight.  Loads are unconditional
+    // one group of member ids and scores in flight (two register sets, A and
+    // B, alternate so that no loaded value is copied).  Loads are unconditional
     // raw buffer loads (scalar chunk offset, constant lane offset): lanes past
-    // a chunk's members read in-range data or 0.
-    constexpr int PIPE = 4;
+    // a chunk's members read in-range data or 0.  The group's descriptor
+    // reads, and its bitmap test-and-sets, are issued back to back: LDS
+    // operations of a wave complete in order, so each chunk still sees the
+    // bits the chunks before it set.
+    constexpr int PIPE = SEL_PIPE;
     const __amdgpu_buffer_rsrc_t prs =
         __builtin_amdgcn_make_buffer_rsrc((void *)p.sid, (short)0, p.perm_bytes, SSA_BUF_FLAGS);
     const __amdgpu_buffer_rsrc_t srs =
         __builtin_amdgcn_make_buffer_rsrc((void *)srow, (short)0, (int)(p.Call * 4), SSA_BUF_FLAGS);
     const int lane4 = lane * 4;
-    uint64_t cm[PIPE];
-    int craw[PIPE];
-    uint32_t csk[PIPE];
+    uint64_t mA[PIPE], mB[PIPE];
+    int rA[PIPE], rB[PIPE];
+    uint32_t sA[PIPE], sB[PIPE];
+    auto fetch = [&](int ci0, uint64_t (&m)[PIPE], int (&raw)[PIPE], uint32_t (&sk)[PIPE])
+        __attribute__((always_inline)) {
+        int4 d[PIPE];
 #pragma unroll
-    for (int u = 0; u < PIPE; ++u) {
-        const int4 d = u < nch ? tab[u] : make_int4(0, 0, 0, 0);
-        cm[u] = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane(d.w) << 32) |
-                (uint32_t)__builtin_amdgcn_readfirstlane(d.y);
-        const int x = __builtin_amdgcn_readfirstlane(d.x);
-        const int z = __builtin_amdgcn_readfirstlane(d.z);
-        craw[u] = __builtin_amdgcn_raw_buffer_load_b32(prs, lane4, x * 4, 0);
-        csk[u] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(srs, lane4, z * 4, 0);
-    }
-    for (int ci0 = 0; ci0 < nch; ci0 += PIPE) {
-        uint64_t nm[PIPE];
-        int nraw[PIPE];
-        uint32_t nsk[PIPE];
-        if (ci0 + PIPE < nch) {
+        for (int u = 0; u < PIPE; ++u) d[u] = tab[ci0 + u];     // the tail holds empty chunks
 #pragma unroll
-            for (int u = 0; u < PIPE; ++u) {
-                const int ci = ci0 + PIPE + u;
-                const int4 d = ci < nch ? tab[ci] : make_int4(0, 0, 0, 0);
-                nm[u] = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane(d.w) << 32) |
-                        (uint32_t)__builtin_amdgcn_readfirstlane(d.y);
-                const int x = __builtin_amdgcn_readfirstlane(d.x);
-                const int z = __builtin_amdgcn_readfirstlane(d.z);
-                nraw[u] = __builtin_amdgcn_raw_buffer_load_b32(prs, lane4, x * 4, 0);
-                nsk[u] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(srs, lane4, z * 4, 0);
-            }
+        for (int u = 0; u < PIPE; ++u) {
+            m[u] = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane(d[u].w) << 32) |
+                   (uint32_t)__builtin_amdgcn_readfirstlane(d[u].y);
+            const int x = __builtin_amdgcn_readfirstlane(d[u].x);
+            const int z = __builtin_amdgcn_readfirstlane(d[u].z);
+            raw[u] = __builtin_amdgcn_raw_buffer_load_b32(prs, lane4, x * 4, 0);
+            sk[u] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(srs, lane4, z * 4, 0);
+        }
+    };
+    auto absorb = [&](const uint64_t (&cm)[PIPE], const int (&craw)[PIPE],
+                      const uint32_t (&csk)[PIPE]) __attribute__((always_inline)) {
+        uint32_t old[PIPE], bit[PIPE];
+#pragma unroll
+        for (int u = 0; u < PIPE; ++u) {
+            bit[u] = 1u << (craw[u] & 31);
+            old[u] = 0u;
+            if (in_mask(cm[u])) old[u] = atomicOr(&bm[craw[u] >> 5], bit[u]);
         }
 #pragma unroll
-        for (int u = 0; u < PIPE; ++u)
-            sel_absorb(bm, ckey, cval, cm[u], craw[u], csk[u], lo, cnt, nkept);
+        for (int u = 0; u < PIPE; ++u) {
+            const uint64_t km = cm[u] & wave_ballot((old[u] & bit[u]) == 0u);
+            nkept += __popcll(km);
+            const uint64_t am = km & wave_ballot(csk[u] >= lo);
+            const int pos = cnt + lanes_below(am);
+            const int dst = (in_mask(am) & (pos < SEL_CAP)) ? pos : SEL_CAP + lane;
+            ckey[dst] = csk[u];
+            cval[dst] = (uint32_t)craw[u];
+            cnt += __popcll(am);
+        }
         if (cnt >= fill && cnt >= kk && !overflow) {
             wave_lds_sync();
             const int m0 = cnt < SEL_CAP ? cnt : SEL_CAP;
             uint32_t sv[SEL_CAP / SSA_WAVE];
 #pragma unroll
-            for (int i = 0; i < SEL_CAP / SSA_WAVE; ++i) {
-                const int e = lane + SSA_WAVE * i;
-                sv[i] = e < m0 ? ckey[e] : 0u;
-            }
+            for (int i = 0; i < SEL_CAP / SSA_WAVE; ++i) sv[i] = ckey[lane + SSA_WAVE * i];
+#pragma unroll
+            for (int i = 0; i < SEL_CAP / SSA_WAVE; ++i)
+                sv[i] = lane + SSA_WAVE * i < m0 ? sv[i] : 0u;   // slots past the count are stale
             uint32_t mx = 0u, mn = 0xffffffffu;
 #pragma unroll
             for (int i = 0; i < SEL_CAP / SSA_WAVE; ++i) {
@@ -1329,10 +1426,7 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
             lo = nlo > lo ? nlo : lo;
             uint32_t sl[SEL_CAP / SSA_WAVE];
 #pragma unroll
-            for (int i = 0; i < SEL_CAP / SSA_WAVE; ++i) {
-                const int e = lane + SSA_WAVE * i;
-                sl[i] = e < m0 ? cval[e] : 0u;
-            }
+            for (int i = 0; i < SEL_CAP / SSA_WAVE; ++i) sl[i] = cval[lane + SSA_WAVE * i];
             wave_lds_sync();
             int nc = 0;
 #pragma unroll
@@ -1346,12 +1440,17 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
             cnt = nc;
             wave_lds_sync();
         }
-#pragma unroll
-        for (int u = 0; u < PIPE; ++u) {
-            cm[u] = nm[u];
-            craw[u] = nraw[u];
-            csk[u] = nsk[u];
-        }
+    };
+    // Fetches past the last chunk are unconditional (they read the empty tail
+    // chunks), so every path into a group sees the same loads in flight and
+    // waits only for its own.
+    fetch(0, mA, rA, sA);
+    for (int ci0 = 0; ci0 < nch; ci0 += 2 * PIPE) {
+        fetch(ci0 + PIPE, mB, rB, sB);
+        absorb(mA, rA, sA);
+        if (ci0 + PIPE >= nch) break;
+        fetch(ci0 + 2 * PIPE, mA, rA, sA);
+        absorb(mB, rB, sB);
     }
     overflow = overflow || cnt > SEL_CAP;
     wave_lds_sync();
@@ -1400,29 +1499,13 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     const bool compacted = !overflow;  // every key >= the threshold is in ckey
     if (nk > kk) {
         if (compacted) {
-            uint32_t cv[SEL_CAP / SSA_WAVE];
-#pragma unroll
-            for (int i = 0; i < SEL_CAP / SSA_WAVE; ++i) {
-                const int e = lane + SSA_WAVE * i;
-                cv[i] = e < cnt ? ckey[e] : 0u;
-            }
-            uint32_t mx = 0u, mn = 0xffffffffu;
-#pragma unroll
-            for (int i = 0; i < SEL_CAP / SSA_WAVE; ++i) {
-                mx = cv[i] > mx ? cv[i] : mx;
-                mn = (cv[i] != 0u && cv[i] < mn) ? cv[i] : mn;
-            }
-            mx = wave_max_u(mx);
-            mn = wave_min_u(mn);
-            thr = kth_search(cv, kk, lo > mn ? lo : mn, mx, 0);
-            int ge = 0, gt = 0;
-#pragma unroll
-            for (int i = 0; i < SEL_CAP / SSA_WAVE; ++i) {
-                ge += __popcll(wave_ballot(cv[i] >= thr));
-                gt += __popcll(wave_ballot(cv[i] > thr));
-            }
-            need = kk - gt;
-            btie = ge - gt > need;
+            // keys held per lane: as few as the buffer needs
+            if (cnt <= 2 * SSA_WAVE)
+                sel_threshold<2>(ckey, cnt, kk, lo, thr, need, btie);
+            else if (cnt <= 4 * SSA_WAVE)
+                sel_threshold<4>(ckey, cnt, kk, lo, thr, need, btie);
+            else
+                sel_threshold<SEL_CAP / SSA_WAVE>(ckey, cnt, kk, lo, thr, need, btie);
         } else {
             // rare: exact search over the whole kept stream (one walk per bit)
             uint32_t t0 = 0u;
@@ -1512,7 +1595,7 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     }
     if (btie && lane == 0 && p.tie_list) p.tie_list[atomicAdd(p.tie_count, 1)] = (int)rloc;
 
-    full_merge_emit(bm, p, n, row, f);
+    full_merge_emit(bm, p, n, row, f, (int32_t *)ckey, 2 * SEL_BUF);
 }
 
 // ------------------------------------------------------------------ exact top-k replay
@@ -1897,7 +1980,7 @@ topk_replay_kernel(SelP p, int chunk, int W) {
             rp_sync();
             for (int t = lane; t < fcount; t += SSA_WAVE) bm_set(bm, A.cand[t]);
             rp_sync();
-            full_merge_emit(bm, p, n, row, fcount);
+            full_merge_emit(bm, p, n, row, fcount, (int32_t *)A.key, W);
         }
         rp_sync();
     }
@@ -2317,6 +2400,7 @@ int build_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *w
         sp.qid = qp.qid; sp.perm = cp.perm; sp.bstart = rp.bstart; sp.bsize = rp.bsize;
         sp.sid = rp.sid; sp.rnk = (const int32_t *)(ws + L.rnk);
         sp.inv = (const int32_t *)(ws + L.inv); sp.cut = cp.cut;
+        sp.nl_magic = (uint32_t)((((uint64_t)1 << 32) + D.nlists - 1) / D.nlists);
         sp.S = rp.S; sp.q = a->q.ptr; sp.k = a->k.ptr;
         sp.qsb = a->q.sb; sp.qsh = a->q.sh; sp.qsn = a->q.sn;
         sp.ksb = a->k.sb; sp.ksh = a->k.sh; sp.ksn = a->k.sn;

@@ -198,6 +198,8 @@ APPLY_CASES = [
     (1, 2, 1, 17, 300, 128, 256),
     (1, 2, 2, 9, 9, 8, 5),
     (1, 2, 2, 20, 30, 32, 64),
+    (1, 2, 1, 10, 40, 256, 24),
+    (1, 4, 2, 12, 20, 4, 10),
 ]
 
 
