@@ -262,11 +262,54 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// Reduce U per-lane partials (one per row) over the 2U lanes of a row group
+// by a butterfly: at each step a lane pair splits its rows, each lane sending
+// the half it drops and adding the half it keeps (row mirror, half mirror,
+// quad swaps as the pairings).  Afterwards lanes li and li ^ 1 both hold the
+// total of row r = 4 [li >= 8] + 2 [li & 4] + [li & 2] (U = 8), or
+// r = 2 [li & 4] + [li & 2] (U = 4).
+template <int U>
+__device__ __forceinline__ float butterfly_rows(float (&v)[U], int li) {
+    static_assert(U == 4 || U == 8, "butterfly over 8 or 16 lanes");
+    float w[4];
+    if constexpr (U == 8) {
+        const bool hi = li >= 8;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float send = hi ? v[k] : v[k + 4], keep = hi ? v[k + 4] : v[k];
+            w[k] = keep + dpp_move<0x140>(send);        // row mirror: li <-> 15 - li
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) w[k] = v[k];
+    }
+    float x[2];
+    {
+        const bool hi = (li & 4) != 0;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const float send = hi ? w[k] : w[k + 2], keep = hi ? w[k + 2] : w[k];
+            x[k] = keep + dpp_move<0x141>(send);        // half mirror: li <-> 7 - li (in 8)
+        }
+    }
+    const bool hi = (li & 2) != 0;
+    const float send = hi ? x[0] : x[1], keep = hi ? x[1] : x[0];
+    float y = keep + dpp_move<0x4E>(send);              // quad perm [2,3,0,1]: li ^ 2
+    return y + dpp_move<0xB1>(y);                       // quad perm [1,0,3,2]: li ^ 1
+}
+
 template <typename T, int D, int U>
 __global__ void __launch_bounds__(WAVES * SSA_WAVE)
 apply_fwd16_kernel(ApplyP p) {
     constexpr int LPR = D / 8;                 // lanes per row, 16 bytes each
     constexpr int RPI = SSA_WAVE / LPR;        // rows per wave load
+    constexpr int STEP = RPI * U;              // slots per loop step
+    constexpr bool BFLY = 2 * U == LPR;        // head dims 64 and 128
     static_assert(sizeof(T) == 2 && D % 8 == 0 && LPR <= 32 && U % 2 == 0, "16-bit path");
     extern __shared__ float smem[];
     const int64_t blk = xcd_logical_block(blockIdx.x, p.nblocks);
@@ -276,8 +319,9 @@ apply_fwd16_kernel(ApplyP p) {
     if (row >= p.rows) return;
     const int lane = lane_id();
     const int sub = lane / LPR, li = lane % LPR;
-    int32_t *ix = reinterpret_cast<int32_t *>(smem) + (int64_t)wid * 2 * p.K;   // key ids, -1 = masked
-    float *sc = reinterpret_cast<float *>(ix + p.K);                          // scores, then p
+    const int Kp = (p.K + STEP - 1) / STEP * STEP;                               // padded slots
+    int32_t *ix = reinterpret_cast<int32_t *>(smem) + (int64_t)wid * 2 * Kp;    // key ids, -1 = masked
+    float *sc = reinterpret_cast<float *>(ix + Kp);                           // scores, then p
 
     const int n = (int)(row % p.N);
     const int64_t bh = row / p.N;
@@ -292,56 +336,75 @@ apply_fwd16_kernel(ApplyP p) {
     const int64_t *nb = p.nb + row * p.K;
     const uint8_t *va = p.valid ? p.valid + row * p.K : nullptr;
 
-    for (int j = lane; j < p.K; j += SSA_WAVE) {
-        const int64_t x = nb[j];
-        const bool o = (va ? va[j] != 0 : true) && x >= 0 && x < p.M;
-        ix[j] = o ? (int)x : -1;
+    // neighbour ids as int32 in LDS; masked, out-of-range and padding slots -1
+    for (int j = lane; j < Kp; j += SSA_WAVE) {
+        int x = -1;
+        if (j < p.K) {
+            const int64_t y = nb[j];
+            if ((va ? va[j] != 0 : true) && y >= 0 && y < p.M) x = (int)y;
+        }
+        ix[j] = x;
     }
     const uint4 q4 = *reinterpret_cast<const uint4 *>(qrow + li * 8);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    // ---- scores
-    for (int j0 = 0; j0 < p.K; j0 += RPI * U) {
+    // ---- scores q.k * scale (masked slots are set to -inf by the softmax)
+    for (int j0 = 0; j0 < Kp; j0 += STEP) {
         int xi[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int j = j0 + u * RPI + sub;
-            xi[u] = j < p.K ? ix[j] : -1;
-        }
+        for (int u = 0; u < U; ++u) xi[u] = ix[j0 + u * RPI + sub];
         uint4 kv[U];
 #pragma unroll
         for (int u = 0; u < U; ++u)
             kv[u] = *reinterpret_cast<const uint4 *>(
                 kb + (__umul24((uint32_t)max(xi[u], 0), krb) + lio));
+        float part[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            float part = Dot2<T>::dot(q4.x, kv[u].x, 0.f);
-            part = Dot2<T>::dot(q4.y, kv[u].y, part);
-            part = Dot2<T>::dot(q4.z, kv[u].z, part);
-            part = Dot2<T>::dot(q4.w, kv[u].w, part);
-            part = group_sum<LPR>(part);
-            const int j = j0 + u * RPI + sub;
-            if (li == 0 && j < p.K) sc[j] = xi[u] >= 0 ? part * p.scale : -INFINITY;
+            part[u] = Dot2<T>::dot(q4.x, kv[u].x, 0.f);
+            part[u] = Dot2<T>::dot(q4.y, kv[u].y, part[u]);
+            part[u] = Dot2<T>::dot(q4.z, kv[u].z, part[u]);
+            part[u] = Dot2<T>::dot(q4.w, kv[u].w, part[u]);
+        }
+        if constexpr (BFLY) {
+            const float tot = butterfly_rows<U>(part, li);
+            const int r = (U == 8 ? 4 * (li >= 8) : 0) + 2 * ((li & 4) != 0) + ((li & 2) != 0);
+            if ((li & 1) == 0) sc[j0 + r * RPI + sub] = tot * p.scale;
+        } else {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const float tot = group_sum<LPR>(part[u]);
+                if (li == 0) sc[j0 + u * RPI + sub] = tot * p.scale;
+            }
         }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    // ---- fp32 softmax; p rounded to the value dtype (inverted dropout on p)
+    // ---- fp32 softmax; p rounded to the value dtype (inverted dropout on p);
+    // padding slots get p = 0
     float m = -INFINITY;
-    for (int j = lane; j < p.K; j += SSA_WAVE) m = fmaxf(m, sc[j]);
+    for (int j = lane; j < p.K; j += SSA_WAVE) {
+        const float s = ix[j] >= 0 ? sc[j] : -INFINITY;
+        sc[j] = s;
+        m = fmaxf(m, s);
+    }
     m = wave_max(m);
     float l = 0.f;
     for (int j = lane; j < p.K; j += SSA_WAVE) l += expf(sc[j] - m);
     l = wave_sum(l);
     const float inv = 1.f / l;
-    for (int j = lane; j < p.K; j += SSA_WAVE) {
-        float w = Cvt<T>::round(expf(sc[j] - m) * inv);
-        if (p.drop_p > 0.f)
-            w = (drop_uniform(p.seed, row, j) < p.drop_p) ? 0.f : Cvt<T>::round(w * p.drop_scale);
+    for (int j = lane; j < Kp; j += SSA_WAVE) {
+        float w = 0.f;
+        if (j < p.K) {
+            w = Cvt<T>::round(expf(sc[j] - m) * inv);
+            if (p.drop_p > 0.f)
+                w = (drop_uniform(p.seed, row, j) < p.drop_p) ? 0.f
+                                                              : Cvt<T>::round(w * p.drop_scale);
+        }
         sc[j] = w;
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -352,15 +415,13 @@ apply_fwd16_kernel(ApplyP p) {
     float acc[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] = 0.f;
-    for (int j0 = 0; j0 < p.K; j0 += RPI * U) {
+    for (int j0 = 0; j0 < Kp; j0 += STEP) {
         int xi[U];
         float pj[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int j = j0 + u * RPI + sub;
-            const bool in = j < p.K;
-            xi[u] = in ? ix[j] : -1;
-            pj[u] = in ? sc[j] : 0.f;
+            xi[u] = ix[j0 + u * RPI + sub];
+            pj[u] = sc[j0 + u * RPI + sub];
         }
         uint4 vv[U];
 #pragma unroll
@@ -531,6 +592,9 @@ int launch_apply(const ApplyP &p, hipStream_t st, bool bwd) {
     const int64_t grid = 8 * ceil_div(p.nblocks, 8);
     if (bwd) {
         const size_t lds = (size_t)WAVES * 2 * p.K * sizeof(float);
+        if (lds > 65536)
+            SSA_CHECK_HIP(hipFuncSetAttribute((const void *)apply_bwd_kernel<T, D>,
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
         hipLaunchKernelGGL((apply_bwd_kernel<T, D>), dim3((unsigned)grid), dim3(WAVES * SSA_WAVE),
                            lds, st, p);
     } else {
@@ -538,12 +602,21 @@ int launch_apply(const ApplyP &p, hipStream_t st, bool bwd) {
         constexpr int U = (Geo<T, D>::RPI >= 8) ? 4 : 8;
         if constexpr (sizeof(T) == 2 && D >= 8) {
             if (fwd16_ok(p, (int)sizeof(T), D)) {
+                constexpr int STEP = (SSA_WAVE / (D / 8)) * U;
+                const size_t lds16 = (size_t)WAVES * 2 * ceil_div(p.K, STEP) * STEP * sizeof(float);
+                if (lds16 > 65536)
+                    SSA_CHECK_HIP(hipFuncSetAttribute((const void *)apply_fwd16_kernel<T, D, U>,
+                                                      hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                      (int)lds16));
                 hipLaunchKernelGGL((apply_fwd16_kernel<T, D, U>), dim3((unsigned)grid),
-                                   dim3(WAVES * SSA_WAVE), lds, st, p);
+                                   dim3(WAVES * SSA_WAVE), lds16, st, p);
                 SSA_CHECK_LAUNCH();
                 return SSA_OK;
             }
         }
+        if (lds > 65536)
+            SSA_CHECK_HIP(hipFuncSetAttribute((const void *)apply_fwd_kernel<T, D, U>,
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
         hipLaunchKernelGGL((apply_fwd_kernel<T, D, U>), dim3((unsigned)grid),
                            dim3(WAVES * SSA_WAVE), lds, st, p);
     }

@@ -200,6 +200,7 @@ APPLY_CASES = [
     (1, 2, 2, 20, 30, 32, 64),
     (1, 2, 1, 10, 40, 256, 24),
     (1, 4, 2, 12, 20, 4, 10),
+    (1, 1, 1, 3, 500, 128, 2500),
 ]
 
 
