@@ -440,6 +440,7 @@ struct RsP {
     uint32_t *S;       // score keys (score_key); slot = list * C + sorted member index
     int N, M, R, NS, NB, C, Hq, Hkv, rep, bh0, causal;
     int vec4;          // rows and list starts of S are 16-byte aligned (C % 4 == 0)
+    int k32;           // byte offsets of the K rows of a (batch, kv head) fit 32 bits
     int64_t Call;
 };
 
@@ -617,91 +618,106 @@ __global__ void __launch_bounds__(256) rescore_mfma_kernel(RsP p) {
     }
     const bool active = 16 * wid < qc;
 
-    // the tile's candidate ids, then candidate rows [c0, c0 + 64) copied
-    // through registers into LDS two slices ahead of their use
+    // the tile's candidate ids; then, per 64-candidate slice j: the K rows of
+    // slice j + 1 are loaded into registers, slice j (in LDS) is scored, its
+    // score keys stored, and the loaded rows committed to the other LDS buffer
     int32_t *prl = reinterpret_cast<int32_t *>(rs_lds + 2 * (64 * RB));
     for (int c = tid; c < nva; c += 256) prl[c] = pr[c];
     __syncthreads();
     const int nv = rs_tile_cutoff(prl, nva, nidx, qc, p.causal);
     constexpr int PER = (64 * SEGS + 255) / 256;
-    uint4 sa[PER], sb[PER];
-    auto fetch = [&](int c0, uint4 (&stage)[PER]) {
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int x = tid + 256 * i;
-            const int row = x / SEGS, seg = x % SEGS;
-            const bool ok = x < 64 * SEGS && c0 + row < nv;
-            const T *src = kbase + (int64_t)(ok ? prl[c0 + row] : 0) * p.ksn + seg * 8;
-            stage[i] = ok ? *reinterpret_cast<const uint4 *>(src) : make_uint4(0, 0, 0, 0);
-        }
-    };
-    auto commit = [&](int buf, const uint4 (&stage)[PER]) {
-        unsigned char *dst = rs_lds + buf * (64 * RB);
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int x = tid + 256 * i;
-            if (x < 64 * SEGS) {
-                const int row = x / SEGS, seg = x % SEGS;
-                *reinterpret_cast<uint4 *>(dst + row * RB + seg * 16) = stage[i];
-            }
-        }
-    };
+    // rows are addressed by 32-bit byte offsets from the head's base (the
+    // dispatcher picks this kernel only when they fit); rows past the slice
+    // read row 0 (in range, never scored)
+    const uint32_t rowb = (uint32_t)(p.ksn * (int64_t)sizeof(T));
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    u32x4 sa[PER];
+#define RS_FETCH(C0)                                                                         \
+    _Pragma("unroll") for (int i = 0; i < PER; ++i) {                                        \
+        const int x = tid + 256 * i;                                                         \
+        const int row = x / SEGS, seg = x % SEGS;                                            \
+        const int id = (x < 64 * SEGS && (C0) + row < nv) ? prl[(C0) + row] : 0;            \
+        sa[i] = *reinterpret_cast<const u32x4 *>((const char *)kbase +                       \
+                                                 (__umul24((uint32_t)id, rowb) + seg * 16u)); \
+    }
+#define RS_COMMIT(BUF)                                                                       \
+    _Pragma("unroll") for (int i = 0; i < PER; ++i) {                                        \
+        const int x = tid + 256 * i;                                                         \
+        if (x < 64 * SEGS)                                                                   \
+            *reinterpret_cast<u32x4 *>(rs_lds + (BUF) * (64 * RB) + (x / SEGS) * RB +        \
+                                       (x % SEGS) * 16) = sa[i];                             \
+    }
     const int64_t slotbase = (int64_t)(r * p.NS + t) * p.C;
     uint32_t *srow = p.S + ((int64_t)bhl * p.N + nidx[qok ? qrow : 0]) * p.Call + slotbase;
     const int nsl = (nv + 63) / 64;
-    fetch(0, sa);
-    commit(0, sa);
-    if (nsl > 1) fetch(64, sa);
-    if (nsl > 2) fetch(128, sb);
+    RS_FETCH(0)
+    RS_COMMIT(0)
     __syncthreads();
+    // score keys of the previous slice, stored at the top of the next
+    // iteration: the loads issued after them (and awaited by the commit) then
+    // find them long complete
+    u32x4 kq[4];
+    int cq = -1;
+#define RS_STORE_KEYS()                                                                      \
+    if (cq >= 0 && qok) {                                                                    \
+        _Pragma("unroll") for (int ct = 0; ct < 4; ++ct) {                                   \
+            const int cc = cq + ct * 16 + 4 * lg;                                            \
+            if (cc + 3 < nv && p.vec4) {                                                     \
+                *reinterpret_cast<u32x4 *>(srow + cc) = kq[ct];                              \
+            } else {                                                                         \
+                if (cc < nv) srow[cc] = kq[ct].x;                                            \
+                if (cc + 1 < nv) srow[cc + 1] = kq[ct].y;                                    \
+                if (cc + 2 < nv) srow[cc + 2] = kq[ct].z;                                    \
+                if (cc + 3 < nv) srow[cc + 3] = kq[ct].w;                                    \
+            }                                                                                \
+        }                                                                                    \
+    }
     for (int j = 0; j < nsl; ++j) {
         const int c0 = 64 * j;
+        const bool more = j + 1 < nsl;
+        RS_STORE_KEYS()
+        if (more) { RS_FETCH(c0 + 64) }
         if (active) {
             const unsigned char *kl = rs_lds + (j & 1) * (64 * RB);
+            auto frag = [&](int s, V (&kf)[4]) __attribute__((always_inline)) {
+                const int e0 = 32 * s + 8 * lg;
+#pragma unroll
+                for (int ct = 0; ct < 4; ++ct)
+                    kf[ct] = e0 < D ? __builtin_bit_cast(
+                                          V, *reinterpret_cast<const uint4 *>(
+                                                 kl + (ct * 16 + li) * RB + e0 * 2))
+                                    : __builtin_bit_cast(V, make_uint4(0, 0, 0, 0));
+            };
+            // fragments two k steps deep: the reads of step s + 2 overlap the
+            // products of step s
+            V kf[2][4];
+            frag(0, kf[0]);
+            if (KS > 1) frag(1, kf[1]);
             f32x4_t acc[4];
 #pragma unroll
             for (int ct = 0; ct < 4; ++ct) acc[ct] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int s = 0; s < KS; ++s) {
-                const int e0 = 32 * s + 8 * lg;
 #pragma unroll
-                for (int ct = 0; ct < 4; ++ct) {
-                    const V kf = e0 < D ? __builtin_bit_cast(
-                                              V, *reinterpret_cast<const uint4 *>(
-                                                     kl + (ct * 16 + li) * RB + e0 * 2))
-                                        : __builtin_bit_cast(V, make_uint4(0, 0, 0, 0));
-                    acc[ct] = Mfma16<T>::mma(kf, qf[s], acc[ct]);
-                }
+                for (int ct = 0; ct < 4; ++ct)
+                    acc[ct] = Mfma16<T>::mma(kf[s & 1][ct], qf[s], acc[ct]);
+                if (s + 2 < KS) frag(s + 2, kf[s & 1]);
             }
             // lane (li, lg) holds candidates c0 + 16 ct + 4 lg + rr of query li
-            if (qok) {
 #pragma unroll
-                for (int ct = 0; ct < 4; ++ct) {
-                    const int cc = c0 + ct * 16 + 4 * lg;
-                    uint4 kv;
-                    kv.x = score_key(acc[ct][0]);
-                    kv.y = score_key(acc[ct][1]);
-                    kv.z = score_key(acc[ct][2]);
-                    kv.w = score_key(acc[ct][3]);
-                    if (cc + 3 < nv && p.vec4) {
-                        *reinterpret_cast<uint4 *>(srow + cc) = kv;
-                    } else {
-                        if (cc < nv) srow[cc] = kv.x;
-                        if (cc + 1 < nv) srow[cc + 1] = kv.y;
-                        if (cc + 2 < nv) srow[cc + 2] = kv.z;
-                        if (cc + 3 < nv) srow[cc + 3] = kv.w;
-                    }
-                }
-            }
+            for (int ct = 0; ct < 4; ++ct)
+                kq[ct] = u32x4{score_key(acc[ct][0]), score_key(acc[ct][1]),
+                               score_key(acc[ct][2]), score_key(acc[ct][3])};
+            cq = c0;
         }
-        // slice j + 1 was fetched a full iteration ago; every wave is done
-        // with the buffer it replaces (last read in iteration j - 1)
-        if (j + 1 < nsl) commit((j + 1) & 1, sa);
+        // the other buffer was last read in iteration j - 1, before its barrier
+        if (more) { RS_COMMIT((j + 1) & 1) }
         __syncthreads();
-#pragma unroll
-        for (int i = 0; i < PER; ++i) sa[i] = sb[i];
-        if (j + 3 < nsl) fetch(c0 + 192, sb);
     }
+    RS_STORE_KEYS()
+#undef RS_FETCH
+#undef RS_COMMIT
+#undef RS_STORE_KEYS
 }
 
 // ------------------------------------------------------------------ sorted candidate lists
@@ -2194,7 +2210,8 @@ bool rows_aligned16(const RsP &rp, int elem) {
 
 template <typename T>
 bool rescore_uses_mfma(int d, const RsP &rp) {
-    return !std::is_same<T, float>::value && d >= 8 && d <= 128 && rows_aligned16(rp, 2);
+    return !std::is_same<T, float>::value && d >= 8 && d <= 128 && rows_aligned16(rp, 2) &&
+           rp.k32;
 }
 
 template <typename T>
@@ -2368,6 +2385,11 @@ int build_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *w
         rp.Hq = D.Hq; rp.Hkv = D.Hkv; rp.rep = D.rep; rp.bh0 = (int)bh0; rp.Call = D.Call;
         rp.causal = a->causal ? 1 : 0;
         rp.vec4 = (D.C % 4 == 0) ? 1 : 0;
+        {
+            const int64_t el = a->q.dtype == SSA_F32 ? 4 : 2;
+            rp.k32 = (rp.ksn * el < ((int64_t)1 << 24) &&
+                      ((int64_t)D.M * rp.ksn + D.d) * el < ((int64_t)1 << 31)) ? 1 : 0;
+        }
         const int64_t grid = 8 * ceil_div((int64_t)ninst * (ceil_div(D.N, TQ) + D.NB), 8);
         rc = rescore_dispatch<T>(D.d, rp, grid, st);
         if (rc) return rc;
