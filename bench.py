@@ -80,6 +80,10 @@ def recall_at_32(q, k, nb, va, rep, causal_variant=False):
     return res[0], sum(res) / len(res)
 
 
+# the apply kernel the bf16 workload launches (16-bit packed path)
+APPLY_KERNEL = "apply_fwd16_kernel"
+
+
 def measured_traffic(kernel):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE /
     WRITE_SIZE summary (a line `traffic <kernel> <bytes>`), or None."""
@@ -210,7 +214,7 @@ def main():
     K_out = nb.shape[-1]
     bytes_apply = B * H * N * (2 * K_out * d + 2 * d) * 2
     achieved = bytes_apply / (t_apply / 1000.0)
-    traffic = measured_traffic("apply_fwd_kernel")
+    traffic = measured_traffic(APPLY_KERNEL)
     print(f"# build {t_build:.3f} ms, apply {t_apply:.3f} ms", file=sys.stderr, flush=True)
 
     # rows whose k-th LSH score is tied (selection decided by the tie rule)
@@ -242,7 +246,7 @@ def main():
                    "global_batch": B, "seq_len": N, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": achieved / 1e9, "peak": PEAK_HBM / 1e9,
                      "unit": "GB/s", "frac": achieved / PEAK_HBM, "traffic": traffic,
-                     "kernel": "apply_fwd_kernel", "bytes_per_launch": bytes_apply,
+                     "kernel": APPLY_KERNEL, "bytes_per_launch": bytes_apply,
                      "ms_per_launch": t_apply},
         "t_build_ms": t_build, "t_apply_ms": t_apply, "k_out": K_out,
         "tie_rows": tie_rows, "query_rows": B * H * N,
