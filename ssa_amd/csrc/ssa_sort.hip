@@ -18,6 +18,8 @@
 //     ballots, s by binary search, then performs all s swaps in parallel;
 //   * both children inherit depth - 1; a segment reaching depth 0 is heap-
 //     sorted by one lane (the depth limit is 2*floor(log2 n));
+//   * a segment of at most 64 elements is finished (down to its leaves) by one
+//     wavefront in registers;
 //   * segments of <= 16 elements are left for the final insertion sort.
 //     Because every partition leaves max(left) <= min(right), that final pass
 //     equals a stable insertion sort inside each leaf, done one leaf per thread.
@@ -27,7 +29,7 @@
 
 namespace {
 
-constexpr int SORT_THREADS = 512;
+constexpr int SORT_THREADS = 1024;
 constexpr int SORT_WAVES = SORT_THREADS / SSA_WAVE;
 constexpr int LEAF = 16;
 
@@ -151,6 +153,102 @@ __device__ int wave_partition(uint16_t *key, uint16_t *idx, uint16_t *TL, uint16
     return cut;
 }
 
+// index of the k-th (0-based) set bit of a 32 / 64-bit mask (k < popcount)
+__device__ __forceinline__ int nth_set_bit32(uint32_t b, int k) {
+    int pos = 0;
+#pragma unroll
+    for (int sh = 16; sh >= 1; sh >>= 1) {
+        const int c = __popc(b & ((1u << sh) - 1u));
+        const bool up = k >= c;
+        k = up ? k - c : k;
+        b = up ? b >> sh : b;
+        pos = up ? pos + sh : pos;
+    }
+    return pos;
+}
+__device__ __forceinline__ int nth_set_bit64(uint64_t m, int k) {
+    const int c = __popc((uint32_t)m);
+    const bool up = k >= c;
+    return (up ? 32 : 0) + nth_set_bit32(up ? (uint32_t)(m >> 32) : (uint32_t)m, up ? k - c : k);
+}
+
+// The whole introsort subtree of a segment of at most 64 keys, in one
+// wavefront's registers (lane i holds position f + i).  Each partition is the
+// same median-of-three + Hoare scan as wave_partition, computed with ballots:
+// L_k / R_k are the k-th set bits of the stopper masks (from the bottom / the
+// top), every lane finds its swap partner with one shuffle, and the cut is
+// read from lane s.  Pending segments are bits of a mask (segment starts), so
+// the order in which independent segments are split does not matter.
+__device__ void wave_small_sort(uint16_t *key, uint16_t *idx, uint32_t *bits, int f, int n,
+                                int depth0) {
+    const int lane = lane_id();
+    int kv = lane < n ? (int)key[f + lane] : 0;
+    int xv = lane < n ? (int)idx[f + lane] : 0;
+    int dep = lane == 0 ? depth0 : 0;          // depth of the segment starting at this lane
+    uint64_t bnd = 1ull;                       // segment starts
+    uint64_t pend = n > LEAF ? 1ull : 0ull;    // starts of segments still to split
+    while (pend) {
+        const int a = __ffsll((long long)pend) - 1;
+        pend &= pend - 1ull;
+        const uint64_t above = bnd & ~((2ull << a) - 1ull);
+        const int b = above ? __ffsll((long long)above) - 1 : n;
+        const int d = __builtin_amdgcn_readlane(dep, a);
+        if (d == 0) {                          // depth limit: heap sort through LDS
+            if (lane < n) { key[f + lane] = (uint16_t)kv; idx[f + lane] = (uint16_t)xv; }
+            wave_sync_lds();
+            if (lane == 0) heap_sort_range(key, idx, f + a, f + b);
+            wave_sync_lds();
+            if (lane < n) { kv = key[f + lane]; xv = idx[f + lane]; }
+            continue;
+        }
+        const int m = b - a;
+        const int ia = a + 1, ib = a + m / 2, ic = b - 1;
+        const int ka = __builtin_amdgcn_readlane(kv, ia), kb = __builtin_amdgcn_readlane(kv, ib),
+                  kc = __builtin_amdgcn_readlane(kv, ic);
+        int x, p;
+        if (ka < kb) {
+            if (kb < kc) { x = ib; p = kb; }
+            else if (ka < kc) { x = ic; p = kc; }
+            else { x = ia; p = ka; }
+        } else if (ka < kc) { x = ia; p = ka; }
+        else if (kb < kc) { x = ic; p = kc; }
+        else { x = ib; p = kb; }
+        {                                       // pivot to the front
+            const int kx = __builtin_amdgcn_readlane(kv, x), xx = __builtin_amdgcn_readlane(xv, x);
+            const int k0 = __builtin_amdgcn_readlane(kv, a), x0 = __builtin_amdgcn_readlane(xv, a);
+            if (lane == a) { kv = kx; xv = xx; }
+            else if (lane == x) { kv = k0; xv = x0; }
+        }
+        const bool in = lane >= a && lane < b;
+        const uint64_t bL = wave_ballot(in && lane > a && kv >= p);
+        const uint64_t bR = wave_ballot(in && kv <= p);
+        const int nL = __popcll(bL), nR = __popcll(bR);
+        const int Lj = nth_set_bit64(bL, lane);                                   // lane < nL
+        const int Rj = 63 - nth_set_bit64(__builtin_bitreverse64(bR), lane);      // lane < nR
+        const int mn = nL < nR ? nL : nR;
+        const int sw = __popcll(wave_ballot(lane < mn && Lj < Rj));               // a prefix
+        const int rl = lanes_below(bL);
+        const int rr = __popcll(bR & ~((2ull << lane) - 1ull));
+        const int tR = __shfl(Rj, rl, SSA_WAVE);   // R_rl
+        const int tL = __shfl(Lj, rr, SSA_WAVE);   // L_rr
+        int partner = lane;
+        if (((bL >> lane) & 1ull) && rl < sw) partner = tR;
+        else if (((bR >> lane) & 1ull) && rr < sw) partner = tL;
+        kv = __shfl(kv, partner, SSA_WAVE);
+        xv = __shfl(xv, partner, SSA_WAVE);
+        const int cL = sw < nL ? __builtin_amdgcn_readlane(Lj, sw) : 0x7fffffff;
+        const int cR = sw > 0 ? __builtin_amdgcn_readlane(Rj, sw - 1) : 0x7fffffff;
+        const int c = cL < cR ? cL : cR;
+        if (lane == 0) atomicOr(&bits[(f + c) >> 5], 1u << ((f + c) & 31));
+        bnd |= 1ull << c;
+        dep = (lane == a || lane == c) ? d - 1 : dep;
+        if (c - a > LEAF) pend |= 1ull << a;
+        if (b - c > LEAF) pend |= 1ull << c;
+    }
+    if (lane < n) { key[f + lane] = (uint16_t)kv; idx[f + lane] = (uint16_t)xv; }
+    wave_sync_lds();
+}
+
 struct SortShared {
     int ncur, nnxt;
 };
@@ -214,6 +312,10 @@ bucket_sort_kernel(const uint16_t *ids, int n, int NB, int32_t *perm, int32_t *b
             if (depth == 0) {
                 if (lane == 0) heap_sort_range(key, idx, f, l);
                 wave_sync_lds();
+                continue;
+            }
+            if (l - f <= SSA_WAVE) {           // the rest of this subtree in registers
+                wave_small_sort(key, idx, bits, f, l - f, depth);
                 continue;
             }
             const int cut = wave_partition(key, idx, TL, TR, f, l);
