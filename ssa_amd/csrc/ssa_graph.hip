@@ -2046,7 +2046,7 @@ Layout plan(const Dims &D) {
     return L;
 }
 
-int make_dims(const ssa_graph_args *a, Dims &D) {
+int make_dims(const ssa_graph_args *a, Dims &D, bool need_q = true) {
     SSA_CHECK_ARG(a != nullptr, "build_graph: null args");
     SSA_CHECK_ARG(a->mode == SSA_GRAPH_FULL || a->mode == SSA_GRAPH_LSH, "build_graph: bad mode");
     SSA_CHECK_ARG(a->B >= 1 && a->Hq >= 1 && a->Hkv >= 1 && a->N >= 1 && a->M >= 1,
@@ -2058,7 +2058,7 @@ int make_dims(const ssa_graph_args *a, Dims &D) {
     SSA_CHECK_ARG(a->C <= (1 << 24), "build_graph: C=%d above 2^24", a->C);
     SSA_CHECK_ARG(a->G >= 0 && a->G <= 63, "build_graph: G=%d outside 0..63", a->G);
     SSA_CHECK_ARG(a->rand_proj || (a->q_proj && a->k_proj), "build_graph: no hyperplanes");
-    SSA_CHECK_ARG(a->q.ptr && a->k.ptr, "build_graph: null q/k");
+    SSA_CHECK_ARG((a->q.ptr || !need_q) && a->k.ptr, "build_graph: null q/k");
     SSA_CHECK_ARG(a->q.dtype == a->k.dtype && a->q.dtype >= 0 && a->q.dtype <= 2,
                   "build_graph: q/k dtype");
     SSA_CHECK_ARG(a->G == 0 || a->glob, "build_graph: glob is null");
@@ -2159,19 +2159,18 @@ bool view_aligned16(const ssa_tensor4 &t, int elem) {
 
 template <typename T>
 int launch_hash(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws,
-                hipStream_t st) {
+                hipStream_t st, bool keys) {
     HashP hp{};
     hp.planes = a->rand_proj;
     hp.R = D.R; hp.maxP = D.maxP; hp.P = D.P; hp.Tp = D.Tp; hp.NS = D.NS; hp.d = D.d;
-    // keys
-    hp.x = a->k.ptr; hp.sb = a->k.sb; hp.sh = a->k.sh; hp.sn = a->k.sn;
-    hp.nh = D.Hkv; hp.L = D.M; hp.inj = a->k_proj; hp.key_layout = 1;
-    hp.vec16 = view_aligned16(a->k, (int)sizeof(T)) ? 1 : 0;
-    hp.out = (uint16_t *)(ws + L.kid);
-    hp.rows = D.BK * D.M;
-    int rc = launch_hash_one<T>(hp, D.d, st);
-    if (rc) return rc;
-    // queries
+    if (keys) {
+        hp.x = a->k.ptr; hp.sb = a->k.sb; hp.sh = a->k.sh; hp.sn = a->k.sn;
+        hp.nh = D.Hkv; hp.L = D.M; hp.inj = a->k_proj; hp.key_layout = 1;
+        hp.vec16 = view_aligned16(a->k, (int)sizeof(T)) ? 1 : 0;
+        hp.out = (uint16_t *)(ws + L.kid);
+        hp.rows = D.BK * D.M;
+        return launch_hash_one<T>(hp, D.d, st);
+    }
     hp.x = a->q.ptr; hp.sb = a->q.sb; hp.sh = a->q.sh; hp.sn = a->q.sn;
     hp.nh = D.Hq; hp.L = D.N; hp.inj = a->q_proj; hp.key_layout = 0;
     hp.vec16 = view_aligned16(a->q, (int)sizeof(T)) ? 1 : 0;
@@ -2313,11 +2312,18 @@ int select_dispatch(const SelP &sp, hipStream_t st) {
     return sp.causal ? launch_select<T, false, true>(sp, st) : launch_select<T, false, false>(sp, st);
 }
 
+// Key phases: bucket ids of the keys (SSA_PHASE_KEY_HASH); the bucket
+// permutation and tables and the sorted candidate lists (SSA_PHASE_KEY_SORT)
+// -- everything that needs k but not q.
 template <typename T>
-int build_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws,
-                hipStream_t st) {
-    int rc = launch_hash<T>(D, a, L, ws, st);
-    if (rc) return rc;
+int keys_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws,
+               hipStream_t st, int phases) {
+    int rc = SSA_OK;
+    if (phases & SSA_PHASE_KEY_HASH) {
+        rc = launch_hash<T>(D, a, L, ws, st, true);
+        if (rc) return rc;
+    }
+    if (!(phases & SSA_PHASE_KEY_SORT)) return SSA_OK;
     rc = ssa_launch_bucket_sort((const uint16_t *)(ws + L.kid), (int)(D.BK * D.R), D.M, D.P,
                                 (int32_t *)(ws + L.perm), (int32_t *)(ws + L.bstart),
                                 (int32_t *)(ws + L.bsize), (uint16_t *)(ws + L.sorttmp), st);
@@ -2341,6 +2347,15 @@ int build_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *w
                            lp);
         SSA_CHECK_LAUNCH();
     }
+    return SSA_OK;
+}
+
+// Query phase: everything else, given the key phase's results in ws.
+template <typename T>
+int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws,
+                  hipStream_t st) {
+    int rc = launch_hash<T>(D, a, L, ws, st, false);
+    if (rc) return rc;
     for (int64_t bh0 = 0; bh0 < D.BH; bh0 += D.nbh_chunk) {
         const int nbh = (int)((D.BH - bh0) < D.nbh_chunk ? (D.BH - bh0) : D.nbh_chunk);
         const int ninst = nbh * D.R * D.NS;
@@ -2455,23 +2470,28 @@ int build_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *w
 
 extern "C" int64_t ssa_graph_out_width(const ssa_graph_args *a) {
     Dims D;
-    if (make_dims(a, D)) return -1;
+    if (make_dims(a, D, false)) return -1;
     return D.Kout;
 }
 
 extern "C" int64_t ssa_graph_workspace_bytes(const ssa_graph_args *a) {
     Dims D;
-    if (make_dims(a, D)) return -1;
+    if (make_dims(a, D, false)) return -1;
     return plan(D).total;
 }
 
-extern "C" int ssa_build_graph(const ssa_graph_args *a, void *workspace, int64_t workspace_bytes,
-                               void *stream) {
+namespace {
+int build_phase(const ssa_graph_args *a, void *workspace, int64_t workspace_bytes, void *stream,
+                int phases) {
+    SSA_CHECK_ARG(phases > 0 && phases <= SSA_PHASE_ALL, "build_graph: phases %d", phases);
     Dims D;
-    int rc = make_dims(a, D);
+    const bool qphase = (phases & SSA_PHASE_QUERIES) != 0;
+    int rc = make_dims(a, D, qphase);
     if (rc) return rc;
-    SSA_CHECK_ARG(a->out_idx, "build_graph: out_idx is null");
-    SSA_CHECK_ARG(a->mode != SSA_GRAPH_FULL || a->out_valid, "build_graph: out_valid is null");
+    if (qphase) {
+        SSA_CHECK_ARG(a->out_idx, "build_graph: out_idx is null");
+        SSA_CHECK_ARG(a->mode != SSA_GRAPH_FULL || a->out_valid, "build_graph: out_valid is null");
+    }
     const Layout L = plan(D);
     if (workspace_bytes < L.total || !workspace) {
         ssa_set_error("build_graph: workspace %lld < %lld bytes", (long long)workspace_bytes,
@@ -2480,10 +2500,28 @@ extern "C" int ssa_build_graph(const ssa_graph_args *a, void *workspace, int64_t
     }
     hipStream_t st = (hipStream_t)stream;
     char *ws = (char *)workspace;
-    switch (a->q.dtype) {
-        case SSA_F32: return build_typed<float>(D, a, L, ws, st);
-        case SSA_BF16: return build_typed<bf16_t>(D, a, L, ws, st);
-        case SSA_F16: return build_typed<f16_t>(D, a, L, ws, st);
+    const int kp = phases & (SSA_PHASE_KEY_HASH | SSA_PHASE_KEY_SORT);
+    switch (a->k.dtype) {
+        case SSA_F32:
+            if (kp && (rc = keys_typed<float>(D, a, L, ws, st, kp))) return rc;
+            return qphase ? queries_typed<float>(D, a, L, ws, st) : SSA_OK;
+        case SSA_BF16:
+            if (kp && (rc = keys_typed<bf16_t>(D, a, L, ws, st, kp))) return rc;
+            return qphase ? queries_typed<bf16_t>(D, a, L, ws, st) : SSA_OK;
+        case SSA_F16:
+            if (kp && (rc = keys_typed<f16_t>(D, a, L, ws, st, kp))) return rc;
+            return qphase ? queries_typed<f16_t>(D, a, L, ws, st) : SSA_OK;
     }
     return SSA_E_ARG;
+}
+}  // namespace
+
+extern "C" int ssa_build_graph(const ssa_graph_args *a, void *workspace, int64_t workspace_bytes,
+                               void *stream) {
+    return build_phase(a, workspace, workspace_bytes, stream, SSA_PHASE_ALL);
+}
+
+extern "C" int ssa_build_graph_phases(const ssa_graph_args *a, void *workspace,
+                                      int64_t workspace_bytes, void *stream, int phases) {
+    return build_phase(a, workspace, workspace_bytes, stream, phases);
 }

@@ -24,6 +24,8 @@
 //     Because every partition leaves max(left) <= min(right), that final pass
 //     equals a stable insertion sort inside each leaf, done one leaf per thread.
 // The bucket start/size tables come from binary searches on the sorted keys.
+#include <algorithm>
+
 #include "ssa_common.h"
 #include "ssa_graph_internal.h"
 
@@ -249,29 +251,45 @@ __device__ void wave_small_sort(uint16_t *key, uint16_t *idx, uint32_t *bits, in
     wave_sync_lds();
 }
 
-struct SortShared {
+// ---------------------------------------------------------------- top levels
+// Kernel A, one workgroup of NW waves per row: loads the row, writes the
+// bucket tables from a histogram (bstart[u] = #keys < u, bsize[u] = #keys
+// == u: what binary searches on the sorted row give), and splits segments
+// larger than SEG_T.  While a level has few segments, the waves of a group
+// cooperate on one segment (each wave finds the stoppers of its stretch; the
+// stopper lists are concatenated by prefix counts); with many segments each
+// wave partitions its own.  Children of at most SEG_T keys (and leaves) are
+// appended to a global segment list for kernel B, and the row as it stands
+// (keys | ids << 16) is written out; so is `perm`, which kernel B overwrites
+// for every listed segment (a segment heap-sorted here keeps these values).
+constexpr int SEG_T = 256;                 // segments handed to kernel B
+constexpr int NW = SORT_WAVES;
+
+struct TopShared {
     int ncur, nnxt;
+    int piv[NW], cnt[NW][2], s[NW], cut[NW], nL[NW], nR[NW];
 };
 
-// ids: rows x n (uint16); perm rows x n (int32); bstart/bsize rows x NB.
-// tmp: rows x 2n uint16 scratch for the stopper lists when they do not fit LDS.
+__device__ __forceinline__ void emit_segment(int4 *segs, int *segcount, int row, int f, int l,
+                                             int depth) {
+    segs[atomicAdd(segcount, 1)] = make_int4(row, f, l - f, depth);
+}
+
 __global__ void __launch_bounds__(SORT_THREADS)
-bucket_sort_kernel(const uint16_t *ids, int n, int NB, int32_t *perm, int32_t *bstart,
-                   int32_t *bsize, uint16_t *tmp, int tl_in_lds, int cap) {
+sort_top_kernel(const uint16_t *ids, int n, int NB, int32_t *perm, int32_t *bstart, int32_t *bsize,
+                uint32_t *gkv, int4 *segs, int *segcount, uint16_t *tmp, int tl_in_lds, int cap) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
-    __shared__ SortShared sh;
+    __shared__ TopShared sh;
     const int row = blockIdx.x;
     const int tid = threadIdx.x;
     const int wid = tid / SSA_WAVE;
     const int lane = lane_id();
     const uint16_t *src = ids + (int64_t)row * n;
 
-    // LDS layout
     uint16_t *key = (uint16_t *)smem_raw;
     uint16_t *idx = key + n;
-    uint32_t *bits = (uint32_t *)(smem_raw + ((size_t)4 * n + 15) / 16 * 16);
-    const int nwords = (n + 31) / 32 + 1;
-    uint32_t *segA = bits + nwords;
+    int32_t *hist = (int32_t *)(smem_raw + ((size_t)4 * n + 15) / 16 * 16);
+    uint32_t *segA = (uint32_t *)(hist + NB);
     uint32_t *segB = segA + cap;
     uint8_t *depA = (uint8_t *)(segB + cap);
     uint8_t *depB = depA + cap;
@@ -285,51 +303,178 @@ bucket_sort_kernel(const uint16_t *ids, int n, int NB, int32_t *perm, int32_t *b
         TR = TL + n;
     }
 
-    for (int i = tid; i < n; i += SORT_THREADS) { key[i] = src[i]; idx[i] = (uint16_t)i; }
-    for (int i = tid; i < nwords; i += SORT_THREADS) bits[i] = 0;
+    for (int u = tid; u < NB; u += SORT_THREADS) hist[u] = 0;
+    __syncthreads();
+    for (int i = tid; i < n; i += SORT_THREADS) {
+        const uint16_t k = src[i];
+        key[i] = k;
+        idx[i] = (uint16_t)i;
+        if (k < NB) atomicAdd(&hist[k], 1);
+    }
+    const int depth0 = 2 * floor_log2_i(n);
     if (tid == 0) {
         sh.ncur = 0;
         sh.nnxt = 0;
-        if (n > LEAF) {
+        if (n > SEG_T) {
             segA[0] = 0u | ((uint32_t)n << 16);
-            depA[0] = (uint8_t)(2 * floor_log2_i(n));
+            depA[0] = (uint8_t)depth0;
             sh.ncur = 1;
+        } else {
+            emit_segment(segs, segcount, row, 0, n, depth0);
         }
     }
     __syncthreads();
-    if (tid == 0) bits[0] = 1u;
+    if (wid == 0) {                                // bucket tables: exclusive scan of hist
+        int carry = 0;
+        for (int u0 = 0; u0 < NB; u0 += SSA_WAVE) {
+            const int u = u0 + lane;
+            const int c = u < NB ? hist[u] : 0;
+            int x = c;
+#pragma unroll
+            for (int o = 1; o < SSA_WAVE; o <<= 1) {
+                const int y = __shfl_up(x, o, SSA_WAVE);
+                if (lane >= o) x += y;
+            }
+            if (u < NB) {
+                bstart[(int64_t)row * NB + u] = carry + x - c;
+                bsize[(int64_t)row * NB + u] = c;
+            }
+            carry += __shfl(x, SSA_WAVE - 1, SSA_WAVE);
+        }
+    }
 
     uint32_t *cur = segA, *nxt = segB;
     uint8_t *dcur = depA, *dnxt = depB;
+    auto child = [&](int f, int l, int depth) {
+        if (l - f > SEG_T) {
+            const int slot = atomicAdd(&sh.nnxt, 1);
+            nxt[slot] = (uint32_t)f | ((uint32_t)l << 16);
+            dnxt[slot] = (uint8_t)depth;
+        } else {
+            emit_segment(segs, segcount, row, f, l, depth);
+        }
+    };
     for (int level = 0; level < 64; ++level) {
         __syncthreads();
         const int ncur = sh.ncur;
         if (ncur == 0) break;
-        for (int s = wid; s < ncur; s += SORT_WAVES) {
-            const int f = (int)(cur[s] & 0xffffu);
-            const int l = (int)(cur[s] >> 16);
-            const int depth = dcur[s];
-            if (depth == 0) {
-                if (lane == 0) heap_sort_range(key, idx, f, l);
-                wave_sync_lds();
-                continue;
+        if (2 * ncur <= NW) {
+            // ---- group mode: gw waves per segment, gi = index in the group
+            const int gw = NW / ncur;
+            const int g = wid / gw, gi = wid - g * gw;
+            const bool act = g < ncur;
+            int f = 0, l = 0, depth = 1;
+            if (act) {
+                f = (int)(cur[g] & 0xffffu);
+                l = (int)(cur[g] >> 16);
+                depth = dcur[g];
             }
-            if (l - f <= SSA_WAVE) {           // the rest of this subtree in registers
-                wave_small_sort(key, idx, bits, f, l - f, depth);
-                continue;
-            }
-            const int cut = wave_partition(key, idx, TL, TR, f, l);
-            if (lane == 0) {
-                atomicOr(&bits[cut >> 5], 1u << (cut & 31));
-                if (cut - f > LEAF) {
-                    const int slot = atomicAdd(&sh.nnxt, 1);
-                    nxt[slot] = (uint32_t)f | ((uint32_t)cut << 16);
-                    dnxt[slot] = (uint8_t)(depth - 1);
+            // a segment at the depth limit is heap-sorted by its group's first lane
+            if (act && depth == 0) {
+                if (gi == 0 && lane == 0) heap_sort_range(key, idx, f, l);
+            } else if (act && gi == 0) {               // median of three to the front
+                const int nn = l - f;
+                const int a = f + 1, b = f + nn / 2, c = l - 1;
+                const int ka = key[a], kb = key[b], kc = key[c];
+                int x, p;
+                if (ka < kb) {
+                    if (kb < kc) { x = b; p = kb; }
+                    else if (ka < kc) { x = c; p = kc; }
+                    else { x = a; p = ka; }
+                } else if (ka < kc) { x = a; p = ka; }
+                else if (kb < kc) { x = c; p = kc; }
+                else { x = b; p = kb; }
+                if (lane == 0) {
+                    const uint16_t tk = key[f], ti = idx[f];
+                    key[f] = key[x]; idx[f] = idx[x];
+                    key[x] = tk; idx[x] = ti;
+                    sh.piv[g] = p;
                 }
-                if (l - cut > LEAF) {
-                    const int slot = atomicAdd(&sh.nnxt, 1);
-                    nxt[slot] = (uint32_t)cut | ((uint32_t)l << 16);
-                    dnxt[slot] = (uint8_t)(depth - 1);
+            }
+            __syncthreads();
+            const bool part = act && depth > 0;
+            // stretch of this wave: [f + gi*per, ...), per a multiple of 64
+            const int per = part ? ((l - f + gw - 1) / gw + SSA_WAVE - 1) / SSA_WAVE * SSA_WAVE : 0;
+            const int s0 = f + gi * per, s1 = min(s0 + per, l);
+            const int p = part ? sh.piv[g] : 0;
+            if (part) {
+                int cL = 0, cR = 0;
+                for (int base = s0; base < s1; base += SSA_WAVE) {
+                    const int i = base + lane;
+                    const bool in = i < s1;
+                    const int kv = in ? (int)key[i] : 0;
+                    cL += __popcll(wave_ballot(in && i > f && kv >= p));
+                    cR += __popcll(wave_ballot(in && kv <= p));
+                }
+                if (lane == 0) { sh.cnt[wid][0] = cL; sh.cnt[wid][1] = cR; }
+            }
+            __syncthreads();
+            if (part) {
+                int oL = 0, oR = 0, tL = 0, tR = 0;
+                for (int w = 0; w < gw; ++w) {
+                    const int cl = sh.cnt[g * gw + w][0], cr = sh.cnt[g * gw + w][1];
+                    if (w < gi) { oL += cl; oR += cr; }
+                    tL += cl;
+                    tR += cr;
+                }
+                int numL = oL, numR = oR;
+                for (int base = s0; base < s1; base += SSA_WAVE) {
+                    const int i = base + lane;
+                    const bool in = i < s1;
+                    const int kv = in ? (int)key[i] : 0;
+                    const bool isL = in && i > f && kv >= p;
+                    const bool isR = in && kv <= p;
+                    const uint64_t bL = wave_ballot(isL), bR = wave_ballot(isR);
+                    if (isL) TL[f + numL + lanes_below(bL)] = (uint16_t)i;
+                    if (isR) TR[f + numR + lanes_below(bR)] = (uint16_t)i;
+                    numL += __popcll(bL);
+                    numR += __popcll(bR);
+                }
+                if (gi == 0 && lane == 0) { sh.nL[g] = tL; sh.nR[g] = tR; }
+            }
+            __syncthreads();
+            if (part && gi == 0) {                    // s = #k with L_k < R_k
+                const int numL = sh.nL[g], numR = sh.nR[g];
+                int lo = 0, hi = numL < numR ? numL : numR;
+                while (lo < hi) {
+                    const int mid = (lo + hi + 1) >> 1;
+                    if ((int)TL[f + mid - 1] < (int)TR[f + numR - mid]) lo = mid; else hi = mid - 1;
+                }
+                int cut = 0x7fffffff;
+                if (lo < numL) cut = TL[f + lo];
+                if (lo > 0) { const int r = TR[f + numR - lo]; cut = r < cut ? r : cut; }
+                if (lane == 0) { sh.s[g] = lo; sh.cut[g] = cut; }
+            }
+            __syncthreads();
+            if (part) {
+                const int sw = sh.s[g], numR = sh.nR[g];
+                for (int k = gi * SSA_WAVE + lane; k < sw; k += gw * SSA_WAVE) {
+                    const int pa = TL[f + k], pb = TR[f + numR - 1 - k];
+                    const uint16_t tk = key[pa], ti = idx[pa];
+                    key[pa] = key[pb]; idx[pa] = idx[pb];
+                    key[pb] = tk; idx[pb] = ti;
+                }
+                if (gi == 0 && lane == 0) {
+                    const int cut = sh.cut[g];
+                    child(f, cut, depth - 1);
+                    child(cut, l, depth - 1);
+                }
+            }
+        } else {
+            // ---- wave mode: one wave per segment
+            for (int sgi = wid; sgi < ncur; sgi += NW) {
+                const int f = (int)(cur[sgi] & 0xffffu);
+                const int l = (int)(cur[sgi] >> 16);
+                const int depth = dcur[sgi];
+                if (depth == 0) {
+                    if (lane == 0) heap_sort_range(key, idx, f, l);
+                    wave_sync_lds();
+                    continue;
+                }
+                const int cut = wave_partition(key, idx, TL, TR, f, l);
+                if (lane == 0) {
+                    child(f, cut, depth - 1);
+                    child(cut, l, depth - 1);
                 }
             }
         }
@@ -339,27 +484,93 @@ bucket_sort_kernel(const uint16_t *ids, int n, int NB, int32_t *perm, int32_t *b
         uint8_t *td = dcur; dcur = dnxt; dnxt = td;
     }
     __syncthreads();
+    uint32_t *okv = gkv + (int64_t)row * n;
+    int32_t *pout = perm + (int64_t)row * n;
+    for (int i = tid; i < n; i += SORT_THREADS) {
+        okv[i] = (uint32_t)key[i] | ((uint32_t)idx[i] << 16);
+        pout[i] = idx[i];
+    }
+}
 
-    // final insertion sort: one leaf (run between consecutive boundary bits) per thread
-    for (int w = tid; w < (n + 31) / 32; w += SORT_THREADS) {
-        uint32_t word = bits[w];
-        while (word) {
-            const int bpos = __ffs(word) - 1;
-            word &= word - 1;
-            const int s0 = w * 32 + bpos;
-            if (s0 >= n) break;
-            // end = next boundary after s0
-            int e = n;
-            uint32_t rest = word;
-            if (rest) {
-                e = w * 32 + __ffs(rest) - 1;
-            } else {
-                for (int w2 = w + 1; w2 < (n + 31) / 32; ++w2) {
-                    if (bits[w2]) { e = w2 * 32 + __ffs(bits[w2]) - 1; break; }
+// ---------------------------------------------------------------- segments
+// Kernel B, one wavefront per listed segment (<= SEG_T keys), anywhere on the
+// chip: the segment's remaining introsort subtree (wave partitions above 64
+// keys, the register path below), then the final insertion sort of each leaf
+// (one leaf per lane; partitions leave max(left) <= min(right), so this equals
+// the reference's final insertion pass over the row), and its slice of perm.
+constexpr int SEG_WAVES = 4;
+constexpr int SEG_STACK = SEG_T / (LEAF + 1) + 2;
+
+__host__ __device__ constexpr int seg_lds_words() {
+    // key, idx, TL, TR (u16 x SEG_T each), bits, stack
+    return (4 * SEG_T) / 2 + (SEG_T / 32 + 1) + 2 * SEG_STACK;
+}
+
+__global__ void __launch_bounds__(SEG_WAVES * SSA_WAVE)
+sort_seg_kernel(const uint32_t *gkv, int n, const int4 *segs, const int *segcount, int32_t *perm) {
+    __shared__ uint32_t lds[SEG_WAVES * seg_lds_words()];
+    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / SSA_WAVE);
+    const int lane = lane_id();
+    uint32_t *w0 = lds + wid * seg_lds_words();
+    uint16_t *key = (uint16_t *)w0;
+    uint16_t *idx = key + SEG_T;
+    uint16_t *TL = idx + SEG_T;
+    uint16_t *TR = TL + SEG_T;
+    uint32_t *bits = (uint32_t *)(TR + SEG_T);
+    uint32_t *stk = bits + (SEG_T / 32 + 1);
+    uint32_t *sdep = stk + SEG_STACK;
+    const int count = *segcount;
+    const int stride = (int)gridDim.x * SEG_WAVES;
+    for (int sgi = (int)blockIdx.x * SEG_WAVES + wid; sgi < count; sgi += stride) {
+        const int4 e = segs[sgi];
+        const int row = e.x, f0 = e.y, m = e.z, depth0 = e.w;
+        const uint32_t *src = gkv + (int64_t)row * n + f0;
+        for (int i = lane; i < m; i += SSA_WAVE) {
+            const uint32_t v = src[i];
+            key[i] = (uint16_t)(v & 0xffffu);
+            idx[i] = (uint16_t)(v >> 16);
+        }
+        for (int w = lane; w < SEG_T / 32 + 1; w += SSA_WAVE) bits[w] = w == 0 ? 1u : 0u;
+        wave_sync_lds();
+        if (m > LEAF) {
+            int top = 1;
+            if (lane == 0) { stk[0] = (uint32_t)m << 16; sdep[0] = (uint32_t)depth0; }
+            wave_sync_lds();
+            while (top > 0) {
+                --top;
+                const uint32_t se = stk[top];
+                const int a = (int)(se & 0xffffu), b = (int)(se >> 16);
+                const int d = (int)sdep[top];
+                wave_sync_lds();
+                if (d == 0) {
+                    if (lane == 0) heap_sort_range(key, idx, a, b);
+                    wave_sync_lds();
+                    continue;
                 }
+                if (b - a <= SSA_WAVE) {
+                    wave_small_sort(key, idx, bits, a, b - a, d);
+                    continue;
+                }
+                const int cut = wave_partition(key, idx, TL, TR, a, b);
+                if (lane == 0) {
+                    atomicOr(&bits[cut >> 5], 1u << (cut & 31));
+                    if (cut - a > LEAF) { stk[top] = (uint32_t)a | ((uint32_t)cut << 16); sdep[top] = d - 1; }
+                }
+                if (cut - a > LEAF) ++top;
+                if (lane == 0 && b - cut > LEAF) {
+                    stk[top] = (uint32_t)cut | ((uint32_t)b << 16);
+                    sdep[top] = d - 1;
+                }
+                if (b - cut > LEAF) ++top;
+                wave_sync_lds();
             }
-            if (e > n) e = n;
-            for (int i = s0 + 1; i < e; ++i) {
+        }
+        // final insertion sort, one leaf per lane
+        for (int s0 = lane; s0 < m; s0 += SSA_WAVE) {
+            if (!((bits[s0 >> 5] >> (s0 & 31)) & 1u)) continue;
+            int e1 = s0 + 1;
+            while (e1 < m && !((bits[e1 >> 5] >> (e1 & 31)) & 1u)) ++e1;
+            for (int i = s0 + 1; i < e1; ++i) {
                 const uint16_t vk = key[i], vi = idx[i];
                 int j = i;
                 while (j > s0 && key[j - 1] > vk) {
@@ -371,47 +582,47 @@ bucket_sort_kernel(const uint16_t *ids, int n, int NB, int32_t *perm, int32_t *b
                 idx[j] = vi;
             }
         }
+        wave_sync_lds();
+        int32_t *pout = perm + (int64_t)row * n + f0;
+        for (int i = lane; i < m; i += SSA_WAVE) pout[i] = idx[i];
+        wave_sync_lds();
     }
-    __syncthreads();
+}
 
-    int32_t *pout = perm + (int64_t)row * n;
-    for (int i = tid; i < n; i += SORT_THREADS) pout[i] = idx[i];
-    for (int u = tid; u < NB; u += SORT_THREADS) {
-        int lo = 0, hi = n;          // lower_bound(u)
-        while (lo < hi) { const int mid = (lo + hi) >> 1; if (key[mid] < u) lo = mid + 1; else hi = mid; }
-        const int st = lo;
-        hi = n;                      // upper_bound(u)
-        while (lo < hi) { const int mid = (lo + hi) >> 1; if (key[mid] <= u) lo = mid + 1; else hi = mid; }
-        bstart[(int64_t)row * NB + u] = st;
-        bsize[(int64_t)row * NB + u] = lo - st;
-    }
+__global__ void sort_zero_kernel(int *p) {
+    if (threadIdx.x == 0) *p = 0;
 }
 
 }  // namespace
 
-// LDS plan for a row of n keys
-static void sort_plan(int n, int *cap, int *tl_in_lds, size_t *lds) {
-    const int c = n / (LEAF + 1) + 2;
-    const size_t base = ((size_t)4 * n + 15) / 16 * 16 + ((size_t)(n + 31) / 32 + 1) * 4 +
-                        (size_t)c * 8 + (size_t)c * 2;
+// LDS plan of kernel A for a row of n keys and NB buckets
+static void sort_plan(int n, int NB, int *cap, int *tl_in_lds, size_t *lds) {
+    const int c = n / (SEG_T + 1) + 2;
+    const size_t base = ((size_t)4 * n + 15) / 16 * 16 + (size_t)NB * 4 + (size_t)c * 8 +
+                        (size_t)c * 2;
     const size_t with_tl = (base + 15) / 16 * 16 + (size_t)4 * n;
     *cap = c;
     if (with_tl <= SSA_LDS_BYTES) { *tl_in_lds = 1; *lds = with_tl; }
     else { *tl_in_lds = 0; *lds = base; }
 }
 
+// scratch: the rows after kernel A (4 B per key), the segment list (16 B per
+// key at most), its counter, and the stopper lists when they do not fit LDS
+static int64_t al256(int64_t x) { return (x + 255) / 256 * 256; }
+
 int64_t ssa_sort_tmp_bytes(int rows, int n) {
     int cap, tl;
     size_t lds;
-    sort_plan(n, &cap, &tl, &lds);
-    return tl ? 0 : (int64_t)rows * 2 * n * (int64_t)sizeof(uint16_t);
+    sort_plan(n, 4096, &cap, &tl, &lds);
+    const int64_t rn = (int64_t)rows * n;
+    return al256(rn * 4) + al256(rn * 16) + 256 + (tl ? 0 : rn * 4);
 }
 
 int ssa_sort_supported(int n) {
     int cap, tl;
     size_t lds;
     if (n < 1 || n > 32768) return 0;
-    sort_plan(n, &cap, &tl, &lds);
+    sort_plan(n, 4096, &cap, &tl, &lds);
     return lds <= SSA_LDS_BYTES;
 }
 
@@ -422,13 +633,26 @@ int ssa_launch_bucket_sort(const uint16_t *ids, int rows, int n, int P, int32_t 
         return SSA_E_UNSUP;
     }
     if (rows == 0) return SSA_OK;
+    const int NB = 1 << P;
     int cap, tl;
     size_t lds;
-    sort_plan(n, &cap, &tl, &lds);
-    SSA_CHECK_HIP(hipFuncSetAttribute((const void *)bucket_sort_kernel,
+    sort_plan(n, NB, &cap, &tl, &lds);
+    const int64_t rn = (int64_t)rows * n;
+    char *t = (char *)tmp;
+    uint32_t *gkv = (uint32_t *)t;
+    int4 *segs = (int4 *)(t + al256(rn * 4));
+    int *segcount = (int *)(t + al256(rn * 4) + al256(rn * 16));
+    uint16_t *tl_tmp = (uint16_t *)(t + al256(rn * 4) + al256(rn * 16) + 256);
+    hipLaunchKernelGGL(sort_zero_kernel, dim3(1), dim3(64), 0, st, segcount);
+    SSA_CHECK_LAUNCH();
+    SSA_CHECK_HIP(hipFuncSetAttribute((const void *)sort_top_kernel,
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    hipLaunchKernelGGL(bucket_sort_kernel, dim3(rows), dim3(SORT_THREADS), lds, st, ids, n,
-                       1 << P, perm, bstart, bsize, tmp, tl, cap);
+    hipLaunchKernelGGL(sort_top_kernel, dim3(rows), dim3(SORT_THREADS), lds, st, ids, n, NB, perm,
+                       bstart, bsize, gkv, segs, segcount, tl_tmp, tl, cap);
+    SSA_CHECK_LAUNCH();
+    const int64_t waves = std::max<int64_t>(1, std::min<int64_t>(rn / 128, 8192));
+    hipLaunchKernelGGL(sort_seg_kernel, dim3((unsigned)ceil_div(waves, SEG_WAVES)),
+                       dim3(SEG_WAVES * SSA_WAVE), 0, st, gkv, n, segs, segcount, perm);
     SSA_CHECK_LAUNCH();
     return SSA_OK;
 }

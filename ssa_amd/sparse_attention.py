@@ -26,6 +26,7 @@ from typing import Optional, Tuple
 
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 
 from . import _lib
 
@@ -339,6 +340,49 @@ class SparseAttention(nn.Module):
             mode=_lib.GRAPH_FULL, q_proj=qp, k_proj=kp)
         return out, valid
 
+    def _fused_weight(self, mods):
+        """The weights of `mods` stacked along the output dimension.  Under
+        autograd they are concatenated on every call (gradients flow back to
+        each projection); otherwise the stack is cached until a weight's
+        storage or version changes."""
+        ws = [m.weight for m in mods]
+        if torch.is_grad_enabled() and any(w.requires_grad for w in ws):
+            return torch.cat(ws, 0)
+        key = tuple((w.data_ptr(), w._version, w.dtype, w.device) for w in ws)
+        cache = self.__dict__.setdefault("_wcat", {})
+        hit = cache.get(len(mods))
+        if hit is None or hit[0] != key:
+            with torch.no_grad():
+                hit = (key, torch.cat(ws, 0))
+            cache[len(mods)] = hit
+        return hit[1]
+
+    def _project(self, x, src, is_cross):
+        """q (B, H, N, d), k and v (B, n_kv, M, d) as views of one fused
+        projection GEMM (two when cross-attending): the same products as
+        Wq(x), Wk(src), Wv(src) (sparse_attention.py:1484-1486), without the
+        GQA expansion."""
+        hq = self.H * self.d_head
+        hk = self.n_kv * self.d_head
+        if not is_cross:
+            y = F.linear(x, self._fused_weight((self.Wq, self.Wk, self.Wv)))
+            qx, kx, vx = y[..., :hq], y[..., hq:hq + hk], y[..., hq + hk:]
+        else:
+            qx = self.Wq(x)
+            y = F.linear(src, self._fused_weight((self.Wk, self.Wv)))
+            kx, vx = y[..., :hk], y[..., hk:]
+        return self._split_q(qx), self._split_kv_compact(kx), self._split_kv_compact(vx)
+
+    def _graph_build(self, k, B, N, M, causal, is_cross):
+        """build_graph split into its key and query phases (same result)."""
+        _lib.require_device(k)
+        glob = self.glob_builder(M, k.device)
+        lb = self.lsh_builder
+        p_eff = lb.compute_effective_p(M, lb.C, lb.max_P)
+        return _lib.GraphBuild(B, self.H, N, k, lb.rand_proj, P=p_eff, T=lb.T, C=lb.C,
+                               top_k=self.lsh_k, window=self.config.window_size, causal=causal,
+                               is_cross=is_cross, total_k=self.K, glob=glob, mode=_lib.GRAPH_FULL)
+
     def apply_graph(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                     neighbors: torch.Tensor, valid: torch.Tensor) -> torch.Tensor:
         """sparse_gather_attention with this module's scale / dropout / fp32
@@ -363,9 +407,7 @@ class SparseAttention(nn.Module):
         src = key_value if is_cross else x
         M = src.shape[1]
         causal = self.config.causal and not is_cross
-        q = self._split_q(self.Wq(x))
-        k = self._split_kv_compact(self.Wk(src))
-        v = self._split_kv_compact(self.Wv(src))
+        q, k, v = self._project(x, src, is_cross)
         neighbors, valid = self.build_graph(q, k, N, M, B, x.device, causal, is_cross)
         out = self.apply_graph(q, k, v, neighbors, valid)
         out_proj = self.Wo(self._merge(out))

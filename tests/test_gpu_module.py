@@ -290,3 +290,58 @@ def test_recall_beats_random_and_grows_with_probes():
         rs.append(_recall(nb, va, q, k))
     assert rs[0] > 2 * 64 / 2048
     assert rs[1] > rs[0] and rs[2] > rs[1], rs
+
+
+@pytest.mark.parametrize("causal,cross", [(True, False), (False, False), (False, True)])
+def test_two_phase_build_on_a_side_stream_equals_single_call(causal, cross):
+    """The phased build (key hash, the key sort on a side stream, the query
+    phase after it, on one workspace) gives exactly the single-call graph, and
+    forward equals build + apply on its own fused projections."""
+    kw = dict(d_model=256, num_heads=4, num_kv_heads=2, num_neighbors=48, max_num_hashes=6,
+              window_size=5, num_global_tokens=2, causal=causal)
+    torch.manual_seed(3)
+    a = _attn(**kw).eval()
+    B, N, M = 2, 300, (420 if cross else 300)
+    x = torch.randn(B, N, 256, device=DEV)
+    src = torch.randn(B, M, 256, device=DEV) if cross else x
+    with torch.no_grad():
+        q, k, v = a._project(x, src, cross)
+        nb1, va1 = a.build_graph(q, k, N, M, B, DEV, causal, cross)
+        gb = a._graph_build(k, B, N, M, causal, cross)
+        gb.key_hash()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            gb.key_sort()
+        torch.cuda.current_stream().wait_stream(side)
+        nb2, va2 = gb.queries(q)
+        out_fwd, _ = a(x, key_value=src if cross else None)
+        out_ref = a.Wo(a._merge(a.apply_graph(q, k, v, nb1, va1)))
+    torch.cuda.synchronize()
+    assert torch.equal(nb1, nb2) and torch.equal(va1, va2)
+    assert torch.equal(out_fwd, out_ref)
+
+
+def test_fused_projection_matches_separate_projections():
+    """q, k, v from one fused GEMM equal Wq(x), Wk(x), Wv(x) to fp32 rounding,
+    and gradients reach every projection."""
+    kw = dict(d_model=256, num_heads=4, num_kv_heads=2, num_neighbors=32, max_num_hashes=4,
+              window_size=3, num_global_tokens=1, causal=True)
+    torch.manual_seed(5)
+    a = _attn(**kw)
+    x = torch.randn(2, 96, 256, device=DEV)
+    for cross in (False, True):
+        src = torch.randn(2, 80, 256, device=DEV) if cross else x
+        with torch.no_grad():
+            q, k, v = a._project(x, src, cross)
+            q2 = a._split_q(a.Wq(x))
+            k2 = a._split_kv_compact(a.Wk(src))
+            v2 = a._split_kv_compact(a.Wv(src))
+        for u, w in ((q, q2), (k, k2), (v, v2)):
+            assert torch.allclose(u, w, rtol=1e-5, atol=1e-5)
+    a.train()
+    out, _ = a(x)
+    out.float().pow(2).mean().backward()
+    for m in (a.Wq, a.Wk, a.Wv, a.Wo):
+        assert m.weight.grad is not None and torch.isfinite(m.weight.grad).all()
+        assert m.weight.grad.abs().sum() > 0
