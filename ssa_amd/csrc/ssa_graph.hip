@@ -350,7 +350,8 @@ __device__ __forceinline__ int64_t qb_order_key(const QbP &p, int inst, int64_t 
     return ((bk * p.R + r) * p.NS + t) * p.rep + h % p.rep;
 }
 
-// one block: tile list in that order, and the tile count
+// one block: the first tile of each instance in that order (kbase), and the
+// tile count
 __global__ void __launch_bounds__(256) qb_order_kernel(QbP p, int64_t nkeys) {
     __shared__ int32_t part[256];
     const int64_t bk_first = (int64_t)(p.bh0 / p.Hq) * p.Hkv + (p.bh0 % p.Hq) / p.rep;
@@ -378,36 +379,57 @@ __global__ void __launch_bounds__(256) qb_order_kernel(QbP p, int64_t nkeys) {
         p.kbase[k] = acc;
         acc += v;
     }
-    __syncthreads();
-    for (int inst = threadIdx.x; inst < p.ninst; inst += 256) {
-        int bh, r, t;
-        inst_decode(p, inst, bh, r, t);
-        const int b = bh / p.Hq, h = bh % p.Hq, g = h / p.rep;
-        const int64_t krow = ((int64_t)b * p.Hkv + g) * p.R + r;
-        int at = p.kbase[qb_order_key(p, inst, bk_first)];
-        for (int u = 0; u < p.NB; ++u) {
-            const int c = p.cnt[(int64_t)inst * p.NB + u];
-            if (c == 0 || p.bsize[krow * p.NB + u] == 0) continue;
+}
+
+// The tiles of one instance from its first tile (kbase): buckets in order,
+// up to TQ queries per tile; buckets without keys or queries have none.
+__device__ void qb_write_tiles(const QbP &p, int inst, int bh, int r, int t, int32_t *scan) {
+    const int b = bh / p.Hq, h = bh % p.Hq, g = h / p.rep;
+    const int64_t krow = ((int64_t)b * p.Hkv + g) * p.R + r;
+    const int64_t bk_first = (int64_t)(p.bh0 / p.Hq) * p.Hkv + (p.bh0 % p.Hq) / p.rep;
+    int carry = p.kbase[qb_order_key(p, inst, bk_first)];
+    for (int u0 = 0; u0 < p.NB; u0 += blockDim.x) {
+        const int u = u0 + threadIdx.x;
+        int c = 0, nt = 0;
+        if (u < p.NB) {
+            c = p.cnt[(int64_t)inst * p.NB + u];
+            nt = (c > 0 && p.bsize[krow * p.NB + u] > 0) ? (c + TQ - 1) / TQ : 0;
+        }
+        scan[threadIdx.x] = nt;
+        __syncthreads();
+        for (int o = 1; o < (int)blockDim.x; o <<= 1) {      // inclusive scan
+            const int y = threadIdx.x >= (unsigned)o ? scan[threadIdx.x - o] : 0;
+            __syncthreads();
+            scan[threadIdx.x] += y;
+            __syncthreads();
+        }
+        int at = carry + scan[threadIdx.x] - nt;
+        if (nt > 0) {
             const int aq = p.off[(int64_t)inst * p.NB + u];
-            for (int k = 0; k * TQ < c; ++k) {
-                int32_t *e = p.tiles + (int64_t)at * 4;
+            for (int k = 0; k < nt; ++k) {
+                int32_t *e = p.tiles + (int64_t)(at + k) * 4;
                 e[0] = inst;
                 e[1] = u;
                 e[2] = aq + k * TQ;
                 e[3] = min(TQ, c - k * TQ);
-                ++at;
             }
         }
+        carry += scan[blockDim.x - 1];
+        __syncthreads();
     }
 }
 
 __global__ void __launch_bounds__(256) qb_scatter_kernel(QbP p) {
     // rank of each query among the block's queries of its bucket, in position
     // order: per wave one ballot per distinct bucket, then the waves in order
-    extern __shared__ int32_t sc_smem[];   // [4][NB] per-wave counts
+    extern __shared__ int32_t sc_smem[];   // [4][NB] per-wave counts, then a scan buffer
     const int inst = blockIdx.y;
     int bh, r, t;
     inst_decode(p, inst, bh, r, t);
+    if (blockIdx.x == 0) {
+        qb_write_tiles(p, inst, bh, r, t, sc_smem);
+        __syncthreads();
+    }
     const int wid = threadIdx.x / SSA_WAVE;
     for (int x = threadIdx.x; x < 4 * p.NB; x += blockDim.x) sc_smem[x] = 0;
     __syncthreads();
@@ -730,6 +752,8 @@ __global__ void __launch_bounds__(256) rescore_mfma_kernel(RsP p) {
 //   rnk[st + c]  sorted index of the member at list slot c
 //   smin[st + i] smallest list slot among sorted members i.. (first future slot)
 //   inv[key]     permutation position of every key
+constexpr int LS_RANK_MIN = 128;   // lists at least this long are ranked through a bitmap
+
 struct LsP {
     const int32_t *perm, *bstart, *bsize;
     int32_t *sid, *rnk, *smin, *inv;
@@ -750,6 +774,62 @@ __global__ void __launch_bounds__(256) list_sort_kernel(LsP p) {
     const int64_t base = prow * p.M;
     const int32_t *pr = p.perm + base;
     for (int i = tid; i < sz; i += 256) p.inv[base + pr[st + i]] = st + i;
+    if (nv >= LS_RANK_MIN) {
+        // long lists: the rank of a member is the number of member ids below
+        // it, read off an M-bit map of the list with per-word prefix counts
+        const int W = (p.M + 31) / 32;
+        uint32_t *bmp = ls_key;                       // [W]
+        int32_t *pre = (int32_t *)(bmp + W);          // [W]
+        int32_t *sor = pre + W;                       // [nv] list slot of each rank
+        int32_t *wsum = sor + min(p.C, p.M);          // [4]
+        for (int w = tid; w < W; w += 256) bmp[w] = 0u;
+        __syncthreads();
+        for (int i = tid; i < nv; i += 256) {
+            const int id = pr[st + i];
+            atomicOr(&bmp[id >> 5], 1u << (id & 31));
+        }
+        __syncthreads();
+        const int per = (W + 255) / 256, w0 = tid * per;
+        int c = 0;
+        for (int w = w0; w < w0 + per && w < W; ++w) c += __popc(bmp[w]);
+        const int lane = lane_id(), wv = tid / SSA_WAVE;
+        int x = c;
+#pragma unroll
+        for (int o = 1; o < SSA_WAVE; o <<= 1) {
+            const int y = __shfl_up(x, o, SSA_WAVE);
+            if (lane >= o) x += y;
+        }
+        if (lane == SSA_WAVE - 1) wsum[wv] = x;
+        __syncthreads();
+        int acc = x - c;
+        for (int k = 0; k < wv; ++k) acc += wsum[k];
+        for (int w = w0; w < w0 + per && w < W; ++w) { pre[w] = acc; acc += __popc(bmp[w]); }
+        __syncthreads();
+        for (int i = tid; i < nv; i += 256) {
+            const int id = pr[st + i];
+            const int r = pre[id >> 5] + __popc(bmp[id >> 5] & ((1u << (id & 31)) - 1u));
+            p.sid[base + st + r] = id;
+            p.rnk[base + st + i] = r;
+            sor[r] = i;
+        }
+        __syncthreads();
+        if (tid < SSA_WAVE) {                      // suffix minimum of the list slots
+            int carry = p.C;
+            for (int hi = nv; hi > 0; hi -= SSA_WAVE) {
+                const int i = hi - SSA_WAVE + lane;
+                int cs = i >= 0 ? sor[i] : p.C;
+#pragma unroll
+                for (int o = 1; o < SSA_WAVE; o <<= 1) {
+                    const int y = __shfl_down(cs, o, SSA_WAVE);
+                    if (lane + o < SSA_WAVE) cs = min(cs, y);
+                }
+                cs = min(cs, carry);
+                if (i >= 0) p.smin[base + st + i] = cs;
+                carry = __shfl(cs, 0, SSA_WAVE);
+            }
+        }
+        return;
+    }
     // key id << 16 | list slot: ids < 2^15, slots < 2^16
     for (int i = tid; i < P2; i += 256)
         ls_key[i] = i < nv ? (((uint32_t)pr[st + i] << 16) | (uint32_t)i) : 0xffffffffu;
@@ -2340,7 +2420,8 @@ int keys_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws
         lp.M = D.M; lp.NB = D.NB; lp.C = D.C;
         int p2 = 1;
         while (p2 < std::min(D.C, D.M)) p2 <<= 1;
-        const size_t lds = (size_t)p2 * 4;
+        const size_t lds = std::max((size_t)p2 * 4,
+                                    (size_t)(2 * ((D.M + 31) / 32) + std::min(D.C, D.M) + 4) * 4);
         SSA_CHECK_HIP(hipFuncSetAttribute((const void *)list_sort_kernel,
                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
         hipLaunchKernelGGL(list_sort_kernel, dim3((unsigned)(D.BK * D.R * D.NB)), dim3(256), lds, st,
@@ -2384,7 +2465,8 @@ int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char 
             hipLaunchKernelGGL(qb_order_kernel, dim3(1), dim3(256), 0, st, qp, nkeys);
             SSA_CHECK_LAUNCH();
         }
-        hipLaunchKernelGGL(qb_scatter_kernel, gq, dim3(256), (size_t)D.NB * 16, st, qp);
+        hipLaunchKernelGGL(qb_scatter_kernel, gq, dim3(256), (size_t)std::max(D.NB * 16, 256 * 4),
+                           st, qp);
         SSA_CHECK_LAUNCH();
 
         RsP rp{};
