@@ -1069,7 +1069,7 @@ __device__ __forceinline__ void wave_compiler_fence() {
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
 }
 
-constexpr int SEL_CAP = 512;   // keys kept in LDS for the exact threshold search
+constexpr int SEL_CAP = 384;   // keys kept in LDS for the exact threshold search
 
 // Per-wave LDS of the select kernel, in 32-bit words:
 //   tab   [4*nch]     per 64-member chunk of a sorted list prefix: index of its
@@ -1081,15 +1081,20 @@ constexpr int SEL_CAP = 512;   // keys kept in LDS for the exact threshold searc
 //   bm    [words]     seen bitmap, later the merge bitmap
 //   ckey  [SEL_CAP+64] kept keys >= the lower bound; the last 64 entries take
 //                     the stores of lanes that append nothing
-//   cval  [SEL_CAP+64] key id of each compacted key
+//   cval  [SEL_CAP+64] key id of each compacted key (ckey and cval together span
+//                     at least `words`: the overflow path's second bitmap)
 //   gsc   [64]        score keys of glob[0..G-1] and key 0 (empty buckets)
 //   gid   [64]        the ids glob[0..G-1], 0
 //   LSH mode: ekey/eval/eslot [kk] the selected entries
 constexpr int SEL_BUF = SEL_CAP + 64;
-constexpr int SEL_PIPE = 4;            // chunks per group in pass 1
+constexpr int SEL_PIPE = 2;            // chunks per group in pass 1
+// ckey + cval, which also hold the overflow path's second seen bitmap
+__host__ __device__ inline int sel_buf_words(int words) {
+    return 2 * SEL_BUF > words ? 2 * SEL_BUF : words;
+}
 __host__ __device__ inline int sel_tab_entries(int nch) { return nch + 2 * SEL_PIPE; }
 __host__ __device__ inline int sel_lds_words(int nch, int words, int kk, bool lsh, int nlists) {
-    return (4 * sel_tab_entries(nch) + 4 * nlists + words + 2 * SEL_BUF + 128 +
+    return (4 * sel_tab_entries(nch) + 4 * nlists + words + sel_buf_words(words) + 128 +
             (lsh ? 3 * kk : 0) + 1) & ~1;
 }
 
@@ -1322,7 +1327,7 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     uint32_t *bm = (uint32_t *)(lst + nl);
     uint32_t *ckey = bm + p.words;
     uint32_t *cval = ckey + SEL_BUF;
-    uint32_t *gsc = cval + SEL_BUF;
+    uint32_t *gsc = ckey + sel_buf_words(p.words);
     int32_t *gid = (int32_t *)(gsc + 64);
     uint32_t *ekey = (uint32_t *)(gid + 64);
     uint32_t *eval = ekey + p.kk;
@@ -1434,7 +1439,8 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     // is raised to (a 16-bit floor of) the kk-th largest key in the buffer --
     // a subset of the stream -- and the buffer is filtered in place.
     const int kk = p.kk;
-    const int fill = SEL_CAP / 2;      // checked once per group of 4 chunks (<= 256 keys)
+    // checked once per group of SEL_PIPE chunks: a group adds at most 64 * SEL_PIPE keys
+    const int fill = SEL_CAP - SEL_PIPE * SSA_WAVE;
     int nkept = nkeep ? 1 : 0, cnt = 0;
     uint32_t lo = 0u;
     bool overflow = false;
@@ -1691,7 +1697,7 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     }
     if (btie && lane == 0 && p.tie_list) p.tie_list[atomicAdd(p.tie_count, 1)] = (int)rloc;
 
-    full_merge_emit(bm, p, n, row, f, (int32_t *)ckey, 2 * SEL_BUF);
+    full_merge_emit(bm, p, n, row, f, (int32_t *)ckey, sel_buf_words(p.words));
 }
 
 // ------------------------------------------------------------------ exact top-k replay
