@@ -358,19 +358,16 @@ class SparseAttention(nn.Module):
         return hit[1]
 
     def _project(self, x, src, is_cross):
-        """q (B, H, N, d), k and v (B, n_kv, M, d) as views of one fused
-        projection GEMM (two when cross-attending): the same products as
-        Wq(x), Wk(src), Wv(src) (sparse_attention.py:1484-1486), without the
-        GQA expansion."""
-        hq = self.H * self.d_head
+        """q (B, H, N, d), and k and v (B, n_kv, M, d) as views of one GEMM
+        against the stacked Wk/Wv weights: the same products as Wq(x),
+        Wk(src), Wv(src) (sparse_attention.py:1484-1486), without the GQA
+        expansion."""
         hk = self.n_kv * self.d_head
-        if not is_cross:
-            y = F.linear(x, self._fused_weight((self.Wq, self.Wk, self.Wv)))
-            qx, kx, vx = y[..., :hq], y[..., hq:hq + hk], y[..., hq + hk:]
-        else:
-            qx = self.Wq(x)
-            y = F.linear(src, self._fused_weight((self.Wk, self.Wv)))
-            kx, vx = y[..., :hk], y[..., hk:]
+        # q on its own, k and v stacked: measured faster at the bench workload
+        # (4096 tokens, d_model 4096, 8 kv heads) than one GEMM for all three
+        qx = self.Wq(x)
+        y = F.linear(src, self._fused_weight((self.Wk, self.Wv)))
+        kx, vx = y[..., :hk], y[..., hk:]
         return self._split_q(qx), self._split_kv_compact(kx), self._split_kv_compact(vx)
 
     def _graph_build(self, k, B, N, M, causal, is_cross):
