@@ -113,6 +113,13 @@ __device__ __forceinline__ uint32_t wave_reduce_dpp(uint32_t v) {
 __device__ __forceinline__ uint32_t wave_max_u(uint32_t v) { return wave_reduce_dpp<true>(v); }
 __device__ __forceinline__ uint32_t wave_min_u(uint32_t v) { return wave_reduce_dpp<false>(v); }
 
+// orders one wavefront's own LDS accesses across its lanes
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // ballot over the 64-lane wave
 __device__ __forceinline__ uint64_t wave_ballot(bool p) { return __ballot(p); }
 

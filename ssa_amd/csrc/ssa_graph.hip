@@ -60,6 +60,7 @@ struct Dims {
     int64_t Call, BH, BK;
     int nbh_chunk;
     int chunk;         // width of the reference's running top-k chunks (:903)
+    int Cs;            // score row stride: min(C, M) rounded up to 64 members
 };
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -264,6 +265,7 @@ struct QbP {
     int32_t *tcnt;          // tiles per instance
     int32_t *kbase;         // first tile of each order key
     int32_t *hcnt;          // per (instance, query block, bucket): count, then first position
+    int32_t *qpos;          // per (instance, query): position in qlist
     int N, R, NS, NB, Hq, Hkv, rep, bh0, ninst;
 };
 
@@ -451,6 +453,7 @@ __global__ void __launch_bounds__(256) qb_scatter_kernel(QbP p) {
         int pos = p.hcnt[((int64_t)inst * gridDim.x + blockIdx.x) * p.NB + u] + local;
         for (int w = 0; w < wid; ++w) pos += sc_smem[w * p.NB + u];
         p.qlist[(int64_t)inst * p.N + pos] = n;
+        p.qpos[(int64_t)inst * p.N + n] = pos;
     }
 }
 
@@ -459,10 +462,11 @@ struct RsP {
     const int32_t *tiles, *ntiles, *qlist, *sid, *bstart, *bsize;
     const void *q, *k;
     int64_t qsb, qsh, qsn, ksb, ksh, ksn;
-    uint32_t *S;       // score keys (score_key); slot = list * C + sorted member index
+    uint32_t *S;       // score keys (score_key): row (instance * N + qlist position) of C
     int N, M, R, NS, NB, C, Hq, Hkv, rep, bh0, causal;
-    int vec4;          // rows and list starts of S are 16-byte aligned (C % 4 == 0)
+    int Cs;            // score row stride (a multiple of 64)
     int k32;           // byte offsets of the K rows of a (batch, kv head) fit 32 bits
+    uint32_t *trash;   // 64 x 16 words that lanes without a query store to
     int64_t Call;
 };
 
@@ -506,7 +510,7 @@ __global__ void __launch_bounds__(256) rescore_kernel(RsP p) {
     if (tile < 0) return;
     const int32_t *e = p.tiles + (int64_t)tile * 4;
     const int inst = e[0], u = e[1], qb = e[2], qc = e[3];
-    const int t = inst % p.NS, r = (inst / p.NS) % p.R, bhl = inst / (p.NS * p.R);
+    const int r = (inst / p.NS) % p.R, bhl = inst / (p.NS * p.R);
     const int bh = p.bh0 + bhl;
     const int b = bh / p.Hq, h = bh % p.Hq, g = h / p.rep;
     const int64_t prow = ((int64_t)b * p.Hkv + g) * p.R + r;
@@ -523,7 +527,6 @@ __global__ void __launch_bounds__(256) rescore_kernel(RsP p) {
         const int i = x / D, c = x % D;
         Qs[i * LD + c] = i < qc ? to_f32(qbase[(int64_t)nidx[i] * p.qsn + c]) : 0.f;
     }
-    const int64_t slotbase = (int64_t)(r * p.NS + t) * p.C;
     const int ty = tid / 16, tx = tid % 16;
     for (int c0 = 0; c0 < nv; c0 += TC) {
         __syncthreads();
@@ -554,7 +557,7 @@ __global__ void __launch_bounds__(256) rescore_kernel(RsP p) {
         for (int a = 0; a < 4; ++a) {
             const int i = ty * 4 + a;
             if (i >= qc) continue;
-            uint32_t *srow = p.S + ((int64_t)bhl * p.N + nidx[i]) * p.Call + slotbase + c0;
+            uint32_t *srow = p.S + ((int64_t)inst * p.N + qb + i) * p.Cs + c0;
 #pragma unroll
             for (int bb = 0; bb < 4; ++bb) {
                 const int cc = tx + 16 * bb;
@@ -609,7 +612,7 @@ __global__ void __launch_bounds__(256) rescore_mfma_kernel(RsP p) {
     if (tile < 0) return;
     const int32_t *e = p.tiles + (int64_t)tile * 4;
     const int inst = e[0], u = e[1], qb = e[2], qc = e[3];
-    const int t = inst % p.NS, r = (inst / p.NS) % p.R, bhl = inst / (p.NS * p.R);
+    const int r = (inst / p.NS) % p.R, bhl = inst / (p.NS * p.R);
     const int bh = p.bh0 + bhl;
     const int b = bh / p.Hq, h = bh % p.Hq, g = h / p.rep;
     const int64_t prow = ((int64_t)b * p.Hkv + g) * p.R + r;
@@ -669,36 +672,24 @@ __global__ void __launch_bounds__(256) rescore_mfma_kernel(RsP p) {
             *reinterpret_cast<u32x4 *>(rs_lds + (BUF) * (64 * RB) + (x / SEGS) * RB +        \
                                        (x % SEGS) * 16) = sa[i];                             \
     }
-    const int64_t slotbase = (int64_t)(r * p.NS + t) * p.C;
-    uint32_t *srow = p.S + ((int64_t)bhl * p.N + nidx[qok ? qrow : 0]) * p.Call + slotbase;
     const int nsl = (nv + 63) / 64;
     RS_FETCH(0)
     RS_COMMIT(0)
     __syncthreads();
-    // score keys of the previous slice, stored at the top of the next
-    // iteration: the loads issued after them (and awaited by the commit) then
-    // find them long complete
-    u32x4 kq[4];
-    int cq = -1;
-#define RS_STORE_KEYS()                                                                      \
-    if (cq >= 0 && qok) {                                                                    \
-        _Pragma("unroll") for (int ct = 0; ct < 4; ++ct) {                                   \
-            const int cc = cq + ct * 16 + 4 * lg;                                            \
-            if (cc + 3 < nv && p.vec4) {                                                     \
-                *reinterpret_cast<u32x4 *>(srow + cc) = kq[ct];                              \
-            } else {                                                                         \
-                if (cc < nv) srow[cc] = kq[ct].x;                                            \
-                if (cc + 1 < nv) srow[cc + 1] = kq[ct].y;                                    \
-                if (cc + 2 < nv) srow[cc + 2] = kq[ct].z;                                    \
-                if (cc + 3 < nv) srow[cc + 3] = kq[ct].w;                                    \
-            }                                                                                \
-        }                                                                                    \
-    }
+    // Score rows are padded to a multiple of 64 members, so each lane stores
+    // its 4 x 4 keys as full 16-byte vectors (members past the cutoff land in
+    // the padding and are never read).  Every iteration issues exactly these
+    // stores after its loads, so the commit waits for the loads only.
+    // lanes without a query store into a scratch row of their own instead, so
+    // that the stores need no branch
+    uint32_t *srow = qok ? p.S + ((int64_t)inst * p.N + qb + qrow) * p.Cs + 4 * lg
+                         : p.trash + lane * 16;
+    const int cstep = qok ? 64 : 0;
     for (int j = 0; j < nsl; ++j) {
         const int c0 = 64 * j;
         const bool more = j + 1 < nsl;
-        RS_STORE_KEYS()
         if (more) { RS_FETCH(c0 + 64) }
+        u32x4 kq[4] = {};
         if (active) {
             const unsigned char *kl = rs_lds + (j & 1) * (64 * RB);
             auto frag = [&](int s, V (&kf)[4]) __attribute__((always_inline)) {
@@ -725,21 +716,24 @@ __global__ void __launch_bounds__(256) rescore_mfma_kernel(RsP p) {
                     acc[ct] = Mfma16<T>::mma(kf[s & 1][ct], qf[s], acc[ct]);
                 if (s + 2 < KS) frag(s + 2, kf[s & 1]);
             }
-            // lane (li, lg) holds candidates c0 + 16 ct + 4 lg + rr of query li
+            // lane (li, lg) holds members c0 + 16 ct + 4 lg + rr of query li
 #pragma unroll
             for (int ct = 0; ct < 4; ++ct)
                 kq[ct] = u32x4{score_key(acc[ct][0]), score_key(acc[ct][1]),
                                score_key(acc[ct][2]), score_key(acc[ct][3])};
-            cq = c0;
         }
+        // every wave stores (idle waves into the scratch rows): the same four
+        // stores on every path
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct)
+            *reinterpret_cast<u32x4 *>(srow + (qok ? 16 * ct : 4 * ct)) = kq[ct];
+        srow += cstep;
         // the other buffer was last read in iteration j - 1, before its barrier
         if (more) { RS_COMMIT((j + 1) & 1) }
         __syncthreads();
     }
-    RS_STORE_KEYS()
 #undef RS_FETCH
 #undef RS_COMMIT
-#undef RS_STORE_KEYS
 }
 
 // ------------------------------------------------------------------ sorted candidate lists
@@ -879,10 +873,12 @@ __global__ void __launch_bounds__(256) list_sort_kernel(LsP p) {
 // first slot C: none.  Sizes, cutoffs, starts and keys stay below 2^16.
 struct CutP {
     const uint16_t *qid;
-    const int32_t *perm, *bstart, *bsize, *sid, *smin;
+    const int32_t *perm, *bstart, *bsize, *sid, *smin, *qpos;
     const int64_t *glob;
     int4 *cut;
-    int N, M, R, NS, NB, C, Hq, Hkv, rep, bh0, G, causal, nlists;
+    int32_t *srix;     // per (row, list): offset of the query's score row in its head's
+                       // region of S (lists * N * C elements), in elements
+    int N, M, R, NS, NB, C, Cs, Hq, Hkv, rep, bh0, G, causal, nlists;
     int64_t rows;
 };
 
@@ -929,6 +925,8 @@ __global__ void __launch_bounds__(256) cut_kernel(CutP p) {
     }
     p.cut[x] = make_int4((int)(prow * p.M) + st, sz | (f << 16), cutoff | (st << 16),
                          first * 2 + real);
+    const int64_t inst = (rloc / p.N) * p.nlists + list;
+    p.srix[x] = (int32_t)(((int64_t)list * p.N + p.qpos[inst * p.N + n]) * p.Cs);
 }
 
 // ------------------------------------------------------------------ extra scores
@@ -1027,12 +1025,15 @@ struct SelP {
     const int32_t *perm, *bstart, *bsize;
     const int32_t *sid, *rnk, *inv;   // sorted list members, their ranks, key positions
     const int4 *cut;       // per (row, list): bucket offset, size/filler, cutoff/start, first
+    const int32_t *srix;   // per (row, list): offset of the query's score row in its head's
+                           // region of S
+    uint32_t head_bytes;   // bytes of one head's region of S (< 2^32)
     uint32_t nl_magic;     // ceil(2^32 / nlists): pair index / nlists as a high product
     const uint32_t *S;     // score keys (score_key), row-major (rows, Call)
     const void *q, *k;
     int64_t qsb, qsh, qsn, ksb, ksh, ksn;
     const int64_t *glob;
-    int N, M, d, R, NS, NB, C, CPL, nlists, Hq, Hkv, rep, G, kk, window, causal, cross, mode,
+    int N, M, d, R, NS, NB, C, Cs, CPL, nlists, Hq, Hkv, rep, G, kk, window, causal, cross, mode,
         total_k, Kw, Kout, bh0, words;
     int64_t Call, rows;
     int64_t *out_idx;
@@ -1048,11 +1049,6 @@ struct SelP {
 
 __device__ __forceinline__ void bm_set(uint32_t *bm, int v) { atomicOr(&bm[v >> 5], 1u << (v & 31)); }
 
-__device__ __forceinline__ void wave_lds_sync() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
 
 __device__ __forceinline__ int wave_excl_scan(int v) {
     const int lane = lane_id();
@@ -1334,13 +1330,14 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     uint32_t *eslot = eval + p.kk;
 
     const int n = (int)((uint32_t)rloc % (uint32_t)p.N);     // rows of a chunk < 2^31
+    const int bhl = (int)((uint32_t)rloc / (uint32_t)p.N);
+    const uint32_t *shead = p.S + (int64_t)bhl * nl * p.N * p.Cs;
     const int64_t row = (int64_t)p.bh0 * p.N + rloc;
     // scores the candidate lists do not carry (computed with the rescore's
     // arithmetic, so equal keys get equal scores): the query's own key and the
     // empty-bucket list glob ++ 0
     const float *arow = p.aux + rloc * p.NA;
     const uint32_t kself = CAUSAL ? score_key(arow[0]) : 0u;
-    const uint32_t *srow = p.S + rloc * p.Call;
     const int ng = min(p.G + 1, SSA_WAVE);
     for (int w = lane; w < p.words; w += SSA_WAVE) bm[w] = 0u;
 
@@ -1350,10 +1347,12 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     bool nkeep = false;                // the query's own key is kept
     bool nfound = !CAUSAL;
     const int4 *crow = p.cut + rloc * nl;
+    const int32_t *xrow = p.srix + rloc * nl;
     for (int l0 = 0; l0 < nl; l0 += SSA_WAVE) {
         const int list = l0 + lane;
         const bool in = list < nl;
         const int4 ct = in ? crow[list] : make_int4(0, 0, 0, 0);
+        const int so = in ? xrow[list] : 0;
         const int sz = ct.y & 0xffff, cutoff = ct.z & 0xffff, st = ct.z >> 16;
         if (in) lst[list] = make_int4(st, sz, ct.x - st, ct.y >> 16);
         const int nc = (in && sz > 0) ? (cutoff + SSA_WAVE - 1) / SSA_WAVE : 0;
@@ -1361,8 +1360,7 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
         for (int k = 0; k < nc; ++k) {
             const int c0 = k * SSA_WAVE;
             const uint64_t m = lanes_mask(cutoff - c0);
-            tab[at + k] = make_int4(ct.x + c0, (int)(uint32_t)m, list * p.C + c0,
-                                    (int)(uint32_t)(m >> 32));
+            tab[at + k] = make_int4(ct.x + c0, (int)(uint32_t)m, so + c0, (int)(uint32_t)(m >> 32));
         }
         nch += wave_sum_i(nc);
         any_empty = any_empty || wave_ballot(in && sz == 0) != 0ull;
@@ -1466,7 +1464,7 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     const __amdgpu_buffer_rsrc_t prs =
         __builtin_amdgcn_make_buffer_rsrc((void *)p.sid, (short)0, p.perm_bytes, SSA_BUF_FLAGS);
     const __amdgpu_buffer_rsrc_t srs =
-        __builtin_amdgcn_make_buffer_rsrc((void *)srow, (short)0, (int)(p.Call * 4), SSA_BUF_FLAGS);
+        __builtin_amdgcn_make_buffer_rsrc((void *)shead, (short)0, (int)p.head_bytes, SSA_BUF_FLAGS);
     const int lane4 = lane * 4;
     uint64_t mA[PIPE], mB[PIPE];
     int rA[PIPE], rB[PIPE];
@@ -1483,7 +1481,7 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
             const int x = __builtin_amdgcn_readfirstlane(d[u].x);
             const int z = __builtin_amdgcn_readfirstlane(d[u].z);
             raw[u] = __builtin_amdgcn_raw_buffer_load_b32(prs, lane4, x * 4, 0);
-            sk[u] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(srs, lane4, z * 4, 0);
+            sk[u] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(srs, lane4, (int)((uint32_t)z << 2), 0);
         }
     };
     auto absorb = [&](const uint64_t (&cm)[PIPE], const int (&craw)[PIPE],
@@ -1588,7 +1586,7 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
             uint32_t kv = 0u;
             if (in_mask(Min)) {
                 v = p.sid[__builtin_amdgcn_readfirstlane(d.x) + lane];
-                kv = srow[__builtin_amdgcn_readfirstlane(d.z) + lane];
+                kv = shead[(uint32_t)__builtin_amdgcn_readfirstlane(d.z) + lane];
             }
             walk_chunk(Min, v, kv, 65 + ci * SSA_WAVE + lane);
         }
@@ -1979,7 +1977,7 @@ topk_replay_kernel(SelP p, int chunk, int W) {
         for (int w = lane; w < p.words; w += SSA_WAVE) bm[w] = 0u;
         for (int t = lane; t < kk; t += SSA_WAVE) { A.key[t] = RP_NEGINF; A.cand[t] = 0; }
         const uint16_t *qids = p.qid + row * p.R * p.NS;
-        const uint32_t *srow = p.S + ((int64_t)bhl * p.N + n) * p.Call;
+        const int32_t *xrow = p.srix + rloc * p.nlists;
         rp_sync();
 
         for (int64_t s0 = 0; s0 < p.Call; s0 += chunk) {
@@ -2024,7 +2022,8 @@ topk_replay_kernel(SelP p, int chunk, int W) {
                     if (keep)
                         sk = (p.causal && v == n)
                                  ? kself
-                                 : srow[(int64_t)list * p.C + p.rnk[prow * p.M + st + c]];
+                                 : p.S[(int64_t)bhl * p.nlists * p.N * p.Cs + xrow[list] +
+                                       p.rnk[prow * p.M + st + c]];
                 } else {
                     // empty bucket: glob ++ 0, all valid; duplicates resolved in slot order
                     const int jg = c < ng - 1 ? c : ng - 1;
@@ -2092,8 +2091,9 @@ topk_replay_kernel(SelP p, int chunk, int W) {
 int supported_d(int d) { return d >= 4 && d <= 256 && (d & (d - 1)) == 0; }
 
 struct Layout {
-    int64_t kid, qid, perm, bstart, bsize, sorttmp, sid, rnk, smin, inv, cut, cnt, off, cur,
-        qlist, tiles, ntiles, tcnt, kbase, S,
+    int64_t kid, qid, perm, bstart, bsize, sorttmp, sid, rnk, smin, inv, cut, srix, qpos, cnt, off,
+        cur,
+        qlist, tiles, ntiles, tcnt, kbase, S, trash,
         tie_list, tie_count, aux, total;
 };
 
@@ -2116,6 +2116,8 @@ Layout plan(const Dims &D) {
     L.smin = take(D.BK * D.R * D.M * 4);
     L.inv = take(D.BK * D.R * D.M * 4);
     L.cut = take(nbh * D.N * D.nlists * 16);
+    L.srix = take(nbh * D.N * D.nlists * 4);
+    L.qpos = take(ninst * D.N * 4);
     L.cnt = take(ninst * D.NB * 4);
     L.off = take(ninst * D.NB * 4);
     L.cur = take(ninst * ceil_div(D.N, 256) * D.NB * 4);   // per-block counts / bases
@@ -2124,7 +2126,8 @@ Layout plan(const Dims &D) {
     L.ntiles = take(4);
     L.tcnt = take(ninst * 4);
     L.kbase = take((nbh / D.rep + 2) * D.R * D.NS * D.rep * 4);
-    L.S = take(nbh * D.N * D.Call * 4);
+    L.S = take(nbh * D.N * D.nlists * D.Cs * 4);
+    L.trash = take(64 * 16 * 4);
     L.tie_list = take(nbh * D.N * 4);
     L.tie_count = take(4);
     L.aux = take(nbh * D.N * (D.G + 2) * 4);
@@ -2164,6 +2167,7 @@ int make_dims(const ssa_graph_args *a, Dims &D, bool need_q = true) {
     D.NS = 1 + D.Tp;
     D.NB = 1 << a->P;
     D.C = a->C;
+    D.Cs = (int)ceil_div(std::min<int64_t>(a->C, a->M), 64) * 64;
     D.CPL = (int)ceil_div(a->C, SSA_WAVE);
     D.nlists = a->R * D.NS;
     D.G = a->G;
@@ -2192,8 +2196,13 @@ int make_dims(const ssa_graph_args *a, Dims &D, bool need_q = true) {
     }
     SSA_CHECK_ARG(!a->causal || a->N <= a->M, "build_graph: causal needs N <= M");
     // chunk the query heads so the score buffer stays near 2 GiB
-    const int64_t per_bh = (int64_t)a->N * D.Call * 4;
-    int64_t nbh = ((int64_t)2 << 30) / (per_bh > 0 ? per_bh : 1);
+    const int64_t per_bh = (int64_t)a->N * D.nlists * D.Cs * 4;
+    if (per_bh >= ((int64_t)4 << 30)) {
+        ssa_set_error("build_graph: one head's score table (N * R * id sets * C * 4 = %lld bytes) "
+                      "must stay below 4 GiB", (long long)per_bh);
+        return SSA_E_UNSUP;
+    }
+    int64_t nbh = ((int64_t)2 << 30) / per_bh;
     if (nbh < 1) nbh = 1;
     if (nbh > D.BH) nbh = D.BH;
     D.nbh_chunk = (int)nbh;
@@ -2453,6 +2462,7 @@ int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char 
         qp.off = (int32_t *)(ws + L.off);
         qp.cur = nullptr;
         qp.hcnt = (int32_t *)(ws + L.cur);
+        qp.qpos = (int32_t *)(ws + L.qpos);
         qp.qlist = (int32_t *)(ws + L.qlist);
         qp.tiles = (int32_t *)(ws + L.tiles);
         qp.ntiles = (int32_t *)(ws + L.ntiles);
@@ -2487,7 +2497,8 @@ int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char 
         rp.N = D.N; rp.M = D.M; rp.R = D.R; rp.NS = D.NS; rp.NB = D.NB; rp.C = D.C;
         rp.Hq = D.Hq; rp.Hkv = D.Hkv; rp.rep = D.rep; rp.bh0 = (int)bh0; rp.Call = D.Call;
         rp.causal = a->causal ? 1 : 0;
-        rp.vec4 = (D.C % 4 == 0) ? 1 : 0;
+        rp.Cs = D.Cs;
+        rp.trash = (uint32_t *)(ws + L.trash);
         {
             const int64_t el = a->q.dtype == SSA_F32 ? 4 : 2;
             rp.k32 = (rp.ksn * el < ((int64_t)1 << 24) &&
@@ -2514,7 +2525,9 @@ int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char 
         cp.smin = (const int32_t *)(ws + L.smin);
         cp.glob = a->glob;
         cp.cut = (int4 *)(ws + L.cut);
-        cp.N = D.N; cp.M = D.M; cp.R = D.R; cp.NS = D.NS; cp.NB = D.NB; cp.C = D.C;
+        cp.qpos = qp.qpos;
+        cp.srix = (int32_t *)(ws + L.srix);
+        cp.N = D.N; cp.M = D.M; cp.R = D.R; cp.NS = D.NS; cp.NB = D.NB; cp.C = D.C; cp.Cs = D.Cs;
         cp.Hq = D.Hq; cp.Hkv = D.Hkv; cp.rep = D.rep; cp.bh0 = (int)bh0; cp.G = D.G;
         cp.causal = a->causal ? 1 : 0; cp.nlists = D.nlists; cp.rows = (int64_t)nbh * D.N;
         hipLaunchKernelGGL(cut_kernel, dim3((unsigned)ceil_div(cp.rows * D.nlists, 256)), dim3(256),
@@ -2524,13 +2537,15 @@ int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char 
         SelP sp{};
         sp.qid = qp.qid; sp.perm = cp.perm; sp.bstart = rp.bstart; sp.bsize = rp.bsize;
         sp.sid = rp.sid; sp.rnk = (const int32_t *)(ws + L.rnk);
-        sp.inv = (const int32_t *)(ws + L.inv); sp.cut = cp.cut;
+        sp.inv = (const int32_t *)(ws + L.inv); sp.cut = cp.cut; sp.srix = cp.srix;
+        sp.head_bytes = (uint32_t)((int64_t)D.N * D.nlists * D.Cs * 4);
         sp.nl_magic = (uint32_t)((((uint64_t)1 << 32) + D.nlists - 1) / D.nlists);
         sp.S = rp.S; sp.q = a->q.ptr; sp.k = a->k.ptr;
         sp.qsb = a->q.sb; sp.qsh = a->q.sh; sp.qsn = a->q.sn;
         sp.ksb = a->k.sb; sp.ksh = a->k.sh; sp.ksn = a->k.sn;
         sp.glob = a->glob;
         sp.N = D.N; sp.M = D.M; sp.d = D.d; sp.R = D.R; sp.NS = D.NS; sp.NB = D.NB; sp.C = D.C;
+        sp.Cs = D.Cs;
         sp.CPL = D.CPL; sp.nlists = D.nlists; sp.Hq = D.Hq; sp.Hkv = D.Hkv; sp.rep = D.rep;
         sp.G = D.G; sp.kk = D.kk; sp.window = a->window; sp.causal = a->causal;
         sp.cross = a->is_cross; sp.mode = a->mode; sp.total_k = a->total_k; sp.Kw = D.Kw;
