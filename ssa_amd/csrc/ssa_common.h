@@ -151,6 +151,22 @@ __device__ __forceinline__ uint32_t score_key(float f) {
     const uint32_t k = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
     return k == 0 ? 1u : k;
 }
+// 16-bit score code: a monotone map of the score onto [0, 65535], with
+// `scale` taking +-(a bound of the query's scores) to the ends of the range and
+// NaN above everything.  Monotone (fma, clamp and truncation all are), so a
+// larger code means a larger score and equal scores share a code; scores that
+// share a code are told apart by their exact keys.
+__device__ __forceinline__ uint32_t score_code(float s, float scale) {
+    if (s != s) return 0xffffu;
+    return (uint32_t)fminf(fmaxf(fmaf(s, scale, 32768.f), 0.f), 65535.f);
+}
+// scale of a query with |q|^2 = q2 against keys with max |k|^2 = k2: every
+// score q.k lies within +-sqrt(q2 k2), which maps onto +-32767 (any positive
+// scale is correct, only how often codes tie depends on it)
+__device__ __forceinline__ float code_scale(float q2, float k2) {
+    const float sc = 32767.f / (sqrtf(q2) * sqrtf(k2));
+    return (sc > 0.f && sc < 3.0e38f) ? sc : 1.f;
+}
 __device__ __forceinline__ float key_score(uint32_t k) {
     uint32_t u = (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k;
     return __uint_as_float(u);

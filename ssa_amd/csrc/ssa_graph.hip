@@ -257,6 +257,59 @@ __global__ void fill_i32_kernel(int32_t *p, int64_t n, int32_t v) {
         p[i] = v;
 }
 
+// max |k|^2 over the keys of each (batch, kv head), as float bits (non-negative
+// floats order as their bit patterns); out must start at zero.  Block
+// (c, bk) takes rows [c * per, (c + 1) * per) of head bk and issues one atomic.
+struct KnP {
+    const void *k;
+    int64_t ksb, ksh, ksn;
+    int Hkv, M, d, per;
+    uint32_t *out;     // (B * Hkv)
+};
+
+// SEG > 0: rows of SEG 16-byte segments, one per lane (64 / SEG rows per
+// wavefront step); SEG == 0: one row per lane, element by element.
+template <typename T, int SEG>
+__global__ void __launch_bounds__(256) knorm_kernel(KnP p) {
+    __shared__ uint32_t red[4];
+    const int lane = lane_id(), wid = threadIdx.x / SSA_WAVE;
+    const int bk = blockIdx.y;
+    const int m0 = blockIdx.x * p.per, m1 = min(m0 + p.per, p.M);
+    const T *kh = (const T *)p.k + (bk / p.Hkv) * p.ksb + (bk % p.Hkv) * p.ksh;
+    float mx = 0.f;
+    if constexpr (SEG > 0) {
+        constexpr int RPW = SSA_WAVE / SEG;           // rows per wavefront step
+        constexpr int E = 16 / (int)sizeof(T);        // elements per segment
+#pragma unroll 4
+        for (int m = m0 + wid * RPW + lane / SEG; m < m1; m += 4 * RPW) {
+            T ev[E];
+            const uint4 w = *reinterpret_cast<const uint4 *>(kh + (int64_t)m * p.ksn + (lane % SEG) * E);
+            __builtin_memcpy(ev, &w, sizeof(w));
+            float s2 = 0.f;
+#pragma unroll
+            for (int e = 0; e < E; ++e) s2 = fmaf(to_f32(ev[e]), to_f32(ev[e]), s2);
+            // the row's sum, over its group of SEG lanes
+#pragma unroll
+            for (int o = 1; o < SEG; o <<= 1) s2 += __shfl_xor(s2, o, SSA_WAVE);
+            mx = fmaxf(mx, s2);
+        }
+    } else {
+        for (int m = m0 + (int)threadIdx.x; m < m1; m += 256) {
+            const T *row = kh + (int64_t)m * p.ksn;
+            float s2 = 0.f;
+            for (int c = 0; c < p.d; ++c) s2 = fmaf(to_f32(row[c]), to_f32(row[c]), s2);
+            mx = fmaxf(mx, s2);
+        }
+    }
+    const uint32_t wm = wave_max_u(__float_as_uint(mx));
+    if (lane == 0) red[wid] = wm;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t b = max(max(red[0], red[1]), max(red[2], red[3]));
+        atomicMax(&p.out[bk], b);
+    }
+}
+
 // ------------------------------------------------------------------ query bucketing
 struct QbP {
     const uint16_t *qid;
@@ -462,11 +515,14 @@ struct RsP {
     const int32_t *tiles, *ntiles, *qlist, *sid, *bstart, *bsize;
     const void *q, *k;
     int64_t qsb, qsh, qsn, ksb, ksh, ksn;
-    uint32_t *S;       // score keys (score_key): row (instance * N + qlist position) of C
+    uint16_t *S;       // 16-bit score codes (score_code): row (instance * N + qlist
+                       // position) of Cs
+    const float *aux;  // per query row: NA floats, the last the query's code scale
+    int NA;
     int N, M, R, NS, NB, C, Hq, Hkv, rep, bh0, causal;
     int Cs;            // score row stride (a multiple of 64)
     int k32;           // byte offsets of the K rows of a (batch, kv head) fit 32 bits
-    uint32_t *trash;   // 64 x 16 words that lanes without a query store to
+    uint16_t *trash;   // 64 x 32 bytes that lanes without a query store to
     int64_t Call;
 };
 
@@ -557,11 +613,12 @@ __global__ void __launch_bounds__(256) rescore_kernel(RsP p) {
         for (int a = 0; a < 4; ++a) {
             const int i = ty * 4 + a;
             if (i >= qc) continue;
-            uint32_t *srow = p.S + ((int64_t)inst * p.N + qb + i) * p.Cs + c0;
+            uint16_t *srow = p.S + ((int64_t)inst * p.N + qb + i) * p.Cs + c0;
+            const float sc = p.aux[((int64_t)bhl * p.N + nidx[i]) * p.NA + p.NA - 1];
 #pragma unroll
             for (int bb = 0; bb < 4; ++bb) {
                 const int cc = tx + 16 * bb;
-                if (c0 + cc < nv) srow[cc] = score_key(acc[a][bb]);
+                if (c0 + cc < nv) srow[cc] = (uint16_t)score_code(acc[a][bb], sc);
             }
         }
     }
@@ -590,15 +647,30 @@ template <> struct Mfma16<f16_t> {
 };
 
 // MFMA rescore of one tile (up to 64 queries of one bucket x the bucket's
-// candidates in ascending id order, up to the tile's cutoff).  The block stages each 64-candidate slice of K rows in LDS once
-// (double-buffered, rows padded by 16 bytes so the fragment reads are free of
-// bank conflicts); wave w scores queries 16w..16w+15 against the slice as
-// K . Q^T, so each lane holds 4 consecutive candidates of one query and writes
-// their score keys with one 16-byte store.
+// candidates in ascending id order, up to the tile's cutoff).  The block stages
+// each 64-candidate slice of K rows in LDS once (double-buffered, rows padded by
+// 16 bytes so the fragment reads are free of bank conflicts, in the row order of
+// rs_stage_row); wave w scores queries 16w..16w+15 against the slice as K . Q^T,
+// so each lane holds 2 x 8 consecutive candidates of one query and writes their
+// 16-bit score codes with two 16-byte stores.
 constexpr int RS_ROWB_PAD = 16;
 
 template <int D>
 __host__ __device__ constexpr int rs_row_bytes() { return D * 2 + RS_ROWB_PAD; }
+
+// LDS row of slice member m.  Tile ct of a slice multiplies LDS rows
+// 16 ct .. 16 ct + 15, and lane (li, lg) receives rows 4 lg .. 4 lg + 3 of each
+// tile; staging member 32 X + 8 a + 4 b + c at row 16 (2 X + b) + 4 a + c hands
+// lane (li, lg) the 8 consecutive members 32 X + 8 lg .. +7 in tiles 2 X, 2 X + 1,
+// which it stores as one 16-byte vector of 16-bit keys.
+__device__ __forceinline__ int rs_stage_row(int m) {
+    return (m & 0x23) | ((m & 0x04) << 2) | ((m & 0x18) >> 1);
+}
+
+// two 16-bit score codes, a at the lower address
+__device__ __forceinline__ uint32_t code_pair(float a, float b, float sc) {
+    return score_code(a, sc) | (score_code(b, sc) << 16);
+}
 
 template <typename T, int D>
 __global__ void __launch_bounds__(256) rescore_mfma_kernel(RsP p) {
@@ -642,6 +714,8 @@ __global__ void __launch_bounds__(256) rescore_mfma_kernel(RsP p) {
         }
     }
     const bool active = 16 * wid < qc;
+    // the query's code scale (written by the aux kernel)
+    const float qsc = qok ? p.aux[((int64_t)bhl * p.N + nidx[qrow]) * p.NA + p.NA - 1] : 1.f;
 
     // the tile's candidate ids; then, per 64-candidate slice j: the K rows of
     // slice j + 1 are loaded into registers, slice j (in LDS) is scored, its
@@ -669,27 +743,27 @@ __global__ void __launch_bounds__(256) rescore_mfma_kernel(RsP p) {
     _Pragma("unroll") for (int i = 0; i < PER; ++i) {                                        \
         const int x = tid + 256 * i;                                                         \
         if (x < 64 * SEGS)                                                                   \
-            *reinterpret_cast<u32x4 *>(rs_lds + (BUF) * (64 * RB) + (x / SEGS) * RB +        \
-                                       (x % SEGS) * 16) = sa[i];                             \
+            *reinterpret_cast<u32x4 *>(rs_lds + (BUF) * (64 * RB) +                          \
+                                       rs_stage_row(x / SEGS) * RB + (x % SEGS) * 16) = sa[i]; \
     }
     const int nsl = (nv + 63) / 64;
     RS_FETCH(0)
     RS_COMMIT(0)
     __syncthreads();
     // Score rows are padded to a multiple of 64 members, so each lane stores
-    // its 4 x 4 keys as full 16-byte vectors (members past the cutoff land in
-    // the padding and are never read).  Every iteration issues exactly these
-    // stores after its loads, so the commit waits for the loads only.
-    // lanes without a query store into a scratch row of their own instead, so
-    // that the stores need no branch
-    uint32_t *srow = qok ? p.S + ((int64_t)inst * p.N + qb + qrow) * p.Cs + 4 * lg
+    // its 2 x 8 score codes as full 16-byte vectors (members past the cutoff
+    // land in the padding and are never read).  Every iteration issues exactly
+    // these stores after its loads, so the commit waits for the loads only.
+    // Lanes without a query store into a scratch row of their own instead, so
+    // that the stores need no branch.
+    uint16_t *srow = qok ? p.S + ((int64_t)inst * p.N + qb + qrow) * p.Cs + 8 * lg
                          : p.trash + lane * 16;
     const int cstep = qok ? 64 : 0;
     for (int j = 0; j < nsl; ++j) {
         const int c0 = 64 * j;
         const bool more = j + 1 < nsl;
         if (more) { RS_FETCH(c0 + 64) }
-        u32x4 kq[4] = {};
+        u32x4 kq[2] = {};
         if (active) {
             const unsigned char *kl = rs_lds + (j & 1) * (64 * RB);
             auto frag = [&](int s, V (&kf)[4]) __attribute__((always_inline)) {
@@ -716,17 +790,20 @@ __global__ void __launch_bounds__(256) rescore_mfma_kernel(RsP p) {
                     acc[ct] = Mfma16<T>::mma(kf[s & 1][ct], qf[s], acc[ct]);
                 if (s + 2 < KS) frag(s + 2, kf[s & 1]);
             }
-            // lane (li, lg) holds members c0 + 16 ct + 4 lg + rr of query li
+            // lane (li, lg) holds members c0 + 32 X + 8 lg + 4 b + rr of query li
+            // in acc[2 X + b][rr]
 #pragma unroll
-            for (int ct = 0; ct < 4; ++ct)
-                kq[ct] = u32x4{score_key(acc[ct][0]), score_key(acc[ct][1]),
-                               score_key(acc[ct][2]), score_key(acc[ct][3])};
+            for (int X = 0; X < 2; ++X)
+                kq[X] = u32x4{code_pair(acc[2 * X][0], acc[2 * X][1], qsc),
+                              code_pair(acc[2 * X][2], acc[2 * X][3], qsc),
+                              code_pair(acc[2 * X + 1][0], acc[2 * X + 1][1], qsc),
+                              code_pair(acc[2 * X + 1][2], acc[2 * X + 1][3], qsc)};
         }
-        // every wave stores (idle waves into the scratch rows): the same four
+        // every wave stores (idle waves into the scratch rows): the same two
         // stores on every path
 #pragma unroll
-        for (int ct = 0; ct < 4; ++ct)
-            *reinterpret_cast<u32x4 *>(srow + (qok ? 16 * ct : 4 * ct)) = kq[ct];
+        for (int X = 0; X < 2; ++X)
+            *reinterpret_cast<u32x4 *>(srow + (qok ? 32 * X : 8 * X)) = kq[X];
         srow += cstep;
         // the other buffer was last read in iteration j - 1, before its barrier
         if (more) { RS_COMMIT((j + 1) & 1) }
@@ -940,8 +1017,9 @@ struct AuxP {
     const void *q, *k;
     int64_t qsb, qsh, qsn, ksb, ksh, ksn;
     const int64_t *glob;
-    int N, Hq, Hkv, rep, bh0, nbh, G, NA, causal;
-    float *out;        // (nbh * N, NA)
+    const uint32_t *knorm;   // max |k|^2 per (batch, kv head), float bits
+    int N, Hq, Hkv, rep, bh0, nbh, G, NA, causal, d;
+    float *out;        // (nbh * N, NA): q.k_n, q.k_glob[0..G-1], q.k_0, code scale
 };
 
 template <typename T, int D>
@@ -973,6 +1051,22 @@ __global__ void __launch_bounds__(256) aux_mfma_kernel(AuxP p) {
     // operand roles as in the rescore (keys as A, queries as B): lane (li, lg)
     // receives C[4 lg + rr][li] = score of key row 4 lg + rr for query n0 + li
     float *ob = p.out + ((int64_t)bhl * p.N + n0) * p.NA;
+    {
+        // the query's code scale from |q|^2 (lanes lg hold quarters of the row)
+        float q2 = 0.f;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            T qe[8];
+            __builtin_memcpy(qe, &qa[s], sizeof(qe));
+#pragma unroll
+            for (int e = 0; e < 8; ++e) q2 = fmaf(to_f32(qe[e]), to_f32(qe[e]), q2);
+        }
+        q2 += __shfl_xor(q2, 16, SSA_WAVE);
+        q2 += __shfl_xor(q2, 32, SSA_WAVE);
+        if (lg == 0 && okq)
+            ob[(int64_t)li * p.NA + p.NA - 1] =
+                code_scale(q2, __uint_as_float(p.knorm[b * p.Hkv + g]));
+    }
     if (p.causal) {            // key row li is key n0 + li: the diagonal is q_n . k_n
         V kb[KS];
 #pragma unroll
@@ -1011,8 +1105,14 @@ __global__ void __launch_bounds__(256) aux_valu_kernel(AuxP p) {
     const int bh = p.bh0 + (int)(rloc / p.N);
     const int b = bh / p.Hq, h = bh % p.Hq, g = h / p.rep;
     if (a == 0 && !p.causal) return;
-    const int key = a == 0 ? n : (a - 1 < p.G ? (int)p.glob[a - 1] : 0);
     const T *qr = (const T *)p.q + b * p.qsb + h * p.qsh + (int64_t)n * p.qsn;
+    if (a == p.NA - 1) {               // the query's code scale
+        float q2 = 0.f;
+        for (int c = 0; c < D; ++c) q2 = fmaf(to_f32(qr[c]), to_f32(qr[c]), q2);
+        p.out[idx] = code_scale(q2, __uint_as_float(p.knorm[b * p.Hkv + g]));
+        return;
+    }
+    const int key = a == 0 ? n : (a - 1 < p.G ? (int)p.glob[a - 1] : 0);
     const T *kr = (const T *)p.k + b * p.ksb + g * p.ksh + (int64_t)key * p.ksn;
     float acc = 0.f;
     for (int c = 0; c < D; ++c) acc = fmaf(to_f32(qr[c]), to_f32(kr[c]), acc);
@@ -1029,7 +1129,8 @@ struct SelP {
                            // region of S
     uint32_t head_bytes;   // bytes of one head's region of S (< 2^32)
     uint32_t nl_magic;     // ceil(2^32 / nlists): pair index / nlists as a high product
-    const uint32_t *S;     // score keys (score_key), row-major (rows, Call)
+    const uint16_t *S;     // score-key prefixes (score_key >> 16), rows as the rescore wrote
+    int mfma;              // the rescore used MFMA k-steps (else one fmaf chain over d)
     const void *q, *k;
     int64_t qsb, qsh, qsn, ksb, ksh, ksn;
     const int64_t *glob;
@@ -1048,6 +1149,76 @@ struct SelP {
 };
 
 __device__ __forceinline__ void bm_set(uint32_t *bm, int v) { atomicOr(&bm[v >> 5], 1u << (v & 31)); }
+
+// index of the k-th (0-based) set bit of b (k < popcount(b))
+__device__ __forceinline__ int nth_set_bit(uint32_t b, int k) {
+    int pos = 0;
+#pragma unroll
+    for (int sh = 16; sh >= 1; sh >>= 1) {
+        const int c = __popc(b & ((1u << sh) - 1u));
+        const bool up = k >= c;
+        k = up ? k - c : k;
+        b = up ? b >> sh : b;
+        pos = up ? pos + sh : pos;
+    }
+    return pos;
+}
+
+// Exact score keys of one query row qr against the keys v of the lanes with
+// `want` set (0 elsewhere), computed with the arithmetic of the rescore that
+// wrote the table, whose 16-bit prefixes they extend: MFMA k-steps of 32 with
+// the keys as A rows and the query as every B column (the wanted lanes taken 16
+// at a time, in lane order), or one fmaf chain over d.  kb: the kv head's K rows.
+template <typename T>
+__device__ uint32_t exact_keys(const SelP &p, const T *qr, const T *kb, int v, bool want) {
+    const int lane = lane_id();
+    if constexpr (!std::is_same<T, float>::value) {
+        if (p.mfma) {
+            using V = typename Mfma16<T>::vec;
+            const uint64_t wm = wave_ballot(want);
+            const int li = lane & 15, lg = lane >> 4;
+            const int KS = (p.d + 31) >> 5;
+            const int rank = lanes_below(wm);
+            const int total = __popcll(wm);
+            const uint32_t wlo = (uint32_t)wm, whi = (uint32_t)(wm >> 32);
+            const int clo = __popc(wlo);
+            uint32_t out = 0u;
+            for (int g0 = 0; g0 < total; g0 += 16) {
+                const int j = g0 + li;             // A row li: the j-th wanted lane
+                const bool ok = j < total;
+                const int src = !ok ? 0 : (j < clo ? nth_set_bit(wlo, j)
+                                                   : 32 + nth_set_bit(whi, j - clo));
+                const int vid = __shfl(v, src, SSA_WAVE);
+                const T *kr = kb + (int64_t)(ok ? vid : 0) * p.ksn;
+                f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+                for (int s = 0; s < KS; ++s) {
+                    const int e0 = 32 * s + 8 * lg;
+                    const V a = (ok && e0 < p.d)
+                                    ? __builtin_bit_cast(V, *reinterpret_cast<const uint4 *>(kr + e0))
+                                    : __builtin_bit_cast(V, make_uint4(0, 0, 0, 0));
+                    const V b = e0 < p.d
+                                    ? __builtin_bit_cast(V, *reinterpret_cast<const uint4 *>(qr + e0))
+                                    : __builtin_bit_cast(V, make_uint4(0, 0, 0, 0));
+                    acc = Mfma16<T>::mma(a, b, acc);
+                }
+                // lane (li, lg) holds rows 4 lg .. 4 lg + 3, every column alike:
+                // row r is read from lane 16 (r / 4) + r % 4, which offers acc[li % 4]
+                const int sel = li & 3;
+                const float x = sel == 0 ? acc[0] : sel == 1 ? acc[1] : sel == 2 ? acc[2] : acc[3];
+                const int r = (rank - g0) & 15;
+                const float y = __shfl(x, 16 * (r >> 2) + (r & 3), SSA_WAVE);
+                if (want && rank >= g0 && rank < g0 + 16) out = score_key(y);
+            }
+            return out;
+        }
+    }
+    float acc = 0.f;
+    if (want) {
+        const T *kr = kb + (int64_t)v * p.ksn;
+        for (int c = 0; c < p.d; ++c) acc = fmaf(to_f32(qr[c]), to_f32(kr[c]), acc);
+    }
+    return want ? score_key(acc) : 0u;
+}
 
 
 __device__ __forceinline__ int wave_excl_scan(int v) {
@@ -1149,20 +1320,6 @@ __device__ __forceinline__ int wave_incl_max(int v) {
     return v;
 }
 
-// index of the k-th (0-based) set bit of b (k < popcount(b))
-__device__ __forceinline__ int nth_set_bit(uint32_t b, int k) {
-    int pos = 0;
-#pragma unroll
-    for (int sh = 16; sh >= 1; sh >>= 1) {
-        const int c = __popc(b & ((1u << sh) - 1u));
-        const bool up = k >= c;
-        k = up ? k - c : k;
-        b = up ? b >> sh : b;
-        pos = up ? pos + sh : pos;
-    }
-    return pos;
-}
-
 // FULL mode tail (merge_neighbors, sparse_attention.py:966-1089): `bm` holds
 // the selected LSH keys; adds the window (:368-376), the globals, key 0 when a
 // -inf slot at or past G falls back to it (:948-957), removes the query itself
@@ -1249,12 +1406,14 @@ __device__ void full_merge_emit(uint32_t *bm, const SelP &p, int n, int64_t row,
     }
 }
 
-// Exact kk-th largest of the cnt compacted keys (all >= lo): the threshold
-// thr, how many keys equal to it are needed (need), and whether more equal
-// keys than needed exist (btie).  NK keys per lane cover cnt.
+// kk-th largest of the cnt compacted keys, known to lie in [lo, hi] and
+// resolved down to bit lo_bit: the threshold thr, how many keys equal to it
+// are needed (need), and whether more equal keys than needed exist (btie).
+// NK keys per lane cover cnt.
 template <int NK>
 __device__ __forceinline__ void sel_threshold(const uint32_t *ckey, int cnt, int kk, uint32_t lo,
-                                              uint32_t &thr, int &need, bool &btie) {
+                                              uint32_t hi, int lo_bit, uint32_t &thr, int &need,
+                                              bool &btie) {
     const int lane = lane_id();
     uint32_t cv[NK];
 #pragma unroll
@@ -1269,7 +1428,7 @@ __device__ __forceinline__ void sel_threshold(const uint32_t *ckey, int cnt, int
     }
     mx = wave_max_u(mx);
     mn = wave_min_u(mn);
-    thr = kth_search(cv, kk, lo > mn ? lo : mn, mx, 0);
+    thr = kth_search(cv, kk, lo > mn ? lo : mn, hi < mx ? hi : mx, lo_bit);
     int ge = 0, gt = 0;
 #pragma unroll
     for (int i = 0; i < NK; ++i) {
@@ -1278,6 +1437,41 @@ __device__ __forceinline__ void sel_threshold(const uint32_t *ckey, int cnt, int
     }
     need = kk - gt;
     btie = ge - gt > need;
+}
+
+// Entries of the buffer whose codes tie at the kk-th place (bit i of ebits:
+// entry lane + 64 i is one, and now holds its exact key): the need-th largest
+// exact key among them decides.  Each such entry is rewritten to
+// pf | 2 / 1 / 0 (above / equal to / below that key), and the threshold
+// becomes pf | 1 with `need` of those equal to it taken, so the selection
+// compares codes everywhere else.
+template <int NK>
+__device__ __forceinline__ void sel_boundary(uint32_t *ckey, int ebits, uint32_t pf, int &need,
+                                             bool &btie) {
+    const int lane = lane_id();
+    uint32_t xv[NK];
+    uint32_t mx = 0u, mn = 0xffffffffu;
+#pragma unroll
+    for (int i = 0; i < NK; ++i) {
+        xv[i] = ((ebits >> i) & 1) ? ckey[lane + SSA_WAVE * i] : 0u;
+        mx = xv[i] > mx ? xv[i] : mx;
+        mn = (xv[i] != 0u && xv[i] < mn) ? xv[i] : mn;
+    }
+    mx = wave_max_u(mx);
+    mn = wave_min_u(mn);
+    const uint32_t xthr = kth_search(xv, need, mn, mx, 0);
+    int gt = 0, eq = 0;
+#pragma unroll
+    for (int i = 0; i < NK; ++i) {
+        gt += __popcll(wave_ballot(xv[i] > xthr));
+        eq += __popcll(wave_ballot(xv[i] == xthr));
+    }
+#pragma unroll
+    for (int i = 0; i < NK; ++i)
+        if ((ebits >> i) & 1)
+            ckey[lane + SSA_WAVE * i] = pf | (xv[i] > xthr ? 2u : (xv[i] == xthr ? 1u : 0u));
+    need -= gt;
+    btie = eq > need;
 }
 
 // One wavefront per query row.  The reference scans the query's candidate
@@ -1331,13 +1525,24 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
 
     const int n = (int)((uint32_t)rloc % (uint32_t)p.N);     // rows of a chunk < 2^31
     const int bhl = (int)((uint32_t)rloc / (uint32_t)p.N);
-    const uint32_t *shead = p.S + (int64_t)bhl * nl * p.N * p.Cs;
+    const uint16_t *shead = p.S + (int64_t)bhl * nl * p.N * p.Cs;
     const int64_t row = (int64_t)p.bh0 * p.N + rloc;
+    // exact keys (where codes tie) of this query row: its q row and its kv
+    // head's K rows are located only on those rare paths
+    auto exact = [&](int v, bool want) {
+        const int bh = p.bh0 + bhl;
+        const int hq = bh % p.Hq;
+        const T *qr = (const T *)p.q + (bh / p.Hq) * p.qsb + hq * p.qsh + (int64_t)n * p.qsn;
+        const T *kb = (const T *)p.k + (bh / p.Hq) * p.ksb + (hq / p.rep) * p.ksh;
+        return exact_keys<T>(p, qr, kb, v, want);
+    };
     // scores the candidate lists do not carry (computed with the rescore's
     // arithmetic, so equal keys get equal scores): the query's own key and the
     // empty-bucket list glob ++ 0
     const float *arow = p.aux + rloc * p.NA;
+    const float qsc = arow[p.NA - 1];          // the query's code scale
     const uint32_t kself = CAUSAL ? score_key(arow[0]) : 0u;
+    const uint32_t cself = CAUSAL ? score_code(arow[0], qsc) : 0u;
     const int ng = min(p.G + 1, SSA_WAVE);
     for (int w = lane; w < p.words; w += SSA_WAVE) bm[w] = 0u;
 
@@ -1378,9 +1583,10 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     if (lane < 2 * SEL_PIPE) tab[nch + lane] = make_int4(0, 0, 0, 0);   // empty tail chunks
     // glob ++ 0 (:711-737): ids and score keys, lane j holding entry j
     int greg_id = 0;
-    uint32_t greg_sc = 0u;
+    uint32_t greg_sc = 0u, greg_c = 0u;
     if (any_empty && lane < ng) {
         greg_sc = score_key(arow[1 + lane]);
+        greg_c = score_code(arow[1 + lane], qsc);
         greg_id = lane < p.G ? (int)p.glob[lane] : 0;
         gsc[lane] = greg_sc;
         gid[lane] = greg_id;
@@ -1442,14 +1648,15 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     int nkept = nkeep ? 1 : 0, cnt = 0;
     uint32_t lo = 0u;
     bool overflow = false;
+    // the buffer holds 16-bit score codes in the high half of each key
     if (nkeep) {
-        if (lane == 0) { ckey[0] = kself; cval[0] = (uint32_t)n; }
+        if (lane == 0) { ckey[0] = cself << 16; cval[0] = (uint32_t)n; }
         cnt = 1;
     }
     if (any_empty) {                   // glob ++ 0; the query's own key is settled
         uint64_t Min = lanes_mask(min(p.C, ng));
         if (CAUSAL) Min &= ~wave_ballot(greg_id == n);
-        sel_absorb(bm, ckey, cval, Min, greg_id, greg_sc, lo, cnt, nkept);
+        sel_absorb(bm, ckey, cval, Min, greg_id, greg_c << 16, lo, cnt, nkept);
     }
     // Chunks are processed PIPE at a time; the loads of the next group are
     // issued before the current group is deduplicated, so a wave always has
@@ -1465,7 +1672,7 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
         __builtin_amdgcn_make_buffer_rsrc((void *)p.sid, (short)0, p.perm_bytes, SSA_BUF_FLAGS);
     const __amdgpu_buffer_rsrc_t srs =
         __builtin_amdgcn_make_buffer_rsrc((void *)shead, (short)0, (int)p.head_bytes, SSA_BUF_FLAGS);
-    const int lane4 = lane * 4;
+    const int lane4 = lane * 4, lane2 = lane * 2;
     uint64_t mA[PIPE], mB[PIPE];
     int rA[PIPE], rB[PIPE];
     uint32_t sA[PIPE], sB[PIPE];
@@ -1481,7 +1688,8 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
             const int x = __builtin_amdgcn_readfirstlane(d[u].x);
             const int z = __builtin_amdgcn_readfirstlane(d[u].z);
             raw[u] = __builtin_amdgcn_raw_buffer_load_b32(prs, lane4, x * 4, 0);
-            sk[u] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(srs, lane4, (int)((uint32_t)z << 2), 0);
+            sk[u] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(srs, lane2, (int)((uint32_t)z << 1), 0)
+                    << 16;
         }
     };
     auto absorb = [&](const uint64_t (&cm)[PIPE], const int (&craw)[PIPE],
@@ -1557,8 +1765,17 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     const int nk = nkept;
 
     // re-walk the kept keys (rare path: the buffer overflowed, so it is free
-    // to hold a fresh seen bitmap)
-    auto walk_kept = [&](auto &&fn) {
+    // to hold a fresh seen bitmap).  A key comes as (xm 0) its code << 16;
+    // (1) its exact key if its code is pfx, else 0; (2) its code << 16, with
+    // the low bits 2 / 1 / 0 if its code is pfx and its exact key is above /
+    // equal to / below xthr; (3) its exact key.
+    auto walk_kept = [&](int xm, uint32_t pfx, uint32_t xthr, auto &&fn) {
+        auto kv_of = [&](uint32_t c, uint32_t x) -> uint32_t {
+            if (xm == 3) return x;
+            if (xm == 1) return c == pfx ? x : 0u;
+            if (xm == 2 && c == pfx) return (c << 16) | (x > xthr ? 2u : (x == xthr ? 1u : 0u));
+            return c << 16;
+        };
         uint32_t *bm2 = ckey;
         wave_lds_sync();
         for (int w = lane; w < p.words; w += SSA_WAVE) bm2[w] = 0u;
@@ -1566,7 +1783,7 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
         for (int L = lane; L < nl; L += SSA_WAVE)
             if (lst[L].w >= 0) bm_set(bm2, lst[L].w);
         wave_lds_sync();
-        if (nkeep) fn(lane == 0, kself, n, 0);
+        if (nkeep) fn(lane == 0, kv_of(cself, kself), n, 0);
         auto walk_chunk = [&](uint64_t Min, int v, uint32_t kv, int slot) {
             const uint32_t bit = 1u << (v & 31);
             uint32_t old = 0u;
@@ -1576,20 +1793,43 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
         if (any_empty) {
             uint64_t Min = lanes_mask(min(p.C, ng));
             if (CAUSAL) Min &= ~wave_ballot(greg_id == n);
-            walk_chunk(Min, greg_id, greg_sc, 1 + lane);
+            walk_chunk(Min, greg_id, kv_of(greg_c, greg_sc), 1 + lane);
         }
         for (int ci = 0; ci < nch; ++ci) {
             const int4 d = tab[ci];
             const uint64_t Min = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane(d.w) << 32) |
                                  (uint32_t)__builtin_amdgcn_readfirstlane(d.y);
             int v = 0;
-            uint32_t kv = 0u;
+            uint32_t c = 0u;
             if (in_mask(Min)) {
                 v = p.sid[__builtin_amdgcn_readfirstlane(d.x) + lane];
-                kv = shead[(uint32_t)__builtin_amdgcn_readfirstlane(d.z) + lane];
+                c = shead[(uint32_t)__builtin_amdgcn_readfirstlane(d.z) + lane];
             }
-            walk_chunk(Min, v, kv, 65 + ci * SSA_WAVE + lane);
+            const bool xw = in_mask(Min) && (xm == 3 || (xm != 0 && c == pfx));
+            uint32_t x = 0u;
+            if (wave_ballot(xw) != 0ull) x = exact(v, xw);
+            walk_chunk(Min, v, kv_of(c, x), 65 + ci * SSA_WAVE + lane);
         }
+    };
+    // kk2-th largest key of the kept stream as walk mode xm gives it, over bits
+    // hi_bit .. lo_bit (above them: t0), with how many keys lie above it and on it
+    auto walk_search = [&](int xm, uint32_t pfx, int kk2, uint32_t t0, int hi_bit, int lo_bit,
+                           int &gt, int &ge) {
+        for (int bit = hi_bit; bit >= lo_bit; --bit) {
+            const uint32_t cand = t0 | (1u << bit);
+            int c = 0;
+            walk_kept(xm, pfx, 0u, [&](bool keep, uint32_t kv, int, int) {
+                c += __popcll(wave_ballot(keep & (kv >= cand)));
+            });
+            if (c >= kk2) t0 = cand;
+        }
+        ge = 0;
+        gt = 0;
+        walk_kept(xm, pfx, 0u, [&](bool keep, uint32_t kv, int, int) {
+            ge += __popcll(wave_ballot(keep & (kv >= t0)));
+            gt += __popcll(wave_ballot(keep & (kv > t0)));
+        });
+        return t0;
     };
 
     // ---- threshold
@@ -1597,34 +1837,73 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     int need = 0;
     bool btie = false;                 // several kept keys equal the kk-th one
     const bool compacted = !overflow;  // every key >= the threshold is in ckey
-    if (nk > kk) {
-        if (compacted) {
-            // keys held per lane: as few as the buffer needs
-            if (cnt <= 2 * SSA_WAVE)
-                sel_threshold<2>(ckey, cnt, kk, lo, thr, need, btie);
-            else if (cnt <= 4 * SSA_WAVE)
-                sel_threshold<4>(ckey, cnt, kk, lo, thr, need, btie);
-            else
-                sel_threshold<SEL_CAP / SSA_WAVE>(ckey, cnt, kk, lo, thr, need, btie);
-        } else {
-            // rare: exact search over the whole kept stream (one walk per bit)
-            uint32_t t0 = 0u;
-            for (int bit = 31; bit >= 0; --bit) {
-                const uint32_t cand = t0 | (1u << bit);
-                int c = 0;
-                walk_kept([&](bool keep, uint32_t kv, int, int) {
-                    c += __popcll(wave_ballot(keep & (kv >= cand)));
-                });
-                if (c >= kk) t0 = cand;
+    uint32_t wpfx = 0x10000u, wxthr = 0u;   // overflow path: the code resolved by exact keys
+    // kk-th largest buffered key in [base, top], resolved down to bit lo_bit;
+    // keys held per lane: as few as the buffer needs
+    auto threshold = [&](uint32_t base, uint32_t top, int lo_bit) {
+        if (cnt <= 2 * SSA_WAVE)
+            sel_threshold<2>(ckey, cnt, kk, base, top, lo_bit, thr, need, btie);
+        else if (cnt <= 4 * SSA_WAVE)
+            sel_threshold<4>(ckey, cnt, kk, base, top, lo_bit, thr, need, btie);
+        else
+            sel_threshold<SEL_CAP / SSA_WAVE>(ckey, cnt, kk, base, top, lo_bit, thr, need, btie);
+    };
+    // exact keys of the buffered entries whose key is `only` (every entry: 0);
+    // bit i of the result: lane's entry lane + 64 i now holds its exact key
+    auto exact_buffer = [&](uint32_t only) {
+        int ebits = 0;
+        for (int i = 0; i * SSA_WAVE < cnt; ++i) {
+            const int e = lane + SSA_WAVE * i;
+            const bool in = e < cnt && (only == 0u || ckey[e] == only);
+            if (wave_ballot(in) == 0ull) continue;
+            const uint32_t x = exact(in ? (int)cval[e] : 0, in);
+            if (in) {
+                ckey[e] = x;
+                ebits |= 1 << i;
             }
-            thr = t0;
-            int ge = 0, gt = 0;
-            walk_kept([&](bool keep, uint32_t kv, int, int) {
-                ge += __popcll(wave_ballot(keep & (kv >= thr)));
-                gt += __popcll(wave_ballot(keep & (kv > thr)));
-            });
+        }
+        wave_lds_sync();
+        return ebits;
+    };
+    if (compacted) {
+        if (LSH_MODE) {
+            // LSH mode ranks the selected keys by score: exact keys throughout
+            exact_buffer(0u);
+            if (nk > kk) threshold(0u, 0xffffffffu, 0);
+        } else if (nk > kk) {
+            threshold(lo, 0xffffffffu, 16);
+            if (btie) {
+                // more buffered codes equal the kk-th than are needed: the
+                // exact keys of those entries decide among them
+                const int ebits = exact_buffer(thr);
+                if (cnt <= 2 * SSA_WAVE)
+                    sel_boundary<2>(ckey, ebits, thr, need, btie);
+                else if (cnt <= 4 * SSA_WAVE)
+                    sel_boundary<4>(ckey, ebits, thr, need, btie);
+                else
+                    sel_boundary<SEL_CAP / SSA_WAVE>(ckey, ebits, thr, need, btie);
+                thr |= 1u;
+                wave_lds_sync();
+            }
+        }
+    } else if (nk > kk) {
+        // rare: search the whole kept stream, one walk per bit
+        int gt, ge;
+        if (LSH_MODE) {
+            thr = walk_search(3, 0u, kk, 0u, 31, 0, gt, ge);
             need = kk - gt;
             btie = ge - gt > need;
+        } else {
+            thr = walk_search(0, 0u, kk, 0u, 31, 16, gt, ge);      // over the codes
+            need = kk - gt;
+            if (ge - gt > need) {
+                // codes tie at the kk-th place: exact keys among that code
+                wpfx = thr >> 16;
+                wxthr = walk_search(1, wpfx, need, 0u, 31, 0, gt, ge);
+                need -= gt;
+                btie = ge - gt > need;
+                thr |= 1u;
+            }
         }
     }
     if (btie && lane == 0 && p.ties) atomicAdd(p.ties, 1);
@@ -1667,7 +1946,7 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
             take(sel, kv, v, e);           // compacted index: increasing in stream order
         }
     } else {
-        walk_kept([&](bool keep, uint32_t kv, int v, int slot) {
+        walk_kept(LSH_MODE ? 3 : 2, wpfx, wxthr, [&](bool keep, uint32_t kv, int v, int slot) {
             take(decide(keep, kv), kv, v, slot);
         });
     }
@@ -1977,7 +2256,8 @@ topk_replay_kernel(SelP p, int chunk, int W) {
         for (int w = lane; w < p.words; w += SSA_WAVE) bm[w] = 0u;
         for (int t = lane; t < kk; t += SSA_WAVE) { A.key[t] = RP_NEGINF; A.cand[t] = 0; }
         const uint16_t *qids = p.qid + row * p.R * p.NS;
-        const int32_t *xrow = p.srix + rloc * p.nlists;
+        const T *qr = (const T *)p.q + b * p.qsb + h * p.qsh + (int64_t)n * p.qsn;
+        const T *kb = (const T *)p.k + b * p.ksb + g * p.ksh;
         rp_sync();
 
         for (int64_t s0 = 0; s0 < p.Call; s0 += chunk) {
@@ -2018,12 +2298,11 @@ topk_replay_kernel(SelP p, int chunk, int W) {
                                 keep = !seen && lane == (int)(__ffsll((long long)nm) - 1);
                         }
                     }
-                    // scores are stored by the member's rank in the sorted list
-                    if (keep)
-                        sk = (p.causal && v == n)
-                                 ? kself
-                                 : p.S[(int64_t)bhl * p.nlists * p.N * p.Cs + xrow[list] +
-                                       p.rnk[prow * p.M + st + c]];
+                    // exact keys with the rescore's arithmetic (the table holds
+                    // only their prefixes); the query itself scores as in aux
+                    const bool xk = keep && !(p.causal && v == n);
+                    const uint32_t ex = exact_keys<T>(p, qr, kb, v, xk);
+                    if (keep) sk = xk ? ex : kself;
                 } else {
                     // empty bucket: glob ++ 0, all valid; duplicates resolved in slot order
                     const int jg = c < ng - 1 ? c : ng - 1;
@@ -2094,7 +2373,7 @@ struct Layout {
     int64_t kid, qid, perm, bstart, bsize, sorttmp, sid, rnk, smin, inv, cut, srix, qpos, cnt, off,
         cur,
         qlist, tiles, ntiles, tcnt, kbase, S, trash,
-        tie_list, tie_count, aux, total;
+        tie_list, tie_count, aux, knorm, total;
 };
 
 int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
@@ -2126,11 +2405,12 @@ Layout plan(const Dims &D) {
     L.ntiles = take(4);
     L.tcnt = take(ninst * 4);
     L.kbase = take((nbh / D.rep + 2) * D.R * D.NS * D.rep * 4);
-    L.S = take(nbh * D.N * D.nlists * D.Cs * 4);
+    L.S = take(nbh * D.N * D.nlists * D.Cs * 2);
     L.trash = take(64 * 16 * 4);
     L.tie_list = take(nbh * D.N * 4);
     L.tie_count = take(4);
-    L.aux = take(nbh * D.N * (D.G + 2) * 4);
+    L.aux = take(nbh * D.N * (D.G + 3) * 4);
+    L.knorm = take(D.BK * 4);
     L.total = o;
     return L;
 }
@@ -2196,9 +2476,9 @@ int make_dims(const ssa_graph_args *a, Dims &D, bool need_q = true) {
     }
     SSA_CHECK_ARG(!a->causal || a->N <= a->M, "build_graph: causal needs N <= M");
     // chunk the query heads so the score buffer stays near 2 GiB
-    const int64_t per_bh = (int64_t)a->N * D.nlists * D.Cs * 4;
+    const int64_t per_bh = (int64_t)a->N * D.nlists * D.Cs * 2;
     if (per_bh >= ((int64_t)4 << 30)) {
-        ssa_set_error("build_graph: one head's score table (N * R * id sets * C * 4 = %lld bytes) "
+        ssa_set_error("build_graph: one head's score table (N * R * id sets * C * 2 = %lld bytes) "
                       "must stay below 4 GiB", (long long)per_bh);
         return SSA_E_UNSUP;
     }
@@ -2417,6 +2697,30 @@ int keys_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws
     if (phases & SSA_PHASE_KEY_HASH) {
         rc = launch_hash<T>(D, a, L, ws, st, true);
         if (rc) return rc;
+        // max |k|^2 per (batch, kv head): the query code scales derive from it
+        KnP kp{};
+        kp.k = a->k.ptr; kp.ksb = a->k.sb; kp.ksh = a->k.sh; kp.ksn = a->k.sn;
+        kp.Hkv = D.Hkv; kp.M = D.M; kp.d = D.d;
+        kp.out = (uint32_t *)(ws + L.knorm);
+        hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(256), 0, st, (int32_t *)kp.out,
+                           (int64_t)D.BK, 0);
+        SSA_CHECK_LAUNCH();
+        if (D.BK * D.M > 0) {
+            const int seg = (int)((int64_t)D.d * (int64_t)sizeof(T) / 16);
+            const bool vec = view_aligned16(a->k, (int)sizeof(T)) && D.d * (int)sizeof(T) % 16 == 0 &&
+                             seg >= 4 && seg <= 32;
+            // about 256 blocks, at least 64 rows each
+            const int64_t nc = std::max<int64_t>(
+                1, std::min<int64_t>(ceil_div(256, D.BK), ceil_div(D.M, 64)));
+            kp.per = (int)ceil_div(D.M, nc);
+            const dim3 grid((unsigned)ceil_div(D.M, kp.per), (unsigned)D.BK);
+            if (vec && seg == 4) hipLaunchKernelGGL((knorm_kernel<T, 4>), grid, dim3(256), 0, st, kp);
+            else if (vec && seg == 8) hipLaunchKernelGGL((knorm_kernel<T, 8>), grid, dim3(256), 0, st, kp);
+            else if (vec && seg == 16) hipLaunchKernelGGL((knorm_kernel<T, 16>), grid, dim3(256), 0, st, kp);
+            else if (vec && seg == 32) hipLaunchKernelGGL((knorm_kernel<T, 32>), grid, dim3(256), 0, st, kp);
+            else hipLaunchKernelGGL((knorm_kernel<T, 0>), grid, dim3(256), 0, st, kp);
+            SSA_CHECK_LAUNCH();
+        }
     }
     if (!(phases & SSA_PHASE_KEY_SORT)) return SSA_OK;
     rc = ssa_launch_bucket_sort((const uint16_t *)(ws + L.kid), (int)(D.BK * D.R), D.M, D.P,
@@ -2493,29 +2797,33 @@ int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char 
         rp.q = a->q.ptr; rp.k = a->k.ptr;
         rp.qsb = a->q.sb; rp.qsh = a->q.sh; rp.qsn = a->q.sn;
         rp.ksb = a->k.sb; rp.ksh = a->k.sh; rp.ksn = a->k.sn;
-        rp.S = (uint32_t *)(ws + L.S);
+        rp.S = (uint16_t *)(ws + L.S);
         rp.N = D.N; rp.M = D.M; rp.R = D.R; rp.NS = D.NS; rp.NB = D.NB; rp.C = D.C;
         rp.Hq = D.Hq; rp.Hkv = D.Hkv; rp.rep = D.rep; rp.bh0 = (int)bh0; rp.Call = D.Call;
         rp.causal = a->causal ? 1 : 0;
         rp.Cs = D.Cs;
-        rp.trash = (uint32_t *)(ws + L.trash);
+        rp.trash = (uint16_t *)(ws + L.trash);
         {
             const int64_t el = a->q.dtype == SSA_F32 ? 4 : 2;
             rp.k32 = (rp.ksn * el < ((int64_t)1 << 24) &&
                       ((int64_t)D.M * rp.ksn + D.d) * el < ((int64_t)1 << 31)) ? 1 : 0;
         }
-        const int64_t grid = 8 * ceil_div((int64_t)ninst * (ceil_div(D.N, TQ) + D.NB), 8);
-        rc = rescore_dispatch<T>(D.d, rp, grid, st);
-        if (rc) return rc;
+        // aux first: the rescore codes its scores with the query scales it writes
         AuxP ap{};
         ap.q = a->q.ptr; ap.k = a->k.ptr;
         ap.qsb = a->q.sb; ap.qsh = a->q.sh; ap.qsn = a->q.sn;
         ap.ksb = a->k.sb; ap.ksh = a->k.sh; ap.ksn = a->k.sn;
         ap.glob = a->glob;
+        ap.knorm = (const uint32_t *)(ws + L.knorm);
         ap.N = D.N; ap.Hq = D.Hq; ap.Hkv = D.Hkv; ap.rep = D.rep; ap.bh0 = (int)bh0;
-        ap.nbh = nbh; ap.G = D.G; ap.NA = D.G + 2; ap.causal = a->causal;
+        ap.nbh = nbh; ap.G = D.G; ap.NA = D.G + 3; ap.causal = a->causal; ap.d = D.d;
         ap.out = (float *)(ws + L.aux);
         rc = aux_dispatch<T>(D.d, rescore_uses_mfma<T>(D.d, rp), ap, st);
+        if (rc) return rc;
+        rp.aux = ap.out;
+        rp.NA = ap.NA;
+        const int64_t grid = 8 * ceil_div((int64_t)ninst * (ceil_div(D.N, TQ) + D.NB), 8);
+        rc = rescore_dispatch<T>(D.d, rp, grid, st);
         if (rc) return rc;
 
         CutP cp{};
@@ -2538,7 +2846,8 @@ int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char 
         sp.qid = qp.qid; sp.perm = cp.perm; sp.bstart = rp.bstart; sp.bsize = rp.bsize;
         sp.sid = rp.sid; sp.rnk = (const int32_t *)(ws + L.rnk);
         sp.inv = (const int32_t *)(ws + L.inv); sp.cut = cp.cut; sp.srix = cp.srix;
-        sp.head_bytes = (uint32_t)((int64_t)D.N * D.nlists * D.Cs * 4);
+        sp.head_bytes = (uint32_t)((int64_t)D.N * D.nlists * D.Cs * 2);
+        sp.mfma = rescore_uses_mfma<T>(D.d, rp) ? 1 : 0;
         sp.nl_magic = (uint32_t)((((uint64_t)1 << 32) + D.nlists - 1) / D.nlists);
         sp.S = rp.S; sp.q = a->q.ptr; sp.k = a->k.ptr;
         sp.qsb = a->q.sb; sp.qsh = a->q.sh; sp.qsn = a->q.sn;
