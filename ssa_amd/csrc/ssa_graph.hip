@@ -1489,9 +1489,13 @@ __device__ __forceinline__ void sel_boundary(uint32_t *ckey, int ebits, uint32_t
 // What remains is order-free, so each list contributes only its members below
 // the query (causal; all otherwise) in ascending id order, whose scores the
 // rescore wrote contiguously, plus glob ++ 0 for an empty bucket:
-//  pass 1  dedup by test-and-set of the key's bit in LDS; the kept members of
-//          each 64-member chunk as one ballot; kept keys >= a lower bound
-//          compacted (key, id) into LDS;
+//  pass 1  members whose key is below a running lower bound are dropped
+//          first (a key scores the same in every list, so each of its
+//          occurrences is dropped alike); the rest are deduplicated by a
+//          test-and-set of the key's bit in LDS, and the kept ones compacted
+//          (key, id) into LDS.  The count of kept keys is exact while the
+//          bound is 0; once it is raised, at least kk distinct keys lie above
+//          it, which is all the selection needs of the count;
 //  bound   the kk-th largest buffered key over the top 16 bits raises the
 //          lower bound whenever the buffer fills (the buffer is a subset of the
 //          stream);
@@ -1663,10 +1667,10 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     // one group of member ids and scores in flight (two register sets, A and
     // B, alternate so that no loaded value is copied).  Loads are unconditional
     // raw buffer loads (scalar chunk offset, constant lane offset): lanes past
-    // a chunk's members read in-range data or 0.  The group's descriptor
-    // reads, and its bitmap test-and-sets, are issued back to back: LDS
-    // operations of a wave complete in order, so each chunk still sees the
-    // bits the chunks before it set.
+    // a chunk's members read in-range data or 0.  The group's bitmap
+    // test-and-sets are issued back to back: LDS operations of a wave
+    // complete in order, so each chunk still sees the bits the chunks before
+    // it set.
     constexpr int PIPE = SEL_PIPE;
     const __amdgpu_buffer_rsrc_t prs =
         __builtin_amdgcn_make_buffer_rsrc((void *)p.sid, (short)0, p.perm_bytes, SSA_BUF_FLAGS);
@@ -1676,17 +1680,25 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     uint64_t mA[PIPE], mB[PIPE];
     int rA[PIPE], rB[PIPE];
     uint32_t sA[PIPE], sB[PIPE];
+    // descriptors of 64 chunks at a time, lane j holding chunk (window + j);
+    // a chunk's fields are read with a lane select, so no LDS read waits in
+    // front of each group's loads.  Chunks past the table read as empty.
+    int dwin = 0;
+    const int ntab = nch + 2 * SEL_PIPE;
+    int4 dl = lane < ntab ? tab[lane] : make_int4(0, 0, 0, 0);
     auto fetch = [&](int ci0, uint64_t (&m)[PIPE], int (&raw)[PIPE], uint32_t (&sk)[PIPE])
         __attribute__((always_inline)) {
-        int4 d[PIPE];
-#pragma unroll
-        for (int u = 0; u < PIPE; ++u) d[u] = tab[ci0 + u];     // the tail holds empty chunks
+        if ((ci0 & ~(SSA_WAVE - 1)) != dwin) {      // groups never straddle a window
+            dwin = ci0 & ~(SSA_WAVE - 1);
+            dl = dwin + lane < ntab ? tab[dwin + lane] : make_int4(0, 0, 0, 0);
+        }
 #pragma unroll
         for (int u = 0; u < PIPE; ++u) {
-            m[u] = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane(d[u].w) << 32) |
-                   (uint32_t)__builtin_amdgcn_readfirstlane(d[u].y);
-            const int x = __builtin_amdgcn_readfirstlane(d[u].x);
-            const int z = __builtin_amdgcn_readfirstlane(d[u].z);
+            const int j = (ci0 + u) & (SSA_WAVE - 1);
+            m[u] = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(dl.w, j) << 32) |
+                   (uint32_t)__builtin_amdgcn_readlane(dl.y, j);
+            const int x = __builtin_amdgcn_readlane(dl.x, j);
+            const int z = __builtin_amdgcn_readlane(dl.z, j);
             raw[u] = __builtin_amdgcn_raw_buffer_load_b32(prs, lane4, x * 4, 0);
             sk[u] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(srs, lane2, (int)((uint32_t)z << 1), 0)
                     << 16;
@@ -1695,17 +1707,18 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     auto absorb = [&](const uint64_t (&cm)[PIPE], const int (&craw)[PIPE],
                       const uint32_t (&csk)[PIPE]) __attribute__((always_inline)) {
         uint32_t old[PIPE], bit[PIPE];
+        uint64_t lm[PIPE];
 #pragma unroll
         for (int u = 0; u < PIPE; ++u) {
             bit[u] = 1u << (craw[u] & 31);
             old[u] = 0u;
-            if (in_mask(cm[u])) old[u] = atomicOr(&bm[craw[u] >> 5], bit[u]);
+            lm[u] = cm[u] & wave_ballot(csk[u] >= lo);
+            if (in_mask(lm[u])) old[u] = atomicOr(&bm[craw[u] >> 5], bit[u]);
         }
 #pragma unroll
         for (int u = 0; u < PIPE; ++u) {
-            const uint64_t km = cm[u] & wave_ballot((old[u] & bit[u]) == 0u);
-            nkept += __popcll(km);
-            const uint64_t am = km & wave_ballot(csk[u] >= lo);
+            const uint64_t am = lm[u] & wave_ballot((old[u] & bit[u]) == 0u);
+            nkept += __popcll(am);
             const int pos = cnt + lanes_below(am);
             const int dst = (in_mask(am) & (pos < SEL_CAP)) ? pos : SEL_CAP + lane;
             ckey[dst] = csk[u];
@@ -1762,7 +1775,9 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     }
     overflow = overflow || cnt > SEL_CAP;
     wave_lds_sync();
-    const int nk = nkept;
+    // with the bound raised, nkept misses the keys below it, but at least kk
+    // distinct keys lie above it
+    const int nk = (lo > 0u && nkept <= kk) ? kk + 1 : nkept;
 
     // re-walk the kept keys (rare path: the buffer overflowed, so it is free
     // to hold a fresh seen bitmap).  A key comes as (xm 0) its code << 16;
