@@ -1221,14 +1221,34 @@ __device__ uint32_t exact_keys(const SelP &p, const T *qr, const T *kb, int v, b
 }
 
 
-__device__ __forceinline__ int wave_excl_scan(int v) {
-    const int lane = lane_id();
-    int x = v;
-#pragma unroll
-    for (int o = 1; o < SSA_WAVE; o <<= 1) {
-        const int y = __shfl_up(x, o, SSA_WAVE);
-        if (lane >= o) x += y;
-    }
+// Inclusive prefix scans over the 64 lanes with DPP: row shifts by 1, 2, 4
+// and 8 scan each row of 16 lanes, then row broadcasts 15 (into rows 1 and
+// 3) and 31 (into rows 2 and 3) carry the row totals -- VALU only, no LDS
+// round trips.  Lanes a shift or broadcast leaves out see the identity.
+// Every lane must be active.
+__device__ __forceinline__ int wave_incl_sum(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, false);   // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, false);   // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, false);   // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, false);   // row_shr:8
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);   // row_bcast:15
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);   // row_bcast:31
+    return v;
+}
+// values >= -1 (-1 is the identity)
+__device__ __forceinline__ int wave_incl_max(int v) {
+    v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x111, 0xF, 0xF, false));
+    v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x112, 0xF, 0xF, false));
+    v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x114, 0xF, 0xF, false));
+    v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x118, 0xF, 0xF, false));
+    v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x142, 0xA, 0xF, false));
+    v = max(v, __builtin_amdgcn_update_dpp(-1, v, 0x143, 0xC, 0xF, false));
+    return v;
+}
+// exclusive prefix sum and the wave total
+__device__ __forceinline__ int wave_excl_scan(int v, int &total) {
+    const int x = wave_incl_sum(v);
+    total = __builtin_amdgcn_readlane(x, SSA_WAVE - 1);
     return x - v;
 }
 
@@ -1310,15 +1330,6 @@ __device__ __forceinline__ uint32_t kth_search(const uint32_t (&k)[NK], int kk, 
     return thr;
 }
 
-__device__ __forceinline__ int wave_incl_max(int v) {
-    const int lane = lane_id();
-#pragma unroll
-    for (int o = 1; o < SSA_WAVE; o <<= 1) {
-        const int y = __shfl_up(v, o, SSA_WAVE);
-        if (lane >= o) v = max(v, y);
-    }
-    return v;
-}
 
 // FULL mode tail (merge_neighbors, sparse_attention.py:966-1089): `bm` holds
 // the selected LSH keys; adds the window (:368-376), the globals, key 0 when a
@@ -1354,8 +1365,8 @@ __device__ void full_merge_emit(uint32_t *bm, const SelP &p, int n, int64_t row,
     const int w0 = lane * wpl;
     int cntb = 0;
     for (int w = w0; w < w0 + wpl && w < p.words; ++w) cntb += __popc(bm[w]);
-    const int pos = wave_excl_scan(cntb);
-    const int total = wave_sum_i(cntb);
+    int total;
+    const int pos = wave_excl_scan(cntb, total);
     const int filled = total < ks ? total : ks;
     if (ks <= scr_cap) {
         // output slot t holds the (t - s)-th key of the word whose first key
@@ -1555,6 +1566,7 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     bool any_empty = false;            // some bucket is empty: glob ++ 0 (same for all)
     bool nkeep = false;                // the query's own key is kept
     bool nfound = !CAUSAL;
+    bool any_fill = false;             // some list has an overflow filler below the query
     const int4 *crow = p.cut + rloc * nl;
     const int32_t *xrow = p.srix + rloc * nl;
     for (int l0 = 0; l0 < nl; l0 += SSA_WAVE) {
@@ -1563,15 +1575,19 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
         const int4 ct = in ? crow[list] : make_int4(0, 0, 0, 0);
         const int so = in ? xrow[list] : 0;
         const int sz = ct.y & 0xffff, cutoff = ct.z & 0xffff, st = ct.z >> 16;
-        if (in) lst[list] = make_int4(st, sz, ct.x - st, ct.y >> 16);
+        // a filler that cannot matter (no overflow, or past the query) is -1
+        const bool fl = in && sz > 0 && sz < p.C && (!CAUSAL || (ct.y >> 16) < n);
+        if (in) lst[list] = make_int4(st, sz, ct.x - st, fl ? ct.y >> 16 : -1);
+        any_fill = any_fill || wave_ballot(fl) != 0ull;
         const int nc = (in && sz > 0) ? (cutoff + SSA_WAVE - 1) / SSA_WAVE : 0;
-        const int at = nch + wave_excl_scan(nc);
+        int ncs;
+        const int at = nch + wave_excl_scan(nc, ncs);
         for (int k = 0; k < nc; ++k) {
             const int c0 = k * SSA_WAVE;
             const uint64_t m = lanes_mask(cutoff - c0);
             tab[at + k] = make_int4(ct.x + c0, (int)(uint32_t)m, so + c0, (int)(uint32_t)(m >> 32));
         }
-        nch += wave_sum_i(nc);
+        nch += ncs;
         any_empty = any_empty || wave_ballot(in && sz == 0) != 0ull;
         if (!nfound) {
             // earliest list holding the query's key: its first slot decides
@@ -1600,8 +1616,10 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     // ---- overflow fillers: list L (0 < size < C) holds its round's filler key
     // f at slots size..C-1, invalid.  Lane pairs (L, L2 <= L) look for a real
     // occurrence of f in list L2 or a filler of f in an earlier list; with
-    // neither, f's first occurrence is L's filler and f is never kept.
-    {
+    // neither, f's first occurrence is L's filler and f is never kept.  The
+    // table marked such lists by a filler key >= 0 (else -1, which every
+    // later use of the key reads as "no filler").
+    if (any_fill) {
         uint32_t *fhit = ckey;         // per list: f occurs earlier (scratch before pass 1)
         for (int w = lane; w < (nl + 31) / 32; w += SSA_WAVE) fhit[w] = 0u;
         wave_lds_sync();
@@ -1612,8 +1630,8 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
             const int L2 = pi - L * nl;
             if (pi < np && L2 <= L) {
                 const int4 a = lst[L];
-                const int v = a.w;
-                if (a.y > 0 && a.y < p.C && (!CAUSAL || v < n)) {
+                const int v = a.w;                     // >= 0: L's filler can matter
+                if (v >= 0) {
                     const int4 c2 = lst[L2];
                     bool hit;
                     if (c2.y == 0) {                   // glob ++ 0, all valid
@@ -1634,8 +1652,7 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
         wave_lds_sync();
         for (int L = lane; L < nl; L += SSA_WAVE) {
             const int4 a = lst[L];
-            const bool mark = a.y > 0 && a.y < p.C && (!CAUSAL || a.w < n) &&
-                              !((fhit[L >> 5] >> (L & 31)) & 1u);
+            const bool mark = a.w >= 0 && !((fhit[L >> 5] >> (L & 31)) & 1u);
             if (mark) bm_set(bm, a.w);
             lst[L].w = mark ? a.w : -1;
         }
@@ -1743,7 +1760,10 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
             mx = wave_max_u(mx);
             mn = wave_min_u(mn);
             const uint32_t base0 = lo > mn ? lo : mn;     // every buffered key >= lo
-            const uint32_t nlo = kth_search(sv, kk, base0, mx, 16);
+            // any lower bound of the kk-th key will do: the search stops 6 bits
+            // below the highest bit in which the buffer's keys differ
+            const int hbit = base0 >= mx ? 16 : 31 - __clz(base0 ^ mx);
+            const uint32_t nlo = kth_search(sv, kk, base0, mx, max(16, hbit - 5));
             lo = nlo > lo ? nlo : lo;
             uint32_t sl[SEL_CAP / SSA_WAVE];
 #pragma unroll
