@@ -1270,8 +1270,6 @@ constexpr int SEL_CAP = 384;   // keys kept in LDS for the exact threshold searc
 //                     the stores of lanes that append nothing
 //   cval  [SEL_CAP+64] key id of each compacted key (ckey and cval together span
 //                     at least `words`: the overflow path's second bitmap)
-//   gsc   [64]        score keys of glob[0..G-1] and key 0 (empty buckets)
-//   gid   [64]        the ids glob[0..G-1], 0
 //   LSH mode: ekey/eval/eslot [kk] the selected entries
 constexpr int SEL_BUF = SEL_CAP + 64;
 constexpr int SEL_PIPE = 2;            // chunks per group in pass 1
@@ -1281,7 +1279,7 @@ __host__ __device__ inline int sel_buf_words(int words) {
 }
 __host__ __device__ inline int sel_tab_entries(int nch) { return nch + 2 * SEL_PIPE; }
 __host__ __device__ inline int sel_lds_words(int nch, int words, int kk, bool lsh, int nlists) {
-    return (4 * sel_tab_entries(nch) + 4 * nlists + words + sel_buf_words(words) + 128 +
+    return (4 * sel_tab_entries(nch) + 4 * nlists + words + sel_buf_words(words) +
             (lsh ? 3 * kk : 0) + 1) & ~1;
 }
 
@@ -1517,7 +1515,10 @@ __device__ __forceinline__ void sel_boundary(uint32_t *ckey, int ebits, uint32_t
 //          keys by descending score, FULL mode merges them with the window and
 //          the globals through a key bitmap.
 template <typename T, bool LSH_MODE, bool CAUSAL>
-__global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
+// Registers are held to what 8 waves per SIMD allow (the kernel waits on
+// memory and LDS; the bench workload's 5 KB of LDS per wave fits 8 as well).
+__global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) __attribute__((amdgpu_waves_per_eu(8, 8)))
+select_kernel(SelP p) {
     extern __shared__ uint32_t sel_smem[];
     const int64_t blk = xcd_logical_block(blockIdx.x, p.nblocks);
     if (blk >= p.nblocks) return;
@@ -1532,9 +1533,7 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
     uint32_t *bm = (uint32_t *)(lst + nl);
     uint32_t *ckey = bm + p.words;
     uint32_t *cval = ckey + SEL_BUF;
-    uint32_t *gsc = ckey + sel_buf_words(p.words);
-    int32_t *gid = (int32_t *)(gsc + 64);
-    uint32_t *ekey = (uint32_t *)(gid + 64);
+    uint32_t *ekey = ckey + sel_buf_words(p.words);
     uint32_t *eval = ekey + p.kk;
     uint32_t *eslot = eval + p.kk;
 
@@ -1608,8 +1607,6 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
         greg_sc = score_key(arow[1 + lane]);
         greg_c = score_code(arow[1 + lane], qsc);
         greg_id = lane < p.G ? (int)p.glob[lane] : 0;
-        gsc[lane] = greg_sc;
-        gid[lane] = greg_id;
     }
     wave_lds_sync();
 
@@ -1637,7 +1634,7 @@ __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) select_kernel(SelP p) {
                     if (c2.y == 0) {                   // glob ++ 0, all valid
                         hit = v == 0 && p.G < p.C;
                         const int gl = min(p.G, p.C);
-                        for (int j = 0; j < gl; ++j) hit |= gid[j] == v;
+                        for (int j = 0; j < gl; ++j) hit |= (int)p.glob[j] == v;
                     } else {
                         hit = L2 < L && c2.y < p.C && c2.w == v;
                         if (!hit) {
