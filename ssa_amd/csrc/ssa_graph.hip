@@ -79,10 +79,22 @@ struct HashP {
     int key_layout;
     int vec16;          // rows 16-byte aligned: quarter rows load with 16-byte loads
     int64_t rows;
+    uint32_t *zero;     // block 0 clears zero[0..nzero) and *zero1 (later kernels'
+    int nzero;          // accumulator and counter; either may be null)
+    int32_t *zero1;
+    uint32_t *kpart;    // key hash: max |k|^2 of each 16-row tile as float bits, or null
 };
+
+__device__ __forceinline__ void hash_clear(const HashP &p) {
+    if (blockIdx.x == 0) {
+        for (int i = threadIdx.x; i < p.nzero; i += blockDim.x) p.zero[i] = 0u;
+        if (p.zero1 && threadIdx.x == 0) *p.zero1 = 0;
+    }
+}
 
 template <typename T>
 __global__ void __launch_bounds__(256) hash_kernel(HashP p) {
+    hash_clear(p);
     const int64_t row = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (row >= p.rows) return;
     const int i = (int)(row % p.L);
@@ -167,8 +179,10 @@ __device__ __forceinline__ void write_ids(const float *pr, int P, int Tp, uint16
 // of rows x planes, lane l feeding row (l % 16) and plane (l % 16) with the
 // element k = l / 16 of the step.  The reduction over the head dim is split so
 // that lane group g = l / 16 walks the contiguous quarter [g*d/4, (g+1)*d/4):
-// every lane loads its quarter row once with wide loads.  One wavefront handles
-// 16 rows against all R*P planes (staged in LDS, fp32, row stride d+1).
+// every lane loads its quarter row once with wide loads.  The block stages all
+// R*P planes in LDS once (fp32, row stride d+1); each wavefront then takes
+// HASH_TILES tiles of 16 rows against them.
+constexpr int HASH_TILES = 1;
 template <typename T, int D>
 __global__ void __launch_bounds__(256) hash_mfma_kernel(HashP p) {
     constexpr int DQ = D / 4;
@@ -178,34 +192,41 @@ __global__ void __launch_bounds__(256) hash_mfma_kernel(HashP p) {
     float *W = hs;                                    // [NT*16][D+1]
     float *proj = W + NT * 16 * (D + 1);              // [4 waves][16][NT*16 + 1]
     const int pst = NT * 16 + 1;
-    for (int x = threadIdx.x; x < NT * 16 * D; x += blockDim.x) {
-        const int j = x / D, e = x % D;
-        float w = 0.f;
-        if (j < NP) w = p.planes[((int64_t)(j / p.P) * p.maxP + (j % p.P)) * D + e];
-        W[j * (D + 1) + e] = w;
-    }
-    __syncthreads();
+    hash_clear(p);
     const int wid = threadIdx.x / SSA_WAVE;
     const int lane = lane_id();
+    // plane j (round j / P, hash j % P) is staged by wave j % 4, D / 64 elements a lane
+    for (int j = wid; j < NT * 16; j += 4) {
+        const bool real = j < NP;
+        const float *src = p.planes + (real ? ((int64_t)(j / p.P) * p.maxP + (j % p.P)) * D : 0);
+        for (int e = lane; e < D; e += SSA_WAVE) W[j * (D + 1) + e] = real ? src[e] : 0.f;
+    }
+    __syncthreads();
     const int li = lane % 16, lg = lane / 16;
-    const int64_t row0 = ((int64_t)blockIdx.x * 4 + wid) * 16;
-    if (row0 >= p.rows) return;
-    const int64_t row = row0 + li;
-    float xs[DQ];
-    if (row < p.rows) {
-        const int i = (int)(row % p.L);
-        const int64_t bh = row / p.L;
-        const T *x = (const T *)p.x + (bh / p.nh) * p.sb + (bh % p.nh) * p.sh + (int64_t)i * p.sn +
-                     lg * DQ;
-        constexpr int PER16 = 16 / (int)sizeof(T);
-        if constexpr (DQ % PER16 == 0) {
-            if (p.vec16) {
+    for (int tile = 0; tile < HASH_TILES; ++tile) {
+        // the block's 4 waves take adjacent 16-row tiles at each step
+        const int64_t row0 = (((int64_t)blockIdx.x * HASH_TILES + tile) * 4 + wid) * 16;
+        if (row0 >= p.rows) break;
+        const int64_t row = row0 + li;
+        float xs[DQ];
+        if (row < p.rows) {
+            const int i = (int)(row % p.L);
+            const int64_t bh = row / p.L;
+            const T *x = (const T *)p.x + (bh / p.nh) * p.sb + (bh % p.nh) * p.sh + (int64_t)i * p.sn +
+                         lg * DQ;
+            constexpr int PER16 = 16 / (int)sizeof(T);
+            if constexpr (DQ % PER16 == 0) {
+                if (p.vec16) {
 #pragma unroll
-                for (int e0 = 0; e0 < DQ; e0 += PER16) {
-                    const uint4 w = *reinterpret_cast<const uint4 *>(x + e0);
-                    const T *tv = reinterpret_cast<const T *>(&w);
+                    for (int e0 = 0; e0 < DQ; e0 += PER16) {
+                        const uint4 w = *reinterpret_cast<const uint4 *>(x + e0);
+                        const T *tv = reinterpret_cast<const T *>(&w);
 #pragma unroll
-                    for (int e = 0; e < PER16; ++e) xs[e0 + e] = to_f32(tv[e]);
+                        for (int e = 0; e < PER16; ++e) xs[e0 + e] = to_f32(tv[e]);
+                    }
+                } else {
+#pragma unroll
+                    for (int e = 0; e < DQ; ++e) xs[e] = to_f32(x[e]);
                 }
             } else {
 #pragma unroll
@@ -213,40 +234,53 @@ __global__ void __launch_bounds__(256) hash_mfma_kernel(HashP p) {
             }
         } else {
 #pragma unroll
-            for (int e = 0; e < DQ; ++e) xs[e] = to_f32(x[e]);
+            for (int e = 0; e < DQ; ++e) xs[e] = 0.f;
         }
-    } else {
+        if (p.kpart) {
+            // |k|^2 of the tile's rows (lane groups hold quarters; rows past the
+            // end are 0), maximised over the tile: non-negative floats order as
+            // their bit patterns
+            float s2 = 0.f;
 #pragma unroll
-        for (int e = 0; e < DQ; ++e) xs[e] = 0.f;
-    }
-    float *pw = proj + wid * 16 * pst;
-    for (int t = 0; t < NT; ++t) {
-        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-        const float *wr = W + (t * 16 + li) * (D + 1) + lg * DQ;
+            for (int e = 0; e < DQ; ++e) s2 = fmaf(xs[e], xs[e], s2);
+            s2 += __shfl_xor(s2, 16, SSA_WAVE);
+            s2 += __shfl_xor(s2, 32, SSA_WAVE);
+            const uint32_t m = wave_max_u(__float_as_uint(s2));
+            if (lane == 0) p.kpart[row0 / 16] = m;
+        }
+        float *pw = proj + wid * 16 * pst;
+        for (int t = 0; t < NT; ++t) {
+            f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+            const float *wr = W + (t * 16 + li) * (D + 1) + lg * DQ;
 #pragma unroll
-        for (int s = 0; s < DQ; ++s)
-            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xs[s], wr[s], acc, 0, 0, 0);
+            for (int s = 0; s < DQ; ++s)
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xs[s], wr[s], acc, 0, 0, 0);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) pw[(4 * lg + r) * pst + t * 16 + li] = acc[r];
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    if (lane < 16 && row0 + lane < p.rows) {
-        const int64_t rw = row0 + lane;
-        const int i = (int)(rw % p.L);
-        const int64_t bh = rw / p.L;
-        for (int r = 0; r < p.R; ++r) {
-            const float *pr = pw + lane * pst + r * p.P;
-            if (p.key_layout) {
-                int id = 0;
-                for (int j = 0; j < p.P; ++j)
-                    if (pr[j] > 0.f) id |= 1 << j;
-                p.out[(bh * p.R + r) * p.L + i] = (uint16_t)id;
-            } else {
-                write_ids(pr, p.P, p.Tp, p.out + ((bh * p.L + i) * p.R + r) * p.NS);
+            for (int r = 0; r < 4; ++r) pw[(4 * lg + r) * pst + t * 16 + li] = acc[r];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (lane < 16 && row0 + lane < p.rows) {
+            const int64_t rw = row0 + lane;
+            const int i = (int)(rw % p.L);
+            const int64_t bh = rw / p.L;
+            for (int r = 0; r < p.R; ++r) {
+                const float *pr = pw + lane * pst + r * p.P;
+                if (p.key_layout) {
+                    int id = 0;
+                    for (int j = 0; j < p.P; ++j)
+                        if (pr[j] > 0.f) id |= 1 << j;
+                    p.out[(bh * p.R + r) * p.L + i] = (uint16_t)id;
+                } else {
+                    write_ids(pr, p.P, p.Tp, p.out + ((bh * p.L + i) * p.R + r) * p.NS);
+                }
             }
         }
+        // this wave's projection rows are rewritten by its next tile
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
 }
 
@@ -829,12 +863,28 @@ struct LsP {
     const int32_t *perm, *bstart, *bsize;
     int32_t *sid, *rnk, *smin, *inv;
     int M, NB, C;
+    // with kpart: block (kv head bk, round 0, bucket 0) also writes knorm[bk], the
+    // max of the key hash's M / 16 tile maxima of |k|^2 for that head
+    const uint32_t *kpart;
+    uint32_t *knorm;
+    int R;
 };
 
 __global__ void __launch_bounds__(256) list_sort_kernel(LsP p) {
     extern __shared__ uint32_t ls_key[];
     const int64_t prow = blockIdx.x / p.NB;
     const int u = (int)(blockIdx.x % p.NB);
+    if (p.kpart && u == 0 && prow % p.R == 0) {
+        __shared__ uint32_t kred[4];
+        const int64_t bk = prow / p.R;
+        const int nt = p.M / 16;
+        uint32_t m = 0u;
+        for (int i = threadIdx.x; i < nt; i += 256) m = max(m, p.kpart[bk * nt + i]);
+        m = wave_max_u(m);
+        if (lane_id() == 0) kred[threadIdx.x / SSA_WAVE] = m;
+        __syncthreads();
+        if (threadIdx.x == 0) p.knorm[bk] = max(max(kred[0], kred[1]), max(kred[2], kred[3]));
+    }
     const int st = p.bstart[prow * p.NB + u];
     const int sz = p.bsize[prow * p.NB + u];
     if (sz == 0) return;
@@ -957,10 +1007,12 @@ struct CutP {
                        // region of S (lists * N * C elements), in elements
     int N, M, R, NS, NB, C, Cs, Hq, Hkv, rep, bh0, G, causal, nlists;
     int64_t rows;
+    int32_t *zero;     // cleared by thread 0 (the select kernel's tie-row counter)
 };
 
 __global__ void __launch_bounds__(256) cut_kernel(CutP p) {
     const int64_t x = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (x == 0) *p.zero = 0;
     if (x >= p.rows * p.nlists) return;
     const int list = (int)(x % p.nlists);
     const int64_t rloc = x / p.nlists;
@@ -2405,7 +2457,7 @@ struct Layout {
     int64_t kid, qid, perm, bstart, bsize, sorttmp, sid, rnk, smin, inv, cut, srix, qpos, cnt, off,
         cur,
         qlist, tiles, ntiles, tcnt, kbase, S, trash,
-        tie_list, tie_count, aux, knorm, total;
+        tie_list, tie_count, aux, knorm, kpart, total;
 };
 
 int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
@@ -2443,6 +2495,7 @@ Layout plan(const Dims &D) {
     L.tie_count = take(4);
     L.aux = take(nbh * D.N * (D.G + 3) * 4);
     L.knorm = take(D.BK * 4);
+    L.kpart = take(D.BK * (D.M / 16) * 4);
     L.total = o;
     return L;
 }
@@ -2531,8 +2584,8 @@ int launch_hash_mfma(const HashP &hp, hipStream_t st) {
     }
     SSA_CHECK_HIP(hipFuncSetAttribute((const void *)hash_mfma_kernel<T, Dh>,
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    hipLaunchKernelGGL((hash_mfma_kernel<T, Dh>), dim3((unsigned)ceil_div(hp.rows, 64)), dim3(256),
-                       lds, st, hp);
+    hipLaunchKernelGGL((hash_mfma_kernel<T, Dh>), dim3((unsigned)ceil_div(hp.rows, 64 * HASH_TILES)),
+                       dim3(256), lds, st, hp);
     SSA_CHECK_LAUNCH();
     return SSA_OK;
 }
@@ -2564,6 +2617,12 @@ bool view_aligned16(const ssa_tensor4 &t, int elem) {
     return (uintptr_t)t.ptr % 16 == 0 && t.sb % v == 0 && t.sh % v == 0 && t.sn % v == 0;
 }
 
+// The key hash can also give max |k|^2 per kv head when it reads the key rows
+// itself (no injected projections) and 16-row tiles never straddle two heads.
+bool key_norm_in_hash(const Dims &D, const ssa_graph_args *a) {
+    return !a->k_proj && D.M % 16 == 0 && D.BK * D.M > 0;
+}
+
 template <typename T>
 int launch_hash(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws,
                 hipStream_t st, bool keys) {
@@ -2576,6 +2635,16 @@ int launch_hash(const Dims &D, const ssa_graph_args *a, const Layout &L, char *w
         hp.vec16 = view_aligned16(a->k, (int)sizeof(T)) ? 1 : 0;
         hp.out = (uint16_t *)(ws + L.kid);
         hp.rows = D.BK * D.M;
+        // the bucket sort's segment counter starts at zero
+        hp.zero1 = ssa_sort_counter((uint16_t *)(ws + L.sorttmp), (int)(D.BK * D.R), D.M);
+        if (key_norm_in_hash(D, a)) {
+            // max |k|^2 per tile here, per kv head in the list sort
+            hp.kpart = (uint32_t *)(ws + L.kpart);
+        } else {
+            // the max |k|^2 accumulators of knorm_kernel start at zero
+            hp.zero = (uint32_t *)(ws + L.knorm);
+            hp.nzero = (int)D.BK;
+        }
         return launch_hash_one<T>(hp, D.d, st);
     }
     hp.x = a->q.ptr; hp.sb = a->q.sb; hp.sh = a->q.sh; hp.sn = a->q.sn;
@@ -2734,10 +2803,13 @@ int keys_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws
         kp.k = a->k.ptr; kp.ksb = a->k.sb; kp.ksh = a->k.sh; kp.ksn = a->k.sn;
         kp.Hkv = D.Hkv; kp.M = D.M; kp.d = D.d;
         kp.out = (uint32_t *)(ws + L.knorm);
-        hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(256), 0, st, (int32_t *)kp.out,
-                           (int64_t)D.BK, 0);
-        SSA_CHECK_LAUNCH();
-        if (D.BK * D.M > 0) {
+        if (key_norm_in_hash(D, a)) {
+            // the list sort reduces the key hash's tile maxima
+        } else if (D.BK * D.M == 0) {  // else the key hash cleared it
+            hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(256), 0, st, (int32_t *)kp.out,
+                               (int64_t)D.BK, 0);
+            SSA_CHECK_LAUNCH();
+        } else {
             const int seg = (int)((int64_t)D.d * (int64_t)sizeof(T) / 16);
             const bool vec = view_aligned16(a->k, (int)sizeof(T)) && D.d * (int)sizeof(T) % 16 == 0 &&
                              seg >= 4 && seg <= 32;
@@ -2755,9 +2827,11 @@ int keys_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws
         }
     }
     if (!(phases & SSA_PHASE_KEY_SORT)) return SSA_OK;
+    // the key hash cleared the sort's counter when it ran in this call
     rc = ssa_launch_bucket_sort((const uint16_t *)(ws + L.kid), (int)(D.BK * D.R), D.M, D.P,
                                 (int32_t *)(ws + L.perm), (int32_t *)(ws + L.bstart),
-                                (int32_t *)(ws + L.bsize), (uint16_t *)(ws + L.sorttmp), st);
+                                (int32_t *)(ws + L.bsize), (uint16_t *)(ws + L.sorttmp), st,
+                                !(phases & SSA_PHASE_KEY_HASH));
     if (rc) return rc;
     {
         LsP lp{};
@@ -2769,6 +2843,11 @@ int keys_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws
         lp.smin = (int32_t *)(ws + L.smin);
         lp.inv = (int32_t *)(ws + L.inv);
         lp.M = D.M; lp.NB = D.NB; lp.C = D.C;
+        if (key_norm_in_hash(D, a)) {
+            lp.kpart = (const uint32_t *)(ws + L.kpart);
+            lp.knorm = (uint32_t *)(ws + L.knorm);
+            lp.R = D.R;
+        }
         int p2 = 1;
         while (p2 < std::min(D.C, D.M)) p2 <<= 1;
         const size_t lds = std::max((size_t)p2 * 4,
@@ -2870,8 +2949,14 @@ int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char 
         cp.N = D.N; cp.M = D.M; cp.R = D.R; cp.NS = D.NS; cp.NB = D.NB; cp.C = D.C; cp.Cs = D.Cs;
         cp.Hq = D.Hq; cp.Hkv = D.Hkv; cp.rep = D.rep; cp.bh0 = (int)bh0; cp.G = D.G;
         cp.causal = a->causal ? 1 : 0; cp.nlists = D.nlists; cp.rows = (int64_t)nbh * D.N;
-        hipLaunchKernelGGL(cut_kernel, dim3((unsigned)ceil_div(cp.rows * D.nlists, 256)), dim3(256),
-                           0, st, cp);
+        // the cut kernel also clears the select kernel's tie-row counter
+        cp.zero = (int32_t *)(ws + L.tie_count);
+        const int64_t cut_blocks = ceil_div(cp.rows * D.nlists, 256);
+        if (cut_blocks > 0) {
+            hipLaunchKernelGGL(cut_kernel, dim3((unsigned)cut_blocks), dim3(256), 0, st, cp);
+        } else {
+            hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(64), 0, st, cp.zero, (int64_t)1, 0);
+        }
         SSA_CHECK_LAUNCH();
 
         SelP sp{};
@@ -2899,8 +2984,6 @@ int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char 
         sp.NA = ap.NA;
         sp.perm_bytes = (int)(D.BK * D.R * D.M * 4);
         sp.nblocks = ceil_div(sp.rows, SEL_WAVES);
-        hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(64), 0, st, sp.tie_count, (int64_t)1, 0);
-        SSA_CHECK_LAUNCH();
         rc = select_dispatch<T>(sp, st);
         if (rc) return rc;
         rc = sp.mode == SSA_GRAPH_LSH ? launch_replay<T, true>(sp, D.chunk, st)

@@ -8,5 +8,9 @@
 
 int ssa_sort_supported(int n);
 int64_t ssa_sort_tmp_bytes(int rows, int n);
+// the segment counter inside the sort's scratch `tmp`: it must be 0 when the
+// sort starts (counter_clear: the sort clears it itself; else the caller has)
+int32_t *ssa_sort_counter(uint16_t *tmp, int rows, int n);
 int ssa_launch_bucket_sort(const uint16_t *ids, int rows, int n, int P, int32_t *perm,
-                           int32_t *bstart, int32_t *bsize, uint16_t *tmp, hipStream_t st);
+                           int32_t *bstart, int32_t *bsize, uint16_t *tmp, hipStream_t st,
+                           bool counter_clear = true);

@@ -626,8 +626,14 @@ int ssa_sort_supported(int n) {
     return lds <= SSA_LDS_BYTES;
 }
 
+int32_t *ssa_sort_counter(uint16_t *tmp, int rows, int n) {
+    const int64_t rn = (int64_t)rows * n;
+    return (int32_t *)((char *)tmp + al256(rn * 4) + al256(rn * 16));
+}
+
 int ssa_launch_bucket_sort(const uint16_t *ids, int rows, int n, int P, int32_t *perm,
-                           int32_t *bstart, int32_t *bsize, uint16_t *tmp, hipStream_t st) {
+                           int32_t *bstart, int32_t *bsize, uint16_t *tmp, hipStream_t st,
+                           bool counter_clear) {
     if (!ssa_sort_supported(n)) {
         ssa_set_error("bucket sort: key length %d unsupported (1..32768)", n);
         return SSA_E_UNSUP;
@@ -641,10 +647,12 @@ int ssa_launch_bucket_sort(const uint16_t *ids, int rows, int n, int P, int32_t 
     char *t = (char *)tmp;
     uint32_t *gkv = (uint32_t *)t;
     int4 *segs = (int4 *)(t + al256(rn * 4));
-    int *segcount = (int *)(t + al256(rn * 4) + al256(rn * 16));
+    int *segcount = ssa_sort_counter(tmp, rows, n);
     uint16_t *tl_tmp = (uint16_t *)(t + al256(rn * 4) + al256(rn * 16) + 256);
-    hipLaunchKernelGGL(sort_zero_kernel, dim3(1), dim3(64), 0, st, segcount);
-    SSA_CHECK_LAUNCH();
+    if (counter_clear) {
+        hipLaunchKernelGGL(sort_zero_kernel, dim3(1), dim3(64), 0, st, segcount);
+        SSA_CHECK_LAUNCH();
+    }
     SSA_CHECK_HIP(hipFuncSetAttribute((const void *)sort_top_kernel,
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     hipLaunchKernelGGL(sort_top_kernel, dim3(rows), dim3(SORT_THREADS), lds, st, ids, n, NB, perm,

@@ -330,7 +330,7 @@ class SparseAttention(nn.Module):
         """(neighbors int64, valid bool), both (B, H, N, K_out)
         (sparse_attention.py:1325-1390).  ``k`` may be expanded or not."""
         _lib.require_device(q, k)
-        glob = self.glob_builder(M, q.device)
+        glob = self._glob_ids(M, q.device)
         p_eff = self.lsh_builder.compute_effective_p(M, self.lsh_builder.C, self.lsh_builder.max_P)
         qp, kp = _proj if _proj is not None else (None, None)
         out, valid, _ = _lib.build_graph(
@@ -339,6 +339,21 @@ class SparseAttention(nn.Module):
             causal=causal, is_cross=is_cross, total_k=self.K, glob=glob,
             mode=_lib.GRAPH_FULL, q_proj=qp, k_proj=kp)
         return out, valid
+
+    def _glob_ids(self, M: int, device) -> torch.Tensor:
+        """``glob_builder(M, device)``, kept per (M, device) so that a forward
+        launches no arange: the ids depend on nothing else (explicit indices
+        are keyed by their buffer's storage and version).  The kernels only
+        read it."""
+        fx = getattr(self.glob_builder, "_fixed_idx", None)
+        key = (M, str(device), None if fx is None else (fx.data_ptr(), fx._version))
+        cache = self.__dict__.setdefault("_globc", {})
+        t = cache.get(key)
+        if t is None:
+            t = self.glob_builder(M, device)
+            cache.clear()
+            cache[key] = t
+        return t
 
     def _fused_weight(self, mods):
         """The weights of `mods` stacked along the output dimension.  Under
