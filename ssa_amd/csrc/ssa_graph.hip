@@ -556,7 +556,6 @@ struct RsP {
     int N, M, R, NS, NB, C, Hq, Hkv, rep, bh0, causal;
     int Cs;            // score row stride (a multiple of 64)
     int k32;           // byte offsets of the K rows of a (batch, kv head) fit 32 bits
-    uint16_t *trash;   // 64 x 32 bytes that lanes without a query store to
     int64_t Call;
 };
 
@@ -784,15 +783,28 @@ __global__ void __launch_bounds__(256) rescore_mfma_kernel(RsP p) {
     RS_FETCH(0)
     RS_COMMIT(0)
     __syncthreads();
-    // Score rows are padded to a multiple of 64 members, so each lane stores
-    // its 2 x 8 score codes as full 16-byte vectors (members past the cutoff
-    // land in the padding and are never read).  Every iteration issues exactly
-    // these stores after its loads, so the commit waits for the loads only.
-    // Lanes without a query store into a scratch row of their own instead, so
-    // that the stores need no branch.
-    uint16_t *srow = qok ? p.S + ((int64_t)inst * p.N + qb + qrow) * p.Cs + 8 * lg
-                         : p.trash + lane * 16;
-    const int cstep = qok ? 64 : 0;
+    // Each lane stores its 2 x 8 score codes as 16-byte vectors through a raw
+    // buffer over the instance's rows (rows are padded to a multiple of 64
+    // members).  A group of 8 members is stored only when its first member is
+    // below the lane's query (causal; the select kernel reads no further) and
+    // the lane has a query: other lanes give an offset past the buffer's end,
+    // which the hardware drops.  So every iteration issues exactly these
+    // stores after its loads, and the commit waits for the loads only.
+    int cq = qok ? nv : 0;             // members of this lane's query row to store
+    if (qok && p.causal) {
+        // members with an id below the query: a binary search of the ascending ids
+        const int nq = nidx[qrow];
+        int lo = 0, hi = nv;
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (prl[mid] < nq) lo = mid + 1;
+            else hi = mid;
+        }
+        cq = lo;
+    }
+    const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(p.S + (int64_t)inst * p.N * p.Cs), (short)0, p.N * p.Cs * 2, SSA_BUF_FLAGS);
+    const uint32_t sbase = (uint32_t)((qb + qrow) * p.Cs + 8 * lg) * 2u;
     for (int j = 0; j < nsl; ++j) {
         const int c0 = 64 * j;
         const bool more = j + 1 < nsl;
@@ -833,12 +845,13 @@ __global__ void __launch_bounds__(256) rescore_mfma_kernel(RsP p) {
                               code_pair(acc[2 * X + 1][0], acc[2 * X + 1][1], qsc),
                               code_pair(acc[2 * X + 1][2], acc[2 * X + 1][3], qsc)};
         }
-        // every wave stores (idle waves into the scratch rows): the same two
-        // stores on every path
+        // every wave issues the same two stores (dropped where out of range)
 #pragma unroll
-        for (int X = 0; X < 2; ++X)
-            *reinterpret_cast<u32x4 *>(srow + (qok ? 32 * X : 8 * X)) = kq[X];
-        srow += cstep;
+        for (int X = 0; X < 2; ++X) {
+            const int c = c0 + 32 * X + 8 * lg;
+            const uint32_t off = c < cq ? sbase + (uint32_t)(c0 + 32 * X) * 2u : 0x80000000u;
+            __builtin_amdgcn_raw_buffer_store_b128(kq[X], srs, off, 0, 0);
+        }
         // the other buffer was last read in iteration j - 1, before its barrier
         if (more) { RS_COMMIT((j + 1) & 1) }
         __syncthreads();
@@ -2456,7 +2469,7 @@ int supported_d(int d) { return d >= 4 && d <= 256 && (d & (d - 1)) == 0; }
 struct Layout {
     int64_t kid, qid, perm, bstart, bsize, sorttmp, sid, rnk, smin, inv, cut, srix, qpos, cnt, off,
         cur,
-        qlist, tiles, ntiles, tcnt, kbase, S, trash,
+        qlist, tiles, ntiles, tcnt, kbase, S,
         tie_list, tie_count, aux, knorm, kpart, total;
 };
 
@@ -2490,7 +2503,6 @@ Layout plan(const Dims &D) {
     L.tcnt = take(ninst * 4);
     L.kbase = take((nbh / D.rep + 2) * D.R * D.NS * D.rep * 4);
     L.S = take(nbh * D.N * D.nlists * D.Cs * 2);
-    L.trash = take(64 * 16 * 4);
     L.tie_list = take(nbh * D.N * 4);
     L.tie_count = take(4);
     L.aux = take(nbh * D.N * (D.G + 3) * 4);
@@ -2913,7 +2925,6 @@ int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char 
         rp.Hq = D.Hq; rp.Hkv = D.Hkv; rp.rep = D.rep; rp.bh0 = (int)bh0; rp.Call = D.Call;
         rp.causal = a->causal ? 1 : 0;
         rp.Cs = D.Cs;
-        rp.trash = (uint16_t *)(ws + L.trash);
         {
             const int64_t el = a->q.dtype == SSA_F32 ? 4 : 2;
             rp.k32 = (rp.ksn * el < ((int64_t)1 << 24) &&
