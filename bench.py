@@ -20,7 +20,14 @@ Also reported:
 * roofline.traffic: HBM bytes per apply launch from the committed rocprofv3
   FETCH_SIZE/WRITE_SIZE summary (profiles/hbm_traffic_bf16_gqa_n4096.md).
 
+`--workload NAME` measures one of the other workload shapes instead (no CPU
+baseline): fp32_b2_n1024, mqa_n32768, cross_fp32, cross_bf16, transformer6.
+Each is built as the full-size GPU tests build it (seeded construction, the
+same input recipe) and reports forward tokens/s plus the apply kernel's
+event-timed roofline.
+
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu]
+                       [--workload NAME]
 """
 import argparse
 import json
@@ -54,6 +61,130 @@ def build_module(dev):
     g = torch.Generator().manual_seed(1000)
     x = (torch.randn(1, 4096, 4096, generator=g) * 0.02).to(torch.bfloat16).to(dev)
     return cfg, attn, x
+
+
+# The other workload shapes: (description, SSAConfig fields, B, N, M (cross), dtype,
+# x scale, xavier re-init)
+OTHER = {
+    "fp32_b2_n1024": ("SparseAttention fp32 causal, d_model=512, 8 heads (d_head=64), B=2, "
+                      "N=1024, K=128, window=8, 2 global tokens, R=8",
+                      dict(d_model=512, num_heads=8, num_neighbors=128, window_size=8,
+                           num_global_tokens=2, num_hash_rounds=8, max_num_hashes=12,
+                           lsh_num_probes=0, causal=True), 2, 1024, None, "f32", 1.0),
+    "mqa_n32768": ("SparseAttention bf16 MQA causal, d_model=4096, 32 q heads / 1 kv head "
+                   "(d_head=128), B=1, N=32768, K=256, window=32, globals [0,1,16384], R=8, "
+                   "2 probes",
+                   dict(d_model=4096, num_heads=32, num_kv_heads=1, num_neighbors=256,
+                        window_size=32, global_token_indices=[0, 1, 16384], num_hash_rounds=8,
+                        max_num_hashes=12, lsh_num_probes=2, causal=True),
+                   1, 32768, None, "bf16", 1.0),
+    "cross_fp32": ("SparseAttention fp32 cross-attention, d_model=1024, 16 heads (d_head=64), "
+                   "B=4, 2048 queries over 512 keys, K=64, window=4, 2 global tokens, R=6",
+                   dict(d_model=1024, num_heads=16, num_neighbors=64, window_size=4,
+                        num_global_tokens=2, num_hash_rounds=6, max_num_hashes=12,
+                        lsh_num_probes=0, causal=False), 4, 2048, 512, "f32", 1.0),
+    "cross_bf16": ("SparseAttention bf16 cross-attention, d_model=1024, 16 heads (d_head=64), "
+                   "B=4, 2048 queries over 512 keys, K=64, window=4, 2 global tokens, R=6",
+                   dict(d_model=1024, num_heads=16, num_neighbors=64, window_size=4,
+                        num_global_tokens=2, num_hash_rounds=6, max_num_hashes=12,
+                        lsh_num_probes=0, causal=False), 4, 2048, 512, "bf16", 1.0),
+    "transformer6": ("SparseTransformer, 6 layers, d_model=1024, 16 q heads / 4 kv heads, "
+                     "vocab 32000, B=2, N=8192, K=128, window=16, R=8, 1 probe, causal, bf16, "
+                     "return_stats=True",
+                     dict(d_model=1024, num_heads=16, num_kv_heads=4, num_neighbors=128,
+                          window_size=16, num_hash_rounds=8, lsh_num_probes=1, causal=True),
+                     2, 8192, None, "bf16", None),
+}
+
+
+def _timed(fn, steps, warmup):
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def _stage_times(attn, q, k, v, N, M, B, causal, cross, reps):
+    """build and apply, each bracketed by events on the launch stream."""
+    import torch
+    st = torch.cuda.current_stream()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(reps)]
+    for e in evs:
+        e[0].record(st)
+        nb, va = attn.build_graph(q, k, N, M, B, q.device, causal, cross)
+        e[1].record(st)
+        attn.apply_graph(q, k, v, nb, va)
+        e[2].record(st)
+    torch.cuda.synchronize()
+    t_build = sum(e[0].elapsed_time(e[1]) for e in evs) / reps
+    t_apply = sum(e[1].elapsed_time(e[2]) for e in evs) / reps
+    return t_build, t_apply, nb.shape[-1]
+
+
+def other_workload(name, args):
+    import torch
+    from ssa_amd import SSAConfig, SparseAttention, SparseTransformer
+    desc, cfg_kw, B, N, M, dt, xscale = OTHER[name]
+    dtype = torch.float32 if dt == "f32" else torch.bfloat16
+    dev = "cuda:0"
+    torch.manual_seed(0)
+    g = torch.Generator().manual_seed(1000)
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")
+        if name == "transformer6":
+            model = SparseTransformer(SSAConfig(**cfg_kw), num_layers=6, vocab_size=32000)
+        else:
+            model = SparseAttention(SSAConfig(**cfg_kw))
+    model = model.to(dev)
+    for p in model.parameters():
+        p.data = p.data.to(dtype)
+    model.eval()
+    with torch.no_grad():
+        if name == "transformer6":
+            ids = torch.randint(0, 32000, (B, N), generator=g).to(dev)
+            t = _timed(lambda: model(ids, return_stats=True), args.steps, args.warmup)
+            # the stage timing and roofline of layer 0's attention, on its own input
+            attn = model.layers[0].attn
+            src = xin = model.layers[0].norm1(model.embed(ids))
+        else:
+            attn = model
+            xin = (torch.randn(B, N, cfg_kw["d_model"], generator=g) * xscale).to(dtype).to(dev)
+            src = (torch.randn(B, M, cfg_kw["d_model"], generator=g).to(dtype).to(dev)
+                   if M else xin)
+            kv = src if M else None
+            t = _timed(lambda: model(xin, key_value=kv), args.steps, args.warmup)
+        Mk = src.shape[1]
+        cross = M is not None
+        causal = cfg_kw.get("causal", False) and not cross
+        q = attn._split_q(attn.Wq(xin))
+        k = attn._split_kv_compact(attn.Wk(src))
+        v = attn._split_kv_compact(attn.Wv(src))
+        t_build, t_apply, K_out = _stage_times(attn, q, k, v, N, Mk, B, causal, cross,
+                                               max(args.steps, 5))
+    esize = 4 if dtype == torch.float32 else 2
+    bytes_apply = B * attn.H * N * (2 * K_out * attn.d_head + 2 * attn.d_head) * esize
+    achieved = bytes_apply / (t_apply / 1000.0)
+    line = {
+        "metric": "sparse-attn fwd tokens/sec at N=4096,K=128; % HBM roofline; recall@32",
+        "value": B * N / t, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": t * 1000.0, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": dt, "data": "synthetic",
+        "config": {"workload": desc, "global_batch": B, "seq_len": N,
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": achieved / 1e9, "peak": PEAK_HBM / 1e9,
+                     "unit": "GB/s", "frac": achieved / PEAK_HBM, "traffic": None,
+                     "kernel": "apply (" + ("layer 0, " if name == "transformer6" else "") +
+                               "gather attention)",
+                     "bytes_per_launch": bytes_apply, "ms_per_launch": t_apply},
+        "t_build_ms": t_build, "t_apply_ms": t_apply, "k_out": K_out,
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
 
 
 def recall_at_32(q, k, nb, va, rep, causal_variant=False):
@@ -153,6 +284,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-recall", action="store_true")
+    ap.add_argument("--workload", default="gqa_n4096",
+                    choices=["gqa_n4096"] + sorted(OTHER),
+                    help="gqa_n4096 (default): the bf16 GQA N=4096 workload above")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run a plain bf16 copy kernel (x*1, 256 MiB in, 256 MiB out) "
                          "5 times, as the reference point for rocprofv3 FETCH_SIZE/WRITE_SIZE")
@@ -164,6 +298,9 @@ def main():
         sys.exit(2)
     import torch
     dev = "cuda:0"
+    if args.workload != "gqa_n4096":
+        other_workload(args.workload, args)
+        return
     if args.calibrate_copy:
         n = 128 << 20
         src = torch.ones(n, dtype=torch.bfloat16, device=dev)

@@ -1020,12 +1020,10 @@ struct CutP {
                        // region of S (lists * N * C elements), in elements
     int N, M, R, NS, NB, C, Cs, Hq, Hkv, rep, bh0, G, causal, nlists;
     int64_t rows;
-    int32_t *zero;     // cleared by thread 0 (the select kernel's tie-row counter)
 };
 
 __global__ void __launch_bounds__(256) cut_kernel(CutP p) {
     const int64_t x = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (x == 0) *p.zero = 0;
     if (x >= p.rows * p.nlists) return;
     const int list = (int)(x % p.nlists);
     const int64_t rloc = x / p.nlists;
@@ -1205,7 +1203,7 @@ struct SelP {
     int64_t *out_idx;
     uint8_t *out_valid;
     int32_t *ties;
-    int32_t *tie_list;     // rows (within the chunk) handed to the exact top-k replay
+    int32_t *tie_list;     // rows (bh * N + n) handed to the exact top-k replay
     int32_t *tie_count;
     const float *aux;      // per row: q.k_n, then q.k_glob[j] (j < G), then q.k_0
     int NA;
@@ -2066,10 +2064,10 @@ select_kernel(SelP p) {
         // the order among equal scores (and a tied kk-th place) follows the
         // reference's nth_element / sort internals: replayed exactly later
         if ((btie || wave_ballot(dup)) && lane == 0 && p.tie_list)
-            p.tie_list[atomicAdd(p.tie_count, 1)] = (int)rloc;
+            p.tie_list[atomicAdd(p.tie_count, 1)] = (int)row;
         return;
     }
-    if (btie && lane == 0 && p.tie_list) p.tie_list[atomicAdd(p.tie_count, 1)] = (int)rloc;
+    if (btie && lane == 0 && p.tie_list) p.tie_list[atomicAdd(p.tie_count, 1)] = (int)row;
 
     full_merge_emit(bm, p, n, row, f, (int32_t *)ckey, sel_buf_words(p.words));
 }
@@ -2339,22 +2337,25 @@ topk_replay_kernel(SelP p, int chunk, int W) {
     const int cnt = *p.tie_count;
     const int kk = p.kk;
     for (int it = (int)blockIdx.x * RP_WAVES + wid; it < cnt; it += total) {
-        const int64_t rloc = p.tie_list[it];
-        const int n = (int)(rloc % p.N);
-        const int bhl = (int)(rloc / p.N);
-        const int bh = p.bh0 + bhl;
+        const int64_t row = p.tie_list[it];          // bh * N + n, over all query heads
+        const int n = (int)(row % p.N);
+        const int bh = (int)(row / p.N);
         const int b = bh / p.Hq, h = bh % p.Hq, g = h / p.rep;
         const int bk = b * p.Hkv + g;
-        const int64_t row = (int64_t)bh * p.N + n;
-        const float *arow = p.aux + rloc * p.NA;
-        const uint32_t kself = p.causal ? score_key(arow[0]) : 0u;
+        const T *qr = (const T *)p.q + b * p.qsb + h * p.qsh + (int64_t)n * p.qsn;
+        const T *kb = (const T *)p.k + b * p.ksb + g * p.ksh;
+        // the scores the candidate lists do not carry, with the rescore's
+        // arithmetic (as the aux kernel computes them): the query's own key,
+        // and glob ++ 0 for an empty bucket (lane j: entry j)
         const int ng = min(p.G + 1, SSA_WAVE);
-        if (lane < ng) gsc[lane] = score_key(arow[1 + lane]);
+        const uint32_t kq = exact_keys<T>(p, qr, kb, n, p.causal && lane == 0);
+        const uint32_t kself = (uint32_t)__builtin_amdgcn_readfirstlane((int)kq);
+        const int gv = lane < p.G ? (int)p.glob[lane < p.G ? lane : 0] : 0;
+        const uint32_t gk = exact_keys<T>(p, qr, kb, gv, lane < ng);
+        if (lane < ng) gsc[lane] = gk;
         for (int w = lane; w < p.words; w += SSA_WAVE) bm[w] = 0u;
         for (int t = lane; t < kk; t += SSA_WAVE) { A.key[t] = RP_NEGINF; A.cand[t] = 0; }
         const uint16_t *qids = p.qid + row * p.R * p.NS;
-        const T *qr = (const T *)p.q + b * p.qsb + h * p.qsh + (int64_t)n * p.qsn;
-        const T *kb = (const T *)p.k + b * p.ksb + g * p.ksh;
         rp_sync();
 
         for (int64_t s0 = 0; s0 < p.Call; s0 += chunk) {
@@ -2503,7 +2504,7 @@ Layout plan(const Dims &D) {
     L.tcnt = take(ninst * 4);
     L.kbase = take((nbh / D.rep + 2) * D.R * D.NS * D.rep * 4);
     L.S = take(nbh * D.N * D.nlists * D.Cs * 2);
-    L.tie_list = take(nbh * D.N * 4);
+    L.tie_list = take(D.BH * D.N * 4);
     L.tie_count = take(4);
     L.aux = take(nbh * D.N * (D.G + 3) * 4);
     L.knorm = take(D.BK * 4);
@@ -2664,6 +2665,8 @@ int launch_hash(const Dims &D, const ssa_graph_args *a, const Layout &L, char *w
     hp.vec16 = view_aligned16(a->q, (int)sizeof(T)) ? 1 : 0;
     hp.out = (uint16_t *)(ws + L.qid);
     hp.rows = D.BH * D.N;
+    // the tie-row counter of the select kernels (replayed once, after every chunk)
+    hp.zero1 = (int32_t *)(ws + L.tie_count);
     return launch_hash_one<T>(hp, D.d, st);
 }
 
@@ -2786,7 +2789,8 @@ int launch_replay(const SelP &sp, int chunk, hipStream_t st) {
     if (lds > SSA_LDS_BYTES || W > 65535) return SSA_OK;
     SSA_CHECK_HIP(hipFuncSetAttribute((const void *)topk_replay_kernel<T, LSH>,
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    const int64_t blocks = std::min<int64_t>(ceil_div(sp.rows, RP_WAVES), 1024);
+    // enough blocks for every resident wave to take a row (the rest exit at once)
+    const int64_t blocks = std::min<int64_t>(ceil_div(sp.rows, RP_WAVES), 8192);
     hipLaunchKernelGGL((topk_replay_kernel<T, LSH>), dim3((unsigned)blocks),
                        dim3(RP_WAVES * SSA_WAVE), lds, st, sp, chunk, W);
     SSA_CHECK_LAUNCH();
@@ -2879,6 +2883,7 @@ int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char 
                   hipStream_t st) {
     int rc = launch_hash<T>(D, a, L, ws, st, false);
     if (rc) return rc;
+    SelP last{};
     for (int64_t bh0 = 0; bh0 < D.BH; bh0 += D.nbh_chunk) {
         const int nbh = (int)((D.BH - bh0) < D.nbh_chunk ? (D.BH - bh0) : D.nbh_chunk);
         const int ninst = nbh * D.R * D.NS;
@@ -2960,14 +2965,8 @@ int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char 
         cp.N = D.N; cp.M = D.M; cp.R = D.R; cp.NS = D.NS; cp.NB = D.NB; cp.C = D.C; cp.Cs = D.Cs;
         cp.Hq = D.Hq; cp.Hkv = D.Hkv; cp.rep = D.rep; cp.bh0 = (int)bh0; cp.G = D.G;
         cp.causal = a->causal ? 1 : 0; cp.nlists = D.nlists; cp.rows = (int64_t)nbh * D.N;
-        // the cut kernel also clears the select kernel's tie-row counter
-        cp.zero = (int32_t *)(ws + L.tie_count);
-        const int64_t cut_blocks = ceil_div(cp.rows * D.nlists, 256);
-        if (cut_blocks > 0) {
-            hipLaunchKernelGGL(cut_kernel, dim3((unsigned)cut_blocks), dim3(256), 0, st, cp);
-        } else {
-            hipLaunchKernelGGL(fill_i32_kernel, dim3(1), dim3(64), 0, st, cp.zero, (int64_t)1, 0);
-        }
+        hipLaunchKernelGGL(cut_kernel, dim3((unsigned)ceil_div(cp.rows * D.nlists, 256)), dim3(256),
+                           0, st, cp);
         SSA_CHECK_LAUNCH();
 
         SelP sp{};
@@ -2997,11 +2996,16 @@ int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char 
         sp.nblocks = ceil_div(sp.rows, SEL_WAVES);
         rc = select_dispatch<T>(sp, st);
         if (rc) return rc;
-        rc = sp.mode == SSA_GRAPH_LSH ? launch_replay<T, true>(sp, D.chunk, st)
-                                      : launch_replay<T, false>(sp, D.chunk, st);
-        if (rc) return rc;
+        last = sp;
     }
-    return SSA_OK;
+    if (D.BH * D.N == 0) return SSA_OK;
+    // the rows every chunk flagged, in one launch: each row's replay is a long
+    // chain of dependent steps, so rows from all chunks run side by side
+    SelP rp = last;
+    rp.bh0 = 0;
+    rp.rows = D.BH * D.N;
+    return rp.mode == SSA_GRAPH_LSH ? launch_replay<T, true>(rp, D.chunk, st)
+                                    : launch_replay<T, false>(rp, D.chunk, st);
 }
 
 }  // namespace
