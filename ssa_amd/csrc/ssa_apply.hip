@@ -320,7 +320,9 @@ apply_fwd16_kernel(ApplyP p) {
     const int lane = lane_id();
     const int sub = lane / LPR, li = lane % LPR;
     const int Kp = (p.K + STEP - 1) / STEP * STEP;                               // padded slots
-    int32_t *ix = reinterpret_cast<int32_t *>(smem) + (int64_t)wid * 2 * Kp;    // key ids, -1 = masked
+    // key ids; masked, out-of-range and padding slots hold INT_MIN, whose low
+    // 24 bits (all a 24-bit multiply reads) address row 0
+    int32_t *ix = reinterpret_cast<int32_t *>(smem) + (int64_t)wid * 2 * Kp;
     float *sc = reinterpret_cast<float *>(ix + Kp);                           // scores, then p
 
     const int n = (int)(row % p.N);
@@ -336,9 +338,9 @@ apply_fwd16_kernel(ApplyP p) {
     const int64_t *nb = p.nb + row * p.K;
     const uint8_t *va = p.valid ? p.valid + row * p.K : nullptr;
 
-    // neighbour ids as int32 in LDS; masked, out-of-range and padding slots -1
+    // neighbour ids as int32 in LDS (ids < 2^24, checked at dispatch)
     for (int j = lane; j < Kp; j += SSA_WAVE) {
-        int x = -1;
+        int x = INT32_MIN;
         if (j < p.K) {
             const int64_t y = nb[j];
             if ((va ? va[j] != 0 : true) && y >= 0 && y < p.M) x = (int)y;
@@ -358,8 +360,7 @@ apply_fwd16_kernel(ApplyP p) {
         uint4 kv[U];
 #pragma unroll
         for (int u = 0; u < U; ++u)
-            kv[u] = *reinterpret_cast<const uint4 *>(
-                kb + (__umul24((uint32_t)max(xi[u], 0), krb) + lio));
+            kv[u] = *reinterpret_cast<const uint4 *>(kb + (__umul24((uint32_t)xi[u], krb) + lio));
         float part[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -426,8 +427,7 @@ apply_fwd16_kernel(ApplyP p) {
         uint4 vv[U];
 #pragma unroll
         for (int u = 0; u < U; ++u)
-            vv[u] = *reinterpret_cast<const uint4 *>(
-                vb + (__umul24((uint32_t)max(xi[u], 0), vrb) + lio));
+            vv[u] = *reinterpret_cast<const uint4 *>(vb + (__umul24((uint32_t)xi[u], vrb) + lio));
 #pragma unroll
         for (int u = 0; u < U; u += 2) {
             const uint32_t pp = Dot2<T>::pack(pj[u], pj[u + 1]);
@@ -571,8 +571,9 @@ apply_bwd_kernel(ApplyP p) {
     }
 }
 
-// The 16-bit path needs weights in the value dtype, 16-byte aligned rows and
-// byte offsets of every K / V row (and q row slice) within 32 bits.
+// The 16-bit path needs weights in the value dtype, 16-byte aligned rows,
+// byte offsets of every K / V row (and q row slice) within 32 bits, and key
+// ids below 2^24 (rows are addressed by 24-bit multiplies).
 bool fwd16_ok(const ApplyP &p, int elem, int D) {
     const int64_t v = 16 / elem;
     const bool aligned = ((uintptr_t)p.q % 16 == 0) && ((uintptr_t)p.k % 16 == 0) &&
@@ -581,7 +582,7 @@ bool fwd16_ok(const ApplyP &p, int elem, int D) {
                          p.ksh % v == 0 && p.ksn % v == 0 && p.vsb % v == 0 && p.vsh % v == 0 &&
                          p.vsn % v == 0 && p.osb % v == 0 && p.osh % v == 0 && p.osn % v == 0;
     const int64_t lim = (int64_t)1 << 24;
-    const bool small = p.ksn * elem < lim && p.vsn * elem < lim &&
+    const bool small = p.M < lim && p.ksn * elem < lim && p.vsn * elem < lim &&
                        ((int64_t)p.M * p.ksn + D) * elem < ((int64_t)1 << 31) &&
                        ((int64_t)p.M * p.vsn + D) * elem < ((int64_t)1 << 31);
     return !p.fp32w && aligned && small;
