@@ -141,6 +141,34 @@ __device__ __forceinline__ int lanes_below(uint64_t m) {
                                      __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
 }
 
+// Swap count of a Hoare partition from its stopper lists: TL[f ..] holds the
+// numL left stoppers in ascending position, TR[f ..] the numR right stoppers
+// in ascending position; pair k couples the k-th left stopper with the k-th
+// right stopper from the end, and the pairs that swap (left one left of the
+// right one) are a prefix.  The largest s with TL[f + s - 1] < TR[f + numR - s]
+// is found by a 64-ary search: each round the wave tests 64 evenly spaced
+// candidates at once and keeps the range between the last true and the first
+// false, so the answer takes one or two rounds of parallel LDS reads.  Every
+// lane must be active; the result is wave-uniform.
+__device__ __forceinline__ int hoare_swap_count(const uint16_t *TL, const uint16_t *TR, int f,
+                                                int numL, int numR) {
+    const int lane = (int)__lane_id();
+    int lo = 0, hi = numL < numR ? numL : numR;     // the answer lies in [lo, hi]
+    while (hi > lo) {
+        const int span = hi - lo;
+        // lane j tests lo + ceil(span (j + 1) / 64): non-decreasing, the last is hi,
+        // and every value of (lo, hi] appears once span <= 64
+        const int mid = lo + (span * (lane + 1) + 63) / 64;
+        const bool t = (int)TL[f + mid - 1] < (int)TR[f + numR - mid];
+        const int c = __popcll(__ballot(t));        // lanes 0 .. c-1 hold true
+        const int nlo = c > 0 ? __builtin_amdgcn_readlane(mid, c - 1) : lo;
+        const int nhi = c < 64 ? __builtin_amdgcn_readlane(mid, c < 64 ? c : 63) - 1 : hi;
+        lo = nlo;
+        hi = nhi;
+    }
+    return lo;
+}
+
 // order-preserving map fp32 -> uint32 (larger float -> larger key); all
 // finite values and +/-inf map above 0, so 0 can mark "no score".
 __device__ __forceinline__ uint32_t score_key(float f) {

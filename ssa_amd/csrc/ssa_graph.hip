@@ -2221,12 +2221,7 @@ __device__ int rp_partition(const RpArr &a, uint16_t *TL, uint16_t *TR, int f, i
         numR += __popcll(bR);
     }
     rp_sync();
-    int lo = 0, hi = numL < numR ? numL : numR;
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if ((int)TL[f + mid - 1] < (int)TR[f + numR - mid]) lo = mid; else hi = mid - 1;
-    }
-    const int sw = lo;
+    const int sw = hoare_swap_count(TL, TR, f, numL, numR);
     for (int k0 = 0; k0 < sw; k0 += SSA_WAVE) {
         const int k = k0 + lane;
         if (k < sw) rp_swap(a, TL[f + k], TR[f + numR - 1 - k]);

@@ -15,7 +15,7 @@
 //     and R_k the k-th position in [f, l) holding key <= p (descending), the
 //     scan swaps (L_k, R_k) for every k with L_k < R_k (a prefix k <= s) and
 //     stops at cut = min(L_{s+1}, R_s).  A wave finds the stoppers with
-//     ballots, s by binary search, then performs all s swaps in parallel;
+//     ballots, s by a 64-ary search, then performs all s swaps in parallel;
 //   * both children inherit depth - 1; a segment reaching depth 0 is heap-
 //     sorted by one lane (the depth limit is 2*floor(log2 n));
 //   * a segment of at most 64 elements is finished (down to its leaves) by one
@@ -133,12 +133,7 @@ __device__ int wave_partition(uint16_t *key, uint16_t *idx, uint16_t *TL, uint16
     wave_sync_lds();
 
     // s = number of k (1-based) with L_k < R_k, where R_k = TR[numR - k]
-    int lo = 0, hi = numL < numR ? numL : numR;
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if ((int)TL[f + mid - 1] < (int)TR[f + numR - mid]) lo = mid; else hi = mid - 1;
-    }
-    const int s = lo;
+    const int s = hoare_swap_count(TL, TR, f, numL, numR);
     for (int k0 = 0; k0 < s; k0 += SSA_WAVE) {
         const int k = k0 + lane;
         if (k < s) {
@@ -435,11 +430,7 @@ sort_top_kernel(const uint16_t *ids, int n, int NB, int32_t *perm, int32_t *bsta
             __syncthreads();
             if (part && gi == 0) {                    // s = #k with L_k < R_k
                 const int numL = sh.nL[g], numR = sh.nR[g];
-                int lo = 0, hi = numL < numR ? numL : numR;
-                while (lo < hi) {
-                    const int mid = (lo + hi + 1) >> 1;
-                    if ((int)TL[f + mid - 1] < (int)TR[f + numR - mid]) lo = mid; else hi = mid - 1;
-                }
+                const int lo = hoare_swap_count(TL, TR, f, numL, numR);
                 int cut = 0x7fffffff;
                 if (lo < numL) cut = TL[f + lo];
                 if (lo > 0) { const int r = TR[f + numR - lo]; cut = r < cut ? r : cut; }
