@@ -110,20 +110,21 @@ def _timed(fn, steps, warmup):
 
 
 def _stage_times(attn, q, k, v, N, M, B, causal, cross, reps):
-    """build and apply, each bracketed by events on the launch stream."""
+    """build and apply as forward runs them without autograd (int32 ids), each
+    bracketed by events on the launch stream."""
     import torch
     st = torch.cuda.current_stream()
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(reps)]
     for e in evs:
         e[0].record(st)
-        nb, va = attn.build_graph(q, k, N, M, B, q.device, causal, cross)
+        ids = attn._build_graph_ids32(q, k, N, M, B, causal, cross)
         e[1].record(st)
-        attn.apply_graph(q, k, v, nb, va)
+        attn.apply_graph(q, k, v, ids, None)
         e[2].record(st)
     torch.cuda.synchronize()
     t_build = sum(e[0].elapsed_time(e[1]) for e in evs) / reps
     t_apply = sum(e[1].elapsed_time(e[2]) for e in evs) / reps
-    return t_build, t_apply, nb.shape[-1]
+    return t_build, t_apply, ids.shape[-1]
 
 
 def other_workload(name, args):
@@ -330,8 +331,9 @@ def main():
     print(f"# forward {ms:.3f} ms/step", file=sys.stderr, flush=True)
 
     # per-stage timing with events on the launch stream (torch's current stream):
-    # build then apply, as inside forward, with each stage bracketed by its own
-    # events so that the apply launches see the same cache state as in forward
+    # build then apply as forward runs them without autograd (the graph as int32
+    # ids, -1 = invalid), each stage bracketed by its own events so that the
+    # apply launches see the same cache state as in forward
     with torch.no_grad():
         q = attn._split_q(attn.Wq(x))
         k = attn._split_kv_compact(attn.Wk(x))
@@ -341,24 +343,24 @@ def main():
         evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(reps)]
         for e in evs:
             e[0].record(st)
-            nb, va = attn.build_graph(q, k, N, N, B, x.device, True, False)
+            ids = attn._build_graph_ids32(q, k, N, N, B, True, False)
             e[1].record(st)
-            out = attn.apply_graph(q, k, v, nb, va)
+            out = attn.apply_graph(q, k, v, ids, None)
             e[2].record(st)
         torch.cuda.synchronize()
         # apply alone, back to back on one graph: K/V rows, q and the index
         # table stay cache-resident, so this is the gather path's warm rate
         ew = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
-        out = attn.apply_graph(q, k, v, nb, va)
+        out = attn.apply_graph(q, k, v, ids, None)
         ew[0].record(st)
         for _ in range(reps):
-            out = attn.apply_graph(q, k, v, nb, va)
+            out = attn.apply_graph(q, k, v, ids, None)
         ew[1].record(st)
         torch.cuda.synchronize()
     t_apply_warm = ew[0].elapsed_time(ew[1]) / reps
     t_build = sum(e[0].elapsed_time(e[1]) for e in evs) / reps
     t_apply = sum(e[1].elapsed_time(e[2]) for e in evs) / reps
-    K_out = nb.shape[-1]
+    K_out = ids.shape[-1]
     bytes_apply = B * H * N * (2 * K_out * d + 2 * d) * 2
     achieved = bytes_apply / (t_apply / 1000.0)
     traffic = measured_traffic(APPLY_KERNEL)
@@ -378,6 +380,7 @@ def main():
     rec = None
     if not args.no_recall:
         with torch.no_grad():
+            nb, va = ids.long().clamp_min(0), ids >= 0      # build_graph's (neighbors, valid)
             r0, rall = recall_at_32(q, k, nb, va, attn.kv_rep)
             c0, call = recall_at_32(q, k, nb, va, attn.kv_rep, causal_variant=True)
         rec = {"head0": r0, "all_heads": rall, "causal_head0": c0, "causal_all_heads": call}

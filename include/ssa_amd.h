@@ -89,6 +89,11 @@ typedef struct {
     int32_t *out_ties;       /* optional single counter (caller zeroes it): queries   */
                              /* whose kk-th LSH score is tied; their selection is     */
                              /* replayed with the reference's top-k tie order         */
+    /* FULL mode, optional (no counterpart in the reference): the same graph as   */
+    /* (B,Hq,N,k_out) int32 ids with -1 in the invalid slots, for callers that    */
+    /* only hand the graph to ssa_sparse_gather_attention; when set, out_idx and */
+    /* out_valid are not written and may be NULL.                                */
+    int32_t *out_idx32;
 } ssa_graph_args;
 
 /* Output width of the FULL graph: self-attention 1 + min(K-1, 2w+1+G+kk),
@@ -170,6 +175,10 @@ typedef struct {
     uint64_t seed;
     void *out;               /* dtype of q */
     int64_t out_sb, out_sh, out_sn;
+    /* optional (no counterpart in the reference): the graph as int32 ids, a     */
+    /* negative id marking an invalid slot (ssa_graph_args.out_idx32); when set, */
+    /* neighbors and valid are not read.  Not accepted by the backward.          */
+    const int32_t *neighbors32;
 } ssa_apply_args;
 
 int ssa_sparse_gather_attention(const ssa_apply_args *a, void *stream);

@@ -42,6 +42,7 @@ class GraphArgs(ctypes.Structure):
         ("glob", c_vp), ("G", c_i32),
         ("q_proj", c_vp), ("k_proj", c_vp),
         ("out_idx", c_vp), ("out_valid", c_vp), ("out_ties", c_vp),
+        ("out_idx32", c_vp),
     ]
 
 
@@ -54,6 +55,7 @@ class ApplyArgs(ctypes.Structure):
         ("scale", ctypes.c_float), ("fp32_weights", c_i32), ("dropout_p", ctypes.c_float),
         ("seed", ctypes.c_uint64),
         ("out", c_vp), ("out_sb", c_i64), ("out_sh", c_i64), ("out_sn", c_i64),
+        ("neighbors32", c_vp),
     ]
 
 
@@ -144,10 +146,11 @@ def _ptr(t):
 
 # --------------------------------------------------------------------------- graph build
 def build_graph(q, k, rand_proj, *, P, T, C, top_k, window, causal, is_cross, total_k, glob,
-                mode=GRAPH_FULL, q_proj=None, k_proj=None, count_ties=False):
+                mode=GRAPH_FULL, q_proj=None, k_proj=None, count_ties=False, ids32=False):
     """Run ssa_build_graph.  q (B,Hq,N,d), k (B,Hkv,M,d) views on one device.
 
-    Returns (out_idx, out_valid or None, ties or None)."""
+    Returns (out_idx, out_valid or None, ties or None).  With ids32 (FULL mode)
+    out_idx is int32 with -1 in the invalid slots and out_valid is None."""
     require_device(q, k, rand_proj, glob)
     B, Hq, N, d = q.shape
     Bk, Hkv, M, dk = k.shape
@@ -178,12 +181,18 @@ def build_graph(q, k, rand_proj, *, P, T, C, top_k, window, causal, is_cross, to
     wsb = L.ssa_graph_workspace_bytes(ctypes.byref(a))
     if wsb < 0:
         _check(-1, "build_graph")
-    out = torch.empty((B, Hq, N, width), dtype=torch.int64, device=q.device)
+    compact = ids32 and mode == GRAPH_FULL
+    out = torch.empty((B, Hq, N, width), dtype=torch.int32 if compact else torch.int64,
+                      device=q.device)
     valid = (torch.empty((B, Hq, N, width), dtype=torch.bool, device=q.device)
-             if mode == GRAPH_FULL else None)
+             if mode == GRAPH_FULL and not compact else None)
     ties = torch.zeros(1, dtype=torch.int32, device=q.device) if count_ties else None
     ws = torch.empty(max(int(wsb), 1), dtype=torch.uint8, device=q.device)
-    a.out_idx, a.out_valid, a.out_ties = out.data_ptr(), _ptr(valid), _ptr(ties)
+    if compact:
+        a.out_idx32 = out.data_ptr()
+    else:
+        a.out_idx, a.out_valid = out.data_ptr(), _ptr(valid)
+    a.out_ties = _ptr(ties)
     _check(L.ssa_build_graph(ctypes.byref(a), ws.data_ptr(), int(wsb), _stream(q)), "build_graph")
     # keep inputs alive until the stream has consumed them
     _keep = (qk, kk_, rp, g, qp, kp, ws)
@@ -297,19 +306,25 @@ def merge_neighbors(win, glob, lsh, has_self: bool, total_k: int):
 
 
 # --------------------------------------------------------------------------- apply
-def _apply_args(q, k, v, neighbors, valid, scale, fp32w, dropout_p, seed, out):
+def _apply_args(q, k, v, neighbors, valid, scale, fp32w, dropout_p, seed, out, ids32=True):
+    """int32 neighbours without a mask are passed as they are (a negative id
+    is an invalid slot, as the int64 path treats it) when ids32 allows."""
     B, Hq, N, d = q.shape
     _, Hkv, M, _ = k.shape
     K = neighbors.shape[-1]
     qa, qk = view4(q)
     ka, kk_ = view4(k)
     va, vk = view4(v)
-    nb = neighbors.to(torch.int64).contiguous()
-    vl = valid.to(torch.bool).contiguous() if valid is not None else None
     a = ApplyArgs()
     a.B, a.Hq, a.Hkv, a.N, a.M, a.d, a.K = B, Hq, Hkv, N, M, d, K
     a.q, a.k, a.v = qa, ka, va
-    a.neighbors, a.valid = nb.data_ptr(), _ptr(vl)
+    if ids32 and neighbors.dtype == torch.int32 and valid is None:
+        nb, vl = neighbors.contiguous(), None
+        a.neighbors32 = nb.data_ptr()
+    else:
+        nb = neighbors.to(torch.int64).contiguous()
+        vl = valid.to(torch.bool).contiguous() if valid is not None else None
+        a.neighbors, a.valid = nb.data_ptr(), _ptr(vl)
     a.scale, a.fp32_weights, a.dropout_p, a.seed = float(scale), int(fp32w), float(dropout_p), seed
     a.out = out.data_ptr()
     a.out_sb, a.out_sh, a.out_sn = out.stride(0), out.stride(1), out.stride(2)
@@ -339,7 +354,8 @@ def gather_attention_bwd(q, k, v, neighbors, valid, scale, fp32w, dropout_p, see
     dk = torch.zeros((B, Hkv, M, d), dtype=torch.float32, device=q.device)
     dv = torch.zeros((B, Hkv, M, d), dtype=torch.float32, device=q.device)
     dummy = torch.empty((B, N, Hq, d), dtype=q.dtype, device=q.device).transpose(1, 2)
-    a, keep = _apply_args(q, k, v, neighbors, valid, scale, fp32w, dropout_p, seed, dummy)
+    a, keep = _apply_args(q, k, v, neighbors, valid, scale, fp32w, dropout_p, seed, dummy,
+                          ids32=False)
     b = ApplyBwdArgs()
     b.fwd = a
     b.dout, b.dq, b.dk, b.dv = do.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr()

@@ -25,6 +25,7 @@ struct ApplyP {
     int64_t qsb, qsh, qsn, ksb, ksh, ksn, vsb, vsh, vsn;
     const int64_t *nb;
     const uint8_t *valid;
+    const int32_t *nb32;   // or the graph as int32 ids, negative = invalid
     float scale;
     int32_t fp32w;
     float drop_p;
@@ -106,13 +107,13 @@ apply_fwd_kernel(ApplyP p) {
     const T *qrow = (const T *)p.q + b * p.qsb + h * p.qsh + (int64_t)n * p.qsn;
     const T *kb = (const T *)p.k + b * p.ksb + g * p.ksh;
     const T *vb = (const T *)p.v + b * p.vsb + g * p.vsh;
-    const int64_t *nb = p.nb + row * p.K;
+    const int64_t *nb = p.nb ? p.nb + row * p.K : nullptr;
     const uint8_t *va = p.valid ? p.valid + row * p.K : nullptr;
 
     // neighbour ids once, as int32 in LDS; masked or out-of-range slots -> -1
     for (int j = lane; j < p.K; j += SSA_WAVE) {
-        const int64_t x = nb[j];
-        const bool o = (va ? va[j] != 0 : true) && x >= 0 && x < p.M;
+        const int64_t x = p.nb32 ? (int64_t)p.nb32[row * p.K + j] : nb[j];
+        const bool o = (p.nb32 ? true : (va ? va[j] != 0 : true)) && x >= 0 && x < p.M;
         ix[j] = o ? (int)x : -1;
     }
     float qf[VEC];
@@ -335,15 +336,15 @@ apply_fwd16_kernel(ApplyP p) {
     const char *vb = (const char *)((const T *)p.v + b * p.vsb + g * p.vsh);
     const uint32_t krb = (uint32_t)(p.ksn * 2), vrb = (uint32_t)(p.vsn * 2);   // row bytes < 2^24
     const uint32_t lio = (uint32_t)li * 16u;
-    const int64_t *nb = p.nb + row * p.K;
+    const int64_t *nb = p.nb ? p.nb + row * p.K : nullptr;
     const uint8_t *va = p.valid ? p.valid + row * p.K : nullptr;
 
     // neighbour ids as int32 in LDS (ids < 2^24, checked at dispatch)
     for (int j = lane; j < Kp; j += SSA_WAVE) {
         int x = INT32_MIN;
         if (j < p.K) {
-            const int64_t y = nb[j];
-            if ((va ? va[j] != 0 : true) && y >= 0 && y < p.M) x = (int)y;
+            const int64_t y = p.nb32 ? (int64_t)p.nb32[row * p.K + j] : nb[j];
+            if ((p.nb32 ? true : (va ? va[j] != 0 : true)) && y >= 0 && y < p.M) x = (int)y;
         }
         ix[j] = x;
     }
@@ -659,7 +660,8 @@ int apply_common(const ssa_apply_args *a, ApplyP &p) {
     if ((rc = check_view(a->q, a->q.dtype, "q"))) return rc;
     if ((rc = check_view(a->k, a->q.dtype, "k"))) return rc;
     if ((rc = check_view(a->v, a->q.dtype, "v"))) return rc;
-    SSA_CHECK_ARG(a->neighbors != nullptr && a->out != nullptr, "sparse_gather_attention: null");
+    SSA_CHECK_ARG((a->neighbors != nullptr || a->neighbors32 != nullptr) && a->out != nullptr,
+                  "sparse_gather_attention: null");
     SSA_CHECK_ARG(a->dropout_p >= 0.f && a->dropout_p < 1.f, "dropout p must be in [0, 1)");
     p = ApplyP{};
     p.B = a->B; p.Hq = a->Hq; p.Hkv = a->Hkv; p.N = a->N; p.M = a->M; p.K = a->K;
@@ -668,7 +670,7 @@ int apply_common(const ssa_apply_args *a, ApplyP &p) {
     p.qsb = a->q.sb; p.qsh = a->q.sh; p.qsn = a->q.sn;
     p.ksb = a->k.sb; p.ksh = a->k.sh; p.ksn = a->k.sn;
     p.vsb = a->v.sb; p.vsh = a->v.sh; p.vsn = a->v.sn;
-    p.nb = a->neighbors; p.valid = a->valid;
+    p.nb = a->neighbors; p.valid = a->valid; p.nb32 = a->neighbors32;
     p.scale = a->scale; p.fp32w = a->fp32_weights;
     p.drop_p = a->dropout_p;
     p.drop_scale = a->dropout_p > 0.f ? 1.f / (1.f - a->dropout_p) : 1.f;
@@ -705,6 +707,8 @@ extern "C" int ssa_sparse_gather_attention_bwd(const ssa_apply_bwd_args *a, void
     int rc = apply_common(&a->fwd, p);
     if (rc) return rc;
     SSA_CHECK_ARG(a->dout && a->dq && a->dk && a->dv, "sparse_gather_attention_bwd: null grad");
+    SSA_CHECK_ARG(a->fwd.neighbors32 == nullptr && a->fwd.neighbors != nullptr,
+                  "sparse_gather_attention_bwd: needs the int64 neighbours");
     p.dout = a->dout; p.dq = a->dq; p.dk = a->dk; p.dv = a->dv;
     return run_apply(p, a->fwd.q.dtype, a->fwd.d, (hipStream_t)stream, true);
 }

@@ -1202,6 +1202,7 @@ struct SelP {
     int64_t Call, rows;
     int64_t *out_idx;
     uint8_t *out_valid;
+    int32_t *out_idx32;    // FULL mode: the graph as int32 ids (-1 = invalid) instead
     int32_t *ties;
     int32_t *tie_list;     // rows (bh * N + n) handed to the exact top-k replay
     int32_t *tie_count;
@@ -1420,8 +1421,16 @@ __device__ void full_merge_emit(uint32_t *bm, const SelP &p, int n, int64_t row,
 
     const int self = p.cross ? 0 : 1;
     const int ks = p.Kout - self;
-    int64_t *orow = p.out_idx + row * p.Kout;
-    uint8_t *vrow = p.out_valid + row * p.Kout;
+    // slot i gets key id v (valid) or the padding; as int64 + valid byte, or
+    // as one int32 with -1 for padding
+    auto put = [&](int i, int v, bool valid) {
+        if (p.out_idx32) {
+            p.out_idx32[row * p.Kout + i] = valid ? v : -1;
+        } else {
+            p.out_idx[row * p.Kout + i] = valid ? (int64_t)v : 0;
+            p.out_valid[row * p.Kout + i] = valid ? 1 : 0;
+        }
+    };
     const int wpl = (p.words + SSA_WAVE - 1) / SSA_WAVE;
     const int w0 = lane * wpl;
     int cntb = 0;
@@ -1451,8 +1460,7 @@ __device__ void full_merge_emit(uint32_t *bm, const SelP &p, int n, int64_t row,
             carry = __builtin_amdgcn_readlane(s, SSA_WAVE - 1);
             if (in) {
                 const int w = scr[s];
-                orow[self + t] = (int64_t)(w * 32 + nth_set_bit(bm[w], t - s));
-                vrow[self + t] = 1;
+                put(self + t, w * 32 + nth_set_bit(bm[w], t - s), true);
             }
         }
     } else {
@@ -1462,19 +1470,16 @@ __device__ void full_merge_emit(uint32_t *bm, const SelP &p, int n, int64_t row,
             while (word && q < ks) {
                 const int bitp = __ffs(word) - 1;
                 word &= word - 1;
-                orow[self + q] = (int64_t)(w * 32 + bitp);
-                vrow[self + q] = 1;
+                put(self + q, w * 32 + bitp, true);
                 ++q;
             }
         }
     }
     for (int i = self + filled + lane; i < p.Kout; i += SSA_WAVE) {
-        orow[i] = 0;
-        vrow[i] = 0;
+        put(i, 0, false);
     }
     if (self && lane == 0) {
-        orow[0] = n;
-        vrow[0] = 1;
+        put(0, n, true);
     }
 }
 
@@ -2983,6 +2988,7 @@ int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char 
         sp.Kout = D.Kout; sp.bh0 = (int)bh0; sp.words = ((D.M + 31) / 32 + 2) & ~1;
         sp.Call = D.Call; sp.rows = (int64_t)nbh * D.N;
         sp.out_idx = a->out_idx; sp.out_valid = a->out_valid; sp.ties = a->out_ties;
+        sp.out_idx32 = a->mode == SSA_GRAPH_FULL ? a->out_idx32 : nullptr;
         sp.tie_list = (int32_t *)(ws + L.tie_list);
         sp.tie_count = (int32_t *)(ws + L.tie_count);
         sp.aux = ap.out;
@@ -3026,8 +3032,10 @@ int build_phase(const ssa_graph_args *a, void *workspace, int64_t workspace_byte
     int rc = make_dims(a, D, qphase);
     if (rc) return rc;
     if (qphase) {
-        SSA_CHECK_ARG(a->out_idx, "build_graph: out_idx is null");
-        SSA_CHECK_ARG(a->mode != SSA_GRAPH_FULL || a->out_valid, "build_graph: out_valid is null");
+        const bool i32 = a->mode == SSA_GRAPH_FULL && a->out_idx32;
+        SSA_CHECK_ARG(i32 || a->out_idx, "build_graph: out_idx is null");
+        SSA_CHECK_ARG(i32 || a->mode != SSA_GRAPH_FULL || a->out_valid,
+                      "build_graph: out_valid is null");
     }
     const Layout L = plan(D);
     if (workspace_bytes < L.total || !workspace) {

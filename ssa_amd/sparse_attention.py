@@ -340,6 +340,16 @@ class SparseAttention(nn.Module):
             mode=_lib.GRAPH_FULL, q_proj=qp, k_proj=kp)
         return out, valid
 
+    def _build_graph_ids32(self, q, k, N, M, B, causal, is_cross) -> torch.Tensor:
+        """build_graph's graph as one int32 tensor, -1 where valid is False."""
+        _lib.require_device(q, k)
+        lb = self.lsh_builder
+        out, _, _ = _lib.build_graph(
+            q, k, lb.rand_proj, P=lb.compute_effective_p(M, lb.C, lb.max_P), T=lb.T, C=lb.C,
+            top_k=self.lsh_k, window=self.config.window_size, causal=causal, is_cross=is_cross,
+            total_k=self.K, glob=self._glob_ids(M, q.device), mode=_lib.GRAPH_FULL, ids32=True)
+        return out
+
     def _glob_ids(self, M: int, device) -> torch.Tensor:
         """``glob_builder(M, device)``, kept per (M, device) so that a forward
         launches no arange: the ids depend on nothing else (explicit indices
@@ -420,8 +430,15 @@ class SparseAttention(nn.Module):
         M = src.shape[1]
         causal = self.config.causal and not is_cross
         q, k, v = self._project(x, src, is_cross)
-        neighbors, valid = self.build_graph(q, k, N, M, B, x.device, causal, is_cross)
-        out = self.apply_graph(q, k, v, neighbors, valid)
+        if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
+            neighbors, valid = self.build_graph(q, k, N, M, B, x.device, causal, is_cross)
+            out = self.apply_graph(q, k, v, neighbors, valid)
+        else:
+            # no autograd: the same graph as int32 ids with -1 in the invalid
+            # slots, which the gather attention reads as it is (a third of the
+            # bytes of int64 ids and a mask, written once and read once)
+            neighbors, valid = self._build_graph_ids32(q, k, N, M, B, causal, is_cross), None
+            out = self.apply_graph(q, k, v, neighbors, None)
         out_proj = self.Wo(self._merge(out))
         if not return_stats:
             return out_proj, {}
@@ -432,7 +449,8 @@ class SparseAttention(nn.Module):
             "peak_sparse_elems": peak_sparse,
             "peak_full_elems": peak_full,
             "compression": peak_full / peak_sparse,
-            "padding_fraction": (~valid).float().mean().item(),
+            "padding_fraction": ((~valid).float().mean().item() if valid is not None
+                                 else (neighbors < 0).float().mean().item()),
         }
 
 

@@ -4,6 +4,8 @@ import ctypes
 import os
 import re
 
+import pytest
+
 from conftest import ROOT
 
 HEADER = os.path.join(ROOT, "include", "ssa_amd.h")
@@ -38,13 +40,36 @@ def test_version_and_error_text():
     assert isinstance(_lib.lib().ssa_last_error(), bytes)
 
 
-def test_struct_sizes_match_c_layout():
-    """ctypes mirrors of the header structs have the C layout sizes."""
+def test_struct_layouts_match_the_header(tmp_path):
+    """Every field of the ctypes mirrors sits at the offset the C compiler gives
+    it in include/ssa_amd.h, and the structs have the same sizes."""
+    import shutil
+    import subprocess
     from ssa_amd import _lib
-    assert ctypes.sizeof(_lib.Tensor4) == 40
-    # every field of GraphArgs is 4 or 8 bytes with natural alignment
-    assert ctypes.sizeof(_lib.GraphArgs) % 8 == 0
-    assert _lib.GraphArgs.out_ties.offset + 8 == ctypes.sizeof(_lib.GraphArgs)
+    gcc = shutil.which("gcc")
+    if gcc is None:
+        pytest.skip("no C compiler")
+    mirrors = {"ssa_tensor4": _lib.Tensor4, "ssa_graph_args": _lib.GraphArgs,
+               "ssa_apply_args": _lib.ApplyArgs, "ssa_apply_bwd_args": _lib.ApplyBwdArgs}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "ssa_amd.h"', 'int main(void) {']
+    for cname, py in mirrors.items():
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for f in py._fields_:
+            lines.append(f'printf("{cname} {f[0]} %zu\\n", offsetof({cname}, {f[0]}));')
+    lines += ['return 0;', '}']
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "layout"
+    inc = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include")
+    subprocess.check_call([gcc, "-std=c99", "-I", inc, str(src), "-o", str(exe)])
+    got = {}
+    for line in subprocess.check_output([str(exe)], text=True).splitlines():
+        cname, field, val = line.split()
+        got[(cname, field)] = int(val)
+    for cname, py in mirrors.items():
+        assert got[(cname, "size")] == ctypes.sizeof(py), cname
+        for f in py._fields_:
+            assert got[(cname, f[0])] == getattr(py, f[0]).offset, (cname, f[0])
 
 
 def test_argument_errors_are_reported_without_a_gpu():

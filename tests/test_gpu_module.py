@@ -185,6 +185,40 @@ def test_build_apply_split_matches_forward():
         assert torch.allclose(ref, out, atol=1e-6)
 
 
+def test_forward_without_autograd_uses_int32_graph_bit_identically():
+    """forward() without autograd builds the graph as int32 ids (-1 = invalid):
+    the same ids as build_graph where valid, and the same output, bit for bit,
+    as build_graph + apply_graph on the int64 graph (bf16 and fp32, self and
+    cross); the stats read the same padding fraction."""
+    from ssa_amd import _lib
+    for dtype in (torch.float32, torch.bfloat16):
+        for kw, cross in [(BASE, False), (CAUSAL, False), (BASE, True)]:
+            a = _attn(**kw).eval()
+            for p_ in a.parameters():
+                p_.data = p_.data.to(dtype)
+            x = torch.randn(2, 48, kw["d_model"], device=DEV).to(dtype)
+            kv = torch.randn(2, 80, kw["d_model"], device=DEV).to(dtype) if cross else None
+            src = kv if cross else x
+            M = src.shape[1]
+            causal = kw["causal"] and not cross
+            with torch.no_grad():
+                out, stats = a(x, key_value=kv, return_stats=True)
+                q = a._split_q(a.Wq(x))
+                k = a._split_kv_compact(a.Wk(src))
+                v = a._split_kv_compact(a.Wv(src))
+                nb, va = a.build_graph(q, k, 48, M, 2, DEV, causal, cross)
+                ids = a._build_graph_ids32(q, k, 48, M, 2, causal, cross)
+                ref = a.Wo(a._merge(a.apply_graph(q, k, v, nb, va)))
+                via32 = _lib.gather_attention_fwd(q, k, v, ids, None, a.scale)
+                via64 = _lib.gather_attention_fwd(q, k, v, nb, va, a.scale)
+            assert ids.dtype == torch.int32
+            assert torch.equal(ids.long(), torch.where(va, nb, torch.full_like(nb, -1)))
+            assert torch.equal(out, ref)
+            assert torch.equal(via32, via64)
+            assert stats["padding_fraction"] == (~va).float().mean().item()
+            assert stats["neighbors_shape"] == tuple(nb.shape)
+
+
 def test_gradients_reach_all_projections():
     a = _attn(d_model=32, num_heads=2, num_neighbors=12, max_num_hashes=2, window_size=3,
               num_global_tokens=1)
