@@ -74,7 +74,11 @@ template <> struct Cvt<f16_t> {
 };
 
 // ---------------------------------------------------------------- wave ops
-__device__ __forceinline__ int lane_id() { return (int)__lane_id(); }
+__device__ __forceinline__ int lane_id() {
+    const unsigned l = __lane_id();
+    __builtin_assume(l < SSA_WAVE);
+    return (int)l;
+}
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -183,10 +187,14 @@ __device__ __forceinline__ uint32_t score_key(float f) {
 // `scale` taking +-(a bound of the query's scores) to the ends of the range and
 // NaN above everything.  Monotone (fma, clamp and truncation all are), so a
 // larger code means a larger score and equal scores share a code; scores that
-// share a code are told apart by their exact keys.
+// share a code are told apart by their exact keys.  The code is 65535 minus
+// the clamped, truncated -s * scale + 32767: fmaxf(NaN, 0) is 0, so a NaN
+// score gets 65535 with no test of its own (the clamp is one v_med3_f32).
+__device__ __forceinline__ uint32_t score_neg_code(float s, float scale) {
+    return (uint32_t)fminf(fmaxf(fmaf(-s, scale, 32767.f), 0.f), 65535.f);
+}
 __device__ __forceinline__ uint32_t score_code(float s, float scale) {
-    if (s != s) return 0xffffu;
-    return (uint32_t)fminf(fmaxf(fmaf(s, scale, 32768.f), 0.f), 65535.f);
+    return 65535u - score_neg_code(s, scale);
 }
 // scale of a query with |q|^2 = q2 against keys with max |k|^2 = k2: every
 // score q.k lies within +-sqrt(q2 k2), which maps onto +-32767 (any positive

@@ -348,13 +348,24 @@ __global__ void __launch_bounds__(256) knorm_kernel(KnP p) {
 struct QbP {
     const uint16_t *qid;
     const int32_t *bsize;   // key bucket sizes (BK*R, NB)
+    const int32_t *bstart;  // key bucket starts (BK*R, NB)
     int32_t *cnt, *off, *cur, *qlist, *tiles, *ntiles;
     int32_t *tcnt;          // tiles per instance
     int32_t *kbase;         // first tile of each order key
     int32_t *hcnt;          // per (instance, query block, bucket): count, then first position
     int32_t *qpos;          // per (instance, query): position in qlist
-    int N, R, NS, NB, Hq, Hkv, rep, bh0, ninst;
+    int N, R, NS, NB, Hq, Hkv, rep, bh0, ninst, C;
 };
+
+// Rescore tiles are stored in launch order: the dispatcher sends block i to
+// XCD i % 8, and XCD x is to take the contiguous tile range [x * per,
+// (x + 1) * per) in order, so that its L2 keeps the candidate rows adjacent
+// tiles share.  Tile L therefore sits in slot (L % per) * 8 + L / per, and a
+// block reads its slot and the tile count together (no dependent read).
+__device__ __forceinline__ int rs_tile_slot(int L, int ntiles) {
+    const int per = (ntiles + 7) / 8;
+    return (L % per) * 8 + L / per;
+}
 
 __device__ __forceinline__ void inst_decode(const QbP &p, int inst, int &bh, int &r, int &t) {
     t = inst % p.NS;
@@ -495,13 +506,12 @@ __device__ void qb_write_tiles(const QbP &p, int inst, int bh, int r, int t, int
         int at = carry + scan[threadIdx.x] - nt;
         if (nt > 0) {
             const int aq = p.off[(int64_t)inst * p.NB + u];
-            for (int k = 0; k < nt; ++k) {
-                int32_t *e = p.tiles + (int64_t)(at + k) * 4;
-                e[0] = inst;
-                e[1] = u;
-                e[2] = aq + k * TQ;
-                e[3] = min(TQ, c - k * TQ);
-            }
+            const int bst = p.bstart[krow * p.NB + u];
+            const int nva = min(p.bsize[krow * p.NB + u], p.C);
+            const int ntiles = p.ntiles[0];
+            for (int k = 0; k < nt; ++k)
+                reinterpret_cast<int4 *>(p.tiles)[rs_tile_slot(at + k, ntiles)] =
+                    make_int4(inst, aq + k * TQ, bst, min(TQ, c - k * TQ) | (nva << 8));
         }
         carry += scan[blockDim.x - 1];
         __syncthreads();
@@ -559,14 +569,19 @@ struct RsP {
     int64_t Call;
 };
 
-// Tile of this block: the dispatcher sends block i to XCD i % 8, so XCD x
-// takes the contiguous tile range [x * per, (x + 1) * per) in order and its L2
-// keeps the candidate rows those adjacent tiles share.  -1: no tile.
-__device__ __forceinline__ int rs_tile_of_block(int ntiles) {
-    const int per = (ntiles + 7) / 8;
-    const int x = (int)(blockIdx.x % 8), k = (int)(blockIdx.x / 8);
-    const int tile = x * per + k;
-    return (k < per && tile < ntiles) ? tile : -1;
+// This block's tile (slot blockIdx.x, see rs_tile_slot): instance, first
+// position in the instance's query list, the bucket's first sorted member,
+// query count and member count (the bucket size clamped to C).  False: the
+// slot holds no tile.
+struct RsTile { int inst, qb, st, qc, nva; };
+__device__ __forceinline__ bool rs_tile_fetch(const RsP &p, RsTile &t) {
+    const int slot = (int)blockIdx.x;
+    const int4 e = reinterpret_cast<const int4 *>(p.tiles)[slot];
+    const int ntiles = *p.ntiles;
+    const int per = (ntiles + 7) / 8, x = slot % 8, k = slot / 8;
+    if (k >= per || x * per + k >= ntiles) return false;
+    t.inst = e.x; t.qb = e.y; t.st = e.z; t.qc = e.w & 0xff; t.nva = e.w >> 8;
+    return true;
 }
 
 // Sorted members a tile needs: a causal query only uses members below its own
@@ -595,15 +610,13 @@ __global__ void __launch_bounds__(256) rescore_kernel(RsP p) {
     float *Ks = Qs + TQ * LD;           // [TC][LD]
     int *nidx = (int *)(Ks + TC * LD);  // [TQ]
     int *kidx = nidx + TQ;              // [TC]
-    const int tile = rs_tile_of_block(*p.ntiles);
-    if (tile < 0) return;
-    const int32_t *e = p.tiles + (int64_t)tile * 4;
-    const int inst = e[0], u = e[1], qb = e[2], qc = e[3];
+    RsTile tl;
+    if (!rs_tile_fetch(p, tl)) return;
+    const int inst = tl.inst, qb = tl.qb, qc = tl.qc, st = tl.st;
     const int r = (inst / p.NS) % p.R, bhl = inst / (p.NS * p.R);
     const int bh = p.bh0 + bhl;
     const int b = bh / p.Hq, h = bh % p.Hq, g = h / p.rep;
     const int64_t prow = ((int64_t)b * p.Hkv + g) * p.R + r;
-    const int st = p.bstart[prow * p.NB + u];
     const int tid = threadIdx.x;
     const T *qbase = (const T *)p.q + b * p.qsb + h * p.qsh;
     const T *kbase = (const T *)p.k + b * p.ksb + g * p.ksh;
@@ -611,7 +624,7 @@ __global__ void __launch_bounds__(256) rescore_kernel(RsP p) {
 
     if (tid < TQ) nidx[tid] = tid < qc ? p.qlist[(int64_t)inst * p.N + qb + tid] : 0;
     __syncthreads();
-    const int nv = rs_tile_cutoff(sd, min(p.bsize[prow * p.NB + u], p.C), nidx, qc, p.causal);
+    const int nv = rs_tile_cutoff(sd, tl.nva, nidx, qc, p.causal);
     for (int x = tid; x < TQ * D; x += 256) {
         const int i = x / D, c = x % D;
         Qs[i * LD + c] = i < qc ? to_f32(qbase[(int64_t)nidx[i] * p.qsn + c]) : 0.f;
@@ -702,7 +715,8 @@ __device__ __forceinline__ int rs_stage_row(int m) {
 
 // two 16-bit score codes, a at the lower address
 __device__ __forceinline__ uint32_t code_pair(float a, float b, float sc) {
-    return score_code(a, sc) | (score_code(b, sc) << 16);
+    // both complements at once: 65535 - x is ~x in 16 bits
+    return ~(score_neg_code(a, sc) | (score_neg_code(b, sc) << 16));
 }
 
 template <typename T, int D>
@@ -713,16 +727,13 @@ __global__ void __launch_bounds__(256) rescore_mfma_kernel(RsP p) {
     constexpr int SEGS = D / 8;                // 16-byte segments per row
     __shared__ int nidx[TQ];
     extern __shared__ __align__(16) unsigned char rs_lds[];   // [2][64][RB]
-    const int tile = rs_tile_of_block(*p.ntiles);
-    if (tile < 0) return;
-    const int32_t *e = p.tiles + (int64_t)tile * 4;
-    const int inst = e[0], u = e[1], qb = e[2], qc = e[3];
+    RsTile tl;
+    if (!rs_tile_fetch(p, tl)) return;
+    const int inst = tl.inst, qb = tl.qb, qc = tl.qc, st = tl.st, nva = tl.nva;
     const int r = (inst / p.NS) % p.R, bhl = inst / (p.NS * p.R);
     const int bh = p.bh0 + bhl;
     const int b = bh / p.Hq, h = bh % p.Hq, g = h / p.rep;
     const int64_t prow = ((int64_t)b * p.Hkv + g) * p.R + r;
-    const int st = p.bstart[prow * p.NB + u];
-    const int nva = min(p.bsize[prow * p.NB + u], p.C);
     const int tid = threadIdx.x;
     const int wid = tid / SSA_WAVE;
     const int lane = lane_id();
@@ -730,7 +741,11 @@ __global__ void __launch_bounds__(256) rescore_mfma_kernel(RsP p) {
     const T *qbase = (const T *)p.q + b * p.qsb + h * p.qsh;
     const T *kbase = (const T *)p.k + b * p.ksb + g * p.ksh;
     const int32_t *pr = p.sid + prow * p.M + st;
+    // the tile's queries and candidate ids (the list's members, ascending)
+    // load together, before one barrier
+    int32_t *prl = reinterpret_cast<int32_t *>(rs_lds + 2 * (64 * RB));
     if (tid < TQ) nidx[tid] = tid < qc ? p.qlist[(int64_t)inst * p.N + qb + tid] : 0;
+    for (int c = tid; c < nva; c += 256) prl[c] = pr[c];
     __syncthreads();
 
     // this wave's 16 queries as the B operand (column li = query 16*wid + li)
@@ -742,7 +757,7 @@ __global__ void __launch_bounds__(256) rescore_mfma_kernel(RsP p) {
 #pragma unroll
         for (int s = 0; s < KS; ++s) {
             const int e0 = 32 * s + 8 * lg;
-            qf[s] = (qok && e0 < D) ? __builtin_bit_cast(V, *reinterpret_cast<const uint4 *>(src + e0))
+            qf[s] = (qok && (D % 32 == 0 || e0 < D)) ? __builtin_bit_cast(V, *reinterpret_cast<const uint4 *>(src + e0))
                                     : __builtin_bit_cast(V, make_uint4(0, 0, 0, 0));
         }
     }
@@ -750,12 +765,9 @@ __global__ void __launch_bounds__(256) rescore_mfma_kernel(RsP p) {
     // the query's code scale (written by the aux kernel)
     const float qsc = qok ? p.aux[((int64_t)bhl * p.N + nidx[qrow]) * p.NA + p.NA - 1] : 1.f;
 
-    // the tile's candidate ids; then, per 64-candidate slice j: the K rows of
-    // slice j + 1 are loaded into registers, slice j (in LDS) is scored, its
-    // score keys stored, and the loaded rows committed to the other LDS buffer
-    int32_t *prl = reinterpret_cast<int32_t *>(rs_lds + 2 * (64 * RB));
-    for (int c = tid; c < nva; c += 256) prl[c] = pr[c];
-    __syncthreads();
+    // per 64-candidate slice j: the K rows of slice j + 1 are loaded into
+    // registers, slice j (in LDS) is scored, its score codes stored, and the
+    // loaded rows committed to the other LDS buffer
     const int nv = rs_tile_cutoff(prl, nva, nidx, qc, p.causal);
     constexpr int PER = (64 * SEGS + 255) / 256;
     // rows are addressed by 32-bit byte offsets from the head's base (the
@@ -768,7 +780,9 @@ __global__ void __launch_bounds__(256) rescore_mfma_kernel(RsP p) {
     _Pragma("unroll") for (int i = 0; i < PER; ++i) {                                        \
         const int x = tid + 256 * i;                                                         \
         const int row = x / SEGS, seg = x % SEGS;                                            \
-        const int id = (x < 64 * SEGS && (C0) + row < nv) ? prl[(C0) + row] : 0;            \
+        const int cr = (C0) + row;  /* the read is clamped in range; the select drops it */ \
+        const int rid = prl[max(min(cr, nv - 1), 0)];                                        \
+        const int id = (x < 64 * SEGS && cr < nv) ? rid : 0;                                 \
         sa[i] = *reinterpret_cast<const u32x4 *>((const char *)kbase +                       \
                                                  (__umul24((uint32_t)id, rowb) + seg * 16u)); \
     }
@@ -816,7 +830,7 @@ __global__ void __launch_bounds__(256) rescore_mfma_kernel(RsP p) {
                 const int e0 = 32 * s + 8 * lg;
 #pragma unroll
                 for (int ct = 0; ct < 4; ++ct)
-                    kf[ct] = e0 < D ? __builtin_bit_cast(
+                    kf[ct] = (D % 32 == 0 || e0 < D) ? __builtin_bit_cast(
                                           V, *reinterpret_cast<const uint4 *>(
                                                  kl + (ct * 16 + li) * RB + e0 * 2))
                                     : __builtin_bit_cast(V, make_uint4(0, 0, 0, 0));
@@ -1103,7 +1117,7 @@ __global__ void __launch_bounds__(256) aux_mfma_kernel(AuxP p) {
     const T *kbase = (const T *)p.k + b * p.ksb + g * p.ksh;
     auto frag = [&](const T *src, bool ok, int s) {
         const int e0 = 32 * s + 8 * lg;
-        if (ok && e0 < D) return __builtin_bit_cast(V, *reinterpret_cast<const uint4 *>(src + e0));
+        if (ok && (D % 32 == 0 || e0 < D)) return __builtin_bit_cast(V, *reinterpret_cast<const uint4 *>(src + e0));
         return __builtin_bit_cast(V, make_uint4(0, 0, 0, 0));
     };
     const int nq = n0 + li;
@@ -2499,7 +2513,8 @@ Layout plan(const Dims &D) {
     L.off = take(ninst * D.NB * 4);
     L.cur = take(ninst * ceil_div(D.N, 256) * D.NB * 4);   // per-block counts / bases
     L.qlist = take(ninst * D.N * 4);
-    L.tiles = take(ninst * (ceil_div(D.N, TQ) + D.NB) * 16);
+    // one 16-byte slot per block of the rescore grid (a multiple of 8)
+    L.tiles = take(8 * ceil_div(ninst * (ceil_div(D.N, TQ) + D.NB), 8) * 16);
     L.ntiles = take(4);
     L.tcnt = take(ninst * 4);
     L.kbase = take((nbh / D.rep + 2) * D.R * D.NS * D.rep * 4);
@@ -2890,6 +2905,7 @@ int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char 
         QbP qp{};
         qp.qid = (const uint16_t *)(ws + L.qid);
         qp.bsize = (const int32_t *)(ws + L.bsize);
+        qp.bstart = (const int32_t *)(ws + L.bstart);
         qp.cnt = (int32_t *)(ws + L.cnt);
         qp.off = (int32_t *)(ws + L.off);
         qp.cur = nullptr;
@@ -2901,7 +2917,7 @@ int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char 
         qp.tcnt = (int32_t *)(ws + L.tcnt);
         qp.kbase = (int32_t *)(ws + L.kbase);
         qp.N = D.N; qp.R = D.R; qp.NS = D.NS; qp.NB = D.NB; qp.Hq = D.Hq; qp.Hkv = D.Hkv;
-        qp.rep = D.rep; qp.bh0 = (int)bh0; qp.ninst = ninst;
+        qp.rep = D.rep; qp.bh0 = (int)bh0; qp.ninst = ninst; qp.C = D.C;
         const dim3 gq((unsigned)ceil_div(D.N, 256), (unsigned)ninst);
         hipLaunchKernelGGL(qb_hist_kernel, gq, dim3(256), (size_t)D.NB * 4, st, qp);
         SSA_CHECK_LAUNCH();
