@@ -439,15 +439,17 @@ __global__ void __launch_bounds__(256) qb_scan_kernel(QbP p) {
     }
 }
 
-// Position of an instance in the tile list: ordered by (kv head, round, id
-// set, query head within the GQA group), so the tiles that read one round's
-// candidate rows of one kv head are adjacent.
+// Position of an instance in the tile list: ordered by (kv head, query head
+// within the GQA group, round, id set).  An XCD takes a contiguous range of
+// tiles, so it works through one query head's rounds back to back while that
+// head's q rows (N * d elements) and the kv head's K rows stay in its L2; with
+// the rounds outside the query heads, every round re-read the group's q rows.
 __device__ __forceinline__ int64_t qb_order_key(const QbP &p, int inst, int64_t bk_first) {
     int bh, r, t;
     inst_decode(p, inst, bh, r, t);
     const int b = bh / p.Hq, h = bh % p.Hq;
     const int64_t bk = (int64_t)b * p.Hkv + h / p.rep - bk_first;
-    return ((bk * p.R + r) * p.NS + t) * p.rep + h % p.rep;
+    return ((bk * p.rep + h % p.rep) * p.R + r) * p.NS + t;
 }
 
 // one block: the first tile of each instance in that order (kbase), and the
