@@ -195,6 +195,18 @@ typedef struct {
 
 int ssa_sparse_gather_attention_bwd(const ssa_apply_bwd_args *a, void *stream);
 
+/* ---------------------------------------------------------------------------
+ * Measurement helper (no counterpart in the reference): the L2-to-CU delivery
+ * rate that bounds the gather attention, whose repeated K/V rows are served by
+ * the L2 rather than HBM.  `blocks` workgroups of 256 threads each stream the
+ * `bytes` of `buf` (a power of two, 32 KiB .. 2 GiB; small enough to stay in
+ * the L2, larger than a CU's L1) `iters` times with 16-byte loads.  Bytes
+ * delivered = blocks * bytes * iters.  `sink` holds `blocks` uint32 (written
+ * only in a case the kernel never meets).
+ * --------------------------------------------------------------------------- */
+int ssa_measure_l2_read(const void *buf, int64_t bytes, int32_t blocks, int32_t iters,
+                        uint32_t *sink, void *stream);
+
 /* Library identification and error text. */
 const char *ssa_version(void);
 const char *ssa_last_error(void);

@@ -174,7 +174,8 @@ def apply(q, k, v, nb, scale, valid, fp32w=False):
     return torch.einsum("bhnk,bhnkd->bhnd", p.to(vg.dtype), vg)
 
 
-def forward(x, Wq, Wk, Wv, Wo, rand_proj, *, H, n_kv, K, window, glob_n, R, max_p, T, causal):
+def forward(x, Wq, Wk, Wv, Wo, rand_proj, *, H, n_kv, K, window, glob_n, R, max_p, T, causal,
+            fp32w=False):
     """SparseAttention.forward (:1420-1491) for self-attention with default
     (first-G) global tokens.  Weights are (out, in) like nn.Linear."""
     B, N, _ = x.shape
@@ -198,5 +199,5 @@ def forward(x, Wq, Wk, Wv, Wo, rand_proj, *, H, n_kv, K, window, glob_n, R, max_
     lsh = lsh_forward(q, k, rand_proj, lsh_k, causal, glob, 4 * lsh_k, R, max_p, T)
     self_idx = pos.view(1, 1, N).expand(B, H, N)
     nb, valid = merge(win, glob, lsh, self_idx, K, N, B, H)
-    out = apply(q, k, v, nb, d ** -0.5, valid)
+    out = apply(q, k, v, nb, d ** -0.5, valid, fp32w)
     return out.transpose(1, 2).contiguous().view(B, N, H * d) @ Wo.T

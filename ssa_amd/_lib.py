@@ -95,6 +95,8 @@ def lib():
                                           c_i32, c_i32, c_vp, c_vp, c_vp, c_vp]
         L.ssa_sparse_gather_attention.restype = ctypes.c_int
         L.ssa_sparse_gather_attention.argtypes = [ctypes.POINTER(ApplyArgs), c_vp]
+        L.ssa_measure_l2_read.restype = ctypes.c_int
+        L.ssa_measure_l2_read.argtypes = [c_vp, c_i64, c_i32, c_i32, c_vp, c_vp]
         L.ssa_sparse_gather_attention_bwd.restype = ctypes.c_int
         L.ssa_sparse_gather_attention_bwd.argtypes = [ctypes.POINTER(ApplyBwdArgs), c_vp]
         _lib = L
@@ -151,11 +153,27 @@ def build_graph(q, k, rand_proj, *, P, T, C, top_k, window, causal, is_cross, to
 
     Returns (out_idx, out_valid or None, ties or None).  With ids32 (FULL mode)
     out_idx is int32 with -1 in the invalid slots and out_valid is None."""
-    require_device(q, k, rand_proj, glob)
+    if q.dim() != 4 or k.dim() != 4:
+        raise RuntimeError(f"ssa_amd.build_graph: q {tuple(q.shape)} and k {tuple(k.shape)} must "
+                           "be 4-D")
     B, Hq, N, d = q.shape
     Bk, Hkv, M, dk = k.shape
     if Bk != B or dk != d:
         raise RuntimeError(f"ssa_amd.build_graph: q {tuple(q.shape)} / k {tuple(k.shape)} mismatch")
+    if Hkv < 1 or Hq % Hkv != 0:
+        raise RuntimeError(f"ssa_amd.build_graph: {Hq} query heads are not a multiple of {Hkv} "
+                           "kv heads")
+    if rand_proj.dim() != 3 or rand_proj.shape[2] != d or not 1 <= P <= rand_proj.shape[1]:
+        raise RuntimeError(f"ssa_amd.build_graph: hyperplanes {tuple(rand_proj.shape)} do not "
+                           f"fit head dim {d} and {P} planes")
+    R = rand_proj.shape[0]
+    if q_proj is not None and tuple(q_proj.shape) != (B * Hq, R, N, P):
+        raise RuntimeError(f"ssa_amd.build_graph: q_proj {tuple(q_proj.shape)} is not "
+                           f"{(B * Hq, R, N, P)}")
+    if k_proj is not None and tuple(k_proj.shape) != (B * Hkv, R, M, P):
+        raise RuntimeError(f"ssa_amd.build_graph: k_proj {tuple(k_proj.shape)} is not "
+                           f"{(B * Hkv, R, M, P)}")
+    require_device(q, k, rand_proj, glob)
     if q.dtype != k.dtype:
         raise RuntimeError("ssa_amd.build_graph: q and k dtypes differ")
     qa, qk = view4(q)
@@ -187,13 +205,14 @@ def build_graph(q, k, rand_proj, *, P, T, C, top_k, window, causal, is_cross, to
     valid = (torch.empty((B, Hq, N, width), dtype=torch.bool, device=q.device)
              if mode == GRAPH_FULL and not compact else None)
     ties = torch.zeros(1, dtype=torch.int32, device=q.device) if count_ties else None
-    ws = torch.empty(max(int(wsb), 1), dtype=torch.uint8, device=q.device)
     if compact:
         a.out_idx32 = out.data_ptr()
     else:
         a.out_idx, a.out_valid = out.data_ptr(), _ptr(valid)
     a.out_ties = _ptr(ties)
-    _check(L.ssa_build_graph(ctypes.byref(a), ws.data_ptr(), int(wsb), _stream(q)), "build_graph")
+    ws = torch.empty(max(int(wsb), 1), dtype=torch.uint8, device=q.device)
+    _check(L.ssa_build_graph(ctypes.byref(a), ws.data_ptr(), int(wsb), _stream(q)),
+           "build_graph")
     # keep inputs alive until the stream has consumed them
     _keep = (qk, kk_, rp, g, qp, kp, ws)
     del _keep
@@ -306,9 +325,49 @@ def merge_neighbors(win, glob, lsh, has_self: bool, total_k: int):
 
 
 # --------------------------------------------------------------------------- apply
+def check_apply_shapes(q, k, v, neighbors, valid, out=None):
+    """Raise RuntimeError unless the operands of the gather attention agree:
+    q (B, Hq, N, d); k and v (B, Hkv, M, d) with Hq % Hkv == 0; neighbors
+    (B, Hq, N, K); valid None or neighbors' shape; out (B, Hq, N, d).  The
+    kernels index every row of these shapes, so a mismatch (a cached graph of
+    another size, a broadcast (N, K) graph, a short v) is refused here, before
+    any launch, where the reference's reshape would raise
+    (sparse_attention.py:1137-1142)."""
+    for name, t in (("q", q), ("k", k), ("v", v), ("neighbors", neighbors)):
+        if t.dim() != 4:
+            raise RuntimeError(f"ssa_amd.sparse_gather_attention: {name} must be 4-D, got "
+                               f"shape {tuple(t.shape)}")
+    B, Hq, N, d = q.shape
+    Bk, Hkv, M, dk = k.shape
+    if tuple(v.shape) != tuple(k.shape):
+        raise RuntimeError(f"ssa_amd.sparse_gather_attention: v {tuple(v.shape)} and k "
+                           f"{tuple(k.shape)} differ")
+    if Bk != B or dk != d:
+        raise RuntimeError(f"ssa_amd.sparse_gather_attention: k {tuple(k.shape)} does not match "
+                           f"q {tuple(q.shape)} in batch or head dim")
+    if Hkv < 1 or Hq % Hkv != 0:
+        raise RuntimeError(f"ssa_amd.sparse_gather_attention: {Hq} query heads are not a "
+                           f"multiple of {Hkv} kv heads")
+    if M < 1:
+        raise RuntimeError("ssa_amd.sparse_gather_attention: k has no keys")
+    if tuple(neighbors.shape[:3]) != (B, Hq, N):
+        raise RuntimeError(f"ssa_amd.sparse_gather_attention: neighbors {tuple(neighbors.shape)} "
+                           f"do not match q {tuple(q.shape)} in (B, H, N)")
+    if valid is not None and tuple(valid.shape) != tuple(neighbors.shape):
+        raise RuntimeError(f"ssa_amd.sparse_gather_attention: valid {tuple(valid.shape)} and "
+                           f"neighbors {tuple(neighbors.shape)} differ")
+    if neighbors.dtype not in (torch.int64, torch.int32):
+        raise RuntimeError(f"ssa_amd.sparse_gather_attention: neighbors dtype {neighbors.dtype} "
+                           "(int64 or int32)")
+    if out is not None and tuple(out.shape) != (B, Hq, N, d):
+        raise RuntimeError(f"ssa_amd.sparse_gather_attention: out {tuple(out.shape)} does not "
+                           f"match q {tuple(q.shape)}")
+
+
 def _apply_args(q, k, v, neighbors, valid, scale, fp32w, dropout_p, seed, out, ids32=True):
     """int32 neighbours without a mask are passed as they are (a negative id
     is an invalid slot, as the int64 path treats it) when ids32 allows."""
+    check_apply_shapes(q, k, v, neighbors, valid, out)
     B, Hq, N, d = q.shape
     _, Hkv, M, _ = k.shape
     K = neighbors.shape[-1]
@@ -333,6 +392,7 @@ def _apply_args(q, k, v, neighbors, valid, scale, fp32w, dropout_p, seed, out, i
 
 def gather_attention_fwd(q, k, v, neighbors, valid, scale, fp32w=False, dropout_p=0.0, seed=0,
                          out=None):
+    check_apply_shapes(q, k, v, neighbors, valid, out)
     require_device(q, k, v, neighbors, valid)
     if not (q.dtype == k.dtype == v.dtype):
         raise RuntimeError("ssa_amd.sparse_gather_attention: q, k, v dtypes differ")
@@ -347,6 +407,8 @@ def gather_attention_fwd(q, k, v, neighbors, valid, scale, fp32w=False, dropout_
 
 
 def gather_attention_bwd(q, k, v, neighbors, valid, scale, fp32w, dropout_p, seed, dout):
+    check_apply_shapes(q, k, v, neighbors, valid, dout)
+    require_device(q, k, v, neighbors, valid, dout)
     B, Hq, N, d = q.shape
     _, Hkv, M, _ = k.shape
     do = dout.to(torch.float32).contiguous()
@@ -363,3 +425,14 @@ def gather_attention_bwd(q, k, v, neighbors, valid, scale, fp32w, dropout_p, see
            "sparse_gather_attention_bwd")
     del keep
     return dq, dk, dv
+
+
+# --------------------------------------------------------------------------- measurement
+def measure_l2_read(buf: torch.Tensor, blocks: int, iters: int, sink: torch.Tensor):
+    """Launch ssa_measure_l2_read over `buf` (uint8, power-of-two size) on the
+    current stream: blocks * buf.numel() * iters bytes delivered from the L2."""
+    require_device(buf, sink)
+    if sink.numel() * sink.element_size() < 4 * blocks:
+        raise RuntimeError("ssa_amd.measure_l2_read: sink holds fewer than `blocks` uint32")
+    _check(lib().ssa_measure_l2_read(buf.data_ptr(), buf.numel() * buf.element_size(), blocks,
+                                     iters, sink.data_ptr(), _stream(buf)), "measure_l2_read")

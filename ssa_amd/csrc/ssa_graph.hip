@@ -819,8 +819,10 @@ __global__ void __launch_bounds__(256) rescore_mfma_kernel(RsP p) {
         cq = lo;
     }
     const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(p.S + (int64_t)inst * p.N * p.Cs), (short)0, p.N * p.Cs * 2, SSA_BUF_FLAGS);
-    const uint32_t sbase = (uint32_t)((qb + qrow) * p.Cs + 8 * lg) * 2u;
+        (void *)(p.S + (int64_t)inst * p.N * p.Cs), (short)0, (int)((int64_t)p.N * p.Cs * 2),
+        SSA_BUF_FLAGS);
+    // make_dims keeps an instance's rows (N * Cs * 2 bytes) below 2^31
+    const uint32_t sbase = ((uint32_t)(qb + qrow) * (uint32_t)p.Cs + 8u * lg) * 2u;
     for (int j = 0; j < nsl; ++j) {
         const int c0 = 64 * j;
         const bool more = j + 1 < nsl;
@@ -2332,13 +2334,19 @@ __device__ void rp_sort(const RpArr &a, uint16_t *TL, uint16_t *TR, uint32_t *lb
     rp_sync();
 }
 
-template <typename T, bool LSH_MODE>
+// GLB: the per-wave arrays live in a device buffer (`gscr`, rp_lds_words(W)
+// words per resident wave) instead of LDS, for rows whose kk + chunk slots do
+// not fit; the same code runs on either (all accesses of a wave's arrays come
+// from that wave, whose stores its own later loads see after rp_sync).
+template <typename T, bool LSH_MODE, bool GLB>
 __global__ void __launch_bounds__(RP_WAVES * SSA_WAVE)
-topk_replay_kernel(SelP p, int chunk, int W) {
+topk_replay_kernel(SelP p, int chunk, int W, uint32_t *gscr) {
     extern __shared__ uint32_t rp_smem[];
     const int wid = threadIdx.x / SSA_WAVE;
     const int lane = lane_id();
-    uint32_t *base = rp_smem + (int64_t)wid * rp_lds_words(W, p.words);
+    const int64_t wave_words = rp_lds_words(W, p.words);
+    uint32_t *base = GLB ? gscr + ((int64_t)blockIdx.x * RP_WAVES + wid) * wave_words
+                         : rp_smem + (int64_t)wid * wave_words;
     RpArr A;
     A.key = base;
     A.cand = (int32_t *)(base + W);
@@ -2483,11 +2491,23 @@ topk_replay_kernel(SelP p, int chunk, int W) {
 // ------------------------------------------------------------------ host side
 int supported_d(int d) { return d >= 4 && d <= 256 && (d & (d - 1)) == 0; }
 
+// Whether RP_WAVES replayed rows of W = kk + chunk slots fit one workgroup's LDS.
+bool replay_fits_lds(int W, int words) {
+    return (int64_t)RP_WAVES * rp_lds_words(W, words) * 4 <= SSA_LDS_BYTES;
+}
+
+// Blocks of the replay whose per-wave arrays live in the workspace: as many as
+// keep that region near 64 MiB (at least one, at most 256).
+int64_t replay_glb_blocks(int W, int words) {
+    const int64_t per_block = (int64_t)RP_WAVES * rp_lds_words(W, words) * 4;
+    return std::max<int64_t>(1, std::min<int64_t>(256, ((int64_t)64 << 20) / per_block));
+}
+
 struct Layout {
     int64_t kid, qid, perm, bstart, bsize, sorttmp, sid, rnk, smin, inv, cut, srix, qpos, cnt, off,
         cur,
         qlist, tiles, ntiles, tcnt, kbase, S,
-        tie_list, tie_count, aux, knorm, kpart, total;
+        tie_list, tie_count, aux, knorm, kpart, rpscr, total;
 };
 
 int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
@@ -2526,11 +2546,24 @@ Layout plan(const Dims &D) {
     L.aux = take(nbh * D.N * (D.G + 3) * 4);
     L.knorm = take(D.BK * 4);
     L.kpart = take(D.BK * (D.M / 16) * 4);
+    {
+        // the replay's per-wave arrays, when they do not fit LDS
+        const int W = D.kk + D.chunk;
+        const int words = ((D.M + 31) / 32 + 2) & ~1;
+        L.rpscr = take(replay_fits_lds(W, words)
+                           ? 0
+                           : replay_glb_blocks(W, words) * RP_WAVES * rp_lds_words(W, words) * 4);
+    }
     L.total = o;
     return L;
 }
 
-int make_dims(const ssa_graph_args *a, Dims &D, bool need_q = true) {
+Layout plan(const Dims &D);
+
+// ws_cap > 0: query heads go in chunks small enough that the workspace stays
+// within ws_cap bytes (the build without allocation runs in a fixed scratch
+// array); SSA_E_WORKSPACE when even one head per chunk needs more.
+int make_dims(const ssa_graph_args *a, Dims &D, bool need_q = true, int64_t ws_cap = 0) {
     SSA_CHECK_ARG(a != nullptr, "build_graph: null args");
     SSA_CHECK_ARG(a->mode == SSA_GRAPH_FULL || a->mode == SSA_GRAPH_LSH, "build_graph: bad mode");
     SSA_CHECK_ARG(a->B >= 1 && a->Hq >= 1 && a->Hkv >= 1 && a->N >= 1 && a->M >= 1,
@@ -2590,6 +2623,12 @@ int make_dims(const ssa_graph_args *a, Dims &D, bool need_q = true) {
         D.Kout = D.kk;
     }
     SSA_CHECK_ARG(!a->causal || a->N <= a->M, "build_graph: causal needs N <= M");
+    if (D.kk + D.chunk > 65535) {
+        // the replay of tied rows indexes best ++ chunk with 16-bit positions
+        ssa_set_error("build_graph: LSH top-k %d with stream chunks of %d slots exceeds the "
+                      "65535 slots the exact tie replay supports", D.kk, D.chunk);
+        return SSA_E_UNSUP;
+    }
     // chunk the query heads so the score buffer stays near 2 GiB
     const int64_t per_bh = (int64_t)a->N * D.nlists * D.Cs * 2;
     if (per_bh >= ((int64_t)4 << 30)) {
@@ -2597,10 +2636,35 @@ int make_dims(const ssa_graph_args *a, Dims &D, bool need_q = true) {
                       "must stay below 4 GiB", (long long)per_bh);
         return SSA_E_UNSUP;
     }
+    if ((int64_t)a->N * D.Cs * 2 >= ((int64_t)1 << 31)) {
+        // the rescore addresses one (head, round, id set) instance's score rows
+        // through 32-bit buffer offsets
+        ssa_set_error("build_graph: one instance's score rows (N * C * 2 = %lld bytes) must stay "
+                      "below 2 GiB", (long long)a->N * D.Cs * 2);
+        return SSA_E_UNSUP;
+    }
     int64_t nbh = ((int64_t)2 << 30) / per_bh;
     if (nbh < 1) nbh = 1;
     if (nbh > D.BH) nbh = D.BH;
     D.nbh_chunk = (int)nbh;
+    if (ws_cap > 0 && plan(D).total > ws_cap) {
+        // the workspace grows with the chunk's head count: the largest count
+        // in [1, nbh) that fits, by bisection
+        int lo = 1, hi = D.nbh_chunk - 1;
+        while (lo < hi) {
+            D.nbh_chunk = (lo + hi + 1) / 2;
+            if (plan(D).total <= ws_cap) lo = D.nbh_chunk;
+            else hi = D.nbh_chunk - 1;
+        }
+        D.nbh_chunk = lo;
+        const int64_t need = plan(D).total;
+        if (need > ws_cap) {
+            ssa_set_error("build_graph: this problem needs %lld bytes of workspace with one query "
+                          "head per chunk; the scratch array holds %lld",
+                          (long long)need, (long long)ws_cap);
+            return SSA_E_WORKSPACE;
+        }
+    }
     return SSA_OK;
 }
 
@@ -2797,19 +2861,26 @@ int aux_dispatch(int d, bool mfma, const AuxP &ap, hipStream_t st) {
     return SSA_OK;
 }
 
-// Exact top-k replay of the rows select flagged.  Rows whose replay does not
-// fit LDS (kk + chunk above ~12k slots) keep the select kernel's rule.
+// Exact top-k replay of the rows select flagged.  A replayed row needs
+// rp_lds_words(kk + chunk) words; when RP_WAVES of them fit LDS the arrays live
+// there, else in the workspace region `rpscr` (replay_glb_blocks blocks).
 template <typename T, bool LSH>
-int launch_replay(const SelP &sp, int chunk, hipStream_t st) {
+int launch_replay(const SelP &sp, int chunk, uint32_t *rpscr, hipStream_t st) {
     const int W = sp.kk + chunk;
+    if (!replay_fits_lds(W, sp.words)) {
+        const int64_t blocks = replay_glb_blocks(W, sp.words);
+        hipLaunchKernelGGL((topk_replay_kernel<T, LSH, true>), dim3((unsigned)blocks),
+                           dim3(RP_WAVES * SSA_WAVE), 0, st, sp, chunk, W, rpscr);
+        SSA_CHECK_LAUNCH();
+        return SSA_OK;
+    }
     const size_t lds = (size_t)RP_WAVES * rp_lds_words(W, sp.words) * 4;
-    if (lds > SSA_LDS_BYTES || W > 65535) return SSA_OK;
-    SSA_CHECK_HIP(hipFuncSetAttribute((const void *)topk_replay_kernel<T, LSH>,
+    SSA_CHECK_HIP(hipFuncSetAttribute((const void *)topk_replay_kernel<T, LSH, false>,
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     // enough blocks for every resident wave to take a row (the rest exit at once)
     const int64_t blocks = std::min<int64_t>(ceil_div(sp.rows, RP_WAVES), 8192);
-    hipLaunchKernelGGL((topk_replay_kernel<T, LSH>), dim3((unsigned)blocks),
-                       dim3(RP_WAVES * SSA_WAVE), lds, st, sp, chunk, W);
+    hipLaunchKernelGGL((topk_replay_kernel<T, LSH, false>), dim3((unsigned)blocks),
+                       dim3(RP_WAVES * SSA_WAVE), lds, st, sp, chunk, W, (uint32_t *)nullptr);
     SSA_CHECK_LAUNCH();
     return SSA_OK;
 }
@@ -3023,8 +3094,9 @@ int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char 
     SelP rp = last;
     rp.bh0 = 0;
     rp.rows = D.BH * D.N;
-    return rp.mode == SSA_GRAPH_LSH ? launch_replay<T, true>(rp, D.chunk, st)
-                                    : launch_replay<T, false>(rp, D.chunk, st);
+    uint32_t *rpscr = (uint32_t *)(ws + L.rpscr);
+    return rp.mode == SSA_GRAPH_LSH ? launch_replay<T, true>(rp, D.chunk, rpscr, st)
+                                    : launch_replay<T, false>(rp, D.chunk, rpscr, st);
 }
 
 }  // namespace
@@ -3043,11 +3115,11 @@ extern "C" int64_t ssa_graph_workspace_bytes(const ssa_graph_args *a) {
 
 namespace {
 int build_phase(const ssa_graph_args *a, void *workspace, int64_t workspace_bytes, void *stream,
-                int phases) {
+                int phases, int64_t ws_cap = 0) {
     SSA_CHECK_ARG(phases > 0 && phases <= SSA_PHASE_ALL, "build_graph: phases %d", phases);
     Dims D;
     const bool qphase = (phases & SSA_PHASE_QUERIES) != 0;
-    int rc = make_dims(a, D, qphase);
+    int rc = make_dims(a, D, qphase, ws_cap);
     if (rc) return rc;
     if (qphase) {
         const bool i32 = a->mode == SSA_GRAPH_FULL && a->out_idx32;
@@ -3087,4 +3159,16 @@ extern "C" int ssa_build_graph(const ssa_graph_args *a, void *workspace, int64_t
 extern "C" int ssa_build_graph_phases(const ssa_graph_args *a, void *workspace,
                                       int64_t workspace_bytes, void *stream, int phases) {
     return build_phase(a, workspace, workspace_bytes, stream, phases);
+}
+
+int64_t ssa_graph_workspace_bytes_capped(const ssa_graph_args *a, int64_t ws_cap) {
+    Dims D;
+    const int rc = make_dims(a, D, false, ws_cap);
+    if (rc) return rc;
+    return plan(D).total;
+}
+
+int ssa_build_graph_capped(const ssa_graph_args *a, void *workspace, int64_t ws_cap,
+                           void *stream) {
+    return build_phase(a, workspace, ws_cap, stream, SSA_PHASE_ALL, ws_cap);
 }

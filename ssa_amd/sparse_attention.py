@@ -244,6 +244,7 @@ def sparse_gather_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     """Attention of each query over its K gathered neighbours
     (sparse_attention.py:1096-1199).  ``k``/``v`` may be (B, H, M, d) or the
     un-expanded (B, n_kv, M, d)."""
+    _lib.check_apply_shapes(q, k, v, neighbors, valid)
     _lib.require_device(q, k, v, neighbors, valid)
     p = float(dropout) if (training and dropout > 0.0) else 0.0
     seed = int(torch.randint(0, 2 ** 62, (1,)).item()) if p > 0.0 else 0

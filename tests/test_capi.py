@@ -5,6 +5,7 @@ import os
 import re
 
 import pytest
+import torch
 
 from conftest import ROOT
 
@@ -81,3 +82,109 @@ def test_argument_errors_are_reported_without_a_gpu():
     assert rc == -1
     assert b"mode" in _lib.lib().ssa_last_error()
     assert _lib.lib().ssa_graph_out_width(ctypes.byref(a)) == -1
+
+
+# ---------------------------------------------------------------------------- exact replay
+# Words of one replayed row's arrays (rank keys, key ids, two 16-bit stopper
+# lists, leaf bits, the partition stack, the seen bitmap, glob scores); two
+# rows share a workgroup's 160 KiB of LDS (minus 512 bytes of static data).
+def _replay_words(W, M):
+    words = ((M + 31) // 32 + 2) & ~1
+    return (3 * W + (W + 31) // 32 + 1 + 3 * 64 + words + 64 + 1) & ~1
+
+
+def _replay_fits(W, M):
+    return 2 * _replay_words(W, M) * 4 <= 160 * 1024 - 512
+
+
+def _full_args(N, K, w=4, G=2, R=2, d=16):
+    from ssa_amd import _lib
+    lsh_k = max(K - (2 * w + 1 + G + 1), 8)
+    a = _lib.GraphArgs()
+    a.mode = _lib.GRAPH_FULL
+    a.B, a.Hq, a.Hkv, a.N, a.M, a.d = 1, 1, 1, N, N, d
+    a.q = _lib.Tensor4(1, _lib.SSA_F32, N * d, N * d, d)   # never dereferenced here
+    a.k = _lib.Tensor4(1, _lib.SSA_F32, N * d, N * d, d)
+    a.rand_proj = 1
+    a.R, a.max_p, a.P, a.T, a.C, a.top_k = R, 12, 1, 0, 4 * lsh_k, lsh_k
+    a.window, a.causal, a.is_cross, a.total_k = w, 1, 0, K
+    a.glob, a.G = 1, G
+    return a, lsh_k
+
+
+def test_replay_beyond_lds_takes_a_workspace_region():
+    """Tied rows are always replayed: when two replayed rows of kk + chunk
+    slots no longer fit a workgroup's LDS, the workspace grows by a region for
+    the replay's per-wave arrays (a jump at exactly that kk)."""
+    from ssa_amd import _lib
+    L = _lib.lib()
+    N = 2048
+    prev = None
+    crossed = 0
+    for K in range(1200, 1500, 4):
+        a, kk = _full_args(N, K)
+        Call = 2 * 4 * kk
+        chunk = min(Call, max(256, 4 * kk))
+        W = min(kk, Call) + chunk
+        wsb = L.ssa_graph_workspace_bytes(ctypes.byref(a))
+        assert wsb > 0, _lib.lib().ssa_last_error()
+        fits = _replay_fits(W, N)
+        if prev is not None and prev[1] and not fits:
+            crossed += 1
+            blocks = max(1, min(256, (64 << 20) // (2 * _replay_words(W, N) * 4)))
+            region = blocks * 2 * _replay_words(W, N) * 4
+            # everything else grows by a few KB per step of K
+            assert wsb - prev[0] >= region
+        prev = (wsb, fits)
+    assert crossed == 1
+
+
+def test_replay_limit_is_an_error_not_a_silent_skip():
+    """kk + chunk above 65535 slots is refused (the replay's 16-bit positions)."""
+    from ssa_amd import _lib
+    a, kk = _full_args(32768, 14000)
+    assert _lib.lib().ssa_graph_workspace_bytes(ctypes.byref(a)) < 0
+    assert b"tie replay" in _lib.lib().ssa_last_error()
+
+
+# ---------------------------------------------------------------------------- apply shapes
+def _apply_operands(B=1, Hq=4, Hkv=2, N=8, M=8, d=16, K=5):
+    q = torch.zeros(B, Hq, N, d)
+    k = torch.zeros(B, Hkv, M, d)
+    v = torch.zeros(B, Hkv, M, d)
+    nb = torch.zeros(B, Hq, N, K, dtype=torch.long)
+    va = torch.ones(B, Hq, N, K, dtype=torch.bool)
+    return q, k, v, nb, va
+
+
+@pytest.mark.parametrize("bad", ["broadcast_graph", "graph_rows", "short_v", "valid_shape",
+                                 "head_dim", "batch", "heads"])
+def test_apply_shape_mismatch_raises_before_any_launch(bad):
+    """The gather attention refuses operands whose shapes disagree (a cached
+    graph of another size, a broadcast (N, K) graph, a short v) on the host,
+    before the device check and before any launch."""
+    from ssa_amd import sparse_gather_attention
+    q, k, v, nb, va = _apply_operands()
+    if bad == "broadcast_graph":
+        nb, va = nb[0, 0], va[0, 0]
+    elif bad == "graph_rows":
+        nb, va = nb[:, :, :6], va[:, :, :6]
+    elif bad == "short_v":
+        v = v[:, :, :5]
+    elif bad == "valid_shape":
+        va = va[..., :4]
+    elif bad == "head_dim":
+        k, v = k[..., :8], v[..., :8]
+    elif bad == "batch":
+        k, v = torch.cat([k, k]), torch.cat([v, v])
+    elif bad == "heads":
+        k, v = torch.zeros(1, 3, 8, 16), torch.zeros(1, 3, 8, 16)
+    with pytest.raises(RuntimeError, match="sparse_gather_attention"):
+        sparse_gather_attention(q, k, v, nb, 0.25, valid=va)
+
+
+def test_apply_matching_shapes_reach_the_device_check():
+    from ssa_amd import sparse_gather_attention
+    q, k, v, nb, va = _apply_operands()
+    with pytest.raises(RuntimeError, match="ROCm devices only"):
+        sparse_gather_attention(q, k, v, nb, 0.25, valid=va)

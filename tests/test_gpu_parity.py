@@ -145,6 +145,28 @@ def test_lsh_builder_exact_tier_matches_oracle(case):
     np.testing.assert_array_equal(g, r)
 
 
+# num_neighbors 1400: kk = 1388, so best ++ chunk spans 6,940 slots and two
+# replayed rows no longer fit a workgroup's LDS; small integers tie at the
+# kk-th score on many rows, so the replay runs from its workspace region
+HUGE_K = ("huge_k_replay_workspace", 1, 1, 1, 2048, 2048, 16, 2, 3, 0, 1400, 4, 2, True, False)
+
+
+def test_full_graph_exact_tier_huge_k_replay_outside_lds():
+    attn, got, got_v, ref, (B, H, N, M, K, w, cross, causal, glob) = _graph_case(HUGE_K, 0)
+    print(f"  huge K: {ref['n_ties']} rows with a tied kk-th score", flush=True)
+    assert ref["n_ties"] > 0
+    win = attn.win_builder(N, M, "cpu").numpy()
+    rnb, rva = oracle.merge(win, glob.numpy(), ref["idx"], has_self=True, total_k=K)
+    np.testing.assert_array_equal(got.cpu().numpy().reshape(B * H, N, -1), rnb)
+    np.testing.assert_array_equal(got_v.cpu().numpy().reshape(B * H, N, -1), rva)
+
+
+def test_lsh_builder_exact_tier_huge_k_replay_outside_lds():
+    attn, got, _, ref, (B, H, N, M, K, w, cross, causal, glob) = _graph_case(HUGE_K, 1,
+                                                                            lsh_only=True)
+    np.testing.assert_array_equal(got.cpu().numpy().reshape(B * H, N, -1), ref["idx"])
+
+
 def test_graph_bf16_inputs_exact_tier():
     """bf16 q/k holding small integers are exact: same graph as fp32."""
     case = GRAPH_CASES[1]

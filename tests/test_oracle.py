@@ -277,3 +277,35 @@ def test_planted_mistake_fails_a_pinning_check(mut):
     with oracle.mutation(mut):
         failed = _pinning_failures()
     assert failed, f"planted mistake '{MUTATIONS[mut]}' passes every pinning check"
+
+
+# ---------------------------------------------------------------------------- CPU baseline
+def _self_attention_fixtures():
+    out = []
+    for path in golden_files():
+        z, m = load_golden(path)
+        if not m["cross"] and m["config"]["global_token_indices"] is None:
+            out.append(path)
+    return out
+
+
+@pytest.mark.parametrize("path", _self_attention_fixtures(), ids=os.path.basename)
+def test_cpu_baseline_port_reproduces_reference_forward(path):
+    """oracle/torch_port.forward, the timed CPU baseline, issues the reference's
+    torch op sequence: its output is bit-identical to the reference's own
+    SparseAttention.forward on every self-attention fixture."""
+    import torch
+    from oracle import torch_port
+    z, m = load_golden(path)
+    c = m["config"]
+    dt = getattr(torch, m["dtype"])
+    W = {n: torch.from_numpy(z["sd_" + n + ".weight"]).to(dt) for n in ("Wq", "Wk", "Wv", "Wo")}
+    x = torch.from_numpy(z["x"]).to(dt)
+    with torch.no_grad():
+        out = torch_port.forward(
+            x, W["Wq"], W["Wk"], W["Wv"], W["Wo"],
+            torch.from_numpy(z["sd_lsh_builder.rand_proj"]), H=m["H"], n_kv=m["n_kv"],
+            K=c["num_neighbors"], window=c["window_size"], glob_n=c["num_global_tokens"],
+            R=c["num_hash_rounds"], max_p=c["max_num_hashes"], T=c["lsh_num_probes"],
+            causal=m["causal"], fp32w=c["fp32_attn_weights"])
+    assert torch.equal(out.float(), torch.from_numpy(z["out"]))
