@@ -17,8 +17,17 @@ Also reported:
 * cpu_baseline: the reference's torch op sequence (oracle/torch_port.py) on
   the host cores, on two kv-head groups (8 of 32 query heads) of the same
   workload, scaled to whole-workload tokens/s;
-* roofline.traffic: HBM bytes per apply launch from the committed rocprofv3
-  FETCH_SIZE/WRITE_SIZE summary (profiles/hbm_traffic_bf16_gqa_n4096.md).
+* roofline.traffic / hbm_frac: HBM bytes per apply launch from the committed
+  rocprofv3 FETCH_SIZE/WRITE_SIZE summary (profiles/hbm_traffic_bf16_gqa_n4096.md)
+  and the share of the 8 TB/s peak they use;
+* roofline.binding: the bound that applies to the gather kernel.  Its K/V rows
+  repeat across queries and are served by the L2, so the kernel is priced
+  against the L2-to-CU delivery rate: bytes the CUs' L1 caches requested from
+  the L2 per launch (TCP_TCC_READ_REQ from the committed summary
+  profiles/l2_traffic_bf16_gqa_n4096.md, times the bytes per request measured
+  on the reference read kernel) over the launch time, against that rate
+  measured live here with ssa_measure_l2_read (every CU streaming an
+  L2-resident buffer with 16-byte loads).
 
 `--workload NAME` measures one of the other workload shapes instead (no CPU
 baseline): fp32_b2_n1024, mqa_n32768, cross_fp32, cross_bf16, transformer6.
@@ -231,12 +240,87 @@ def measured_traffic(kernel):
     return None
 
 
+def _l2_profile_value(tag, kernel):
+    """A `<tag> <kernel> <value>` line of the committed rocprofv3 summary
+    profiles/l2_traffic_bf16_gqa_n4096.md, or None."""
+    path = os.path.join(ROOT, "profiles", "l2_traffic_bf16_gqa_n4096.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                parts = line.strip().strip("`").split()
+                if len(parts) == 3 and parts[0] == tag and parts[1] == kernel:
+                    return float(parts[2])
+    except OSError:
+        pass
+    return None
+
+
+def l2_bytes_per_launch(kernel):
+    """Bytes the CUs' L1 caches requested from the L2 per launch of `kernel`
+    (TCP_TCC_READ_REQ x 128 bytes), or None."""
+    v = _l2_profile_value("l2bytes", kernel)
+    return None if v is None else int(v)
+
+
+def measure_l2_peak(dev, reps=5):
+    """Load rate (bytes/s) of ssa_measure_l2_read with 8 workgroups of 256
+    threads per CU, each streaming the same 1 MiB buffer 8 times (the buffer
+    stays in every XCD's 4 MiB L2; a CU's L1 is 32 KiB), timed with events on
+    the launch stream; the best of `reps` launches after one warm-up."""
+    import torch
+    from ssa_amd import _lib
+    nbytes, iters = 1 << 20, 8
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    blocks = 8 * cus
+    buf = torch.randint(0, 255, (nbytes,), dtype=torch.uint8, device=dev)
+    sink = torch.zeros(blocks, dtype=torch.int32, device=dev)
+    st = torch.cuda.current_stream()
+    _lib.measure_l2_read(buf, blocks, iters, sink)
+    best = None
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(st)
+        _lib.measure_l2_read(buf, blocks, iters, sink)
+        e1.record(st)
+        torch.cuda.synchronize()
+        t = e0.elapsed_time(e1) / 1000.0
+        best = t if best is None or t < best else best
+    return blocks * nbytes * iters / best, {"blocks": blocks, "buffer_bytes": nbytes,
+                                            "iters": iters, "cus": cus}
+
+
+def host_info():
+    model, mem = "", None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+        with open("/proc/meminfo") as f:
+            for line in f:
+                if line.startswith("MemTotal"):
+                    mem = int(line.split()[1]) * 1024
+                    break
+    except OSError:
+        pass
+    return model, mem
+
+
 def cpu_baseline(attn_gpu):
     """Time the reference's CPU op sequence on one kv group of the workload."""
     import torch
     from oracle import torch_port
     cfg = attn_gpu.config
-    nthreads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    # the cores this process may use: its CPU affinity, which on a shared GPU
+    # host is the job's share (os.cpu_count() counts every core of the host)
+    try:
+        nthreads = len(os.sched_getaffinity(0))
+    except AttributeError:
+        nthreads = os.cpu_count() or 1
+    omp = os.environ.get("OMP_NUM_THREADS")
+    if omp:
+        nthreads = min(nthreads, int(omp))
     torch.set_num_threads(nthreads)
     rep = attn_gpu.kv_rep
     d = attn_gpu.d_head
@@ -261,21 +345,17 @@ def cpu_baseline(attn_gpu):
     t = sorted(times[1:])[1]
     groups = cfg.num_heads // rep
     tok_s = 4096 / (t * groups / ng)
-    model = ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
+    model, mem = host_info()
     return {"value": tok_s, "unit": "tokens/s", "cores": torch.get_num_threads(),
             "kind": "port",
             "sample": f"{ng} of {groups} kv-head groups ({ng * rep} query heads, {ng} kv heads) "
                       f"of the same workload through the reference's torch CPU op sequence "
-                      f"(oracle/torch_port.py), median {t:.2f} s, scaled x{groups // ng}; "
-                      f"1 warm-up + 3 timed runs; CPU: {model}"}
+                      f"(oracle/torch_port.py, bit-identical to the reference on its fixtures), "
+                      f"median {t:.2f} s, scaled x{groups // ng} (kv groups are independent "
+                      f"work of equal size; the whole workload would take about "
+                      f"{4 * t * groups / ng:.0f} s for 1 warm-up + 3 runs); CPU: {model}",
+            "os_cpu_count": os.cpu_count(), "omp_num_threads": os.environ.get("OMP_NUM_THREADS"),
+            "host_ram_bytes": mem}
 
 
 def main():
@@ -365,6 +445,14 @@ def main():
     achieved = bytes_apply / (t_apply / 1000.0)
     traffic = measured_traffic(APPLY_KERNEL)
     print(f"# build {t_build:.3f} ms, apply {t_apply:.3f} ms", file=sys.stderr, flush=True)
+    l2_rate, l2_setup = measure_l2_peak(dev)
+    # the share of the reference kernel's loads that the L2 served (the rest
+    # hit in L1), from the same counters as the apply kernel's L2 bytes
+    l2_share = _l2_profile_value("l2share", "l2_read_kernel")
+    l2_peak = l2_rate * (l2_share if l2_share is not None else 1.0)
+    l2_setup["l2_share"] = l2_share
+    l2_bytes = l2_bytes_per_launch(APPLY_KERNEL)
+    print(f"# L2-to-CU delivery {l2_peak / 1e12:.2f} TB/s", file=sys.stderr, flush=True)
 
     # rows whose k-th LSH score is tied (selection decided by the tie rule)
     from ssa_amd import _lib
@@ -397,7 +485,22 @@ def main():
         "roofline": {"bound": "hbm", "achieved": achieved / 1e9, "peak": PEAK_HBM / 1e9,
                      "unit": "GB/s", "frac": achieved / PEAK_HBM, "traffic": traffic,
                      "kernel": APPLY_KERNEL, "bytes_per_launch": bytes_apply,
-                     "ms_per_launch": t_apply},
+                     "ms_per_launch": t_apply,
+                     # measured HBM bytes per launch over the launch time: the
+                     # gathered rows repeat, so HBM carries ~2% of the
+                     # algorithmic bytes and frac above (algorithmic bytes at
+                     # the HBM peak) exceeds 1
+                     "hbm_frac": (traffic / (t_apply / 1000.0) / PEAK_HBM
+                                  if traffic is not None else None),
+                     "binding": {
+                         "resource": "L2 to CU",
+                         "achieved": (l2_bytes / (t_apply / 1000.0) / 1e9
+                                      if l2_bytes is not None else None),
+                         "peak": l2_peak / 1e9, "unit": "GB/s",
+                         "frac": (l2_bytes / (t_apply / 1000.0) / l2_peak
+                                  if l2_bytes is not None else None),
+                         "bytes_per_launch": l2_bytes,
+                         "peak_kernel": "ssa_measure_l2_read", "peak_setup": l2_setup}},
         "t_build_ms": t_build, "t_apply_ms": t_apply, "t_apply_warm_ms": t_apply_warm,
         "k_out": K_out,
         "tie_rows": tie_rows, "query_rows": B * H * N,

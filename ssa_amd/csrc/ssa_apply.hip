@@ -82,6 +82,15 @@ __device__ __forceinline__ float drop_uniform(uint64_t seed, int64_t row, int j)
     return (float)(x >> 40) * (1.0f / 16777216.0f);
 }
 
+// The factor kept weights are multiplied by: the reference's dropout runs on
+// the weights in their own dtype (the value dtype, or fp32 with
+// fp32_attn_weights), whose noise tensor holds 1 / (1 - p) rounded to that
+// dtype (sparse_attention.py:1193-1194).
+template <typename T>
+__device__ __forceinline__ float drop_scale_of(const ApplyP &p) {
+    return p.fp32w ? p.drop_scale : Cvt<T>::round(p.drop_scale);
+}
+
 template <typename T, int D, int U>
 __global__ void __launch_bounds__(WAVES * SSA_WAVE)
 apply_fwd_kernel(ApplyP p) {
@@ -162,7 +171,7 @@ apply_fwd_kernel(ApplyP p) {
         float w = expf(sc[j] - m) * inv;
         if (!p.fp32w) w = Cvt<T>::round(w);
         if (p.drop_p > 0.f) {
-            w = (drop_uniform(p.seed, row, j) < p.drop_p) ? 0.f : w * p.drop_scale;
+            w = (drop_uniform(p.seed, row, j) < p.drop_p) ? 0.f : w * drop_scale_of<T>(p);
             if (!p.fp32w) w = Cvt<T>::round(w);
         }
         sc[j] = w;
@@ -405,7 +414,7 @@ apply_fwd16_kernel(ApplyP p) {
             w = Cvt<T>::round(expf(sc[j] - m) * inv);
             if (p.drop_p > 0.f)
                 w = (drop_uniform(p.seed, row, j) < p.drop_p) ? 0.f
-                                                              : Cvt<T>::round(w * p.drop_scale);
+                                                              : Cvt<T>::round(w * drop_scale_of<T>(p));
         }
         sc[j] = w;
     }
@@ -526,7 +535,7 @@ apply_bwd_kernel(ApplyP p) {
     for (int j = lane; j < p.K; j += SSA_WAVE) {
         float pj = expf(sc[j] - m) / l;
         float mask = 1.f;
-        if (p.drop_p > 0.f) mask = (drop_uniform(p.seed, row, j) < p.drop_p) ? 0.f : p.drop_scale;
+        if (p.drop_p > 0.f) mask = (drop_uniform(p.seed, row, j) < p.drop_p) ? 0.f : drop_scale_of<T>(p);
         float dpj = dpv[j] * mask;
         pdp += pj * dpj;
         sc[j] = pj;          // keep p
@@ -548,7 +557,7 @@ apply_bwd_kernel(ApplyP p) {
         const float pj = sc[j];
         const float draw = pj * (dpv[j] - pdp) * p.scale;
         float mask = 1.f;
-        if (p.drop_p > 0.f) mask = (drop_uniform(p.seed, row, j) < p.drop_p) ? 0.f : p.drop_scale;
+        if (p.drop_p > 0.f) mask = (drop_uniform(p.seed, row, j) < p.drop_p) ? 0.f : drop_scale_of<T>(p);
         const float pw = pj * mask;
         float kf[VEC];
         load_vec<T, VEC>(kb + x * p.ksn + li * VEC, kf);
@@ -673,7 +682,9 @@ int apply_common(const ssa_apply_args *a, ApplyP &p) {
     p.nb = a->neighbors; p.valid = a->valid; p.nb32 = a->neighbors32;
     p.scale = a->scale; p.fp32w = a->fp32_weights;
     p.drop_p = a->dropout_p;
-    p.drop_scale = a->dropout_p > 0.f ? 1.f / (1.f - a->dropout_p) : 1.f;
+    // inverted dropout scales kept weights by 1 / (1 - p), the keep rate taken
+    // in double and rounded to fp32 as torch's dropout divides its noise
+    p.drop_scale = a->dropout_p > 0.f ? 1.f / (float)(1.0 - (double)a->dropout_p) : 1.f;
     p.seed = a->seed;
     p.out = a->out; p.osb = a->out_sb; p.osh = a->out_sh; p.osn = a->out_sn;
     p.rows = (int64_t)a->B * a->Hq * a->N;

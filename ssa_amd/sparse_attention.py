@@ -24,6 +24,7 @@ import warnings
 from dataclasses import dataclass
 from typing import Optional, Tuple
 
+import numpy as np
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
@@ -450,9 +451,17 @@ class SparseAttention(nn.Module):
             "peak_sparse_elems": peak_sparse,
             "peak_full_elems": peak_full,
             "compression": peak_full / peak_sparse,
-            "padding_fraction": ((~valid).float().mean().item() if valid is not None
-                                 else (neighbors < 0).float().mean().item()),
+            "padding_fraction": _padding_fraction(~valid if valid is not None
+                                                  else neighbors < 0),
         }
+
+
+def _padding_fraction(invalid: torch.Tensor) -> float:
+    """Mean of a boolean mask as the reference's CPU ``.float().mean()``
+    rounds it: the exact count divided by the element count in fp32 (the
+    device's mean multiplies by a rounded reciprocal instead)."""
+    count = int(invalid.sum().item())
+    return float(np.float32(count) / np.float32(max(invalid.numel(), 1)))
 
 
 # ---------------------------------------------------------------------------- transformer
@@ -581,7 +590,7 @@ class CachedGraphSparseTransformer(nn.Module):
                 stats_list.append({
                     "neighbors_shape": tuple(nb.shape),
                     "compression": peak_full / peak_sparse,
-                    "padding_fraction": (~va).float().mean().item(),
+                    "padding_fraction": _padding_fraction(~va),
                     "graph_recomputed": recompute,
                 })
             else:

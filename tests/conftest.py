@@ -45,3 +45,12 @@ def has_gpu() -> bool:
         return torch.cuda.is_available()
     except Exception:
         return False
+
+
+def row_rel_err(got, ref):
+    """Largest per-row relative error: max over rows (the last dimension) of
+    max |got - ref| / max |ref| within the row."""
+    g = np.asarray(got, np.float64).reshape(-1, np.shape(got)[-1])
+    r = np.asarray(ref, np.float64).reshape(-1, np.shape(ref)[-1])
+    scale = np.maximum(np.abs(r).max(-1), 1e-30)
+    return float((np.abs(g - r).max(-1) / scale).max())

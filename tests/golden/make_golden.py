@@ -14,7 +14,7 @@ fallback, chunked top-k, -inf fallback), merge_neighbors, build_graph,
 sparse_gather_attention, SparseAttention.forward with its stats, and the RNG
 consumption order of seeded construction.
 
-Usage:  python tests/golden/make_golden.py [--only-empty-ranked]
+Usage:  python tests/golden/make_golden.py [--only-empty-ranked | --only-models]
 """
 from __future__ import annotations
 
@@ -190,10 +190,134 @@ def lsh_empty_bucket_ranked_case(sa):
                 rand_proj=_np(lsh.rand_proj)), dict(C=4, top_k=2, max_P=1, R=2)
 
 
+# ---------------------------------------------------------------------------- models
+# Tiny SparseTransformer / CachedGraphSparseTransformer configurations: per
+# layer they store the layer's input, q / k (expanded, as the reference holds
+# them) / v, the fp32 hash projections as the reference computes them, the
+# graph, the attention output and the layer's output; plus the final output,
+# the stats list and the construction state_dict.
+MODEL_CFG = dict(d_model=32, num_heads=4, num_kv_heads=2, num_neighbors=16, window_size=2,
+                 num_global_tokens=2, max_num_hashes=4, num_hash_rounds=3, lsh_num_probes=1,
+                 causal=True)
+MODEL_SHAPE = (2, 96)          # batch, tokens
+MODEL_DIR = os.path.join(HERE, "models")
+
+
+def _projections(builder, q, k, N, M):
+    """fp32 hash projections of q and k per round, (BH, R, L, P), as the
+    reference computes them (sparse_attention.py:593-597)."""
+    lb = builder.lsh_builder
+    p_eff = lb.compute_effective_p(M, lb.C, lb.max_P)
+    B, H = q.shape[:2]
+    qf = q.reshape(B * H, N, -1)
+    kf = k.reshape(B * H, M, -1)
+    qp = torch.stack([lb._hash_proj(qf, r, p_eff) for r in range(lb.R)], 1)
+    kp = torch.stack([lb._hash_proj(kf, r, p_eff) for r in range(lb.R)], 1)
+    return qp, kp, p_eff
+
+
+def _stats_json(stats_list):
+    return [{k: (list(v) if isinstance(v, tuple) else v) for k, v in st.items()}
+            for st in stats_list]
+
+
+def model_case(sa, kind, dtype, seed):
+    """kind: 'transformer' (2-layer SparseTransformer with a 50-token
+    vocabulary, token ids in) or 'cached' (3-layer
+    CachedGraphSparseTransformer, reuse_every=2, embeddings in)."""
+    cfg = sa.SSAConfig(**MODEL_CFG)
+    B, N = MODEL_SHAPE
+    torch.manual_seed(seed)
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")
+        if kind == "transformer":
+            model = sa.SparseTransformer(cfg, num_layers=2, vocab_size=50)
+        else:
+            model = sa.CachedGraphSparseTransformer(cfg, num_layers=3, reuse_every=2)
+    model.eval()
+    init_state = {k: _np(v) for k, v in model.state_dict().items()}
+    dt = getattr(torch, dtype)
+    if dtype != "float32":
+        # parameters only: the hyperplane buffers stay fp32 (the reference's
+        # fp32 hash matmul needs them so)
+        for p in model.parameters():
+            p.data = p.data.to(dt)
+    gen = torch.Generator().manual_seed(2000 + seed)
+    rec = {}
+    with torch.no_grad():
+        if kind == "transformer":
+            ids = torch.randint(0, 50, (B, N), generator=gen)
+            rec["ids"] = ids.numpy()
+            out, stats = model(ids, return_stats=True)
+            h = model.embed(ids)
+        else:
+            x = torch.randn(B, N, cfg.d_model, generator=gen).to(dt)
+            rec["x"] = _np(x)
+            out, stats = model(x, return_stats=True)
+            h = x
+        # the layer loop again, step by step, with the reference's own methods
+        cached, cached_group = None, None
+        for li, layer in enumerate(model.layers):
+            attn = layer.attn
+            normed = layer.norm1(h)
+            q = attn._split_q(attn.Wq(normed))
+            k = attn._split_kv(attn.Wk(normed))
+            v = attn._split_kv(attn.Wv(normed))
+            if kind == "transformer":
+                builder, recompute = attn, True
+            else:
+                group = model.group_of[li]
+                builder, recompute = model.shared_attn_per_group[group], group != cached_group
+            qp, kp, p_eff = _projections(builder, q, k, N, N)
+            if recompute:
+                nb, va = builder.build_graph(q, k, N, N, B, "cpu", cfg.causal, False)
+                if kind == "cached":
+                    cached, cached_group = (nb, va), group
+            else:
+                nb, va = cached
+            att = attn.apply_graph(q, k, v, nb, va)
+            a = attn.Wo(attn._merge(att))
+            h_next = h + a + layer.ff(layer.norm2(h + a))
+            if kind == "transformer":
+                ref_next, _ = layer(h)
+                assert torch.equal(ref_next, h_next), "layer loop restated differently"
+            for key, val in (("in", h), ("q", q), ("k", k), ("v", v), ("qproj", qp),
+                             ("kproj", kp), ("neighbors", nb), ("valid", va),
+                             ("attn_out", att), ("out", h_next)):
+                rec[f"l{li}_{key}"] = _np(val)
+            rec[f"l{li}_recompute"] = np.array(recompute)
+            h = h_next
+        assert torch.equal(model.norm(h), out), "model output restated differently"
+    rec["out"] = _np(out)
+    rec.update({"sd_" + k: v for k, v in init_state.items()})
+    meta = dict(kind=kind, seed=seed, dtype=dtype, B=B, N=N, config=MODEL_CFG,
+                num_layers=len(model.layers), stats=_stats_json(stats),
+                group_of=list(getattr(model, "group_of", [])))
+    return rec, meta
+
+
+def write_models(sa):
+    os.makedirs(MODEL_DIR, exist_ok=True)
+    names = []
+    for kind in ("transformer", "cached"):
+        for dtype in ("float32", "bfloat16"):
+            for seed in SEEDS:
+                rec, meta = model_case(sa, kind, dtype, seed)
+                fn = f"{kind}_{'fp32' if dtype == 'float32' else 'bf16'}_seed{seed}.npz"
+                np.savez_compressed(os.path.join(MODEL_DIR, fn), meta=json.dumps(meta), **rec)
+                names.append(fn)
+                print("wrote models/" + fn, flush=True)
+    with open(os.path.join(MODEL_DIR, "index.json"), "w") as f:
+        json.dump(names, f, indent=1)
+
+
 def main():
     sys.path.insert(0, REF)
     import sparse_attention as sa  # the reference module (read-only checkout)
 
+    if "--only-models" in sys.argv:
+        write_models(sa)
+        return
     if "--only-empty-ranked" in sys.argv:
         rec, meta = lsh_empty_bucket_ranked_case(sa)
         np.savez_compressed(os.path.join(HERE, "lsh_empty_bucket_ranked.npz"),
@@ -217,6 +341,7 @@ def main():
     index.append("lsh_empty_bucket_ranked.npz")
     with open(os.path.join(HERE, "index.json"), "w") as f:
         json.dump(index, f, indent=1)
+    write_models(sa)
 
 
 if __name__ == "__main__":

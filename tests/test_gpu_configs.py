@@ -25,7 +25,7 @@ import pytest
 import torch
 
 import oracle
-from conftest import has_gpu
+from conftest import has_gpu, row_rel_err
 
 pytestmark = [pytest.mark.gpu,
               pytest.mark.skipif(not has_gpu(), reason="needs a ROCm GPU")]
@@ -164,7 +164,8 @@ def _check_against_oracle(attn, q, k, v, nb, va, causal, cross, q_step, heads=No
                 assert _near_tie_ok(qf[h0, n].astype(np.float64), kf[g].astype(np.float64),
                                     a, b, kth), f"unexplained LSH difference head {h0} row {n}"
                 n_near += 1
-    assert n_exact >= 0.95 * n_rows, (n_rows, n_exact, n_tie, n_near)
+    # each non-exact row is a proven fp32 near tie; they stay rare
+    assert n_near <= max(2, n_rows // 100), (n_rows, n_exact, n_tie, n_near)
     print(f"  sampled rows {n_rows} (tied kk-th score: {n_tie}): exact {n_exact}, "
           f"near-tie {n_near}", flush=True)
 
@@ -181,7 +182,7 @@ def _check_against_oracle(attn, q, k, v, nb, va, causal, cross, q_step, heads=No
     if mode == 1:
         ref_o = torch.from_numpy(ref_o).to(torch.bfloat16).float().numpy()
     tol = 1e-5 if mode == 0 else 2e-2
-    err = np.abs(og - ref_o).max() / max(np.abs(ref_o).max(), 1e-30)
+    err = row_rel_err(og, ref_o)
     assert err <= tol, err
 
 
@@ -223,7 +224,8 @@ def test_bf16_mqa_n32768_probes_explicit_globals():
     cfg = dict(d_model=4096, num_heads=32, num_kv_heads=1, num_neighbors=256, window_size=32,
                global_token_indices=[0, 1, 16384], num_hash_rounds=8, max_num_hashes=12,
                lsh_num_probes=2, causal=True)
-    _run_self(cfg, 1, 32768, torch.bfloat16, 0, 1.0, False, q_step=1024, heads=[0, 17, 31])
+    _run_self(cfg, 1, 32768, torch.bfloat16, 0, 1.0, False, q_step=128,
+              heads=[0, 7, 17, 24, 31])
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])

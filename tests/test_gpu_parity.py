@@ -1,7 +1,8 @@
 """GPU parity of the HIP kernels against the oracle (and the golden vectors).
 
 Bar: neighbor ids / valid masks / permutations bit-exact; attention output
-within 1e-5 relative (fp32) and 2e-2 (bf16/fp16), relative to max |ref|.
+within 1e-5 relative (fp32) and 2e-2 (bf16/fp16), per query row: the row's
+largest deviation over the row's largest reference magnitude.
 
 Two input tiers (sparse_attention.py cannot fix fp32 summation order):
 * exact-arithmetic inputs (small integers): every fp32 projection and score is
@@ -19,7 +20,7 @@ import pytest
 import torch
 
 import oracle
-from conftest import golden_files, has_gpu, load_golden
+from conftest import golden_files, has_gpu, load_golden, row_rel_err
 
 pytestmark = [pytest.mark.gpu,
               pytest.mark.skipif(not has_gpu(), reason="needs a ROCm GPU")]
@@ -257,7 +258,7 @@ def test_apply_matches_oracle(case, dtype, fp32w):
                        mode=MODE[dtype], fp32_attn_weights=fp32w)
     ref = torch.from_numpy(ref).to(dtype).float().numpy()   # reference output dtype
     got = out.float().cpu().numpy().reshape(B * H, N, d)
-    err = np.abs(got - ref).max() / np.abs(ref).max()
+    err = row_rel_err(got, ref)
     assert err <= REL[dtype], err
 
 
@@ -302,6 +303,117 @@ def test_apply_backward_matches_autograd_reference(dtype):
         assert e < tol, e
 
 
+# ------------------------------------------------------------------ dropout
+@pytest.mark.parametrize("dtype,fp32w", [(torch.float32, False), (torch.bfloat16, False),
+                                         (torch.bfloat16, True)])
+def test_dropout_keep_rate_scaling_and_backward(dtype, fp32w):
+    """Training-mode dropout on the attention weights (sparse_attention.py:
+    1193-1194) over 1,048,576 slots.  V rows are one-hot, so each output
+    element is the weight of one key: the output shows every slot's weight
+    with and without dropout.
+    * the kept fraction is within 5 sigma of 1 - p (overall and per slot);
+    * a dropped weight is 0 and a kept one is the weight times 1 / (1 - p),
+      both in the weights' dtype (torch's dropout multiplies by a noise
+      tensor of that dtype holding 1 / (1 - p));
+    * the backward of the same call (same seed) matches float64 autograd of
+      the forward with the mask read off its output."""
+    from ssa_amd import sparse_gather_attention
+    B, H, N, M, d, K = 1, 2, 4096, 128, 128, 128
+    p = 0.25
+    scale = d ** -0.5
+    g = torch.Generator().manual_seed(11)
+    q = torch.randn(B, H, N, d, generator=g).to(dtype)
+    k = torch.randn(B, H, M, d, generator=g).to(dtype)
+    v = torch.eye(M, d).expand(B, H, M, d).contiguous().to(dtype)
+    nb = torch.argsort(torch.rand(B, H, N, K, generator=g), -1)   # every key once per row
+    qd, kd, vd, nbd = (t.to(DEV) for t in (q, k, v, nb))
+    with torch.no_grad():
+        w0 = sparse_gather_attention(qd, kd, vd, nbd, scale, fp32_attn_weights=fp32w)
+    torch.manual_seed(1234)
+    qg, kg_, vg_ = (t.clone().requires_grad_(True) for t in (qd, kd, vd))
+    out = sparse_gather_attention(qg, kg_, vg_, nbd, scale, dropout=p, training=True,
+                                  fp32_attn_weights=fp32w)
+    G = torch.randn(B, H, N, d, generator=g).to(DEV, dtype)
+    out.backward(G)
+    torch.cuda.synchronize()
+    w0c, w1 = w0.float().cpu(), out.detach().float().cpu()
+    assert (w0c > 0).all()
+    keep = w1 != 0
+    n = keep.numel()
+    rate = keep.float().mean().item()
+    sig = (p * (1 - p) / n) ** 0.5
+    assert abs(rate - (1 - p)) < 5 * sig, (rate, sig)
+    per_slot = keep.reshape(-1, d).float().mean(0)
+    sig1 = (p * (1 - p) / (n // d)) ** 0.5
+    assert (per_slot - (1 - p)).abs().max().item() < 5 * sig1
+    s32 = torch.tensor(1.0, dtype=torch.float32) / torch.tensor(1.0 - p, dtype=torch.float32)
+    if fp32w:
+        # fp32 weights scaled in fp32, the output rounded once to bf16; the
+        # undropped output is itself the weight rounded to bf16, so the two
+        # differ by at most two bf16 roundings (2^-8 relative each)
+        rel = ((w1[keep] - w0c[keep] * s32) / (w0c[keep] * s32)).abs().max().item()
+        assert rel <= 2 ** -7, rel
+    else:
+        s_dt = s32.to(dtype)
+        expect = (w0.cpu() * s_dt).float()          # product in fp32, rounded to dtype
+        expect = expect.to(dtype).float()
+        assert torch.equal(w1[keep], expect[keep])
+    # backward against float64 autograd (on the device) with the observed
+    # mask: slot j of a row holds key nb[j], whose output column shows it
+    mask = torch.gather(keep.double(), 3, nb).to(DEV)
+    qr, kr, vr = (t.to(DEV).double().requires_grad_(True) for t in (q, k, v))
+    flat = (nbd + torch.arange(B * H, device=DEV).view(B, H, 1, 1) * M).reshape(-1)
+    kgat = kr.reshape(B * H * M, d).index_select(0, flat).view(B, H, N, K, d)
+    vgat = vr.reshape(B * H * M, d).index_select(0, flat).view(B, H, N, K, d)
+    sc = (qr.unsqueeze(3) * kgat).sum(-1) * scale
+    pr = torch.softmax(sc, -1) * mask * float(s32)
+    o = (pr.unsqueeze(-1) * vgat).sum(3)
+    o.backward(G.double())
+    tol = 1e-4 if dtype == torch.float32 else 5e-2
+    for name, got, exp in [("dq", qg.grad, qr.grad), ("dk", kg_.grad, kr.grad),
+                           ("dv", vg_.grad, vr.grad)]:
+        e = ((got.double() - exp).abs().max() / exp.abs().max()).item()
+        assert e < tol, (name, e)
+
+
+@pytest.mark.parametrize("dtype,fp32w", [(torch.bfloat16, False), (torch.bfloat16, True),
+                                         (torch.float32, False)])
+def test_apply_backward_at_bench_head_shape(dtype, fp32w):
+    """Backward at the bf16 GQA bench shape (N=4096, K=128, d=128), two kv
+    groups (8 query heads), against float64 autograd of the same function
+    computed on the device."""
+    from ssa_amd import sparse_gather_attention
+    B, H, nkv, N, M, d, K = 1, 8, 2, 4096, 4096, 128, 128
+    g = torch.Generator().manual_seed(21)
+    q = (torch.randn(B, H, N, d, generator=g) * 0.5).to(dtype)
+    k = (torch.randn(B, nkv, M, d, generator=g) * 0.5).to(dtype)
+    v = torch.randn(B, nkv, M, d, generator=g).to(dtype)
+    nb = torch.randint(0, M, (B, H, N, K), generator=g)
+    va = torch.rand(B, H, N, K, generator=g) > 0.2
+    va[..., 0] = True
+    dout = torch.randn(B, H, N, d, generator=g)
+    qd, kd, vd = (t.to(DEV).requires_grad_(True) for t in (q, k, v))
+    out = sparse_gather_attention(qd, kd, vd, nb.to(DEV), d ** -0.5, valid=va.to(DEV),
+                                  fp32_attn_weights=fp32w)
+    out.backward(dout.to(DEV, dtype))
+    qr, kr, vr = (t.to(DEV).double().requires_grad_(True) for t in (q, k, v))
+    nbd, vad = nb.to(DEV), va.to(DEV)
+    ke = kr.repeat_interleave(H // nkv, 1)
+    ve = vr.repeat_interleave(H // nkv, 1)
+    flat = (nbd + torch.arange(B * H, device=DEV).view(B, H, 1, 1) * M).reshape(-1)
+    kg = ke.reshape(B * H * M, d).index_select(0, flat).view(B, H, N, K, d)
+    vg = ve.reshape(B * H * M, d).index_select(0, flat).view(B, H, N, K, d)
+    s = (qr.unsqueeze(3) * kg).sum(-1) * d ** -0.5
+    p = torch.softmax(s.masked_fill(~vad, float("-inf")), -1)
+    o = (p.unsqueeze(-1) * vg).sum(3)
+    o.backward(dout.to(DEV).double())
+    tol = 1e-4 if dtype == torch.float32 else 5e-2
+    for name, got, exp in [("dq", qd.grad, qr.grad), ("dk", kd.grad, kr.grad),
+                           ("dv", vd.grad, vr.grad)]:
+        e = ((got.double() - exp).abs().max() / exp.abs().max()).item()
+        assert e < tol, (name, e)
+
+
 # ------------------------------------------------------------------ merge
 @pytest.mark.parametrize("has_self", [True, False])
 @pytest.mark.parametrize("K", [8, 24, 200])
@@ -337,6 +449,5 @@ def test_apply_graph_on_reference_vectors(path):
     va = torch.from_numpy(z["valid"]).to(DEV)
     with torch.no_grad():
         out = attn.apply_graph(q, k, v, nb, va)
-    ref = z["attn_out"]
-    err = np.abs(out.float().cpu().numpy() - ref).max() / np.abs(ref).max()
+    err = row_rel_err(out.float().cpu().numpy(), z["attn_out"])
     assert err <= REL[dt], err

@@ -159,3 +159,32 @@ def test_transformer_structure_and_state_keys():
               "norm.bias"]:
         assert k in keys
     assert SparseTransformer(cfg, num_layers=1).embed is None
+
+
+MODEL_FIXTURES = sorted(__import__("glob").glob(
+    __import__("os").path.join(__import__("conftest").GOLDEN, "models", "*_seed*.npz")))
+
+
+@pytest.mark.parametrize("path", MODEL_FIXTURES, ids=lambda p: p.split("/")[-1])
+def test_seeded_model_construction_matches_reference_state_dict(path):
+    """SparseTransformer (embedding, layers, final norm) and
+    CachedGraphSparseTransformer (shared graph builders per group, then the
+    layers) draw the reference's weights and hyperplanes in its order."""
+    import json
+    from ssa_amd import CachedGraphSparseTransformer
+    z = np.load(path)
+    m = json.loads(str(z["meta"]))
+    cfg = SSAConfig(**m["config"])
+    torch.manual_seed(m["seed"])
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")
+        if m["kind"] == "transformer":
+            model = SparseTransformer(cfg, num_layers=m["num_layers"], vocab_size=50)
+        else:
+            model = CachedGraphSparseTransformer(cfg, num_layers=m["num_layers"], reuse_every=2)
+            assert model.group_of == m["group_of"]
+    sd = model.state_dict()
+    ref_keys = sorted(k[3:] for k in z.files if k.startswith("sd_"))
+    assert sorted(sd.keys()) == ref_keys
+    for key in ref_keys:
+        np.testing.assert_array_equal(sd[key].numpy(), z["sd_" + key], err_msg=key)
