@@ -127,6 +127,20 @@ int ssa_build_graph(const ssa_graph_args *a, void *workspace, int64_t workspace_
 int ssa_build_graph_phases(const ssa_graph_args *a, void *workspace, int64_t workspace_bytes,
                            void *stream, int phases);
 
+/* ssa_build_graph without any device allocation (no counterpart in the
+ * reference): for callers that cannot allocate -- code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc.  The same
+ * arguments, outputs and results as ssa_build_graph, but the workspace is a
+ * fixed array of SSA_NOALLOC_SCRATCH_BYTES in device memory that the library
+ * holds on every GPU it runs on until the process ends.  Query heads are built
+ * in chunks small enough for it; a problem that needs more than the array with
+ * one query head per chunk fails with SSA_E_WORKSPACE before any launch.  The
+ * caller still allocates the outputs.  `stream` must belong to the current
+ * device.  All calls on one GPU share its array: calls that overlap on one GPU
+ * (other streams, other host threads) race and must not be issued. */
+#define SSA_NOALLOC_SCRATCH_BYTES (64 << 20)
+int ssa_build_graph_noalloc(const ssa_graph_args *a, void *stream);
+
 /* ---------------------------------------------------------------------------
  * Bucket permutation: for each of `rows` rows of `n` bucket ids (uint16, values
  * < 2^P), the permutation torch.sort(ids, dim=-1) returns on the CPU (an

@@ -83,6 +83,8 @@ def lib():
         L.ssa_graph_workspace_bytes.argtypes = [ctypes.POINTER(GraphArgs)]
         L.ssa_build_graph.restype = ctypes.c_int
         L.ssa_build_graph.argtypes = [ctypes.POINTER(GraphArgs), c_vp, c_i64, c_vp]
+        L.ssa_build_graph_noalloc.restype = ctypes.c_int
+        L.ssa_build_graph_noalloc.argtypes = [ctypes.POINTER(GraphArgs), c_vp]
         L.ssa_build_graph_phases.restype = ctypes.c_int
         L.ssa_build_graph_phases.argtypes = [ctypes.POINTER(GraphArgs), c_vp, c_i64, c_vp, c_i32]
         L.ssa_bucket_sort_workspace_bytes.restype = c_i64
@@ -148,11 +150,15 @@ def _ptr(t):
 
 # --------------------------------------------------------------------------- graph build
 def build_graph(q, k, rand_proj, *, P, T, C, top_k, window, causal, is_cross, total_k, glob,
-                mode=GRAPH_FULL, q_proj=None, k_proj=None, count_ties=False, ids32=False):
+                mode=GRAPH_FULL, q_proj=None, k_proj=None, count_ties=False, ids32=False,
+                noalloc=False):
     """Run ssa_build_graph.  q (B,Hq,N,d), k (B,Hkv,M,d) views on one device.
 
     Returns (out_idx, out_valid or None, ties or None).  With ids32 (FULL mode)
-    out_idx is int32 with -1 in the invalid slots and out_valid is None."""
+    out_idx is int32 with -1 in the invalid slots and out_valid is None.  With
+    noalloc the build runs through ssa_build_graph_noalloc: no workspace is
+    allocated (the library's fixed scratch array serves instead; the outputs
+    are still allocated here)."""
     if q.dim() != 4 or k.dim() != 4:
         raise RuntimeError(f"ssa_amd.build_graph: q {tuple(q.shape)} and k {tuple(k.shape)} must "
                            "be 4-D")
@@ -196,7 +202,7 @@ def build_graph(q, k, rand_proj, *, P, T, C, top_k, window, causal, is_cross, to
     width = L.ssa_graph_out_width(ctypes.byref(a))
     if width < 0:
         _check(-1, "build_graph")
-    wsb = L.ssa_graph_workspace_bytes(ctypes.byref(a))
+    wsb = 0 if noalloc else L.ssa_graph_workspace_bytes(ctypes.byref(a))
     if wsb < 0:
         _check(-1, "build_graph")
     compact = ids32 and mode == GRAPH_FULL
@@ -210,9 +216,14 @@ def build_graph(q, k, rand_proj, *, P, T, C, top_k, window, causal, is_cross, to
     else:
         a.out_idx, a.out_valid = out.data_ptr(), _ptr(valid)
     a.out_ties = _ptr(ties)
-    ws = torch.empty(max(int(wsb), 1), dtype=torch.uint8, device=q.device)
-    _check(L.ssa_build_graph(ctypes.byref(a), ws.data_ptr(), int(wsb), _stream(q)),
-           "build_graph")
+    if noalloc:
+        ws = None
+        with torch.cuda.device(q.device):
+            _check(L.ssa_build_graph_noalloc(ctypes.byref(a), _stream(q)), "build_graph_noalloc")
+    else:
+        ws = torch.empty(max(int(wsb), 1), dtype=torch.uint8, device=q.device)
+        _check(L.ssa_build_graph(ctypes.byref(a), ws.data_ptr(), int(wsb), _stream(q)),
+               "build_graph")
     # keep inputs alive until the stream has consumed them
     _keep = (qk, kk_, rp, g, qp, kp, ws)
     del _keep
