@@ -15,12 +15,15 @@
 // !valid; p = exp(s - max) / sum in fp32; 16-bit models round p to the value
 // dtype before P.V (fp32_attn_weights keeps it fp32); P.V accumulates in fp32
 // and is rounded once to the output dtype.
+#include <type_traits>
+
 #include "ssa_common.h"
 
 namespace {
 
 struct ApplyP {
     int32_t B, Hq, Hkv, N, M, K, rep;
+    int32_t d;             // head dim (<= the kernel's D; lanes past it load zeros, store nothing)
     const void *q, *k, *v;
     int64_t qsb, qsh, qsn, ksb, ksh, ksn, vsb, vsh, vsn;
     const int64_t *nb;
@@ -125,8 +128,13 @@ apply_fwd_kernel(ApplyP p) {
         const bool o = (p.nb32 ? true : (va ? va[j] != 0 : true)) && x >= 0 && x < p.M;
         ix[j] = o ? (int)x : -1;
     }
+    // lanes whose elements lie past the head dim hold zeros and store nothing
+    const bool live = li * VEC < p.d;
+    const int lofs = live ? li * VEC : 0;
     float qf[VEC];
-    load_vec<T, VEC>(qrow + li * VEC, qf);
+    load_vec<T, VEC>(qrow + lofs, qf);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) qf[e] = live ? qf[e] : 0.f;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -142,7 +150,7 @@ apply_fwd_kernel(ApplyP p) {
         float kf[U][VEC];
 #pragma unroll
         for (int u = 0; u < U; ++u)
-            load_vec<T, VEC>(kb + (int64_t)(xi[u] < 0 ? 0 : xi[u]) * p.ksn + li * VEC, kf[u]);
+            load_vec<T, VEC>(kb + (int64_t)(xi[u] < 0 ? 0 : xi[u]) * p.ksn + lofs, kf[u]);
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             float part = 0.f;
@@ -197,7 +205,7 @@ apply_fwd_kernel(ApplyP p) {
         float vf[U][VEC];
 #pragma unroll
         for (int u = 0; u < U; ++u)
-            load_vec<T, VEC>(vb + (int64_t)(xi[u] < 0 ? 0 : xi[u]) * p.vsn + li * VEC, vf[u]);
+            load_vec<T, VEC>(vb + (int64_t)(xi[u] < 0 ? 0 : xi[u]) * p.vsn + lofs, vf[u]);
 #pragma unroll
         for (int u = 0; u < U; ++u)
 #pragma unroll
@@ -207,7 +215,7 @@ apply_fwd_kernel(ApplyP p) {
     for (int o = LPR; o < SSA_WAVE; o <<= 1)
 #pragma unroll
         for (int e = 0; e < VEC; ++e) acc[e] += __shfl_xor(acc[e], o, SSA_WAVE);
-    if (sub == 0) {
+    if (sub == 0 && live) {
         T *orow = (T *)p.out + b * p.osb + h * p.osh + (int64_t)n * p.osn + li * VEC;
 #pragma unroll
         for (int e = 0; e < VEC; ++e) Cvt<T>::store(orow + e, acc[e]);
@@ -344,7 +352,9 @@ apply_fwd16_kernel(ApplyP p) {
     const char *kb = (const char *)((const T *)p.k + b * p.ksb + g * p.ksh);
     const char *vb = (const char *)((const T *)p.v + b * p.vsb + g * p.vsh);
     const uint32_t krb = (uint32_t)(p.ksn * 2), vrb = (uint32_t)(p.vsn * 2);   // row bytes < 2^24
-    const uint32_t lio = (uint32_t)li * 16u;
+    // lanes whose 8 elements lie past the head dim hold zeros and store nothing
+    const bool live = li * 8 < p.d;
+    const uint32_t lio = live ? (uint32_t)li * 16u : 0u;
     const int64_t *nb = p.nb ? p.nb + row * p.K : nullptr;
     const uint8_t *va = p.valid ? p.valid + row * p.K : nullptr;
 
@@ -357,7 +367,8 @@ apply_fwd16_kernel(ApplyP p) {
         }
         ix[j] = x;
     }
-    const uint4 q4 = *reinterpret_cast<const uint4 *>(qrow + li * 8);
+    uint4 q4 = *reinterpret_cast<const uint4 *>(qrow + (live ? li * 8 : 0));
+    if (!live) q4 = make_uint4(0, 0, 0, 0);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -456,7 +467,7 @@ apply_fwd16_kernel(ApplyP p) {
     for (int o = LPR; o < SSA_WAVE; o <<= 1)
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[e] += __shfl_xor(acc[e], o, SSA_WAVE);
-    if (sub == 0) {
+    if (sub == 0 && live) {
         T *orow = (T *)p.out + b * p.osb + h * p.osh + (int64_t)n * p.osn + li * 8;
         uint4 o4;
         o4.x = Dot2<T>::bits(acc[0]) | (Dot2<T>::bits(acc[1]) << 16);
@@ -495,12 +506,19 @@ apply_bwd_kernel(ApplyP p) {
     const T *vb = (const T *)p.v + b * p.vsb + g * p.vsh;
     const int64_t *nb = p.nb + row * p.K;
     const uint8_t *va = p.valid ? p.valid + row * p.K : nullptr;
-    const float *dorow = p.dout + row * D + li * VEC;
+    // gradients are (rows, d) fp32; lanes past the head dim hold zeros and
+    // write nothing
+    const bool live = li * VEC < p.d;
+    const int lofs = live ? li * VEC : 0;
+    const float *dorow = p.dout + row * p.d + lofs;
 
     float qf[VEC], dof[VEC];
-    load_vec<T, VEC>(qrow + li * VEC, qf);
+    load_vec<T, VEC>(qrow + lofs, qf);
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) dof[e] = dorow[e];
+    for (int e = 0; e < VEC; ++e) {
+        dof[e] = live ? dorow[e] : 0.f;
+        qf[e] = live ? qf[e] : 0.f;
+    }
 
     for (int j0 = 0; j0 < p.K; j0 += RPI) {
         const int j = j0 + sub;
@@ -509,8 +527,8 @@ apply_bwd_kernel(ApplyP p) {
         if (j < p.K) { x = nb[j]; o = va ? (va[j] != 0) : true; }
         if (x < 0 || x >= p.M) { x = 0; o = false; }
         float kf[VEC], vf[VEC];
-        load_vec<T, VEC>(kb + x * p.ksn + li * VEC, kf);
-        load_vec<T, VEC>(vb + x * p.vsn + li * VEC, vf);
+        load_vec<T, VEC>(kb + x * p.ksn + lofs, kf);
+        load_vec<T, VEC>(vb + x * p.vsn + lofs, vf);
         float s = 0.f, dp = 0.f;
 #pragma unroll
         for (int e = 0; e < VEC; ++e) { s = fmaf(qf[e], kf[e], s); dp = fmaf(dof[e], vf[e], dp); }
@@ -560,22 +578,22 @@ apply_bwd_kernel(ApplyP p) {
         if (p.drop_p > 0.f) mask = (drop_uniform(p.seed, row, j) < p.drop_p) ? 0.f : drop_scale_of<T>(p);
         const float pw = pj * mask;
         float kf[VEC];
-        load_vec<T, VEC>(kb + x * p.ksn + li * VEC, kf);
-        float *dkr = p.dk + (((int64_t)b * p.Hkv + g) * p.M + x) * D + li * VEC;
-        float *dvr = p.dv + (((int64_t)b * p.Hkv + g) * p.M + x) * D + li * VEC;
+        load_vec<T, VEC>(kb + x * p.ksn + lofs, kf);
+        float *dkr = p.dk + (((int64_t)b * p.Hkv + g) * p.M + x) * p.d + lofs;
+        float *dvr = p.dv + (((int64_t)b * p.Hkv + g) * p.M + x) * p.d + lofs;
 #pragma unroll
         for (int e = 0; e < VEC; ++e) {
             dqa[e] = fmaf(draw, kf[e], dqa[e]);
-            if (draw != 0.f) unsafeAtomicAdd(dkr + e, draw * qf[e]);
-            if (pw != 0.f) unsafeAtomicAdd(dvr + e, pw * dof[e]);
+            if (live && draw != 0.f) unsafeAtomicAdd(dkr + e, draw * qf[e]);
+            if (live && pw != 0.f) unsafeAtomicAdd(dvr + e, pw * dof[e]);
         }
     }
 #pragma unroll
     for (int o = LPR; o < SSA_WAVE; o <<= 1)
 #pragma unroll
         for (int e = 0; e < VEC; ++e) dqa[e] += __shfl_xor(dqa[e], o, SSA_WAVE);
-    if (sub == 0) {
-        float *dqr = p.dq + row * D + li * VEC;
+    if (sub == 0 && live) {
+        float *dqr = p.dq + row * p.d + lofs;
 #pragma unroll
         for (int e = 0; e < VEC; ++e) dqr[e] = dqa[e];
     }
@@ -637,7 +655,12 @@ int launch_apply(const ApplyP &p, hipStream_t st, bool bwd) {
 
 template <typename T>
 int dispatch_d(const ApplyP &p, int d, hipStream_t st, bool bwd) {
-    switch (d) {
+    if (!ssa_head_dim_ok(d, std::is_same<T, float>::value ? SSA_F32 : SSA_BF16)) {
+        ssa_set_error("sparse_gather_attention: head dim %d unsupported (4..256: a power of two "
+                      "or a multiple of %d)", d, std::is_same<T, float>::value ? 4 : 8);
+        return SSA_E_UNSUP;
+    }
+    switch (ssa_pow2_instance(d)) {
         case 4: return launch_apply<T, 4>(p, st, bwd);
         case 8: return launch_apply<T, 8>(p, st, bwd);
         case 16: return launch_apply<T, 16>(p, st, bwd);
@@ -675,6 +698,7 @@ int apply_common(const ssa_apply_args *a, ApplyP &p) {
     p = ApplyP{};
     p.B = a->B; p.Hq = a->Hq; p.Hkv = a->Hkv; p.N = a->N; p.M = a->M; p.K = a->K;
     p.rep = a->Hq / a->Hkv;
+    p.d = a->d;
     p.q = a->q.ptr; p.k = a->k.ptr; p.v = a->v.ptr;
     p.qsb = a->q.sb; p.qsh = a->q.sh; p.qsn = a->q.sn;
     p.ksb = a->k.sb; p.ksh = a->k.sh; p.ksn = a->k.sn;

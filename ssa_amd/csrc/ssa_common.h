@@ -210,6 +210,21 @@ __device__ __forceinline__ float key_score(uint32_t k) {
 
 __host__ __device__ __forceinline__ int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Head dims the kernels take: 4..256, whole vectors of the element type (8
+// elements of a 16-bit type, 4 of fp32: rows are read in 16-byte pieces) or a
+// power of two.  A kernel instance for head dim D serves every d <= D: lanes
+// and elements past d read zeros and store nothing.
+inline bool ssa_head_dim_ok(int d, int dtype) {
+    const int vec = dtype == SSA_F32 ? 4 : 8;
+    return d >= 4 && d <= 256 && ((d & (d - 1)) == 0 || d % vec == 0);
+}
+// the smallest power-of-two instance (4..256) that covers d
+inline int ssa_pow2_instance(int d) {
+    int D = 4;
+    while (D < d) D <<= 1;
+    return D;
+}
+
 // XCD-aware block order: the dispatcher sends workgroup i to XCD i % 8.  Map
 // physical block id -> logical id so that each XCD walks one contiguous range
 // of logical blocks (consecutive logical blocks share K/V rows in L2).

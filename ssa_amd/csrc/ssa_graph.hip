@@ -180,8 +180,9 @@ __device__ __forceinline__ void write_ids(const float *pr, int P, int Tp, uint16
 // element k = l / 16 of the step.  The reduction over the head dim is split so
 // that lane group g = l / 16 walks the contiguous quarter [g*d/4, (g+1)*d/4):
 // every lane loads its quarter row once with wide loads.  The block stages all
-// R*P planes in LDS once (fp32, row stride d+1); each wavefront then takes
-// HASH_TILES tiles of 16 rows against them.
+// R*P planes in LDS once (fp32, row stride D+1); each wavefront then takes
+// HASH_TILES tiles of 16 rows against them.  D is the instance's head dim; the
+// rows' own d <= D: elements past d are zero in the rows and the planes.
 constexpr int HASH_TILES = 1;
 template <typename T, int D>
 __global__ void __launch_bounds__(256) hash_mfma_kernel(HashP p) {
@@ -198,8 +199,8 @@ __global__ void __launch_bounds__(256) hash_mfma_kernel(HashP p) {
     // plane j (round j / P, hash j % P) is staged by wave j % 4, D / 64 elements a lane
     for (int j = wid; j < NT * 16; j += 4) {
         const bool real = j < NP;
-        const float *src = p.planes + (real ? ((int64_t)(j / p.P) * p.maxP + (j % p.P)) * D : 0);
-        for (int e = lane; e < D; e += SSA_WAVE) W[j * (D + 1) + e] = real ? src[e] : 0.f;
+        const float *src = p.planes + (real ? ((int64_t)(j / p.P) * p.maxP + (j % p.P)) * p.d : 0);
+        for (int e = lane; e < D; e += SSA_WAVE) W[j * (D + 1) + e] = (real && e < p.d) ? src[e] : 0.f;
     }
     __syncthreads();
     const int li = lane % 16, lg = lane / 16;
@@ -214,23 +215,26 @@ __global__ void __launch_bounds__(256) hash_mfma_kernel(HashP p) {
             const int64_t bh = row / p.L;
             const T *x = (const T *)p.x + (bh / p.nh) * p.sb + (bh % p.nh) * p.sh + (int64_t)i * p.sn +
                          lg * DQ;
+            const int dq = p.d - lg * DQ;             // this quarter's elements below d
             constexpr int PER16 = 16 / (int)sizeof(T);
             if constexpr (DQ % PER16 == 0) {
                 if (p.vec16) {
+                    // d fills whole 16-byte pieces (a multiple of PER16)
 #pragma unroll
                     for (int e0 = 0; e0 < DQ; e0 += PER16) {
-                        const uint4 w = *reinterpret_cast<const uint4 *>(x + e0);
+                        uint4 w = make_uint4(0, 0, 0, 0);
+                        if (e0 < dq) w = *reinterpret_cast<const uint4 *>(x + e0);
                         const T *tv = reinterpret_cast<const T *>(&w);
 #pragma unroll
                         for (int e = 0; e < PER16; ++e) xs[e0 + e] = to_f32(tv[e]);
                     }
                 } else {
 #pragma unroll
-                    for (int e = 0; e < DQ; ++e) xs[e] = to_f32(x[e]);
+                    for (int e = 0; e < DQ; ++e) xs[e] = e < dq ? to_f32(x[e]) : 0.f;
                 }
             } else {
 #pragma unroll
-                for (int e = 0; e < DQ; ++e) xs[e] = to_f32(x[e]);
+                for (int e = 0; e < DQ; ++e) xs[e] = e < dq ? to_f32(x[e]) : 0.f;
             }
         } else {
 #pragma unroll
@@ -566,6 +570,7 @@ struct RsP {
     const float *aux;  // per query row: NA floats, the last the query's code scale
     int NA;
     int N, M, R, NS, NB, C, Hq, Hkv, rep, bh0, causal;
+    int d;             // head dim (<= the instance's D; elements past it are zero)
     int Cs;            // score row stride (a multiple of 64)
     int k32;           // byte offsets of the K rows of a (batch, kv head) fit 32 bits
     int64_t Call;
@@ -629,7 +634,7 @@ __global__ void __launch_bounds__(256) rescore_kernel(RsP p) {
     const int nv = rs_tile_cutoff(sd, tl.nva, nidx, qc, p.causal);
     for (int x = tid; x < TQ * D; x += 256) {
         const int i = x / D, c = x % D;
-        Qs[i * LD + c] = i < qc ? to_f32(qbase[(int64_t)nidx[i] * p.qsn + c]) : 0.f;
+        Qs[i * LD + c] = (i < qc && c < p.d) ? to_f32(qbase[(int64_t)nidx[i] * p.qsn + c]) : 0.f;
     }
     const int ty = tid / 16, tx = tid % 16;
     for (int c0 = 0; c0 < nv; c0 += TC) {
@@ -638,7 +643,8 @@ __global__ void __launch_bounds__(256) rescore_kernel(RsP p) {
         __syncthreads();
         for (int x = tid; x < TC * D; x += 256) {
             const int j = x / D, c = x % D;
-            Ks[j * LD + c] = (c0 + j < nv) ? to_f32(kbase[(int64_t)kidx[j] * p.ksn + c]) : 0.f;
+            Ks[j * LD + c] = (c0 + j < nv && c < p.d) ? to_f32(kbase[(int64_t)kidx[j] * p.ksn + c])
+                                                       : 0.f;
         }
         __syncthreads();
         float acc[4][4];
@@ -646,7 +652,8 @@ __global__ void __launch_bounds__(256) rescore_kernel(RsP p) {
         for (int a = 0; a < 4; ++a)
 #pragma unroll
             for (int bb = 0; bb < 4; ++bb) acc[a][bb] = 0.f;
-        for (int c = 0; c < D; ++c) {
+        // one fmaf chain over the head dim, as the select's exact keys run it
+        for (int c = 0; c < p.d; ++c) {
             float qa[4], kb[4];
 #pragma unroll
             for (int a = 0; a < 4; ++a) qa[a] = Qs[(ty * 4 + a) * LD + c];
@@ -759,8 +766,8 @@ __global__ void __launch_bounds__(256) rescore_mfma_kernel(RsP p) {
 #pragma unroll
         for (int s = 0; s < KS; ++s) {
             const int e0 = 32 * s + 8 * lg;
-            qf[s] = (qok && (D % 32 == 0 || e0 < D)) ? __builtin_bit_cast(V, *reinterpret_cast<const uint4 *>(src + e0))
-                                    : __builtin_bit_cast(V, make_uint4(0, 0, 0, 0));
+            qf[s] = (qok && e0 < p.d) ? __builtin_bit_cast(V, *reinterpret_cast<const uint4 *>(src + e0))
+                                      : __builtin_bit_cast(V, make_uint4(0, 0, 0, 0));
         }
     }
     const bool active = 16 * wid < qc;
@@ -785,8 +792,10 @@ __global__ void __launch_bounds__(256) rescore_mfma_kernel(RsP p) {
         const int cr = (C0) + row;  /* the read is clamped in range; the select drops it */ \
         const int rid = prl[max(min(cr, nv - 1), 0)];                                        \
         const int id = (x < 64 * SEGS && cr < nv) ? rid : 0;                                 \
+        /* segments past the head dim read segment 0 (never multiplied) */                  \
+        const uint32_t sg = seg * 8 < p.d ? (uint32_t)seg : 0u;                              \
         sa[i] = *reinterpret_cast<const u32x4 *>((const char *)kbase +                       \
-                                                 (__umul24((uint32_t)id, rowb) + seg * 16u)); \
+                                                 (__umul24((uint32_t)id, rowb) + sg * 16u)); \
     }
 #define RS_COMMIT(BUF)                                                                       \
     _Pragma("unroll") for (int i = 0; i < PER; ++i) {                                        \
@@ -834,10 +843,10 @@ __global__ void __launch_bounds__(256) rescore_mfma_kernel(RsP p) {
                 const int e0 = 32 * s + 8 * lg;
 #pragma unroll
                 for (int ct = 0; ct < 4; ++ct)
-                    kf[ct] = (D % 32 == 0 || e0 < D) ? __builtin_bit_cast(
+                    kf[ct] = e0 < p.d ? __builtin_bit_cast(
                                           V, *reinterpret_cast<const uint4 *>(
                                                  kl + (ct * 16 + li) * RB + e0 * 2))
-                                    : __builtin_bit_cast(V, make_uint4(0, 0, 0, 0));
+                                      : __builtin_bit_cast(V, make_uint4(0, 0, 0, 0));
             };
             // fragments two k steps deep: the reads of step s + 2 overlap the
             // products of step s
@@ -1119,9 +1128,11 @@ __global__ void __launch_bounds__(256) aux_mfma_kernel(AuxP p) {
     const int b = bh / p.Hq, h = bh % p.Hq, g = h / p.rep;
     const T *qbase = (const T *)p.q + b * p.qsb + h * p.qsh;
     const T *kbase = (const T *)p.k + b * p.ksb + g * p.ksh;
+    // k steps of 32 over the head dim d <= D, elements past d zero (as the
+    // rescore and the select's exact keys take them)
     auto frag = [&](const T *src, bool ok, int s) {
         const int e0 = 32 * s + 8 * lg;
-        if (ok && (D % 32 == 0 || e0 < D)) return __builtin_bit_cast(V, *reinterpret_cast<const uint4 *>(src + e0));
+        if (ok && e0 < p.d) return __builtin_bit_cast(V, *reinterpret_cast<const uint4 *>(src + e0));
         return __builtin_bit_cast(V, make_uint4(0, 0, 0, 0));
     };
     const int nq = n0 + li;
@@ -1189,14 +1200,14 @@ __global__ void __launch_bounds__(256) aux_valu_kernel(AuxP p) {
     const T *qr = (const T *)p.q + b * p.qsb + h * p.qsh + (int64_t)n * p.qsn;
     if (a == p.NA - 1) {               // the query's code scale
         float q2 = 0.f;
-        for (int c = 0; c < D; ++c) q2 = fmaf(to_f32(qr[c]), to_f32(qr[c]), q2);
+        for (int c = 0; c < p.d; ++c) q2 = fmaf(to_f32(qr[c]), to_f32(qr[c]), q2);
         p.out[idx] = code_scale(q2, __uint_as_float(p.knorm[b * p.Hkv + g]));
         return;
     }
     const int key = a == 0 ? n : (a - 1 < p.G ? (int)p.glob[a - 1] : 0);
     const T *kr = (const T *)p.k + b * p.ksb + g * p.ksh + (int64_t)key * p.ksn;
     float acc = 0.f;
-    for (int c = 0; c < D; ++c) acc = fmaf(to_f32(qr[c]), to_f32(kr[c]), acc);
+    for (int c = 0; c < p.d; ++c) acc = fmaf(to_f32(qr[c]), to_f32(kr[c]), acc);
     p.out[idx] = acc;
 }
 
@@ -2489,7 +2500,10 @@ topk_replay_kernel(SelP p, int chunk, int W, uint32_t *gscr) {
 }
 
 // ------------------------------------------------------------------ host side
-int supported_d(int d) { return d >= 4 && d <= 256 && (d & (d - 1)) == 0; }
+// Instance of the matrix-core rescore / aux kernels for head dim d (8..128,
+// whole 8-element pieces): k steps of 32, so ceil(d / 32) steps as the select's
+// exact keys take them
+int mfma_instance(int d) { return d <= 8 ? 8 : d <= 16 ? 16 : (d + 31) / 32 * 32; }
 
 // Whether RP_WAVES replayed rows of W = kk + chunk slots fit one workgroup's LDS.
 bool replay_fits_lds(int W, int words) {
@@ -2579,8 +2593,9 @@ int make_dims(const ssa_graph_args *a, Dims &D, bool need_q = true, int64_t ws_c
     SSA_CHECK_ARG(a->q.dtype == a->k.dtype && a->q.dtype >= 0 && a->q.dtype <= 2,
                   "build_graph: q/k dtype");
     SSA_CHECK_ARG(a->G == 0 || a->glob, "build_graph: glob is null");
-    if (!supported_d(a->d)) {
-        ssa_set_error("build_graph: head dim %d unsupported (4..256, power of 2)", a->d);
+    if (!ssa_head_dim_ok(a->d, a->q.dtype)) {
+        ssa_set_error("build_graph: head dim %d unsupported (4..256: a power of two or a multiple "
+                      "of %d)", a->d, a->q.dtype == SSA_F32 ? 4 : 8);
         return SSA_E_UNSUP;
     }
     if (!ssa_sort_supported(a->M)) {
@@ -2693,7 +2708,7 @@ int launch_hash_one(const HashP &hp, int d, hipStream_t st) {
         SSA_CHECK_LAUNCH();
         return SSA_OK;
     }
-    switch (d) {
+    switch (ssa_pow2_instance(d)) {
         case 4: return launch_hash_mfma<T, 4>(hp, st);
         case 8: return launch_hash_mfma<T, 8>(hp, st);
         case 16: return launch_hash_mfma<T, 16>(hp, st);
@@ -2789,16 +2804,17 @@ template <typename T>
 int rescore_dispatch(int d, const RsP &rp, int64_t grid, hipStream_t st) {
     if constexpr (!std::is_same<T, float>::value) {
         if (rescore_uses_mfma<T>(d, rp)) {
-            switch (d) {
+            switch (mfma_instance(d)) {
                 case 8: return launch_rescore_mfma<T, 8>(rp, grid, st);
                 case 16: return launch_rescore_mfma<T, 16>(rp, grid, st);
                 case 32: return launch_rescore_mfma<T, 32>(rp, grid, st);
                 case 64: return launch_rescore_mfma<T, 64>(rp, grid, st);
+                case 96: return launch_rescore_mfma<T, 96>(rp, grid, st);
                 case 128: return launch_rescore_mfma<T, 128>(rp, grid, st);
             }
         }
     }
-    switch (d) {
+    switch (ssa_pow2_instance(d)) {
         case 4: return launch_rescore<T, 4>(rp, grid, st);
         case 8: return launch_rescore<T, 8>(rp, grid, st);
         case 16: return launch_rescore<T, 16>(rp, grid, st);
@@ -2838,9 +2854,9 @@ int aux_dispatch(int d, bool mfma, const AuxP &ap, hipStream_t st) {
             const dim3 grid((unsigned)ceil_div(waves, 4));
 #define SSA_AUX_MFMA(DD) \
     case DD: hipLaunchKernelGGL((aux_mfma_kernel<T, DD>), grid, dim3(256), 0, st, ap); break;
-            switch (d) {
+            switch (mfma_instance(d)) {
                 SSA_AUX_MFMA(8) SSA_AUX_MFMA(16) SSA_AUX_MFMA(32) SSA_AUX_MFMA(64)
-                SSA_AUX_MFMA(128)
+                SSA_AUX_MFMA(96) SSA_AUX_MFMA(128)
                 default: ssa_set_error("aux scores: head dim %d", d); return SSA_E_UNSUP;
             }
 #undef SSA_AUX_MFMA
@@ -2851,7 +2867,7 @@ int aux_dispatch(int d, bool mfma, const AuxP &ap, hipStream_t st) {
     const dim3 grid((unsigned)ceil_div(rows * ap.NA, 256));
 #define SSA_AUX_VALU(DD) \
     case DD: hipLaunchKernelGGL((aux_valu_kernel<T, DD>), grid, dim3(256), 0, st, ap); break;
-    switch (d) {
+    switch (ssa_pow2_instance(d)) {
         SSA_AUX_VALU(4) SSA_AUX_VALU(8) SSA_AUX_VALU(16) SSA_AUX_VALU(32) SSA_AUX_VALU(64)
         SSA_AUX_VALU(128) SSA_AUX_VALU(256)
         default: ssa_set_error("aux scores: head dim %d", d); return SSA_E_UNSUP;
@@ -3019,6 +3035,7 @@ int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char 
         rp.Hq = D.Hq; rp.Hkv = D.Hkv; rp.rep = D.rep; rp.bh0 = (int)bh0; rp.Call = D.Call;
         rp.causal = a->causal ? 1 : 0;
         rp.Cs = D.Cs;
+        rp.d = D.d;
         {
             const int64_t el = a->q.dtype == SSA_F32 ? 4 : 2;
             rp.k32 = (rp.ksn * el < ((int64_t)1 << 24) &&

@@ -188,3 +188,20 @@ def test_apply_matching_shapes_reach_the_device_check():
     q, k, v, nb, va = _apply_operands()
     with pytest.raises(RuntimeError, match="ROCm devices only"):
         sparse_gather_attention(q, k, v, nb, 0.25, valid=va)
+
+
+@pytest.mark.parametrize("d,dtype,ok", [(96, 1, True), (80, 1, True), (112, 2, True), (48, 0, True),
+                                        (12, 0, True), (12, 1, False), (100, 1, False),
+                                        (264, 0, False), (2, 0, False)])
+def test_head_dim_rule(d, dtype, ok):
+    """Head dims 4..256 that are powers of two or whole 16-byte pieces of the
+    element type are taken; others are refused with a message, before any
+    launch."""
+    from ssa_amd import _lib
+    a, _ = _full_args(256, 64, d=d)
+    a.q.dtype = a.k.dtype = dtype
+    wsb = _lib.lib().ssa_graph_workspace_bytes(ctypes.byref(a))
+    if ok:
+        assert wsb > 0, _lib.lib().ssa_last_error()
+    else:
+        assert wsb < 0 and b"head dim" in _lib.lib().ssa_last_error()

@@ -229,6 +229,16 @@ def test_bf16_mqa_n32768_probes_explicit_globals():
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_head_dim_96_gqa_n2048(dtype):
+    """A head dim that is not a power of two: d_model 768 over 8 query heads
+    (d_head 96) and 2 kv heads."""
+    cfg = dict(d_model=768, num_heads=8, num_kv_heads=2, num_neighbors=64, window_size=8,
+               num_global_tokens=2, num_hash_rounds=4, max_num_hashes=12, lsh_num_probes=1,
+               causal=True)
+    _run_self(cfg, 1, 2048, dtype, 0, 1.0, False, q_step=16, heads=[0, 3, 5, 7])
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_cross_attention_b4_2048_over_512(dtype):
     cfg = dict(d_model=1024, num_heads=16, num_neighbors=64, window_size=4, num_global_tokens=2,
                num_hash_rounds=6, max_num_hashes=12, lsh_num_probes=0, causal=False)

@@ -74,6 +74,12 @@ GRAPH_CASES = [
     ("oversize_window", 1, 2, 2, 48, 48, 16, 2, 3, 0, 16, 16, 2, False, False),
     ("mid_r8", 1, 2, 2, 512, 512, 64, 8, 12, 0, 64, 8, 2, True, False),
     ("big_bucket_bits", 1, 2, 1, 1024, 1024, 32, 2, 12, 1, 40, 2, 2, False, False),
+    # head dims that are not powers of two (the next instance's kernels, the
+    # elements past d zero)
+    ("head_dim_96", 1, 4, 2, 160, 160, 96, 3, 4, 1, 32, 4, 2, True, False),
+    ("head_dim_80_cross", 2, 2, 1, 60, 100, 80, 2, 4, 1, 24, 4, 2, False, True),
+    ("head_dim_112", 1, 2, 2, 128, 128, 112, 2, 4, 0, 24, 3, 2, True, False),
+    ("head_dim_48", 1, 2, 1, 96, 96, 48, 2, 3, 0, 20, 2, 1, False, False),
 ]
 
 
@@ -168,14 +174,18 @@ def test_lsh_builder_exact_tier_huge_k_replay_outside_lds():
     np.testing.assert_array_equal(got.cpu().numpy().reshape(B * H, N, -1), ref["idx"])
 
 
-def test_graph_bf16_inputs_exact_tier():
-    """bf16 q/k holding small integers are exact: same graph as fp32."""
-    case = GRAPH_CASES[1]
+@pytest.mark.parametrize("case", [GRAPH_CASES[1]] + [c for c in GRAPH_CASES
+                                                    if c[0].startswith("head_dim")],
+                         ids=lambda c: c[0])
+def test_graph_bf16_inputs_exact_tier(case):
+    """bf16 q/k holding small integers are exact: same graph as fp32 (the
+    matrix-core rescore, aux and exact-key paths)."""
     attn, got, got_v, ref, (B, H, N, M, K, w, cross, causal, glob) = _graph_case(
         case, 5, dtype=torch.bfloat16)
-    win = attn.win_builder(N, M, "cpu").numpy()
-    rnb, rva = oracle.merge(win, glob.numpy(), ref["idx"], has_self=True, total_k=K)
+    win = (np.zeros((N, 0), np.int64) if cross else attn.win_builder(N, M, "cpu").numpy())
+    rnb, rva = oracle.merge(win, glob.numpy(), ref["idx"], has_self=not cross, total_k=K)
     np.testing.assert_array_equal(got.cpu().numpy().reshape(B * H, N, -1), rnb)
+    np.testing.assert_array_equal(got_v.cpu().numpy().reshape(B * H, N, -1), rva)
 
 
 # ------------------------------------------------------------------ graph, reference vectors
@@ -224,6 +234,11 @@ APPLY_CASES = [
     (1, 2, 1, 10, 40, 256, 24),
     (1, 4, 2, 12, 20, 4, 10),
     (1, 1, 1, 3, 500, 128, 2500),
+    (1, 4, 2, 40, 50, 96, 24),
+    (1, 2, 1, 30, 60, 80, 33),
+    (1, 2, 2, 20, 30, 112, 16),
+    (2, 2, 2, 9, 15, 48, 12),
+    (1, 2, 1, 11, 40, 200, 20),
 ]
 
 
@@ -274,10 +289,26 @@ def test_apply_expanded_kv_equals_grouped_kv():
     assert torch.equal(o1, o2)
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_apply_backward_matches_autograd_reference(dtype):
+def test_apply_fp32_head_dim_12_matches_oracle():
+    """fp32 takes head dims in whole 4-element pieces (12: the 16 instance)."""
     from ssa_amd import sparse_gather_attention
-    case = (1, 4, 2, 24, 30, 32, 16)
+    case = (1, 2, 1, 17, 25, 12, 9)
+    B, H, nkv, N, M, d, K = case
+    q, k, v, nb, va = _apply_inputs(case, torch.float32, 2)
+    with torch.no_grad():
+        out = sparse_gather_attention(q.to(DEV), k.to(DEV), v.to(DEV), nb.to(DEV), d ** -0.5,
+                                      valid=va.to(DEV))
+    ref = oracle.apply(q.reshape(B * H, N, d).numpy(), k.reshape(B * nkv, M, d).numpy(),
+                       v.reshape(B * nkv, M, d).numpy(), nb.reshape(B * H, N, K).numpy(),
+                       va.reshape(B * H, N, K).numpy(), kv_rep=H // nkv, scale=d ** -0.5, mode=0)
+    assert row_rel_err(out.cpu().numpy().reshape(B * H, N, d), ref) <= REL[torch.float32]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("case", [(1, 4, 2, 24, 30, 32, 16), (1, 4, 2, 24, 30, 96, 16)],
+                         ids=["d32", "d96"])
+def test_apply_backward_matches_autograd_reference(dtype, case):
+    from ssa_amd import sparse_gather_attention
     B, H, nkv, N, M, d, K = case
     q, k, v, nb, va = _apply_inputs(case, dtype, 5)
     g = torch.Generator().manual_seed(9)
