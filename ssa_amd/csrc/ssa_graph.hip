@@ -1415,9 +1415,10 @@ __device__ __forceinline__ void wave_compiler_fence() {
 constexpr int SEL_CAP = 384;   // keys kept in LDS for the exact threshold search
 
 // Per-wave LDS of the select kernel, in 32-bit words:
-//   tab   [4*nch]     per 64-member chunk of a sorted list prefix: index of its
-//                     first member id, lane mask (low), score slot of its first
-//                     member, lane mask (high)
+//   lch   [4*nlists]  per list, for its 64-member chunks: index of its first
+//                     member id, score slot of its first member, members below
+//                     the query (the cutoff), index of its first chunk in the
+//                     row's chunk sequence
 //   lst   [4*nlists]  per list: bucket start, size, offset of its kv-head/round
 //                     row, overflow filler key (after the filler rule: the key
 //                     if it is marked seen, else -1)
@@ -1433,10 +1434,8 @@ constexpr int SEL_PIPE = 2;            // chunks per group in pass 1
 __host__ __device__ inline int sel_buf_words(int words) {
     return 2 * SEL_BUF > words ? 2 * SEL_BUF : words;
 }
-__host__ __device__ inline int sel_tab_entries(int nch) { return nch + 2 * SEL_PIPE; }
-__host__ __device__ inline int sel_lds_words(int nch, int words, int kk, bool lsh, int nlists) {
-    return (4 * sel_tab_entries(nch) + 4 * nlists + words + sel_buf_words(words) +
-            (lsh ? 3 * kk : 0) + 1) & ~1;
+__host__ __device__ inline int sel_lds_words(int words, int kk, bool lsh, int nlists) {
+    return (8 * nlists + words + sel_buf_words(words) + (lsh ? 3 * kk : 0) + 1) & ~1;
 }
 
 // Dedup one chunk of members (lanes in Min) against the seen bitmap, count the
@@ -1687,9 +1686,8 @@ select_kernel(SelP p) {
     if (rloc >= p.rows) return;
     const int lane = lane_id();
     const int nl = p.nlists;
-    const int nchmax = nl * p.CPL;
-    int4 *tab = (int4 *)(sel_smem + (int64_t)wid * sel_lds_words(nchmax, p.words, p.kk, LSH_MODE, nl));
-    int4 *lst = tab + sel_tab_entries(nchmax);
+    int4 *lch = (int4 *)(sel_smem + (int64_t)wid * sel_lds_words(p.words, p.kk, LSH_MODE, nl));
+    int4 *lst = lch + nl;
     uint32_t *bm = (uint32_t *)(lst + nl);
     uint32_t *ckey = bm + p.words;
     uint32_t *cval = ckey + SEL_BUF;
@@ -1720,7 +1718,7 @@ select_kernel(SelP p) {
     const int ng = min(p.G + 1, SSA_WAVE);
     for (int w = lane; w < p.words; w += SSA_WAVE) bm[w] = 0u;
 
-    // ---- chunk table of the sorted prefixes, one lane per list
+    // ---- per-list chunk data of the sorted prefixes, one lane per list
     int nch = 0;
     bool any_empty = false;            // some bucket is empty: glob ++ 0 (same for all)
     bool nkeep = false;                // the query's own key is kept
@@ -1741,11 +1739,7 @@ select_kernel(SelP p) {
         const int nc = (in && sz > 0) ? (cutoff + SSA_WAVE - 1) / SSA_WAVE : 0;
         int ncs;
         const int at = nch + wave_excl_scan(nc, ncs);
-        for (int k = 0; k < nc; ++k) {
-            const int c0 = k * SSA_WAVE;
-            const uint64_t m = lanes_mask(cutoff - c0);
-            tab[at + k] = make_int4(ct.x + c0, (int)(uint32_t)m, so + c0, (int)(uint32_t)(m >> 32));
-        }
+        if (in) lch[list] = make_int4(ct.x, so, cutoff, at);
         nch += ncs;
         any_empty = any_empty || wave_ballot(in && sz == 0) != 0ull;
         if (!nfound) {
@@ -1759,7 +1753,6 @@ select_kernel(SelP p) {
         }
     }
     nch = __builtin_amdgcn_readfirstlane(nch);
-    if (lane < 2 * SEL_PIPE) tab[nch + lane] = make_int4(0, 0, 0, 0);   // empty tail chunks
     // glob ++ 0 (:711-737): ids and score keys, lane j holding entry j
     int greg_id = 0;
     uint32_t greg_sc = 0u, greg_c = 0u;
@@ -1816,6 +1809,26 @@ select_kernel(SelP p) {
         wave_lds_sync();
     }
 
+    // Descriptor of chunk dwin + lane: index of its first member id, lane mask
+    // (low), score slot of its first member, lane mask (high); zero past the
+    // last chunk.  Its list is the last one whose first chunk is at or before
+    // it (lists without chunks share the next list's first chunk index).
+    const int lstep = nl > 1 ? 1 << (31 - __clz(nl - 1)) : 0;
+    auto desc_window = [&](int dwin) {
+        const int ci = dwin + lane;
+        int4 d = make_int4(0, 0, 0, 0);
+        if (ci < nch) {
+            int L = 0;
+            for (int step = lstep; step > 0; step >>= 1)
+                if (L + step < nl && lch[L + step].w <= ci) L += step;
+            const int4 e = lch[L];
+            const int c0 = (ci - e.w) * SSA_WAVE;
+            const uint64_t m = lanes_mask(e.z - c0);
+            d = make_int4(e.x + c0, (int)(uint32_t)m, e.y + c0, (int)(uint32_t)(m >> 32));
+        }
+        return d;
+    };
+
     // ---- pass 1: dedup, and the kept keys >= lo into LDS.  lo is a lower
     // bound of the final threshold: whenever the buffer nears its capacity, lo
     // is raised to (a 16-bit floor of) the kk-th largest key in the buffer --
@@ -1856,15 +1869,14 @@ select_kernel(SelP p) {
     uint32_t sA[PIPE], sB[PIPE];
     // descriptors of 64 chunks at a time, lane j holding chunk (window + j);
     // a chunk's fields are read with a lane select, so no LDS read waits in
-    // front of each group's loads.  Chunks past the table read as empty.
+    // front of each group's loads.  Chunks past the last read as empty.
     int dwin = 0;
-    const int ntab = nch + 2 * SEL_PIPE;
-    int4 dl = lane < ntab ? tab[lane] : make_int4(0, 0, 0, 0);
+    int4 dl = desc_window(0);
     auto fetch = [&](int ci0, uint64_t (&m)[PIPE], int (&raw)[PIPE], uint32_t (&sk)[PIPE])
         __attribute__((always_inline)) {
         if ((ci0 & ~(SSA_WAVE - 1)) != dwin) {      // groups never straddle a window
             dwin = ci0 & ~(SSA_WAVE - 1);
-            dl = dwin + lane < ntab ? tab[dwin + lane] : make_int4(0, 0, 0, 0);
+            dl = desc_window(dwin);
         }
 #pragma unroll
         for (int u = 0; u < PIPE; ++u) {
@@ -1987,15 +1999,17 @@ select_kernel(SelP p) {
             if (CAUSAL) Min &= ~wave_ballot(greg_id == n);
             walk_chunk(Min, greg_id, kv_of(greg_c, greg_sc), 1 + lane);
         }
+        int4 dw = make_int4(0, 0, 0, 0);
         for (int ci = 0; ci < nch; ++ci) {
-            const int4 d = tab[ci];
-            const uint64_t Min = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane(d.w) << 32) |
-                                 (uint32_t)__builtin_amdgcn_readfirstlane(d.y);
+            const int j = ci & (SSA_WAVE - 1);
+            if (j == 0) dw = desc_window(ci);
+            const uint64_t Min = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(dw.w, j) << 32) |
+                                 (uint32_t)__builtin_amdgcn_readlane(dw.y, j);
             int v = 0;
             uint32_t c = 0u;
             if (in_mask(Min)) {
-                v = p.sid[__builtin_amdgcn_readfirstlane(d.x) + lane];
-                c = shead[(uint32_t)__builtin_amdgcn_readfirstlane(d.z) + lane];
+                v = p.sid[__builtin_amdgcn_readlane(dw.x, j) + lane];
+                c = shead[(uint32_t)__builtin_amdgcn_readlane(dw.z, j) + lane];
             }
             const bool xw = in_mask(Min) && (xm == 3 || (xm != 0 && c == pfx));
             uint32_t x = 0u;
@@ -3024,7 +3038,7 @@ int rescore_dispatch(int d, const RsP &rp, int64_t grid, hipStream_t st) {
 template <typename T, bool LSH, bool CAUSAL>
 int launch_select(const SelP &sp, hipStream_t st) {
     const size_t lds =
-        (size_t)SEL_WAVES * sel_lds_words(sp.nlists * sp.CPL, sp.words, sp.kk, LSH, sp.nlists) * 4;
+        (size_t)SEL_WAVES * sel_lds_words(sp.words, sp.kk, LSH, sp.nlists) * 4;
     if (lds > SSA_LDS_BYTES) {
         ssa_set_error("build_graph: select needs %zu bytes of LDS", lds);
         return SSA_E_UNSUP;
