@@ -1412,7 +1412,11 @@ __device__ __forceinline__ void wave_compiler_fence() {
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
 }
 
-constexpr int SEL_CAP = 384;   // keys kept in LDS for the exact threshold search
+// Keys kept in LDS for the exact threshold search (CAP): 384, or 512 when kk
+// is above SEL_CAP_LARGE_KK -- a buffer filled to CAP - 128 then holds more
+// than kk keys, so its lower bound is raised once or twice per row instead
+// of every few chunks (the larger buffer costs LDS, hence occupancy).
+constexpr int SEL_CAP_SMALL = 384, SEL_CAP_LARGE = 512, SEL_CAP_LARGE_KK = 160;
 
 // Per-wave LDS of the select kernel, in 32-bit words:
 //   lch   [4*nlists]  per list, for its 64-member chunks: index of its first
@@ -1423,25 +1427,25 @@ constexpr int SEL_CAP = 384;   // keys kept in LDS for the exact threshold searc
 //                     row, overflow filler key (after the filler rule: the key
 //                     if it is marked seen, else -1)
 //   bm    [words]     seen bitmap, later the merge bitmap
-//   ckey  [SEL_CAP+64] kept keys >= the lower bound; the last 64 entries take
+//   ckey  [CAP+64]    kept keys >= the lower bound; the last 64 entries take
 //                     the stores of lanes that append nothing
-//   cval  [SEL_CAP+64] key id of each compacted key (ckey and cval together span
+//   cval  [CAP+64]    key id of each compacted key (ckey and cval together span
 //                     at least `words`: the overflow path's second bitmap)
 //   LSH mode: ekey/eval/eslot [kk] the selected entries
-constexpr int SEL_BUF = SEL_CAP + 64;
 constexpr int SEL_PIPE = 2;            // chunks per group in pass 1
 // ckey + cval, which also hold the overflow path's second seen bitmap
-__host__ __device__ inline int sel_buf_words(int words) {
-    return 2 * SEL_BUF > words ? 2 * SEL_BUF : words;
+__host__ __device__ inline int sel_buf_words(int words, int cap) {
+    return 2 * (cap + 64) > words ? 2 * (cap + 64) : words;
 }
-__host__ __device__ inline int sel_lds_words(int words, int kk, bool lsh, int nlists) {
-    return (8 * nlists + words + sel_buf_words(words) + (lsh ? 3 * kk : 0) + 1) & ~1;
+__host__ __device__ inline int sel_lds_words(int words, int kk, bool lsh, int nlists, int cap) {
+    return (8 * nlists + words + sel_buf_words(words, cap) + (lsh ? 3 * kk : 0) + 1) & ~1;
 }
 
 // Dedup one chunk of members (lanes in Min) against the seen bitmap, count the
 // kept ones, and append the kept keys >= lo to the compacted buffer.  Every
 // lane stores: lanes that append nothing (or would pass the capacity) write
-// to their own slot past SEL_CAP, which is never read.
+// to their own slot past CAP, which is never read.
+template <int CAP>
 __device__ __forceinline__ void sel_absorb(uint32_t *bm, uint32_t *ckey, uint32_t *cval,
                                            uint64_t Min, int v, uint32_t kv, uint32_t lo,
                                            int &cnt, int &nkept) {
@@ -1453,7 +1457,7 @@ __device__ __forceinline__ void sel_absorb(uint32_t *bm, uint32_t *ckey, uint32_
     nkept += __popcll(km);
     const uint64_t am = km & wave_ballot(kv >= lo);
     const int pos = cnt + lanes_below(am);
-    const int dst = (in_mask(am) & (pos < SEL_CAP)) ? pos : SEL_CAP + lane;
+    const int dst = (in_mask(am) & (pos < CAP)) ? pos : CAP + lane;
     ckey[dst] = kv;
     cval[dst] = (uint32_t)v;
     cnt += __popcll(am);
@@ -1673,7 +1677,7 @@ __device__ __forceinline__ void sel_boundary(uint32_t *ckey, int ebits, uint32_t
 //          mode) are handed to the exact replay.  LSH mode writes the selected
 //          keys by descending score, FULL mode merges them with the window and
 //          the globals through a key bitmap.
-template <typename T, bool LSH_MODE, bool CAUSAL>
+template <typename T, bool LSH_MODE, bool CAUSAL, int CAP>
 // Registers are held to what 8 waves per SIMD allow (the kernel waits on
 // memory and LDS; the bench workload's 5 KB of LDS per wave fits 8 as well).
 __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) __attribute__((amdgpu_waves_per_eu(8, 8)))
@@ -1686,12 +1690,12 @@ select_kernel(SelP p) {
     if (rloc >= p.rows) return;
     const int lane = lane_id();
     const int nl = p.nlists;
-    int4 *lch = (int4 *)(sel_smem + (int64_t)wid * sel_lds_words(p.words, p.kk, LSH_MODE, nl));
+    int4 *lch = (int4 *)(sel_smem + (int64_t)wid * sel_lds_words(p.words, p.kk, LSH_MODE, nl, CAP));
     int4 *lst = lch + nl;
     uint32_t *bm = (uint32_t *)(lst + nl);
     uint32_t *ckey = bm + p.words;
-    uint32_t *cval = ckey + SEL_BUF;
-    uint32_t *ekey = ckey + sel_buf_words(p.words);
+    uint32_t *cval = ckey + CAP + 64;
+    uint32_t *ekey = ckey + sel_buf_words(p.words, CAP);
     uint32_t *eval = ekey + p.kk;
     uint32_t *eslot = eval + p.kk;
 
@@ -1835,7 +1839,7 @@ select_kernel(SelP p) {
     // a subset of the stream -- and the buffer is filtered in place.
     const int kk = p.kk;
     // checked once per group of SEL_PIPE chunks: a group adds at most 64 * SEL_PIPE keys
-    const int fill = SEL_CAP - SEL_PIPE * SSA_WAVE;
+    const int fill = CAP - SEL_PIPE * SSA_WAVE;
     int nkept = nkeep ? 1 : 0, cnt = 0;
     uint32_t lo = 0u;
     bool overflow = false;
@@ -1847,7 +1851,7 @@ select_kernel(SelP p) {
     if (any_empty) {                   // glob ++ 0; the query's own key is settled
         uint64_t Min = lanes_mask(min(p.C, ng));
         if (CAUSAL) Min &= ~wave_ballot(greg_id == n);
-        sel_absorb(bm, ckey, cval, Min, greg_id, greg_c << 16, lo, cnt, nkept);
+        sel_absorb<CAP>(bm, ckey, cval, Min, greg_id, greg_c << 16, lo, cnt, nkept);
     }
     // Chunks are processed PIPE at a time; the loads of the next group are
     // issued before the current group is deduplicated, so a wave always has
@@ -1906,23 +1910,23 @@ select_kernel(SelP p) {
             const uint64_t am = lm[u] & wave_ballot((old[u] & bit[u]) == 0u);
             nkept += __popcll(am);
             const int pos = cnt + lanes_below(am);
-            const int dst = (in_mask(am) & (pos < SEL_CAP)) ? pos : SEL_CAP + lane;
+            const int dst = (in_mask(am) & (pos < CAP)) ? pos : CAP + lane;
             ckey[dst] = csk[u];
             cval[dst] = (uint32_t)craw[u];
             cnt += __popcll(am);
         }
         if (cnt >= fill && cnt >= kk && !overflow) {
             wave_lds_sync();
-            const int m0 = cnt < SEL_CAP ? cnt : SEL_CAP;
-            uint32_t sv[SEL_CAP / SSA_WAVE];
+            const int m0 = cnt < CAP ? cnt : CAP;
+            uint32_t sv[CAP / SSA_WAVE];
 #pragma unroll
-            for (int i = 0; i < SEL_CAP / SSA_WAVE; ++i) sv[i] = ckey[lane + SSA_WAVE * i];
+            for (int i = 0; i < CAP / SSA_WAVE; ++i) sv[i] = ckey[lane + SSA_WAVE * i];
 #pragma unroll
-            for (int i = 0; i < SEL_CAP / SSA_WAVE; ++i)
+            for (int i = 0; i < CAP / SSA_WAVE; ++i)
                 sv[i] = lane + SSA_WAVE * i < m0 ? sv[i] : 0u;   // slots past the count are stale
             uint32_t mx = 0u, mn = 0xffffffffu;
 #pragma unroll
-            for (int i = 0; i < SEL_CAP / SSA_WAVE; ++i) {
+            for (int i = 0; i < CAP / SSA_WAVE; ++i) {
                 mx = sv[i] > mx ? sv[i] : mx;
                 mn = (sv[i] != 0u && sv[i] < mn) ? sv[i] : mn;
             }
@@ -1934,19 +1938,19 @@ select_kernel(SelP p) {
             const int hbit = base0 >= mx ? 16 : 31 - __clz(base0 ^ mx);
             const uint32_t nlo = kth_search(sv, kk, base0, mx, max(16, hbit - 5));
             lo = nlo > lo ? nlo : lo;
-            uint32_t sl[SEL_CAP / SSA_WAVE];
+            uint32_t sl[CAP / SSA_WAVE];
 #pragma unroll
-            for (int i = 0; i < SEL_CAP / SSA_WAVE; ++i) sl[i] = cval[lane + SSA_WAVE * i];
+            for (int i = 0; i < CAP / SSA_WAVE; ++i) sl[i] = cval[lane + SSA_WAVE * i];
             wave_lds_sync();
             int nc = 0;
 #pragma unroll
-            for (int i = 0; i < SEL_CAP / SSA_WAVE; ++i) {
+            for (int i = 0; i < CAP / SSA_WAVE; ++i) {
                 const bool t = sv[i] >= lo && sv[i] != 0u;
                 const uint64_t m = wave_ballot(t);
                 if (t) { ckey[nc + lanes_below(m)] = sv[i]; cval[nc + lanes_below(m)] = sl[i]; }
                 nc += __popcll(m);
             }
-            overflow = cnt > SEL_CAP;
+            overflow = cnt > CAP;
             cnt = nc;
             wave_lds_sync();
         }
@@ -1962,7 +1966,7 @@ select_kernel(SelP p) {
         fetch(ci0 + 2 * PIPE, mA, rA, sA);
         absorb(mB, rB, sB);
     }
-    overflow = overflow || cnt > SEL_CAP;
+    overflow = overflow || cnt > CAP;
     wave_lds_sync();
     // with the bound raised, nkept misses the keys below it, but at least kk
     // distinct keys lie above it
@@ -2052,7 +2056,7 @@ select_kernel(SelP p) {
         else if (cnt <= 4 * SSA_WAVE)
             sel_threshold<4>(ckey, cnt, kk, base, top, lo_bit, thr, need, btie);
         else
-            sel_threshold<SEL_CAP / SSA_WAVE>(ckey, cnt, kk, base, top, lo_bit, thr, need, btie);
+            sel_threshold<CAP / SSA_WAVE>(ckey, cnt, kk, base, top, lo_bit, thr, need, btie);
     };
     // exact keys of the buffered entries whose key is `only` (every entry: 0);
     // bit i of the result: lane's entry lane + 64 i now holds its exact key
@@ -2087,7 +2091,7 @@ select_kernel(SelP p) {
                 else if (cnt <= 4 * SSA_WAVE)
                     sel_boundary<4>(ckey, ebits, thr, need, btie);
                 else
-                    sel_boundary<SEL_CAP / SSA_WAVE>(ckey, ebits, thr, need, btie);
+                    sel_boundary<CAP / SSA_WAVE>(ckey, ebits, thr, need, btie);
                 thr |= 1u;
                 wave_lds_sync();
             }
@@ -2180,7 +2184,7 @@ select_kernel(SelP p) {
     }
     if (btie && lane == 0 && p.tie_list) p.tie_list[atomicAdd(p.tie_count, 1)] = (int)row;
 
-    full_merge_emit(bm, p, n, row, f, (int32_t *)ckey, sel_buf_words(p.words));
+    full_merge_emit(bm, p, n, row, f, (int32_t *)ckey, sel_buf_words(p.words, CAP));
 }
 
 // ------------------------------------------------------------------ exact top-k replay
@@ -3035,18 +3039,18 @@ int rescore_dispatch(int d, const RsP &rp, int64_t grid, hipStream_t st) {
     return SSA_E_UNSUP;
 }
 
-template <typename T, bool LSH, bool CAUSAL>
+template <typename T, bool LSH, bool CAUSAL, int CAP>
 int launch_select(const SelP &sp, hipStream_t st) {
     const size_t lds =
-        (size_t)SEL_WAVES * sel_lds_words(sp.words, sp.kk, LSH, sp.nlists) * 4;
+        (size_t)SEL_WAVES * sel_lds_words(sp.words, sp.kk, LSH, sp.nlists, CAP) * 4;
     if (lds > SSA_LDS_BYTES) {
         ssa_set_error("build_graph: select needs %zu bytes of LDS", lds);
         return SSA_E_UNSUP;
     }
-    SSA_CHECK_HIP(hipFuncSetAttribute((const void *)select_kernel<T, LSH, CAUSAL>,
+    SSA_CHECK_HIP(hipFuncSetAttribute((const void *)select_kernel<T, LSH, CAUSAL, CAP>,
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     const int64_t grid = 8 * ceil_div(sp.nblocks, 8);
-    hipLaunchKernelGGL((select_kernel<T, LSH, CAUSAL>), dim3((unsigned)grid),
+    hipLaunchKernelGGL((select_kernel<T, LSH, CAUSAL, CAP>), dim3((unsigned)grid),
                        dim3(SEL_WAVES * SSA_WAVE), lds, st, sp);
     SSA_CHECK_LAUNCH();
     return SSA_OK;
@@ -3109,11 +3113,20 @@ int launch_replay(const SelP &sp, int chunk, uint32_t *rpscr, hipStream_t st) {
     return SSA_OK;
 }
 
+template <typename T, bool LSH>
+int sel_dispatch_cap(const SelP &sp, hipStream_t st) {
+    if (sp.kk > SEL_CAP_LARGE_KK)
+        return sp.causal ? launch_select<T, LSH, true, SEL_CAP_LARGE>(sp, st)
+                         : launch_select<T, LSH, false, SEL_CAP_LARGE>(sp, st);
+    return sp.causal ? launch_select<T, LSH, true, SEL_CAP_SMALL>(sp, st)
+                     : launch_select<T, LSH, false, SEL_CAP_SMALL>(sp, st);
+}
+
 template <typename T>
 int select_dispatch(const SelP &sp, hipStream_t st) {
     if (sp.mode == SSA_GRAPH_LSH)
-        return sp.causal ? launch_select<T, true, true>(sp, st) : launch_select<T, true, false>(sp, st);
-    return sp.causal ? launch_select<T, false, true>(sp, st) : launch_select<T, false, false>(sp, st);
+        return sel_dispatch_cap<T, true>(sp, st);
+    return sel_dispatch_cap<T, false>(sp, st);
 }
 
 // Key phases: bucket ids of the keys (SSA_PHASE_KEY_HASH); the bucket
