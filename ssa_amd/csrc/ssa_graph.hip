@@ -153,25 +153,40 @@ __global__ void __launch_bounds__(256) hash_kernel(HashP p) {
     }
 }
 
-// bucket id and probe ids of one row from its P projections (plane j = bit j)
+// bucket id and probe ids of one row from its P <= 12 projections (plane j =
+// bit j); the projections are read once into registers (the loops below are
+// unrolled to 12, so nothing is indexed at run time)
 __device__ __forceinline__ void write_ids(const float *pr, int P, int Tp, uint16_t *o) {
+    float v[12];
+#pragma unroll
+    for (int j = 0; j < 12; ++j) v[j] = j < P ? pr[j] : 0.f;
     int id = 0;
-    for (int j = 0; j < P; ++j)
-        if (pr[j] > 0.f) id |= 1 << j;
+#pragma unroll
+    for (int j = 0; j < 12; ++j)
+        if (j < P && v[j] > 0.f) id |= 1 << j;
     o[0] = (uint16_t)id;
-    for (int t = 0; t < Tp; ++t) {
-        // plane whose stable rank of |proj| is t
-        int pos = 0;
-        for (int j = 0; j < P; ++j) {
-            const float aj = fabsf(pr[j]);
+    if (Tp > 0) {
+        // stable rank of |proj_j| among the P planes; probe t flips the plane
+        // of rank t
+        int rk[12];
+#pragma unroll
+        for (int j = 0; j < 12; ++j) {
+            const float aj = fabsf(v[j]);
             int rank = 0;
-            for (int q = 0; q < P; ++q) {
-                const float aq = fabsf(pr[q]);
-                rank += (aq < aj) || (aq == aj && q < j);
+#pragma unroll
+            for (int q = 0; q < 12; ++q) {
+                const float aq = fabsf(v[q]);
+                rank += (q < P) && ((aq < aj) || (aq == aj && q < j));
             }
-            if (rank == t) pos = j;
+            rk[j] = rank;
         }
-        o[1 + t] = (uint16_t)(id ^ (1 << pos));
+        for (int t = 0; t < Tp; ++t) {
+            int pos = 0;
+#pragma unroll
+            for (int j = 0; j < 12; ++j)
+                if (j < P && rk[j] == t) pos = j;
+            o[1 + t] = (uint16_t)(id ^ (1 << pos));
+        }
     }
 }
 
@@ -265,20 +280,27 @@ __global__ void __launch_bounds__(256) hash_mfma_kernel(HashP p) {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        if (lane < 16 && row0 + lane < p.rows) {
-            const int64_t rw = row0 + lane;
-            const int i = (int)(rw % p.L);
-            const int64_t bh = rw / p.L;
-            for (int r = 0; r < p.R; ++r) {
-                const float *pr = pw + lane * pst + r * p.P;
-                if (p.key_layout) {
+        if (p.key_layout) {
+            if (lane < 16 && row0 + lane < p.rows) {
+                const int64_t rw = row0 + lane;
+                const int i = (int)(rw % p.L);
+                const int64_t bh = rw / p.L;
+                for (int r = 0; r < p.R; ++r) {
+                    const float *pr = pw + lane * pst + r * p.P;
                     int id = 0;
                     for (int j = 0; j < p.P; ++j)
                         if (pr[j] > 0.f) id |= 1 << j;
                     p.out[(bh * p.R + r) * p.L + i] = (uint16_t)id;
-                } else {
-                    write_ids(pr, p.P, p.Tp, p.out + ((bh * p.L + i) * p.R + r) * p.NS);
                 }
+            }
+        } else {
+            // query layout: one (row, round) pair per lane, in the ids' memory
+            // order (row-major over the tile's rows, then rounds)
+            for (int x0 = 0; x0 < 16 * p.R; x0 += SSA_WAVE) {
+                const int x = x0 + lane;
+                const int rl = x / p.R, r = x - rl * p.R;
+                if (rl < 16 && row0 + rl < p.rows)
+                    write_ids(pw + rl * pst + r * p.P, p.P, p.Tp, p.out + ((row0 + rl) * p.R + r) * p.NS);
             }
         }
         // this wave's projection rows are rewritten by its next tile
@@ -1110,6 +1132,14 @@ struct AuxP {
     const uint32_t *knorm;   // max |k|^2 per (batch, kv head), float bits
     int N, Hq, Hkv, rep, bh0, nbh, G, NA, causal, d;
     float *out;        // (nbh * N, NA): q.k_n, q.k_glob[0..G-1], q.k_0, code scale
+    // aux_mfma_kernel with qid set also hashes its query rows (the query hash
+    // of hash_mfma_kernel on the q rows it has loaded anyway): planes as
+    // HashP's (16-byte aligned), ids in the query layout; zero1, if set, is
+    // cleared by block 0 (the select kernels' tie-row counter)
+    const float *planes;
+    int R, maxP, P, Tp, NS;
+    uint16_t *qid;
+    int32_t *zero1;
 };
 
 template <typename T, int D>
@@ -1140,6 +1170,53 @@ __global__ void __launch_bounds__(256) aux_mfma_kernel(AuxP p) {
     V qa[KS];
 #pragma unroll
     for (int s = 0; s < KS; ++s) qa[s] = frag(qbase + (int64_t)(okq ? nq : 0) * p.qsn, okq, s);
+    if (p.qid) {
+        // bucket and probe ids of the 16 rows (sparse_attention.py:559-646):
+        // fp32 projections on v_mfma_f32_16x16x4f32, lane (li, lg) feeding row
+        // li and plane li with element 32 s + 8 lg + e at step (s, e) -- the
+        // elements its bf16/f16 fragments hold -- then through LDS to one lane
+        // per row, which writes the ids as the query hash does
+        extern __shared__ float aux_proj[];
+        if (p.zero1 && blockIdx.x == 0 && threadIdx.x == 0) *p.zero1 = 0;
+        const int NP = p.R * p.P;
+        const int NT = (NP + 15) / 16;
+        const int pst = NT * 16 + 1;
+        float *pw = aux_proj + wid * 16 * pst;
+        for (int t = 0; t < NT; ++t) {
+            const int j = t * 16 + li;
+            const bool real = j < NP;
+            const float *pl = p.planes + (real ? ((int64_t)(j / p.P) * p.maxP + (j % p.P)) * p.d : 0);
+            f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < KS; ++s) {
+                const int e0 = 32 * s + 8 * lg;
+                float4 w0 = make_float4(0.f, 0.f, 0.f, 0.f), w1 = w0;
+                if (real && e0 < p.d) {
+                    w0 = *reinterpret_cast<const float4 *>(pl + e0);
+                    w1 = *reinterpret_cast<const float4 *>(pl + e0 + 4);
+                }
+                const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+                T qe[8];
+                __builtin_memcpy(qe, &qa[s], sizeof(qe));
+#pragma unroll
+                for (int e = 0; e < 8; ++e)
+                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(to_f32(qe[e]), wv[e], acc, 0, 0, 0);
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) pw[(4 * lg + r) * pst + t * 16 + li] = acc[r];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // one (row, round) pair per lane, in the ids' memory order
+        for (int x0 = 0; x0 < 16 * p.R; x0 += SSA_WAVE) {
+            const int x = x0 + lane;
+            const int rl = x / p.R, r = x - rl * p.R;
+            if (rl < 16 && n0 + rl < p.N)
+                write_ids(pw + rl * pst + r * p.P, p.P, p.Tp,
+                          p.qid + (((int64_t)bh * p.N + n0 + rl) * p.R + r) * p.NS);
+        }
+    }
     // operand roles as in the rescore (keys as A, queries as B): lane (li, lg)
     // receives C[4 lg + rr][li] = score of key row 4 lg + rr for query n0 + li
     float *ob = p.out + ((int64_t)bhl * p.N + n0) * p.NA;
@@ -3064,8 +3141,11 @@ int aux_dispatch(int d, bool mfma, const AuxP &ap, hipStream_t st) {
         if (mfma) {
             const int64_t waves = (int64_t)ap.nbh * ((ap.N + 15) / 16);
             const dim3 grid((unsigned)ceil_div(waves, 4));
+            // fused query hash: 16 projection rows of every plane tile per wave
+            const size_t lds =
+                ap.qid ? (size_t)4 * 16 * (ceil_div((int64_t)ap.R * ap.P, 16) * 16 + 1) * 4 : 0;
 #define SSA_AUX_MFMA(DD) \
-    case DD: hipLaunchKernelGGL((aux_mfma_kernel<T, DD>), grid, dim3(256), 0, st, ap); break;
+    case DD: hipLaunchKernelGGL((aux_mfma_kernel<T, DD>), grid, dim3(256), lds, st, ap); break;
             switch (mfma_instance(d)) {
                 SSA_AUX_MFMA(8) SSA_AUX_MFMA(16) SSA_AUX_MFMA(32) SSA_AUX_MFMA(64)
                 SSA_AUX_MFMA(96) SSA_AUX_MFMA(128)
@@ -3206,12 +3286,61 @@ int keys_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws
 template <typename T>
 int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws,
                   hipStream_t st) {
-    int rc = launch_hash<T>(D, a, L, ws, st, false);
-    if (rc) return rc;
+    // the rescore's parameters that hold for every head chunk
+    RsP rp{};
+    rp.sid = (const int32_t *)(ws + L.sid);
+    rp.bstart = (const int32_t *)(ws + L.bstart);
+    rp.bsize = (const int32_t *)(ws + L.bsize);
+    rp.q = a->q.ptr; rp.k = a->k.ptr;
+    rp.qsb = a->q.sb; rp.qsh = a->q.sh; rp.qsn = a->q.sn;
+    rp.ksb = a->k.sb; rp.ksh = a->k.sh; rp.ksn = a->k.sn;
+    rp.S = (uint16_t *)(ws + L.S);
+    rp.N = D.N; rp.M = D.M; rp.R = D.R; rp.NS = D.NS; rp.NB = D.NB; rp.C = D.C;
+    rp.Hq = D.Hq; rp.Hkv = D.Hkv; rp.rep = D.rep; rp.Call = D.Call;
+    rp.causal = a->causal ? 1 : 0;
+    rp.Cs = D.Cs;
+    rp.d = D.d;
+    {
+        const int64_t el = a->q.dtype == SSA_F32 ? 4 : 2;
+        rp.k32 = (rp.ksn * el < ((int64_t)1 << 24) &&
+                  ((int64_t)D.M * rp.ksn + D.d) * el < ((int64_t)1 << 31)) ? 1 : 0;
+    }
+    const bool mfma = rescore_uses_mfma<T>(D.d, rp);
+    // With aux on the matrix cores, aux_mfma_kernel also hashes the queries
+    // (one pass over q): without injected projections, with 16-byte aligned
+    // planes and their projection rows within 48 KB of LDS per block
+    const int np16 = (int)ceil_div((int64_t)D.R * D.P, 16) * 16;
+    const bool fuse_qhash = mfma && !a->q_proj && (uintptr_t)a->rand_proj % 16 == 0 &&
+                            (size_t)4 * 16 * (np16 + 1) * 4 <= 48 * 1024;
+    int rc = SSA_OK;
+    if (!fuse_qhash) {
+        rc = launch_hash<T>(D, a, L, ws, st, false);
+        if (rc) return rc;
+    }
     SelP last{};
     for (int64_t bh0 = 0; bh0 < D.BH; bh0 += D.nbh_chunk) {
         const int nbh = (int)((D.BH - bh0) < D.nbh_chunk ? (D.BH - bh0) : D.nbh_chunk);
         const int ninst = nbh * D.R * D.NS;
+        // aux first: the rescore codes its scores with the query scales it
+        // writes, and the query buckets need the ids it writes when fused
+        AuxP ap{};
+        ap.q = a->q.ptr; ap.k = a->k.ptr;
+        ap.qsb = a->q.sb; ap.qsh = a->q.sh; ap.qsn = a->q.sn;
+        ap.ksb = a->k.sb; ap.ksh = a->k.sh; ap.ksn = a->k.sn;
+        ap.glob = a->glob;
+        ap.knorm = (const uint32_t *)(ws + L.knorm);
+        ap.N = D.N; ap.Hq = D.Hq; ap.Hkv = D.Hkv; ap.rep = D.rep; ap.bh0 = (int)bh0;
+        ap.nbh = nbh; ap.G = D.G; ap.NA = D.G + 3; ap.causal = a->causal; ap.d = D.d;
+        ap.out = (float *)(ws + L.aux);
+        if (fuse_qhash) {
+            ap.planes = a->rand_proj;
+            ap.R = D.R; ap.maxP = D.maxP; ap.P = D.P; ap.Tp = D.Tp; ap.NS = D.NS;
+            ap.qid = (uint16_t *)(ws + L.qid);
+            // the tie-row counter of the select kernels (replayed once, after every chunk)
+            ap.zero1 = bh0 == 0 ? (int32_t *)(ws + L.tie_count) : nullptr;
+        }
+        rc = aux_dispatch<T>(D.d, mfma, ap, st);
+        if (rc) return rc;
         QbP qp{};
         qp.qid = (const uint16_t *)(ws + L.qid);
         qp.bsize = (const int32_t *)(ws + L.bsize);
@@ -3243,37 +3372,8 @@ int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char 
                            st, qp);
         SSA_CHECK_LAUNCH();
 
-        RsP rp{};
         rp.tiles = qp.tiles; rp.ntiles = qp.ntiles; rp.qlist = qp.qlist;
-        rp.sid = (const int32_t *)(ws + L.sid);
-        rp.bstart = (const int32_t *)(ws + L.bstart);
-        rp.bsize = (const int32_t *)(ws + L.bsize);
-        rp.q = a->q.ptr; rp.k = a->k.ptr;
-        rp.qsb = a->q.sb; rp.qsh = a->q.sh; rp.qsn = a->q.sn;
-        rp.ksb = a->k.sb; rp.ksh = a->k.sh; rp.ksn = a->k.sn;
-        rp.S = (uint16_t *)(ws + L.S);
-        rp.N = D.N; rp.M = D.M; rp.R = D.R; rp.NS = D.NS; rp.NB = D.NB; rp.C = D.C;
-        rp.Hq = D.Hq; rp.Hkv = D.Hkv; rp.rep = D.rep; rp.bh0 = (int)bh0; rp.Call = D.Call;
-        rp.causal = a->causal ? 1 : 0;
-        rp.Cs = D.Cs;
-        rp.d = D.d;
-        {
-            const int64_t el = a->q.dtype == SSA_F32 ? 4 : 2;
-            rp.k32 = (rp.ksn * el < ((int64_t)1 << 24) &&
-                      ((int64_t)D.M * rp.ksn + D.d) * el < ((int64_t)1 << 31)) ? 1 : 0;
-        }
-        // aux first: the rescore codes its scores with the query scales it writes
-        AuxP ap{};
-        ap.q = a->q.ptr; ap.k = a->k.ptr;
-        ap.qsb = a->q.sb; ap.qsh = a->q.sh; ap.qsn = a->q.sn;
-        ap.ksb = a->k.sb; ap.ksh = a->k.sh; ap.ksn = a->k.sn;
-        ap.glob = a->glob;
-        ap.knorm = (const uint32_t *)(ws + L.knorm);
-        ap.N = D.N; ap.Hq = D.Hq; ap.Hkv = D.Hkv; ap.rep = D.rep; ap.bh0 = (int)bh0;
-        ap.nbh = nbh; ap.G = D.G; ap.NA = D.G + 3; ap.causal = a->causal; ap.d = D.d;
-        ap.out = (float *)(ws + L.aux);
-        rc = aux_dispatch<T>(D.d, rescore_uses_mfma<T>(D.d, rp), ap, st);
-        if (rc) return rc;
+        rp.bh0 = (int)bh0;
         rp.aux = ap.out;
         rp.NA = ap.NA;
         const int64_t grid = 8 * ceil_div((int64_t)ninst * (ceil_div(D.N, TQ) + D.NB), 8);
@@ -3301,7 +3401,7 @@ int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char 
         sp.sid = rp.sid; sp.rnk = (const int32_t *)(ws + L.rnk);
         sp.inv = (const int32_t *)(ws + L.inv); sp.cut = cp.cut; sp.srix = cp.srix;
         sp.head_bytes = (uint32_t)((int64_t)D.N * D.nlists * D.Cs * 2);
-        sp.mfma = rescore_uses_mfma<T>(D.d, rp) ? 1 : 0;
+        sp.mfma = mfma ? 1 : 0;
         sp.nl_magic = (uint32_t)((((uint64_t)1 << 32) + D.nlists - 1) / D.nlists);
         sp.S = rp.S; sp.q = a->q.ptr; sp.k = a->k.ptr;
         sp.qsb = a->q.sb; sp.qsh = a->q.sh; sp.qsn = a->q.sn;
@@ -3329,12 +3429,12 @@ int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char 
     if (D.BH * D.N == 0) return SSA_OK;
     // the rows every chunk flagged, in one launch: each row's replay is a long
     // chain of dependent steps, so rows from all chunks run side by side
-    SelP rp = last;
-    rp.bh0 = 0;
-    rp.rows = D.BH * D.N;
+    SelP xp = last;
+    xp.bh0 = 0;
+    xp.rows = D.BH * D.N;
     uint32_t *rpscr = (uint32_t *)(ws + L.rpscr);
-    return rp.mode == SSA_GRAPH_LSH ? launch_replay<T, true>(rp, D.chunk, rpscr, st)
-                                    : launch_replay<T, false>(rp, D.chunk, rpscr, st);
+    return xp.mode == SSA_GRAPH_LSH ? launch_replay<T, true>(xp, D.chunk, rpscr, st)
+                                    : launch_replay<T, false>(xp, D.chunk, rpscr, st);
 }
 
 }  // namespace
