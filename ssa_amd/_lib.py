@@ -149,6 +149,11 @@ def _ptr(t):
 
 
 # --------------------------------------------------------------------------- graph build
+# largest key length and number of global tokens ssa_build_graph accepts
+MAX_KEYS = 32768
+MAX_GLOBALS = 63
+
+
 def build_graph(q, k, rand_proj, *, P, T, C, top_k, window, causal, is_cross, total_k, glob,
                 mode=GRAPH_FULL, q_proj=None, k_proj=None, count_ties=False, ids32=False,
                 noalloc=False):
@@ -179,6 +184,12 @@ def build_graph(q, k, rand_proj, *, P, T, C, top_k, window, causal, is_cross, to
     if k_proj is not None and tuple(k_proj.shape) != (B * Hkv, R, M, P):
         raise RuntimeError(f"ssa_amd.build_graph: k_proj {tuple(k_proj.shape)} is not "
                            f"{(B * Hkv, R, M, P)}")
+    if not 1 <= M <= MAX_KEYS:
+        raise RuntimeError(f"ssa_amd.build_graph: key length {M} unsupported (1..{MAX_KEYS}: the "
+                           "bucket sort keeps a row's keys in LDS and key ids are packed in 16 bits)")
+    if glob.numel() > MAX_GLOBALS:
+        raise RuntimeError(f"ssa_amd.build_graph: {glob.numel()} global tokens unsupported "
+                           f"(0..{MAX_GLOBALS}: one wavefront holds them)")
     require_device(q, k, rand_proj, glob)
     if q.dtype != k.dtype:
         raise RuntimeError("ssa_amd.build_graph: q and k dtypes differ")

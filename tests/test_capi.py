@@ -205,3 +205,35 @@ def test_head_dim_rule(d, dtype, ok):
         assert wsb > 0, _lib.lib().ssa_last_error()
     else:
         assert wsb < 0 and b"head dim" in _lib.lib().ssa_last_error()
+
+
+# ---------------------------------------------------------------------------- size envelope
+@pytest.mark.parametrize("M", [32769, 40000, 65536])
+def test_key_length_beyond_the_sort_is_refused(M):
+    """Keys beyond 32768 are refused by the library before any launch (the
+    bucket sort keeps a row's keys in LDS, key ids are packed in 16 bits),
+    and by the Python wrapper before it touches a device."""
+    import torch
+
+    from ssa_amd import _lib
+    a, _ = _full_args(M, 64)
+    assert _lib.lib().ssa_graph_workspace_bytes(ctypes.byref(a)) < 0
+    assert b"key length" in _lib.lib().ssa_last_error()
+    q = torch.zeros(1, 1, 8, 16)
+    k = torch.zeros(1, 1, M, 16)
+    with pytest.raises(RuntimeError, match="key length"):
+        _lib.build_graph(q, k, torch.zeros(2, 12, 16), P=1, T=0, C=64, top_k=32, window=4,
+                         causal=False, is_cross=True, total_k=64, glob=torch.zeros(2))
+
+
+def test_globals_beyond_a_wavefront_are_refused():
+    import torch
+
+    from ssa_amd import _lib
+    a, _ = _full_args(1024, 128, G=64)
+    assert _lib.lib().ssa_graph_workspace_bytes(ctypes.byref(a)) < 0
+    assert b"G=64" in _lib.lib().ssa_last_error()
+    with pytest.raises(RuntimeError, match="global tokens"):
+        _lib.build_graph(torch.zeros(1, 1, 8, 16), torch.zeros(1, 1, 8, 16), torch.zeros(2, 12, 16),
+                         P=1, T=0, C=64, top_k=32, window=4, causal=False, is_cross=False,
+                         total_k=64, glob=torch.zeros(64))
