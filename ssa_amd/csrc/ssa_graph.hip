@@ -2427,138 +2427,11 @@ __device__ int rp_partition(const RpArr &a, uint16_t *TL, uint16_t *TR, int f, i
 
 __device__ __forceinline__ int rp_log2(int n) { return 31 - __clz(n); }
 
-// k-th (0-based) set bit of a 64-bit mask (k < popcount)
-__device__ __forceinline__ int rp_nth_bit64(uint64_t m, int k) {
-    const int c = __popc((uint32_t)m);
-    const bool up = k >= c;
-    return (up ? 32 : 0) + nth_set_bit(up ? (uint32_t)(m >> 32) : (uint32_t)m, up ? k - c : k);
-}
-
-// ---- the same partition for a segment of at most 64 entries held in one
-// wavefront's registers (lane i: position i of the held range, key kv, key id
-// cv): [a, b) is split as rp_partition splits it -- median of a+1, middle and
-// b-1 moved to a, then the unguarded Hoare scan, whose swaps pair the k-th
-// left stopper (key >= pivot, after a) with the k-th right stopper (key <=
-// pivot, from the top) while the former lies left of the latter -- with
-// ballots and one shuffle instead of LDS round trips.  Returns the cut.
-__device__ int rp_reg_partition(uint32_t &kv, int32_t &cv, int a, int b) {
-    const int lane = lane_id();
-    const int m = b - a;
-    const int ia = a + 1, ib = a + m / 2, ic = b - 1;
-    const uint32_t ka = (uint32_t)__builtin_amdgcn_readlane((int)kv, ia);
-    const uint32_t kb = (uint32_t)__builtin_amdgcn_readlane((int)kv, ib);
-    const uint32_t kc = (uint32_t)__builtin_amdgcn_readlane((int)kv, ic);
-    int x;
-    uint32_t pv;
-    if (ka < kb) {
-        if (kb < kc) { x = ib; pv = kb; }
-        else if (ka < kc) { x = ic; pv = kc; }
-        else { x = ia; pv = ka; }
-    } else if (ka < kc) { x = ia; pv = ka; }
-    else if (kb < kc) { x = ic; pv = kc; }
-    else { x = ib; pv = kb; }
-    {                                           // pivot to the front
-        const uint32_t kx = (uint32_t)__builtin_amdgcn_readlane((int)kv, x);
-        const int32_t xx = __builtin_amdgcn_readlane(cv, x);
-        const uint32_t k0 = (uint32_t)__builtin_amdgcn_readlane((int)kv, a);
-        const int32_t x0 = __builtin_amdgcn_readlane(cv, a);
-        if (lane == a) { kv = kx; cv = xx; }
-        else if (lane == x) { kv = k0; cv = x0; }
-    }
-    const bool in = lane >= a && lane < b;
-    const uint64_t bL = wave_ballot(in && lane > a && kv >= pv);
-    const uint64_t bR = wave_ballot(in && kv <= pv);
-    const int nL = __popcll(bL), nR = __popcll(bR);
-    const int Lj = lane < nL ? rp_nth_bit64(bL, lane) : 0;
-    const int Rj = lane < nR ? 63 - rp_nth_bit64(__builtin_bitreverse64(bR), lane) : 0;
-    const int mn = nL < nR ? nL : nR;
-    const int sw = __popcll(wave_ballot(lane < mn && Lj < Rj));                 // a prefix
-    const int rl = lanes_below(bL);
-    const int rr = __popcll(bR & ~((2ull << lane) - 1ull));
-    const int tR = __shfl(Rj, rl, SSA_WAVE);   // the rl-th right stopper
-    const int tL = __shfl(Lj, rr, SSA_WAVE);   // the rr-th left stopper
-    int partner = lane;
-    if (((bL >> lane) & 1ull) && rl < sw) partner = tR;
-    else if (((bR >> lane) & 1ull) && rr < sw) partner = tL;
-    kv = (uint32_t)__shfl((int)kv, partner, SSA_WAVE);
-    cv = __shfl(cv, partner, SSA_WAVE);
-    const int cL = sw < nL ? __builtin_amdgcn_readlane(Lj, sw) : 0x7fffffff;
-    const int cR = sw > 0 ? __builtin_amdgcn_readlane(Rj, sw - 1) : 0x7fffffff;
-    return cL < cR ? cL : cR;
-}
-
-// std::sort's introsort subtree of [f, f + n) (n <= 64, depth0 levels left)
-// in registers: pending segments are bits of a mask, so the order in which
-// independent segments split does not matter; every cut is marked in lbits;
-// a segment reaching the depth limit is heap-sorted through LDS by one lane
-__device__ void rp_small_sort(const RpArr &A, uint32_t *lbits, int f, int n, int depth0) {
-    const int lane = lane_id();
-    uint32_t kv = lane < n ? A.key[f + lane] : 0u;
-    int32_t cv = lane < n ? A.cand[f + lane] : 0;
-    int dep = lane == 0 ? depth0 : 0;           // depth left of the segment starting at this lane
-    uint64_t bnd = 1ull;                        // segment starts
-    uint64_t pend = n > 16 ? 1ull : 0ull;       // starts of segments still to split
-    while (pend) {
-        const int a = __ffsll((long long)pend) - 1;
-        pend &= pend - 1ull;
-        const uint64_t above = bnd & ~((2ull << a) - 1ull);
-        const int b = above ? __ffsll((long long)above) - 1 : n;
-        const int d = __builtin_amdgcn_readlane(dep, a);
-        if (d == 0) {
-            if (lane < n) { A.key[f + lane] = kv; A.cand[f + lane] = cv; }
-            rp_sync();
-            if (lane == 0) {
-                rp_heap_select(A, f + a, f + b, f + b);
-                rp_heap_sort(A, f + a, f + b);
-            }
-            rp_sync();
-            if (lane < n) { kv = A.key[f + lane]; cv = A.cand[f + lane]; }
-            continue;
-        }
-        const int c = rp_reg_partition(kv, cv, a, b);
-        if (lane == 0) atomicOr(&lbits[(f + c) >> 5], 1u << ((f + c) & 31));
-        bnd |= 1ull << c;
-        dep = (lane == a || lane == c) ? d - 1 : dep;
-        if (c - a > 16) pend |= 1ull << a;
-        if (b - c > 16) pend |= 1ull << c;
-    }
-    if (lane < n) { A.key[f + lane] = kv; A.cand[f + lane] = cv; }
-    rp_sync();
-}
-
 // std::nth_element(f, nth, l)
 __device__ void rp_nth_element(const RpArr &a, uint16_t *TL, uint16_t *TR, int f, int nth, int l) {
     if (f == l || nth == l) return;
     int depth = 2 * rp_log2(l - f);
     while (l - f > 3) {
-        if (l - f <= SSA_WAVE) {
-            // the rest in registers: the held range starts at f0
-            const int f0 = f, lane = lane_id();
-            uint32_t kv = lane < l - f ? a.key[f + lane] : 0u;
-            int32_t cv = lane < l - f ? a.cand[f + lane] : 0;
-            int lo = 0, hi = l - f;
-            const int nr = nth - f0;
-            bool heap = false;
-            while (hi - lo > 3) {
-                if (depth == 0) { heap = true; break; }
-                --depth;
-                const int c = rp_reg_partition(kv, cv, lo, hi);
-                if (c <= nr) lo = c; else hi = c;
-            }
-            if (lane < l - f0) { a.key[f0 + lane] = kv; a.cand[f0 + lane] = cv; }
-            rp_sync();
-            f = f0 + lo;
-            l = f0 + hi;
-            if (heap) {
-                if (lane_id() == 0) {
-                    rp_heap_select(a, f, nth + 1, l);
-                    rp_swap(a, f, nth);
-                }
-                rp_sync();
-                return;
-            }
-            break;
-        }
         if (depth == 0) {
             if (lane_id() == 0) {
                 rp_heap_select(a, f, nth + 1, l);
@@ -2594,10 +2467,6 @@ __device__ void rp_sort(const RpArr &a, uint16_t *TL, uint16_t *TR, uint32_t *lb
         --top;
         const int sf = stk[top], sl = stk[RP_STACK + top], sd = stk[2 * RP_STACK + top];
         rp_sync();
-        if (sl - sf <= SSA_WAVE && sd > 0) {
-            rp_small_sort(a, lbits, sf, sl - sf, sd);
-            continue;
-        }
         if (sd == 0) {
             if (lane == 0) {
                 rp_heap_select(a, sf, sl, sl);
@@ -2638,9 +2507,14 @@ __device__ void rp_sort(const RpArr &a, uint16_t *TL, uint16_t *TR, uint32_t *lb
 // words per resident wave) instead of LDS, for rows whose kk + chunk slots do
 // not fit; the same code runs on either (all accesses of a wave's arrays come
 // from that wave, whose stores its own later loads see after rp_sync).
-template <typename T, bool LSH_MODE, bool GLB>
+// WIDE: the exact keys of a chunk with all four MFMA rounds' K rows in flight
+// (exact_keys_wide) -- a shorter chain per row for many more registers, so
+// fewer rows in flight.  Both instances are launched; a wide instance
+// replays only when at most wide_max rows are tied (they are all resident
+// at once), the narrow one only when more are (wide_max < 0: always).
+template <typename T, bool LSH_MODE, bool GLB, bool WIDE>
 __global__ void __launch_bounds__(RP_WAVES * SSA_WAVE)
-topk_replay_kernel(SelP p, int chunk, int W, uint32_t *gscr) {
+topk_replay_kernel(SelP p, int chunk, int W, uint32_t *gscr, int wide_max) {
     extern __shared__ uint32_t rp_smem[];
     const int wid = threadIdx.x / SSA_WAVE;
     const int lane = lane_id();
@@ -2659,6 +2533,7 @@ topk_replay_kernel(SelP p, int chunk, int W, uint32_t *gscr) {
 
     const int total = (int)gridDim.x * RP_WAVES;
     const int cnt = *p.tie_count;
+    if (WIDE ? cnt > wide_max : cnt <= wide_max) return;
     const int kk = p.kk;
     for (int it = (int)blockIdx.x * RP_WAVES + wid; it < cnt; it += total) {
         const int64_t row = p.tie_list[it];          // bh * N + n, over all query heads
@@ -2723,7 +2598,9 @@ topk_replay_kernel(SelP p, int chunk, int W, uint32_t *gscr) {
                     // exact keys with the rescore's arithmetic (the table holds
                     // only their prefixes); the query itself scores as in aux
                     const bool xk = keep && !(p.causal && v == n);
-                    const uint32_t ex = exact_keys_wide<T, 4>(p, qr, kb, v, xk);
+                    uint32_t ex;
+                    if constexpr (WIDE) ex = exact_keys_wide<T, 4>(p, qr, kb, v, xk);
+                    else ex = exact_keys<T>(p, qr, kb, v, xk);
                     if (keep) sk = xk ? ex : kself;
                 } else {
                     // empty bucket: glob ++ 0, all valid; duplicates resolved in slot order
@@ -3177,18 +3054,37 @@ int launch_replay(const SelP &sp, int chunk, uint32_t *rpscr, hipStream_t st) {
     const int W = sp.kk + chunk;
     if (!replay_fits_lds(W, sp.words)) {
         const int64_t blocks = replay_glb_blocks(W, sp.words);
-        hipLaunchKernelGGL((topk_replay_kernel<T, LSH, true>), dim3((unsigned)blocks),
-                           dim3(RP_WAVES * SSA_WAVE), 0, st, sp, chunk, W, rpscr);
+        hipLaunchKernelGGL((topk_replay_kernel<T, LSH, true, false>), dim3((unsigned)blocks),
+                           dim3(RP_WAVES * SSA_WAVE), 0, st, sp, chunk, W, rpscr, -1);
         SSA_CHECK_LAUNCH();
         return SSA_OK;
     }
     const size_t lds = (size_t)RP_WAVES * rp_lds_words(W, sp.words) * 4;
-    SSA_CHECK_HIP(hipFuncSetAttribute((const void *)topk_replay_kernel<T, LSH, false>,
+    // the wide instance's resident rows: two waves per SIMD (its registers)
+    int wide_max = -1;
+    if constexpr (!std::is_same<T, float>::value) {
+      if (sp.mfma) {
+        int dev = 0, cus = 0;
+        SSA_CHECK_HIP(hipGetDevice(&dev));
+        SSA_CHECK_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+        wide_max = 2 * 4 * cus;
+        SSA_CHECK_HIP(hipFuncSetAttribute((const void *)topk_replay_kernel<T, LSH, false, true>,
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        const int64_t wblocks = std::min<int64_t>(ceil_div(sp.rows, RP_WAVES),
+                                                  ceil_div(wide_max, RP_WAVES));
+        hipLaunchKernelGGL((topk_replay_kernel<T, LSH, false, true>), dim3((unsigned)wblocks),
+                           dim3(RP_WAVES * SSA_WAVE), lds, st, sp, chunk, W, (uint32_t *)nullptr,
+                           wide_max);
+        SSA_CHECK_LAUNCH();
+      }
+    }
+    SSA_CHECK_HIP(hipFuncSetAttribute((const void *)topk_replay_kernel<T, LSH, false, false>,
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     // enough blocks for every resident wave to take a row (the rest exit at once)
     const int64_t blocks = std::min<int64_t>(ceil_div(sp.rows, RP_WAVES), 8192);
-    hipLaunchKernelGGL((topk_replay_kernel<T, LSH, false>), dim3((unsigned)blocks),
-                       dim3(RP_WAVES * SSA_WAVE), lds, st, sp, chunk, W, (uint32_t *)nullptr);
+    hipLaunchKernelGGL((topk_replay_kernel<T, LSH, false, false>), dim3((unsigned)blocks),
+                       dim3(RP_WAVES * SSA_WAVE), lds, st, sp, chunk, W, (uint32_t *)nullptr,
+                       wide_max);
     SSA_CHECK_LAUNCH();
     return SSA_OK;
 }
