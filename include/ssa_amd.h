@@ -108,25 +108,6 @@ int64_t ssa_graph_workspace_bytes(const ssa_graph_args *a);
 int ssa_build_graph(const ssa_graph_args *a, void *workspace, int64_t workspace_bytes,
                     void *stream);
 
-/* ssa_build_graph in phases over one workspace (no counterpart in the
- * reference, which has no streams).  The key phases read only a->k, so a
- * caller can run them while it still computes q (a->q.ptr may then be NULL;
- * q's shape and dtype fields must be set):
- *   SSA_PHASE_KEY_HASH  bucket ids of the keys (:559-597);
- *   SSA_PHASE_KEY_SORT  bucket permutation and tables (:769-792) and the
- *                       sorted candidate lists, after KEY_HASH;
- *   SSA_PHASE_QUERIES   everything else, after both key phases.
- * Phases given in one call run in that order on `stream`; phases given in
- * separate calls (on different streams, say) must be ordered by the caller.
- * All calls take the same arguments and workspace;
- * ssa_build_graph(a) == ssa_build_graph_phases(a, ..., SSA_PHASE_ALL). */
-#define SSA_PHASE_KEY_HASH 1
-#define SSA_PHASE_KEY_SORT 2
-#define SSA_PHASE_QUERIES 4
-#define SSA_PHASE_ALL 7
-int ssa_build_graph_phases(const ssa_graph_args *a, void *workspace, int64_t workspace_bytes,
-                           void *stream, int phases);
-
 /* ssa_build_graph without any device allocation (no counterpart in the
  * reference): for callers that cannot allocate -- code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc.  The same

@@ -85,8 +85,6 @@ def lib():
         L.ssa_build_graph.argtypes = [ctypes.POINTER(GraphArgs), c_vp, c_i64, c_vp]
         L.ssa_build_graph_noalloc.restype = ctypes.c_int
         L.ssa_build_graph_noalloc.argtypes = [ctypes.POINTER(GraphArgs), c_vp]
-        L.ssa_build_graph_phases.restype = ctypes.c_int
-        L.ssa_build_graph_phases.argtypes = [ctypes.POINTER(GraphArgs), c_vp, c_i64, c_vp, c_i32]
         L.ssa_bucket_sort_workspace_bytes.restype = c_i64
         L.ssa_bucket_sort_workspace_bytes.argtypes = [c_i32, c_i32]
         L.ssa_bucket_sort.restype = ctypes.c_int
@@ -239,75 +237,6 @@ def build_graph(q, k, rand_proj, *, P, T, C, top_k, window, causal, is_cross, to
     _keep = (qk, kk_, rp, g, qp, kp, ws)
     del _keep
     return out, valid, ties
-
-
-# phases of ssa_build_graph_phases (include/ssa_amd.h)
-PHASE_KEY_HASH, PHASE_KEY_SORT, PHASE_QUERIES = 1, 2, 4
-
-
-class GraphBuild:
-    """ssa_build_graph in its phases over one workspace: ``key_hash()`` and
-    ``key_sort()`` need only k, so the sort may run on a side stream while the
-    caller computes q; ``queries(q)`` runs the rest on the current stream once
-    that stream waits for the key phases.  Outputs and workspace are allocated
-    on the current stream at construction."""
-
-    def __init__(self, B, Hq, N, k, rand_proj, *, P, T, C, top_k, window, causal, is_cross,
-                 total_k, glob, mode=GRAPH_FULL):
-        require_device(k, rand_proj, glob)
-        Bk, Hkv, M, d = k.shape
-        if Bk != B:
-            raise RuntimeError(f"ssa_amd.build_graph: k {tuple(k.shape)} / batch {B} mismatch")
-        self.ka, self._kk = view4(k)
-        self.rp = rand_proj.detach().to(torch.float32).contiguous()
-        self.g = glob.detach().to(device=k.device, dtype=torch.int64).contiguous()
-        a = GraphArgs()
-        a.mode = mode
-        a.B, a.Hq, a.Hkv, a.N, a.M, a.d = B, Hq, Hkv, N, M, d
-        a.q = Tensor4(None, dtype_code(k.dtype), 0, 0, 0)     # set by queries()
-        a.k = self.ka
-        a.rand_proj = self.rp.data_ptr()
-        a.R, a.max_p = self.rp.shape[0], self.rp.shape[1]
-        a.P, a.T, a.C, a.top_k = P, T, C, top_k
-        a.window, a.causal, a.is_cross, a.total_k = window, int(causal), int(is_cross), total_k
-        a.glob, a.G = (self.g.data_ptr() if self.g.numel() else None), self.g.numel()
-        a.q_proj, a.k_proj = None, None
-        L = lib()
-        width = L.ssa_graph_out_width(ctypes.byref(a))
-        if width < 0:
-            _check(-1, "build_graph")
-        self.wsb = L.ssa_graph_workspace_bytes(ctypes.byref(a))
-        if self.wsb < 0:
-            _check(-1, "build_graph")
-        self.out = torch.empty((B, Hq, N, width), dtype=torch.int64, device=k.device)
-        self.valid = (torch.empty((B, Hq, N, width), dtype=torch.bool, device=k.device)
-                      if mode == GRAPH_FULL else None)
-        self.ws = torch.empty(max(int(self.wsb), 1), dtype=torch.uint8, device=k.device)
-        a.out_idx, a.out_valid, a.out_ties = self.out.data_ptr(), _ptr(self.valid), None
-        self.a = a
-
-    def _run(self, phases, stream_of):
-        _check(lib().ssa_build_graph_phases(ctypes.byref(self.a), self.ws.data_ptr(),
-                                            int(self.wsb), _stream(stream_of), phases),
-               "build_graph")
-
-    def key_hash(self):
-        """Bucket ids of the keys, on torch's current stream."""
-        self._run(PHASE_KEY_HASH, self.ws)
-
-    def key_sort(self):
-        """Bucket permutation, tables and sorted lists, on torch's current stream."""
-        self._run(PHASE_KEY_SORT, self.ws)
-
-    def queries(self, q):
-        """Query phase on torch's current stream; returns (out_idx, out_valid)."""
-        require_device(q)
-        if q.dtype != self._kk.dtype or tuple(q.shape) != (self.a.B, self.a.Hq, self.a.N, self.a.d):
-            raise RuntimeError(f"ssa_amd.build_graph: q {tuple(q.shape)} {q.dtype} mismatch")
-        self.a.q, qk = view4(q)
-        self._run(PHASE_QUERIES, q)
-        del qk
-        return self.out, self.valid
 
 
 def bucket_sort(ids: torch.Tensor, P: int):

@@ -3105,14 +3105,13 @@ int select_dispatch(const SelP &sp, hipStream_t st) {
     return sel_dispatch_cap<T, false>(sp, st);
 }
 
-// Key phases: bucket ids of the keys (SSA_PHASE_KEY_HASH); the bucket
-// permutation and tables and the sorted candidate lists (SSA_PHASE_KEY_SORT)
-// -- everything that needs k but not q.
+// Key phase: bucket ids of the keys, the bucket permutation and tables and
+// the sorted candidate lists -- everything that needs k but not q.
 template <typename T>
 int keys_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws,
-               hipStream_t st, int phases) {
+               hipStream_t st) {
     int rc = SSA_OK;
-    if (phases & SSA_PHASE_KEY_HASH) {
+    {
         rc = launch_hash<T>(D, a, L, ws, st, true);
         if (rc) return rc;
         // max |k|^2 per (batch, kv head): the query code scales derive from it
@@ -3143,12 +3142,11 @@ int keys_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws
             SSA_CHECK_LAUNCH();
         }
     }
-    if (!(phases & SSA_PHASE_KEY_SORT)) return SSA_OK;
-    // the key hash cleared the sort's counter when it ran in this call
+    // the key hash cleared the sort's counter
     rc = ssa_launch_bucket_sort((const uint16_t *)(ws + L.kid), (int)(D.BK * D.R), D.M, D.P,
                                 (int32_t *)(ws + L.perm), (int32_t *)(ws + L.bstart),
                                 (int32_t *)(ws + L.bsize), (uint16_t *)(ws + L.sorttmp), st,
-                                !(phases & SSA_PHASE_KEY_HASH));
+                                false);
     if (rc) return rc;
     {
         LsP lp{};
@@ -3348,14 +3346,12 @@ extern "C" int64_t ssa_graph_workspace_bytes(const ssa_graph_args *a) {
 }
 
 namespace {
-int build_phase(const ssa_graph_args *a, void *workspace, int64_t workspace_bytes, void *stream,
-                int phases, int64_t ws_cap = 0) {
-    SSA_CHECK_ARG(phases > 0 && phases <= SSA_PHASE_ALL, "build_graph: phases %d", phases);
+int build_impl(const ssa_graph_args *a, void *workspace, int64_t workspace_bytes, void *stream,
+               int64_t ws_cap = 0) {
     Dims D;
-    const bool qphase = (phases & SSA_PHASE_QUERIES) != 0;
-    int rc = make_dims(a, D, qphase, ws_cap);
+    int rc = make_dims(a, D, true, ws_cap);
     if (rc) return rc;
-    if (qphase) {
+    {
         const bool i32 = a->mode == SSA_GRAPH_FULL && a->out_idx32;
         SSA_CHECK_ARG(i32 || a->out_idx, "build_graph: out_idx is null");
         SSA_CHECK_ARG(i32 || a->mode != SSA_GRAPH_FULL || a->out_valid,
@@ -3369,17 +3365,16 @@ int build_phase(const ssa_graph_args *a, void *workspace, int64_t workspace_byte
     }
     hipStream_t st = (hipStream_t)stream;
     char *ws = (char *)workspace;
-    const int kp = phases & (SSA_PHASE_KEY_HASH | SSA_PHASE_KEY_SORT);
     switch (a->k.dtype) {
         case SSA_F32:
-            if (kp && (rc = keys_typed<float>(D, a, L, ws, st, kp))) return rc;
-            return qphase ? queries_typed<float>(D, a, L, ws, st) : SSA_OK;
+            if ((rc = keys_typed<float>(D, a, L, ws, st))) return rc;
+            return queries_typed<float>(D, a, L, ws, st);
         case SSA_BF16:
-            if (kp && (rc = keys_typed<bf16_t>(D, a, L, ws, st, kp))) return rc;
-            return qphase ? queries_typed<bf16_t>(D, a, L, ws, st) : SSA_OK;
+            if ((rc = keys_typed<bf16_t>(D, a, L, ws, st))) return rc;
+            return queries_typed<bf16_t>(D, a, L, ws, st);
         case SSA_F16:
-            if (kp && (rc = keys_typed<f16_t>(D, a, L, ws, st, kp))) return rc;
-            return qphase ? queries_typed<f16_t>(D, a, L, ws, st) : SSA_OK;
+            if ((rc = keys_typed<f16_t>(D, a, L, ws, st))) return rc;
+            return queries_typed<f16_t>(D, a, L, ws, st);
     }
     return SSA_E_ARG;
 }
@@ -3387,12 +3382,7 @@ int build_phase(const ssa_graph_args *a, void *workspace, int64_t workspace_byte
 
 extern "C" int ssa_build_graph(const ssa_graph_args *a, void *workspace, int64_t workspace_bytes,
                                void *stream) {
-    return build_phase(a, workspace, workspace_bytes, stream, SSA_PHASE_ALL);
-}
-
-extern "C" int ssa_build_graph_phases(const ssa_graph_args *a, void *workspace,
-                                      int64_t workspace_bytes, void *stream, int phases) {
-    return build_phase(a, workspace, workspace_bytes, stream, phases);
+    return build_impl(a, workspace, workspace_bytes, stream);
 }
 
 int64_t ssa_graph_workspace_bytes_capped(const ssa_graph_args *a, int64_t ws_cap) {
@@ -3404,5 +3394,5 @@ int64_t ssa_graph_workspace_bytes_capped(const ssa_graph_args *a, int64_t ws_cap
 
 int ssa_build_graph_capped(const ssa_graph_args *a, void *workspace, int64_t ws_cap,
                            void *stream) {
-    return build_phase(a, workspace, ws_cap, stream, SSA_PHASE_ALL, ws_cap);
+    return build_impl(a, workspace, ws_cap, stream, ws_cap);
 }

@@ -397,16 +397,6 @@ class SparseAttention(nn.Module):
         kx, vx = y[..., :hk], y[..., hk:]
         return self._split_q(qx), self._split_kv_compact(kx), self._split_kv_compact(vx)
 
-    def _graph_build(self, k, B, N, M, causal, is_cross):
-        """build_graph split into its key and query phases (same result)."""
-        _lib.require_device(k)
-        glob = self.glob_builder(M, k.device)
-        lb = self.lsh_builder
-        p_eff = lb.compute_effective_p(M, lb.C, lb.max_P)
-        return _lib.GraphBuild(B, self.H, N, k, lb.rand_proj, P=p_eff, T=lb.T, C=lb.C,
-                               top_k=self.lsh_k, window=self.config.window_size, causal=causal,
-                               is_cross=is_cross, total_k=self.K, glob=glob, mode=_lib.GRAPH_FULL)
-
     def apply_graph(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                     neighbors: torch.Tensor, valid: torch.Tensor) -> torch.Tensor:
         """sparse_gather_attention with this module's scale / dropout / fp32
