@@ -420,48 +420,92 @@ __global__ void __launch_bounds__(256) qb_hist_kernel(QbP p) {
 // each query block's queries in each bucket (so queries stay in position
 // order inside a bucket), and the instance's tile count
 __global__ void __launch_bounds__(256) qb_scan_kernel(QbP p) {
-    __shared__ int32_t part_q[256], part_t[256];
+    // thread = (bucket column, query-block group): with NB <= 256 the NB
+    // columns are split over 256 / NB groups of query blocks; with more
+    // buckets a thread takes NB / 256 columns over every block
+    __shared__ int32_t part[256];          // per thread: its sum, then its starting offset
+    __shared__ int32_t sq[256], st[256];   // per column: bucket count, tile count (scanned)
     const int inst = blockIdx.x;
+    const int tid = threadIdx.x;
     int bh, r, t;
     inst_decode(p, inst, bh, r, t);
     const int b = bh / p.Hq, h = bh % p.Hq, g = h / p.rep;
     const int64_t krow = ((int64_t)b * p.Hkv + g) * p.R + r;
     const int nblk = (p.N + 255) / 256;
     int32_t *hb = p.hcnt + (int64_t)inst * nblk * p.NB;
-    const int per = (p.NB + 255) / 256;
-    const int u0 = threadIdx.x * per;
-    int sq = 0, st = 0;
-    for (int u = u0; u < u0 + per && u < p.NB; ++u) {
-        int c = 0;
-        for (int k = 0; k < nblk; ++k) c += hb[(int64_t)k * p.NB + u];
-        p.cnt[(int64_t)inst * p.NB + u] = c;
-        sq += c;
-        if (c > 0 && p.bsize[krow * p.NB + u] > 0) st += (c + TQ - 1) / TQ;
+    const int ncol = p.NB < 256 ? p.NB : 256;           // NB is a power of two
+    const int per = p.NB / ncol;                        // buckets per column
+    const int ngrp = 256 / ncol;                        // query-block groups per column
+    const int col = tid % ncol, grp = tid / ncol;
+    const int kper = (nblk + ngrp - 1) / ngrp;
+    const int k0 = min(grp * kper, nblk), k1 = min(k0 + kper, nblk);
+    // 1: each thread's sum over its blocks (per == 1 whenever ngrp > 1)
+    if (per == 1) {
+        int s = 0;
+        for (int k = k0; k < k1; ++k) s += hb[(int64_t)k * p.NB + col];
+        part[tid] = s;
     }
-    part_q[threadIdx.x] = sq;
-    part_t[threadIdx.x] = st;
     __syncthreads();
-    if (threadIdx.x == 0) {
-        int aq = 0, at = 0;
-        for (int i = 0; i < 256; ++i) {
-            const int vq = part_q[i];
-            part_q[i] = aq;
-            aq += vq;
-            at += part_t[i];
+    // 2: per column, bucket counts, tile counts and the groups' offsets within
+    // their bucket
+    if (tid < ncol) {
+        int cq = 0, ct = 0;
+        if (per == 1) {
+            for (int gg = 0; gg < ngrp; ++gg) {
+                const int v = part[gg * ncol + tid];
+                part[gg * ncol + tid] = cq;
+                cq += v;
+            }
+            p.cnt[(int64_t)inst * p.NB + tid] = cq;
+            if (cq > 0 && p.bsize[krow * p.NB + tid] > 0) ct = (cq + TQ - 1) / TQ;
+        } else {
+            for (int u = tid * per; u < tid * per + per; ++u) {
+                int c = 0;
+                for (int k = 0; k < nblk; ++k) c += hb[(int64_t)k * p.NB + u];
+                p.cnt[(int64_t)inst * p.NB + u] = c;
+                cq += c;
+                if (c > 0 && p.bsize[krow * p.NB + u] > 0) ct += (c + TQ - 1) / TQ;
+            }
         }
-        p.tcnt[inst] = at;
+        sq[tid] = cq;
+        st[tid] = ct;
+    } else {
+        sq[tid] = 0;
+        st[tid] = 0;
     }
     __syncthreads();
-    int aq = part_q[threadIdx.x];
-    for (int u = u0; u < u0 + per && u < p.NB; ++u) {
-        p.off[(int64_t)inst * p.NB + u] = aq;
-        int base = aq;
-        for (int k = 0; k < nblk; ++k) {
-            const int c = hb[(int64_t)k * p.NB + u];
-            hb[(int64_t)k * p.NB + u] = base;
+    // 3: inclusive scans of the column counts (Hillis-Steele over 256)
+    for (int o = 1; o < 256; o <<= 1) {
+        const int yq = tid >= o ? sq[tid - o] : 0;
+        const int yt = tid >= o ? st[tid - o] : 0;
+        __syncthreads();
+        sq[tid] += yq;
+        st[tid] += yt;
+        __syncthreads();
+    }
+    if (tid == 0) p.tcnt[inst] = st[255];
+    // 4: bucket offsets and each block's first position in its bucket
+    const int cstart = col > 0 ? sq[col - 1] : 0;
+    if (per == 1) {
+        if (grp == 0) p.off[(int64_t)inst * p.NB + col] = cstart;
+        int base = cstart + part[tid];
+        for (int k = k0; k < k1; ++k) {
+            const int c = hb[(int64_t)k * p.NB + col];
+            hb[(int64_t)k * p.NB + col] = base;
             base += c;
         }
-        aq = base;
+    } else if (tid < ncol) {
+        int aq = cstart;
+        for (int u = tid * per; u < tid * per + per; ++u) {
+            p.off[(int64_t)inst * p.NB + u] = aq;
+            int base = aq;
+            for (int k = 0; k < nblk; ++k) {
+                const int c = hb[(int64_t)k * p.NB + u];
+                hb[(int64_t)k * p.NB + u] = base;
+                base += c;
+            }
+            aq = base;
+        }
     }
 }
 
