@@ -66,6 +66,7 @@ struct Dims {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 // ------------------------------------------------------------------ hashing
 struct HashP {
@@ -768,24 +769,40 @@ template <> struct Mfma16<f16_t> {
 };
 
 // MFMA rescore of one tile (up to 64 queries of one bucket x the bucket's
-// candidates in ascending id order, up to the tile's cutoff).  The block stages
-// each 64-candidate slice of K rows in LDS once (double-buffered, rows padded by
-// 16 bytes so the fragment reads are free of bank conflicts, in the row order of
-// rs_stage_row); wave w scores queries 16w..16w+15 against the slice as K . Q^T,
-// so each lane holds 2 x 8 consecutive candidates of one query and writes their
-// 16-bit score codes with two 16-byte stores.
-constexpr int RS_ROWB_PAD = 16;
+// candidates in ascending id order, up to the tile's cutoff).  The K rows of
+// each 32-candidate slice go from global memory straight into LDS (one
+// global_load_lds_dwordx4 per 1 KB: lane l of a wave load writes bytes
+// 16 l .. 16 l + 15 of it), in three buffers so slices j + 1 and j + 2 are in
+// flight while slice j is scored; wave w scores queries 16w..16w+15 against
+// the slice as K . Q^T, so each lane holds 8 consecutive candidates of one
+// query and writes their 16-bit score codes with one 16-byte store.  About
+// 26 KB of LDS and at most 80 registers per lane: 6 blocks per CU.
+constexpr int RS_SLICE = 32;   // candidates per staged K slice
 
 template <int D>
-__host__ __device__ constexpr int rs_row_bytes() { return D * 2 + RS_ROWB_PAD; }
+struct RsStage {
+    static constexpr int SEGS = D / 8;                          // 16-byte pieces per K row
+    static constexpr int RB = D * 2;                            // LDS bytes per row
+    static constexpr int NI = (RS_SLICE * SEGS + 63) / 64;      // 1 KB wave loads per slice
+    static constexpr int NIW = (NI + 3) / 4;                    // of them per wave (at most)
+    static constexpr int BUF = NI * 1024;                       // LDS bytes per slice buffer
+    static constexpr int W1 = SEGS >= 8 ? 1 : 8 / SEGS;        // rows per 128 bytes
+    // Rows are stored unpadded with their pieces rotated: piece x of LDS row R
+    // sits in slot (x + rot(R)) % SEGS.  A fragment read takes one piece of
+    // 16 consecutive rows 16 ct .. 16 ct + 15; with this rotation its 16 lanes
+    // hit 16 different 16-byte bank groups, and any 8 consecutive of them 8
+    static __device__ __forceinline__ int rot(int R) {
+        const int r = R % 16;
+        return (r / W1 + r / (W1 * SEGS)) % SEGS;
+    }
+};
 
-// LDS row of slice member m.  Tile ct of a slice multiplies LDS rows
-// 16 ct .. 16 ct + 15, and lane (li, lg) receives rows 4 lg .. 4 lg + 3 of each
-// tile; staging member 32 X + 8 a + 4 b + c at row 16 (2 X + b) + 4 a + c hands
-// lane (li, lg) the 8 consecutive members 32 X + 8 lg .. +7 in tiles 2 X, 2 X + 1,
-// which it stores as one 16-byte vector of 16-bit keys.
-__device__ __forceinline__ int rs_stage_row(int m) {
-    return (m & 0x23) | ((m & 0x04) << 2) | ((m & 0x18) >> 1);
+// Slice member held by LDS row R.  Tile ct of a slice multiplies LDS rows
+// 16 ct .. 16 ct + 15 and lane (li, lg) receives rows 16 ct + 4 lg .. + 3;
+// storing member 8 a + 4 b + c at row 16 b + 4 a + c hands lane (li, lg) the 8
+// consecutive members 8 lg .. 8 lg + 7 (tiles 0 and 1).
+__device__ __forceinline__ int rs_row_member(int R) {
+    return ((R & 12) << 1) | ((R & 16) >> 2) | (R & 3);
 }
 
 // two 16-bit score codes, a at the lower address
@@ -794,14 +811,20 @@ __device__ __forceinline__ uint32_t code_pair(float a, float b, float sc) {
     return ~(score_neg_code(a, sc) | (score_neg_code(b, sc) << 16));
 }
 
+typedef __attribute__((address_space(3))) void lds_void_t;
+
 template <typename T, int D>
-__global__ void __launch_bounds__(256) rescore_mfma_kernel(RsP p) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(6)))
+rescore_mfma_kernel(RsP p) {
     using V = typename Mfma16<T>::vec;
+    using S = RsStage<D>;
     constexpr int KS = (D + 31) / 32;          // k steps of 32
-    constexpr int RB = rs_row_bytes<D>();      // LDS bytes per staged row
-    constexpr int SEGS = D / 8;                // 16-byte segments per row
+    constexpr int SEGS = S::SEGS;
     __shared__ int nidx[TQ];
-    extern __shared__ __align__(16) unsigned char rs_lds[];   // [2][64][RB]
+    // the slice buffers are separate arrays, so the compiler can tell a load
+    // into one from the reads of another
+    __shared__ __align__(1024) unsigned char kb0[S::BUF], kb1[S::BUF], kb2[S::BUF];
+    extern __shared__ int32_t prl[];           // the tile's candidate ids
     RsTile tl;
     if (!rs_tile_fetch(p, tl)) return;
     const int inst = tl.inst, qb = tl.qb, qc = tl.qc, st = tl.st, nva = tl.nva;
@@ -810,17 +833,17 @@ __global__ void __launch_bounds__(256) rescore_mfma_kernel(RsP p) {
     const int b = bh / p.Hq, h = bh % p.Hq, g = h / p.rep;
     const int64_t prow = ((int64_t)b * p.Hkv + g) * p.R + r;
     const int tid = threadIdx.x;
-    const int wid = tid / SSA_WAVE;
+    const int wid = __builtin_amdgcn_readfirstlane(tid / SSA_WAVE);
     const int lane = lane_id();
     const int li = lane % 16, lg = lane / 16;
     const T *qbase = (const T *)p.q + b * p.qsb + h * p.qsh;
     const T *kbase = (const T *)p.k + b * p.ksb + g * p.ksh;
     const int32_t *pr = p.sid + prow * p.M + st;
-    // the tile's queries and candidate ids (the list's members, ascending)
-    // load together, before one barrier
-    int32_t *prl = reinterpret_cast<int32_t *>(rs_lds + 2 * (64 * RB));
+    // the tile's queries and candidate ids (the list's members, ascending,
+    // then INT_MAX up to a whole slice) load together, before one barrier
     if (tid < TQ) nidx[tid] = tid < qc ? p.qlist[(int64_t)inst * p.N + qb + tid] : 0;
-    for (int c = tid; c < nva; c += 256) prl[c] = pr[c];
+    const int nvp = (nva + RS_SLICE - 1) / RS_SLICE * RS_SLICE;
+    for (int c = tid; c < nvp; c += 256) prl[c] = c < nva ? pr[c] : INT_MAX;
     __syncthreads();
 
     // this wave's 16 queries as the B operand (column li = query 16*wid + li)
@@ -839,118 +862,140 @@ __global__ void __launch_bounds__(256) rescore_mfma_kernel(RsP p) {
     const bool active = 16 * wid < qc;
     // the query's code scale (written by the aux kernel)
     const float qsc = qok ? p.aux[((int64_t)bhl * p.N + nidx[qrow]) * p.NA + p.NA - 1] : 1.f;
-
-    // per 64-candidate slice j: the K rows of slice j + 1 are loaded into
-    // registers, slice j (in LDS) is scored, its score codes stored, and the
-    // loaded rows committed to the other LDS buffer
     const int nv = rs_tile_cutoff(prl, nva, nidx, qc, p.causal);
-    constexpr int PER = (64 * SEGS + 255) / 256;
-    // rows are addressed by 32-bit byte offsets from the head's base (the
-    // dispatcher picks this kernel only when they fit); rows past the slice
-    // read row 0 (in range, never scored)
+    const int nsl = (nv + RS_SLICE - 1) / RS_SLICE;
+
+    // This lane's part of the wave's slice loads: wave load i = wid + 4 t
+    // fills bytes 1024 i .. of a buffer, its lane the 16-byte slot
+    // g = 64 i + lane, i.e. slot g % SEGS of LDS row g / SEGS (rows past the
+    // slice, only at D = 8, land in the buffer's unused half).  Rows are
+    // addressed by 32-bit byte offsets from the head's base (the dispatcher
+    // picks this kernel only when they fit); pieces past the head dim load
+    // piece 0 and slots past the list the last row (neither is used).
     const uint32_t rowb = (uint32_t)(p.ksn * (int64_t)sizeof(T));
-    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-    u32x4 sa[PER];
-#define RS_FETCH(C0)                                                                         \
-    _Pragma("unroll") for (int i = 0; i < PER; ++i) {                                        \
-        const int x = tid + 256 * i;                                                         \
-        const int row = x / SEGS, seg = x % SEGS;                                            \
-        const int cr = (C0) + row;  /* the read is clamped in range; the select drops it */ \
-        const int rid = prl[max(min(cr, nv - 1), 0)];                                        \
-        const int id = (x < 64 * SEGS && cr < nv) ? rid : 0;                                 \
-        /* segments past the head dim read segment 0 (never multiplied) */                  \
-        const uint32_t sg = seg * 8 < p.d ? (uint32_t)seg : 0u;                              \
-        sa[i] = *reinterpret_cast<const u32x4 *>((const char *)kbase +                       \
-                                                 (__umul24((uint32_t)id, rowb) + sg * 16u)); \
+    int lmem[S::NIW];
+    uint32_t lseg[S::NIW];
+#pragma unroll
+    for (int t = 0; t < S::NIW; ++t) {
+        const int gs = 64 * (wid + 4 * t) + lane;
+        const int R = gs / SEGS;
+        const int x = (gs % SEGS + SEGS - S::rot(R)) % SEGS;
+        lmem[t] = rs_row_member(R % RS_SLICE);
+        lseg[t] = (uint32_t)(x * 8 < p.d ? x : 0) * 16u;
     }
-#define RS_COMMIT(BUF)                                                                       \
-    _Pragma("unroll") for (int i = 0; i < PER; ++i) {                                        \
-        const int x = tid + 256 * i;                                                         \
-        if (x < 64 * SEGS)                                                                   \
-            *reinterpret_cast<u32x4 *>(rs_lds + (BUF) * (64 * RB) +                          \
-                                       rs_stage_row(x / SEGS) * RB + (x % SEGS) * 16) = sa[i]; \
-    }
-    const int nsl = (nv + 63) / 64;
-    RS_FETCH(0)
-    RS_COMMIT(0)
-    __syncthreads();
-    // Each lane stores its 2 x 8 score codes as 16-byte vectors through a raw
+    // (the member ids are read before the first load: a read of LDS after a
+    // load into LDS waits for that load)
+    auto stage = [&](unsigned char *buf, int c0) __attribute__((always_inline)) {
+        uint32_t ro[S::NIW];
+#pragma unroll
+        for (int t = 0; t < S::NIW; ++t)
+            ro[t] = __umul24(min((uint32_t)prl[c0 + lmem[t]], (uint32_t)(p.M - 1)), rowb) + lseg[t];
+#pragma unroll
+        for (int t = 0; t < S::NIW; ++t) {
+            const int i = wid + 4 * t;
+            if (S::NI % 4 == 0 || i < S::NI)
+                __builtin_amdgcn_global_load_lds((const void *)((const char *)kbase + ro[t]),
+                                                 (lds_void_t *)(buf + 1024 * i), 16, 0, 0);
+        }
+    };
+    if (nsl > 0) stage(kb0, 0);
+    if (nsl > 1) stage(kb1, RS_SLICE);
+
+    // Each lane stores its 8 score codes as a 16-byte vector through a raw
     // buffer over the instance's rows (rows are padded to a multiple of 64
     // members).  A group of 8 members is stored only when its first member is
-    // below the lane's query (causal; the select kernel reads no further) and
-    // the lane has a query: other lanes give an offset past the buffer's end,
-    // which the hardware drops.  So every iteration issues exactly these
-    // stores after its loads, and the commit waits for the loads only.
-    int cq = qok ? nv : 0;             // members of this lane's query row to store
-    if (qok && p.causal) {
-        // members with an id below the query: a binary search of the ascending ids
-        const int nq = nidx[qrow];
-        int lo = 0, hi = nv;
-        while (lo < hi) {
-            const int mid = (lo + hi) >> 1;
-            if (prl[mid] < nq) lo = mid + 1;
-            else hi = mid;
-        }
-        cq = lo;
-    }
+    // below the lane's query (causal; the select kernel reads no further), is
+    // on the list (not INT_MAX) and the lane has a query: other lanes give an
+    // offset past the buffer's end, which the hardware drops.  So every slice
+    // issues exactly one store per wave after its loads, and waiting for a
+    // slice's loads leaves the last store in flight.
+    const int nqe = !qok ? INT_MIN : p.causal ? nidx[qrow] : INT_MAX;
     const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(
         (void *)(p.S + (int64_t)inst * p.N * p.Cs), (short)0, (int)((int64_t)p.N * p.Cs * 2),
         SSA_BUF_FLAGS);
     // make_dims keeps an instance's rows (N * Cs * 2 bytes) below 2^31
     const uint32_t sbase = ((uint32_t)(qb + qrow) * (uint32_t)p.Cs + 8u * lg) * 2u;
-    for (int j = 0; j < nsl; ++j) {
-        const int c0 = 64 * j;
-        const bool more = j + 1 < nsl;
-        if (more) { RS_FETCH(c0 + 64) }
-        u32x4 kq[2] = {};
+    // TAIL: k steps reach past the head dim, so the pieces there are zeroed
+    // (they hold piece 0 of the row; its product with the zero q pieces would
+    // still turn an infinite element into NaN)
+    const int rrot = S::rot(li);
+    auto score = [&](const unsigned char *kl, int c0, auto tail) __attribute__((always_inline)) {
+        constexpr bool TAIL = decltype(tail)::value;
+        u32x4_t kq = {};
         if (active) {
-            const unsigned char *kl = rs_lds + (j & 1) * (64 * RB);
-            auto frag = [&](int s, V (&kf)[4]) __attribute__((always_inline)) {
-                const int e0 = 32 * s + 8 * lg;
-#pragma unroll
-                for (int ct = 0; ct < 4; ++ct)
-                    kf[ct] = e0 < p.d ? __builtin_bit_cast(
-                                          V, *reinterpret_cast<const uint4 *>(
-                                                 kl + (ct * 16 + li) * RB + e0 * 2))
-                                      : __builtin_bit_cast(V, make_uint4(0, 0, 0, 0));
-            };
-            // fragments two k steps deep: the reads of step s + 2 overlap the
-            // products of step s
-            V kf[2][4];
-            frag(0, kf[0]);
-            if (KS > 1) frag(1, kf[1]);
-            f32x4_t acc[4];
-#pragma unroll
-            for (int ct = 0; ct < 4; ++ct) acc[ct] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            f32x4_t acc[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
+            // rows li and 16 + li share their rotation
+            const unsigned char *kr = kl + li * S::RB;
 #pragma unroll
             for (int s = 0; s < KS; ++s) {
+                const int x = 4 * s + lg;      // the lane's 16-byte piece of the k step
+                const int slot = (x + rrot) % SEGS;
 #pragma unroll
-                for (int ct = 0; ct < 4; ++ct)
-                    acc[ct] = Mfma16<T>::mma(kf[s & 1][ct], qf[s], acc[ct]);
-                if (s + 2 < KS) frag(s + 2, kf[s & 1]);
+                for (int ct = 0; ct < 2; ++ct) {
+                    uint4 kv = *reinterpret_cast<const uint4 *>(kr + 16 * ct * S::RB + slot * 16);
+                    if constexpr (TAIL) {
+                        const uint32_t m = 8 * x < p.d ? ~0u : 0u;
+                        kv = make_uint4(kv.x & m, kv.y & m, kv.z & m, kv.w & m);
+                    }
+                    acc[ct] = Mfma16<T>::mma(__builtin_bit_cast(V, kv), qf[s], acc[ct]);
+                }
             }
-            // lane (li, lg) holds members c0 + 32 X + 8 lg + 4 b + rr of query li
-            // in acc[2 X + b][rr]
-#pragma unroll
-            for (int X = 0; X < 2; ++X)
-                kq[X] = u32x4{code_pair(acc[2 * X][0], acc[2 * X][1], qsc),
-                              code_pair(acc[2 * X][2], acc[2 * X][3], qsc),
-                              code_pair(acc[2 * X + 1][0], acc[2 * X + 1][1], qsc),
-                              code_pair(acc[2 * X + 1][2], acc[2 * X + 1][3], qsc)};
+            // lane (li, lg) holds members c0 + 8 lg + 4 ct + rr of query li in acc[ct][rr]
+            kq = u32x4_t{code_pair(acc[0][0], acc[0][1], qsc), code_pair(acc[0][2], acc[0][3], qsc),
+                         code_pair(acc[1][0], acc[1][1], qsc), code_pair(acc[1][2], acc[1][3], qsc)};
         }
-        // every wave issues the same two stores (dropped where out of range)
-#pragma unroll
-        for (int X = 0; X < 2; ++X) {
-            const int c = c0 + 32 * X + 8 * lg;
-            const uint32_t off = c < cq ? sbase + (uint32_t)(c0 + 32 * X) * 2u : 0x80000000u;
-            __builtin_amdgcn_raw_buffer_store_b128(kq[X], srs, off, 0, 0);
+        // every wave issues the same store (dropped where out of range)
+        const uint32_t off = prl[c0 + 8 * lg] < nqe ? sbase : 0x80000000u;
+        __builtin_amdgcn_raw_buffer_store_b128(kq, srs, off, 2 * c0, 0);
+    };
+    // The barrier before slice j: each wave first waits for its own loads of
+    // the slice (the hardware writes a load's data to LDS before it counts
+    // the load done), so after the barrier the whole slice is in LDS; the
+    // reads of the buffer the next loads overwrite (slice j - 1's) were
+    // consumed by the MFMAs before it.  A wave's vector memory operations
+    // issue in the order: loads of slice j, store of slice j - 2, loads of
+    // slice j + 1, store of slice j - 1, and complete in order, so the wait
+    // leaves the ones after the loads of slice j in flight: at least NW loads
+    // per slice and wave (waves with more wait a little longer than they
+    // need).  Before slice 0 everything is waited for (the q rows and slice 1
+    // too: the compiler then knows the q rows have landed).  The wait is
+    // the builtin (so the compiler counts it and adds none of its own),
+    // fenced by empty asm statements that keep memory operations on their
+    // side of it, and the barrier a bare s_barrier: the workgroup fence of
+    // __syncthreads would also wait for the score stores.
+    constexpr int NW = S::NI / 4;
+    auto slice_barrier = [&](int j) __attribute__((always_inline)) {
+        const int after = j == 0 ? 0 : (j >= 2) + (j + 1 < nsl ? NW : 0) + 1;
+        asm volatile("" ::: "memory");
+        // vmcnt(after); lgkmcnt and expcnt not waited for
+        if (after == 0) __builtin_amdgcn_s_waitcnt(0x0F70);
+        else if (after == 1) __builtin_amdgcn_s_waitcnt(0x0F71);
+        else if (after == 2) __builtin_amdgcn_s_waitcnt(0x0F72);
+        else if (after == 3) __builtin_amdgcn_s_waitcnt(0x0F73);
+        else __builtin_amdgcn_s_waitcnt(0x0F74);
+        asm volatile("s_barrier" ::: "memory");
+    };
+    static_assert(NW <= 2, "vmcnt immediates above cover at most 4 operations");
+    auto slices = [&](auto tail) __attribute__((always_inline)) {
+        for (int j = 0; j < nsl; j += 3) {
+            // slice j is in kb0, j + 1 in kb1, j + 2 in kb2; the buffer a
+            // stage fills was last read by the slice before the barrier
+            slice_barrier(j);
+            if (j + 2 < nsl) stage(kb2, RS_SLICE * (j + 2));
+            score(kb0, RS_SLICE * j, tail);
+            if (j + 1 >= nsl) break;
+            slice_barrier(j + 1);
+            if (j + 3 < nsl) stage(kb0, RS_SLICE * (j + 3));
+            score(kb1, RS_SLICE * (j + 1), tail);
+            if (j + 2 >= nsl) break;
+            slice_barrier(j + 2);
+            if (j + 4 < nsl) stage(kb1, RS_SLICE * (j + 4));
+            score(kb2, RS_SLICE * (j + 2), tail);
         }
-        // the other buffer was last read in iteration j - 1, before its barrier
-        if (more) { RS_COMMIT((j + 1) & 1) }
-        __syncthreads();
-    }
-#undef RS_FETCH
-#undef RS_COMMIT
+    };
+    // below D = 32 the k steps also cover pieces past the row (at piece 0)
+    if (p.d == D && D % 32 == 0) slices(std::false_type{});
+    else slices(std::true_type{});
 }
 
 // ------------------------------------------------------------------ sorted candidate lists
@@ -2988,7 +3033,8 @@ int launch_rescore(const RsP &rp, int64_t grid, hipStream_t st) {
 
 template <typename T, int Dh>
 int launch_rescore_mfma(const RsP &rp, int64_t grid, hipStream_t st) {
-    const size_t lds = (size_t)2 * 64 * rs_row_bytes<Dh>() + (size_t)rp.C * 4;
+    // the member ids, rounded up to a whole slice (the slice buffers are static)
+    const size_t lds = (size_t)ceil_div(rp.C, RS_SLICE) * RS_SLICE * 4;
     SSA_CHECK_HIP(hipFuncSetAttribute((const void *)rescore_mfma_kernel<T, Dh>,
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     hipLaunchKernelGGL((rescore_mfma_kernel<T, Dh>), dim3((unsigned)grid), dim3(256), lds, st, rp);

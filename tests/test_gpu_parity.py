@@ -80,6 +80,9 @@ GRAPH_CASES = [
     ("head_dim_80_cross", 2, 2, 1, 60, 100, 80, 2, 4, 1, 24, 4, 2, False, True),
     ("head_dim_112", 1, 2, 2, 128, 128, 112, 2, 4, 0, 24, 3, 2, True, False),
     ("head_dim_48", 1, 2, 1, 96, 96, 48, 2, 3, 0, 20, 2, 1, False, False),
+    # the smallest and the largest matrix-core rescore instances
+    ("head_dim_8", 1, 2, 2, 80, 80, 8, 2, 3, 0, 16, 2, 1, True, False),
+    ("head_dim_128", 1, 2, 1, 256, 256, 128, 2, 4, 1, 32, 4, 2, True, False),
 ]
 
 
@@ -174,12 +177,10 @@ def test_lsh_builder_exact_tier_huge_k_replay_outside_lds():
     np.testing.assert_array_equal(got.cpu().numpy().reshape(B * H, N, -1), ref["idx"])
 
 
-@pytest.mark.parametrize("case", [GRAPH_CASES[1]] + [c for c in GRAPH_CASES
-                                                    if c[0].startswith("head_dim")],
-                         ids=lambda c: c[0])
+@pytest.mark.parametrize("case", GRAPH_CASES, ids=lambda c: c[0])
 def test_graph_bf16_inputs_exact_tier(case):
     """bf16 q/k holding small integers are exact: same graph as fp32 (the
-    matrix-core rescore, aux and exact-key paths)."""
+    matrix-core rescore, aux and exact-key paths, every head-dim instance)."""
     attn, got, got_v, ref, (B, H, N, M, K, w, cross, causal, glob) = _graph_case(
         case, 5, dtype=torch.bfloat16)
     win = (np.zeros((N, 0), np.int64) if cross else attn.win_builder(N, M, "cpu").numpy())
