@@ -2899,7 +2899,9 @@ int make_dims(const ssa_graph_args *a, Dims &D, bool need_q = true, int64_t ws_c
                       "65535 slots the exact tie replay supports", D.kk, D.chunk);
         return SSA_E_UNSUP;
     }
-    // chunk the query heads so the score buffer stays near 2 GiB
+    // chunk the query heads so the score buffer stays near 8 GiB (a chunk's
+    // select and rescore grids grow with it: one head of the 32k MQA workload
+    // per chunk leaves a long tail per launch)
     const int64_t per_bh = (int64_t)a->N * D.nlists * D.Cs * 2;
     if (per_bh >= ((int64_t)4 << 30)) {
         ssa_set_error("build_graph: one head's score table (N * R * id sets * C * 2 = %lld bytes) "
@@ -2913,7 +2915,7 @@ int make_dims(const ssa_graph_args *a, Dims &D, bool need_q = true, int64_t ws_c
                       "below 2 GiB", (long long)a->N * D.Cs * 2);
         return SSA_E_UNSUP;
     }
-    int64_t nbh = ((int64_t)2 << 30) / per_bh;
+    int64_t nbh = ((int64_t)8 << 30) / per_bh;
     if (nbh < 1) nbh = 1;
     if (nbh > D.BH) nbh = D.BH;
     D.nbh_chunk = (int)nbh;
