@@ -425,9 +425,12 @@ class SparseAttention(nn.Module):
                                        fp32_attn_weights=self.config.fp32_attn_weights)
 
     def forward(self, x: torch.Tensor, key_value: Optional[torch.Tensor] = None,
-                attention_mask: Optional[torch.Tensor] = None, return_stats: bool = False
-                ) -> Tuple[torch.Tensor, dict]:
-        """(out (B, N, d_model), stats or {}) (sparse_attention.py:1420-1510)."""
+                attention_mask: Optional[torch.Tensor] = None, return_stats: bool = False,
+                *, _defer_stats: bool = False) -> Tuple[torch.Tensor, dict]:
+        """(out (B, N, d_model), stats or {}) (sparse_attention.py:1420-1510).
+        ``_defer_stats`` (for the layer stacks below): padding_fraction is left
+        as a pending device count for ``_resolve_stats``, so a stack syncs with
+        the host once instead of once per layer."""
         if attention_mask is not None:
             raise ValueError(
                 "SparseAttention does not accept an external attention_mask. Use "
@@ -455,22 +458,39 @@ class SparseAttention(nn.Module):
             return out_proj, {}
         peak_sparse = B * self.H * N * self.K * self.d_head
         peak_full = B * self.H * N * M * self.d_head
+        pad = _PendingFraction(~valid if valid is not None else neighbors < 0)
         return out_proj, {
             "neighbors_shape": tuple(neighbors.shape),
             "peak_sparse_elems": peak_sparse,
             "peak_full_elems": peak_full,
             "compression": peak_full / peak_sparse,
-            "padding_fraction": _padding_fraction(~valid if valid is not None
-                                                  else neighbors < 0),
+            "padding_fraction": pad if _defer_stats else pad.value(),
         }
 
 
-def _padding_fraction(invalid: torch.Tensor) -> float:
+class _PendingFraction:
     """Mean of a boolean mask as the reference's CPU ``.float().mean()``
     rounds it: the exact count divided by the element count in fp32 (the
-    device's mean multiplies by a rounded reciprocal instead)."""
-    count = int(invalid.sum().item())
-    return float(np.float32(count) / np.float32(max(invalid.numel(), 1)))
+    device's mean multiplies by a rounded reciprocal instead).  The count is
+    taken on the device as bytes summed in int32 while that cannot overflow (a
+    bool tensor's own sum first copies it to int64); ``value()`` waits for it."""
+
+    def __init__(self, invalid: torch.Tensor):
+        self.numel = invalid.numel()
+        acc = torch.int32 if self.numel < (1 << 31) else torch.int64
+        self.count = invalid.view(torch.uint8).sum(dtype=acc)
+
+    def value(self) -> float:
+        return float(np.float32(int(self.count.item())) / np.float32(max(self.numel, 1)))
+
+
+def _resolve_stats(stats_list):
+    """Replace pending padding fractions by their values (one host sync)."""
+    for st in stats_list:
+        pad = st.get("padding_fraction")
+        if isinstance(pad, _PendingFraction):
+            st["padding_fraction"] = pad.value()
+    return stats_list
 
 
 # ---------------------------------------------------------------------------- transformer
@@ -487,8 +507,9 @@ class SparseTransformerLayer(nn.Module):
         self.norm1 = nn.LayerNorm(d)
         self.norm2 = nn.LayerNorm(d)
 
-    def forward(self, x, return_stats: bool = False):
-        a, stats = self.attn(self.norm1(x), return_stats=return_stats)
+    def forward(self, x, return_stats: bool = False, *, _defer_stats: bool = False):
+        a, stats = self.attn(self.norm1(x), return_stats=return_stats,
+                             _defer_stats=_defer_stats)
         return x + a + self.ff(self.norm2(x + a)), stats
 
 
@@ -507,9 +528,9 @@ class SparseTransformer(nn.Module):
             x = self.embed(x)
         stats_list = []
         for layer in self.layers:
-            x, stats = layer(x, return_stats=return_stats)
+            x, stats = layer(x, return_stats=return_stats, _defer_stats=True)
             stats_list.append(stats)
-        return self.norm(x), stats_list
+        return self.norm(x), _resolve_stats(stats_list)
 
 
 # ---------------------------------------------------------------------------- graph reuse
@@ -599,9 +620,9 @@ class CachedGraphSparseTransformer(nn.Module):
                 stats_list.append({
                     "neighbors_shape": tuple(nb.shape),
                     "compression": peak_full / peak_sparse,
-                    "padding_fraction": _padding_fraction(~va),
+                    "padding_fraction": _PendingFraction(~va),
                     "graph_recomputed": recompute,
                 })
             else:
                 stats_list.append({})
-        return self.norm(h), stats_list
+        return self.norm(h), _resolve_stats(stats_list)
