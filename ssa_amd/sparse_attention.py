@@ -510,7 +510,9 @@ class SparseTransformerLayer(nn.Module):
     def forward(self, x, return_stats: bool = False, *, _defer_stats: bool = False):
         a, stats = self.attn(self.norm1(x), return_stats=return_stats,
                              _defer_stats=_defer_stats)
-        return x + a + self.ff(self.norm2(x + a)), stats
+        # x + a + ff(norm2(x + a)) evaluates (x + a) + ff(...): one x + a serves both
+        h = x + a
+        return h + self.ff(self.norm2(h)), stats
 
 
 class SparseTransformer(nn.Module):
@@ -562,7 +564,8 @@ def measure_cross_layer_overlap(model: "SparseTransformer", x: torch.Tensor) -> 
         graphs.append((nb.detach(), va.detach()))
         out = attn.apply_graph(q, k, v, nb, va)
         a = attn.Wo(attn._merge(out))
-        h = h + a + layer.ff(layer.norm2(h + a))
+        h = h + a
+        h = h + layer.ff(layer.norm2(h))
     overlaps = [neighbor_overlap(graphs[i][0], graphs[i + 1][0], graphs[i][1], graphs[i + 1][1])
                 for i in range(len(graphs) - 1)]
     return {
@@ -613,7 +616,8 @@ class CachedGraphSparseTransformer(nn.Module):
                 nb, va = cached
             out = attn.apply_graph(q, k, v, nb, va)
             a = attn.Wo(attn._merge(out))
-            h = h + a + layer.ff(layer.norm2(h + a))
+            h = h + a
+            h = h + layer.ff(layer.norm2(h))
             if return_stats:
                 peak_sparse = B * attn.H * N * attn.K * attn.d_head
                 peak_full = B * attn.H * N * N * attn.d_head
