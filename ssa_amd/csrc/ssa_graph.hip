@@ -1607,6 +1607,10 @@ constexpr int SEL_CAP_SMALL = 384, SEL_CAP_LARGE = 512, SEL_CAP_LARGE_KK = 160;
 //   LSH mode: ekey/eval/eslot [kk] the selected entries
 constexpr int SEL_PIPE = 2;            // chunks per group in pass 1
 // ckey + cval, which also hold the overflow path's second seen bitmap
+// seen bitmap over M key ids, in 32-bit words rounded up to an even count
+// (at M = 8192 the select kernel's per-wave words then come to 1,280: 8 waves
+// per SIMD fill the 160 KB of LDS exactly)
+__host__ __device__ inline int sel_bitmap_words(int M) { return ((M + 31) / 32 + 1) & ~1; }
 __host__ __device__ inline int sel_buf_words(int words, int cap) {
     return 2 * (cap + 64) > words ? 2 * (cap + 64) : words;
 }
@@ -2825,7 +2829,7 @@ Layout plan(const Dims &D) {
     {
         // the replay's per-wave arrays, when they do not fit LDS
         const int W = D.kk + D.chunk;
-        const int words = ((D.M + 31) / 32 + 2) & ~1;
+        const int words = sel_bitmap_words(D.M);
         L.rpscr = take(replay_fits_lds(W, words)
                            ? 0
                            : replay_glb_blocks(W, words) * RP_WAVES * rp_lds_words(W, words) * 4);
@@ -3408,7 +3412,7 @@ int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char 
         sp.CPL = D.CPL; sp.nlists = D.nlists; sp.Hq = D.Hq; sp.Hkv = D.Hkv; sp.rep = D.rep;
         sp.G = D.G; sp.kk = D.kk; sp.window = a->window; sp.causal = a->causal;
         sp.cross = a->is_cross; sp.mode = a->mode; sp.total_k = a->total_k; sp.Kw = D.Kw;
-        sp.Kout = D.Kout; sp.bh0 = (int)bh0; sp.words = ((D.M + 31) / 32 + 2) & ~1;
+        sp.Kout = D.Kout; sp.bh0 = (int)bh0; sp.words = sel_bitmap_words(D.M);
         sp.Call = D.Call; sp.rows = (int64_t)nbh * D.N;
         sp.out_idx = a->out_idx; sp.out_valid = a->out_valid; sp.ties = a->out_ties;
         sp.out_idx32 = a->mode == SSA_GRAPH_FULL ? a->out_idx32 : nullptr;

@@ -89,7 +89,7 @@ def test_argument_errors_are_reported_without_a_gpu():
 # lists, leaf bits, the partition stack, the seen bitmap, glob scores); two
 # rows share a workgroup's 160 KiB of LDS (minus 512 bytes of static data).
 def _replay_words(W, M):
-    words = ((M + 31) // 32 + 2) & ~1
+    words = ((M + 31) // 32 + 1) & ~1
     return (3 * W + (W + 31) // 32 + 1 + 3 * 64 + words + 64 + 1) & ~1
 
 
