@@ -61,6 +61,8 @@ struct Dims {
     int nbh_chunk;
     int chunk;         // width of the reference's running top-k chunks (:903)
     int Cs;            // score row stride: min(C, M) rounded up to 64 members
+    int rpw_blocks;    // blocks of the workgroup tie replay (0: the per-wave replay)
+    int rpw_nsim;      // its replaying waves per block
 };
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -2598,6 +2600,7 @@ __device__ void rp_sort(const RpArr &a, uint16_t *TL, uint16_t *TR, uint32_t *lb
     for (int i = lane; i < nl; i += SSA_WAVE) {
         const int s0 = TL[i];
         const int e = i + 1 < nl ? (int)TL[i + 1] : l;
+        // a leaf above 16 entries was heap-sorted (the insertion sort leaves it)
         rp_insertion(a, s0, e);
     }
     rp_sync();
@@ -2607,14 +2610,11 @@ __device__ void rp_sort(const RpArr &a, uint16_t *TL, uint16_t *TR, uint32_t *lb
 // words per resident wave) instead of LDS, for rows whose kk + chunk slots do
 // not fit; the same code runs on either (all accesses of a wave's arrays come
 // from that wave, whose stores its own later loads see after rp_sync).
-// WIDE: the exact keys of a chunk with all four MFMA rounds' K rows in flight
-// (exact_keys_wide) -- a shorter chain per row for many more registers, so
-// fewer rows in flight.  Both instances are launched; a wide instance
-// replays only when at most wide_max rows are tied (they are all resident
-// at once), the narrow one only when more are (wide_max < 0: always).
-template <typename T, bool LSH_MODE, bool GLB, bool WIDE>
+// Rows are taken only when more than `skip_max` are tied (fewer go to the
+// workgroup replay; skip_max < 0: always).
+template <typename T, bool LSH_MODE, bool GLB>
 __global__ void __launch_bounds__(RP_WAVES * SSA_WAVE)
-topk_replay_kernel(SelP p, int chunk, int W, uint32_t *gscr, int wide_max) {
+topk_replay_kernel(SelP p, int chunk, int W, uint32_t *gscr, int skip_max) {
     extern __shared__ uint32_t rp_smem[];
     const int wid = threadIdx.x / SSA_WAVE;
     const int lane = lane_id();
@@ -2633,7 +2633,7 @@ topk_replay_kernel(SelP p, int chunk, int W, uint32_t *gscr, int wide_max) {
 
     const int total = (int)gridDim.x * RP_WAVES;
     const int cnt = *p.tie_count;
-    if (WIDE ? cnt > wide_max : cnt <= wide_max) return;
+    if (cnt <= skip_max) return;
     const int kk = p.kk;
     for (int it = (int)blockIdx.x * RP_WAVES + wid; it < cnt; it += total) {
         const int64_t row = p.tie_list[it];          // bh * N + n, over all query heads
@@ -2698,9 +2698,7 @@ topk_replay_kernel(SelP p, int chunk, int W, uint32_t *gscr, int wide_max) {
                     // exact keys with the rescore's arithmetic (the table holds
                     // only their prefixes); the query itself scores as in aux
                     const bool xk = keep && !(p.causal && v == n);
-                    uint32_t ex;
-                    if constexpr (WIDE) ex = exact_keys_wide<T, 4>(p, qr, kb, v, xk);
-                    else ex = exact_keys<T>(p, qr, kb, v, xk);
+                    const uint32_t ex = exact_keys<T>(p, qr, kb, v, xk);
                     if (keep) sk = xk ? ex : kself;
                 } else {
                     // empty bucket: glob ++ 0, all valid; duplicates resolved in slot order
@@ -2765,6 +2763,480 @@ topk_replay_kernel(SelP p, int chunk, int W, uint32_t *gscr, int wide_max) {
     }
 }
 
+// ---- tie replay, one workgroup per row
+// The running top-k of the reference (sparse_attention.py:904-922) holds after
+// chunk s the kk smallest rank keys of chunks 0..s in sorted order (nth_element
+// + sort of the first kk - 1, or partial_sort): the key array of every state
+// S_s follows from the stream alone.  Only which candidate sits in which of
+// several equal keys depends on the comparisons and swaps made, and those look
+// at keys only.  So chunk s replays by itself, on S_{s-1}'s keys ++ the chunk's
+// keys with input positions as payload, into a map pi_s from output slot to
+// input position; where the first kk + 1 merged keys of a chunk hold no two
+// equal finite keys, the sorted merge gives the same map.  For a graph (a set)
+// only the ties at the final kk-th key matter: other equal keys are all kept
+// or all dropped, so only the chunks where that key is tied are replayed.  A
+// row runs as
+//   1. the stream: each slot's key id and validity, its first occurrence (the
+//      smallest slot holding the id, by atomicMin: the reference's stable sort
+//      by id, :884-890), then per chunk the exact keys and the chunk's finite
+//      keys sorted -- all waves;
+//   2. the states' keys by merging each state with its chunk's sorted head,
+//      noting the tied keys per chunk -- wave 0;
+//   3. the chunks to replay, replayed as the reference runs them, one wave each;
+//   4. every finite output slot followed back through the maps to its stream
+//      slot, then the emit -- wave 0.
+// For many tied rows the per-wave replay (one row per wave, more rows in
+// flight) is faster; a launch takes its rows only when at most `cap` are tied.
+constexpr int RPW_WAVES = 8;
+constexpr int RPW_THREADS = RPW_WAVES * SSA_WAVE;
+constexpr int RPW_MAX_BLOCKS = 1024;
+constexpr int RPW_TV = 4;            // tied key values noted per chunk
+constexpr uint32_t RPW_VALID = 1u << 31, RPW_EMPTY = 1u << 30, RPW_OWNER = 1u << 29,
+                   RPW_VMASK = RPW_OWNER - 1u;
+
+// LDS of one replaying wave: keys and payload (W each), TL/TR, leaf bits, stack
+__host__ __device__ inline int rpw_slot_words(int W) {
+    return (3 * W + (W + 31) / 32 + 1 + 3 * RP_STACK + 1) & ~1;
+}
+// LDS shared by the workgroup: bitmap, glob scores, list table, state keys,
+// merge output, per chunk (head length, tie count, tied keys, input state,
+// marked list), misc, keep bits, the maps (u16)
+__host__ __device__ inline int rpw_shared_words(int words, int nls, int kk, int nch, int64_t Call) {
+    return (int)((words + SSA_WAVE + 2 * nls + kk + 2 * (kk + 1) + (int64_t)nch * (4 + RPW_TV) + 8 +
+                  (Call + 31) / 32 + ((int64_t)nch * kk + 1) / 2 + 1) & ~1);
+}
+// workspace words of one block: stream keys and ids, first occurrences, the
+// tied chunks' input state keys, each chunk's sorted head (kk + 1 keys, tags)
+__host__ __device__ inline int64_t rpw_scratch_words(int64_t Call, int M, int kk, int nch) {
+    return (2 * Call + M + (int64_t)nch * kk + 2 * (int64_t)nch * (kk + 1) + 63) / 64 * 64;
+}
+
+// a wave's LDS stores seen by its later loads, without waiting for its
+// global loads (rp_sync waits for every counter)
+__device__ __forceinline__ void rpw_lsync() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);    // lgkmcnt(0)
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// one wave sorts k[0, e) ascending, t alongside (bitonic with a mirrored first
+// step, which sorts any e when pairs reaching past e are skipped)
+__device__ void rpw_sort(uint32_t *k, uint32_t *t, int e) {
+    const int lane = lane_id();
+    for (int size = 2; size < 2 * e; size <<= 1) {
+        for (int j = size >> 1; j > 0; j >>= 1) {
+            for (int i0 = 0; i0 < e; i0 += SSA_WAVE) {
+                const int i = i0 + lane;
+                const int pi = j == (size >> 1) ? (i ^ (size - 1)) : (i ^ j);
+                if (i < e && pi > i && pi < e) {
+                    const uint32_t a = k[i], b = k[pi];
+                    if (b < a) {
+                        k[i] = b;
+                        k[pi] = a;
+                        const uint32_t ta = t[i];
+                        t[i] = t[pi];
+                        t[pi] = ta;
+                    }
+                }
+            }
+            rp_sync();
+        }
+    }
+}
+
+// entries of sorted k[0, n) below x (or at most x)
+__device__ __forceinline__ int rpw_rank(const uint32_t *k, int n, uint32_t x, bool incl) {
+    int lo = 0, hi = n;
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        const uint32_t y = k[mid];
+        if (incl ? y <= x : y < x) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo;
+}
+
+template <typename T, bool LSH_MODE>
+__global__ void __launch_bounds__(RPW_THREADS)
+topk_replay_wg_kernel(SelP p, int chunk, int W, int nsim, uint32_t *gscr, int64_t scr_words,
+                      int cap) {
+    extern __shared__ uint32_t rp_smem[];
+    const int wid = threadIdx.x / SSA_WAVE;
+    const int lane = lane_id();
+    const int cnt = *p.tie_count;
+    if (cnt > cap || (int)blockIdx.x >= cnt) return;
+    const int kk = p.kk;
+    const int nls = p.R * p.NS;
+    const int nch = (int)((p.Call + chunk - 1) / chunk);
+    const int sw = rpw_slot_words(W);
+    uint32_t *slot = rp_smem + (int64_t)(wid < nsim ? wid : 0) * sw;
+    uint32_t *sh = rp_smem + (int64_t)nsim * sw;
+    uint32_t *bm = sh;
+    uint32_t *gsc = bm + p.words;
+    int32_t *lst = (int32_t *)(gsc + SSA_WAVE);
+    int32_t *lsz = lst + nls;
+    uint32_t *Sk = (uint32_t *)(lsz + nls);
+    uint32_t *Sn = Sk + kk;
+    uint32_t *Tn = Sn + kk + 1;
+    int32_t *chd = (int32_t *)(Tn + kk + 1);    // per chunk: sorted head length
+    int32_t *ctc = chd + nch;                   // tied key values
+    int32_t *csi = ctc + nch;                   // its input state's index in SK
+    int32_t *mk = csi + nch;                    // the chunks to replay
+    uint32_t *ctv = (uint32_t *)(mk + nch);     // RPW_TV tied keys per chunk
+    int32_t *misc = (int32_t *)(ctv + (int64_t)nch * RPW_TV);
+    uint32_t *kbits = (uint32_t *)(misc + 8);   // kept slots
+    uint16_t *PI = (uint16_t *)(kbits + (p.Call + 31) / 32);
+
+    uint32_t *g = gscr + (int64_t)blockIdx.x * scr_words;
+    uint32_t *skey = g;
+    uint32_t *svs = g + p.Call;
+    uint32_t *first = svs + p.Call;
+    uint32_t *SK = first + p.M;
+    uint32_t *SS = SK + (int64_t)nch * kk;
+    uint32_t *ST = SS + (int64_t)nch * (kk + 1);
+    for (int i = threadIdx.x; i < p.M; i += RPW_THREADS) first[i] = 0xffffffffu;
+
+    for (int it = (int)blockIdx.x; it < cnt; it += (int)gridDim.x) {
+        const int64_t row = p.tie_list[it];          // bh * N + n, over all query heads
+        const int n = (int)(row % p.N);
+        const int bh = (int)(row / p.N);
+        const int b = bh / p.Hq, h = bh % p.Hq, gq = h / p.rep;
+        const int bk = b * p.Hkv + gq;
+        const T *qr = (const T *)p.q + b * p.qsb + h * p.qsh + (int64_t)n * p.qsn;
+        const T *kb = (const T *)p.k + b * p.ksb + gq * p.ksh;
+        const int ng = min(p.G + 1, SSA_WAVE);
+        const uint16_t *qids = p.qid + row * p.R * p.NS;
+        for (int l = threadIdx.x; l < nls; l += RPW_THREADS) {
+            const int u = qids[l];
+            const int64_t prow = (int64_t)bk * p.R + l / p.NS;
+            lst[l] = p.bstart[prow * p.NB + u];
+            lsz[l] = p.bsize[prow * p.NB + u];
+        }
+        for (int64_t w = threadIdx.x; w < (p.Call + 31) / 32; w += RPW_THREADS) kbits[w] = 0u;
+        if (wid == 0) {
+            // the scores the stream does not carry, with the rescore's arithmetic
+            // (as the aux kernel computes them): the query's own key, and
+            // glob ++ 0 for an empty bucket (lane j: entry j)
+            const uint32_t kq = exact_keys<T>(p, qr, kb, n, p.causal && lane == 0);
+            const int gv = lane < p.G ? (int)p.glob[lane < p.G ? lane : 0] : 0;
+            const uint32_t gk = exact_keys<T>(p, qr, kb, gv, lane < ng);
+            if (lane < ng) gsc[lane] = gk;
+            if (lane == 0) misc[0] = (int)kq;
+        }
+        __syncthreads();
+
+        // 1a. key ids and validity of every slot; first occurrences
+        for (int64_t j0 = threadIdx.x; j0 < p.Call; j0 += 8 * RPW_THREADS) {
+            int v[8];
+            uint32_t fl[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int64_t j = j0 + (int64_t)u * RPW_THREADS;
+                v[u] = 0;
+                fl[u] = 0u;
+                if (j < p.Call) {
+                    const int list = (int)(j / p.C);
+                    const int c = (int)(j - (int64_t)list * p.C);
+                    const int sz = lsz[list];
+                    if (sz > 0) {
+                        const bool real = c < min(sz, p.C);
+                        const int64_t prow = (int64_t)bk * p.R + list / p.NS;
+                        const int raw = p.perm[prow * p.M + (real ? lst[list] + c : p.M - 1)];
+                        v[u] = (p.causal && raw > n) ? n : raw;
+                        fl[u] = real ? RPW_VALID : 0u;
+                    } else {
+                        // empty bucket: glob ++ 0, all valid
+                        v[u] = c < p.G ? (int)p.glob[c < p.G ? c : 0] : 0;
+                        fl[u] = RPW_VALID | RPW_EMPTY;
+                    }
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                // a wave's slots are consecutive: a run of one id needs only its
+                // first slot's atomic, and so do the slots clamped to the query
+                const int64_t j = j0 + (int64_t)u * RPW_THREADS;
+                const bool in = j < p.Call;
+                const int vu = in ? v[u] : -1;
+                const int vprev = __shfl_up(vu, 1, SSA_WAVE);
+                const uint64_t nm = wave_ballot(in && vu == n);
+                bool need = in && !(lane > 0 && vprev == vu);
+                if (in && vu == n) need = lane == (int)(__ffsll((long long)nm) - 1);
+                if (need) atomicMin(&first[vu], (uint32_t)j);
+                if (in) svs[j] = (uint32_t)vu | fl[u];
+            }
+        }
+        __syncthreads();
+
+        // 1b. the first occurrences own their ids; valid owners are kept
+        for (int64_t j0 = threadIdx.x; j0 < p.Call; j0 += 8 * RPW_THREADS) {
+            uint32_t vs[8], fv[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int64_t j = j0 + (int64_t)u * RPW_THREADS;
+                vs[u] = j < p.Call ? svs[j] : 0u;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int64_t j = j0 + (int64_t)u * RPW_THREADS;
+                fv[u] = j < p.Call ? __hip_atomic_load(&first[vs[u] & RPW_VMASK], __ATOMIC_RELAXED,
+                                                       __HIP_MEMORY_SCOPE_AGENT)
+                                   : 0xffffffffu;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int64_t j = j0 + (int64_t)u * RPW_THREADS;
+                if (j < p.Call && fv[u] == (uint32_t)j) {
+                    svs[j] = vs[u] | RPW_OWNER;
+                    if (vs[u] & RPW_VALID) atomicOr(&kbits[j >> 5], 1u << (j & 31));
+                }
+            }
+        }
+        __syncthreads();
+
+        // 1c. per chunk: the first-occurrence table back to empty, the kept
+        // slots' exact keys (the query itself scores as in aux), the finite
+        // keys sorted
+        const uint32_t kself = (uint32_t)misc[0];
+        if (wid < nsim) {
+            uint32_t *Ek = slot, *Et = slot + W;
+            for (int s = wid; s < nch; s += nsim) {
+                const int64_t s0 = (int64_t)s * chunk;
+                const int c = (int)min((int64_t)chunk, p.Call - s0);
+                // the kept slots, compacted: ids into Ek, positions into Et
+                int e = 0;
+                for (int j0 = 0; j0 < c; j0 += 4 * SSA_WAVE) {
+                    uint32_t vs[4];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const int jl = j0 + u * SSA_WAVE + lane;
+                        vs[u] = jl < c ? svs[s0 + jl] : 0u;
+                    }
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const int jl = j0 + u * SSA_WAVE + lane;
+                        const int64_t j = s0 + jl;
+                        const bool in = jl < c;
+                        const bool keep = in && ((kbits[j >> 5] >> (j & 31)) & 1u);
+                        if (in && (vs[u] & RPW_OWNER)) first[vs[u] & RPW_VMASK] = 0xffffffffu;
+                        if (in && !keep) skey[j] = RP_NEGINF;
+                        const uint64_t m = wave_ballot(keep);
+                        if (keep) {
+                            const int at = e + lanes_below(m);
+                            Ek[at] = vs[u] & RPW_VMASK;
+                            Et[at] = (uint32_t)(kk + jl);
+                        }
+                        e += __popcll(m);
+                    }
+                }
+                rp_sync();
+                for (int g0 = 0; g0 < e; g0 += SSA_WAVE) {
+                    const int t = g0 + lane;
+                    const bool in = t < e;
+                    const int v = in ? (int)Ek[t] : 0;
+                    const int64_t j = s0 + (in ? (int)Et[t] - kk : 0);
+                    const int list = (int)(j / p.C);
+                    const bool empty = lsz[list] == 0;
+                    const bool xk = in && !empty && !(p.causal && v == n);
+                    const uint32_t ex = exact_keys_wide<T, 4>(p, qr, kb, v, xk);
+                    if (in) {
+                        const int cl = (int)(j - (int64_t)list * p.C);
+                        const uint32_t key = ~(empty ? gsc[cl < ng - 1 ? cl : ng - 1] : (xk ? ex : kself));
+                        Ek[t] = key;
+                        skey[j] = key;
+                    }
+                }
+                rp_sync();
+                rpw_sort(Ek, Et, e);
+                // the sorted head: the first kk + 1 finite keys (-inf sorts last)
+                const int hl = min(rpw_rank(Ek, e, RP_NEGINF, false), kk + 1);
+                for (int t = lane; t < hl; t += SSA_WAVE) {
+                    SS[(int64_t)s * (kk + 1) + t] = Ek[t];
+                    ST[(int64_t)s * (kk + 1) + t] = Et[t];
+                }
+                if (lane == 0) chd[s] = hl;
+                rp_sync();
+            }
+        }
+        __syncthreads();
+
+        if (wid == 0) {
+            // 2. the states' keys: S_s = the kk smallest of S_{s-1} ++ chunk s
+            uint32_t *Ek = slot, *Et = slot + W;
+            for (int t = lane; t < kk; t += SSA_WAVE) Sk[t] = RP_NEGINF;
+            int a = 0;       // finite keys in Sk
+            int nst = 0;     // input states kept
+            // the next chunk's head, its first 4 * 64 entries loaded a step ahead
+            uint32_t hk[4], ht[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int t = u * SSA_WAVE + lane;
+                hk[u] = t < chd[0] ? SS[t] : 0u;
+                ht[u] = t < chd[0] ? ST[t] : 0u;
+            }
+            rpw_lsync();
+            for (int s = 0; s < nch; ++s) {
+                const int hl = chd[s];
+                const uint32_t thr = a == kk ? Sk[kk - 1] : RP_NEGINF;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int t = u * SSA_WAVE + lane;
+                    if (t < hl) { Ek[t] = hk[u]; Et[t] = ht[u]; }
+                }
+                for (int t = 4 * SSA_WAVE + lane; t < hl; t += SSA_WAVE) {
+                    Ek[t] = SS[(int64_t)s * (kk + 1) + t];
+                    Et[t] = ST[(int64_t)s * (kk + 1) + t];
+                }
+                if (s + 1 < nch) {
+                    const int hn = chd[s + 1];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const int t = u * SSA_WAVE + lane;
+                        hk[u] = t < hn ? SS[(int64_t)(s + 1) * (kk + 1) + t] : 0u;
+                        ht[u] = t < hn ? ST[(int64_t)(s + 1) * (kk + 1) + t] : 0u;
+                    }
+                }
+                rpw_lsync();
+                // the head's keys that enter (at most the state's worst)
+                const int e = rpw_rank(Ek, hl, thr, true);
+                // merge: state entries before chunk entries of the same key
+                const int nout = min(kk + 1, a + e);
+                for (int t = lane; t < a; t += SSA_WAVE) {
+                    const uint32_t x = Sk[t];
+                    const int r = t + rpw_rank(Ek, e, x, false);
+                    if (r < nout) { Sn[r] = x; Tn[r] = (uint32_t)t; }
+                }
+                for (int t = lane; t < e && t < nout; t += SSA_WAVE) {
+                    const uint32_t x = Ek[t];
+                    const int r = t + rpw_rank(Sk, a, x, true);
+                    if (r < nout) { Sn[r] = x; Tn[r] = Et[t]; }
+                }
+                rpw_lsync();
+                // equal finite keys among the first kk + 1: note each tied value
+                int ntv = 0;
+                for (int t0 = 0; t0 < kk && t0 + 1 < nout; t0 += SSA_WAVE) {
+                    const int t = t0 + lane;
+                    const bool run = t < kk && t + 1 < nout && Sn[t] == Sn[t + 1] &&
+                                     (t == 0 || Sn[t - 1] != Sn[t]);
+                    const uint64_t m = wave_ballot(run);
+                    if (run) {
+                        const int at = ntv + lanes_below(m);
+                        if (at < RPW_TV) ctv[(int64_t)s * RPW_TV + at] = Sn[t];
+                    }
+                    ntv += __popcll(m);
+                }
+                if (ntv > 0) {
+                    for (int t = lane; t < kk; t += SSA_WAVE) SK[(int64_t)nst * kk + t] = Sk[t];
+                    if (lane == 0) csi[s] = nst;
+                    ++nst;
+                }
+                if (lane == 0) ctc[s] = ntv;
+                const int an = min(kk, a + e);
+                for (int t = lane; t < kk; t += SSA_WAVE) {
+                    Sk[t] = t < an ? Sn[t] : RP_NEGINF;
+                    PI[(int64_t)s * kk + t] = (uint16_t)(t < an ? Tn[t] : 0u);
+                }
+                a = an;
+                rpw_lsync();
+            }
+            // the chunks to replay: every tie for an ordered list; for a set,
+            // the chunks where the final kk-th key is tied (none when fewer
+            // than kk keys are finite: all of them are kept)
+            const uint32_t vstar = Sk[kk - 1];
+            int nmark = 0;
+            for (int s0 = 0; s0 < nch; s0 += SSA_WAVE) {
+                const int s = s0 + lane;
+                bool mark = false;
+                if (s < nch && ctc[s] > 0) {
+                    if (LSH_MODE || ctc[s] > RPW_TV) {
+                        mark = LSH_MODE || a == kk;
+                    } else if (a == kk) {
+                        for (int u = 0; u < ctc[s]; ++u) mark |= ctv[(int64_t)s * RPW_TV + u] == vstar;
+                    }
+                }
+                const uint64_t m = wave_ballot(mark);
+                if (mark) mk[nmark + lanes_below(m)] = s;
+                nmark += __popcll(m);
+            }
+            if (lane == 0) { misc[1] = nmark; misc[2] = a; }
+        }
+        __syncthreads();
+
+        // 3. the chunks to replay, replayed as the reference runs them
+        const int nmark = misc[1];
+        if (wid < nsim) {
+            RpArr A;
+            A.key = slot;
+            A.cand = (int32_t *)(slot + W);
+            uint16_t *TL = (uint16_t *)(slot + 2 * W);
+            uint16_t *TR = TL + W;
+            uint32_t *lbits = slot + 3 * W;
+            int32_t *stk = (int32_t *)(lbits + (W + 31) / 32 + 1);
+            for (int f = wid; f < nmark; f += nsim) {
+                const int s = mk[f];
+                const int64_t s0 = (int64_t)s * chunk;
+                const int c = (int)min((int64_t)chunk, p.Call - s0);
+                const int si = csi[s];
+                for (int t = lane; t < kk; t += SSA_WAVE) {
+                    A.key[t] = SK[(int64_t)si * kk + t];
+                    A.cand[t] = t;
+                }
+                for (int t = lane; t < c; t += SSA_WAVE) {
+                    A.key[kk + t] = skey[s0 + t];
+                    A.cand[kk + t] = kk + t;
+                }
+                rp_sync();
+                // torch.topk(best ++ chunk, kk): partial_sort when 64*kk <= width,
+                // else nth_element(kk-1) + sort(kk-1)
+                const int w = kk + c;
+                if ((int64_t)kk * 64 <= w) {
+                    if (lane == 0) {
+                        rp_heap_select(A, 0, kk, w);
+                        rp_heap_sort(A, 0, kk);
+                    }
+                    rp_sync();
+                } else {
+                    rp_nth_element(A, TL, TR, 0, kk - 1, w);
+                    rp_sort(A, TL, TR, lbits, stk, 0, kk - 1);
+                }
+                for (int t = lane; t < kk; t += SSA_WAVE) PI[(int64_t)s * kk + t] = (uint16_t)A.cand[t];
+                rp_sync();
+            }
+        }
+        __syncthreads();
+
+        if (wid == 0) {
+            // 4. each finite output slot back to its stream slot
+            const int fcount = misc[2];
+            int32_t *cand = (int32_t *)(slot + W);
+            for (int t = lane; t < fcount; t += SSA_WAVE) {
+                int pos = t;
+                int64_t js = -1;
+                for (int s = nch - 1; s >= 0; --s) {
+                    const int tg = PI[(int64_t)s * kk + pos];
+                    if (tg >= kk) { js = (int64_t)s * chunk + (tg - kk); break; }
+                    pos = tg;
+                }
+                cand[t] = js >= 0 ? (int32_t)(svs[js] & RPW_VMASK) : 0;
+            }
+            rp_sync();
+            if (LSH_MODE) {
+                int64_t *orow = p.out_idx + row * kk;
+                for (int t = lane; t < kk; t += SSA_WAVE)
+                    orow[t] = t < fcount ? (int64_t)cand[t] : (t < p.G ? p.glob[t] : 0);
+            } else {
+                for (int w = lane; w < p.words; w += SSA_WAVE) bm[w] = 0u;
+                rp_sync();
+                for (int t = lane; t < fcount; t += SSA_WAVE) bm_set(bm, cand[t]);
+                rp_sync();
+                full_merge_emit(bm, p, n, row, fcount, (int32_t *)slot, W);
+            }
+        }
+        __syncthreads();
+    }
+}
+
 // ------------------------------------------------------------------ host side
 // Instance of the matrix-core rescore / aux kernels for head dim d (8..128,
 // whole 8-element pieces): k steps of 32, so ceil(d / 32) steps as the select's
@@ -2787,7 +3259,7 @@ struct Layout {
     int64_t kid, qid, perm, bstart, bsize, sorttmp, sid, rnk, smin, inv, cut, srix, qpos, cnt, off,
         cur,
         qlist, tiles, ntiles, tcnt, kbase, S,
-        tie_list, tie_count, aux, knorm, kpart, rpscr, total;
+        tie_list, tie_count, aux, knorm, kpart, rpscr, rpw, total;
 };
 
 int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
@@ -2833,6 +3305,8 @@ Layout plan(const Dims &D) {
         L.rpscr = take(replay_fits_lds(W, words)
                            ? 0
                            : replay_glb_blocks(W, words) * RP_WAVES * rp_lds_words(W, words) * 4);
+        L.rpw = take((int64_t)D.rpw_blocks *
+                     rpw_scratch_words(D.Call, D.M, D.kk, (int)ceil_div(D.Call, D.chunk)) * 4);
     }
     L.total = o;
     return L;
@@ -2925,6 +3399,18 @@ int make_dims(const ssa_graph_args *a, Dims &D, bool need_q = true, int64_t ws_c
         ssa_set_error("build_graph: one instance's score rows (N * C * 2 = %lld bytes) must stay "
                       "below 2 GiB", (long long)a->N * D.Cs * 2);
         return SSA_E_UNSUP;
+    }
+    {
+        // the workgroup replay: as many blocks as 256 MiB of workspace hold (a
+        // quarter of ws_cap without allocation), when its LDS fits
+        const int nch = (int)ceil_div(D.Call, D.chunk);
+        const int W = D.kk + D.chunk;
+        const int shared = rpw_shared_words(sel_bitmap_words(D.M), D.nlists, D.kk, nch, D.Call);
+        D.rpw_nsim = std::min<int>(RPW_WAVES, (SSA_LDS_BYTES / 4 - shared) / rpw_slot_words(W));
+        const int64_t per = rpw_scratch_words(D.Call, D.M, D.kk, nch) * 4;
+        const int64_t budget = ws_cap > 0 ? ws_cap / 4 : ((int64_t)256 << 20);
+        D.rpw_blocks = (int)std::min<int64_t>(RPW_MAX_BLOCKS, budget / per);
+        if (D.rpw_nsim < 1 || D.M >= (1 << 29) || D.Call >= ((int64_t)1 << 31)) D.rpw_blocks = 0;
     }
     int64_t nbh = ((int64_t)8 << 30) / per_bh;
     if (nbh < 1) nbh = 1;
@@ -3149,45 +3635,55 @@ int aux_dispatch(int d, bool mfma, const AuxP &ap, hipStream_t st) {
     return SSA_OK;
 }
 
-// Exact top-k replay of the rows select flagged.  A replayed row needs
-// rp_lds_words(kk + chunk) words; when RP_WAVES of them fit LDS the arrays live
-// there, else in the workspace region `rpscr` (replay_glb_blocks blocks).
+// Exact top-k replay of the rows select flagged.  Up to `cap` tied rows go
+// to the workgroup replay (rpw_blocks blocks at most, its arrays in LDS and in
+// the workspace region `rpwscr`); more go to the per-wave replay, whose arrays
+// (rp_lds_words(kk + chunk) words per row) live in LDS when RP_WAVES of them
+// fit, else in the workspace region `rpscr` (replay_glb_blocks blocks).  Both
+// are launched: each reads the tie count on the device and exits at once when
+// the rows are the other's.
 template <typename T, bool LSH>
-int launch_replay(const SelP &sp, int chunk, uint32_t *rpscr, hipStream_t st) {
+int launch_replay(const SelP &sp, const Dims &D, uint32_t *rpscr, uint32_t *rpwscr,
+                  hipStream_t st) {
+    const int chunk = D.chunk;
     const int W = sp.kk + chunk;
+    int cap = -1;
+    if (D.rpw_blocks > 0) {
+        const int nch = (int)ceil_div(sp.Call, chunk);
+        const int lds = (D.rpw_nsim * rpw_slot_words(W) +
+                         rpw_shared_words(sp.words, sp.R * sp.NS, sp.kk, nch, sp.Call)) * 4;
+        int dev = 0, cus = 0;
+        SSA_CHECK_HIP(hipGetDevice(&dev));
+        SSA_CHECK_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+        SSA_CHECK_HIP(hipFuncSetAttribute((const void *)topk_replay_wg_kernel<T, LSH>,
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, lds));
+        // the blocks resident at once (registers and LDS): each loops over its
+        // rows; up to four rows per block beat the per-wave replay
+        int per_cu = 0;
+        SSA_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu, (const void *)topk_replay_wg_kernel<T, LSH>, RPW_THREADS, lds));
+        const int64_t blocks = std::min<int64_t>(
+            std::min<int64_t>(D.rpw_blocks, (int64_t)cus * std::max(1, per_cu)), sp.rows);
+        cap = (int)std::min<int64_t>(4 * blocks, sp.rows);
+        hipLaunchKernelGGL((topk_replay_wg_kernel<T, LSH>), dim3((unsigned)blocks),
+                           dim3(RPW_THREADS), (size_t)lds, st, sp, chunk, W, D.rpw_nsim, rpwscr,
+                           rpw_scratch_words(sp.Call, sp.M, sp.kk, nch), cap);
+        SSA_CHECK_LAUNCH();
+    }
     if (!replay_fits_lds(W, sp.words)) {
         const int64_t blocks = replay_glb_blocks(W, sp.words);
-        hipLaunchKernelGGL((topk_replay_kernel<T, LSH, true, false>), dim3((unsigned)blocks),
-                           dim3(RP_WAVES * SSA_WAVE), 0, st, sp, chunk, W, rpscr, -1);
+        hipLaunchKernelGGL((topk_replay_kernel<T, LSH, true>), dim3((unsigned)blocks),
+                           dim3(RP_WAVES * SSA_WAVE), 0, st, sp, chunk, W, rpscr, cap);
         SSA_CHECK_LAUNCH();
         return SSA_OK;
     }
     const size_t lds = (size_t)RP_WAVES * rp_lds_words(W, sp.words) * 4;
-    // the wide instance's resident rows: two waves per SIMD (its registers)
-    int wide_max = -1;
-    if constexpr (!std::is_same<T, float>::value) {
-      if (sp.mfma) {
-        int dev = 0, cus = 0;
-        SSA_CHECK_HIP(hipGetDevice(&dev));
-        SSA_CHECK_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-        wide_max = 2 * 4 * cus;
-        SSA_CHECK_HIP(hipFuncSetAttribute((const void *)topk_replay_kernel<T, LSH, false, true>,
-                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        const int64_t wblocks = std::min<int64_t>(ceil_div(sp.rows, RP_WAVES),
-                                                  ceil_div(wide_max, RP_WAVES));
-        hipLaunchKernelGGL((topk_replay_kernel<T, LSH, false, true>), dim3((unsigned)wblocks),
-                           dim3(RP_WAVES * SSA_WAVE), lds, st, sp, chunk, W, (uint32_t *)nullptr,
-                           wide_max);
-        SSA_CHECK_LAUNCH();
-      }
-    }
-    SSA_CHECK_HIP(hipFuncSetAttribute((const void *)topk_replay_kernel<T, LSH, false, false>,
+    SSA_CHECK_HIP(hipFuncSetAttribute((const void *)topk_replay_kernel<T, LSH, false>,
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     // enough blocks for every resident wave to take a row (the rest exit at once)
     const int64_t blocks = std::min<int64_t>(ceil_div(sp.rows, RP_WAVES), 8192);
-    hipLaunchKernelGGL((topk_replay_kernel<T, LSH, false, false>), dim3((unsigned)blocks),
-                       dim3(RP_WAVES * SSA_WAVE), lds, st, sp, chunk, W, (uint32_t *)nullptr,
-                       wide_max);
+    hipLaunchKernelGGL((topk_replay_kernel<T, LSH, false>), dim3((unsigned)blocks),
+                       dim3(RP_WAVES * SSA_WAVE), lds, st, sp, chunk, W, (uint32_t *)nullptr, cap);
     SSA_CHECK_LAUNCH();
     return SSA_OK;
 }
@@ -3433,8 +3929,9 @@ int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char 
     xp.bh0 = 0;
     xp.rows = D.BH * D.N;
     uint32_t *rpscr = (uint32_t *)(ws + L.rpscr);
-    return xp.mode == SSA_GRAPH_LSH ? launch_replay<T, true>(xp, D.chunk, rpscr, st)
-                                    : launch_replay<T, false>(xp, D.chunk, rpscr, st);
+    uint32_t *rpwscr = (uint32_t *)(ws + L.rpw);
+    return xp.mode == SSA_GRAPH_LSH ? launch_replay<T, true>(xp, D, rpscr, rpwscr, st)
+                                    : launch_replay<T, false>(xp, D, rpscr, rpwscr, st);
 }
 
 }  // namespace

@@ -177,6 +177,31 @@ def test_lsh_builder_exact_tier_huge_k_replay_outside_lds():
     np.testing.assert_array_equal(got.cpu().numpy().reshape(B * H, N, -1), ref["idx"])
 
 
+# Tied-row counts on either side of the replay's two paths (a 256-CU device):
+# up to four tied rows per workgroup take the workgroup replay (several rows
+# per workgroup past 256), more take the per-wave replay
+MANY_TIES = [
+    # 428 tied rows
+    ("many_ties_workgroup_replay", 1, 4, 2, 512, 512, 16, 4, 6, 1, 32, 4, 2, True, False, 256, 1024),
+    # 1339 tied rows
+    ("many_ties_per_wave_replay", 2, 8, 2, 384, 384, 8, 3, 5, 1, 24, 4, 2, True, False, 1024, 6144),
+]
+
+
+@pytest.mark.parametrize("case", MANY_TIES, ids=lambda c: c[0])
+def test_graph_exact_tier_many_tied_rows(case):
+    lo, hi = case[-2:]
+    attn, got, got_v, ref, (B, H, N, M, K, w, cross, causal, glob) = _graph_case(case[:-2], 0)
+    print(f"  {case[0]}: {ref['n_ties']} rows with a tied kk-th score", flush=True)
+    assert lo < ref["n_ties"] <= hi
+    win = attn.win_builder(N, M, "cpu").numpy()
+    rnb, rva = oracle.merge(win, glob.numpy(), ref["idx"], has_self=True, total_k=K)
+    np.testing.assert_array_equal(got.cpu().numpy().reshape(B * H, N, -1), rnb)
+    np.testing.assert_array_equal(got_v.cpu().numpy().reshape(B * H, N, -1), rva)
+    _, got, _, ref, _ = _graph_case(case[:-2], 0, lsh_only=True)
+    np.testing.assert_array_equal(got.cpu().numpy().reshape(B * H, N, -1), ref["idx"])
+
+
 @pytest.mark.parametrize("case", GRAPH_CASES, ids=lambda c: c[0])
 def test_graph_bf16_inputs_exact_tier(case):
     """bf16 q/k holding small integers are exact: same graph as fp32 (the
