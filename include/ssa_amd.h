@@ -174,6 +174,11 @@ typedef struct {
     /* negative id marking an invalid slot (ssa_graph_args.out_idx32); when set, */
     /* neighbors and valid are not read.  Not accepted by the backward.          */
     const int32_t *neighbors32;
+    /* optional (no counterpart in the reference): B*Hq*N int32, written with    */
+    /* each query row's count of invalid slots (masked, negative or out of       */
+    /* range), the reference's padding statistic (sparse_attention.py:1500-1508) */
+    /* without a pass of its own over the graph.  Forward only.                  */
+    int32_t *row_invalid;
 } ssa_apply_args;
 
 int ssa_sparse_gather_attention(const ssa_apply_args *a, void *stream);

@@ -55,7 +55,7 @@ class ApplyArgs(ctypes.Structure):
         ("scale", ctypes.c_float), ("fp32_weights", c_i32), ("dropout_p", ctypes.c_float),
         ("seed", ctypes.c_uint64),
         ("out", c_vp), ("out_sb", c_i64), ("out_sh", c_i64), ("out_sn", c_i64),
-        ("neighbors32", c_vp),
+        ("neighbors32", c_vp), ("row_invalid", c_vp),
     ]
 
 
@@ -342,15 +342,24 @@ def _apply_args(q, k, v, neighbors, valid, scale, fp32w, dropout_p, seed, out, i
 
 
 def gather_attention_fwd(q, k, v, neighbors, valid, scale, fp32w=False, dropout_p=0.0, seed=0,
-                         out=None):
+                         out=None, row_invalid=None):
+    """row_invalid: optional (B*Hq*N,) int32, written with each query row's
+    count of invalid slots."""
     check_apply_shapes(q, k, v, neighbors, valid, out)
-    require_device(q, k, v, neighbors, valid)
+    require_device(q, k, v, neighbors, valid, row_invalid)
+    if row_invalid is not None:
+        B, Hq, N, _ = q.shape
+        if (row_invalid.dtype != torch.int32 or row_invalid.numel() != B * Hq * N
+                or not row_invalid.is_contiguous()):
+            raise RuntimeError("ssa_amd.sparse_gather_attention: row_invalid must be a "
+                               f"contiguous int32 tensor of {B * Hq * N} elements")
     if not (q.dtype == k.dtype == v.dtype):
         raise RuntimeError("ssa_amd.sparse_gather_attention: q, k, v dtypes differ")
     if out is None:
         B, Hq, N, d = q.shape
         out = torch.empty((B, N, Hq, d), dtype=q.dtype, device=q.device).transpose(1, 2)
     a, keep = _apply_args(q, k, v, neighbors, valid, scale, fp32w, dropout_p, seed, out)
+    a.row_invalid = _ptr(row_invalid)
     _check(lib().ssa_sparse_gather_attention(ctypes.byref(a), _stream(q)),
            "sparse_gather_attention")
     del keep

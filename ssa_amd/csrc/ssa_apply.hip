@@ -29,6 +29,7 @@ struct ApplyP {
     const int64_t *nb;
     const uint8_t *valid;
     const int32_t *nb32;   // or the graph as int32 ids, negative = invalid
+    int32_t *row_inv;      // optional: per row, its count of invalid slots
     float scale;
     int32_t fp32w;
     float drop_p;
@@ -123,11 +124,18 @@ apply_fwd_kernel(ApplyP p) {
     const uint8_t *va = p.valid ? p.valid + row * p.K : nullptr;
 
     // neighbour ids once, as int32 in LDS; masked or out-of-range slots -> -1
-    for (int j = lane; j < p.K; j += SSA_WAVE) {
-        const int64_t x = p.nb32 ? (int64_t)p.nb32[row * p.K + j] : nb[j];
-        const bool o = (p.nb32 ? true : (va ? va[j] != 0 : true)) && x >= 0 && x < p.M;
-        ix[j] = o ? (int)x : -1;
+    int ninv = 0;
+    for (int j0 = 0; j0 < p.K; j0 += SSA_WAVE) {
+        const int j = j0 + lane;
+        bool o = false;
+        if (j < p.K) {
+            const int64_t x = p.nb32 ? (int64_t)p.nb32[row * p.K + j] : nb[j];
+            o = (p.nb32 ? true : (va ? va[j] != 0 : true)) && x >= 0 && x < p.M;
+            ix[j] = o ? (int)x : -1;
+        }
+        ninv += __popcll(wave_ballot(j < p.K && !o));
     }
+    if (p.row_inv && lane == 0) p.row_inv[row] = ninv;
     // lanes whose elements lie past the head dim hold zeros and store nothing
     const bool live = li * VEC < p.d;
     const int lofs = live ? li * VEC : 0;
@@ -359,14 +367,18 @@ apply_fwd16_kernel(ApplyP p) {
     const uint8_t *va = p.valid ? p.valid + row * p.K : nullptr;
 
     // neighbour ids as int32 in LDS (ids < 2^24, checked at dispatch)
-    for (int j = lane; j < Kp; j += SSA_WAVE) {
+    int ninv = 0;
+    for (int j0 = 0; j0 < Kp; j0 += SSA_WAVE) {
+        const int j = j0 + lane;
         int x = INT32_MIN;
         if (j < p.K) {
             const int64_t y = p.nb32 ? (int64_t)p.nb32[row * p.K + j] : nb[j];
             if ((p.nb32 ? true : (va ? va[j] != 0 : true)) && y >= 0 && y < p.M) x = (int)y;
         }
         ix[j] = x;
+        ninv += __popcll(wave_ballot(j < p.K && x == INT32_MIN));
     }
+    if (p.row_inv && lane == 0) p.row_inv[row] = ninv;
     uint4 q4 = *reinterpret_cast<const uint4 *>(qrow + (live ? li * 8 : 0));
     if (!live) q4 = make_uint4(0, 0, 0, 0);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -704,6 +716,7 @@ int apply_common(const ssa_apply_args *a, ApplyP &p) {
     p.ksb = a->k.sb; p.ksh = a->k.sh; p.ksn = a->k.sn;
     p.vsb = a->v.sb; p.vsh = a->v.sh; p.vsn = a->v.sn;
     p.nb = a->neighbors; p.valid = a->valid; p.nb32 = a->neighbors32;
+    p.row_inv = a->row_invalid;
     p.scale = a->scale; p.fp32w = a->fp32_weights;
     p.drop_p = a->dropout_p;
     // inverted dropout scales kept weights by 1 / (1 - p), the keep rate taken
@@ -745,5 +758,6 @@ extern "C" int ssa_sparse_gather_attention_bwd(const ssa_apply_bwd_args *a, void
     SSA_CHECK_ARG(a->fwd.neighbors32 == nullptr && a->fwd.neighbors != nullptr,
                   "sparse_gather_attention_bwd: needs the int64 neighbours");
     p.dout = a->dout; p.dq = a->dq; p.dk = a->dk; p.dv = a->dv;
+    p.row_inv = nullptr;
     return run_apply(p, a->fwd.q.dtype, a->fwd.d, (hipStream_t)stream, true);
 }

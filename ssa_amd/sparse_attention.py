@@ -239,8 +239,9 @@ def _alert_nondeterministic_backward():
 
 class _GatherAttention(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, q, k, v, neighbors, valid, scale, fp32w, dropout_p, seed):
-        out = _lib.gather_attention_fwd(q, k, v, neighbors, valid, scale, fp32w, dropout_p, seed)
+    def forward(ctx, q, k, v, neighbors, valid, scale, fp32w, dropout_p, seed, row_invalid=None):
+        out = _lib.gather_attention_fwd(q, k, v, neighbors, valid, scale, fp32w, dropout_p, seed,
+                                        row_invalid=row_invalid)
         ctx.save_for_backward(q, k, v, neighbors, valid)
         ctx.cfg = (scale, fp32w, dropout_p, seed)
         return out
@@ -253,23 +254,25 @@ class _GatherAttention(torch.autograd.Function):
         dq, dk, dv = _lib.gather_attention_bwd(q, k, v, neighbors, valid, scale, fp32w,
                                                dropout_p, seed, dout)
         return (dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None, None, None,
-                None)
+                None, None)
 
 
 def sparse_gather_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                             neighbors: torch.Tensor, scale: float,
                             valid: Optional[torch.Tensor] = None, dropout: float = 0.0,
-                            training: bool = False, fp32_attn_weights: bool = False
-                            ) -> torch.Tensor:
+                            training: bool = False, fp32_attn_weights: bool = False,
+                            *, _row_invalid: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Attention of each query over its K gathered neighbours
     (sparse_attention.py:1096-1199).  ``k``/``v`` may be (B, H, M, d) or the
-    un-expanded (B, n_kv, M, d)."""
+    un-expanded (B, n_kv, M, d).  ``_row_invalid`` (the module's padding
+    statistic): a (B*H*N,) int32 tensor the kernel fills with each row's count
+    of invalid slots."""
     _lib.check_apply_shapes(q, k, v, neighbors, valid)
     _lib.require_device(q, k, v, neighbors, valid)
     p = float(dropout) if (training and dropout > 0.0) else 0.0
     seed = int(torch.randint(0, 2 ** 62, (1,)).item()) if p > 0.0 else 0
     return _GatherAttention.apply(q, k, v, neighbors, valid, float(scale),
-                                  bool(fp32_attn_weights), p, seed)
+                                  bool(fp32_attn_weights), p, seed, _row_invalid)
 
 
 # ---------------------------------------------------------------------------- module
@@ -417,12 +420,14 @@ class SparseAttention(nn.Module):
         return self._split_q(qx), self._split_kv_compact(kx), self._split_kv_compact(vx)
 
     def apply_graph(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
-                    neighbors: torch.Tensor, valid: torch.Tensor) -> torch.Tensor:
+                    neighbors: torch.Tensor, valid: torch.Tensor, *,
+                    _row_invalid: Optional[torch.Tensor] = None) -> torch.Tensor:
         """sparse_gather_attention with this module's scale / dropout / fp32
         weights (sparse_attention.py:1392-1418)."""
         return sparse_gather_attention(q, k, v, neighbors, scale=self.scale, valid=valid,
                                        dropout=self.dp, training=self.training,
-                                       fp32_attn_weights=self.config.fp32_attn_weights)
+                                       fp32_attn_weights=self.config.fp32_attn_weights,
+                                       _row_invalid=_row_invalid)
 
     def forward(self, x: torch.Tensor, key_value: Optional[torch.Tensor] = None,
                 attention_mask: Optional[torch.Tensor] = None, return_stats: bool = False,
@@ -444,21 +449,25 @@ class SparseAttention(nn.Module):
         M = src.shape[1]
         causal = self.config.causal and not is_cross
         q, k, v = self._project(x, src, is_cross)
+        # the padding statistic: each row's invalid slots, counted by the
+        # gather attention as it reads the graph
+        row_inv = (torch.empty(B * self.H * N, dtype=torch.int32, device=x.device)
+                   if return_stats else None)
         if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
             neighbors, valid = self.build_graph(q, k, N, M, B, x.device, causal, is_cross)
-            out = self.apply_graph(q, k, v, neighbors, valid)
+            out = self.apply_graph(q, k, v, neighbors, valid, _row_invalid=row_inv)
         else:
             # no autograd: the same graph as int32 ids with -1 in the invalid
             # slots, which the gather attention reads as it is (a third of the
             # bytes of int64 ids and a mask, written once and read once)
             neighbors, valid = self._build_graph_ids32(q, k, N, M, B, causal, is_cross), None
-            out = self.apply_graph(q, k, v, neighbors, None)
+            out = self.apply_graph(q, k, v, neighbors, None, _row_invalid=row_inv)
         out_proj = self.Wo(self._merge(out))
         if not return_stats:
             return out_proj, {}
         peak_sparse = B * self.H * N * self.K * self.d_head
         peak_full = B * self.H * N * M * self.d_head
-        pad = _PendingFraction(~valid if valid is not None else neighbors < 0)
+        pad = _PendingFraction(rows=row_inv, numel=neighbors.numel())
         return out_proj, {
             "neighbors_shape": tuple(neighbors.shape),
             "peak_sparse_elems": peak_sparse,
@@ -472,10 +481,16 @@ class _PendingFraction:
     """Mean of a boolean mask as the reference's CPU ``.float().mean()``
     rounds it: the exact count divided by the element count in fp32 (the
     device's mean multiplies by a rounded reciprocal instead).  The count is
-    taken on the device as bytes summed in int32 while that cannot overflow (a
+    taken on the device, from per-row counts (``rows``, numel elements in all)
+    or from the mask as bytes summed in int32 while that cannot overflow (a
     bool tensor's own sum first copies it to int64); ``value()`` waits for it."""
 
-    def __init__(self, invalid: torch.Tensor):
+    def __init__(self, invalid: Optional[torch.Tensor] = None, *,
+                 rows: Optional[torch.Tensor] = None, numel: int = 0):
+        if rows is not None:
+            self.numel = numel
+            self.count = rows.sum(dtype=torch.int64)
+            return
         self.numel = invalid.numel()
         acc = torch.int32 if self.numel < (1 << 31) else torch.int64
         self.count = invalid.view(torch.uint8).sum(dtype=acc)
@@ -614,7 +629,9 @@ class CachedGraphSparseTransformer(nn.Module):
                 cached, cached_group = (nb, va), group
             else:
                 nb, va = cached
-            out = attn.apply_graph(q, k, v, nb, va)
+            row_inv = (torch.empty(B * attn.H * N, dtype=torch.int32, device=normed.device)
+                       if return_stats else None)
+            out = attn.apply_graph(q, k, v, nb, va, _row_invalid=row_inv)
             a = attn.Wo(attn._merge(out))
             h = h + a
             h = h + layer.ff(layer.norm2(h))
@@ -624,7 +641,7 @@ class CachedGraphSparseTransformer(nn.Module):
                 stats_list.append({
                     "neighbors_shape": tuple(nb.shape),
                     "compression": peak_full / peak_sparse,
-                    "padding_fraction": _PendingFraction(~va),
+                    "padding_fraction": _PendingFraction(rows=row_inv, numel=va.numel()),
                     "graph_recomputed": recompute,
                 })
             else:

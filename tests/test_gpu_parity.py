@@ -315,6 +315,51 @@ def test_apply_expanded_kv_equals_grouped_kv():
     assert torch.equal(o1, o2)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("ids32", [False, True])
+def test_apply_counts_invalid_slots_per_row(dtype, ids32):
+    """row_invalid: each row's masked, negative or out-of-range slots (the
+    padding statistic), with the same output as without it."""
+    from ssa_amd import _lib
+    case = (2, 4, 2, 50, 60, 64, 37)
+    q, k, v, nb, va = _apply_inputs(case, dtype, 5)
+    nb[0, 1, 3, 4] = 60            # out of range
+    nb[1, 2, 7, 9] = -5            # negative
+    a = [t.to(DEV) for t in (q, k, v)]
+    if ids32:
+        ids = torch.where(va, nb, torch.full_like(nb, -1)).to(torch.int32).to(DEV)
+        nbd, vad = ids, None
+        bad = (ids < 0) | (ids >= 60)
+    else:
+        nbd, vad = nb.to(DEV), va.to(DEV)
+        bad = ~vad | (nbd < 0) | (nbd >= 60)
+    rows = torch.full((2 * 4 * 50,), -7, dtype=torch.int32, device=DEV)
+    with torch.no_grad():
+        o1 = _lib.gather_attention_fwd(a[0], a[1], a[2], nbd, vad, 0.125, row_invalid=rows)
+        o2 = _lib.gather_attention_fwd(a[0], a[1], a[2], nbd, vad, 0.125)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2)
+    assert torch.equal(rows.cpu(), bad.reshape(-1, 37).sum(-1).to(torch.int32).cpu())
+
+
+def test_module_padding_fraction_is_the_mask_mean():
+    """SparseAttention's padding_fraction (from the per-row counts) equals the
+    reference's (~valid).float().mean() on the graph it built."""
+    from ssa_amd import SSAConfig, SparseAttention
+    torch.manual_seed(0)
+    cfg = SSAConfig(d_model=64, num_heads=4, num_kv_heads=2, num_neighbors=40, window_size=3,
+                    num_global_tokens=2, num_hash_rounds=2, causal=True)
+    with _nowarn():
+        attn = SparseAttention(cfg).to(DEV).eval()
+    x = torch.randn(2, 96, 64, device=DEV)
+    with torch.no_grad():
+        _, st = attn(x, return_stats=True)
+        q, k, _ = attn._project(x, x, False)
+        _, valid = attn.build_graph(q, k, 96, 96, 2, x.device, True, False)
+    ref = float((~valid).cpu().float().mean())
+    assert st["padding_fraction"] == ref
+
+
 def test_apply_fp32_head_dim_12_matches_oracle():
     """fp32 takes head dims in whole 4-element pieces (12: the 16 instance)."""
     from ssa_amd import sparse_gather_attention
