@@ -3098,19 +3098,24 @@ topk_replay_wg_kernel(SelP p, int chunk, int W, int nsim, uint32_t *gscr, int64_
                     }
                 }
                 rpw_lsync();
-                // the head's keys that enter (at most the state's worst)
-                const int e = rpw_rank(Ek, hl, thr, true);
-                // merge: state entries before chunk entries of the same key
-                const int nout = min(kk + 1, a + e);
-                for (int t = lane; t < a; t += SSA_WAVE) {
-                    const uint32_t x = Sk[t];
-                    const int r = t + rpw_rank(Ek, e, x, false);
-                    if (r < nout) { Sn[r] = x; Tn[r] = (uint32_t)t; }
+                // the head's keys that enter (at most the state's worst): counted
+                // with ballots, the head being sorted
+                int e = 0;
+                for (int t0 = 0; t0 < hl; t0 += SSA_WAVE) {
+                    const int t = t0 + lane;
+                    e += __popcll(wave_ballot(t < hl && Ek[t] <= thr));
                 }
-                for (int t = lane; t < e && t < nout; t += SSA_WAVE) {
-                    const uint32_t x = Ek[t];
-                    const int r = t + rpw_rank(Sk, a, x, true);
-                    if (r < nout) { Sn[r] = x; Tn[r] = Et[t]; }
+                // merge: state entries before chunk entries of the same key; the
+                // two rank searches of a lane run side by side
+                const int nout = min(kk + 1, a + e);
+                const int em = min(e, nout);
+                for (int t = lane; t < a || t < em; t += SSA_WAVE) {
+                    const bool ds = t < a, de = t < em;
+                    const uint32_t xs = ds ? Sk[t] : 0u, xe = de ? Ek[t] : 0u;
+                    const int rs = t + (ds ? rpw_rank(Ek, e, xs, false) : 0);
+                    const int re = t + (de ? rpw_rank(Sk, a, xe, true) : 0);
+                    if (ds && rs < nout) { Sn[rs] = xs; Tn[rs] = (uint32_t)t; }
+                    if (de && re < nout) { Sn[re] = xe; Tn[re] = Et[t]; }
                 }
                 rpw_lsync();
                 // equal finite keys among the first kk + 1: note each tied value
