@@ -2381,8 +2381,11 @@ constexpr int RP_WAVES = 2;
 constexpr uint32_t RP_NEGINF = 0xff800000u;   // rank key of -inf: ~score_key(-inf)
 constexpr int RP_STACK = 64;
 
+// words of one replayed row: rank keys (W), 16-bit payload (key ids below
+// 2^16, or positions), TL/TR (two 16-bit lists), leaf bits, stack, bitmap,
+// glob scores
 __host__ __device__ inline int rp_lds_words(int W, int words) {
-    return (3 * W + (W + 31) / 32 + 1 + 3 * RP_STACK + words + 64 + 1) & ~1;
+    return (W + (W + 1) / 2 + W + (W + 31) / 32 + 1 + 3 * RP_STACK + words + 64 + 1) & ~1;
 }
 
 __device__ __forceinline__ void rp_sync() {
@@ -2394,7 +2397,7 @@ __device__ __forceinline__ void rp_sync() {
 
 struct RpArr {
     uint32_t *key;     // rank keys: smaller = earlier in top-k order
-    int32_t *cand;     // key ids carried along
+    uint16_t *cand;    // key ids (or positions) carried along
 };
 
 __device__ __forceinline__ void rp_swap(const RpArr &a, int i, int j) {
@@ -2611,9 +2614,10 @@ __device__ void rp_sort(const RpArr &a, uint16_t *TL, uint16_t *TR, uint32_t *lb
 // not fit; the same code runs on either (all accesses of a wave's arrays come
 // from that wave, whose stores its own later loads see after rp_sync).
 // Rows are taken only when more than `skip_max` are tied (fewer go to the
-// workgroup replay; skip_max < 0: always).
+// workgroup replay; skip_max < 0: always).  Six waves per SIMD (80 VGPRs):
+// with many rows the launch runs in rounds of resident rows.
 template <typename T, bool LSH_MODE, bool GLB>
-__global__ void __launch_bounds__(RP_WAVES * SSA_WAVE)
+__global__ void __launch_bounds__(RP_WAVES * SSA_WAVE) __attribute__((amdgpu_waves_per_eu(6)))
 topk_replay_kernel(SelP p, int chunk, int W, uint32_t *gscr, int skip_max) {
     extern __shared__ uint32_t rp_smem[];
     const int wid = threadIdx.x / SSA_WAVE;
@@ -2623,10 +2627,10 @@ topk_replay_kernel(SelP p, int chunk, int W, uint32_t *gscr, int skip_max) {
                          : rp_smem + (int64_t)wid * wave_words;
     RpArr A;
     A.key = base;
-    A.cand = (int32_t *)(base + W);
-    uint16_t *TL = (uint16_t *)(base + 2 * W);
+    A.cand = (uint16_t *)(base + W);
+    uint16_t *TL = (uint16_t *)(base + W + (W + 1) / 2);
     uint16_t *TR = TL + W;
-    uint32_t *lbits = base + 3 * W;
+    uint32_t *lbits = base + 2 * W + (W + 1) / 2;
     int32_t *stk = (int32_t *)(lbits + (W + 31) / 32 + 1);
     uint32_t *bm = (uint32_t *)(stk + 3 * RP_STACK);
     uint32_t *gsc = bm + p.words;
@@ -2723,7 +2727,7 @@ topk_replay_kernel(SelP p, int chunk, int W, uint32_t *gscr, int skip_max) {
                 if (in) {
                     const int at = kk + (int)(j0 - s0) + lane;
                     A.key[at] = keep ? ~sk : RP_NEGINF;
-                    A.cand[at] = v;
+                    A.cand[at] = (uint16_t)v;
                 }
                 rp_sync();
                 j0 += nl;
@@ -2794,9 +2798,10 @@ constexpr int RPW_TV = 4;            // tied key values noted per chunk
 constexpr uint32_t RPW_VALID = 1u << 31, RPW_EMPTY = 1u << 30, RPW_OWNER = 1u << 29,
                    RPW_VMASK = RPW_OWNER - 1u;
 
-// LDS of one replaying wave: keys and payload (W each), TL/TR, leaf bits, stack
+// LDS of one replaying wave: keys (W), 16-bit positions, TL/TR, leaf bits,
+// stack (the first 2 W words also hold a chunk's keys and tags while sorting)
 __host__ __device__ inline int rpw_slot_words(int W) {
-    return (3 * W + (W + 31) / 32 + 1 + 3 * RP_STACK + 1) & ~1;
+    return (2 * W + (W + 1) / 2 + (W + 31) / 32 + 1 + 3 * RP_STACK + 1) & ~1;
 }
 // LDS shared by the workgroup: bitmap, glob scores, list table, state keys,
 // merge output, per chunk (head length, tie count, tied keys, input state,
@@ -3173,10 +3178,10 @@ topk_replay_wg_kernel(SelP p, int chunk, int W, int nsim, uint32_t *gscr, int64_
         if (wid < nsim) {
             RpArr A;
             A.key = slot;
-            A.cand = (int32_t *)(slot + W);
-            uint16_t *TL = (uint16_t *)(slot + 2 * W);
+            A.cand = (uint16_t *)(slot + W);
+            uint16_t *TL = (uint16_t *)(slot + W + (W + 1) / 2);
             uint16_t *TR = TL + W;
-            uint32_t *lbits = slot + 3 * W;
+            uint32_t *lbits = slot + 2 * W + (W + 1) / 2;
             int32_t *stk = (int32_t *)(lbits + (W + 31) / 32 + 1);
             for (int f = wid; f < nmark; f += nsim) {
                 const int s = mk[f];
@@ -3185,11 +3190,11 @@ topk_replay_wg_kernel(SelP p, int chunk, int W, int nsim, uint32_t *gscr, int64_
                 const int si = csi[s];
                 for (int t = lane; t < kk; t += SSA_WAVE) {
                     A.key[t] = SK[(int64_t)si * kk + t];
-                    A.cand[t] = t;
+                    A.cand[t] = (uint16_t)t;
                 }
                 for (int t = lane; t < c; t += SSA_WAVE) {
                     A.key[kk + t] = skey[s0 + t];
-                    A.cand[kk + t] = kk + t;
+                    A.cand[kk + t] = (uint16_t)(kk + t);
                 }
                 rp_sync();
                 // torch.topk(best ++ chunk, kk): partial_sort when 64*kk <= width,

@@ -85,12 +85,12 @@ def test_argument_errors_are_reported_without_a_gpu():
 
 
 # ---------------------------------------------------------------------------- exact replay
-# Words of one replayed row's arrays (rank keys, key ids, two 16-bit stopper
-# lists, leaf bits, the partition stack, the seen bitmap, glob scores); two
+# Words of one replayed row's arrays (rank keys, 16-bit key ids, two 16-bit
+# stopper lists, leaf bits, the partition stack, the seen bitmap, glob scores); two
 # rows share a workgroup's 160 KiB of LDS (minus 512 bytes of static data).
 def _replay_words(W, M):
     words = ((M + 31) // 32 + 1) & ~1
-    return (3 * W + (W + 31) // 32 + 1 + 3 * 64 + words + 64 + 1) & ~1
+    return (W + (W + 1) // 2 + W + (W + 31) // 32 + 1 + 3 * 64 + words + 64 + 1) & ~1
 
 
 def _replay_fits(W, M):
@@ -121,7 +121,7 @@ def test_replay_beyond_lds_takes_a_workspace_region():
     N = 2048
     prev = None
     crossed = 0
-    for K in range(1200, 1500, 4):
+    for K in range(1500, 1700, 4):
         a, kk = _full_args(N, K)
         Call = 2 * 4 * kk
         chunk = min(Call, max(256, 4 * kk))

@@ -155,16 +155,31 @@ def test_lsh_builder_exact_tier_matches_oracle(case):
     np.testing.assert_array_equal(g, r)
 
 
-# num_neighbors 1400: kk = 1388, so best ++ chunk spans 6,940 slots and two
-# replayed rows no longer fit a workgroup's LDS; small integers tie at the
-# kk-th score on many rows, so the replay runs from its workspace region
+# num_neighbors 1400: kk = 1388, so best ++ chunk spans 6,940 slots; about
+# 120 rows tie at the kk-th score (small integers), which the workgroup
+# replay takes with two waves' arrays in LDS
 HUGE_K = ("huge_k_replay_workspace", 1, 1, 1, 2048, 2048, 16, 2, 3, 0, 1400, 4, 2, True, False)
+# num_neighbors 1700 over 4,096 keys: kk = 1688 and 8,440 slots, which no
+# longer fit LDS twice; 1,634 tied rows, more than the workgroup replay takes,
+# so the per-wave replay runs from its workspace region
+HUGE_K_WAVE = ("huge_k_per_wave_replay_workspace", 1, 1, 1, 4096, 4096, 16, 2, 3, 0, 1700, 4, 2,
+               True, False)
 
 
 def test_full_graph_exact_tier_huge_k_replay_outside_lds():
     attn, got, got_v, ref, (B, H, N, M, K, w, cross, causal, glob) = _graph_case(HUGE_K, 0)
     print(f"  huge K: {ref['n_ties']} rows with a tied kk-th score", flush=True)
     assert ref["n_ties"] > 0
+    win = attn.win_builder(N, M, "cpu").numpy()
+    rnb, rva = oracle.merge(win, glob.numpy(), ref["idx"], has_self=True, total_k=K)
+    np.testing.assert_array_equal(got.cpu().numpy().reshape(B * H, N, -1), rnb)
+    np.testing.assert_array_equal(got_v.cpu().numpy().reshape(B * H, N, -1), rva)
+
+
+def test_full_graph_exact_tier_huge_k_per_wave_replay_workspace():
+    attn, got, got_v, ref, (B, H, N, M, K, w, cross, causal, glob) = _graph_case(HUGE_K_WAVE, 0)
+    print(f"  huge K, per-wave replay: {ref['n_ties']} rows with a tied kk-th score", flush=True)
+    assert ref["n_ties"] > 1024
     win = attn.win_builder(N, M, "cpu").numpy()
     rnb, rva = oracle.merge(win, glob.numpy(), ref["idx"], has_self=True, total_k=K)
     np.testing.assert_array_equal(got.cpu().numpy().reshape(B * H, N, -1), rnb)
