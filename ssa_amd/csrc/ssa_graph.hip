@@ -2826,22 +2826,33 @@ __device__ __forceinline__ void rpw_lsync() {
 }
 
 // one wave sorts k[0, e) ascending, t alongside (bitonic with a mirrored first
-// step, which sorts any e when pairs reaching past e are skipped)
+// step, which sorts any e when pairs reaching past e are skipped).  The pairs
+// of a step are disjoint: four rows of 64 are read before any is written.
 __device__ void rpw_sort(uint32_t *k, uint32_t *t, int e) {
     const int lane = lane_id();
     for (int size = 2; size < 2 * e; size <<= 1) {
         for (int j = size >> 1; j > 0; j >>= 1) {
-            for (int i0 = 0; i0 < e; i0 += SSA_WAVE) {
-                const int i = i0 + lane;
-                const int pi = j == (size >> 1) ? (i ^ (size - 1)) : (i ^ j);
-                if (i < e && pi > i && pi < e) {
-                    const uint32_t a = k[i], b = k[pi];
-                    if (b < a) {
-                        k[i] = b;
-                        k[pi] = a;
-                        const uint32_t ta = t[i];
-                        t[i] = t[pi];
-                        t[pi] = ta;
+            for (int i0 = 0; i0 < e; i0 += 4 * SSA_WAVE) {
+                int ii[4], pp[4];
+                bool on[4];
+                uint32_t a[4], b[4], ta[4], tb[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    ii[u] = i0 + u * SSA_WAVE + lane;
+                    pp[u] = j == (size >> 1) ? (ii[u] ^ (size - 1)) : (ii[u] ^ j);
+                    on[u] = ii[u] < e && pp[u] > ii[u] && pp[u] < e;
+                    a[u] = on[u] ? k[ii[u]] : 0u;
+                    b[u] = on[u] ? k[pp[u]] : 0u;
+                    ta[u] = on[u] ? t[ii[u]] : 0u;
+                    tb[u] = on[u] ? t[pp[u]] : 0u;
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    if (on[u] && b[u] < a[u]) {
+                        k[ii[u]] = b[u];
+                        k[pp[u]] = a[u];
+                        t[ii[u]] = tb[u];
+                        t[pp[u]] = ta[u];
                     }
                 }
             }
