@@ -309,3 +309,87 @@ def test_cpu_baseline_port_reproduces_reference_forward(path):
             R=c["num_hash_rounds"], max_p=c["max_num_hashes"], T=c["lsh_num_probes"],
             causal=m["causal"], fp32w=c["fp32_attn_weights"])
     assert torch.equal(out.float(), torch.from_numpy(z["out"]))
+
+
+# ---------------------------------------------------------------------------- chunked top-k
+def _chunked_topk(sc, ids, kk, chunk):
+    """The reference's running top-k over stream chunks (sparse_attention.py:904-922)."""
+    bs = np.full(kk, -np.inf, np.float32)
+    bi = np.zeros(kk, np.int64)
+    for s0 in range(0, len(sc), chunk):
+        v, idx = oracle.topk_row(np.concatenate([bs, sc[s0:s0 + chunk]]), kk)
+        bi = np.concatenate([bi, ids[s0:s0 + chunk]])[np.asarray(idx)]
+        bs = np.asarray(v, np.float32)
+    return bs, bi
+
+
+def _decomposed_topk(sc, ids, kk, chunk, only_cut_ties):
+    """The same result chunk by chunk from the states' sorted keys alone: a
+    chunk replays on the previous state's keys with positions as payload only
+    when equal finite keys reach its first kk + 1 merged places (for a set,
+    only when that key is the final kk-th one); otherwise the sorted merge is
+    its map.  Finite output slots are then followed back through the maps."""
+    nch = (len(sc) + chunk - 1) // chunk
+    S = np.full(kk, -np.inf, np.float32)
+    maps, tied, states = [], [], []
+    for s in range(nch):
+        merged = np.concatenate([S, sc[s * chunk:(s + 1) * chunk]])
+        order = sorted((i for i in range(len(merged)) if np.isfinite(merged[i])),
+                       key=lambda i: (-merged[i], i >= kk))
+        top = order[:kk + 1]
+        tied.append({merged[top[t]] for t in range(min(kk, len(top) - 1))
+                     if merged[top[t]] == merged[top[t + 1]]})
+        states.append(S.copy())
+        maps.append(top[:kk] + [0] * (kk - min(kk, len(top))))
+        an = min(kk, len(order))
+        S = np.full(kk, -np.inf, np.float32)
+        S[:an] = merged[order[:an]]
+    fcount = int(np.isfinite(S).sum())
+    replayed = 0
+    for s in range(nch):
+        if only_cut_ties:
+            need = fcount == kk and S[kk - 1] in tied[s]
+        else:
+            need = bool(tied[s])
+        if need:
+            _, idx = oracle.topk_row(np.concatenate([states[s], sc[s * chunk:(s + 1) * chunk]]), kk)
+            maps[s] = list(np.asarray(idx))
+            replayed += 1
+    out = []
+    for t in range(fcount):
+        pos, slot = t, -1
+        for s in range(nch - 1, -1, -1):
+            tg = maps[s][pos]
+            if tg >= kk:
+                slot = s * chunk + tg - kk
+                break
+            pos = tg
+        out.append(ids[slot])
+    return S, np.array(out, np.int64), replayed
+
+
+@pytest.mark.parametrize("only_cut_ties", [False, True])
+def test_chunked_topk_decomposes_into_independent_chunks(only_cut_ties):
+    """The workgroup tie replay's decomposition: per chunk on the states' keys,
+    then followed back; the ordered list exactly, or the set (cut-key rule)."""
+    rng = np.random.default_rng(11)
+    replayed = chunks = 0
+    for _ in range(150):
+        kk = int(rng.choice([3, 8, 16, 32]))
+        chunk = int(rng.choice([4 * kk, 256, 5 * kk + 3]))
+        n = int(rng.integers(chunk // 2, 6 * chunk))
+        sc = rng.integers(0, int(rng.choice([5, 20, 100, 1000])), n).astype(np.float32)
+        sc[rng.random(n) < rng.choice([0.0, 0.3, 0.7])] = -np.inf
+        ids = rng.permutation(10 * n)[:n].astype(np.int64)
+        bs, bi = _chunked_topk(sc, ids, kk, chunk)
+        S, out, r = _decomposed_topk(sc, ids, kk, chunk, only_cut_ties)
+        f = int(np.isfinite(bs).sum())
+        np.testing.assert_array_equal(S[:f], bs[:f])
+        assert len(out) == f
+        if only_cut_ties:
+            assert sorted(out.tolist()) == sorted(bi[:f].tolist())
+        else:
+            np.testing.assert_array_equal(out, bi[:f])
+        replayed += r
+        chunks += (n + chunk - 1) // chunk
+    assert 0 < replayed < chunks
