@@ -3064,9 +3064,61 @@ topk_replay_wg_kernel(SelP p, int chunk, int W, int nsim, uint32_t *gscr, int64_
                     }
                 }
                 rp_sync();
-                rpw_sort(Ek, Et, e);
                 // the sorted head: the first kk + 1 finite keys (-inf sorts last)
-                const int hl = min(rpw_rank(Ek, e, RP_NEGINF, false), kk + 1);
+                int hl;
+                if (e > kk + 1 && e <= 16 * SSA_WAVE) {
+                    // the (kk + 1)-th smallest key first (a bitwise search over
+                    // the keys in registers), then only the head is sorted; of
+                    // several keys equal to it any may complete the head (equal
+                    // keys that reach a state are ties, and tied chunks replay)
+                    uint32_t kv[16], tv[16];
+                    int nf = 0;
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const int t = i * SSA_WAVE + lane;
+                        kv[i] = t < e ? Ek[t] : 0xffffffffu;
+                        tv[i] = t < e ? Et[t] : 0u;
+                        nf += __popcll(wave_ballot(t < e && kv[i] != RP_NEGINF));
+                    }
+                    hl = min(nf, kk + 1);
+                    uint32_t tau = 0u;
+                    for (int bit = 31; bit >= 0; --bit) {
+                        const uint32_t probe = tau | ((1u << bit) - 1u);
+                        int c = 0;
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) c += __popcll(wave_ballot(kv[i] <= probe));
+                        if (c < hl) tau |= 1u << bit;
+                    }
+                    rp_sync();
+                    int nlt = 0;
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const bool lt = kv[i] < tau;
+                        const uint64_t m = wave_ballot(lt);
+                        if (lt) {
+                            Ek[nlt + lanes_below(m)] = kv[i];
+                            Et[nlt + lanes_below(m)] = tv[i];
+                        }
+                        nlt += __popcll(m);
+                    }
+                    int neq = nlt;
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const bool eq = kv[i] == tau;
+                        const uint64_t m = wave_ballot(eq);
+                        const int at = neq + lanes_below(m);
+                        if (eq && at < hl) {
+                            Ek[at] = kv[i];
+                            Et[at] = tv[i];
+                        }
+                        neq += __popcll(m);
+                    }
+                    rp_sync();
+                    rpw_sort(Ek, Et, hl);
+                } else {
+                    rpw_sort(Ek, Et, e);
+                    hl = min(rpw_rank(Ek, e, RP_NEGINF, false), kk + 1);
+                }
                 for (int t = lane; t < hl; t += SSA_WAVE) {
                     SS[(int64_t)s * (kk + 1) + t] = Ek[t];
                     ST[(int64_t)s * (kk + 1) + t] = Et[t];
