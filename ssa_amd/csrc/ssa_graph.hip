@@ -602,7 +602,8 @@ __device__ void qb_write_tiles(const QbP &p, int inst, int bh, int r, int t, int
 
 __global__ void __launch_bounds__(256) qb_scatter_kernel(QbP p) {
     // rank of each query among the block's queries of its bucket, in position
-    // order: per wave one ballot per distinct bucket, then the waves in order
+    // order: per wave the lanes of one bucket matched bit by bit (log2 NB
+    // ballots), then the waves in order
     extern __shared__ int32_t sc_smem[];   // [4][NB] per-wave counts, then a scan buffer
     const int inst = blockIdx.y;
     int bh, r, t;
@@ -617,16 +618,15 @@ __global__ void __launch_bounds__(256) qb_scatter_kernel(QbP p) {
     const int n = blockIdx.x * blockDim.x + threadIdx.x;
     const bool in = n < p.N;
     const int u = in ? p.qid[(((int64_t)bh * p.N + n) * p.R + r) * p.NS + t] : -1;
-    int local = 0;
-    uint64_t todo = wave_ballot(in);
-    while (todo) {
-        const int leader = (int)__ffsll((long long)todo) - 1;
-        const int ul = __shfl(u, leader, SSA_WAVE);
-        const uint64_t m = wave_ballot(in && u == ul);
-        if (in && u == ul) local = lanes_below(m);
-        if (lane_id() == leader) sc_smem[wid * p.NB + ul] = __popcll(m);
-        todo &= ~m;
+    uint64_t same = wave_ballot(in);
+    for (int b = 0; (1 << b) < p.NB; ++b) {
+        const bool bit = ((u >> b) & 1) != 0;
+        const uint64_t m = wave_ballot(in && bit);
+        same &= bit ? m : ~m;
     }
+    const int local = lanes_below(same);
+    // the lowest lane of each bucket gives the wave's count for it
+    if (in && local == 0) sc_smem[wid * p.NB + u] = __popcll(same);
     __syncthreads();
     if (in) {
         int pos = p.hcnt[((int64_t)inst * gridDim.x + blockIdx.x) * p.NB + u] + local;
