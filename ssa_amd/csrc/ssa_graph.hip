@@ -63,6 +63,7 @@ struct Dims {
     int Cs;            // score row stride: min(C, M) rounded up to 64 members
     int rpw_blocks;    // blocks of the workgroup tie replay (0: the per-wave replay)
     int rpw_nsim;      // its replaying waves per block
+    int ctab;          // the list sort writes the cut's rank table (causal only)
 };
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -1028,6 +1029,10 @@ struct LsP {
     const uint32_t *kpart;
     uint32_t *knorm;
     int R;
+    // optional, per (row, bucket, 32-id word) of a long list: (members with a
+    // smaller id, the word's member bits) -- the cut's count of members below
+    // a query without a search
+    uint2 *ctab;
 };
 
 __global__ void __launch_bounds__(256) list_sort_kernel(LsP p) {
@@ -1084,7 +1089,12 @@ __global__ void __launch_bounds__(256) list_sort_kernel(LsP p) {
         __syncthreads();
         int acc = x - c;
         for (int k = 0; k < wv; ++k) acc += wsum[k];
-        for (int w = w0; w < w0 + per && w < W; ++w) { pre[w] = acc; acc += __popc(bmp[w]); }
+        uint2 *ct = p.ctab ? p.ctab + (prow * p.NB + u) * (int64_t)W : nullptr;
+        for (int w = w0; w < w0 + per && w < W; ++w) {
+            pre[w] = acc;
+            if (ct) ct[w] = make_uint2((uint32_t)acc, bmp[w]);
+            acc += __popc(bmp[w]);
+        }
         __syncthreads();
         for (int i = tid; i < nv; i += 256) {
             const int id = pr[st + i];
@@ -1165,6 +1175,7 @@ struct CutP {
     int4 *cut;
     int32_t *srix;     // per (row, list): offset of the query's score row in its head's
                        // region of S (lists * N * C elements), in elements
+    const uint2 *ctab; // optional: the list sort's rank table of long lists
     int N, M, R, NS, NB, C, Cs, Hq, Hkv, rep, bh0, G, causal, nlists;
     int64_t rows;
 };
@@ -1195,13 +1206,19 @@ __global__ void __launch_bounds__(256) cut_kernel(CutP p) {
     } else {
         const int nv = min(sz, p.C);
         if (p.causal) {
-            const int32_t *sd = p.sid + prow * p.M + st;
-            int lo = 0, hi = nv;                   // members with id < n
-            while (lo < hi) {
-                const int mid = (lo + hi) >> 1;
-                if (sd[mid] < n) lo = mid + 1; else hi = mid;
+            if (p.ctab && nv >= LS_RANK_MIN) {
+                // members with id < n: those below n's 32-id word, then its bits
+                const uint2 e = p.ctab[(prow * p.NB + u) * (int64_t)((p.M + 31) / 32) + (n >> 5)];
+                cutoff = (int)e.x + __popc(e.y & ((1u << (n & 31)) - 1u));
+            } else {
+                const int32_t *sd = p.sid + prow * p.M + st;
+                int lo = 0, hi = nv;               // members with id < n
+                while (lo < hi) {
+                    const int mid = (lo + hi) >> 1;
+                    if (sd[mid] < n) lo = mid + 1; else hi = mid;
+                }
+                cutoff = lo;
             }
-            cutoff = lo;
             const int a = cutoff < nv ? p.smin[prow * p.M + st + cutoff] : p.C;
             const int fb = (sz < p.C && f >= n) ? sz : p.C;
             first = min(a, fb);
@@ -3332,7 +3349,7 @@ struct Layout {
     int64_t kid, qid, perm, bstart, bsize, sorttmp, sid, rnk, smin, inv, cut, srix, qpos, cnt, off,
         cur,
         qlist, tiles, ntiles, tcnt, kbase, S,
-        tie_list, tie_count, aux, knorm, kpart, rpscr, rpw, total;
+        tie_list, tie_count, aux, knorm, kpart, rpscr, rpw, ctab, total;
 };
 
 int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
@@ -3370,6 +3387,7 @@ Layout plan(const Dims &D) {
     L.tie_count = take(4);
     L.aux = take(nbh * D.N * (D.G + 3) * 4);
     L.knorm = take(D.BK * 4);
+    L.ctab = take(D.ctab ? D.BK * D.R * D.NB * (int64_t)((D.M + 31) / 32) * 8 : 0);
     L.kpart = take(D.BK * (D.M / 16) * 4);
     {
         // the replay's per-wave arrays, when they do not fit LDS
@@ -3484,6 +3502,12 @@ int make_dims(const ssa_graph_args *a, Dims &D, bool need_q = true, int64_t ws_c
         const int64_t budget = ws_cap > 0 ? ws_cap / 4 : ((int64_t)256 << 20);
         D.rpw_blocks = (int)std::min<int64_t>(RPW_MAX_BLOCKS, budget / per);
         if (D.rpw_nsim < 1 || D.M >= (1 << 29) || D.Call >= ((int64_t)1 << 31)) D.rpw_blocks = 0;
+    }
+    {
+        // the cut's rank table: 8 bytes per (kv head, round, bucket, 32 key
+        // ids), when causal and within 256 MiB (a sixteenth of ws_cap)
+        const int64_t tb = D.BK * D.R * D.NB * (int64_t)((D.M + 31) / 32) * 8;
+        D.ctab = a->causal && tb <= (ws_cap > 0 ? ws_cap / 16 : ((int64_t)256 << 20)) ? 1 : 0;
     }
     int64_t nbh = ((int64_t)8 << 30) / per_bh;
     if (nbh < 1) nbh = 1;
@@ -3830,6 +3854,7 @@ int keys_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws
         lp.smin = (int32_t *)(ws + L.smin);
         lp.inv = (int32_t *)(ws + L.inv);
         lp.M = D.M; lp.NB = D.NB; lp.C = D.C;
+        lp.ctab = D.ctab ? (uint2 *)(ws + L.ctab) : nullptr;
         if (key_norm_in_hash(D, a)) {
             lp.kpart = (const uint32_t *)(ws + L.kpart);
             lp.knorm = (uint32_t *)(ws + L.knorm);
@@ -3958,6 +3983,7 @@ int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char 
         cp.cut = (int4 *)(ws + L.cut);
         cp.qpos = qp.qpos;
         cp.srix = (int32_t *)(ws + L.srix);
+        cp.ctab = D.ctab ? (const uint2 *)(ws + L.ctab) : nullptr;
         cp.N = D.N; cp.M = D.M; cp.R = D.R; cp.NS = D.NS; cp.NB = D.NB; cp.C = D.C; cp.Cs = D.Cs;
         cp.Hq = D.Hq; cp.Hkv = D.Hkv; cp.rep = D.rep; cp.bh0 = (int)bh0; cp.G = D.G;
         cp.causal = a->causal ? 1 : 0; cp.nlists = D.nlists; cp.rows = (int64_t)nbh * D.N;
