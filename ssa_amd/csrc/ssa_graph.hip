@@ -4131,7 +4131,8 @@ int side_stream(SideStream **out) {
 }
 
 // The build: the key phase, then the query phase.  With a workspace of its own
-// (not the fixed array of the build without allocation) the query hash and aux
+// (not the fixed array of the build without allocation) and a stream that is
+// not being captured into a graph, the query hash and aux
 // of the first head chunk, which need q and the key norms but not the key
 // sort, run on a side stream beside the sort: the sort's top levels hold one
 // workgroup per (kv head, round) and leave most CUs idle.
@@ -4181,7 +4182,11 @@ int build_impl(const ssa_graph_args *a, void *workspace, int64_t workspace_bytes
     }
     hipStream_t st = (hipStream_t)stream;
     char *ws = (char *)workspace;
-    const bool overlap = ws_cap == 0;
+    // a stream under graph capture keeps the whole build (no side stream is
+    // created or joined while capturing)
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    SSA_CHECK_HIP(hipStreamIsCapturing(st, &cap));
+    const bool overlap = ws_cap == 0 && cap == hipStreamCaptureStatusNone;
     switch (a->k.dtype) {
         case SSA_F32: return build_typed<float>(D, a, L, ws, st, overlap);
         case SSA_BF16: return build_typed<bf16_t>(D, a, L, ws, st, overlap);

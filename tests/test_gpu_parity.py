@@ -192,6 +192,37 @@ def test_lsh_builder_exact_tier_huge_k_replay_outside_lds():
     np.testing.assert_array_equal(got.cpu().numpy().reshape(B * H, N, -1), ref["idx"])
 
 
+def test_graph_build_captured_in_a_graph_replays_the_eager_graph():
+    """A build captured into a HIP graph (one stream under capture) gives the
+    eager graph on every replay, with eager builds in between."""
+    from ssa_amd import SSAConfig, SparseAttention
+    torch.manual_seed(5)
+    cfg = SSAConfig(d_model=256, num_heads=4, num_kv_heads=2, num_neighbors=48, window_size=4,
+                    num_global_tokens=2, num_hash_rounds=4, lsh_num_probes=1, causal=True)
+    with _nowarn():
+        attn = SparseAttention(cfg).to(DEV).eval()
+    x = torch.randn(2, 300, 256, device=DEV)
+    with torch.no_grad():
+        q, k, _ = attn._project(x, x, False)
+        eager = attn._build_graph_ids32(q, k, 300, 300, 2, True, False)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            attn._build_graph_ids32(q, k, 300, 300, 2, True, False)
+        torch.cuda.current_stream().wait_stream(side)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            out = attn._build_graph_ids32(q, k, 300, 300, 2, True, False)
+        for _ in range(3):
+            out.fill_(7)
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, eager)
+            again = attn._build_graph_ids32(q, k, 300, 300, 2, True, False)
+            torch.cuda.synchronize()
+            assert torch.equal(again, eager)
+
+
 # Tied-row counts on either side of the replay's two paths (a 256-CU device):
 # up to four tied rows per workgroup take the workgroup replay (several rows
 # per workgroup past 256), more take the per-wave replay
