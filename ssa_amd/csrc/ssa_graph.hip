@@ -1160,21 +1160,6 @@ __global__ void __launch_bounds__(256) list_sort_kernel(LsP p) {
     }
 }
 
-// knorm[bk] = the max of the key hash's M / 16 tile maxima of |k|^2 for kv
-// head bk (one block each): the list sort's reduction, for a build that runs
-// the query-side kernels beside the key sort
-__global__ void __launch_bounds__(256) knorm_reduce_kernel(const uint32_t *kpart,
-                                                           uint32_t *knorm, int nt) {
-    __shared__ uint32_t kred[4];
-    const int64_t bk = blockIdx.x;
-    uint32_t m = 0u;
-    for (int i = threadIdx.x; i < nt; i += 256) m = max(m, kpart[bk * nt + i]);
-    m = wave_max_u(m);
-    if (lane_id() == 0) kred[threadIdx.x / SSA_WAVE] = m;
-    __syncthreads();
-    if (threadIdx.x == 0) knorm[bk] = max(max(kred[0], kred[1]), max(kred[2], kred[3]));
-}
-
 // Per (query row, list): the number of sorted members below the query
 // (causal; all of them otherwise), and where the query's own key first occurs
 // in the list -- a member at or past the query (causal substitution, :698-709),
@@ -3818,13 +3803,11 @@ int select_dispatch(const SelP &sp, hipStream_t st) {
 
 // Key phase: bucket ids of the keys, the bucket permutation and tables and
 // the sorted candidate lists -- everything that needs k but not q.
-// part 1: the key hash and the key norms; part 2: the sort and the lists
-// (list_norms: the list sort also reduces the hash's norm maxima)
 template <typename T>
 int keys_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws,
-               hipStream_t st, int part = 3, bool list_norms = true) {
+               hipStream_t st) {
     int rc = SSA_OK;
-    if (part & 1) {
+    {
         rc = launch_hash<T>(D, a, L, ws, st, true);
         if (rc) return rc;
         // max |k|^2 per (batch, kv head): the query code scales derive from it
@@ -3855,7 +3838,6 @@ int keys_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws
             SSA_CHECK_LAUNCH();
         }
     }
-    if (!(part & 2)) return SSA_OK;
     // the key hash cleared the sort's counter
     rc = ssa_launch_bucket_sort((const uint16_t *)(ws + L.kid), (int)(D.BK * D.R), D.M, D.P,
                                 (int32_t *)(ws + L.perm), (int32_t *)(ws + L.bstart),
@@ -3873,7 +3855,7 @@ int keys_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws
         lp.inv = (int32_t *)(ws + L.inv);
         lp.M = D.M; lp.NB = D.NB; lp.C = D.C;
         lp.ctab = D.ctab ? (uint2 *)(ws + L.ctab) : nullptr;
-        if (key_norm_in_hash(D, a) && list_norms) {
+        if (key_norm_in_hash(D, a)) {
             lp.kpart = (const uint32_t *)(ws + L.kpart);
             lp.knorm = (uint32_t *)(ws + L.knorm);
             lp.R = D.R;
@@ -3891,9 +3873,11 @@ int keys_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws
     return SSA_OK;
 }
 
-// The rescore's parameters that hold for every head chunk
+// Query phase: everything else, given the key phase's results in ws.
 template <typename T>
-RsP rescore_params(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws) {
+int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws,
+                  hipStream_t st) {
+    // the rescore's parameters that hold for every head chunk
     RsP rp{};
     rp.sid = (const int32_t *)(ws + L.sid);
     rp.bstart = (const int32_t *)(ws + L.bstart);
@@ -3912,72 +3896,15 @@ RsP rescore_params(const Dims &D, const ssa_graph_args *a, const Layout &L, char
         rp.k32 = (rp.ksn * el < ((int64_t)1 << 24) &&
                   ((int64_t)D.M * rp.ksn + D.d) * el < ((int64_t)1 << 31)) ? 1 : 0;
     }
-    return rp;
-}
-
-// Whether the rescore (and aux) run on the matrix cores, and whether aux also
-// hashes the queries (one pass over q): without injected projections, with
-// 16-byte aligned planes and their projection rows within 48 KB of LDS per block
-template <typename T>
-void query_modes(const Dims &D, const ssa_graph_args *a, const RsP &rp, bool &mfma,
-                 bool &fuse_qhash) {
-    mfma = rescore_uses_mfma<T>(D.d, rp);
+    const bool mfma = rescore_uses_mfma<T>(D.d, rp);
+    // With aux on the matrix cores, aux_mfma_kernel also hashes the queries
+    // (one pass over q): without injected projections, with 16-byte aligned
+    // planes and their projection rows within 48 KB of LDS per block
     const int np16 = (int)ceil_div((int64_t)D.R * D.P, 16) * 16;
-    fuse_qhash = mfma && !a->q_proj && (uintptr_t)a->rand_proj % 16 == 0 &&
-                 (size_t)4 * 16 * (np16 + 1) * 4 <= 48 * 1024;
-}
-
-// aux of the head chunk [bh0, bh0 + nbh): the rescore codes its scores with
-// the query scales it writes, and the query buckets need the ids it writes
-// when fused
-template <typename T>
-int aux_chunk(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws, int64_t bh0,
-          int nbh, bool mfma, bool fuse_qhash, hipStream_t st) {
-    AuxP ap{};
-    ap.q = a->q.ptr; ap.k = a->k.ptr;
-    ap.qsb = a->q.sb; ap.qsh = a->q.sh; ap.qsn = a->q.sn;
-    ap.ksb = a->k.sb; ap.ksh = a->k.sh; ap.ksn = a->k.sn;
-    ap.glob = a->glob;
-    ap.knorm = (const uint32_t *)(ws + L.knorm);
-    ap.N = D.N; ap.Hq = D.Hq; ap.Hkv = D.Hkv; ap.rep = D.rep; ap.bh0 = (int)bh0;
-    ap.nbh = nbh; ap.G = D.G; ap.NA = D.G + 3; ap.causal = a->causal; ap.d = D.d;
-    ap.out = (float *)(ws + L.aux);
-    if (fuse_qhash) {
-        ap.planes = a->rand_proj;
-        ap.R = D.R; ap.maxP = D.maxP; ap.P = D.P; ap.Tp = D.Tp; ap.NS = D.NS;
-        ap.qid = (uint16_t *)(ws + L.qid);
-        // the tie-row counter of the select kernels (replayed once, after every chunk)
-        ap.zero1 = bh0 == 0 ? (int32_t *)(ws + L.tie_count) : nullptr;
-    }
-    return aux_dispatch<T>(D.d, mfma, ap, st);
-}
-
-// The query hash (when aux does not fuse it) and aux of the first head chunk:
-// they need q and the key norms, not the key sort
-template <typename T>
-int queries_first(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws,
-                  hipStream_t st) {
-    const RsP rp = rescore_params<T>(D, a, L, ws);
-    bool mfma, fuse_qhash;
-    query_modes<T>(D, a, rp, mfma, fuse_qhash);
-    if (!fuse_qhash) {
-        const int rc = launch_hash<T>(D, a, L, ws, st, false);
-        if (rc) return rc;
-    }
-    return aux_chunk<T>(D, a, L, ws, 0, (int)std::min<int64_t>(D.BH, D.nbh_chunk), mfma,
-                        fuse_qhash, st);
-}
-
-// Query phase: everything else, given the key phase's results in ws (and,
-// with first_done, queries_first's)
-template <typename T>
-int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws,
-                  hipStream_t st, bool first_done = false) {
-    RsP rp = rescore_params<T>(D, a, L, ws);
-    bool mfma, fuse_qhash;
-    query_modes<T>(D, a, rp, mfma, fuse_qhash);
+    const bool fuse_qhash = mfma && !a->q_proj && (uintptr_t)a->rand_proj % 16 == 0 &&
+                            (size_t)4 * 16 * (np16 + 1) * 4 <= 48 * 1024;
     int rc = SSA_OK;
-    if (!fuse_qhash && !first_done) {
+    if (!fuse_qhash) {
         rc = launch_hash<T>(D, a, L, ws, st, false);
         if (rc) return rc;
     }
@@ -3985,10 +3912,26 @@ int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char 
     for (int64_t bh0 = 0; bh0 < D.BH; bh0 += D.nbh_chunk) {
         const int nbh = (int)((D.BH - bh0) < D.nbh_chunk ? (D.BH - bh0) : D.nbh_chunk);
         const int ninst = nbh * D.R * D.NS;
-        if (!(first_done && bh0 == 0)) {
-            rc = aux_chunk<T>(D, a, L, ws, bh0, nbh, mfma, fuse_qhash, st);
-            if (rc) return rc;
+        // aux first: the rescore codes its scores with the query scales it
+        // writes, and the query buckets need the ids it writes when fused
+        AuxP ap{};
+        ap.q = a->q.ptr; ap.k = a->k.ptr;
+        ap.qsb = a->q.sb; ap.qsh = a->q.sh; ap.qsn = a->q.sn;
+        ap.ksb = a->k.sb; ap.ksh = a->k.sh; ap.ksn = a->k.sn;
+        ap.glob = a->glob;
+        ap.knorm = (const uint32_t *)(ws + L.knorm);
+        ap.N = D.N; ap.Hq = D.Hq; ap.Hkv = D.Hkv; ap.rep = D.rep; ap.bh0 = (int)bh0;
+        ap.nbh = nbh; ap.G = D.G; ap.NA = D.G + 3; ap.causal = a->causal; ap.d = D.d;
+        ap.out = (float *)(ws + L.aux);
+        if (fuse_qhash) {
+            ap.planes = a->rand_proj;
+            ap.R = D.R; ap.maxP = D.maxP; ap.P = D.P; ap.Tp = D.Tp; ap.NS = D.NS;
+            ap.qid = (uint16_t *)(ws + L.qid);
+            // the tie-row counter of the select kernels (replayed once, after every chunk)
+            ap.zero1 = bh0 == 0 ? (int32_t *)(ws + L.tie_count) : nullptr;
         }
+        rc = aux_dispatch<T>(D.d, mfma, ap, st);
+        if (rc) return rc;
         QbP qp{};
         qp.qid = (const uint16_t *)(ws + L.qid);
         qp.bsize = (const int32_t *)(ws + L.bsize);
@@ -4025,8 +3968,8 @@ int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char 
 
         rp.tiles = qp.tiles; rp.ntiles = qp.ntiles; rp.qlist = qp.qlist;
         rp.bh0 = (int)bh0;
-        rp.aux = (float *)(ws + L.aux);
-        rp.NA = D.G + 3;
+        rp.aux = ap.out;
+        rp.NA = ap.NA;
         const int64_t grid = 8 * ceil_div((int64_t)ninst * (ceil_div(D.N, TQ) + D.NB), 8);
         rc = rescore_dispatch<T>(D.d, rp, grid, st);
         if (rc) return rc;
@@ -4070,8 +4013,8 @@ int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char 
         sp.out_idx32 = a->mode == SSA_GRAPH_FULL ? a->out_idx32 : nullptr;
         sp.tie_list = (int32_t *)(ws + L.tie_list);
         sp.tie_count = (int32_t *)(ws + L.tie_count);
-        sp.aux = (float *)(ws + L.aux);
-        sp.NA = D.G + 3;
+        sp.aux = ap.out;
+        sp.NA = ap.NA;
         sp.perm_bytes = (int)(D.BK * D.R * D.M * 4);
         sp.nblocks = ceil_div(sp.rows, SEL_WAVES);
         rc = select_dispatch<T>(sp, st);
@@ -4105,64 +4048,6 @@ extern "C" int64_t ssa_graph_workspace_bytes(const ssa_graph_args *a) {
 }
 
 namespace {
-// A second stream per (host thread, device) for the query-side kernels that do
-// not wait for the key sort, and the events that fork it from and join it to
-// the caller's stream (default priority; created on first use, kept until the
-// process ends).
-struct SideStream {
-    hipStream_t s = nullptr;
-    hipEvent_t fork = nullptr, join = nullptr;
-};
-
-int side_stream(SideStream **out) {
-    constexpr int kMaxDev = 64;
-    static thread_local SideStream per[kMaxDev];
-    int dev = 0;
-    SSA_CHECK_HIP(hipGetDevice(&dev));
-    SSA_CHECK_ARG(dev >= 0 && dev < kMaxDev, "build_graph: device %d", dev);
-    SideStream &ss = per[dev];
-    if (!ss.s) {
-        SSA_CHECK_HIP(hipStreamCreateWithFlags(&ss.s, hipStreamNonBlocking));
-        SSA_CHECK_HIP(hipEventCreateWithFlags(&ss.fork, hipEventDisableTiming));
-        SSA_CHECK_HIP(hipEventCreateWithFlags(&ss.join, hipEventDisableTiming));
-    }
-    *out = &ss;
-    return SSA_OK;
-}
-
-// The build: the key phase, then the query phase.  With a workspace of its own
-// (not the fixed array of the build without allocation) and a stream that is
-// not being captured into a graph, the query hash and aux
-// of the first head chunk, which need q and the key norms but not the key
-// sort, run on a side stream beside the sort: the sort's top levels hold one
-// workgroup per (kv head, round) and leave most CUs idle.
-template <typename T>
-int build_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws,
-                hipStream_t st, bool overlap) {
-    int rc;
-    if (!overlap) {
-        if ((rc = keys_typed<T>(D, a, L, ws, st))) return rc;
-        return queries_typed<T>(D, a, L, ws, st);
-    }
-    SideStream *ss = nullptr;
-    if ((rc = side_stream(&ss))) return rc;
-    if ((rc = keys_typed<T>(D, a, L, ws, st, 1))) return rc;
-    SSA_CHECK_HIP(hipEventRecord(ss->fork, st));
-    SSA_CHECK_HIP(hipStreamWaitEvent(ss->s, ss->fork, 0));
-    const bool in_hash = key_norm_in_hash(D, a);
-    if (in_hash) {
-        hipLaunchKernelGGL(knorm_reduce_kernel, dim3((unsigned)D.BK), dim3(256), 0, ss->s,
-                           (const uint32_t *)(ws + L.kpart), (uint32_t *)(ws + L.knorm),
-                           D.M / 16);
-        SSA_CHECK_LAUNCH();
-    }
-    if ((rc = queries_first<T>(D, a, L, ws, ss->s))) return rc;
-    SSA_CHECK_HIP(hipEventRecord(ss->join, ss->s));
-    if ((rc = keys_typed<T>(D, a, L, ws, st, 2, !in_hash))) return rc;
-    SSA_CHECK_HIP(hipStreamWaitEvent(st, ss->join, 0));
-    return queries_typed<T>(D, a, L, ws, st, true);
-}
-
 int build_impl(const ssa_graph_args *a, void *workspace, int64_t workspace_bytes, void *stream,
                int64_t ws_cap = 0) {
     Dims D;
@@ -4182,15 +4067,16 @@ int build_impl(const ssa_graph_args *a, void *workspace, int64_t workspace_bytes
     }
     hipStream_t st = (hipStream_t)stream;
     char *ws = (char *)workspace;
-    // a stream under graph capture keeps the whole build (no side stream is
-    // created or joined while capturing)
-    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-    SSA_CHECK_HIP(hipStreamIsCapturing(st, &cap));
-    const bool overlap = ws_cap == 0 && cap == hipStreamCaptureStatusNone;
     switch (a->k.dtype) {
-        case SSA_F32: return build_typed<float>(D, a, L, ws, st, overlap);
-        case SSA_BF16: return build_typed<bf16_t>(D, a, L, ws, st, overlap);
-        case SSA_F16: return build_typed<f16_t>(D, a, L, ws, st, overlap);
+        case SSA_F32:
+            if ((rc = keys_typed<float>(D, a, L, ws, st))) return rc;
+            return queries_typed<float>(D, a, L, ws, st);
+        case SSA_BF16:
+            if ((rc = keys_typed<bf16_t>(D, a, L, ws, st))) return rc;
+            return queries_typed<bf16_t>(D, a, L, ws, st);
+        case SSA_F16:
+            if ((rc = keys_typed<f16_t>(D, a, L, ws, st))) return rc;
+            return queries_typed<f16_t>(D, a, L, ws, st);
     }
     return SSA_E_ARG;
 }

@@ -260,6 +260,42 @@ def test_cross_attention_b4_2048_over_512(dtype):
                           heads=[0, 9, 21, 38, 50, 63])
 
 
+def test_repeated_builds_in_one_process_give_one_graph():
+    """Six LSH-mode builds of the same bf16 cross-attention inputs, with
+    full-mode builds in between, give the same lists each time: every kernel
+    of a build runs in order on the caller's stream, so no build reads a
+    result before it is written or another build's workspace.  (The query
+    hash and aux once ran on a second stream joined by an event; on this
+    workload one head in 64 then came out wrong in about half of the builds.)"""
+    cfg = dict(d_model=1024, num_heads=16, num_neighbors=64, window_size=4, num_global_tokens=2,
+               num_hash_rounds=6, max_num_hashes=12, lsh_num_probes=0, causal=False)
+    dtype = torch.bfloat16
+    attn = _module(cfg, 0, dtype)
+    g = torch.Generator().manual_seed(1000)
+    x = torch.randn(4, 2048, 1024, generator=g).to(dtype).to(DEV)
+    kv = torch.randn(4, 512, 1024, generator=g).to(dtype).to(DEV)
+    lb = attn.lsh_builder
+    with torch.no_grad():
+        q = attn._split_q(attn.Wq(x))
+        k = attn._split_kv_compact(attn.Wk(kv))
+        qp, kp = _projections(attn, q, k, lb.compute_effective_p(512, lb.C, lb.max_P))
+        glob = attn.glob_builder(512, DEV)
+        lsh, full = [], []
+        for i in range(6):
+            if i % 2:
+                nb, va = attn.build_graph(q, k, 2048, 512, 4, DEV, False, True,
+                                          _proj=(qp.to(DEV), kp.to(DEV)))
+                full.append((nb.cpu(), va.cpu()))
+            lsh.append(lb(q, k, attn.lsh_k, False, glob, _proj=(qp.to(DEV), kp.to(DEV))).cpu())
+    torch.cuda.synchronize()
+    for i in range(1, 6):
+        bad = (lsh[i].sort(-1).values != lsh[0].sort(-1).values).any(-1).reshape(64, 2048)
+        assert not bool(bad.any()), \
+            f"build {i}: {int(bad.sum())} rows differ, heads {bad.any(1).nonzero().flatten().tolist()}"
+    for nb, va in full[1:]:
+        assert torch.equal(nb, full[0][0]) and torch.equal(va, full[0][1])
+
+
 def test_transformer_6_layers_bf16_b2_n8192():
     from ssa_amd import SSAConfig, SparseTransformer
     cfg = SSAConfig(d_model=1024, num_heads=16, num_kv_heads=4, num_neighbors=128,
