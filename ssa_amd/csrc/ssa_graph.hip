@@ -2808,7 +2808,7 @@ topk_replay_kernel(SelP p, int chunk, int W, uint32_t *gscr, int skip_max) {
 //      slot, then the emit -- wave 0.
 // For many tied rows the per-wave replay (one row per wave, more rows in
 // flight) is faster; a launch takes its rows only when at most `cap` are tied.
-constexpr int RPW_WAVES = 8;
+constexpr int RPW_WAVES = 16;
 constexpr int RPW_THREADS = RPW_WAVES * SSA_WAVE;
 constexpr int RPW_MAX_BLOCKS = 1024;
 constexpr int RPW_TV = 4;            // tied key values noted per chunk
