@@ -106,6 +106,15 @@ OTHER = {
 }
 
 
+def _set_fuse(model, on):
+    """Whether bf16 forwards take the library's projections with the hash in
+    their epilogue or (the default) torch's projections and a separate hash."""
+    from ssa_amd import SparseAttention
+    for m in model.modules():
+        if isinstance(m, SparseAttention):
+            m._fuse_projections = on
+
+
 def _timed(fn, steps, warmup):
     import torch
     for _ in range(warmup):
@@ -154,6 +163,7 @@ def other_workload(name, args):
     for p in model.parameters():
         p.data = p.data.to(dtype)
     model.eval()
+    _set_fuse(model, args.fuse)
     with torch.no_grad():
         if name == "transformer6":
             ids = torch.randint(0, 32000, (B, N), generator=g).to(dev)
@@ -368,6 +378,10 @@ def main():
     ap.add_argument("--workload", default="gqa_n4096",
                     choices=["gqa_n4096"] + sorted(OTHER),
                     help="gqa_n4096 (default): the bf16 GQA N=4096 workload above")
+    ap.add_argument("--fuse", action="store_true",
+                    help="bf16 models: the library's projections with the hash in their "
+                         "epilogue (ssa_project_build_graph) instead of torch's projections and "
+                         "the build's hash pass")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="first run a plain bf16 copy kernel (x*1, 256 MiB in, 256 MiB out) "
                          "5 times, as the reference point for rocprofv3 FETCH_SIZE/WRITE_SIZE")
@@ -393,6 +407,7 @@ def main():
               flush=True)
         del src, dst
     cfg, attn, x = build_module(dev)
+    _set_fuse(attn, args.fuse)
     B, N = x.shape[0], x.shape[1]
     H, d, K = attn.H, attn.d_head, attn.K
     print("# workload built", file=sys.stderr, flush=True)

@@ -123,6 +123,51 @@ int ssa_build_graph(const ssa_graph_args *a, void *workspace, int64_t workspace_
 int ssa_build_graph_noalloc(const ssa_graph_args *a, void *stream);
 
 /* ---------------------------------------------------------------------------
+ * Projections and graph build in one call (bf16 models).
+ *
+ * Replaces the q / k / v projections of SparseAttention.forward
+ * (sparse_attention.py:1484-1486, Wq(x), Wk(src), Wv(src)) followed by
+ * build_graph (:1325-1390).  The projections run on the library's own
+ * matrix-core GEMM, whose epilogue computes from each output tile what the
+ * build would otherwise read q and k again for: the bucket and probe ids of
+ * every row (_hash_proj / _hash / _probe_ids, :559-646, as :775-779 call
+ * them), the keys' norms and the query-side scores the candidate lists do
+ * not carry.  Same outputs as ssa_build_graph on the q and k it writes.
+ *   x       (B, N, d_model) bf16, rows d_model elements apart
+ *   src     (B, M, d_model) bf16 (x itself for self-attention)
+ *   wq      (Hq*d, d_model) bf16 row-major (Wq.weight)
+ *   wkv     (2*Hkv*d, d_model) bf16 row-major: Wk.weight's rows, then Wv.weight's
+ *   q_out   (B, N, Hq*d) bf16, written (x Wq^T)
+ *   kv_out  (B, M, 2*Hkv*d) bf16, written (src [Wk; Wv]^T: k, then v, per row)
+ *   graph   the build's arguments; graph.q and graph.k must be the
+ *           (B, Hq, N, d) and (B, Hkv, M, d) views of q_out and kv_out,
+ *           graph.q_proj / k_proj NULL.
+ * All pointers 16-byte aligned.  ssa_project_graph_supported() returns 1 when
+ * these sizes take this path: bf16, d 32 / 64 / 128, N and M multiples of 16,
+ * d_model a multiple of 64, Hq*d and 2*Hkv*d multiples of 256, R*P at most
+ * 48 (d 128), 64 (d 64, 32) hyperplanes; else 0 (use the projections of the
+ * caller's choice and ssa_build_graph).
+ * --------------------------------------------------------------------------- */
+typedef struct {
+    const void *x, *src, *wq, *wkv;
+    void *q_out, *kv_out;
+    int32_t d_model;
+    ssa_graph_args graph;
+} ssa_project_graph_args;
+
+int ssa_project_graph_supported(const ssa_project_graph_args *a);
+int64_t ssa_project_graph_workspace_bytes(const ssa_project_graph_args *a);
+int ssa_project_build_graph(const ssa_project_graph_args *a, void *workspace,
+                            int64_t workspace_bytes, void *stream);
+
+/* The bf16 projection GEMM alone (no counterpart in the reference; exposed to
+ * test it): y (rows, cols) = x (rows, K) w (cols, K)^T, fp32 accumulation,
+ * rounded once to bf16.  cols a multiple of 256, K of 64; row strides in
+ * elements, multiples of 8; pointers 16-byte aligned. */
+int ssa_project_gemm(const void *x, int64_t ldx, const void *w, int64_t ldw, void *y,
+                     int64_t ldy, int32_t rows, int32_t cols, int32_t K, void *stream);
+
+/* ---------------------------------------------------------------------------
  * Bucket permutation: for each of `rows` rows of `n` bucket ids (uint16, values
  * < 2^P), the permutation torch.sort(ids, dim=-1) returns on the CPU (an
  * unstable introsort; sparse_attention.py:781), plus bucket start / size

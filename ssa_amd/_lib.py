@@ -46,6 +46,11 @@ class GraphArgs(ctypes.Structure):
     ]
 
 
+class ProjectGraphArgs(ctypes.Structure):
+    _fields_ = [("x", c_vp), ("src", c_vp), ("wq", c_vp), ("wkv", c_vp),
+                ("q_out", c_vp), ("kv_out", c_vp), ("d_model", c_i32), ("graph", GraphArgs)]
+
+
 class ApplyArgs(ctypes.Structure):
     _fields_ = [
         ("B", c_i32), ("Hq", c_i32), ("Hkv", c_i32), ("N", c_i32), ("M", c_i32), ("d", c_i32),
@@ -85,6 +90,15 @@ def lib():
         L.ssa_build_graph.argtypes = [ctypes.POINTER(GraphArgs), c_vp, c_i64, c_vp]
         L.ssa_build_graph_noalloc.restype = ctypes.c_int
         L.ssa_build_graph_noalloc.argtypes = [ctypes.POINTER(GraphArgs), c_vp]
+        L.ssa_project_graph_supported.restype = ctypes.c_int
+        L.ssa_project_graph_supported.argtypes = [ctypes.POINTER(ProjectGraphArgs)]
+        L.ssa_project_graph_workspace_bytes.restype = c_i64
+        L.ssa_project_graph_workspace_bytes.argtypes = [ctypes.POINTER(ProjectGraphArgs)]
+        L.ssa_project_build_graph.restype = ctypes.c_int
+        L.ssa_project_build_graph.argtypes = [ctypes.POINTER(ProjectGraphArgs), c_vp, c_i64, c_vp]
+        L.ssa_project_gemm.restype = ctypes.c_int
+        L.ssa_project_gemm.argtypes = [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_i32, c_i32, c_i32,
+                                       c_vp]
         L.ssa_bucket_sort_workspace_bytes.restype = c_i64
         L.ssa_bucket_sort_workspace_bytes.argtypes = [c_i32, c_i32]
         L.ssa_bucket_sort.restype = ctypes.c_int
@@ -152,16 +166,10 @@ MAX_KEYS = 32768
 MAX_GLOBALS = 63
 
 
-def build_graph(q, k, rand_proj, *, P, T, C, top_k, window, causal, is_cross, total_k, glob,
-                mode=GRAPH_FULL, q_proj=None, k_proj=None, count_ties=False, ids32=False,
-                noalloc=False):
-    """Run ssa_build_graph.  q (B,Hq,N,d), k (B,Hkv,M,d) views on one device.
-
-    Returns (out_idx, out_valid or None, ties or None).  With ids32 (FULL mode)
-    out_idx is int32 with -1 in the invalid slots and out_valid is None.  With
-    noalloc the build runs through ssa_build_graph_noalloc: no workspace is
-    allocated (the library's fixed scratch array serves instead; the outputs
-    are still allocated here)."""
+def _graph_args(q, k, rand_proj, *, P, T, C, top_k, window, causal, is_cross, total_k, glob,
+                mode, q_proj, k_proj):
+    """Checked ssa_graph_args for q (B,Hq,N,d), k (B,Hkv,M,d); returns (args,
+    keep-alive tensors)."""
     if q.dim() != 4 or k.dim() != 4:
         raise RuntimeError(f"ssa_amd.build_graph: q {tuple(q.shape)} and k {tuple(k.shape)} must "
                            "be 4-D")
@@ -207,6 +215,39 @@ def build_graph(q, k, rand_proj, *, P, T, C, top_k, window, causal, is_cross, to
     a.window, a.causal, a.is_cross, a.total_k = window, int(causal), int(is_cross), total_k
     a.glob, a.G = (g.data_ptr() if g.numel() else None), g.numel()
     a.q_proj, a.k_proj = _ptr(qp), _ptr(kp)
+    return a, [qk, kk_, rp, g, qp, kp]
+
+
+def _graph_outputs(a, width, mode, ids32, count_ties, device):
+    """Allocate the graph outputs for width slots and point `a` at them."""
+    B, Hq, N = a.B, a.Hq, a.N
+    compact = ids32 and mode == GRAPH_FULL
+    out = torch.empty((B, Hq, N, width), dtype=torch.int32 if compact else torch.int64,
+                      device=device)
+    valid = (torch.empty((B, Hq, N, width), dtype=torch.bool, device=device)
+             if mode == GRAPH_FULL and not compact else None)
+    ties = torch.zeros(1, dtype=torch.int32, device=device) if count_ties else None
+    if compact:
+        a.out_idx32 = out.data_ptr()
+    else:
+        a.out_idx, a.out_valid = out.data_ptr(), _ptr(valid)
+    a.out_ties = _ptr(ties)
+    return out, valid, ties
+
+
+def build_graph(q, k, rand_proj, *, P, T, C, top_k, window, causal, is_cross, total_k, glob,
+                mode=GRAPH_FULL, q_proj=None, k_proj=None, count_ties=False, ids32=False,
+                noalloc=False):
+    """Run ssa_build_graph.  q (B,Hq,N,d), k (B,Hkv,M,d) views on one device.
+
+    Returns (out_idx, out_valid or None, ties or None).  With ids32 (FULL mode)
+    out_idx is int32 with -1 in the invalid slots and out_valid is None.  With
+    noalloc the build runs through ssa_build_graph_noalloc: no workspace is
+    allocated (the library's fixed scratch array serves instead; the outputs
+    are still allocated here)."""
+    a, keep = _graph_args(q, k, rand_proj, P=P, T=T, C=C, top_k=top_k, window=window,
+                          causal=causal, is_cross=is_cross, total_k=total_k, glob=glob, mode=mode,
+                          q_proj=q_proj, k_proj=k_proj)
     L = lib()
     width = L.ssa_graph_out_width(ctypes.byref(a))
     if width < 0:
@@ -214,17 +255,7 @@ def build_graph(q, k, rand_proj, *, P, T, C, top_k, window, causal, is_cross, to
     wsb = 0 if noalloc else L.ssa_graph_workspace_bytes(ctypes.byref(a))
     if wsb < 0:
         _check(-1, "build_graph")
-    compact = ids32 and mode == GRAPH_FULL
-    out = torch.empty((B, Hq, N, width), dtype=torch.int32 if compact else torch.int64,
-                      device=q.device)
-    valid = (torch.empty((B, Hq, N, width), dtype=torch.bool, device=q.device)
-             if mode == GRAPH_FULL and not compact else None)
-    ties = torch.zeros(1, dtype=torch.int32, device=q.device) if count_ties else None
-    if compact:
-        a.out_idx32 = out.data_ptr()
-    else:
-        a.out_idx, a.out_valid = out.data_ptr(), _ptr(valid)
-    a.out_ties = _ptr(ties)
+    out, valid, ties = _graph_outputs(a, width, mode, ids32, count_ties, q.device)
     if noalloc:
         ws = None
         with torch.cuda.device(q.device):
@@ -234,9 +265,91 @@ def build_graph(q, k, rand_proj, *, P, T, C, top_k, window, causal, is_cross, to
         _check(L.ssa_build_graph(ctypes.byref(a), ws.data_ptr(), int(wsb), _stream(q)),
                "build_graph")
     # keep inputs alive until the stream has consumed them
-    _keep = (qk, kk_, rp, g, qp, kp, ws)
-    del _keep
+    keep.append(ws)
+    del keep
     return out, valid, ties
+
+
+def project_shape_ok(dtype, N, M, d_model, Hq, Hkv, d, R, P) -> bool:
+    """The sizes ssa_project_build_graph takes (ssa_project_graph_supported
+    checks them again with the pointers): bf16; head dim 32, 64 or 128; N and
+    M multiples of 16; d_model a multiple of 64; Hq*d and 2*Hkv*d multiples
+    of 256; the round set's hyperplanes in at most 12 // (d // 32) (and 4)
+    tiles of 16."""
+    if dtype != torch.bfloat16 or d not in (32, 64, 128):
+        return False
+    nt = (R * P + 15) // 16
+    return (N % 16 == 0 and M % 16 == 0 and N >= 16 and M >= 16 and d_model % 64 == 0
+            and (Hq * d) % 256 == 0 and (2 * Hkv * d) % 256 == 0 and nt <= min(4, 12 // (d // 32)))
+
+
+def project_build_graph(x, src, wq, wkv, Hq, Hkv, d, rand_proj, *, P, T, C, top_k, window, causal,
+                        is_cross, total_k, glob, mode=GRAPH_FULL, ids32=True, count_ties=False):
+    """Run ssa_project_build_graph: q = x wq^T, [k v] = src wkv^T (bf16) and the
+    graph on them, the hash in the projections' epilogue.
+
+    x (B, N, d_model), src (B, M, d_model) contiguous bf16; wq (Hq*d, d_model),
+    wkv (2*Hkv*d, d_model) contiguous bf16.  Returns (q, k, v, out_idx,
+    out_valid, ties) with q (B, Hq, N, d) and k, v (B, Hkv, M, d) views of the
+    projections' outputs, or None when the library does not take these sizes
+    (the caller then projects and builds separately)."""
+    B, N, dm = x.shape
+    M = src.shape[1]
+    if (x.dim() != 3 or src.dim() != 3 or src.shape[0] != B or src.shape[2] != dm
+            or tuple(wq.shape) != (Hq * d, dm) or tuple(wkv.shape) != (2 * Hkv * d, dm)):
+        raise RuntimeError(f"ssa_amd.project_build_graph: x {tuple(x.shape)}, src "
+                           f"{tuple(src.shape)}, wq {tuple(wq.shape)}, wkv {tuple(wkv.shape)} do "
+                           f"not fit {Hq} query / {Hkv} kv heads of dim {d}")
+    if not project_shape_ok(x.dtype, N, M, dm, Hq, Hkv, d, rand_proj.shape[0], P):
+        return None
+    for t in (src, wq, wkv):
+        if t.dtype != x.dtype:
+            return None
+    require_device(x, src, wq, wkv)
+    x_, src_, wq_, wkv_ = (t.contiguous() for t in (x, src, wq, wkv))
+    q_out = torch.empty((B, N, Hq * d), dtype=x.dtype, device=x.device)
+    kv_out = torch.empty((B, M, 2 * Hkv * d), dtype=x.dtype, device=x.device)
+    q4 = q_out.view(B, N, Hq, d).transpose(1, 2)
+    kv4 = kv_out.view(B, M, 2 * Hkv, d).transpose(1, 2)
+    k4, v4 = kv4[:, :Hkv], kv4[:, Hkv:]
+    ga, keep = _graph_args(q4, k4, rand_proj, P=P, T=T, C=C, top_k=top_k, window=window,
+                           causal=causal, is_cross=is_cross, total_k=total_k, glob=glob, mode=mode,
+                           q_proj=None, k_proj=None)
+    a = ProjectGraphArgs()
+    a.x, a.src, a.wq, a.wkv = x_.data_ptr(), src_.data_ptr(), wq_.data_ptr(), wkv_.data_ptr()
+    a.q_out, a.kv_out, a.d_model = q_out.data_ptr(), kv_out.data_ptr(), dm
+    a.graph = ga
+    L = lib()
+    if not L.ssa_project_graph_supported(ctypes.byref(a)):
+        return None
+    width = L.ssa_graph_out_width(ctypes.byref(a.graph))
+    wsb = L.ssa_project_graph_workspace_bytes(ctypes.byref(a))
+    if width < 0 or wsb < 0:
+        _check(-1, "project_build_graph")
+    out, valid, ties = _graph_outputs(a.graph, width, mode, ids32, count_ties, x.device)
+    ws = torch.empty(max(int(wsb), 1), dtype=torch.uint8, device=x.device)
+    _check(L.ssa_project_build_graph(ctypes.byref(a), ws.data_ptr(), int(wsb), _stream(x)),
+           "project_build_graph")
+    keep += [x_, src_, wq_, wkv_, ws]
+    del keep
+    return q4, k4, v4, out, valid, ties
+
+
+def project_gemm(x, w):
+    """ssa_project_gemm: x (rows, K) w (cols, K)^T in bf16 on the library's
+    projection GEMM (cols a multiple of 256, K of 64)."""
+    require_device(x, w)
+    if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16 or x.dim() != 2 or w.dim() != 2:
+        raise RuntimeError("ssa_amd.project_gemm: 2-D bf16 operands")
+    x_, w_ = x.contiguous(), w.contiguous()
+    rows, K = x_.shape
+    cols = w_.shape[0]
+    if w_.shape[1] != K:
+        raise RuntimeError(f"ssa_amd.project_gemm: x {tuple(x.shape)} w {tuple(w.shape)}")
+    y = torch.empty((rows, cols), dtype=x.dtype, device=x.device)
+    _check(lib().ssa_project_gemm(x_.data_ptr(), K, w_.data_ptr(), K, y.data_ptr(), cols, rows,
+                                  cols, K, _stream(x)), "project_gemm")
+    return y
 
 
 def bucket_sort(ids: torch.Tensor, P: int):

@@ -173,6 +173,44 @@ __device__ __forceinline__ int hoare_swap_count(const uint16_t *TL, const uint16
     return lo;
 }
 
+// Bucket id and probe ids of one row from its P <= 12 hyperplane projections
+// pr[0..P-1] (sparse_attention.py:559-646): bit j = pr[j] > 0 (+0, -0 and NaN
+// give 0), id = sum of bit j << j; probe t flips, in the base id, the plane
+// with the t-th smallest |pr| in the order of a stable ascending argsort
+// (ties by plane index, NaN after every number).  Writes o[0] = id and
+// o[1 + t] for t < Tp.  The projections are read into registers once and each
+// probe picks its plane in one pass over them: O(P) per probe.
+__device__ __forceinline__ bool abs_before(float a, int ja, float b, int jb) {
+    // |a| before |b| in a stable ascending sort (a, b already absolute)
+    if (a != a) return (b != b) && ja < jb;
+    return (b != b) || a < b || (a == b && ja < jb);
+}
+__device__ __forceinline__ void ssa_write_ids(const float *pr, int P, int Tp, uint16_t *o) {
+    float v[12];
+#pragma unroll
+    for (int j = 0; j < 12; ++j) v[j] = j < P ? pr[j] : 0.f;
+    int id = 0;
+#pragma unroll
+    for (int j = 0; j < 12; ++j)
+        if (j < P && v[j] > 0.f) id |= 1 << j;
+    o[0] = (uint16_t)id;
+    int picked = 0;
+    for (int t = 0; t < Tp; ++t) {
+        int pos = -1;
+        float best = 0.f;
+#pragma unroll
+        for (int j = 0; j < 12; ++j) {
+            const float a = fabsf(v[j]);
+            if (j < P && !((picked >> j) & 1) && (pos < 0 || abs_before(a, j, best, pos))) {
+                best = a;
+                pos = j;
+            }
+        }
+        picked |= 1 << pos;
+        o[1 + t] = (uint16_t)(id ^ (1 << pos));
+    }
+}
+
 // order-preserving map fp32 -> uint32 (larger float -> larger key); all
 // finite values and +/-inf map above 0, so 0 can mark "no score".
 __device__ __forceinline__ uint32_t score_key(float f) {

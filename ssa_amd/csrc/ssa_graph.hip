@@ -64,6 +64,8 @@ struct Dims {
     int rpw_blocks;    // blocks of the workgroup tie replay (0: the per-wave replay)
     int rpw_nsim;      // its replaying waves per block
     int ctab;          // the list sort writes the cut's rank table (causal only)
+    int fused;         // the projections hashed the rows (ssa_project_build_graph): no
+                       // hash or aux pass, aux rows for every head, split hyperplanes
 };
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -153,43 +155,6 @@ __global__ void __launch_bounds__(256) hash_kernel(HashP p) {
                     o[1 + t] = (uint16_t)(id ^ (1 << pos));
                 }
             }
-        }
-    }
-}
-
-// bucket id and probe ids of one row from its P <= 12 projections (plane j =
-// bit j); the projections are read once into registers (the loops below are
-// unrolled to 12, so nothing is indexed at run time)
-__device__ __forceinline__ void write_ids(const float *pr, int P, int Tp, uint16_t *o) {
-    float v[12];
-#pragma unroll
-    for (int j = 0; j < 12; ++j) v[j] = j < P ? pr[j] : 0.f;
-    int id = 0;
-#pragma unroll
-    for (int j = 0; j < 12; ++j)
-        if (j < P && v[j] > 0.f) id |= 1 << j;
-    o[0] = (uint16_t)id;
-    if (Tp > 0) {
-        // stable rank of |proj_j| among the P planes; probe t flips the plane
-        // of rank t
-        int rk[12];
-#pragma unroll
-        for (int j = 0; j < 12; ++j) {
-            const float aj = fabsf(v[j]);
-            int rank = 0;
-#pragma unroll
-            for (int q = 0; q < 12; ++q) {
-                const float aq = fabsf(v[q]);
-                rank += (q < P) && ((aq < aj) || (aq == aj && q < j));
-            }
-            rk[j] = rank;
-        }
-        for (int t = 0; t < Tp; ++t) {
-            int pos = 0;
-#pragma unroll
-            for (int j = 0; j < 12; ++j)
-                if (j < P && rk[j] == t) pos = j;
-            o[1 + t] = (uint16_t)(id ^ (1 << pos));
         }
     }
 }
@@ -304,7 +269,7 @@ __global__ void __launch_bounds__(256) hash_mfma_kernel(HashP p) {
                 const int x = x0 + lane;
                 const int rl = x / p.R, r = x - rl * p.R;
                 if (rl < 16 && row0 + rl < p.rows)
-                    write_ids(pw + rl * pst + r * p.P, p.P, p.Tp, p.out + ((row0 + rl) * p.R + r) * p.NS);
+                    ssa_write_ids(pw + rl * pst + r * p.P, p.P, p.Tp, p.out + ((row0 + rl) * p.R + r) * p.NS);
             }
         }
         // this wave's projection rows are rewritten by its next tile
@@ -1328,7 +1293,7 @@ __global__ void __launch_bounds__(256) aux_mfma_kernel(AuxP p) {
             const int x = x0 + lane;
             const int rl = x / p.R, r = x - rl * p.R;
             if (rl < 16 && n0 + rl < p.N)
-                write_ids(pw + rl * pst + r * p.P, p.P, p.Tp,
+                ssa_write_ids(pw + rl * pst + r * p.P, p.P, p.Tp,
                           p.qid + (((int64_t)bh * p.N + n0 + rl) * p.R + r) * p.NS);
         }
     }
@@ -3349,7 +3314,7 @@ struct Layout {
     int64_t kid, qid, perm, bstart, bsize, sorttmp, sid, rnk, smin, inv, cut, srix, qpos, cnt, off,
         cur,
         qlist, tiles, ntiles, tcnt, kbase, S,
-        tie_list, tie_count, aux, knorm, kpart, rpscr, rpw, ctab, total;
+        tie_list, tie_count, aux, psplit, knorm, kpart, rpscr, rpw, ctab, total;
 };
 
 int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
@@ -3385,7 +3350,8 @@ Layout plan(const Dims &D) {
     L.S = take(nbh * D.N * D.nlists * D.Cs * 2);
     L.tie_list = take(D.BH * D.N * 4);
     L.tie_count = take(4);
-    L.aux = take(nbh * D.N * (D.G + 3) * 4);
+    L.aux = take((D.fused ? D.BH : nbh) * D.N * (D.G + 3) * 4);
+    L.psplit = take(D.fused ? ssa_plane_split_bytes(D.R * D.P, D.d) : 0);
     L.knorm = take(D.BK * 4);
     L.ctab = take(D.ctab ? D.BK * D.R * D.NB * (int64_t)((D.M + 31) / 32) * 8 : 0);
     L.kpart = take(D.BK * (D.M / 16) * 4);
@@ -3408,7 +3374,8 @@ Layout plan(const Dims &D);
 // ws_cap > 0: query heads go in chunks small enough that the workspace stays
 // within ws_cap bytes (the build without allocation runs in a fixed scratch
 // array); SSA_E_WORKSPACE when even one head per chunk needs more.
-int make_dims(const ssa_graph_args *a, Dims &D, bool need_q = true, int64_t ws_cap = 0) {
+int make_dims(const ssa_graph_args *a, Dims &D, bool need_q = true, int64_t ws_cap = 0,
+              bool fused = false) {
     SSA_CHECK_ARG(a != nullptr, "build_graph: null args");
     SSA_CHECK_ARG(a->mode == SSA_GRAPH_FULL || a->mode == SSA_GRAPH_LSH, "build_graph: bad mode");
     SSA_CHECK_ARG(a->B >= 1 && a->Hq >= 1 && a->Hkv >= 1 && a->N >= 1 && a->M >= 1,
@@ -3435,6 +3402,7 @@ int make_dims(const ssa_graph_args *a, Dims &D, bool need_q = true, int64_t ws_c
     }
     SSA_CHECK_ARG((int64_t)a->B * a->Hkv * a->R * a->M < ((int64_t)1 << 29),
                   "build_graph: B*Hkv*R*M must stay below 2^29 (bucket permutation bytes)");
+    D.fused = fused ? 1 : 0;
     D.B = a->B; D.Hq = a->Hq; D.Hkv = a->Hkv; D.rep = a->Hq / a->Hkv;
     D.N = a->N; D.M = a->M; D.d = a->d; D.R = a->R; D.maxP = a->max_p; D.P = a->P;
     D.Tp = a->T < a->P ? a->T : a->P;
@@ -3808,7 +3776,8 @@ int keys_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws
                hipStream_t st) {
     int rc = SSA_OK;
     {
-        rc = launch_hash<T>(D, a, L, ws, st, true);
+        // (fused: the key projection wrote the key ids and the 16-row norm maxima)
+        if (!D.fused) rc = launch_hash<T>(D, a, L, ws, st, true);
         if (rc) return rc;
         // max |k|^2 per (batch, kv head): the query code scales derive from it
         KnP kp{};
@@ -3904,7 +3873,7 @@ int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char 
     const bool fuse_qhash = mfma && !a->q_proj && (uintptr_t)a->rand_proj % 16 == 0 &&
                             (size_t)4 * 16 * (np16 + 1) * 4 <= 48 * 1024;
     int rc = SSA_OK;
-    if (!fuse_qhash) {
+    if (!fuse_qhash && !D.fused) {
         rc = launch_hash<T>(D, a, L, ws, st, false);
         if (rc) return rc;
     }
@@ -3922,7 +3891,8 @@ int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char 
         ap.knorm = (const uint32_t *)(ws + L.knorm);
         ap.N = D.N; ap.Hq = D.Hq; ap.Hkv = D.Hkv; ap.rep = D.rep; ap.bh0 = (int)bh0;
         ap.nbh = nbh; ap.G = D.G; ap.NA = D.G + 3; ap.causal = a->causal; ap.d = D.d;
-        ap.out = (float *)(ws + L.aux);
+        // (fused: the query projection wrote every head's aux rows and ids)
+        ap.out = (float *)(ws + L.aux) + (D.fused ? bh0 * (int64_t)D.N * ap.NA : 0);
         if (fuse_qhash) {
             ap.planes = a->rand_proj;
             ap.R = D.R; ap.maxP = D.maxP; ap.P = D.P; ap.Tp = D.Tp; ap.NS = D.NS;
@@ -3930,7 +3900,7 @@ int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char 
             // the tie-row counter of the select kernels (replayed once, after every chunk)
             ap.zero1 = bh0 == 0 ? (int32_t *)(ws + L.tie_count) : nullptr;
         }
-        rc = aux_dispatch<T>(D.d, mfma, ap, st);
+        if (!D.fused) rc = aux_dispatch<T>(D.d, mfma, ap, st);
         if (rc) return rc;
         QbP qp{};
         qp.qid = (const uint16_t *)(ws + L.qid);
@@ -4097,4 +4067,134 @@ int64_t ssa_graph_workspace_bytes_capped(const ssa_graph_args *a, int64_t ws_cap
 int ssa_build_graph_capped(const ssa_graph_args *a, void *workspace, int64_t ws_cap,
                            void *stream) {
     return build_impl(a, workspace, ws_cap, stream, ws_cap);
+}
+
+// ---------------------------------------------------------------------------
+// Projections and graph build in one call (bf16): the projections' epilogue
+// hashes the rows it writes (ssa_proj.hip), so the build reads q and k only
+// for the rescore, the exact keys and the apply.
+namespace {
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+// The fused path's conditions beyond make_dims'; with `why`, the reason it is
+// refused goes to the error text.
+int project_check(const ssa_project_graph_args *pa, Dims &D, bool why) {
+    auto refuse = [&](const char *msg) {
+        if (why) ssa_set_error("project_build_graph: %s", msg);
+        return SSA_E_UNSUP;
+    };
+    if (!pa) return refuse("null args");
+    const ssa_graph_args *a = &pa->graph;
+    if (make_dims(a, D, true, 0, true)) return why ? SSA_E_ARG : SSA_E_UNSUP;
+    if (a->q.dtype != SSA_BF16 || a->k.dtype != SSA_BF16) return refuse("bf16 only");
+    if (a->q_proj || a->k_proj || !a->rand_proj) return refuse("injected projections");
+    if (!pa->x || !pa->src || !pa->wq || !pa->wkv || !pa->q_out || !pa->kv_out)
+        return refuse("null operand");
+    if (!aligned16(pa->x) || !aligned16(pa->src) || !aligned16(pa->wq) || !aligned16(pa->wkv) ||
+        !aligned16(pa->q_out) || !aligned16(pa->kv_out))
+        return refuse("operands must be 16-byte aligned");
+    const int d = D.d, qc = D.Hq * d, kc = 2 * D.Hkv * d;
+    if (a->q.ptr != pa->q_out || a->q.sb != (int64_t)D.N * qc || a->q.sh != d || a->q.sn != qc)
+        return refuse("graph.q is not the (B, Hq, N, d) view of q_out");
+    if (a->k.ptr != pa->kv_out || a->k.sb != (int64_t)D.M * kc || a->k.sh != d || a->k.sn != kc)
+        return refuse("graph.k is not the (B, Hkv, M, d) view of kv_out");
+    if (D.N % 16 || D.M % 16) return refuse("N and M must be multiples of 16");
+    const int np = D.R * D.P;
+    if (!ssa_project_supported((int)(D.B * (int64_t)D.N), qc, pa->d_model, d, np) ||
+        !ssa_project_supported((int)(D.B * (int64_t)D.M), kc, pa->d_model, d, np) ||
+        D.B * (int64_t)std::max(D.N, D.M) >= ((int64_t)1 << 31))
+        return refuse("sizes outside the projection kernel's (d 32/64/128, d_model a multiple "
+                      "of 64, Hq*d and 2*Hkv*d multiples of 256, few enough hyperplanes)");
+    // the aux scores repeat the matrix-core rescore's arithmetic
+    if ((int64_t)kc * 2 >= ((int64_t)1 << 24) ||
+        ((int64_t)D.M * kc + d) * 2 >= ((int64_t)1 << 31))
+        return refuse("key rows beyond the matrix-core rescore's 32-bit offsets");
+    return SSA_OK;
+}
+
+int project_build_impl(const ssa_project_graph_args *pa, void *workspace, int64_t workspace_bytes,
+                       void *stream) {
+    Dims D;
+    int rc = project_check(pa, D, true);
+    if (rc) return rc;
+    const ssa_graph_args *a = &pa->graph;
+    {
+        const bool i32 = a->mode == SSA_GRAPH_FULL && a->out_idx32;
+        SSA_CHECK_ARG(i32 || a->out_idx, "project_build_graph: out_idx is null");
+        SSA_CHECK_ARG(i32 || a->mode != SSA_GRAPH_FULL || a->out_valid,
+                      "project_build_graph: out_valid is null");
+    }
+    const Layout L = plan(D);
+    if (workspace_bytes < L.total || !workspace) {
+        ssa_set_error("project_build_graph: workspace %lld < %lld bytes",
+                      (long long)workspace_bytes, (long long)L.total);
+        return SSA_E_WORKSPACE;
+    }
+    hipStream_t st = (hipStream_t)stream;
+    char *ws = (char *)workspace;
+    const int d = D.d;
+    uint16_t *psplit = (uint16_t *)(ws + L.psplit);
+    if ((rc = ssa_launch_plane_split(a->rand_proj, D.R, D.maxP, D.P, d, psplit, st))) return rc;
+    ProjP kp{};
+    kp.x = pa->src; kp.ldx = pa->d_model;
+    kp.w = pa->wkv; kp.ldw = pa->d_model;
+    kp.y = pa->kv_out; kp.ldy = 2 * D.Hkv * d;
+    kp.rows = (int)(D.B * (int64_t)D.M); kp.cols = 2 * D.Hkv * d; kp.K = pa->d_model;
+    kp.mode = SSA_PROJ_KEYS; kp.L = D.M; kp.d = d; kp.heads = D.Hkv;
+    kp.psplit = psplit; kp.R = D.R; kp.P = D.P; kp.Tp = D.Tp; kp.NS = D.NS;
+    kp.ids = (uint16_t *)(ws + L.kid);
+    kp.kpart = (uint32_t *)(ws + L.kpart);
+    // the bucket sort's segment counter starts at zero
+    kp.zero1 = ssa_sort_counter((uint16_t *)(ws + L.sorttmp), (int)(D.BK * D.R), D.M);
+    if ((rc = ssa_launch_project(kp, st))) return rc;
+    if ((rc = keys_typed<bf16_t>(D, a, L, ws, st))) return rc;
+    ProjP qp{};
+    qp.x = pa->x; qp.ldx = pa->d_model;
+    qp.w = pa->wq; qp.ldw = pa->d_model;
+    qp.y = pa->q_out; qp.ldy = D.Hq * d;
+    qp.rows = (int)(D.B * (int64_t)D.N); qp.cols = D.Hq * d; qp.K = pa->d_model;
+    qp.mode = SSA_PROJ_QUERIES; qp.L = D.N; qp.Lk = D.M; qp.d = d; qp.heads = D.Hq;
+    qp.psplit = psplit; qp.R = D.R; qp.P = D.P; qp.Tp = D.Tp; qp.NS = D.NS;
+    qp.ids = (uint16_t *)(ws + L.qid);
+    // the tie-row counter of the select kernels (replayed once, after every chunk)
+    qp.zero1 = (int32_t *)(ws + L.tie_count);
+    qp.k = a->k.ptr; qp.ksb = a->k.sb; qp.ksh = a->k.sh; qp.ksn = a->k.sn;
+    qp.glob = a->glob; qp.G = D.G; qp.NA = D.G + 3; qp.causal = a->causal ? 1 : 0;
+    qp.Hq = D.Hq; qp.Hkv = D.Hkv; qp.rep = D.rep;
+    qp.knorm = (const uint32_t *)(ws + L.knorm);
+    qp.aux = (float *)(ws + L.aux);
+    if ((rc = ssa_launch_project(qp, st))) return rc;
+    return queries_typed<bf16_t>(D, a, L, ws, st);
+}
+
+}  // namespace
+
+extern "C" int ssa_project_graph_supported(const ssa_project_graph_args *a) {
+    Dims D;
+    return project_check(a, D, false) == SSA_OK ? 1 : 0;
+}
+
+extern "C" int64_t ssa_project_graph_workspace_bytes(const ssa_project_graph_args *a) {
+    Dims D;
+    const int rc = project_check(a, D, true);
+    if (rc) return rc;
+    return plan(D).total;
+}
+
+extern "C" int ssa_project_build_graph(const ssa_project_graph_args *a, void *workspace,
+                                       int64_t workspace_bytes, void *stream) {
+    return project_build_impl(a, workspace, workspace_bytes, stream);
+}
+
+extern "C" int ssa_project_gemm(const void *x, int64_t ldx, const void *w, int64_t ldw, void *y,
+                                int64_t ldy, int32_t rows, int32_t cols, int32_t K, void *stream) {
+    ProjP p{};
+    p.x = x; p.ldx = ldx; p.w = w; p.ldw = ldw; p.y = y; p.ldy = ldy;
+    p.rows = rows; p.cols = cols; p.K = K;
+    p.mode = SSA_PROJ_PLAIN;
+    SSA_CHECK_ARG(x && w && y && aligned16(x) && aligned16(w) && aligned16(y) && ldx % 8 == 0 &&
+                      ldw % 8 == 0 && ldy % 8 == 0,
+                  "project_gemm: operands must be 16-byte aligned rows");
+    return ssa_launch_project(p, (hipStream_t)stream);
 }

@@ -23,3 +23,40 @@ int ssa_launch_bucket_sort(const uint16_t *ids, int rows, int n, int P, int32_t 
 int64_t ssa_graph_workspace_bytes_capped(const ssa_graph_args *a, int64_t ws_cap);
 int ssa_build_graph_capped(const ssa_graph_args *a, void *workspace, int64_t ws_cap,
                            void *stream);
+
+// ---------------------------------------------------------------------------
+// The projections with the hash in their epilogue (ssa_proj.hip).
+#define SSA_PROJ_PLAIN 0     // Y = X W^T only
+#define SSA_PROJ_KEYS 1      // + key bucket ids and the 16-row maxima of |k|^2
+#define SSA_PROJ_QUERIES 2   // + query bucket / probe ids, code scales, aux scores
+
+struct ProjP {
+    const void *x; int64_t ldx;        // (rows, K) bf16, row stride ldx elements
+    const void *w; int64_t ldw;        // (cols, K) bf16
+    void *y; int64_t ldy;              // (rows, cols) bf16, written
+    int rows, cols, K;
+    int mode;
+    int L;                             // positions per batch: rows = B * L
+    int Lk;                            // QUERIES: key positions per batch (rows of k)
+    int d;                             // head dim (epilogue)
+    int heads;                         // KEYS: kv heads hashed (columns [0, heads * d))
+    const uint16_t *psplit;            // hyperplanes as 3 bf16 terms (ssa_launch_plane_split)
+    int R, P, Tp, NS;
+    uint16_t *ids;                     // KEYS: (B*Hkv*R, L); QUERIES: (B*Hq*L, R, NS)
+    uint32_t *kpart;                   // KEYS: max |k|^2 of each 16 rows of a kv head
+    int32_t *zero1;                    // cleared by block 0 (a later kernel's counter)
+    // QUERIES: the keys (the kv projection's output) and the aux rows
+    const void *k; int64_t ksb, ksh, ksn;
+    const int64_t *glob;
+    int G, NA, causal, Hq, Hkv, rep;
+    const uint32_t *knorm;             // max |k|^2 per (batch, kv head)
+    float *aux;                        // (B*Hq*L, NA)
+};
+
+// whether the hash epilogue takes these sizes (rows = B * L, cols = heads * d,
+// K = d_model, np = R * P hyperplanes)
+bool ssa_project_supported(int rows, int cols, int K, int d, int np);
+int64_t ssa_plane_split_bytes(int np, int d);
+int ssa_launch_plane_split(const float *planes, int R, int maxP, int P, int d, uint16_t *out,
+                           hipStream_t st);
+int ssa_launch_project(const ProjP &p, hipStream_t st);

@@ -419,6 +419,34 @@ class SparseAttention(nn.Module):
         kx, vx = y[..., :hk], y[..., hk:]
         return self._split_q(qx), self._split_kv_compact(kx), self._split_kv_compact(vx)
 
+    # bf16 inference may project and build the graph in one library call whose
+    # projections hash the rows they write (ssa_project_build_graph).  Off by
+    # default: on the workloads measured, torch's projection GEMM plus the
+    # build's own hash pass is as fast or faster (set True on an instance to
+    # take the fused path)
+    _fuse_projections = False
+
+    def _project_build_fused(self, x, src, N, M, causal, is_cross):
+        """(q, k, v, int32 graph) from ssa_project_build_graph, or None when the
+        module or the sizes do not take that path (bf16 weights and inputs,
+        head dims 32 / 64 / 128, N and M multiples of 16, ...)."""
+        if not self._fuse_projections or x.dtype != torch.bfloat16 or x.device.type != "cuda":
+            return None
+        lb = self.lsh_builder
+        P = lb.compute_effective_p(M, lb.C, lb.max_P)
+        if not _lib.project_shape_ok(x.dtype, N, M, self.config.d_model, self.H, self.n_kv,
+                                     self.d_head, lb.rand_proj.shape[0], P):
+            return None
+        r = _lib.project_build_graph(
+            x, src, self.Wq.weight, self._fused_weight((self.Wk, self.Wv)), self.H, self.n_kv,
+            self.d_head, lb.rand_proj, P=P, T=lb.T, C=lb.C, top_k=self.lsh_k,
+            window=self.config.window_size, causal=causal, is_cross=is_cross, total_k=self.K,
+            glob=self._glob_ids(M, x.device), mode=_lib.GRAPH_FULL, ids32=True)
+        if r is None:
+            return None
+        q, k, v, out, _, _ = r
+        return q, k, v, out
+
     def apply_graph(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                     neighbors: torch.Tensor, valid: torch.Tensor, *,
                     _row_invalid: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -448,18 +476,29 @@ class SparseAttention(nn.Module):
         src = key_value if is_cross else x
         M = src.shape[1]
         causal = self.config.causal and not is_cross
-        q, k, v = self._project(x, src, is_cross)
         # the padding statistic: each row's invalid slots, counted by the
         # gather attention as it reads the graph
         row_inv = (torch.empty(B * self.H * N, dtype=torch.int32, device=x.device)
                    if return_stats else None)
-        if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
+        grad = torch.is_grad_enabled() and (
+            x.requires_grad or src.requires_grad
+            or any(m.weight.requires_grad for m in (self.Wq, self.Wk, self.Wv)))
+        fused = None if grad else self._project_build_fused(x, src, N, M, causal, is_cross)
+        if fused is not None:
+            # bf16 inference: the projections hash the rows they write and the
+            # build reads q and k only for scoring (one call into the library)
+            q, k, v, neighbors = fused
+            valid = None
+            out = self.apply_graph(q, k, v, neighbors, None, _row_invalid=row_inv)
+        elif grad:
+            q, k, v = self._project(x, src, is_cross)
             neighbors, valid = self.build_graph(q, k, N, M, B, x.device, causal, is_cross)
             out = self.apply_graph(q, k, v, neighbors, valid, _row_invalid=row_inv)
         else:
             # no autograd: the same graph as int32 ids with -1 in the invalid
             # slots, which the gather attention reads as it is (a third of the
             # bytes of int64 ids and a mask, written once and read once)
+            q, k, v = self._project(x, src, is_cross)
             neighbors, valid = self._build_graph_ids32(q, k, N, M, B, causal, is_cross), None
             out = self.apply_graph(q, k, v, neighbors, None, _row_invalid=row_inv)
         out_proj = self.Wo(self._merge(out))

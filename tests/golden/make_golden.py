@@ -14,7 +14,7 @@ fallback, chunked top-k, -inf fallback), merge_neighbors, build_graph,
 sparse_gather_attention, SparseAttention.forward with its stats, and the RNG
 consumption order of seeded construction.
 
-Usage:  python tests/golden/make_golden.py [--only-empty-ranked | --only-models]
+Usage:  python tests/golden/make_golden.py [--only-empty-ranked | --only-models | --only-proj]
 """
 from __future__ import annotations
 
@@ -86,6 +86,20 @@ CASES = [
 ]
 
 SEEDS = (0, 1)
+
+# bf16 shapes the library's projection kernel takes (head dims 64, Hq*d and
+# 2*Hkv*d multiples of 256, N and M multiples of 16): the q/k/v of these come
+# from the fused projection + hash path in ssa_amd
+PROJ_CASES = [
+    ("bf16_proj_causal", dict(d_model=256, num_heads=4, num_kv_heads=2, num_neighbors=32,
+                              window_size=2, num_global_tokens=2, max_num_hashes=4,
+                              num_hash_rounds=4, lsh_num_probes=1, causal=True), (1, 256, None),
+     "bfloat16", {}),
+    ("bf16_proj_cross", dict(d_model=256, num_heads=4, num_kv_heads=2, num_neighbors=24,
+                             window_size=2, num_global_tokens=2, max_num_hashes=6,
+                             num_hash_rounds=3, lsh_num_probes=2), (1, 128, 256), "bfloat16",
+     {}),
+]
 
 
 def run_case(sa, name, cfg_kw, shape, dtype, extra, seed):
@@ -318,6 +332,20 @@ def main():
     if "--only-models" in sys.argv:
         write_models(sa)
         return
+    if "--only-proj" in sys.argv:
+        with open(os.path.join(HERE, "index.json")) as f:
+            index = json.load(f)
+        for name, cfg_kw, shape, dtype, extra in PROJ_CASES:
+            for seed in SEEDS:
+                rec, meta = run_case(sa, name, cfg_kw, shape, dtype, extra, seed)
+                fn = f"{name}_s{seed}.npz"
+                np.savez_compressed(os.path.join(HERE, fn), meta=json.dumps(meta), **rec)
+                if fn not in index:
+                    index.append(fn)
+                print("wrote", fn, "lsh", rec["lsh"].shape, "nb", rec["neighbors"].shape)
+        with open(os.path.join(HERE, "index.json"), "w") as f:
+            json.dump(index, f, indent=1)
+        return
     if "--only-empty-ranked" in sys.argv:
         rec, meta = lsh_empty_bucket_ranked_case(sa)
         np.savez_compressed(os.path.join(HERE, "lsh_empty_bucket_ranked.npz"),
@@ -325,7 +353,7 @@ def main():
         print("wrote lsh_empty_bucket_ranked.npz", rec["out"].tolist())
         return
     index = []
-    for name, cfg_kw, shape, dtype, extra in CASES:
+    for name, cfg_kw, shape, dtype, extra in CASES + PROJ_CASES:
         for seed in SEEDS:
             rec, meta = run_case(sa, name, cfg_kw, shape, dtype, extra, seed)
             fn = f"{name}_s{seed}.npz"
