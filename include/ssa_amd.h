@@ -220,9 +220,11 @@ typedef struct {
     /* neighbors and valid are not read.  Not accepted by the backward.          */
     const int32_t *neighbors32;
     /* optional (no counterpart in the reference): B*Hq*N int32, written with    */
-    /* each query row's count of invalid slots (masked, negative or out of       */
-    /* range), the reference's padding statistic (sparse_attention.py:1500-1508) */
-    /* without a pass of its own over the graph.  Forward only.                  */
+    /* each query row's count of slots the graph marks invalid (valid false, or  */
+    /* a negative id in neighbors32): the reference's padding statistic          */
+    /* (sparse_attention.py:1500-1508) without a pass of its own over the graph. */
+    /* An out-of-range id marked valid is skipped by the attention (as masked)   */
+    /* but not counted.  Forward only.                                           */
     int32_t *row_invalid;
 } ssa_apply_args;
 

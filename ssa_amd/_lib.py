@@ -457,7 +457,8 @@ def _apply_args(q, k, v, neighbors, valid, scale, fp32w, dropout_p, seed, out, i
 def gather_attention_fwd(q, k, v, neighbors, valid, scale, fp32w=False, dropout_p=0.0, seed=0,
                          out=None, row_invalid=None):
     """row_invalid: optional (B*Hq*N,) int32, written with each query row's
-    count of invalid slots."""
+    count of slots the graph marks invalid (valid false, or a negative int32
+    id): the reference's padding statistic."""
     check_apply_shapes(q, k, v, neighbors, valid, out)
     require_device(q, k, v, neighbors, valid, row_invalid)
     if row_invalid is not None:

@@ -123,17 +123,21 @@ apply_fwd_kernel(ApplyP p) {
     const int64_t *nb = p.nb ? p.nb + row * p.K : nullptr;
     const uint8_t *va = p.valid ? p.valid + row * p.K : nullptr;
 
-    // neighbour ids once, as int32 in LDS; masked or out-of-range slots -> -1
+    // neighbour ids once, as int32 in LDS; masked or out-of-range slots -> -1.
+    // The row's padding count is the reference's (sparse_attention.py:1508):
+    // slots the graph marks invalid (mask false, or a negative id in an int32
+    // graph); an out-of-range id marked valid is skipped here but not counted
     int ninv = 0;
     for (int j0 = 0; j0 < p.K; j0 += SSA_WAVE) {
         const int j = j0 + lane;
-        bool o = false;
+        bool o = false, marked = false;
         if (j < p.K) {
             const int64_t x = p.nb32 ? (int64_t)p.nb32[row * p.K + j] : nb[j];
-            o = (p.nb32 ? true : (va ? va[j] != 0 : true)) && x >= 0 && x < p.M;
+            marked = p.nb32 ? x < 0 : (va ? va[j] == 0 : false);
+            o = !marked && x >= 0 && x < p.M;
             ix[j] = o ? (int)x : -1;
         }
-        ninv += __popcll(wave_ballot(j < p.K && !o));
+        ninv += __popcll(wave_ballot(marked));
     }
     if (p.row_inv && lane == 0) p.row_inv[row] = ninv;
     // lanes whose elements lie past the head dim hold zeros and store nothing
@@ -366,17 +370,20 @@ apply_fwd16_kernel(ApplyP p) {
     const int64_t *nb = p.nb ? p.nb + row * p.K : nullptr;
     const uint8_t *va = p.valid ? p.valid + row * p.K : nullptr;
 
-    // neighbour ids as int32 in LDS (ids < 2^24, checked at dispatch)
+    // neighbour ids as int32 in LDS (ids < 2^24, checked at dispatch); the
+    // padding count takes the slots the graph marks invalid, as above
     int ninv = 0;
     for (int j0 = 0; j0 < Kp; j0 += SSA_WAVE) {
         const int j = j0 + lane;
         int x = INT32_MIN;
+        bool marked = false;
         if (j < p.K) {
             const int64_t y = p.nb32 ? (int64_t)p.nb32[row * p.K + j] : nb[j];
-            if ((p.nb32 ? true : (va ? va[j] != 0 : true)) && y >= 0 && y < p.M) x = (int)y;
+            marked = p.nb32 ? y < 0 : (va ? va[j] == 0 : false);
+            if (!marked && y >= 0 && y < p.M) x = (int)y;
         }
         ix[j] = x;
-        ninv += __popcll(wave_ballot(j < p.K && x == INT32_MIN));
+        ninv += __popcll(wave_ballot(marked));
     }
     if (p.row_inv && lane == 0) p.row_inv[row] = ninv;
     uint4 q4 = *reinterpret_cast<const uint4 *>(qrow + (live ? li * 8 : 0));

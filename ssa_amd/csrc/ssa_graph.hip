@@ -63,6 +63,7 @@ struct Dims {
     int Cs;            // score row stride: min(C, M) rounded up to 64 members
     int rpw_blocks;    // blocks of the workgroup tie replay (0: the per-wave replay)
     int rpw_nsim;      // its replaying waves per block
+    int rp_glb_blocks; // blocks of the per-wave replay when its arrays live in the workspace
     int ctab;          // the list sort writes the cut's rank table (causal only)
     int fused;         // the projections hashed the rows (ssa_project_build_graph): no
                        // hash or aux pass, aux rows for every head, split hyperplanes
@@ -3304,10 +3305,11 @@ bool replay_fits_lds(int W, int words) {
 }
 
 // Blocks of the replay whose per-wave arrays live in the workspace: as many as
-// keep that region near 64 MiB (at least one, at most 256).
-int64_t replay_glb_blocks(int W, int words) {
+// keep that region within `budget` bytes (at least one, at most 256; each
+// block loops over its rows).
+int64_t replay_glb_blocks(int W, int words, int64_t budget) {
     const int64_t per_block = (int64_t)RP_WAVES * rp_lds_words(W, words) * 4;
-    return std::max<int64_t>(1, std::min<int64_t>(256, ((int64_t)64 << 20) / per_block));
+    return std::max<int64_t>(1, std::min<int64_t>(256, budget / per_block));
 }
 
 struct Layout {
@@ -3361,7 +3363,7 @@ Layout plan(const Dims &D) {
         const int words = sel_bitmap_words(D.M);
         L.rpscr = take(replay_fits_lds(W, words)
                            ? 0
-                           : replay_glb_blocks(W, words) * RP_WAVES * rp_lds_words(W, words) * 4);
+                           : (int64_t)D.rp_glb_blocks * RP_WAVES * rp_lds_words(W, words) * 4);
         L.rpw = take((int64_t)D.rpw_blocks *
                      rpw_scratch_words(D.Call, D.M, D.kk, (int)ceil_div(D.Call, D.chunk)) * 4);
     }
@@ -3471,6 +3473,11 @@ int make_dims(const ssa_graph_args *a, Dims &D, bool need_q = true, int64_t ws_c
         D.rpw_blocks = (int)std::min<int64_t>(RPW_MAX_BLOCKS, budget / per);
         if (D.rpw_nsim < 1 || D.M >= (1 << 29) || D.Call >= ((int64_t)1 << 31)) D.rpw_blocks = 0;
     }
+    // the per-wave replay's arrays, when they do not fit LDS: 64 MiB of
+    // workspace (a sixteenth of ws_cap without allocation)
+    D.rp_glb_blocks = (int)replay_glb_blocks(
+        D.kk + D.chunk, sel_bitmap_words(D.M),
+        ws_cap > 0 ? std::min<int64_t>(ws_cap / 16, (int64_t)64 << 20) : ((int64_t)64 << 20));
     {
         // the cut's rank table: 8 bytes per (kv head, round, bucket, 32 key
         // ids), when causal and within 256 MiB (a sixteenth of ws_cap)
@@ -3736,7 +3743,7 @@ int launch_replay(const SelP &sp, const Dims &D, uint32_t *rpscr, uint32_t *rpws
         SSA_CHECK_LAUNCH();
     }
     if (!replay_fits_lds(W, sp.words)) {
-        const int64_t blocks = replay_glb_blocks(W, sp.words);
+        const int64_t blocks = D.rp_glb_blocks;
         hipLaunchKernelGGL((topk_replay_kernel<T, LSH, true>), dim3((unsigned)blocks),
                            dim3(RP_WAVES * SSA_WAVE), 0, st, sp, chunk, W, rpscr, cap);
         SSA_CHECK_LAUNCH();

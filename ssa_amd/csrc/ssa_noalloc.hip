@@ -14,8 +14,18 @@
 // address comes from hipGetSymbolAddress, once per device with that device
 // current, and only that pointer is used.  Every call on one GPU shares the
 // array and it keeps the last call's contents: the build clears what it needs
-// cleared itself (its counters, with kernels), and calls that overlap on one
-// GPU (different streams, different host threads) race on it.
+// cleared itself (its counters, with kernels).
+//
+// Calls on one GPU are ordered: each call's stream first waits for an event
+// recorded at the end of the previous call's work on that GPU (whatever its
+// stream or host thread), and the enqueue itself holds a lock, so calls from
+// several streams or threads run one after another on the device instead of
+// racing on the array.  The event is created once per device at the first
+// call (no device memory).  A call made while its stream is under graph
+// capture neither waits nor records (an event recorded outside a capture
+// cannot be waited on inside it): replays of such a graph are ordered only
+// by the stream they are launched on, so a caller must not replay one on a
+// stream that runs beside another call of this entry point on the same GPU.
 #include <mutex>
 
 #include "ssa_graph_internal.h"
@@ -27,10 +37,13 @@ namespace {
 constexpr int kMaxDevices = 64;
 std::mutex g_mu;
 void *g_scratch[kMaxDevices];   // device address of `scratch` per device (null = not yet)
+hipEvent_t g_done[kMaxDevices]; // end of the last call's work per device
+bool g_done_set[kMaxDevices];   // g_done has been recorded
+std::mutex g_order_mu;          // held while a call is enqueued
 
 // Device address of this device's scratch array.  The stream, when given, must
 // belong to the current device: the address is looked up with it current.
-int scratch_address(void *stream, void **out) {
+int scratch_address(void *stream, void **out, int *dev_out) {
     int dev = -1;
     SSA_CHECK_HIP(hipGetDevice(&dev));
     SSA_CHECK_ARG(dev >= 0 && dev < kMaxDevices, "build_graph_noalloc: device %d", dev);
@@ -46,9 +59,11 @@ int scratch_address(void *stream, void **out) {
         void *ptr = nullptr;
         SSA_CHECK_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
         SSA_CHECK_ARG(ptr != nullptr, "build_graph_noalloc: no address for the scratch array");
+        SSA_CHECK_HIP(hipEventCreateWithFlags(&g_done[dev], hipEventDisableTiming));
         g_scratch[dev] = ptr;
     }
     *out = g_scratch[dev];
+    *dev_out = dev;
     return SSA_OK;
 }
 
@@ -59,7 +74,20 @@ extern "C" int ssa_build_graph_noalloc(const ssa_graph_args *a, void *stream) {
     const int64_t need = ssa_graph_workspace_bytes_capped(a, (int64_t)SSA_NOALLOC_SCRATCH_BYTES);
     if (need < 0) return (int)need;
     void *ws = nullptr;
-    const int rc = scratch_address(stream, &ws);
+    int dev = -1;
+    int rc = scratch_address(stream, &ws, &dev);
     if (rc) return rc;
-    return ssa_build_graph_capped(a, ws, (int64_t)SSA_NOALLOC_SCRATCH_BYTES, stream);
+    const hipStream_t st = (hipStream_t)stream;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    SSA_CHECK_HIP(hipStreamIsCapturing(st, &cs));
+    const bool ordered = cs == hipStreamCaptureStatusNone;
+    std::lock_guard<std::mutex> lk(g_order_mu);
+    if (ordered && g_done_set[dev]) SSA_CHECK_HIP(hipStreamWaitEvent(st, g_done[dev], 0));
+    rc = ssa_build_graph_capped(a, ws, (int64_t)SSA_NOALLOC_SCRATCH_BYTES, stream);
+    if (ordered) {
+        // recorded after a failed call too: whatever it enqueued is covered
+        SSA_CHECK_HIP(hipEventRecord(g_done[dev], st));
+        g_done_set[dev] = true;
+    }
+    return rc;
 }

@@ -138,6 +138,13 @@ def _capture_graphs(model, kind):
     return seen
 
 
+# Tokens of each bf16 fixture (B * N = 192) affected by a graph difference,
+# bounded near what the device's GEMMs give (0, 0, 8 and 0 measured, about
+# twice that allowed); fp32 must have none.
+AFFECTED_MAX = {"cached_bf16_seed0": 4, "cached_bf16_seed1": 4,
+                "transformer_bf16_seed0": 16, "transformer_bf16_seed1": 4}
+
+
 @pytest.mark.parametrize("path", MODELS, ids=os.path.basename)
 def test_model_forward_matches_reference(path):
     """The whole model from the same seed and inputs.  Its layers' q and k come
@@ -194,8 +201,10 @@ def test_model_forward_matches_reference(path):
             else:
                 assert gv == val, (key, gv, val)
     keep = ~affected
-    assert keep.sum() >= 0.5 * keep.size, "most tokens affected by graph differences"
+    name = os.path.basename(path)[:-4]
+    print(f"  {name}: token graphs differing {n_diff}, tokens affected "
+          f"{int(affected.sum())} of {B * N}", flush=True)
+    assert int(affected.sum()) <= AFFECTED_MAX.get(name, 0), "more tokens affected than measured"
     err = _rows_close(out[torch.from_numpy(keep).to(DEV)],
                       z["out"][keep], tol, "model output (unaffected tokens)")
-    print(f"  {os.path.basename(path)}: token graphs differing {n_diff}, tokens affected "
-          f"{int(affected.sum())} of {B * N}, output worst row error {err:.2e}", flush=True)
+    print(f"  output worst row error {err:.2e}", flush=True)

@@ -249,11 +249,13 @@ def test_graph_exact_tier_many_tied_rows(case):
 
 
 @pytest.mark.parametrize("case", GRAPH_CASES, ids=lambda c: c[0])
-def test_graph_bf16_inputs_exact_tier(case):
-    """bf16 q/k holding small integers are exact: same graph as fp32 (the
-    matrix-core rescore, aux and exact-key paths, every head-dim instance)."""
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+def test_graph_16bit_inputs_exact_tier(case, dtype):
+    """bf16 and fp16 q/k holding small integers are exact: same graph as fp32
+    (the matrix-core rescore of either 16-bit type, aux and exact-key paths,
+    every head-dim instance)."""
     attn, got, got_v, ref, (B, H, N, M, K, w, cross, causal, glob) = _graph_case(
-        case, 5, dtype=torch.bfloat16)
+        case, 5, dtype=dtype)
     win = (np.zeros((N, 0), np.int64) if cross else attn.win_builder(N, M, "cpu").numpy())
     rnb, rva = oracle.merge(win, glob.numpy(), ref["idx"], has_self=not cross, total_k=K)
     np.testing.assert_array_equal(got.cpu().numpy().reshape(B * H, N, -1), rnb)
@@ -364,8 +366,11 @@ def test_apply_expanded_kv_equals_grouped_kv():
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("ids32", [False, True])
 def test_apply_counts_invalid_slots_per_row(dtype, ids32):
-    """row_invalid: each row's masked, negative or out-of-range slots (the
-    padding statistic), with the same output as without it."""
+    """row_invalid: each row's slots the graph marks invalid (valid false, or
+    a negative int32 id): the reference's padding statistic, ~valid summed
+    per row (sparse_attention.py:1508); an out-of-range or negative int64 id
+    marked valid is skipped by the attention but not counted.  Same output
+    as without it."""
     from ssa_amd import _lib
     case = (2, 4, 2, 50, 60, 64, 37)
     q, k, v, nb, va = _apply_inputs(case, dtype, 5)
@@ -375,10 +380,10 @@ def test_apply_counts_invalid_slots_per_row(dtype, ids32):
     if ids32:
         ids = torch.where(va, nb, torch.full_like(nb, -1)).to(torch.int32).to(DEV)
         nbd, vad = ids, None
-        bad = (ids < 0) | (ids >= 60)
+        bad = ids < 0
     else:
         nbd, vad = nb.to(DEV), va.to(DEV)
-        bad = ~vad | (nbd < 0) | (nbd >= 60)
+        bad = ~vad
     rows = torch.full((2 * 4 * 50,), -7, dtype=torch.int32, device=DEV)
     with torch.no_grad():
         o1 = _lib.gather_attention_fwd(a[0], a[1], a[2], nbd, vad, 0.125, row_invalid=rows)
@@ -421,6 +426,23 @@ def test_apply_fp32_head_dim_12_matches_oracle():
     assert row_rel_err(out.cpu().numpy().reshape(B * H, N, d), ref) <= REL[torch.float32]
 
 
+# per-row bar of the gradients: each row of dq (a query) or of dk / dv (a key)
+# against the row's own largest reference magnitude, like the forward; a row
+# no query reaches must come out exactly zero
+GRAD_REL = {torch.float32: 1e-5, torch.bfloat16: 2e-2, torch.float16: 2e-2}
+
+
+def _check_grad_rows(name, got, exp, dtype):
+    g = got.detach().double().cpu().numpy()
+    r = exp.detach().double().cpu().numpy()
+    g2, r2 = g.reshape(-1, g.shape[-1]), r.reshape(-1, r.shape[-1])
+    zero = np.abs(r2).max(-1) == 0
+    assert not np.abs(g2[zero]).any(), f"{name}: gradient in a row no query reaches"
+    e = row_rel_err(g2[~zero], r2[~zero]) if (~zero).any() else 0.0
+    print(f"  {name}: {int((~zero).sum())} rows, worst row error {e:.2e}", flush=True)
+    assert e <= GRAD_REL[dtype], (name, e)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("case", [(1, 4, 2, 24, 30, 32, 16), (1, 4, 2, 24, 30, 96, 16)],
                          ids=["d32", "d96"])
@@ -445,10 +467,9 @@ def test_apply_backward_matches_autograd_reference(dtype, case):
     p = torch.softmax(s, -1)
     o = (p.unsqueeze(-1) * vg).sum(3)
     o.backward(dout.double())
-    tol = 1e-4 if dtype == torch.float32 else 5e-2
-    for got, exp in [(qd.grad, qr.grad), (kd.grad, kr.grad), (vd.grad, vr.grad)]:
-        e = (got.float().cpu().double() - exp).abs().max() / exp.abs().max()
-        assert e < tol, e
+    for name, got, exp in [("dq", qd.grad, qr.grad), ("dk", kd.grad, kr.grad),
+                           ("dv", vd.grad, vr.grad)]:
+        _check_grad_rows(name, got, exp, dtype)
 
 
 # ------------------------------------------------------------------ dropout
@@ -517,11 +538,9 @@ def test_dropout_keep_rate_scaling_and_backward(dtype, fp32w):
     pr = torch.softmax(sc, -1) * mask * float(s32)
     o = (pr.unsqueeze(-1) * vgat).sum(3)
     o.backward(G.double())
-    tol = 1e-4 if dtype == torch.float32 else 5e-2
     for name, got, exp in [("dq", qg.grad, qr.grad), ("dk", kg_.grad, kr.grad),
                            ("dv", vg_.grad, vr.grad)]:
-        e = ((got.double() - exp).abs().max() / exp.abs().max()).item()
-        assert e < tol, (name, e)
+        _check_grad_rows(name, got, exp, dtype)
 
 
 @pytest.mark.parametrize("dtype,fp32w", [(torch.bfloat16, False), (torch.bfloat16, True),
@@ -555,11 +574,9 @@ def test_apply_backward_at_bench_head_shape(dtype, fp32w):
     p = torch.softmax(s.masked_fill(~vad, float("-inf")), -1)
     o = (p.unsqueeze(-1) * vg).sum(3)
     o.backward(dout.to(DEV).double())
-    tol = 1e-4 if dtype == torch.float32 else 5e-2
     for name, got, exp in [("dq", qd.grad, qr.grad), ("dk", kd.grad, kr.grad),
                            ("dv", vd.grad, vr.grad)]:
-        e = ((got.double() - exp).abs().max() / exp.abs().max()).item()
-        assert e < tol, (name, e)
+        _check_grad_rows(name, got, exp, dtype)
 
 
 # ------------------------------------------------------------------ merge
