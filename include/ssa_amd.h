@@ -254,6 +254,19 @@ int ssa_sparse_gather_attention_bwd(const ssa_apply_bwd_args *a, void *stream);
 int ssa_measure_l2_read(const void *buf, int64_t bytes, int32_t blocks, int32_t iters,
                         uint32_t *sink, void *stream);
 
+/* ---------------------------------------------------------------------------
+ * Bounds-checked build (no counterpart in the reference): libssa_amd_checked.so
+ * (`make -C ssa_amd/csrc checked`) is this library with the graph build's
+ * data-dependent indices (key ids, sorted-list and bucket positions, tie rows,
+ * output slots on the select, tie replay and merge paths) compared with the
+ * length of what they index; an index outside is recorded and replaced by 0,
+ * so no access leaves its buffer.  ssa_checked_oob synchronizes the device,
+ * copies the record into record[4] (bit i of record[0]: site i saw an index
+ * outside; record[1..3]: the last offender's site, index and length), clears
+ * it and returns 1; in the product build it returns 0 and writes nothing.
+ * --------------------------------------------------------------------------- */
+int ssa_checked_oob(uint32_t *record);
+
 /* Library identification and error text. */
 const char *ssa_version(void);
 const char *ssa_last_error(void);

@@ -9,6 +9,7 @@ fails; there is no CPU or torch fallback for the hot path.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 
@@ -69,52 +70,94 @@ class ApplyBwdArgs(ctypes.Structure):
 
 
 _lib = None
+_override = None
+CHECKED_LIB_PATH = os.path.join(_HERE, "libssa_amd_checked.so")
 
 
 def lib():
-    """Load libssa_amd.so once; raise if it is not built."""
+    """Load libssa_amd.so once; raise if it is not built.  Inside
+    checked_library() the bounds-checked build serves instead."""
     global _lib
+    if _override is not None:
+        return _override
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             raise RuntimeError(
                 f"ssa_amd: {LIB_PATH} is not built; run `make -C ssa_amd/csrc` "
                 "(or __graft_entry__.build()).  There is no fallback path.")
-        L = ctypes.CDLL(LIB_PATH)
-        L.ssa_version.restype = ctypes.c_char_p
-        L.ssa_last_error.restype = ctypes.c_char_p
-        L.ssa_graph_out_width.restype = c_i64
-        L.ssa_graph_out_width.argtypes = [ctypes.POINTER(GraphArgs)]
-        L.ssa_graph_workspace_bytes.restype = c_i64
-        L.ssa_graph_workspace_bytes.argtypes = [ctypes.POINTER(GraphArgs)]
-        L.ssa_build_graph.restype = ctypes.c_int
-        L.ssa_build_graph.argtypes = [ctypes.POINTER(GraphArgs), c_vp, c_i64, c_vp]
-        L.ssa_build_graph_noalloc.restype = ctypes.c_int
-        L.ssa_build_graph_noalloc.argtypes = [ctypes.POINTER(GraphArgs), c_vp]
-        L.ssa_project_graph_supported.restype = ctypes.c_int
-        L.ssa_project_graph_supported.argtypes = [ctypes.POINTER(ProjectGraphArgs)]
-        L.ssa_project_graph_workspace_bytes.restype = c_i64
-        L.ssa_project_graph_workspace_bytes.argtypes = [ctypes.POINTER(ProjectGraphArgs)]
-        L.ssa_project_build_graph.restype = ctypes.c_int
-        L.ssa_project_build_graph.argtypes = [ctypes.POINTER(ProjectGraphArgs), c_vp, c_i64, c_vp]
-        L.ssa_project_gemm.restype = ctypes.c_int
-        L.ssa_project_gemm.argtypes = [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_i32, c_i32, c_i32,
-                                       c_vp]
-        L.ssa_bucket_sort_workspace_bytes.restype = c_i64
-        L.ssa_bucket_sort_workspace_bytes.argtypes = [c_i32, c_i32]
-        L.ssa_bucket_sort.restype = ctypes.c_int
-        L.ssa_bucket_sort.argtypes = [c_vp, c_i32, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp, c_i64,
-                                      c_vp]
-        L.ssa_merge_neighbors.restype = ctypes.c_int
-        L.ssa_merge_neighbors.argtypes = [c_vp, c_i32, c_vp, c_i32, c_vp, c_i32, c_i32, c_i32,
-                                          c_i32, c_i32, c_vp, c_vp, c_vp, c_vp]
-        L.ssa_sparse_gather_attention.restype = ctypes.c_int
-        L.ssa_sparse_gather_attention.argtypes = [ctypes.POINTER(ApplyArgs), c_vp]
-        L.ssa_measure_l2_read.restype = ctypes.c_int
-        L.ssa_measure_l2_read.argtypes = [c_vp, c_i64, c_i32, c_i32, c_vp, c_vp]
-        L.ssa_sparse_gather_attention_bwd.restype = ctypes.c_int
-        L.ssa_sparse_gather_attention_bwd.argtypes = [ctypes.POINTER(ApplyBwdArgs), c_vp]
-        _lib = L
+        _lib = _configure(ctypes.CDLL(LIB_PATH))
     return _lib
+
+
+_checked = None
+
+
+@contextlib.contextmanager
+def checked_library():
+    """Route every call made inside the block through libssa_amd_checked.so:
+    the same kernels with the graph build's data-dependent indices
+    bounds-checked (an index outside its buffer is recorded and replaced by
+    0).  Yields a function that returns and clears the record: None when
+    nothing was out of bounds, else (site bits, last site, index, length)."""
+    global _override, _checked
+    if _checked is None:
+        if not os.path.exists(CHECKED_LIB_PATH):
+            raise RuntimeError(f"ssa_amd: {CHECKED_LIB_PATH} is not built; run "
+                               "`make -C ssa_amd/csrc checked`")
+        _checked = _configure(ctypes.CDLL(CHECKED_LIB_PATH))
+    L = _checked
+
+    def record():
+        rec = (ctypes.c_uint32 * 4)()
+        if L.ssa_checked_oob(rec) != 1:
+            raise RuntimeError("ssa_amd: the checked library does not keep a record")
+        return None if rec[0] == 0 else tuple(rec)
+    prev = _override
+    _override = L
+    try:
+        yield record
+    finally:
+        _override = prev
+
+
+def _configure(L):
+    """Declare the C ABI's signatures on a loaded library."""
+    L.ssa_version.restype = ctypes.c_char_p
+    L.ssa_last_error.restype = ctypes.c_char_p
+    L.ssa_graph_out_width.restype = c_i64
+    L.ssa_graph_out_width.argtypes = [ctypes.POINTER(GraphArgs)]
+    L.ssa_graph_workspace_bytes.restype = c_i64
+    L.ssa_graph_workspace_bytes.argtypes = [ctypes.POINTER(GraphArgs)]
+    L.ssa_build_graph.restype = ctypes.c_int
+    L.ssa_build_graph.argtypes = [ctypes.POINTER(GraphArgs), c_vp, c_i64, c_vp]
+    L.ssa_build_graph_noalloc.restype = ctypes.c_int
+    L.ssa_build_graph_noalloc.argtypes = [ctypes.POINTER(GraphArgs), c_vp]
+    L.ssa_project_graph_supported.restype = ctypes.c_int
+    L.ssa_project_graph_supported.argtypes = [ctypes.POINTER(ProjectGraphArgs)]
+    L.ssa_project_graph_workspace_bytes.restype = c_i64
+    L.ssa_project_graph_workspace_bytes.argtypes = [ctypes.POINTER(ProjectGraphArgs)]
+    L.ssa_project_build_graph.restype = ctypes.c_int
+    L.ssa_project_build_graph.argtypes = [ctypes.POINTER(ProjectGraphArgs), c_vp, c_i64, c_vp]
+    L.ssa_project_gemm.restype = ctypes.c_int
+    L.ssa_project_gemm.argtypes = [c_vp, c_i64, c_vp, c_i64, c_vp, c_i64, c_i32, c_i32, c_i32,
+                                   c_vp]
+    L.ssa_bucket_sort_workspace_bytes.restype = c_i64
+    L.ssa_bucket_sort_workspace_bytes.argtypes = [c_i32, c_i32]
+    L.ssa_bucket_sort.restype = ctypes.c_int
+    L.ssa_bucket_sort.argtypes = [c_vp, c_i32, c_i32, c_i32, c_vp, c_vp, c_vp, c_vp, c_i64,
+                                  c_vp]
+    L.ssa_merge_neighbors.restype = ctypes.c_int
+    L.ssa_merge_neighbors.argtypes = [c_vp, c_i32, c_vp, c_i32, c_vp, c_i32, c_i32, c_i32,
+                                      c_i32, c_i32, c_vp, c_vp, c_vp, c_vp]
+    L.ssa_sparse_gather_attention.restype = ctypes.c_int
+    L.ssa_sparse_gather_attention.argtypes = [ctypes.POINTER(ApplyArgs), c_vp]
+    L.ssa_measure_l2_read.restype = ctypes.c_int
+    L.ssa_measure_l2_read.argtypes = [c_vp, c_i64, c_i32, c_i32, c_vp, c_vp]
+    L.ssa_sparse_gather_attention_bwd.restype = ctypes.c_int
+    L.ssa_sparse_gather_attention_bwd.argtypes = [ctypes.POINTER(ApplyBwdArgs), c_vp]
+    L.ssa_checked_oob.restype = ctypes.c_int
+    L.ssa_checked_oob.argtypes = [ctypes.POINTER(ctypes.c_uint32)]
+    return L
 
 
 def version() -> str:

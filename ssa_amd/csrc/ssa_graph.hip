@@ -49,6 +49,33 @@
 #include "ssa_common.h"
 #include "ssa_graph_internal.h"
 
+// ------------------------------------------------------------------ checked build
+// Built with SSA_CHECKED (`make checked`: libssa_amd_checked.so), the
+// data-dependent indices of the select, tie replay and merge paths are
+// compared with the length of what they index: key ids with the key count,
+// list and bucket positions with the sorted arrays, tie rows with the row
+// count, output slots with the output.  An index outside is recorded in
+// ssa_oob (word 0: one bit per site; words 1-3: the last offender's site,
+// index and length) and replaced by 0, so no access leaves its buffer; the
+// host reads and clears the record with ssa_checked_oob.  The product build
+// compiles SSA_IDX to the index itself.
+#ifdef SSA_CHECKED
+static __device__ uint32_t ssa_oob[4];
+__device__ __attribute__((noinline)) int64_t ssa_idx_bad(int64_t i, int64_t n, int site) {
+    atomicOr(&ssa_oob[0], 1u << site);
+    ssa_oob[1] = (uint32_t)site;
+    ssa_oob[2] = (uint32_t)i;
+    ssa_oob[3] = (uint32_t)n;
+    return 0;
+}
+__device__ __forceinline__ int64_t ssa_idx(int64_t i, int64_t n, int site) {
+    return (i >= 0 && i < n) ? i : ssa_idx_bad(i, n, site);
+}
+#define SSA_IDX(i, n, site) ssa_idx((int64_t)(i), (int64_t)(n), (site))
+#else
+#define SSA_IDX(i, n, site) (i)
+#endif
+
 namespace {
 
 constexpr int TQ = 64;         // queries per rescore tile
@@ -1387,6 +1414,7 @@ struct SelP {
     int N, M, d, R, NS, NB, C, Cs, CPL, nlists, Hq, Hkv, rep, G, kk, window, causal, cross, mode,
         total_k, Kw, Kout, bh0, words;
     int64_t Call, rows;
+    int64_t rows_all;      // query rows of every head (B * Hq * N): tie rows and output rows
     int64_t *out_idx;
     uint8_t *out_valid;
     int32_t *out_idx32;    // FULL mode: the graph as int32 ids (-1 = invalid) instead
@@ -1440,7 +1468,7 @@ __device__ uint32_t exact_keys(const SelP &p, const T *qr, const T *kb, int v, b
                 const int src = !ok ? 0 : (j < clo ? nth_set_bit(wlo, j)
                                                    : 32 + nth_set_bit(whi, j - clo));
                 const int vid = __shfl(v, src, SSA_WAVE);
-                const T *kr = kb + (int64_t)(ok ? vid : 0) * p.ksn;
+                const T *kr = kb + (int64_t)SSA_IDX(ok ? vid : 0, p.M, 0) * p.ksn;
                 f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
                 for (int s = 0; s < KS; ++s) {
                     const int e0 = 32 * s + 8 * lg;
@@ -1465,7 +1493,7 @@ __device__ uint32_t exact_keys(const SelP &p, const T *qr, const T *kb, int v, b
     }
     float acc = 0.f;
     if (want) {
-        const T *kr = kb + (int64_t)v * p.ksn;
+        const T *kr = kb + (int64_t)SSA_IDX(v, p.M, 0) * p.ksn;
         for (int c = 0; c < p.d; ++c) acc = fmaf(to_f32(qr[c]), to_f32(kr[c]), acc);
     }
     return want ? score_key(acc) : 0u;
@@ -1508,7 +1536,7 @@ __device__ uint32_t exact_keys_wide(const SelP &p, const T *qr, const T *kb, int
             const bool ok = j < total;
             const int src = !ok ? 0 : (j < clo ? nth_set_bit(wlo, j) : 32 + nth_set_bit(whi, j - clo));
             const int vid = __shfl(v, src, SSA_WAVE);
-            const T *kr = kb + (int64_t)(ok ? vid : 0) * p.ksn;
+            const T *kr = kb + (int64_t)SSA_IDX(ok ? vid : 0, p.M, 0) * p.ksn;
 #pragma unroll
             for (int s = 0; s < KSM; ++s) {
                 const int e0 = 32 * s + 8 * lg;
@@ -1681,11 +1709,12 @@ __device__ void full_merge_emit(uint32_t *bm, const SelP &p, int n, int64_t row,
     // slot i gets key id v (valid) or the padding; as int64 + valid byte, or
     // as one int32 with -1 for padding
     auto put = [&](int i, int v, bool valid) {
+        const int64_t o = SSA_IDX(row * p.Kout + SSA_IDX(i, p.Kout, 4), p.rows_all * p.Kout, 4);
         if (p.out_idx32) {
-            p.out_idx32[row * p.Kout + i] = valid ? v : -1;
+            p.out_idx32[o] = valid ? v : -1;
         } else {
-            p.out_idx[row * p.Kout + i] = valid ? (int64_t)v : 0;
-            p.out_valid[row * p.Kout + i] = valid ? 1 : 0;
+            p.out_idx[o] = valid ? (int64_t)v : 0;
+            p.out_valid[o] = valid ? 1 : 0;
         }
     };
     const int wpl = (p.words + SSA_WAVE - 1) / SSA_WAVE;
@@ -1957,7 +1986,7 @@ select_kernel(SelP p) {
                     } else {
                         hit = L2 < L && c2.y < p.C && c2.w == v;
                         if (!hit) {
-                            const int pos = p.inv[c2.z + v];
+                            const int pos = p.inv[SSA_IDX(c2.z + v, p.perm_bytes / 4, 1)];
                             hit = pos >= c2.x && pos < c2.x + min(c2.y, p.C);
                         }
                     }
@@ -2174,8 +2203,9 @@ select_kernel(SelP p) {
             int v = 0;
             uint32_t c = 0u;
             if (in_mask(Min)) {
-                v = p.sid[__builtin_amdgcn_readlane(dw.x, j) + lane];
-                c = shead[(uint32_t)__builtin_amdgcn_readlane(dw.z, j) + lane];
+                v = p.sid[SSA_IDX(__builtin_amdgcn_readlane(dw.x, j) + lane, p.perm_bytes / 4, 2)];
+                c = shead[SSA_IDX((int64_t)(uint32_t)__builtin_amdgcn_readlane(dw.z, j) + lane,
+                                  p.head_bytes / 2, 3)];
             }
             const bool xw = in_mask(Min) && (xm == 3 || (xm != 0 && c == pfx));
             uint32_t x = 0u;
@@ -2335,7 +2365,7 @@ select_kernel(SelP p) {
                 rank += (k2 > k0) || (k2 == k0 && eslot[e2] < s0);
                 dup |= (k2 == k0) && (e2 != e);
             }
-            orow[rank] = (int64_t)eval[e];
+            orow[SSA_IDX(rank, kk, 9)] = (int64_t)eval[e];
         }
         for (int t = f + lane; t < kk; t += SSA_WAVE) orow[t] = t < p.G ? p.glob[t] : 0;
         // the order among equal scores (and a tied kk-th place) follows the
@@ -2623,7 +2653,8 @@ topk_replay_kernel(SelP p, int chunk, int W, uint32_t *gscr, int skip_max) {
     if (cnt <= skip_max) return;
     const int kk = p.kk;
     for (int it = (int)blockIdx.x * RP_WAVES + wid; it < cnt; it += total) {
-        const int64_t row = p.tie_list[it];          // bh * N + n, over all query heads
+        // bh * N + n, over all query heads
+        const int64_t row = SSA_IDX(p.tie_list[SSA_IDX(it, p.rows_all, 6)], p.rows_all, 6);
         const int n = (int)(row % p.N);
         const int bh = (int)(row / p.N);
         const int b = bh / p.Hq, h = bh % p.Hq, g = h / p.rep;
@@ -2655,8 +2686,8 @@ topk_replay_kernel(SelP p, int chunk, int W, uint32_t *gscr, int skip_max) {
                 nl = (int64_t)nl < s1 - j0 ? nl : (int)(s1 - j0);
                 const int u = qids[list];
                 const int64_t prow = (int64_t)bk * p.R + list / p.NS;
-                const int st = p.bstart[prow * p.NB + u];
-                const int sz = p.bsize[prow * p.NB + u];
+                const int st = p.bstart[prow * p.NB + SSA_IDX(u, p.NB, 7)];
+                const int sz = p.bsize[prow * p.NB + SSA_IDX(u, p.NB, 7)];
                 const int c = c0 + lane;
                 const bool in = lane < nl;
                 int v = 0;
@@ -2664,7 +2695,8 @@ topk_replay_kernel(SelP p, int chunk, int W, uint32_t *gscr, int skip_max) {
                 uint32_t sk = 0u;
                 if (sz > 0) {
                     const bool real = in && c < min(sz, p.C);
-                    const int raw = in ? p.perm[prow * p.M + (real ? st + c : p.M - 1)] : 0;
+                    const int raw =
+                        in ? p.perm[prow * p.M + SSA_IDX(real ? st + c : p.M - 1, p.M, 8)] : 0;
                     v = (p.causal && raw > n) ? n : raw;
                     const uint32_t bit = 1u << (v & 31);
                     const uint32_t old = atomicOr(&bm[v >> 5], real ? bit : 0u);
@@ -2897,7 +2929,8 @@ topk_replay_wg_kernel(SelP p, int chunk, int W, int nsim, uint32_t *gscr, int64_
     for (int i = threadIdx.x; i < p.M; i += RPW_THREADS) first[i] = 0xffffffffu;
 
     for (int it = (int)blockIdx.x; it < cnt; it += (int)gridDim.x) {
-        const int64_t row = p.tie_list[it];          // bh * N + n, over all query heads
+        // bh * N + n, over all query heads
+        const int64_t row = SSA_IDX(p.tie_list[SSA_IDX(it, p.rows_all, 6)], p.rows_all, 6);
         const int n = (int)(row % p.N);
         const int bh = (int)(row / p.N);
         const int b = bh / p.Hq, h = bh % p.Hq, gq = h / p.rep;
@@ -2909,8 +2942,8 @@ topk_replay_wg_kernel(SelP p, int chunk, int W, int nsim, uint32_t *gscr, int64_
         for (int l = threadIdx.x; l < nls; l += RPW_THREADS) {
             const int u = qids[l];
             const int64_t prow = (int64_t)bk * p.R + l / p.NS;
-            lst[l] = p.bstart[prow * p.NB + u];
-            lsz[l] = p.bsize[prow * p.NB + u];
+            lst[l] = p.bstart[prow * p.NB + SSA_IDX(u, p.NB, 7)];
+            lsz[l] = p.bsize[prow * p.NB + SSA_IDX(u, p.NB, 7)];
         }
         for (int64_t w = threadIdx.x; w < (p.Call + 31) / 32; w += RPW_THREADS) kbits[w] = 0u;
         if (wid == 0) {
@@ -2941,7 +2974,8 @@ topk_replay_wg_kernel(SelP p, int chunk, int W, int nsim, uint32_t *gscr, int64_
                     if (sz > 0) {
                         const bool real = c < min(sz, p.C);
                         const int64_t prow = (int64_t)bk * p.R + list / p.NS;
-                        const int raw = p.perm[prow * p.M + (real ? lst[list] + c : p.M - 1)];
+                        const int raw =
+                            p.perm[prow * p.M + SSA_IDX(real ? lst[list] + c : p.M - 1, p.M, 8)];
                         v[u] = (p.causal && raw > n) ? n : raw;
                         fl[u] = real ? RPW_VALID : 0u;
                     } else {
@@ -2962,7 +2996,7 @@ topk_replay_wg_kernel(SelP p, int chunk, int W, int nsim, uint32_t *gscr, int64_
                 const uint64_t nm = wave_ballot(in && vu == n);
                 bool need = in && !(lane > 0 && vprev == vu);
                 if (in && vu == n) need = lane == (int)(__ffsll((long long)nm) - 1);
-                if (need) atomicMin(&first[vu], (uint32_t)j);
+                if (need) atomicMin(&first[SSA_IDX(vu, p.M, 10)], (uint32_t)j);
                 if (in) svs[j] = (uint32_t)vu | fl[u];
             }
         }
@@ -2979,7 +3013,8 @@ topk_replay_wg_kernel(SelP p, int chunk, int W, int nsim, uint32_t *gscr, int64_
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
                 const int64_t j = j0 + (int64_t)u * RPW_THREADS;
-                fv[u] = j < p.Call ? __hip_atomic_load(&first[vs[u] & RPW_VMASK], __ATOMIC_RELAXED,
+                fv[u] = j < p.Call ? __hip_atomic_load(&first[SSA_IDX(vs[u] & RPW_VMASK, p.M, 10)],
+                                                       __ATOMIC_RELAXED,
                                                        __HIP_MEMORY_SCOPE_AGENT)
                                    : 0xffffffffu;
             }
@@ -3018,7 +3053,8 @@ topk_replay_wg_kernel(SelP p, int chunk, int W, int nsim, uint32_t *gscr, int64_
                         const int64_t j = s0 + jl;
                         const bool in = jl < c;
                         const bool keep = in && ((kbits[j >> 5] >> (j & 31)) & 1u);
-                        if (in && (vs[u] & RPW_OWNER)) first[vs[u] & RPW_VMASK] = 0xffffffffu;
+                        if (in && (vs[u] & RPW_OWNER))
+                            first[SSA_IDX(vs[u] & RPW_VMASK, p.M, 10)] = 0xffffffffu;
                         if (in && !keep) skey[j] = RP_NEGINF;
                         const uint64_t m = wave_ballot(keep);
                         if (keep) {
@@ -3274,7 +3310,7 @@ topk_replay_wg_kernel(SelP p, int chunk, int W, int nsim, uint32_t *gscr, int64_
                     if (tg >= kk) { js = (int64_t)s * chunk + (tg - kk); break; }
                     pos = tg;
                 }
-                cand[t] = js >= 0 ? (int32_t)(svs[js] & RPW_VMASK) : 0;
+                cand[t] = js >= 0 ? (int32_t)(svs[SSA_IDX(js, p.Call, 11)] & RPW_VMASK) : 0;
             }
             rp_sync();
             if (LSH_MODE) {
@@ -3985,7 +4021,7 @@ int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char 
         sp.G = D.G; sp.kk = D.kk; sp.window = a->window; sp.causal = a->causal;
         sp.cross = a->is_cross; sp.mode = a->mode; sp.total_k = a->total_k; sp.Kw = D.Kw;
         sp.Kout = D.Kout; sp.bh0 = (int)bh0; sp.words = sel_bitmap_words(D.M);
-        sp.Call = D.Call; sp.rows = (int64_t)nbh * D.N;
+        sp.Call = D.Call; sp.rows = (int64_t)nbh * D.N; sp.rows_all = D.BH * D.N;
         sp.out_idx = a->out_idx; sp.out_valid = a->out_valid; sp.ties = a->out_ties;
         sp.out_idx32 = a->mode == SSA_GRAPH_FULL ? a->out_idx32 : nullptr;
         sp.tie_list = (int32_t *)(ws + L.tie_list);
@@ -4204,4 +4240,18 @@ extern "C" int ssa_project_gemm(const void *x, int64_t ldx, const void *w, int64
                       ldw % 8 == 0 && ldy % 8 == 0,
                   "project_gemm: operands must be 16-byte aligned rows");
     return ssa_launch_project(p, (hipStream_t)stream);
+}
+
+extern "C" int ssa_checked_oob(uint32_t *record) {
+#ifdef SSA_CHECKED
+    SSA_CHECK_ARG(record != nullptr, "checked_oob: record");
+    SSA_CHECK_HIP(hipDeviceSynchronize());
+    SSA_CHECK_HIP(hipMemcpyFromSymbol(record, HIP_SYMBOL(ssa_oob), sizeof(uint32_t) * 4));
+    const uint32_t zero[4] = {0u, 0u, 0u, 0u};
+    SSA_CHECK_HIP(hipMemcpyToSymbol(HIP_SYMBOL(ssa_oob), zero, sizeof(zero)));
+    return 1;
+#else
+    (void)record;
+    return 0;
+#endif
 }
