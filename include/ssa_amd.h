@@ -242,6 +242,21 @@ typedef struct {
 
 int ssa_sparse_gather_attention_bwd(const ssa_apply_bwd_args *a, void *stream);
 
+/* Deterministic backward (the reference's CPU autograd through
+ * sparse_attention.py:1146-1199 is deterministic; ssa_sparse_gather_attention_bwd
+ * adds dk / dv with fp32 atomics, whose order varies).  Same arguments and
+ * results; each key row's terms are rounded to a fixed-point grid of that
+ * row (the finest for which slot count x largest weight x largest |q| or
+ * |dout| cannot overflow 64 bits) and summed as integers, so every run gives
+ * the same bits.  Needs a 256-byte aligned workspace of
+ * ssa_sparse_gather_attention_bwd_det_workspace_bytes (8 bytes per slot, 16
+ * per key row element and 12 per key row); a key row whose bound is not
+ * finite gets NaN.  SparseAttention takes it under
+ * torch.use_deterministic_algorithms(True). */
+int64_t ssa_sparse_gather_attention_bwd_det_workspace_bytes(const ssa_apply_bwd_args *a);
+int ssa_sparse_gather_attention_bwd_det(const ssa_apply_bwd_args *a, void *workspace,
+                                        int64_t workspace_bytes, void *stream);
+
 /* ---------------------------------------------------------------------------
  * Measurement helper (no counterpart in the reference): the L2-to-CU delivery
  * rate that bounds the gather attention, whose repeated K/V rows are served by

@@ -155,6 +155,12 @@ def _configure(L):
     L.ssa_measure_l2_read.argtypes = [c_vp, c_i64, c_i32, c_i32, c_vp, c_vp]
     L.ssa_sparse_gather_attention_bwd.restype = ctypes.c_int
     L.ssa_sparse_gather_attention_bwd.argtypes = [ctypes.POINTER(ApplyBwdArgs), c_vp]
+    L.ssa_sparse_gather_attention_bwd_det_workspace_bytes.restype = c_i64
+    L.ssa_sparse_gather_attention_bwd_det_workspace_bytes.argtypes = [
+        ctypes.POINTER(ApplyBwdArgs)]
+    L.ssa_sparse_gather_attention_bwd_det.restype = ctypes.c_int
+    L.ssa_sparse_gather_attention_bwd_det.argtypes = [ctypes.POINTER(ApplyBwdArgs), c_vp, c_i64,
+                                                      c_vp]
     L.ssa_checked_oob.restype = ctypes.c_int
     L.ssa_checked_oob.argtypes = [ctypes.POINTER(ctypes.c_uint32)]
     return L
@@ -523,7 +529,11 @@ def gather_attention_fwd(q, k, v, neighbors, valid, scale, fp32w=False, dropout_
     return out
 
 
-def gather_attention_bwd(q, k, v, neighbors, valid, scale, fp32w, dropout_p, seed, dout):
+def gather_attention_bwd(q, k, v, neighbors, valid, scale, fp32w, dropout_p, seed, dout,
+                         deterministic=False):
+    """dq, dk, dv (fp32).  deterministic: ssa_sparse_gather_attention_bwd_det,
+    whose dK / dV sums are fixed-point and so the same bits on every run (a
+    workspace is allocated here); else the fp32-atomic backward."""
     check_apply_shapes(q, k, v, neighbors, valid, dout)
     require_device(q, k, v, neighbors, valid, dout)
     B, Hq, N, d = q.shape
@@ -538,8 +548,19 @@ def gather_attention_bwd(q, k, v, neighbors, valid, scale, fp32w, dropout_p, see
     b = ApplyBwdArgs()
     b.fwd = a
     b.dout, b.dq, b.dk, b.dv = do.data_ptr(), dq.data_ptr(), dk.data_ptr(), dv.data_ptr()
-    _check(lib().ssa_sparse_gather_attention_bwd(ctypes.byref(b), _stream(q)),
-           "sparse_gather_attention_bwd")
+    L = lib()
+    if deterministic:
+        wsb = L.ssa_sparse_gather_attention_bwd_det_workspace_bytes(ctypes.byref(b))
+        if wsb < 0:
+            _check(int(wsb), "sparse_gather_attention_bwd_det")
+        ws = torch.empty(max(int(wsb), 1), dtype=torch.uint8, device=q.device)
+        _check(L.ssa_sparse_gather_attention_bwd_det(ctypes.byref(b), ws.data_ptr(), int(wsb),
+                                                     _stream(q)),
+               "sparse_gather_attention_bwd_det")
+        del ws            # the allocator orders its reuse after this stream's work
+    else:
+        _check(L.ssa_sparse_gather_attention_bwd(ctypes.byref(b), _stream(q)),
+               "sparse_gather_attention_bwd")
     del keep
     return dq, dk, dv
 

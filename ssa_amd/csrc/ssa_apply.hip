@@ -42,6 +42,13 @@ struct ApplyP {
     // backward
     const float *dout;
     float *dq, *dk, *dv;
+    // deterministic backward (workspace): per (row, slot) the two weights the
+    // key and value gradients take, per key row its slot count and largest
+    // weights (float bits), the largest |q| and |dout| (float bits), and the
+    // fixed-point sums
+    float *wdraw, *wpw;
+    uint32_t *kcnt, *kmaxd, *kmaxp, *gmax;
+    unsigned long long *acck, *accv;
 };
 
 constexpr int WAVES = 4;   // waves per workgroup
@@ -499,7 +506,11 @@ apply_fwd16_kernel(ApplyP p) {
 
 // Backward: recompute p, then dp = dO.v, ds = p (dp - sum p dp), draw = ds*scale,
 // dq = sum draw k (direct store), dk += draw q, dv += p' dO (fp32 atomics).
-template <typename T, int D>
+// DET (the deterministic backward's first pass): instead of the atomics, each
+// slot's draw and p' go to the workspace, and its key row's slot count and
+// largest |draw| and |p'| are raised (integer atomics, whose results do not
+// depend on their order), as are the largest |q| and |dout|.
+template <typename T, int D, bool DET>
 __global__ void __launch_bounds__(WAVES * SSA_WAVE)
 apply_bwd_kernel(ApplyP p) {
     using G = Geo<T, D>;
@@ -583,6 +594,21 @@ apply_bwd_kernel(ApplyP p) {
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
+    if (DET) {
+        // the largest |q| and |dout| bound every slot's contributions
+        float qm = 0.f, dm = 0.f;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+            qm = fmaxf(qm, fabsf(qf[e]));
+            dm = fmaxf(dm, fabsf(dof[e]));
+        }
+        qm = wave_max(qm);
+        dm = wave_max(dm);
+        if (lane == 0) {
+            atomicMax(&p.gmax[0], __float_as_uint(qm));
+            atomicMax(&p.gmax[1], __float_as_uint(dm));
+        }
+    }
     float dqa[VEC];
 #pragma unroll
     for (int e = 0; e < VEC; ++e) dqa[e] = 0.f;
@@ -590,7 +616,10 @@ apply_bwd_kernel(ApplyP p) {
         const int j = j0 + sub;
         if (j >= p.K) continue;
         int64_t x = nb[j];
-        if (x < 0 || x >= p.M) continue;
+        if (x < 0 || x >= p.M) {
+            if (DET && li == 0) { p.wdraw[row * p.K + j] = 0.f; p.wpw[row * p.K + j] = 0.f; }
+            continue;
+        }
         const float pj = sc[j];
         const float draw = pj * (dpv[j] - pdp) * p.scale;
         float mask = 1.f;
@@ -598,13 +627,26 @@ apply_bwd_kernel(ApplyP p) {
         const float pw = pj * mask;
         float kf[VEC];
         load_vec<T, VEC>(kb + x * p.ksn + lofs, kf);
-        float *dkr = p.dk + (((int64_t)b * p.Hkv + g) * p.M + x) * p.d + lofs;
-        float *dvr = p.dv + (((int64_t)b * p.Hkv + g) * p.M + x) * p.d + lofs;
+        const int64_t kr = ((int64_t)b * p.Hkv + g) * p.M + x;
+        if (DET) {
+            if (li == 0) {
+                p.wdraw[row * p.K + j] = draw;
+                p.wpw[row * p.K + j] = pw;
+                atomicAdd(&p.kcnt[kr], 1u);
+                atomicMax(&p.kmaxd[kr], __float_as_uint(fabsf(draw)));
+                atomicMax(&p.kmaxp[kr], __float_as_uint(fabsf(pw)));
+            }
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-            dqa[e] = fmaf(draw, kf[e], dqa[e]);
-            if (live && draw != 0.f) unsafeAtomicAdd(dkr + e, draw * qf[e]);
-            if (live && pw != 0.f) unsafeAtomicAdd(dvr + e, pw * dof[e]);
+            for (int e = 0; e < VEC; ++e) dqa[e] = fmaf(draw, kf[e], dqa[e]);
+        } else {
+            float *dkr = p.dk + kr * p.d + lofs;
+            float *dvr = p.dv + kr * p.d + lofs;
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) {
+                dqa[e] = fmaf(draw, kf[e], dqa[e]);
+                if (live && draw != 0.f) unsafeAtomicAdd(dkr + e, draw * qf[e]);
+                if (live && pw != 0.f) unsafeAtomicAdd(dvr + e, pw * dof[e]);
+            }
         }
     }
 #pragma unroll
@@ -616,6 +658,98 @@ apply_bwd_kernel(ApplyP p) {
 #pragma unroll
         for (int e = 0; e < VEC; ++e) dqr[e] = dqa[e];
     }
+}
+
+// ---- deterministic backward: fixed-point sums
+// A key row's gradient is a sum over the (query row, slot) pairs that hold it.
+// Its terms are rounded to a fixed-point grid of that key row and summed as
+// 64-bit integers, whose sum does not depend on the order the atomics land
+// in; the grid 2^-s is the finest for which the sum cannot overflow: count x
+// largest weight x largest |q| (or |dout|) below 2^(61 - s).  Returns -1
+// when the key row has no term, -2 when a bound is not finite.
+__device__ __forceinline__ int fx_shift(uint32_t cnt, uint32_t wbits, uint32_t xbits) {
+    const double bound = (double)cnt * (double)__uint_as_float(wbits) * (double)__uint_as_float(xbits);
+    if (!(bound == bound) || bound > 1e300) return -2;
+    if (!(bound > 0.0)) return -1;
+    int e = 0;
+    (void)frexp(bound, &e);                 // bound < 2^e
+    return 61 - e;
+}
+
+__device__ __forceinline__ unsigned long long fx_of(float c, int s) {
+    return (unsigned long long)(long long)rint(ldexp((double)c, s));
+}
+
+// second pass: per query row, each slot's terms draw * q and p' * dout added
+// to its key row's fixed-point sums
+template <typename T, int D>
+__global__ void __launch_bounds__(WAVES * SSA_WAVE)
+apply_bwd_fx_kernel(ApplyP p) {
+    using G = Geo<T, D>;
+    constexpr int VEC = G::VEC, LPR = G::LPR, RPI = G::RPI;
+    const int64_t blk = xcd_logical_block(blockIdx.x, p.nblocks);
+    if (blk >= p.nblocks) return;
+    const int wid = threadIdx.x / SSA_WAVE;
+    const int64_t row = blk * WAVES + wid;
+    if (row >= p.rows) return;
+    const int lane = lane_id();
+    const int sub = lane / LPR, li = lane % LPR;
+    const int n = (int)(row % p.N);
+    const int64_t bh = row / p.N;
+    const int h = (int)(bh % p.Hq);
+    const int b = (int)(bh / p.Hq);
+    const int g = h / p.rep;
+    const T *qrow = (const T *)p.q + b * p.qsb + h * p.qsh + (int64_t)n * p.qsn;
+    const int64_t *nb = p.nb + row * p.K;
+    const bool live = li * VEC < p.d;
+    const int lofs = live ? li * VEC : 0;
+    const float *dorow = p.dout + row * p.d + lofs;
+    float qf[VEC], dof[VEC];
+    load_vec<T, VEC>(qrow + lofs, qf);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+        dof[e] = live ? dorow[e] : 0.f;
+        qf[e] = live ? qf[e] : 0.f;
+    }
+    const uint32_t qmax = p.gmax[0], dmax = p.gmax[1];
+    for (int j0 = 0; j0 < p.K; j0 += RPI) {
+        const int j = j0 + sub;
+        if (j >= p.K) continue;
+        const int64_t x = nb[j];
+        if (x < 0 || x >= p.M) continue;
+        const float draw = p.wdraw[row * p.K + j], pw = p.wpw[row * p.K + j];
+        const int64_t kr = ((int64_t)b * p.Hkv + g) * p.M + x;
+        const uint32_t cnt = p.kcnt[kr];
+        const int sk = fx_shift(cnt, p.kmaxd[kr], qmax);
+        const int sv = fx_shift(cnt, p.kmaxp[kr], dmax);
+        unsigned long long *ak = p.acck + kr * p.d + lofs;
+        unsigned long long *av = p.accv + kr * p.d + lofs;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+            if (live && draw != 0.f && sk >= 0) atomicAdd(ak + e, fx_of(draw * qf[e], sk));
+            if (live && pw != 0.f && sv >= 0) atomicAdd(av + e, fx_of(pw * dof[e], sv));
+        }
+    }
+}
+
+// last pass: dk += sum * 2^-s, dv likewise, per element (NaN where a bound
+// was not finite)
+__global__ void __launch_bounds__(256) apply_bwd_finish_kernel(ApplyP p, int64_t total) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= total) return;
+    const int64_t kr = i / p.d;
+    const uint32_t cnt = p.kcnt[kr];
+    const int sk = fx_shift(cnt, p.kmaxd[kr], p.gmax[0]);
+    const int sv = fx_shift(cnt, p.kmaxp[kr], p.gmax[1]);
+    if (sk >= 0) p.dk[i] += (float)ldexp((double)(long long)p.acck[i], -sk);
+    else if (sk == -2) p.dk[i] = __builtin_nanf("");
+    if (sv >= 0) p.dv[i] += (float)ldexp((double)(long long)p.accv[i], -sv);
+    else if (sv == -2) p.dv[i] = __builtin_nanf("");
+}
+
+__global__ void __launch_bounds__(256) apply_zero_kernel(uint32_t *w, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+        w[i] = 0u;
 }
 
 // The 16-bit path needs weights in the value dtype, 16-byte aligned rows,
@@ -638,13 +772,30 @@ bool fwd16_ok(const ApplyP &p, int elem, int D) {
 template <typename T, int D>
 int launch_apply(const ApplyP &p, hipStream_t st, bool bwd) {
     const int64_t grid = 8 * ceil_div(p.nblocks, 8);
-    if (bwd) {
+    if (bwd && p.wdraw) {
+        // deterministic: rows (dq, weights, bounds), fixed-point sums, finish
         const size_t lds = (size_t)WAVES * 2 * p.K * sizeof(float);
         if (lds > 65536)
-            SSA_CHECK_HIP(hipFuncSetAttribute((const void *)apply_bwd_kernel<T, D>,
+            SSA_CHECK_HIP(hipFuncSetAttribute((const void *)apply_bwd_kernel<T, D, true>,
                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        hipLaunchKernelGGL((apply_bwd_kernel<T, D>), dim3((unsigned)grid), dim3(WAVES * SSA_WAVE),
-                           lds, st, p);
+        hipLaunchKernelGGL((apply_bwd_kernel<T, D, true>), dim3((unsigned)grid),
+                           dim3(WAVES * SSA_WAVE), lds, st, p);
+        SSA_CHECK_LAUNCH();
+        hipLaunchKernelGGL((apply_bwd_fx_kernel<T, D>), dim3((unsigned)grid),
+                           dim3(WAVES * SSA_WAVE), 0, st, p);
+        SSA_CHECK_LAUNCH();
+        const int64_t total = (int64_t)p.B * p.Hkv * p.M * p.d;
+        if (total > 0) {
+            hipLaunchKernelGGL(apply_bwd_finish_kernel, dim3((unsigned)ceil_div(total, 256)),
+                               dim3(256), 0, st, p, total);
+        }
+    } else if (bwd) {
+        const size_t lds = (size_t)WAVES * 2 * p.K * sizeof(float);
+        if (lds > 65536)
+            SSA_CHECK_HIP(hipFuncSetAttribute((const void *)apply_bwd_kernel<T, D, false>,
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        hipLaunchKernelGGL((apply_bwd_kernel<T, D, false>), dim3((unsigned)grid),
+                           dim3(WAVES * SSA_WAVE), lds, st, p);
     } else {
         const size_t lds = (size_t)WAVES * 2 * p.K * sizeof(float);
         constexpr int U = (Geo<T, D>::RPI >= 8) ? 4 : 8;
@@ -756,9 +907,10 @@ extern "C" int ssa_sparse_gather_attention(const ssa_apply_args *a, void *stream
     return run_apply(p, a->q.dtype, a->d, (hipStream_t)stream, false);
 }
 
-extern "C" int ssa_sparse_gather_attention_bwd(const ssa_apply_bwd_args *a, void *stream) {
+namespace {
+
+int bwd_common(const ssa_apply_bwd_args *a, ApplyP &p) {
     SSA_CHECK_ARG(a != nullptr, "sparse_gather_attention_bwd: null args");
-    ApplyP p;
     int rc = apply_common(&a->fwd, p);
     if (rc) return rc;
     SSA_CHECK_ARG(a->dout && a->dq && a->dk && a->dv, "sparse_gather_attention_bwd: null grad");
@@ -766,5 +918,76 @@ extern "C" int ssa_sparse_gather_attention_bwd(const ssa_apply_bwd_args *a, void
                   "sparse_gather_attention_bwd: needs the int64 neighbours");
     p.dout = a->dout; p.dq = a->dq; p.dk = a->dk; p.dv = a->dv;
     p.row_inv = nullptr;
+    return SSA_OK;
+}
+
+int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
+
+// workspace of the deterministic backward: the per-slot weights, then (zeroed
+// together) the key rows' counts and bounds, the two maxima and the sums
+struct DetLayout {
+    int64_t wdraw, wpw, zero_at, kcnt, kmaxd, kmaxp, gmax, acck, accv, total;
+};
+
+DetLayout det_layout(const ApplyP &p) {
+    DetLayout L{};
+    const int64_t slots = p.rows * p.K, keys = (int64_t)p.B * p.Hkv * p.M;
+    int64_t o = 0;
+    auto take = [&](int64_t bytes) { const int64_t at = o; o += align256(bytes); return at; };
+    L.wdraw = take(slots * 4);
+    L.wpw = take(slots * 4);
+    L.zero_at = o;
+    L.kcnt = take(keys * 4);
+    L.kmaxd = take(keys * 4);
+    L.kmaxp = take(keys * 4);
+    L.gmax = take(8);
+    L.acck = take(keys * p.d * 8);
+    L.accv = take(keys * p.d * 8);
+    L.total = o;
+    return L;
+}
+
+}  // namespace
+
+extern "C" int ssa_sparse_gather_attention_bwd(const ssa_apply_bwd_args *a, void *stream) {
+    ApplyP p;
+    const int rc = bwd_common(a, p);
+    if (rc) return rc;
     return run_apply(p, a->fwd.q.dtype, a->fwd.d, (hipStream_t)stream, true);
+}
+
+extern "C" int64_t ssa_sparse_gather_attention_bwd_det_workspace_bytes(const ssa_apply_bwd_args *a) {
+    ApplyP p;
+    const int rc = bwd_common(a, p);
+    if (rc) return rc;
+    return det_layout(p).total;
+}
+
+extern "C" int ssa_sparse_gather_attention_bwd_det(const ssa_apply_bwd_args *a, void *workspace,
+                                                   int64_t workspace_bytes, void *stream) {
+    ApplyP p;
+    const int rc = bwd_common(a, p);
+    if (rc) return rc;
+    const DetLayout L = det_layout(p);
+    SSA_CHECK_ARG(workspace != nullptr && workspace_bytes >= L.total,
+                  "sparse_gather_attention_bwd_det: workspace of %lld bytes, %lld needed",
+                  (long long)workspace_bytes, (long long)L.total);
+    SSA_CHECK_ARG((uintptr_t)workspace % 256 == 0,
+                  "sparse_gather_attention_bwd_det: workspace must be 256-byte aligned");
+    if (p.rows == 0) return SSA_OK;
+    char *ws = (char *)workspace;
+    p.wdraw = (float *)(ws + L.wdraw);
+    p.wpw = (float *)(ws + L.wpw);
+    p.kcnt = (uint32_t *)(ws + L.kcnt);
+    p.kmaxd = (uint32_t *)(ws + L.kmaxd);
+    p.kmaxp = (uint32_t *)(ws + L.kmaxp);
+    p.gmax = (uint32_t *)(ws + L.gmax);
+    p.acck = (unsigned long long *)(ws + L.acck);
+    p.accv = (unsigned long long *)(ws + L.accv);
+    const hipStream_t st = (hipStream_t)stream;
+    const int64_t nz = (L.total - L.zero_at) / 4;
+    hipLaunchKernelGGL(apply_zero_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(nz, 256), 4096)),
+                       dim3(256), 0, st, (uint32_t *)(ws + L.zero_at), nz);
+    SSA_CHECK_LAUNCH();
+    return run_apply(p, a->fwd.q.dtype, a->fwd.d, st, true);
 }

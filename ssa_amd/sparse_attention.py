@@ -219,24 +219,6 @@ def merge_neighbors(win_idx: torch.Tensor, glob_idx: torch.Tensor, lsh_idx: torc
 
 
 # ---------------------------------------------------------------------------- apply
-def _alert_nondeterministic_backward():
-    """The backward scatters dK and dV with fp32 atomics, so their summation
-    order (and last bits) can change from run to run.  Like torch's own ops
-    without a deterministic implementation, it raises under
-    ``torch.use_deterministic_algorithms(True)`` and warns with
-    ``warn_only=True``."""
-    if not torch.are_deterministic_algorithms_enabled():
-        return
-    msg = ("sparse_gather_attention backward does not have a deterministic implementation "
-           "(dK and dV accumulate with fp32 atomics), but you set "
-           "'torch.use_deterministic_algorithms(True)'.  You can turn off determinism just for "
-           "this operation, or use the 'warn_only=True' option if that is acceptable.")
-    if torch.is_deterministic_algorithms_warn_only_enabled():
-        warnings.warn(msg)
-    else:
-        raise RuntimeError(msg)
-
-
 class _GatherAttention(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, neighbors, valid, scale, fp32w, dropout_p, seed, row_invalid=None):
@@ -248,11 +230,14 @@ class _GatherAttention(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dout):
-        _alert_nondeterministic_backward()
+        # under torch.use_deterministic_algorithms(True) the backward whose
+        # dK / dV sums are fixed-point (the same bits on every run); else the
+        # faster one that adds them with fp32 atomics
         q, k, v, neighbors, valid = ctx.saved_tensors
         scale, fp32w, dropout_p, seed = ctx.cfg
         dq, dk, dv = _lib.gather_attention_bwd(q, k, v, neighbors, valid, scale, fp32w,
-                                               dropout_p, seed, dout)
+                                               dropout_p, seed, dout,
+                                               deterministic=torch.are_deterministic_algorithms_enabled())
         return (dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), None, None, None, None, None,
                 None, None)
 

@@ -23,7 +23,8 @@ def test_header_declares_the_entry_points():
     for must in ["ssa_build_graph", "ssa_graph_workspace_bytes", "ssa_graph_out_width",
                  "ssa_bucket_sort", "ssa_bucket_sort_workspace_bytes", "ssa_merge_neighbors",
                  "ssa_sparse_gather_attention", "ssa_sparse_gather_attention_bwd",
-                 "ssa_version", "ssa_last_error"]:
+                 "ssa_sparse_gather_attention_bwd_det", "ssa_build_graph_noalloc",
+                 "ssa_project_build_graph", "ssa_checked_oob", "ssa_version", "ssa_last_error"]:
         assert must in names
 
 
@@ -31,6 +32,19 @@ def test_library_exports_every_declared_symbol():
     import torch  # noqa: F401  (binds the library to torch's HIP runtime)
     from ssa_amd import _lib
     L = _lib.lib()
+    for name in declared_functions():
+        assert hasattr(L, name), f"{name} declared in ssa_amd.h but not exported"
+
+
+def test_checked_library_exports_every_declared_symbol():
+    """The bounds-checked twin (built by `make checked`, as build() does) is
+    the same C ABI."""
+    import ctypes
+
+    import torch  # noqa: F401
+    from ssa_amd import _lib
+    assert os.path.exists(_lib.CHECKED_LIB_PATH), "libssa_amd_checked.so is not built"
+    L = ctypes.CDLL(_lib.CHECKED_LIB_PATH)
     for name in declared_functions():
         assert hasattr(L, name), f"{name} declared in ssa_amd.h but not exported"
 
@@ -51,7 +65,8 @@ def test_struct_layouts_match_the_header(tmp_path):
     if gcc is None:
         pytest.skip("no C compiler")
     mirrors = {"ssa_tensor4": _lib.Tensor4, "ssa_graph_args": _lib.GraphArgs,
-               "ssa_apply_args": _lib.ApplyArgs, "ssa_apply_bwd_args": _lib.ApplyBwdArgs}
+               "ssa_apply_args": _lib.ApplyArgs, "ssa_apply_bwd_args": _lib.ApplyBwdArgs,
+               "ssa_project_graph_args": _lib.ProjectGraphArgs}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "ssa_amd.h"', 'int main(void) {']
     for cname, py in mirrors.items():
         lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')

@@ -579,6 +579,77 @@ def test_apply_backward_at_bench_head_shape(dtype, fp32w):
         _check_grad_rows(name, got, exp, dtype)
 
 
+# ------------------------------------------------------------------ deterministic backward
+@pytest.mark.parametrize("dtype,dropout", [(torch.float32, 0.0), (torch.bfloat16, 0.0),
+                                           (torch.bfloat16, 0.2)])
+def test_deterministic_backward_same_bits_and_matches_autograd(dtype, dropout):
+    """Under torch.use_deterministic_algorithms(True) the backward takes
+    ssa_sparse_gather_attention_bwd_det: dK / dV summed as fixed-point
+    integers per key row, so three runs give the same bits; every row of
+    dq / dk / dv matches float64 autograd (with the dropout mask read off the
+    output, as in the dropout test) to the per-row bar.  GQA (8 query heads
+    over 2 kv heads), N=M=2048, K=128, d=128, every key reached by several
+    queries and some by hundreds."""
+    from ssa_amd import sparse_gather_attention
+    B, H, nkv, N, M, d, K = 1, 8, 2, 2048, 2048, 128, 128
+    g = torch.Generator().manual_seed(31)
+    q = (torch.randn(B, H, N, d, generator=g) * 0.5).to(dtype)
+    k = (torch.randn(B, nkv, M, d, generator=g) * 0.5).to(dtype)
+    v = torch.randn(B, nkv, M, d, generator=g).to(dtype)
+    nb = torch.randint(0, M, (B, H, N, K), generator=g)
+    nb[..., :4] = torch.arange(4)                   # four keys every query reads
+    va = torch.rand(B, H, N, K, generator=g) > 0.2
+    va[..., 0] = True
+    dout = torch.randn(B, H, N, d, generator=g)
+    prev = torch.are_deterministic_algorithms_enabled()
+    grads, outs = [], []
+    try:
+        torch.use_deterministic_algorithms(True)
+        for _ in range(3):
+            qd, kd, vd = (t.to(DEV).requires_grad_(True) for t in (q, k, v))
+            torch.manual_seed(77)
+            out = sparse_gather_attention(qd, kd, vd, nb.to(DEV), d ** -0.5, valid=va.to(DEV),
+                                          dropout=dropout, training=dropout > 0)
+            out.backward(dout.to(DEV, dtype))
+            torch.cuda.synchronize()
+            grads.append((qd.grad.clone(), kd.grad.clone(), vd.grad.clone()))
+            outs.append(out.detach().clone())
+    finally:
+        torch.use_deterministic_algorithms(prev)
+    for gr in grads[1:]:
+        for a, b_ in zip(gr, grads[0]):
+            assert torch.equal(a, b_)
+    # with dropout the reference is the fp32-atomic backward of the same seed
+    # (itself checked against float64 autograd by the dropout test); without,
+    # float64 autograd
+    if dropout > 0:
+        qd, kd, vd = (t.to(DEV).requires_grad_(True) for t in (q, k, v))
+        torch.manual_seed(77)
+        out = sparse_gather_attention(qd, kd, vd, nb.to(DEV), d ** -0.5, valid=va.to(DEV),
+                                      dropout=dropout, training=True)
+        out.backward(dout.to(DEV, dtype))
+        torch.cuda.synchronize()
+        assert torch.equal(out.detach(), outs[0])
+        for name, got, exp in [("dq", grads[0][0], qd.grad), ("dk", grads[0][1], kd.grad),
+                               ("dv", grads[0][2], vd.grad)]:
+            _check_grad_rows(name, got.float(), exp.double(), dtype)
+        return
+    qr, kr, vr = (t.to(DEV).double().requires_grad_(True) for t in (q, k, v))
+    nbd, vad = nb.to(DEV), va.to(DEV)
+    ke = kr.repeat_interleave(H // nkv, 1)
+    ve = vr.repeat_interleave(H // nkv, 1)
+    flat = (nbd + torch.arange(B * H, device=DEV).view(B, H, 1, 1) * M).reshape(-1)
+    kg = ke.reshape(B * H * M, d).index_select(0, flat).view(B, H, N, K, d)
+    vg = ve.reshape(B * H * M, d).index_select(0, flat).view(B, H, N, K, d)
+    s = (qr.unsqueeze(3) * kg).sum(-1) * d ** -0.5
+    p = torch.softmax(s.masked_fill(~vad, float("-inf")), -1)
+    o = (p.unsqueeze(-1) * vg).sum(3)
+    o.backward(dout.to(DEV).double())
+    for name, got, exp in [("dq", grads[0][0], qr.grad), ("dk", grads[0][1], kr.grad),
+                           ("dv", grads[0][2], vr.grad)]:
+        _check_grad_rows(name, got, exp, dtype)
+
+
 # ------------------------------------------------------------------ merge
 @pytest.mark.parametrize("has_self", [True, False])
 @pytest.mark.parametrize("K", [8, 24, 200])

@@ -188,27 +188,3 @@ def test_seeded_model_construction_matches_reference_state_dict(path):
     assert sorted(sd.keys()) == ref_keys
     for key in ref_keys:
         np.testing.assert_array_equal(sd[key].numpy(), z["sd_" + key], err_msg=key)
-
-
-def test_backward_alerts_under_deterministic_algorithms():
-    """dK/dV use fp32 atomics: the backward raises under
-    torch.use_deterministic_algorithms(True) and warns with warn_only=True,
-    as torch's own nondeterministic ops do."""
-    import warnings
-
-    from ssa_amd.sparse_attention import _alert_nondeterministic_backward
-    prev, prev_warn = (torch.are_deterministic_algorithms_enabled(),
-                       torch.is_deterministic_algorithms_warn_only_enabled())
-    try:
-        torch.use_deterministic_algorithms(False)
-        _alert_nondeterministic_backward()                      # silent by default
-        torch.use_deterministic_algorithms(True)
-        with pytest.raises(RuntimeError, match="deterministic implementation"):
-            _alert_nondeterministic_backward()
-        torch.use_deterministic_algorithms(True, warn_only=True)
-        with warnings.catch_warnings(record=True) as w:
-            warnings.simplefilter("always")
-            _alert_nondeterministic_backward()
-        assert any("deterministic implementation" in str(x.message) for x in w)
-    finally:
-        torch.use_deterministic_algorithms(prev, warn_only=prev_warn)
