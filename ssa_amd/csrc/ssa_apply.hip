@@ -241,6 +241,140 @@ apply_fwd_kernel(ApplyP p) {
     }
 }
 
+// ---------------------------------------------------------------- rows beyond LDS
+// Rows of more than APPLY_KLDS slots (whose scores do not fit a wave's share
+// of LDS): nothing is kept per slot.  The scores are computed again in each
+// pass over the row (same products, same order, so the same values): first
+// the softmax maximum and sum online (a slot raising the maximum rescales the
+// sum), then the weights, whose arithmetic is the kernels' above.
+constexpr int APPLY_KLDS = 4096;
+
+template <typename T, int VEC, int LPR>
+struct LongRow {
+    const ApplyP &p;
+    int64_t row;
+    const T *kb, *vb;
+    const int64_t *nb;
+    const uint8_t *va;
+    int lofs;
+    // key id of slot j, -1 when masked or out of range
+    __device__ int id(int j, bool *marked = nullptr) const {
+        const int64_t x = p.nb32 ? (int64_t)p.nb32[row * p.K + j] : nb[j];
+        const bool mk = p.nb32 ? x < 0 : (va ? va[j] == 0 : false);
+        if (marked) *marked = mk;
+        return (!mk && x >= 0 && x < p.M) ? (int)x : -1;
+    }
+    // score of slot j (key id x, -1: -inf), every lane of the slot's group
+    __device__ float score(const float (&qf)[VEC], int x) const {
+        float kf[VEC];
+        load_vec<T, VEC>(kb + (int64_t)(x < 0 ? 0 : x) * p.ksn + lofs, kf);
+        float part = 0.f;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) part = fmaf(qf[e], kf[e], part);
+#pragma unroll
+        for (int o = LPR / 2; o > 0; o >>= 1) part += __shfl_xor(part, o, SSA_WAVE);
+        return x >= 0 ? part * p.scale : -INFINITY;
+    }
+    // dout . v of key x (row 0 for -1), every lane of the slot's group
+    __device__ float dotv(const float (&dof)[VEC], int x) const {
+        float vf[VEC];
+        load_vec<T, VEC>(vb + (int64_t)(x < 0 ? 0 : x) * p.vsn + lofs, vf);
+        float part = 0.f;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) part = fmaf(dof[e], vf[e], part);
+#pragma unroll
+        for (int o = LPR / 2; o > 0; o >>= 1) part += __shfl_xor(part, o, SSA_WAVE);
+        return part;
+    }
+};
+
+// online softmax statistics of one lane group, then merged over the wave
+__device__ __forceinline__ void online_add(float s, float &m, float &l) {
+    if (s == -INFINITY) return;
+    if (s > m) { l = l * expf(m - s) + 1.f; m = s; }
+    else l += expf(s - m);
+}
+
+__device__ __forceinline__ void online_merge(bool lead, float m, float l, float &mm, float &ll) {
+    mm = wave_max(lead ? m : -INFINITY);
+    ll = wave_sum((lead && m != -INFINITY) ? l * expf(m - mm) : 0.f);
+}
+
+template <typename T, int D>
+__global__ void __launch_bounds__(WAVES * SSA_WAVE)
+apply_fwd_long_kernel(ApplyP p) {
+    using G = Geo<T, D>;
+    constexpr int VEC = G::VEC, LPR = G::LPR, RPI = G::RPI;
+    const int64_t blk = xcd_logical_block(blockIdx.x, p.nblocks);
+    if (blk >= p.nblocks) return;
+    const int wid = threadIdx.x / SSA_WAVE;
+    const int64_t row = blk * WAVES + wid;
+    if (row >= p.rows) return;
+    const int lane = lane_id();
+    const int sub = lane / LPR, li = lane % LPR;
+    const int n = (int)(row % p.N);
+    const int64_t bh = row / p.N;
+    const int h = (int)(bh % p.Hq);
+    const int b = (int)(bh / p.Hq);
+    const int g = h / p.rep;
+    const T *qrow = (const T *)p.q + b * p.qsb + h * p.qsh + (int64_t)n * p.qsn;
+    const bool live = li * VEC < p.d;
+    const LongRow<T, VEC, LPR> R{p, row, (const T *)p.k + b * p.ksb + g * p.ksh,
+                                 (const T *)p.v + b * p.vsb + g * p.vsh,
+                                 p.nb ? p.nb + row * p.K : nullptr,
+                                 p.valid ? p.valid + row * p.K : nullptr, live ? li * VEC : 0};
+    if (p.row_inv) {
+        int ninv = 0;
+        for (int j0 = 0; j0 < p.K; j0 += SSA_WAVE) {
+            bool mk = false;
+            if (j0 + lane < p.K) (void)R.id(j0 + lane, &mk);
+            ninv += __popcll(wave_ballot(mk));
+        }
+        if (lane == 0) p.row_inv[row] = ninv;
+    }
+    float qf[VEC];
+    load_vec<T, VEC>(qrow + R.lofs, qf);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) qf[e] = live ? qf[e] : 0.f;
+    float m = -INFINITY, l = 0.f;
+    for (int j0 = 0; j0 < p.K; j0 += RPI) {
+        const int j = j0 + sub;
+        const float sj = R.score(qf, j < p.K ? R.id(j) : -1);
+        if (j < p.K) online_add(sj, m, l);
+    }
+    float mm, ll;
+    online_merge(li == 0, m, l, mm, ll);
+    const float inv = 1.f / ll;
+    float acc[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) acc[e] = 0.f;
+    for (int j0 = 0; j0 < p.K; j0 += RPI) {
+        const int j = j0 + sub;
+        const int x = j < p.K ? R.id(j) : -1;
+        const float sj = R.score(qf, x);
+        float w = expf(sj - mm) * inv;
+        if (!p.fp32w) w = Cvt<T>::round(w);
+        if (p.drop_p > 0.f) {
+            w = (drop_uniform(p.seed, row, j) < p.drop_p) ? 0.f : w * drop_scale_of<T>(p);
+            if (!p.fp32w) w = Cvt<T>::round(w);
+        }
+        w = j < p.K ? w : 0.f;
+        float vf[VEC];
+        load_vec<T, VEC>(R.vb + (int64_t)(x < 0 ? 0 : x) * p.vsn + R.lofs, vf);
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[e] = fmaf(w, vf[e], acc[e]);
+    }
+#pragma unroll
+    for (int o = LPR; o < SSA_WAVE; o <<= 1)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) acc[e] += __shfl_xor(acc[e], o, SSA_WAVE);
+    if (sub == 0 && live) {
+        T *orow = (T *)p.out + b * p.osb + h * p.osh + (int64_t)n * p.osn + li * VEC;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) Cvt<T>::store(orow + e, acc[e]);
+    }
+}
+
 // ---------------------------------------------------------------- 16-bit forward
 // Packed 16-bit arithmetic for bf16 / fp16 models whose attention weights are
 // rounded to the value dtype (fp32_attn_weights off):
@@ -660,6 +794,127 @@ apply_bwd_kernel(ApplyP p) {
     }
 }
 
+// Backward of rows beyond LDS: the softmax statistics online, then
+// sum p dp, then each slot's draw and p' (the arithmetic of apply_bwd_kernel,
+// with the scores and dout . v computed again in each pass).
+template <typename T, int D, bool DET>
+__global__ void __launch_bounds__(WAVES * SSA_WAVE)
+apply_bwd_long_kernel(ApplyP p) {
+    using G = Geo<T, D>;
+    constexpr int VEC = G::VEC, LPR = G::LPR, RPI = G::RPI;
+    const int64_t blk = xcd_logical_block(blockIdx.x, p.nblocks);
+    if (blk >= p.nblocks) return;
+    const int wid = threadIdx.x / SSA_WAVE;
+    const int64_t row = blk * WAVES + wid;
+    if (row >= p.rows) return;
+    const int lane = lane_id();
+    const int sub = lane / LPR, li = lane % LPR;
+    const int n = (int)(row % p.N);
+    const int64_t bh = row / p.N;
+    const int h = (int)(bh % p.Hq);
+    const int b = (int)(bh / p.Hq);
+    const int g = h / p.rep;
+    const T *qrow = (const T *)p.q + b * p.qsb + h * p.qsh + (int64_t)n * p.qsn;
+    const bool live = li * VEC < p.d;
+    const LongRow<T, VEC, LPR> R{p, row, (const T *)p.k + b * p.ksb + g * p.ksh,
+                                 (const T *)p.v + b * p.vsb + g * p.vsh, p.nb + row * p.K,
+                                 p.valid ? p.valid + row * p.K : nullptr, live ? li * VEC : 0};
+    const float *dorow = p.dout + row * p.d + R.lofs;
+    float qf[VEC], dof[VEC];
+    load_vec<T, VEC>(qrow + R.lofs, qf);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+        dof[e] = live ? dorow[e] : 0.f;
+        qf[e] = live ? qf[e] : 0.f;
+    }
+    if (DET) {
+        float qm = 0.f, dm = 0.f;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+            qm = fmaxf(qm, fabsf(qf[e]));
+            dm = fmaxf(dm, fabsf(dof[e]));
+        }
+        qm = wave_max(qm);
+        dm = wave_max(dm);
+        if (lane == 0) {
+            atomicMax(&p.gmax[0], __float_as_uint(qm));
+            atomicMax(&p.gmax[1], __float_as_uint(dm));
+        }
+    }
+    // the ids are read from the graph in each pass (the graph's validity and
+    // range rules of the forward; the backward takes int64 ids only)
+    float m = -INFINITY, l = 0.f;
+    for (int j0 = 0; j0 < p.K; j0 += RPI) {
+        const int j = j0 + sub;
+        const float sj = R.score(qf, j < p.K ? R.id(j) : -1);
+        if (j < p.K) online_add(sj, m, l);
+    }
+    float mm, ll;
+    online_merge(li == 0, m, l, mm, ll);
+    auto mask_of = [&](int j) {
+        return p.drop_p > 0.f ? ((drop_uniform(p.seed, row, j) < p.drop_p) ? 0.f : drop_scale_of<T>(p))
+                              : 1.f;
+    };
+    float pdp = 0.f;
+    for (int j0 = 0; j0 < p.K; j0 += RPI) {
+        const int j = j0 + sub;
+        const int x = j < p.K ? R.id(j) : -1;
+        const float pj = expf(R.score(qf, x) - mm) / ll;
+        const float dpj = R.dotv(dof, x) * mask_of(j);
+        if (j < p.K && li == 0) pdp += pj * dpj;
+    }
+    pdp = wave_sum(pdp);
+    float dqa[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) dqa[e] = 0.f;
+    for (int j0 = 0; j0 < p.K; j0 += RPI) {
+        const int j = j0 + sub;
+        if (j >= p.K) continue;
+        const int64_t xr = R.nb[j];
+        if (xr < 0 || xr >= p.M) {
+            if (DET && li == 0) { p.wdraw[row * p.K + j] = 0.f; p.wpw[row * p.K + j] = 0.f; }
+            continue;
+        }
+        const int x = R.id(j);
+        const float pj = expf(R.score(qf, x) - mm) / ll;
+        const float mask = mask_of(j);
+        const float draw = pj * (R.dotv(dof, x) * mask - pdp) * p.scale;
+        const float pw = pj * mask;
+        float kf[VEC];
+        load_vec<T, VEC>(R.kb + xr * p.ksn + R.lofs, kf);
+        const int64_t kr = ((int64_t)b * p.Hkv + g) * p.M + xr;
+        if (DET) {
+            if (li == 0) {
+                p.wdraw[row * p.K + j] = draw;
+                p.wpw[row * p.K + j] = pw;
+                atomicAdd(&p.kcnt[kr], 1u);
+                atomicMax(&p.kmaxd[kr], __float_as_uint(fabsf(draw)));
+                atomicMax(&p.kmaxp[kr], __float_as_uint(fabsf(pw)));
+            }
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) dqa[e] = fmaf(draw, kf[e], dqa[e]);
+        } else {
+            float *dkr = p.dk + kr * p.d + R.lofs;
+            float *dvr = p.dv + kr * p.d + R.lofs;
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) {
+                dqa[e] = fmaf(draw, kf[e], dqa[e]);
+                if (live && draw != 0.f) unsafeAtomicAdd(dkr + e, draw * qf[e]);
+                if (live && pw != 0.f) unsafeAtomicAdd(dvr + e, pw * dof[e]);
+            }
+        }
+    }
+#pragma unroll
+    for (int o = LPR; o < SSA_WAVE; o <<= 1)
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) dqa[e] += __shfl_xor(dqa[e], o, SSA_WAVE);
+    if (sub == 0 && live) {
+        float *dqr = p.dq + row * p.d + R.lofs;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) dqr[e] = dqa[e];
+    }
+}
+
 // ---- deterministic backward: fixed-point sums
 // A key row's gradient is a sum over the (query row, slot) pairs that hold it.
 // Its terms are rounded to a fixed-point grid of that key row and summed as
@@ -772,14 +1027,33 @@ bool fwd16_ok(const ApplyP &p, int elem, int D) {
 template <typename T, int D>
 int launch_apply(const ApplyP &p, hipStream_t st, bool bwd) {
     const int64_t grid = 8 * ceil_div(p.nblocks, 8);
+    const bool lng = p.K > APPLY_KLDS;
+    if (lng && !bwd) {
+        hipLaunchKernelGGL((apply_fwd_long_kernel<T, D>), dim3((unsigned)grid),
+                           dim3(WAVES * SSA_WAVE), 0, st, p);
+        SSA_CHECK_LAUNCH();
+        return SSA_OK;
+    }
+    if (lng && !p.wdraw) {
+        hipLaunchKernelGGL((apply_bwd_long_kernel<T, D, false>), dim3((unsigned)grid),
+                           dim3(WAVES * SSA_WAVE), 0, st, p);
+        SSA_CHECK_LAUNCH();
+        return SSA_OK;
+    }
     if (bwd && p.wdraw) {
         // deterministic: rows (dq, weights, bounds), fixed-point sums, finish
-        const size_t lds = (size_t)WAVES * 2 * p.K * sizeof(float);
-        if (lds > 65536)
-            SSA_CHECK_HIP(hipFuncSetAttribute((const void *)apply_bwd_kernel<T, D, true>,
-                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        hipLaunchKernelGGL((apply_bwd_kernel<T, D, true>), dim3((unsigned)grid),
-                           dim3(WAVES * SSA_WAVE), lds, st, p);
+        if (lng) {
+            hipLaunchKernelGGL((apply_bwd_long_kernel<T, D, true>), dim3((unsigned)grid),
+                               dim3(WAVES * SSA_WAVE), 0, st, p);
+        } else {
+            const size_t lds = (size_t)WAVES * 2 * p.K * sizeof(float);
+            if (lds > 65536)
+                SSA_CHECK_HIP(hipFuncSetAttribute((const void *)apply_bwd_kernel<T, D, true>,
+                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                  (int)lds));
+            hipLaunchKernelGGL((apply_bwd_kernel<T, D, true>), dim3((unsigned)grid),
+                               dim3(WAVES * SSA_WAVE), lds, st, p);
+        }
         SSA_CHECK_LAUNCH();
         hipLaunchKernelGGL((apply_bwd_fx_kernel<T, D>), dim3((unsigned)grid),
                            dim3(WAVES * SSA_WAVE), 0, st, p);
@@ -856,7 +1130,8 @@ int apply_common(const ssa_apply_args *a, ApplyP &p) {
                   "sparse_gather_attention: bad sizes B=%d Hq=%d Hkv=%d N=%d M=%d K=%d", a->B,
                   a->Hq, a->Hkv, a->N, a->M, a->K);
     SSA_CHECK_ARG(a->Hq % a->Hkv == 0, "sparse_gather_attention: Hq %% Hkv != 0");
-    SSA_CHECK_ARG(a->K <= 4096, "sparse_gather_attention: K=%d above 4096", a->K);
+    SSA_CHECK_ARG((int64_t)a->B * a->Hq * a->N * a->K < ((int64_t)1 << 62),
+                  "sparse_gather_attention: too many slots");
     SSA_CHECK_ARG(a->q.dtype >= 0 && a->q.dtype <= 2, "sparse_gather_attention: bad dtype");
     int rc;
     if ((rc = check_view(a->q, a->q.dtype, "q"))) return rc;
