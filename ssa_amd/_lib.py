@@ -210,9 +210,8 @@ def _ptr(t):
 
 
 # --------------------------------------------------------------------------- graph build
-# largest key length and number of global tokens ssa_build_graph accepts
+# largest key length ssa_build_graph accepts
 MAX_KEYS = 32768
-MAX_GLOBALS = 63
 
 
 def _graph_args(q, k, rand_proj, *, P, T, C, top_k, window, causal, is_cross, total_k, glob,
@@ -242,9 +241,8 @@ def _graph_args(q, k, rand_proj, *, P, T, C, top_k, window, causal, is_cross, to
     if not 1 <= M <= MAX_KEYS:
         raise RuntimeError(f"ssa_amd.build_graph: key length {M} unsupported (1..{MAX_KEYS}: the "
                            "bucket sort keeps a row's keys in LDS and key ids are packed in 16 bits)")
-    if glob.numel() > MAX_GLOBALS:
-        raise RuntimeError(f"ssa_amd.build_graph: {glob.numel()} global tokens unsupported "
-                           f"(0..{MAX_GLOBALS}: one wavefront holds them)")
+    if glob.numel() > M:
+        raise RuntimeError(f"ssa_amd.build_graph: {glob.numel()} global tokens for {M} keys")
     require_device(q, k, rand_proj, glob)
     if q.dtype != k.dtype:
         raise RuntimeError("ssa_amd.build_graph: q and k dtypes differ")

@@ -1910,7 +1910,9 @@ select_kernel(SelP p) {
     const float qsc = arow[p.NA - 1];          // the query's code scale
     const uint32_t kself = CAUSAL ? score_key(arow[0]) : 0u;
     const uint32_t cself = CAUSAL ? score_code(arow[0], qsc) : 0u;
-    const int ng = min(p.G + 1, SSA_WAVE);
+    // the empty-bucket list glob ++ 0: its first nge entries (the rest are
+    // further zeros, never first occurrences), 64 at a time
+    const int nge = min(p.G + 1, p.C);
     for (int w = lane; w < p.words; w += SSA_WAVE) bm[w] = 0u;
 
     // ---- per-list chunk data of the sorted prefixes, one lane per list
@@ -1948,14 +1950,22 @@ select_kernel(SelP p) {
         }
     }
     nch = __builtin_amdgcn_readfirstlane(nch);
-    // glob ++ 0 (:711-737): ids and score keys, lane j holding entry j
-    int greg_id = 0;
-    uint32_t greg_sc = 0u, greg_c = 0u;
-    if (any_empty && lane < ng) {
-        greg_sc = score_key(arow[1 + lane]);
-        greg_c = score_code(arow[1 + lane], qsc);
-        greg_id = lane < p.G ? (int)p.glob[lane] : 0;
-    }
+    // glob ++ 0 (:711-737), entries c0 .. c0 + 63: lane j's id, code and key
+    // (its score from the aux row: glob scores, then key 0's)
+    auto glob_entry = [&](int c0, int &id, uint32_t &code, uint32_t &key) {
+        const int c = c0 + lane;
+        id = 0; code = 0u; key = 0u;
+        if (c < nge) {
+            key = score_key(arow[1 + c]);
+            code = score_code(arow[1 + c], qsc);
+            id = c < p.G ? (int)p.glob[c] : 0;
+        }
+        uint64_t Min = wave_ballot(c < nge);
+        if (CAUSAL) Min &= ~wave_ballot(c < nge && id == n);   // the query's own key is settled
+        return Min;
+    };
+    // glob slots 1 .. nge; the chunks' stream slots follow
+    const int slot0 = 1 + SSA_WAVE * (int)((nge + SSA_WAVE - 1) / SSA_WAVE);
     wave_lds_sync();
 
     // ---- overflow fillers: list L (0 < size < C) holds its round's filler key
@@ -2040,9 +2050,12 @@ select_kernel(SelP p) {
         cnt = 1;
     }
     if (any_empty) {                   // glob ++ 0; the query's own key is settled
-        uint64_t Min = lanes_mask(min(p.C, ng));
-        if (CAUSAL) Min &= ~wave_ballot(greg_id == n);
-        sel_absorb<CAP>(bm, ckey, cval, Min, greg_id, greg_c << 16, lo, cnt, nkept);
+        for (int c0 = 0; c0 < nge; c0 += SSA_WAVE) {
+            int gid;
+            uint32_t gc, gk;
+            const uint64_t Min = glob_entry(c0, gid, gc, gk);
+            sel_absorb<CAP>(bm, ckey, cval, Min, gid, gc << 16, lo, cnt, nkept);
+        }
     }
     // Chunks are processed PIPE at a time; the loads of the next group are
     // issued before the current group is deduplicated, so a wave always has
@@ -2190,9 +2203,12 @@ select_kernel(SelP p) {
             fn(in_mask(Min) && !(old & bit), kv, v, slot);
         };
         if (any_empty) {
-            uint64_t Min = lanes_mask(min(p.C, ng));
-            if (CAUSAL) Min &= ~wave_ballot(greg_id == n);
-            walk_chunk(Min, greg_id, kv_of(greg_c, greg_sc), 1 + lane);
+            for (int c0 = 0; c0 < nge; c0 += SSA_WAVE) {
+                int gid;
+                uint32_t gc, gk;
+                const uint64_t Min = glob_entry(c0, gid, gc, gk);
+                walk_chunk(Min, gid, kv_of(gc, gk), 1 + c0 + lane);
+            }
         }
         int4 dw = make_int4(0, 0, 0, 0);
         for (int ci = 0; ci < nch; ++ci) {
@@ -2210,7 +2226,7 @@ select_kernel(SelP p) {
             const bool xw = in_mask(Min) && (xm == 3 || (xm != 0 && c == pfx));
             uint32_t x = 0u;
             if (wave_ballot(xw) != 0ull) x = exact(v, xw);
-            walk_chunk(Min, v, kv_of(c, x), 65 + ci * SSA_WAVE + lane);
+            walk_chunk(Min, v, kv_of(c, x), slot0 + ci * SSA_WAVE + lane);
         }
     };
     // kk2-th largest key of the kept stream as walk mode xm gives it, over bits
@@ -2398,7 +2414,7 @@ constexpr int RP_STACK = 64;
 // 2^16, or positions), TL/TR (two 16-bit lists), leaf bits, stack, bitmap,
 // glob scores
 __host__ __device__ inline int rp_lds_words(int W, int words) {
-    return (W + (W + 1) / 2 + W + (W + 31) / 32 + 1 + 3 * RP_STACK + words + 64 + 1) & ~1;
+    return (W + (W + 1) / 2 + W + (W + 31) / 32 + 1 + 3 * RP_STACK + words + 1) & ~1;
 }
 
 __device__ __forceinline__ void rp_sync() {
@@ -2646,7 +2662,6 @@ topk_replay_kernel(SelP p, int chunk, int W, uint32_t *gscr, int skip_max) {
     uint32_t *lbits = base + 2 * W + (W + 1) / 2;
     int32_t *stk = (int32_t *)(lbits + (W + 31) / 32 + 1);
     uint32_t *bm = (uint32_t *)(stk + 3 * RP_STACK);
-    uint32_t *gsc = bm + p.words;
 
     const int total = (int)gridDim.x * RP_WAVES;
     const int cnt = *p.tie_count;
@@ -2664,12 +2679,8 @@ topk_replay_kernel(SelP p, int chunk, int W, uint32_t *gscr, int skip_max) {
         // the scores the candidate lists do not carry, with the rescore's
         // arithmetic (as the aux kernel computes them): the query's own key,
         // and glob ++ 0 for an empty bucket (lane j: entry j)
-        const int ng = min(p.G + 1, SSA_WAVE);
         const uint32_t kq = exact_keys<T>(p, qr, kb, n, p.causal && lane == 0);
         const uint32_t kself = (uint32_t)__builtin_amdgcn_readfirstlane((int)kq);
-        const int gv = lane < p.G ? (int)p.glob[lane < p.G ? lane : 0] : 0;
-        const uint32_t gk = exact_keys<T>(p, qr, kb, gv, lane < ng);
-        if (lane < ng) gsc[lane] = gk;
         for (int w = lane; w < p.words; w += SSA_WAVE) bm[w] = 0u;
         for (int t = lane; t < kk; t += SSA_WAVE) { A.key[t] = RP_NEGINF; A.cand[t] = 0; }
         const uint16_t *qids = p.qid + row * p.R * p.NS;
@@ -2721,7 +2732,6 @@ topk_replay_kernel(SelP p, int chunk, int W, uint32_t *gscr, int skip_max) {
                     if (keep) sk = xk ? ex : kself;
                 } else {
                     // empty bucket: glob ++ 0, all valid; duplicates resolved in slot order
-                    const int jg = c < ng - 1 ? c : ng - 1;
                     v = (c < p.G) ? (int)p.glob[c < p.G ? c : 0] : 0;
                     bool pending = in;
                     uint64_t pm = wave_ballot(pending);
@@ -2737,7 +2747,10 @@ topk_replay_kernel(SelP p, int chunk, int W, uint32_t *gscr, int skip_max) {
                         pending = pending && !same;
                         pm = wave_ballot(pending);
                     }
-                    if (keep) sk = gsc[jg];
+                    // the glob entries' keys with the exact-key arithmetic
+                    // (the query's own key included), as the aux rows hold them
+                    const uint32_t ex = exact_keys<T>(p, qr, kb, v, keep);
+                    if (keep) sk = ex;
                 }
                 if (in) {
                     const int at = kk + (int)(j0 - s0) + lane;
@@ -2822,7 +2835,7 @@ __host__ __device__ inline int rpw_slot_words(int W) {
 // merge output, per chunk (head length, tie count, tied keys, input state,
 // marked list), misc, keep bits, the maps (u16)
 __host__ __device__ inline int rpw_shared_words(int words, int nls, int kk, int nch, int64_t Call) {
-    return (int)((words + SSA_WAVE + 2 * nls + kk + 2 * (kk + 1) + (int64_t)nch * (4 + RPW_TV) + 8 +
+    return (int)((words + 2 * nls + kk + 2 * (kk + 1) + (int64_t)nch * (4 + RPW_TV) + 8 +
                   (Call + 31) / 32 + ((int64_t)nch * kk + 1) / 2 + 1) & ~1);
 }
 // workspace words of one block: stream keys and ids, first occurrences, the
@@ -2904,8 +2917,7 @@ topk_replay_wg_kernel(SelP p, int chunk, int W, int nsim, uint32_t *gscr, int64_
     uint32_t *slot = rp_smem + (int64_t)(wid < nsim ? wid : 0) * sw;
     uint32_t *sh = rp_smem + (int64_t)nsim * sw;
     uint32_t *bm = sh;
-    uint32_t *gsc = bm + p.words;
-    int32_t *lst = (int32_t *)(gsc + SSA_WAVE);
+    int32_t *lst = (int32_t *)(bm + p.words);
     int32_t *lsz = lst + nls;
     uint32_t *Sk = (uint32_t *)(lsz + nls);
     uint32_t *Sn = Sk + kk;
@@ -2937,7 +2949,6 @@ topk_replay_wg_kernel(SelP p, int chunk, int W, int nsim, uint32_t *gscr, int64_
         const int bk = b * p.Hkv + gq;
         const T *qr = (const T *)p.q + b * p.qsb + h * p.qsh + (int64_t)n * p.qsn;
         const T *kb = (const T *)p.k + b * p.ksb + gq * p.ksh;
-        const int ng = min(p.G + 1, SSA_WAVE);
         const uint16_t *qids = p.qid + row * p.R * p.NS;
         for (int l = threadIdx.x; l < nls; l += RPW_THREADS) {
             const int u = qids[l];
@@ -2951,9 +2962,6 @@ topk_replay_wg_kernel(SelP p, int chunk, int W, int nsim, uint32_t *gscr, int64_
             // (as the aux kernel computes them): the query's own key, and
             // glob ++ 0 for an empty bucket (lane j: entry j)
             const uint32_t kq = exact_keys<T>(p, qr, kb, n, p.causal && lane == 0);
-            const int gv = lane < p.G ? (int)p.glob[lane < p.G ? lane : 0] : 0;
-            const uint32_t gk = exact_keys<T>(p, qr, kb, gv, lane < ng);
-            if (lane < ng) gsc[lane] = gk;
             if (lane == 0) misc[0] = (int)kq;
         }
         __syncthreads();
@@ -3073,11 +3081,12 @@ topk_replay_wg_kernel(SelP p, int chunk, int W, int nsim, uint32_t *gscr, int64_
                     const int64_t j = s0 + (in ? (int)Et[t] - kk : 0);
                     const int list = (int)(j / p.C);
                     const bool empty = lsz[list] == 0;
-                    const bool xk = in && !empty && !(p.causal && v == n);
+                    // glob ++ 0 entries (empty buckets) take the exact-key
+                    // arithmetic even for the query's own key, as the aux rows do
+                    const bool xk = in && (empty || !(p.causal && v == n));
                     const uint32_t ex = exact_keys_wide<T, 4>(p, qr, kb, v, xk);
                     if (in) {
-                        const int cl = (int)(j - (int64_t)list * p.C);
-                        const uint32_t key = ~(empty ? gsc[cl < ng - 1 ? cl : ng - 1] : (xk ? ex : kself));
+                        const uint32_t key = ~(xk ? ex : kself);
                         Ek[t] = key;
                         skey[j] = key;
                     }
@@ -3423,7 +3432,7 @@ int make_dims(const ssa_graph_args *a, Dims &D, bool need_q = true, int64_t ws_c
     SSA_CHECK_ARG(a->P >= 1 && a->P <= 12 && a->P <= a->max_p, "build_graph: P=%d", a->P);
     SSA_CHECK_ARG(a->R >= 1 && a->C >= 1 && a->top_k >= 1 && a->T >= 0, "build_graph: R/C/top_k/T");
     SSA_CHECK_ARG(a->C <= (1 << 24), "build_graph: C=%d above 2^24", a->C);
-    SSA_CHECK_ARG(a->G >= 0 && a->G <= 63, "build_graph: G=%d outside 0..63", a->G);
+    SSA_CHECK_ARG(a->G >= 0 && a->G <= a->M, "build_graph: G=%d outside 0..M (%d)", a->G, a->M);
     SSA_CHECK_ARG(a->rand_proj || (a->q_proj && a->k_proj), "build_graph: no hyperplanes");
     SSA_CHECK_ARG((a->q.ptr || !need_q) && a->k.ptr, "build_graph: null q/k");
     SSA_CHECK_ARG(a->q.dtype == a->k.dtype && a->q.dtype >= 0 && a->q.dtype <= 2,

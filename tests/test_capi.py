@@ -105,7 +105,7 @@ def test_argument_errors_are_reported_without_a_gpu():
 # rows share a workgroup's 160 KiB of LDS (minus 512 bytes of static data).
 def _replay_words(W, M):
     words = ((M + 31) // 32 + 1) & ~1
-    return (W + (W + 1) // 2 + W + (W + 31) // 32 + 1 + 3 * 64 + words + 64 + 1) & ~1
+    return (W + (W + 1) // 2 + W + (W + 31) // 32 + 1 + 3 * 64 + words + 1) & ~1
 
 
 def _replay_fits(W, M):
@@ -241,14 +241,21 @@ def test_key_length_beyond_the_sort_is_refused(M):
                          causal=False, is_cross=True, total_k=64, glob=torch.zeros(2))
 
 
-def test_globals_beyond_a_wavefront_are_refused():
+def test_any_number_of_globals_up_to_the_key_count():
+    """Global tokens beyond a wavefront are taken (the empty-bucket list is
+    walked 64 entries at a time); more globals than keys are refused by the
+    library and by the Python wrapper."""
     import torch
 
     from ssa_amd import _lib
-    a, _ = _full_args(1024, 128, G=64)
+    for G in (64, 300, 1024):
+        a, _ = _full_args(1024, 2000, G=G)
+        assert _lib.lib().ssa_graph_workspace_bytes(ctypes.byref(a)) > 0, \
+            _lib.lib().ssa_last_error()
+    a, _ = _full_args(1024, 2000, G=1025)
     assert _lib.lib().ssa_graph_workspace_bytes(ctypes.byref(a)) < 0
-    assert b"G=64" in _lib.lib().ssa_last_error()
+    assert b"G=1025" in _lib.lib().ssa_last_error()
     with pytest.raises(RuntimeError, match="global tokens"):
         _lib.build_graph(torch.zeros(1, 1, 8, 16), torch.zeros(1, 1, 8, 16), torch.zeros(2, 12, 16),
                          P=1, T=0, C=64, top_k=32, window=4, causal=False, is_cross=False,
-                         total_k=64, glob=torch.zeros(64))
+                         total_k=64, glob=torch.zeros(9))

@@ -83,6 +83,11 @@ GRAPH_CASES = [
     # the smallest and the largest matrix-core rescore instances
     ("head_dim_8", 1, 2, 2, 80, 80, 8, 2, 3, 0, 16, 2, 1, True, False),
     ("head_dim_128", 1, 2, 1, 256, 256, 128, 2, 4, 1, 32, 4, 2, True, False),
+    # more global tokens than a wavefront holds: the empty-bucket list glob ++ 0
+    # taken 64 entries at a time (101 of them, and 100 explicit ones over C=112)
+    ("many_globals", 1, 2, 2, 256, 256, 16, 3, 4, 1, 160, 4, 100, True, False),
+    ("many_globals_cross", 1, 2, 1, 80, 300, 16, 2, 4, 1, 128, 4, list(range(0, 300, 3)),
+     False, True),
 ]
 
 
