@@ -211,7 +211,7 @@ def _ptr(t):
 
 # --------------------------------------------------------------------------- graph build
 # largest key length ssa_build_graph accepts
-MAX_KEYS = 32768
+MAX_KEYS = 65536
 
 
 def _graph_args(q, k, rand_proj, *, P, T, C, top_k, window, causal, is_cross, total_k, glob,
@@ -239,8 +239,8 @@ def _graph_args(q, k, rand_proj, *, P, T, C, top_k, window, causal, is_cross, to
         raise RuntimeError(f"ssa_amd.build_graph: k_proj {tuple(k_proj.shape)} is not "
                            f"{(B * Hkv, R, M, P)}")
     if not 1 <= M <= MAX_KEYS:
-        raise RuntimeError(f"ssa_amd.build_graph: key length {M} unsupported (1..{MAX_KEYS}: the "
-                           "bucket sort keeps a row's keys in LDS and key ids are packed in 16 bits)")
+        raise RuntimeError(f"ssa_amd.build_graph: key length {M} unsupported (1..{MAX_KEYS}: key "
+                           "ids, bucket starts and list positions travel in 16-bit fields)")
     if glob.numel() > M:
         raise RuntimeError(f"ssa_amd.build_graph: {glob.numel()} global tokens for {M} keys")
     require_device(q, k, rand_proj, glob)

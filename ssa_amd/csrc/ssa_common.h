@@ -154,7 +154,8 @@ __device__ __forceinline__ int lanes_below(uint64_t m) {
 // candidates at once and keeps the range between the last true and the first
 // false, so the answer takes one or two rounds of parallel LDS reads.  Every
 // lane must be active; the result is wave-uniform.
-__device__ __forceinline__ int hoare_swap_count(const uint16_t *TL, const uint16_t *TR, int f,
+template <typename Pos>
+__device__ __forceinline__ int hoare_swap_count(const Pos *TL, const Pos *TR, int f,
                                                 int numL, int numR) {
     const int lane = (int)__lane_id();
     int lo = 0, hi = numL < numR ? numL : numR;     // the answer lies in [lo, hi]

@@ -1220,8 +1220,12 @@ __global__ void __launch_bounds__(256) cut_kernel(CutP p) {
             cutoff = nv;
         }
     }
-    p.cut[x] = make_int4((int)(prow * p.M) + st, sz | (f << 16), cutoff | (st << 16),
-                         first * 2 + real);
+    // 16-bit fields, read back as unsigned: the list size capped at C (every
+    // use compares it with 0 and C or takes min(size, C)), the filler key and
+    // the cutoff below 2^16, the bucket start below M <= 65536
+    p.cut[x] = make_int4((int)(prow * p.M) + st,
+                         (int)((uint32_t)min(sz, p.C) | ((uint32_t)f << 16)),
+                         (int)((uint32_t)cutoff | ((uint32_t)st << 16)), first * 2 + real);
     const int64_t inst = (rloc / p.N) * p.nlists + list;
     p.srix[x] = (int32_t)(((int64_t)list * p.N + p.qpos[inst * p.N + n]) * p.Cs);
 }
@@ -1928,10 +1932,11 @@ select_kernel(SelP p) {
         const bool in = list < nl;
         const int4 ct = in ? crow[list] : make_int4(0, 0, 0, 0);
         const int so = in ? xrow[list] : 0;
-        const int sz = ct.y & 0xffff, cutoff = ct.z & 0xffff, st = ct.z >> 16;
+        const int sz = ct.y & 0xffff, cutoff = ct.z & 0xffff;
+        const int st = (int)((uint32_t)ct.z >> 16), fk = (int)((uint32_t)ct.y >> 16);
         // a filler that cannot matter (no overflow, or past the query) is -1
-        const bool fl = in && sz > 0 && sz < p.C && (!CAUSAL || (ct.y >> 16) < n);
-        if (in) lst[list] = make_int4(st, sz, ct.x - st, fl ? ct.y >> 16 : -1);
+        const bool fl = in && sz > 0 && sz < p.C && (!CAUSAL || fk < n);
+        if (in) lst[list] = make_int4(st, sz, ct.x - st, fl ? fk : -1);
         any_fill = any_fill || wave_ballot(fl) != 0ull;
         const int nc = (in && sz > 0) ? (cutoff + SSA_WAVE - 1) / SSA_WAVE : 0;
         int ncs;
@@ -3443,8 +3448,12 @@ int make_dims(const ssa_graph_args *a, Dims &D, bool need_q = true, int64_t ws_c
                       "of %d)", a->d, a->q.dtype == SSA_F32 ? 4 : 8);
         return SSA_E_UNSUP;
     }
-    if (!ssa_sort_supported(a->M)) {
-        ssa_set_error("build_graph: key length %d unsupported (1..32768)", a->M);
+    // key ids, bucket starts and in-list positions travel in 16-bit fields
+    // (the cut entries, the tie replay's payload): M <= 65536, and a list's
+    // size (capped at C) below 2^16
+    if (a->M > 65536 || !ssa_sort_supported(a->M) || (a->M == 65536 && a->C >= 65536)) {
+        ssa_set_error("build_graph: key length %d unsupported (1..65536, with C < 65536 at "
+                      "65536)", a->M);
         return SSA_E_UNSUP;
     }
     SSA_CHECK_ARG((int64_t)a->B * a->Hkv * a->R * a->M < ((int64_t)1 << 29),

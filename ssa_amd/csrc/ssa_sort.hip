@@ -24,7 +24,14 @@
 //     Because every partition leaves max(left) <= min(right), that final pass
 //     equals a stable insertion sort inside each leaf, done one leaf per thread.
 // The bucket start/size tables come from binary searches on the sorted keys.
+//
+// Rows of up to 32768 keys keep keys and 16-bit positions in LDS.  Longer rows
+// (up to SORT_MAX_KEYS) run the same program with 32-bit positions and the
+// row's keys, positions and stopper lists in the workspace (the top levels'
+// memory traffic then goes to the L2 / HBM instead of LDS); kernel B's
+// segments stay in LDS either way.
 #include <algorithm>
+#include <type_traits>
 
 #include "ssa_common.h"
 #include "ssa_graph_internal.h"
@@ -47,8 +54,9 @@ __device__ __forceinline__ void wave_sync_lds() {
 __device__ __forceinline__ int floor_log2_i(int n) { return 31 - __clz(n); }
 
 // ---- heap sort of [f, l) by key, one lane (rare: only at the depth limit)
-__device__ void heap_push_up(uint16_t *key, uint16_t *idx, int base, int hole, int top,
-                             uint16_t vk, uint16_t vi) {
+template <typename Pos>
+__device__ void heap_push_up(uint16_t *key, Pos *idx, int base, int hole, int top,
+                             uint16_t vk, Pos vi) {
     int parent = (hole - 1) / 2;
     while (hole > top && key[base + parent] < vk) {
         key[base + hole] = key[base + parent];
@@ -60,8 +68,9 @@ __device__ void heap_push_up(uint16_t *key, uint16_t *idx, int base, int hole, i
     idx[base + hole] = vi;
 }
 
-__device__ void heap_adjust(uint16_t *key, uint16_t *idx, int base, int hole, int len,
-                            uint16_t vk, uint16_t vi) {
+template <typename Pos>
+__device__ void heap_adjust(uint16_t *key, Pos *idx, int base, int hole, int len,
+                            uint16_t vk, Pos vi) {
     const int top = hole;
     int child = hole;
     while (child < (len - 1) / 2) {
@@ -80,7 +89,8 @@ __device__ void heap_adjust(uint16_t *key, uint16_t *idx, int base, int hole, in
     heap_push_up(key, idx, base, hole, top, vk, vi);
 }
 
-__device__ void heap_sort_range(uint16_t *key, uint16_t *idx, int f, int l) {
+template <typename Pos>
+__device__ void heap_sort_range(uint16_t *key, Pos *idx, int f, int l) {
     const int len = l - f;
     if (len < 2) return;
     for (int parent = (len - 2) / 2;; --parent) {
@@ -88,7 +98,8 @@ __device__ void heap_sort_range(uint16_t *key, uint16_t *idx, int f, int l) {
         if (parent == 0) break;
     }
     for (int last = len - 1; last > 0; --last) {
-        const uint16_t vk = key[f + last], vi = idx[f + last];
+        const uint16_t vk = key[f + last];
+        const Pos vi = idx[f + last];
         key[f + last] = key[f];
         idx[f + last] = idx[f];
         heap_adjust(key, idx, f, 0, last, vk, vi);
@@ -96,8 +107,8 @@ __device__ void heap_sort_range(uint16_t *key, uint16_t *idx, int f, int l) {
 }
 
 // ---- one wavefront partitions [f, l); returns the cut
-__device__ int wave_partition(uint16_t *key, uint16_t *idx, uint16_t *TL, uint16_t *TR, int f,
-                              int l) {
+template <typename Pos>
+__device__ int wave_partition(uint16_t *key, Pos *idx, Pos *TL, Pos *TR, int f, int l) {
     const int lane = lane_id();
     const int n = l - f;
     const int a = f + 1, b = f + n / 2, c = l - 1;
@@ -111,7 +122,8 @@ __device__ int wave_partition(uint16_t *key, uint16_t *idx, uint16_t *TL, uint16
     else if (kb < kc) { x = c; p = kc; }
     else { x = b; p = kb; }
     if (lane == 0) {
-        const uint16_t tk = key[f], ti = idx[f];
+        const uint16_t tk = key[f];
+        const Pos ti = idx[f];
         key[f] = key[x]; idx[f] = idx[x];
         key[x] = tk; idx[x] = ti;
     }
@@ -125,8 +137,8 @@ __device__ int wave_partition(uint16_t *key, uint16_t *idx, uint16_t *TL, uint16
         const bool isL = in && i > f && kv >= p;
         const bool isR = in && kv <= p;
         const uint64_t bL = wave_ballot(isL), bR = wave_ballot(isR);
-        if (isL) TL[f + numL + lanes_below(bL)] = (uint16_t)i;
-        if (isR) TR[f + numR + lanes_below(bR)] = (uint16_t)i;
+        if (isL) TL[f + numL + lanes_below(bL)] = (Pos)i;
+        if (isR) TR[f + numR + lanes_below(bR)] = (Pos)i;
         numL += __popcll(bL);
         numR += __popcll(bR);
     }
@@ -138,7 +150,8 @@ __device__ int wave_partition(uint16_t *key, uint16_t *idx, uint16_t *TL, uint16
         const int k = k0 + lane;
         if (k < s) {
             const int pa = TL[f + k], pb = TR[f + numR - 1 - k];
-            const uint16_t tk = key[pa], ti = idx[pa];
+            const uint16_t tk = key[pa];
+            const Pos ti = idx[pa];
             key[pa] = key[pb]; idx[pa] = idx[pb];
             key[pb] = tk; idx[pb] = ti;
         }
@@ -176,7 +189,8 @@ __device__ __forceinline__ int nth_set_bit64(uint64_t m, int k) {
 // top), every lane finds its swap partner with one shuffle, and the cut is
 // read from lane s.  Pending segments are bits of a mask (segment starts), so
 // the order in which independent segments are split does not matter.
-__device__ void wave_small_sort(uint16_t *key, uint16_t *idx, uint32_t *bits, int f, int n,
+template <typename Pos>
+__device__ void wave_small_sort(uint16_t *key, Pos *idx, uint32_t *bits, int f, int n,
                                 int depth0) {
     const int lane = lane_id();
     int kv = lane < n ? (int)key[f + lane] : 0;
@@ -191,7 +205,7 @@ __device__ void wave_small_sort(uint16_t *key, uint16_t *idx, uint32_t *bits, in
         const int b = above ? __ffsll((long long)above) - 1 : n;
         const int d = __builtin_amdgcn_readlane(dep, a);
         if (d == 0) {                          // depth limit: heap sort through LDS
-            if (lane < n) { key[f + lane] = (uint16_t)kv; idx[f + lane] = (uint16_t)xv; }
+            if (lane < n) { key[f + lane] = (uint16_t)kv; idx[f + lane] = (Pos)xv; }
             wave_sync_lds();
             if (lane == 0) heap_sort_range(key, idx, f + a, f + b);
             wave_sync_lds();
@@ -242,7 +256,7 @@ __device__ void wave_small_sort(uint16_t *key, uint16_t *idx, uint32_t *bits, in
         if (c - a > LEAF) pend |= 1ull << a;
         if (b - c > LEAF) pend |= 1ull << c;
     }
-    if (lane < n) { key[f + lane] = (uint16_t)kv; idx[f + lane] = (uint16_t)xv; }
+    if (lane < n) { key[f + lane] = (uint16_t)kv; idx[f + lane] = (Pos)xv; }
     wave_sync_lds();
 }
 
@@ -270,9 +284,27 @@ __device__ __forceinline__ void emit_segment(int4 *segs, int *segcount, int row,
     segs[atomicAdd(segcount, 1)] = make_int4(row, f, l - f, depth);
 }
 
+// Pos: uint16_t (rows of up to 32768 keys, the row in LDS) or uint32_t (longer
+// rows: keys, positions and stopper lists in `glb`, per row 2 + 3 * 4 bytes
+// per key).  A segment word holds f | l << (8 * sizeof(Pos)).
+// workspace bytes of one row beyond LDS: positions, stopper lists, keys
+__host__ __device__ inline int64_t sort_glb_row_bytes(int n) {
+    return ((int64_t)n * 14 + 15) / 16 * 16;
+}
+
+template <typename Pos> struct SortWords {
+    using W = typename std::conditional<sizeof(Pos) == 2, uint32_t, uint64_t>::type;
+    static constexpr int SH = 8 * (int)sizeof(Pos);
+};
+
+template <typename Pos>
 __global__ void __launch_bounds__(SORT_THREADS)
 sort_top_kernel(const uint16_t *ids, int n, int NB, int32_t *perm, int32_t *bstart, int32_t *bsize,
-                uint32_t *gkv, int4 *segs, int *segcount, uint16_t *tmp, int tl_in_lds, int cap) {
+                typename SortWords<Pos>::W *gkv, int4 *segs, int *segcount, unsigned char *glb,
+                int tl_in_lds, int cap) {
+    using W = typename SortWords<Pos>::W;
+    constexpr int SH = SortWords<Pos>::SH;
+    constexpr bool GLB = sizeof(Pos) == 4;
     extern __shared__ __align__(16) unsigned char smem_raw[];
     __shared__ TopShared sh;
     const int row = blockIdx.x;
@@ -281,20 +313,32 @@ sort_top_kernel(const uint16_t *ids, int n, int NB, int32_t *perm, int32_t *bsta
     const int lane = lane_id();
     const uint16_t *src = ids + (int64_t)row * n;
 
-    uint16_t *key = (uint16_t *)smem_raw;
-    uint16_t *idx = key + n;
-    int32_t *hist = (int32_t *)(smem_raw + ((size_t)4 * n + 15) / 16 * 16);
-    uint32_t *segA = (uint32_t *)(hist + NB);
-    uint32_t *segB = segA + cap;
+    uint16_t *key;
+    Pos *idx, *TL, *TR;
+    int32_t *hist;
+    if (GLB) {
+        unsigned char *g = glb + (int64_t)row * sort_glb_row_bytes(n);
+        idx = (Pos *)g;
+        TL = idx + n;
+        TR = TL + n;
+        key = (uint16_t *)(TR + n);
+        hist = (int32_t *)smem_raw;
+    } else {
+        key = (uint16_t *)smem_raw;
+        idx = (Pos *)(key + n);
+        hist = (int32_t *)(smem_raw + ((size_t)4 * n + 15) / 16 * 16);
+    }
+    W *segA = (W *)(hist + NB);
+    W *segB = segA + cap;
     uint8_t *depA = (uint8_t *)(segB + cap);
     uint8_t *depB = depA + cap;
-    uint16_t *TL, *TR;
-    if (tl_in_lds) {
-        const size_t off = ((size_t)((unsigned char *)(depB + cap) - smem_raw) + 15) / 16 * 16;
-        TL = (uint16_t *)(smem_raw + off);
-        TR = TL + n;
-    } else {
-        TL = tmp + (int64_t)row * 2 * n;
+    if (!GLB) {
+        if (tl_in_lds) {
+            const size_t off = ((size_t)((unsigned char *)(depB + cap) - smem_raw) + 15) / 16 * 16;
+            TL = (Pos *)(smem_raw + off);
+        } else {
+            TL = (Pos *)glb + (int64_t)row * 2 * n;
+        }
         TR = TL + n;
     }
 
@@ -303,7 +347,7 @@ sort_top_kernel(const uint16_t *ids, int n, int NB, int32_t *perm, int32_t *bsta
     for (int i = tid; i < n; i += SORT_THREADS) {
         const uint16_t k = src[i];
         key[i] = k;
-        idx[i] = (uint16_t)i;
+        idx[i] = (Pos)i;
         if (k < NB) atomicAdd(&hist[k], 1);
     }
     const int depth0 = 2 * floor_log2_i(n);
@@ -311,7 +355,7 @@ sort_top_kernel(const uint16_t *ids, int n, int NB, int32_t *perm, int32_t *bsta
         sh.ncur = 0;
         sh.nnxt = 0;
         if (n > SEG_T) {
-            segA[0] = 0u | ((uint32_t)n << 16);
+            segA[0] = (W)n << SH;
             depA[0] = (uint8_t)depth0;
             sh.ncur = 1;
         } else {
@@ -338,12 +382,13 @@ sort_top_kernel(const uint16_t *ids, int n, int NB, int32_t *perm, int32_t *bsta
         }
     }
 
-    uint32_t *cur = segA, *nxt = segB;
+    W *cur = segA, *nxt = segB;
     uint8_t *dcur = depA, *dnxt = depB;
+    constexpr W LOW = ((W)1 << SH) - 1;
     auto child = [&](int f, int l, int depth) {
         if (l - f > SEG_T) {
             const int slot = atomicAdd(&sh.nnxt, 1);
-            nxt[slot] = (uint32_t)f | ((uint32_t)l << 16);
+            nxt[slot] = (W)f | ((W)l << SH);
             dnxt[slot] = (uint8_t)depth;
         } else {
             emit_segment(segs, segcount, row, f, l, depth);
@@ -360,8 +405,8 @@ sort_top_kernel(const uint16_t *ids, int n, int NB, int32_t *perm, int32_t *bsta
             const bool act = g < ncur;
             int f = 0, l = 0, depth = 1;
             if (act) {
-                f = (int)(cur[g] & 0xffffu);
-                l = (int)(cur[g] >> 16);
+                f = (int)(cur[g] & LOW);
+                l = (int)(cur[g] >> SH);
                 depth = dcur[g];
             }
             // a segment at the depth limit is heap-sorted by its group's first lane
@@ -380,7 +425,8 @@ sort_top_kernel(const uint16_t *ids, int n, int NB, int32_t *perm, int32_t *bsta
                 else if (kb < kc) { x = c; p = kc; }
                 else { x = b; p = kb; }
                 if (lane == 0) {
-                    const uint16_t tk = key[f], ti = idx[f];
+                    const uint16_t tk = key[f];
+                    const Pos ti = idx[f];
                     key[f] = key[x]; idx[f] = idx[x];
                     key[x] = tk; idx[x] = ti;
                     sh.piv[g] = p;
@@ -420,8 +466,8 @@ sort_top_kernel(const uint16_t *ids, int n, int NB, int32_t *perm, int32_t *bsta
                     const bool isL = in && i > f && kv >= p;
                     const bool isR = in && kv <= p;
                     const uint64_t bL = wave_ballot(isL), bR = wave_ballot(isR);
-                    if (isL) TL[f + numL + lanes_below(bL)] = (uint16_t)i;
-                    if (isR) TR[f + numR + lanes_below(bR)] = (uint16_t)i;
+                    if (isL) TL[f + numL + lanes_below(bL)] = (Pos)i;
+                    if (isR) TR[f + numR + lanes_below(bR)] = (Pos)i;
                     numL += __popcll(bL);
                     numR += __popcll(bR);
                 }
@@ -441,7 +487,8 @@ sort_top_kernel(const uint16_t *ids, int n, int NB, int32_t *perm, int32_t *bsta
                 const int sw = sh.s[g], numR = sh.nR[g];
                 for (int k = gi * SSA_WAVE + lane; k < sw; k += gw * SSA_WAVE) {
                     const int pa = TL[f + k], pb = TR[f + numR - 1 - k];
-                    const uint16_t tk = key[pa], ti = idx[pa];
+                    const uint16_t tk = key[pa];
+                    const Pos ti = idx[pa];
                     key[pa] = key[pb]; idx[pa] = idx[pb];
                     key[pb] = tk; idx[pb] = ti;
                 }
@@ -454,8 +501,8 @@ sort_top_kernel(const uint16_t *ids, int n, int NB, int32_t *perm, int32_t *bsta
         } else {
             // ---- wave mode: one wave per segment
             for (int sgi = wid; sgi < ncur; sgi += NW) {
-                const int f = (int)(cur[sgi] & 0xffffu);
-                const int l = (int)(cur[sgi] >> 16);
+                const int f = (int)(cur[sgi] & LOW);
+                const int l = (int)(cur[sgi] >> SH);
                 const int depth = dcur[sgi];
                 if (depth == 0) {
                     if (lane == 0) heap_sort_range(key, idx, f, l);
@@ -471,15 +518,15 @@ sort_top_kernel(const uint16_t *ids, int n, int NB, int32_t *perm, int32_t *bsta
         }
         __syncthreads();
         if (tid == 0) { sh.ncur = sh.nnxt; sh.nnxt = 0; }
-        uint32_t *t = cur; cur = nxt; nxt = t;
+        W *t = cur; cur = nxt; nxt = t;
         uint8_t *td = dcur; dcur = dnxt; dnxt = td;
     }
     __syncthreads();
-    uint32_t *okv = gkv + (int64_t)row * n;
+    W *okv = gkv + (int64_t)row * n;
     int32_t *pout = perm + (int64_t)row * n;
     for (int i = tid; i < n; i += SORT_THREADS) {
-        okv[i] = (uint32_t)key[i] | ((uint32_t)idx[i] << 16);
-        pout[i] = idx[i];
+        okv[i] = (W)key[i] | ((W)idx[i] << SH);
+        pout[i] = (int32_t)idx[i];
     }
 }
 
@@ -492,22 +539,27 @@ sort_top_kernel(const uint16_t *ids, int n, int NB, int32_t *perm, int32_t *bsta
 constexpr int SEG_WAVES = 4;
 constexpr int SEG_STACK = SEG_T / (LEAF + 1) + 2;
 
+template <typename Pos>
 __host__ __device__ constexpr int seg_lds_words() {
-    // key, idx, TL, TR (u16 x SEG_T each), bits, stack
-    return (4 * SEG_T) / 2 + (SEG_T / 32 + 1) + 2 * SEG_STACK;
+    // key (u16), idx, TL, TR (Pos) x SEG_T each, bits, stack
+    return (SEG_T * (2 + 3 * (int)sizeof(Pos))) / 4 + (SEG_T / 32 + 1) + 2 * SEG_STACK;
 }
 
+template <typename Pos>
 __global__ void __launch_bounds__(SEG_WAVES * SSA_WAVE)
-sort_seg_kernel(const uint32_t *gkv, int n, const int4 *segs, const int *segcount, int32_t *perm) {
-    __shared__ uint32_t lds[SEG_WAVES * seg_lds_words()];
+sort_seg_kernel(const typename SortWords<Pos>::W *gkv, int n, const int4 *segs,
+                const int *segcount, int32_t *perm) {
+    using W = typename SortWords<Pos>::W;
+    constexpr int SH = SortWords<Pos>::SH;
+    __shared__ uint32_t lds[SEG_WAVES * seg_lds_words<Pos>()];
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / SSA_WAVE);
     const int lane = lane_id();
-    uint32_t *w0 = lds + wid * seg_lds_words();
-    uint16_t *key = (uint16_t *)w0;
-    uint16_t *idx = key + SEG_T;
-    uint16_t *TL = idx + SEG_T;
-    uint16_t *TR = TL + SEG_T;
-    uint32_t *bits = (uint32_t *)(TR + SEG_T);
+    uint32_t *w0 = lds + wid * seg_lds_words<Pos>();
+    Pos *idx = (Pos *)w0;
+    Pos *TL = idx + SEG_T;
+    Pos *TR = TL + SEG_T;
+    uint16_t *key = (uint16_t *)(TR + SEG_T);
+    uint32_t *bits = (uint32_t *)(key + SEG_T);
     uint32_t *stk = bits + (SEG_T / 32 + 1);
     uint32_t *sdep = stk + SEG_STACK;
     const int count = *segcount;
@@ -515,11 +567,11 @@ sort_seg_kernel(const uint32_t *gkv, int n, const int4 *segs, const int *segcoun
     for (int sgi = (int)blockIdx.x * SEG_WAVES + wid; sgi < count; sgi += stride) {
         const int4 e = segs[sgi];
         const int row = e.x, f0 = e.y, m = e.z, depth0 = e.w;
-        const uint32_t *src = gkv + (int64_t)row * n + f0;
+        const W *src = gkv + (int64_t)row * n + f0;
         for (int i = lane; i < m; i += SSA_WAVE) {
-            const uint32_t v = src[i];
+            const W v = src[i];
             key[i] = (uint16_t)(v & 0xffffu);
-            idx[i] = (uint16_t)(v >> 16);
+            idx[i] = (Pos)(v >> SH);
         }
         for (int w = lane; w < SEG_T / 32 + 1; w += SSA_WAVE) bits[w] = w == 0 ? 1u : 0u;
         wave_sync_lds();
@@ -562,7 +614,8 @@ sort_seg_kernel(const uint32_t *gkv, int n, const int4 *segs, const int *segcoun
             int e1 = s0 + 1;
             while (e1 < m && !((bits[e1 >> 5] >> (e1 & 31)) & 1u)) ++e1;
             for (int i = s0 + 1; i < e1; ++i) {
-                const uint16_t vk = key[i], vi = idx[i];
+                const uint16_t vk = key[i];
+                const Pos vi = idx[i];
                 int j = i;
                 while (j > s0 && key[j - 1] > vk) {
                     key[j] = key[j - 1];
@@ -575,7 +628,7 @@ sort_seg_kernel(const uint32_t *gkv, int n, const int4 *segs, const int *segcoun
         }
         wave_sync_lds();
         int32_t *pout = perm + (int64_t)row * n + f0;
-        for (int i = lane; i < m; i += SSA_WAVE) pout[i] = idx[i];
+        for (int i = lane; i < m; i += SSA_WAVE) pout[i] = (int32_t)idx[i];
         wave_sync_lds();
     }
 }
@@ -586,74 +639,97 @@ __global__ void sort_zero_kernel(int *p) {
 
 }  // namespace
 
+// Rows longer than this keep their keys and positions in the workspace
+constexpr int SORT_LDS_KEYS = 32768;
+// ... up to this many keys (kernel A's segment lists stay in LDS)
+constexpr int SORT_MAX_KEYS = 1 << 20;
+
 // LDS plan of kernel A for a row of n keys and NB buckets
 static void sort_plan(int n, int NB, int *cap, int *tl_in_lds, size_t *lds) {
     const int c = n / (SEG_T + 1) + 2;
+    *cap = c;
+    if (n > SORT_LDS_KEYS) {                   // hist and 64-bit segment words only
+        *tl_in_lds = 0;
+        *lds = (size_t)NB * 4 + (size_t)c * 16 + (size_t)c * 2;
+        return;
+    }
     const size_t base = ((size_t)4 * n + 15) / 16 * 16 + (size_t)NB * 4 + (size_t)c * 8 +
                         (size_t)c * 2;
     const size_t with_tl = (base + 15) / 16 * 16 + (size_t)4 * n;
-    *cap = c;
     if (with_tl <= SSA_LDS_BYTES) { *tl_in_lds = 1; *lds = with_tl; }
     else { *tl_in_lds = 0; *lds = base; }
 }
 
-// scratch: the rows after kernel A (4 B per key), the segment list (16 B per
-// key at most), its counter, and the stopper lists when they do not fit LDS
+// scratch: the rows after kernel A (4 B per key, 8 beyond LDS), the segment
+// list (16 B per key at most), its counter, and the stopper lists when they do
+// not fit LDS (beyond LDS: the rows' keys, positions and stopper lists)
 static int64_t al256(int64_t x) { return (x + 255) / 256 * 256; }
+
+static int64_t sort_row_bytes(int n) { return n > SORT_LDS_KEYS ? 8 : 4; }
 
 int64_t ssa_sort_tmp_bytes(int rows, int n) {
     int cap, tl;
     size_t lds;
     sort_plan(n, 4096, &cap, &tl, &lds);
     const int64_t rn = (int64_t)rows * n;
-    return al256(rn * 4) + al256(rn * 16) + 256 + (tl ? 0 : rn * 4);
+    const int64_t rest = n > SORT_LDS_KEYS ? rows * sort_glb_row_bytes(n) : (tl ? 0 : rn * 4);
+    return al256(rn * sort_row_bytes(n)) + al256(rn * 16) + 256 + rest;
 }
 
 int ssa_sort_supported(int n) {
     int cap, tl;
     size_t lds;
-    if (n < 1 || n > 32768) return 0;
+    if (n < 1 || n > SORT_MAX_KEYS) return 0;
     sort_plan(n, 4096, &cap, &tl, &lds);
     return lds <= SSA_LDS_BYTES;
 }
 
 int32_t *ssa_sort_counter(uint16_t *tmp, int rows, int n) {
     const int64_t rn = (int64_t)rows * n;
-    return (int32_t *)((char *)tmp + al256(rn * 4) + al256(rn * 16));
+    return (int32_t *)((char *)tmp + al256(rn * sort_row_bytes(n)) + al256(rn * 16));
+}
+
+template <typename Pos>
+static int launch_sort(const uint16_t *ids, int rows, int n, int NB, int32_t *perm,
+                       int32_t *bstart, int32_t *bsize, char *t, hipStream_t st) {
+    using W = typename SortWords<Pos>::W;
+    int cap, tl;
+    size_t lds;
+    sort_plan(n, NB, &cap, &tl, &lds);
+    const int64_t rn = (int64_t)rows * n;
+    W *gkv = (W *)t;
+    int4 *segs = (int4 *)(t + al256(rn * (int64_t)sizeof(W)));
+    int *segcount = ssa_sort_counter((uint16_t *)t, rows, n);
+    unsigned char *glb = (unsigned char *)t + al256(rn * (int64_t)sizeof(W)) + al256(rn * 16) + 256;
+    SSA_CHECK_HIP(hipFuncSetAttribute((const void *)sort_top_kernel<Pos>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    hipLaunchKernelGGL((sort_top_kernel<Pos>), dim3(rows), dim3(SORT_THREADS), lds, st, ids, n, NB,
+                       perm, bstart, bsize, gkv, segs, segcount, glb, tl, cap);
+    SSA_CHECK_LAUNCH();
+    const int64_t waves = std::max<int64_t>(1, std::min<int64_t>(rn / 128, 8192));
+    hipLaunchKernelGGL((sort_seg_kernel<Pos>), dim3((unsigned)ceil_div(waves, SEG_WAVES)),
+                       dim3(SEG_WAVES * SSA_WAVE), 0, st, gkv, n, segs, segcount, perm);
+    SSA_CHECK_LAUNCH();
+    return SSA_OK;
 }
 
 int ssa_launch_bucket_sort(const uint16_t *ids, int rows, int n, int P, int32_t *perm,
                            int32_t *bstart, int32_t *bsize, uint16_t *tmp, hipStream_t st,
                            bool counter_clear) {
     if (!ssa_sort_supported(n)) {
-        ssa_set_error("bucket sort: key length %d unsupported (1..32768)", n);
+        ssa_set_error("bucket sort: key length %d unsupported (1..%d)", n, SORT_MAX_KEYS);
         return SSA_E_UNSUP;
     }
     if (rows == 0) return SSA_OK;
     const int NB = 1 << P;
-    int cap, tl;
-    size_t lds;
-    sort_plan(n, NB, &cap, &tl, &lds);
-    const int64_t rn = (int64_t)rows * n;
-    char *t = (char *)tmp;
-    uint32_t *gkv = (uint32_t *)t;
-    int4 *segs = (int4 *)(t + al256(rn * 4));
-    int *segcount = ssa_sort_counter(tmp, rows, n);
-    uint16_t *tl_tmp = (uint16_t *)(t + al256(rn * 4) + al256(rn * 16) + 256);
     if (counter_clear) {
-        hipLaunchKernelGGL(sort_zero_kernel, dim3(1), dim3(64), 0, st, segcount);
+        hipLaunchKernelGGL(sort_zero_kernel, dim3(1), dim3(64), 0, st,
+                           ssa_sort_counter(tmp, rows, n));
         SSA_CHECK_LAUNCH();
     }
-    SSA_CHECK_HIP(hipFuncSetAttribute((const void *)sort_top_kernel,
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    hipLaunchKernelGGL(sort_top_kernel, dim3(rows), dim3(SORT_THREADS), lds, st, ids, n, NB, perm,
-                       bstart, bsize, gkv, segs, segcount, tl_tmp, tl, cap);
-    SSA_CHECK_LAUNCH();
-    const int64_t waves = std::max<int64_t>(1, std::min<int64_t>(rn / 128, 8192));
-    hipLaunchKernelGGL(sort_seg_kernel, dim3((unsigned)ceil_div(waves, SEG_WAVES)),
-                       dim3(SEG_WAVES * SSA_WAVE), 0, st, gkv, n, segs, segcount, perm);
-    SSA_CHECK_LAUNCH();
-    return SSA_OK;
+    return n > SORT_LDS_KEYS
+               ? launch_sort<uint32_t>(ids, rows, n, NB, perm, bstart, bsize, (char *)tmp, st)
+               : launch_sort<uint16_t>(ids, rows, n, NB, perm, bstart, bsize, (char *)tmp, st);
 }
 
 extern "C" int64_t ssa_bucket_sort_workspace_bytes(int32_t rows, int32_t n) {

@@ -223,11 +223,11 @@ def test_head_dim_rule(d, dtype, ok):
 
 
 # ---------------------------------------------------------------------------- size envelope
-@pytest.mark.parametrize("M", [32769, 40000, 65536])
-def test_key_length_beyond_the_sort_is_refused(M):
-    """Keys beyond 32768 are refused by the library before any launch (the
-    bucket sort keeps a row's keys in LDS, key ids are packed in 16 bits),
-    and by the Python wrapper before it touches a device."""
+@pytest.mark.parametrize("M", [65537, 100000, 131072])
+def test_key_length_beyond_16_bit_fields_is_refused(M):
+    """Keys beyond 65536 are refused by the library before any launch (key
+    ids, bucket starts and list positions travel in 16-bit fields), and by
+    the Python wrapper before it touches a device."""
     import torch
 
     from ssa_amd import _lib
@@ -239,6 +239,13 @@ def test_key_length_beyond_the_sort_is_refused(M):
     with pytest.raises(RuntimeError, match="key length"):
         _lib.build_graph(q, k, torch.zeros(2, 12, 16), P=1, T=0, C=64, top_k=32, window=4,
                          causal=False, is_cross=True, total_k=64, glob=torch.zeros(2))
+
+
+@pytest.mark.parametrize("M", [32769, 40000, 65536])
+def test_key_lengths_up_to_65536_are_taken(M):
+    a, _ = _full_args(M, 64)
+    from ssa_amd import _lib
+    assert _lib.lib().ssa_graph_workspace_bytes(ctypes.byref(a)) > 0, _lib.lib().ssa_last_error()
 
 
 def test_any_number_of_globals_up_to_the_key_count():

@@ -35,9 +35,11 @@ def _ints(shape, lo, hi, gen):
 
 
 # ------------------------------------------------------------------ bucket sort
+# rows beyond 32768 keys take the sort with 32-bit positions and the row in
+# the workspace (40001: odd, so rows start at unaligned key offsets)
 @pytest.mark.parametrize("rows,n,P", [(3, 17, 1), (2, 1024, 1), (4, 4096, 3), (2, 8192, 4),
                                       (2, 16384, 6), (1, 32768, 5), (2, 300, 12), (5, 16, 2),
-                                      (2, 5, 1)])
+                                      (2, 5, 1), (2, 40001, 7), (2, 65536, 5), (1, 131072, 9)])
 @pytest.mark.parametrize("dist", ["uniform", "skewed", "sorted", "reversed", "constant"])
 def test_bucket_sort_is_torch_sort(rows, n, P, dist):
     from ssa_amd import _lib
@@ -88,6 +90,10 @@ GRAPH_CASES = [
     ("many_globals", 1, 2, 2, 256, 256, 16, 3, 4, 1, 160, 4, 100, True, False),
     ("many_globals_cross", 1, 2, 1, 80, 300, 16, 2, 4, 1, 128, 4, list(range(0, 300, 3)),
      False, True),
+    # key lengths beyond 32768: the bucket sort with 32-bit positions, the
+    # cut entries' 16-bit fields read unsigned
+    ("long_keys_causal", 1, 1, 1, 65536, 65536, 16, 2, 12, 0, 32, 2, 2, True, False),
+    ("long_keys_cross", 1, 2, 1, 512, 40000, 16, 2, 6, 1, 32, 2, 2, False, True),
 ]
 
 
