@@ -59,7 +59,11 @@ template <> struct VecOf<bf16_t> { static constexpr int n = 8; };
 template <> struct VecOf<f16_t> { static constexpr int n = 8; };
 
 template <typename T, int D> struct Geo {
-    static constexpr int VEC = (VecOf<T>::n < D) ? VecOf<T>::n : D;   // elements per lane
+    // elements per lane: a 16-byte load, more when the row is wider than a
+    // wave holds that way (fp32 beyond 256)
+    static constexpr int VEC = (VecOf<T>::n < D) ? (VecOf<T>::n * SSA_WAVE < D ? D / SSA_WAVE
+                                                                              : VecOf<T>::n)
+                                                 : D;
     static constexpr int LPR = D / VEC;                                // lanes per row
     static constexpr int RPI = SSA_WAVE / LPR;                         // rows per wave load
     static_assert(D % VEC == 0, "head dim must be a multiple of the vector width");
@@ -68,7 +72,12 @@ template <typename T, int D> struct Geo {
 
 template <typename T, int VEC>
 __device__ __forceinline__ void load_vec(const T *p, float (&f)[VEC]) {
-    if constexpr (sizeof(T) * VEC == 16) {
+    if constexpr (sizeof(T) * VEC == 32) {
+        uint4 u[2] = {reinterpret_cast<const uint4 *>(p)[0], reinterpret_cast<const uint4 *>(p)[1]};
+        const T *e = reinterpret_cast<const T *>(u);
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) f[i] = to_f32(e[i]);
+    } else if constexpr (sizeof(T) * VEC == 16) {
         uint4 u = *reinterpret_cast<const uint4 *>(p);
         const T *e = reinterpret_cast<const T *>(&u);
 #pragma unroll
@@ -1073,7 +1082,7 @@ int launch_apply(const ApplyP &p, hipStream_t st, bool bwd) {
     } else {
         const size_t lds = (size_t)WAVES * 2 * p.K * sizeof(float);
         constexpr int U = (Geo<T, D>::RPI >= 8) ? 4 : 8;
-        if constexpr (sizeof(T) == 2 && D >= 8) {
+        if constexpr (sizeof(T) == 2 && D >= 8 && D <= 256) {   // two rows per wave at least
             if (fwd16_ok(p, (int)sizeof(T), D)) {
                 constexpr int STEP = (SSA_WAVE / (D / 8)) * U;
                 const size_t lds16 = (size_t)WAVES * 2 * ceil_div(p.K, STEP) * STEP * sizeof(float);
@@ -1100,7 +1109,7 @@ int launch_apply(const ApplyP &p, hipStream_t st, bool bwd) {
 template <typename T>
 int dispatch_d(const ApplyP &p, int d, hipStream_t st, bool bwd) {
     if (!ssa_head_dim_ok(d, std::is_same<T, float>::value ? SSA_F32 : SSA_BF16)) {
-        ssa_set_error("sparse_gather_attention: head dim %d unsupported (4..256: a power of two "
+        ssa_set_error("sparse_gather_attention: head dim %d unsupported (4..512: a power of two "
                       "or a multiple of %d)", d, std::is_same<T, float>::value ? 4 : 8);
         return SSA_E_UNSUP;
     }
@@ -1112,6 +1121,7 @@ int dispatch_d(const ApplyP &p, int d, hipStream_t st, bool bwd) {
         case 64: return launch_apply<T, 64>(p, st, bwd);
         case 128: return launch_apply<T, 128>(p, st, bwd);
         case 256: return launch_apply<T, 256>(p, st, bwd);
+        case 512: return launch_apply<T, 512>(p, st, bwd);
         default:
             ssa_set_error("sparse_gather_attention: head dim %d unsupported (4..256, power of 2)", d);
             return SSA_E_UNSUP;

@@ -19,11 +19,15 @@ void ssa_set_error(const char *fmt, ...);
         }                                        \
     } while (0)
 
+// A failed call's error is also taken off the runtime's last-error slot, so
+// the caller's next HIP call (torch's included) does not report it again: the
+// library reports it once, through its return code and ssa_last_error.
 #define SSA_CHECK_HIP(expr)                                                        \
     do {                                                                           \
         hipError_t e_ = (expr);                                                    \
         if (e_ != hipSuccess) {                                                    \
             ssa_set_error("%s failed: %s", #expr, hipGetErrorString(e_));          \
+            (void)hipGetLastError();                                               \
             return SSA_E_HIP;                                                      \
         }                                                                          \
     } while (0)
@@ -255,9 +259,9 @@ __host__ __device__ __forceinline__ int64_t ceil_div(int64_t a, int64_t b) { ret
 // and elements past d read zeros and store nothing.
 inline bool ssa_head_dim_ok(int d, int dtype) {
     const int vec = dtype == SSA_F32 ? 4 : 8;
-    return d >= 4 && d <= 256 && ((d & (d - 1)) == 0 || d % vec == 0);
+    return d >= 4 && d <= 512 && ((d & (d - 1)) == 0 || d % vec == 0);
 }
-// the smallest power-of-two instance (4..256) that covers d
+// the smallest power-of-two instance (4..512) that covers d
 inline int ssa_pow2_instance(int d) {
     int D = 4;
     while (D < d) D <<= 1;

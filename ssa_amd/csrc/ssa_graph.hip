@@ -681,7 +681,12 @@ __device__ __forceinline__ int rs_tile_cutoff(const int32_t *sd, int nv, const i
 
 template <typename T, int D>
 __global__ void __launch_bounds__(256) rescore_kernel(RsP p) {
-    constexpr int LD = D + 1;
+    // head dims beyond 256 are staged 256 columns at a time (the q slice then
+    // again for every candidate chunk); each score's fmaf chain still runs
+    // over the columns in order
+    constexpr int DS = D < 256 ? D : 256;
+    constexpr bool ONE = D <= DS;
+    constexpr int LD = DS + 1;
     extern __shared__ float rs_smem[];
     float *Qs = rs_smem;                // [TQ][LD]
     float *Ks = Qs + TQ * LD;           // [TC][LD]
@@ -702,37 +707,45 @@ __global__ void __launch_bounds__(256) rescore_kernel(RsP p) {
     if (tid < TQ) nidx[tid] = tid < qc ? p.qlist[(int64_t)inst * p.N + qb + tid] : 0;
     __syncthreads();
     const int nv = rs_tile_cutoff(sd, tl.nva, nidx, qc, p.causal);
-    for (int x = tid; x < TQ * D; x += 256) {
-        const int i = x / D, c = x % D;
-        Qs[i * LD + c] = (i < qc && c < p.d) ? to_f32(qbase[(int64_t)nidx[i] * p.qsn + c]) : 0.f;
-    }
+    auto load_q = [&](int ds0) {
+        for (int x = tid; x < TQ * DS; x += 256) {
+            const int i = x / DS, c = x % DS;
+            Qs[i * LD + c] = (i < qc && ds0 + c < p.d)
+                                 ? to_f32(qbase[(int64_t)nidx[i] * p.qsn + ds0 + c]) : 0.f;
+        }
+    };
+    if (ONE) load_q(0);
     const int ty = tid / 16, tx = tid % 16;
     for (int c0 = 0; c0 < nv; c0 += TC) {
         __syncthreads();
         if (tid < TC) kidx[tid] = (c0 + tid < nv) ? sd[c0 + tid] : 0;
-        __syncthreads();
-        for (int x = tid; x < TC * D; x += 256) {
-            const int j = x / D, c = x % D;
-            Ks[j * LD + c] = (c0 + j < nv && c < p.d) ? to_f32(kbase[(int64_t)kidx[j] * p.ksn + c])
-                                                       : 0.f;
-        }
-        __syncthreads();
         float acc[4][4];
 #pragma unroll
         for (int a = 0; a < 4; ++a)
 #pragma unroll
             for (int bb = 0; bb < 4; ++bb) acc[a][bb] = 0.f;
-        // one fmaf chain over the head dim, as the select's exact keys run it
-        for (int c = 0; c < p.d; ++c) {
-            float qa[4], kb[4];
+        for (int ds0 = 0; ds0 < p.d; ds0 += DS) {
+            __syncthreads();
+            if (!ONE) load_q(ds0);
+            for (int x = tid; x < TC * DS; x += 256) {
+                const int j = x / DS, c = x % DS;
+                Ks[j * LD + c] = (c0 + j < nv && ds0 + c < p.d)
+                                     ? to_f32(kbase[(int64_t)kidx[j] * p.ksn + ds0 + c]) : 0.f;
+            }
+            __syncthreads();
+            // one fmaf chain over the head dim, as the select's exact keys run it
+            const int cn = min(DS, p.d - ds0);
+            for (int c = 0; c < cn; ++c) {
+                float qa[4], kb[4];
 #pragma unroll
-            for (int a = 0; a < 4; ++a) qa[a] = Qs[(ty * 4 + a) * LD + c];
+                for (int a = 0; a < 4; ++a) qa[a] = Qs[(ty * 4 + a) * LD + c];
 #pragma unroll
-            for (int bb = 0; bb < 4; ++bb) kb[bb] = Ks[(tx + 16 * bb) * LD + c];
+                for (int bb = 0; bb < 4; ++bb) kb[bb] = Ks[(tx + 16 * bb) * LD + c];
 #pragma unroll
-            for (int a = 0; a < 4; ++a)
+                for (int a = 0; a < 4; ++a)
 #pragma unroll
-                for (int bb = 0; bb < 4; ++bb) acc[a][bb] = fmaf(qa[a], kb[bb], acc[a][bb]);
+                    for (int bb = 0; bb < 4; ++bb) acc[a][bb] = fmaf(qa[a], kb[bb], acc[a][bb]);
+            }
         }
 #pragma unroll
         for (int a = 0; a < 4; ++a) {
@@ -3444,7 +3457,7 @@ int make_dims(const ssa_graph_args *a, Dims &D, bool need_q = true, int64_t ws_c
                   "build_graph: q/k dtype");
     SSA_CHECK_ARG(a->G == 0 || a->glob, "build_graph: glob is null");
     if (!ssa_head_dim_ok(a->d, a->q.dtype)) {
-        ssa_set_error("build_graph: head dim %d unsupported (4..256: a power of two or a multiple "
+        ssa_set_error("build_graph: head dim %d unsupported (4..512: a power of two or a multiple "
                       "of %d)", a->d, a->q.dtype == SSA_F32 ? 4 : 8);
         return SSA_E_UNSUP;
     }
@@ -3596,6 +3609,7 @@ int launch_hash_one(const HashP &hp, int d, hipStream_t st) {
         case 64: return launch_hash_mfma<T, 64>(hp, st);
         case 128: return launch_hash_mfma<T, 128>(hp, st);
         case 256: return launch_hash_mfma<T, 256>(hp, st);
+        case 512: return launch_hash_mfma<T, 512>(hp, st);
     }
     ssa_set_error("hash: head dim %d", d);
     return SSA_E_UNSUP;
@@ -3648,7 +3662,7 @@ int launch_hash(const Dims &D, const ssa_graph_args *a, const Layout &L, char *w
 
 template <typename T, int Dh>
 int launch_rescore(const RsP &rp, int64_t grid, hipStream_t st) {
-    const size_t lds = (size_t)(TQ + TC) * (Dh + 1) * 4 + (TQ + TC) * 4;
+    const size_t lds = (size_t)(TQ + TC) * ((Dh < 256 ? Dh : 256) + 1) * 4 + (TQ + TC) * 4;
     SSA_CHECK_HIP(hipFuncSetAttribute((const void *)rescore_kernel<T, Dh>,
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     hipLaunchKernelGGL((rescore_kernel<T, Dh>), dim3((unsigned)grid), dim3(256), lds, st, rp);
@@ -3703,6 +3717,7 @@ int rescore_dispatch(int d, const RsP &rp, int64_t grid, hipStream_t st) {
         case 64: return launch_rescore<T, 64>(rp, grid, st);
         case 128: return launch_rescore<T, 128>(rp, grid, st);
         case 256: return launch_rescore<T, 256>(rp, grid, st);
+        case 512: return launch_rescore<T, 512>(rp, grid, st);
     }
     ssa_set_error("rescore: head dim %d", d);
     return SSA_E_UNSUP;
@@ -3753,7 +3768,7 @@ int aux_dispatch(int d, bool mfma, const AuxP &ap, hipStream_t st) {
     case DD: hipLaunchKernelGGL((aux_valu_kernel<T, DD>), grid, dim3(256), 0, st, ap); break;
     switch (ssa_pow2_instance(d)) {
         SSA_AUX_VALU(4) SSA_AUX_VALU(8) SSA_AUX_VALU(16) SSA_AUX_VALU(32) SSA_AUX_VALU(64)
-        SSA_AUX_VALU(128) SSA_AUX_VALU(256)
+        SSA_AUX_VALU(128) SSA_AUX_VALU(256) SSA_AUX_VALU(512)
         default: ssa_set_error("aux scores: head dim %d", d); return SSA_E_UNSUP;
     }
 #undef SSA_AUX_VALU
