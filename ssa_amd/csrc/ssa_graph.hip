@@ -48,6 +48,7 @@
 
 #include "ssa_common.h"
 #include "ssa_graph_internal.h"
+#include "ssa_sort_dev.h"
 
 // ------------------------------------------------------------------ checked build
 // Built with SSA_CHECKED (`make checked`: libssa_amd_checked.so), the
@@ -1265,17 +1266,27 @@ struct AuxP {
     int R, maxP, P, Tp, NS;
     uint16_t *qid;
     int32_t *zero1;
+    // when set (the launch beside the key sort, before the list sort reduces
+    // them): each wave takes max |k|^2 of its kv head from the key hash's
+    // 16-row tile maxima (kp_n per kv head) instead of knorm
+    const uint32_t *kpart;
+    int kp_n;
 };
 
+// LDS floats a wave of aux_mfma_rows needs for the fused query hash
+__host__ __device__ inline int aux_wave_floats(int R, int P) {
+    return 16 * (((R * P + 15) / 16) * 16 + 1);
+}
+
+// One wavefront's 16 query rows of the aux pass (wg: the wave's index over
+// the launch; pw: its LDS region of aux_wave_floats floats).
 template <typename T, int D>
-__global__ void __launch_bounds__(256) aux_mfma_kernel(AuxP p) {
+__device__ void aux_mfma_rows(const AuxP &p, int64_t wg, float *pw) {
     using V = typename Mfma16<T>::vec;
     constexpr int KS = (D + 31) / 32;
-    const int wid = threadIdx.x / SSA_WAVE;
     const int lane = lane_id();
     const int li = lane % 16, lg = lane / 16;
     const int nblk = (p.N + 15) / 16;
-    const int64_t wg = (int64_t)blockIdx.x * 4 + wid;
     if (wg >= (int64_t)p.nbh * nblk) return;
     const int bhl = (int)(wg / nblk);
     const int n0 = (int)(wg % nblk) * 16;
@@ -1301,12 +1312,10 @@ __global__ void __launch_bounds__(256) aux_mfma_kernel(AuxP p) {
         // li and plane li with element 32 s + 8 lg + e at step (s, e) -- the
         // elements its bf16/f16 fragments hold -- then through LDS to one lane
         // per row, which writes the ids as the query hash does
-        extern __shared__ float aux_proj[];
-        if (p.zero1 && blockIdx.x == 0 && threadIdx.x == 0) *p.zero1 = 0;
+        if (p.zero1 && wg == 0 && lane == 0) *p.zero1 = 0;
         const int NP = p.R * p.P;
         const int NT = (NP + 15) / 16;
         const int pst = NT * 16 + 1;
-        float *pw = aux_proj + wid * 16 * pst;
         for (int t = 0; t < NT; ++t) {
             const int j = t * 16 + li;
             const bool real = j < NP;
@@ -1357,9 +1366,17 @@ __global__ void __launch_bounds__(256) aux_mfma_kernel(AuxP p) {
         }
         q2 += __shfl_xor(q2, 16, SSA_WAVE);
         q2 += __shfl_xor(q2, 32, SSA_WAVE);
-        if (lg == 0 && okq)
-            ob[(int64_t)li * p.NA + p.NA - 1] =
-                code_scale(q2, __uint_as_float(p.knorm[b * p.Hkv + g]));
+        uint32_t kn;
+        if (p.kpart) {
+            // max over the tile maxima, as the list sort reduces them
+            const uint32_t *kt = p.kpart + (int64_t)(b * p.Hkv + g) * p.kp_n;
+            uint32_t m = 0u;
+            for (int i = lane; i < p.kp_n; i += SSA_WAVE) m = max(m, kt[i]);
+            kn = wave_max_u(m);
+        } else {
+            kn = p.knorm[b * p.Hkv + g];
+        }
+        if (lg == 0 && okq) ob[(int64_t)li * p.NA + p.NA - 1] = code_scale(q2, __uint_as_float(kn));
     }
     if (p.causal) {            // key row li is key n0 + li: the diagonal is q_n . k_n
         V kb[KS];
@@ -1387,6 +1404,33 @@ __global__ void __launch_bounds__(256) aux_mfma_kernel(AuxP p) {
             if (okq && jj <= p.G) ob[(int64_t)li * p.NA + 1 + jj] = acc[rr];
         }
     }
+}
+
+template <typename T, int D>
+__global__ void __launch_bounds__(256) aux_mfma_kernel(AuxP p) {
+    extern __shared__ float aux_proj[];
+    const int wid = threadIdx.x / SSA_WAVE;
+    aux_mfma_rows<T, D>(p, (int64_t)blockIdx.x * 4 + wid,
+                        aux_proj + (p.qid ? wid * aux_wave_floats(p.R, p.P) : 0));
+}
+
+// The key sort's top levels (workgroups 0 .. s.rows - 1, one row each) and the
+// first head chunk's aux pass with its query hash (the other workgroups, 16
+// waves of aux_mfma_rows each) in one launch: the sort keeps only s.rows
+// CUs busy, and the query side needs only q, the hyperplanes and the key
+// hash's norm tiles.
+template <typename T, int D>
+__global__ void __launch_bounds__(SORT_THREADS) sort_aux_kernel(SortTopArgs s, AuxP p) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    __shared__ TopShared sh;
+    if ((int)blockIdx.x < s.rows) {
+        sort_top_row<uint16_t>((int)blockIdx.x, s.ids, s.n, s.NB, s.perm, s.bstart, s.bsize, s.gkv,
+                               s.segs, s.segcount, s.glb, s.tl_in_lds, s.cap, smem_raw, sh);
+        return;
+    }
+    const int wid = threadIdx.x / SSA_WAVE;
+    aux_mfma_rows<T, D>(p, ((int64_t)blockIdx.x - s.rows) * SORT_WAVES + wid,
+                        (float *)smem_raw + wid * aux_wave_floats(p.R, p.P));
 }
 
 template <typename T, int D>
@@ -3847,9 +3891,121 @@ int select_dispatch(const SelP &sp, hipStream_t st) {
 
 // Key phase: bucket ids of the keys, the bucket permutation and tables and
 // the sorted candidate lists -- everything that needs k but not q.
+// the rescore's parameters that hold for every head chunk
+RsP rescore_common(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws) {
+    RsP rp{};
+    rp.sid = (const int32_t *)(ws + L.sid);
+    rp.bstart = (const int32_t *)(ws + L.bstart);
+    rp.bsize = (const int32_t *)(ws + L.bsize);
+    rp.q = a->q.ptr; rp.k = a->k.ptr;
+    rp.qsb = a->q.sb; rp.qsh = a->q.sh; rp.qsn = a->q.sn;
+    rp.ksb = a->k.sb; rp.ksh = a->k.sh; rp.ksn = a->k.sn;
+    rp.S = (uint16_t *)(ws + L.S);
+    rp.N = D.N; rp.M = D.M; rp.R = D.R; rp.NS = D.NS; rp.NB = D.NB; rp.C = D.C;
+    rp.Hq = D.Hq; rp.Hkv = D.Hkv; rp.rep = D.rep; rp.Call = D.Call;
+    rp.causal = a->causal ? 1 : 0;
+    rp.Cs = D.Cs;
+    rp.d = D.d;
+    {
+        const int64_t el = a->q.dtype == SSA_F32 ? 4 : 2;
+        rp.k32 = (rp.ksn * el < ((int64_t)1 << 24) &&
+                  ((int64_t)D.M * rp.ksn + D.d) * el < ((int64_t)1 << 31)) ? 1 : 0;
+    }
+    return rp;
+}
+
+// With aux on the matrix cores, aux_mfma_kernel also hashes the queries (one
+// pass over q): without injected projections, with 16-byte aligned planes and
+// their projection rows within 48 KB of LDS per block
+template <typename T>
+bool aux_hashes_queries(const Dims &D, const ssa_graph_args *a, bool mfma) {
+    const int np16 = (int)ceil_div((int64_t)D.R * D.P, 16) * 16;
+    return mfma && !a->q_proj && (uintptr_t)a->rand_proj % 16 == 0 &&
+           (size_t)4 * 16 * (np16 + 1) * 4 <= 48 * 1024;
+}
+
+// The first head chunk's aux pass runs beside the key sort's top levels
+// (sort_aux_kernel) when it hashes the queries, the key hash left its norm
+// tiles and the sort keeps its rows in LDS
+template <typename T>
+bool sort_beside_aux(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws) {
+    if constexpr (std::is_same<T, float>::value) {
+        return false;
+    } else {
+        const RsP rp = rescore_common(D, a, L, ws);
+        const bool mfma = rescore_uses_mfma<T>(D.d, rp);
+        return !D.fused && aux_hashes_queries<T>(D, a, mfma) && key_norm_in_hash(D, a) &&
+               D.M <= 32768 && D.BH * D.N > 0;
+    }
+}
+
+AuxP aux_params(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws, int64_t bh0,
+                int nbh, bool qhash) {
+    AuxP ap{};
+    ap.q = a->q.ptr; ap.k = a->k.ptr;
+    ap.qsb = a->q.sb; ap.qsh = a->q.sh; ap.qsn = a->q.sn;
+    ap.ksb = a->k.sb; ap.ksh = a->k.sh; ap.ksn = a->k.sn;
+    ap.glob = a->glob;
+    ap.knorm = (const uint32_t *)(ws + L.knorm);
+    ap.N = D.N; ap.Hq = D.Hq; ap.Hkv = D.Hkv; ap.rep = D.rep; ap.bh0 = (int)bh0;
+    ap.nbh = nbh; ap.G = D.G; ap.NA = D.G + 3; ap.causal = a->causal; ap.d = D.d;
+    // (fused: the query projection wrote every head's aux rows and ids)
+    ap.out = (float *)(ws + L.aux) + (D.fused ? bh0 * (int64_t)D.N * ap.NA : 0);
+    if (qhash) {
+        ap.planes = a->rand_proj;
+        ap.R = D.R; ap.maxP = D.maxP; ap.P = D.P; ap.Tp = D.Tp; ap.NS = D.NS;
+        ap.qid = (uint16_t *)(ws + L.qid);
+        // the tie-row counter of the select kernels (replayed once, after every chunk)
+        ap.zero1 = bh0 == 0 ? (int32_t *)(ws + L.tie_count) : nullptr;
+    }
+    return ap;
+}
+
+template <typename T>
+int launch_sort_aux(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws,
+                    hipStream_t st) {
+    SortTopArgs sa{};
+    int rc = ssa_sort_top_setup((const uint16_t *)(ws + L.kid), (int)(D.BK * D.R), D.M, D.P,
+                                (int32_t *)(ws + L.perm), (int32_t *)(ws + L.bstart),
+                                (int32_t *)(ws + L.bsize), (uint16_t *)(ws + L.sorttmp), &sa);
+    if (rc) return rc;
+    const int nbh = (int)std::min<int64_t>(D.BH, D.nbh_chunk);
+    AuxP ap = aux_params(D, a, L, ws, 0, nbh, true);
+    ap.kpart = (const uint32_t *)(ws + L.kpart);
+    ap.kp_n = D.M / 16;
+    const int64_t waves = (int64_t)nbh * ceil_div(D.N, 16);
+    const int64_t grid = sa.rows + ceil_div(waves, SORT_WAVES);
+    const size_t lds = std::max<size_t>((size_t)sa.lds,
+                                        (size_t)SORT_WAVES * aux_wave_floats(D.R, D.P) * 4);
+    SSA_CHECK_ARG(lds <= SSA_LDS_BYTES, "build_graph: sort and aux need %zu bytes of LDS", lds);
+    const void *fn = nullptr;
+    switch (mfma_instance(D.d)) {
+        case 8: fn = (const void *)sort_aux_kernel<T, 8>; break;
+        case 16: fn = (const void *)sort_aux_kernel<T, 16>; break;
+        case 32: fn = (const void *)sort_aux_kernel<T, 32>; break;
+        case 64: fn = (const void *)sort_aux_kernel<T, 64>; break;
+        case 96: fn = (const void *)sort_aux_kernel<T, 96>; break;
+        case 128: fn = (const void *)sort_aux_kernel<T, 128>; break;
+        default: ssa_set_error("sort and aux: head dim %d", D.d); return SSA_E_UNSUP;
+    }
+    SSA_CHECK_HIP(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    switch (mfma_instance(D.d)) {
+#define SSA_SORT_AUX(DD)                                                                     \
+    case DD:                                                                                 \
+        hipLaunchKernelGGL((sort_aux_kernel<T, DD>), dim3((unsigned)grid), dim3(SORT_THREADS), \
+                           lds, st, sa, ap);                                                 \
+        break;
+        SSA_SORT_AUX(8) SSA_SORT_AUX(16) SSA_SORT_AUX(32) SSA_SORT_AUX(64) SSA_SORT_AUX(96)
+        SSA_SORT_AUX(128)
+#undef SSA_SORT_AUX
+    }
+    SSA_CHECK_LAUNCH();
+    return ssa_launch_sort_seg(sa, st);
+}
+
 template <typename T>
 int keys_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws,
-               hipStream_t st) {
+               hipStream_t st, bool sort_aux) {
     int rc = SSA_OK;
     {
         // (fused: the key projection wrote the key ids and the 16-row norm maxima)
@@ -3884,10 +4040,19 @@ int keys_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws
         }
     }
     // the key hash cleared the sort's counter
-    rc = ssa_launch_bucket_sort((const uint16_t *)(ws + L.kid), (int)(D.BK * D.R), D.M, D.P,
-                                (int32_t *)(ws + L.perm), (int32_t *)(ws + L.bstart),
-                                (int32_t *)(ws + L.bsize), (uint16_t *)(ws + L.sorttmp), st,
-                                false);
+    bool done = false;
+    if constexpr (!std::is_same<T, float>::value) {
+        if (sort_aux) {
+            rc = launch_sort_aux<T>(D, a, L, ws, st);
+            done = true;
+        }
+    }
+    if (!done) {
+        rc = ssa_launch_bucket_sort((const uint16_t *)(ws + L.kid), (int)(D.BK * D.R), D.M, D.P,
+                                    (int32_t *)(ws + L.perm), (int32_t *)(ws + L.bstart),
+                                    (int32_t *)(ws + L.bsize), (uint16_t *)(ws + L.sorttmp), st,
+                                    false);
+    }
     if (rc) return rc;
     {
         LsP lp{};
@@ -3921,33 +4086,10 @@ int keys_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws
 // Query phase: everything else, given the key phase's results in ws.
 template <typename T>
 int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws,
-                  hipStream_t st) {
-    // the rescore's parameters that hold for every head chunk
-    RsP rp{};
-    rp.sid = (const int32_t *)(ws + L.sid);
-    rp.bstart = (const int32_t *)(ws + L.bstart);
-    rp.bsize = (const int32_t *)(ws + L.bsize);
-    rp.q = a->q.ptr; rp.k = a->k.ptr;
-    rp.qsb = a->q.sb; rp.qsh = a->q.sh; rp.qsn = a->q.sn;
-    rp.ksb = a->k.sb; rp.ksh = a->k.sh; rp.ksn = a->k.sn;
-    rp.S = (uint16_t *)(ws + L.S);
-    rp.N = D.N; rp.M = D.M; rp.R = D.R; rp.NS = D.NS; rp.NB = D.NB; rp.C = D.C;
-    rp.Hq = D.Hq; rp.Hkv = D.Hkv; rp.rep = D.rep; rp.Call = D.Call;
-    rp.causal = a->causal ? 1 : 0;
-    rp.Cs = D.Cs;
-    rp.d = D.d;
-    {
-        const int64_t el = a->q.dtype == SSA_F32 ? 4 : 2;
-        rp.k32 = (rp.ksn * el < ((int64_t)1 << 24) &&
-                  ((int64_t)D.M * rp.ksn + D.d) * el < ((int64_t)1 << 31)) ? 1 : 0;
-    }
+                  hipStream_t st, bool sort_aux) {
+    RsP rp = rescore_common(D, a, L, ws);
     const bool mfma = rescore_uses_mfma<T>(D.d, rp);
-    // With aux on the matrix cores, aux_mfma_kernel also hashes the queries
-    // (one pass over q): without injected projections, with 16-byte aligned
-    // planes and their projection rows within 48 KB of LDS per block
-    const int np16 = (int)ceil_div((int64_t)D.R * D.P, 16) * 16;
-    const bool fuse_qhash = mfma && !a->q_proj && (uintptr_t)a->rand_proj % 16 == 0 &&
-                            (size_t)4 * 16 * (np16 + 1) * 4 <= 48 * 1024;
+    const bool fuse_qhash = aux_hashes_queries<T>(D, a, mfma);
     int rc = SSA_OK;
     if (!fuse_qhash && !D.fused) {
         rc = launch_hash<T>(D, a, L, ws, st, false);
@@ -3959,24 +4101,9 @@ int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char 
         const int ninst = nbh * D.R * D.NS;
         // aux first: the rescore codes its scores with the query scales it
         // writes, and the query buckets need the ids it writes when fused
-        AuxP ap{};
-        ap.q = a->q.ptr; ap.k = a->k.ptr;
-        ap.qsb = a->q.sb; ap.qsh = a->q.sh; ap.qsn = a->q.sn;
-        ap.ksb = a->k.sb; ap.ksh = a->k.sh; ap.ksn = a->k.sn;
-        ap.glob = a->glob;
-        ap.knorm = (const uint32_t *)(ws + L.knorm);
-        ap.N = D.N; ap.Hq = D.Hq; ap.Hkv = D.Hkv; ap.rep = D.rep; ap.bh0 = (int)bh0;
-        ap.nbh = nbh; ap.G = D.G; ap.NA = D.G + 3; ap.causal = a->causal; ap.d = D.d;
-        // (fused: the query projection wrote every head's aux rows and ids)
-        ap.out = (float *)(ws + L.aux) + (D.fused ? bh0 * (int64_t)D.N * ap.NA : 0);
-        if (fuse_qhash) {
-            ap.planes = a->rand_proj;
-            ap.R = D.R; ap.maxP = D.maxP; ap.P = D.P; ap.Tp = D.Tp; ap.NS = D.NS;
-            ap.qid = (uint16_t *)(ws + L.qid);
-            // the tie-row counter of the select kernels (replayed once, after every chunk)
-            ap.zero1 = bh0 == 0 ? (int32_t *)(ws + L.tie_count) : nullptr;
-        }
-        if (!D.fused) rc = aux_dispatch<T>(D.d, mfma, ap, st);
+        // (the first chunk's ran beside the key sort when sort_aux)
+        const AuxP ap = aux_params(D, a, L, ws, bh0, nbh, fuse_qhash);
+        if (!D.fused && !(sort_aux && bh0 == 0)) rc = aux_dispatch<T>(D.d, mfma, ap, st);
         if (rc) return rc;
         QbP qp{};
         qp.qid = (const uint16_t *)(ws + L.qid);
@@ -4115,14 +4242,23 @@ int build_impl(const ssa_graph_args *a, void *workspace, int64_t workspace_bytes
     char *ws = (char *)workspace;
     switch (a->k.dtype) {
         case SSA_F32:
-            if ((rc = keys_typed<float>(D, a, L, ws, st))) return rc;
-            return queries_typed<float>(D, a, L, ws, st);
+        {
+            const bool sa = sort_beside_aux<float>(D, a, L, ws);
+            if ((rc = keys_typed<float>(D, a, L, ws, st, sa))) return rc;
+            return queries_typed<float>(D, a, L, ws, st, sa);
+        }
         case SSA_BF16:
-            if ((rc = keys_typed<bf16_t>(D, a, L, ws, st))) return rc;
-            return queries_typed<bf16_t>(D, a, L, ws, st);
+        {
+            const bool sa = sort_beside_aux<bf16_t>(D, a, L, ws);
+            if ((rc = keys_typed<bf16_t>(D, a, L, ws, st, sa))) return rc;
+            return queries_typed<bf16_t>(D, a, L, ws, st, sa);
+        }
         case SSA_F16:
-            if ((rc = keys_typed<f16_t>(D, a, L, ws, st))) return rc;
-            return queries_typed<f16_t>(D, a, L, ws, st);
+        {
+            const bool sa = sort_beside_aux<f16_t>(D, a, L, ws);
+            if ((rc = keys_typed<f16_t>(D, a, L, ws, st, sa))) return rc;
+            return queries_typed<f16_t>(D, a, L, ws, st, sa);
+        }
     }
     return SSA_E_ARG;
 }
@@ -4224,7 +4360,7 @@ int project_build_impl(const ssa_project_graph_args *pa, void *workspace, int64_
     // the bucket sort's segment counter starts at zero
     kp.zero1 = ssa_sort_counter((uint16_t *)(ws + L.sorttmp), (int)(D.BK * D.R), D.M);
     if ((rc = ssa_launch_project(kp, st))) return rc;
-    if ((rc = keys_typed<bf16_t>(D, a, L, ws, st))) return rc;
+    if ((rc = keys_typed<bf16_t>(D, a, L, ws, st, false))) return rc;
     ProjP qp{};
     qp.x = pa->x; qp.ldx = pa->d_model;
     qp.w = pa->wq; qp.ldw = pa->d_model;
@@ -4241,7 +4377,7 @@ int project_build_impl(const ssa_project_graph_args *pa, void *workspace, int64_
     qp.knorm = (const uint32_t *)(ws + L.knorm);
     qp.aux = (float *)(ws + L.aux);
     if ((rc = ssa_launch_project(qp, st))) return rc;
-    return queries_typed<bf16_t>(D, a, L, ws, st);
+    return queries_typed<bf16_t>(D, a, L, ws, st, false);
 }
 
 }  // namespace

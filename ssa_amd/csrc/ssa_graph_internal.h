@@ -12,6 +12,22 @@ int64_t ssa_sort_tmp_bytes(int rows, int n);
 // the segment counter inside the sort's scratch `tmp`: it must be 0 when the
 // sort starts (counter_clear: the sort clears it itself; else the caller has)
 int32_t *ssa_sort_counter(uint16_t *tmp, int rows, int n);
+// The bucket sort's top levels as a caller launches them itself (rows of at
+// most 32768 keys: 16-bit positions, the row in LDS): sort_top_row's
+// arguments, the dynamic LDS it needs, then kernel B after it.
+struct SortTopArgs {
+    const uint16_t *ids;
+    int rows, n, NB;
+    int32_t *perm, *bstart, *bsize;
+    uint32_t *gkv;
+    int4 *segs;
+    int *segcount;
+    unsigned char *glb;
+    int tl_in_lds, cap, lds;
+};
+int ssa_sort_top_setup(const uint16_t *ids, int rows, int n, int P, int32_t *perm,
+                       int32_t *bstart, int32_t *bsize, uint16_t *tmp, SortTopArgs *a);
+int ssa_launch_sort_seg(const SortTopArgs &a, hipStream_t st);
 int ssa_launch_bucket_sort(const uint16_t *ids, int rows, int n, int P, int32_t *perm,
                            int32_t *bstart, int32_t *bsize, uint16_t *tmp, hipStream_t st,
                            bool counter_clear = true);
