@@ -239,6 +239,51 @@ def recall_at_32(q, k, nb, va, rep, causal_variant=False):
     return res[0], sum(res) / len(res)
 
 
+def select_read_stats(attn, q, k, N):
+    """What select_kernel reads per query row at this workload (causal self
+    attention, B=1), from the same hashing, permutation and cut rules on the
+    device: per (row, list) the members below the query (the sorted list's
+    prefix), the 64-member chunks that cover them, and the bytes those chunks
+    load (4 B member id + 2 B score code per lane, whole chunks) against the
+    bytes of the members themselves.  The permutation is torch.sort's on the
+    host (the reference's, which the library reproduces)."""
+    import torch
+    lb = attn.lsh_builder
+    C, R = lb.C, lb.rand_proj.shape[0]
+    P = lb.compute_effective_p(N, C, lb.max_P)
+    Hq, Hkv, rep = attn.H, attn.n_kv, attn.kv_rep
+    planes = lb.rand_proj[:, :P].float()                                   # (R, P, d)
+    w = (2 ** torch.arange(P, device=q.device)).view(1, 1, P)
+    members = torch.zeros(Hq, N, device=q.device)
+    chunks = torch.zeros(Hq, N, device=q.device)
+    nlists = 0
+    for r in range(R):
+        kid = ((k[0].float() @ planes[r].T > 0).long() * w).sum(-1)        # (Hkv, M)
+        qid = ((q[0].float() @ planes[r].T > 0).long() * w).sum(-1)        # (Hq, N)
+        for g in range(Hkv):
+            perm = torch.sort(kid[g].cpu(), dim=-1)[1].to(q.device)        # the reference's order
+            skey = kid[g][perm]
+            for h in range(g * rep, (g + 1) * rep):
+                cut = torch.zeros(N, device=q.device)
+                for u in range(2 ** P):
+                    sel = perm[skey == u][:C]                               # the list: first C members
+                    lst = torch.sort(sel)[0]
+                    rows = qid[h] == u
+                    n = torch.arange(N, device=q.device)[rows]
+                    cut[rows] = torch.searchsorted(lst, n).float()          # members below the query
+                members[h] += cut
+                chunks[h] += torch.ceil(cut / 64)
+        nlists += 1
+    loaded = chunks * 64 * 6
+    needed = members * 6
+    return {"lists_per_row": nlists, "members_per_row": members.mean().item(),
+            "chunks_per_row": chunks.mean().item(),
+            "chunk_fill": (members.sum() / (chunks.sum() * 64)).item(),
+            "bytes_loaded_per_row": loaded.mean().item(),
+            "bytes_of_members_per_row": needed.mean().item(),
+            "cut_and_aux_bytes_per_row": nlists * 20 + (attn.config.num_global_tokens + 3) * 4}
+
+
 # the apply kernel the bf16 workload launches (16-bit packed path)
 APPLY_KERNEL = "apply_fwd16_kernel"
 
@@ -431,6 +476,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-recall", action="store_true")
+    ap.add_argument("--select-stats", action="store_true",
+                    help="also report what select_kernel reads per query row (select_reads)")
     ap.add_argument("--workload", default="gqa_n4096",
                     choices=["gqa_n4096"] + sorted(OTHER),
                     help="gqa_n4096 (default): the bf16 GQA N=4096 workload above")
@@ -559,6 +606,9 @@ def main():
         "tie_rows": tie_rows, "query_rows": B * H * N,
         "recall_at_32": rec,
     }
+    if args.select_stats:
+        with torch.no_grad():
+            line["select_reads"] = select_read_stats(attn, q, k, N)
     if not args.no_cpu:
         cb = cpu_baseline(attn)
         line["cpu_baseline"] = cb
