@@ -114,6 +114,7 @@ struct HashP {
     int key_layout;
     int vec16;          // rows 16-byte aligned: quarter rows load with 16-byte loads
     int64_t rows;
+    int pl16;           // planes 16-byte aligned with d % 4 == 0: planes load with 16-byte loads
     uint32_t *zero;     // block 0 clears zero[0..nzero) and *zero1 (later kernels'
     int nzero;          // accumulator and counter; either may be null)
     int32_t *zero1;
@@ -192,35 +193,29 @@ __global__ void __launch_bounds__(256) hash_kernel(HashP p) {
 // of rows x planes, lane l feeding row (l % 16) and plane (l % 16) with the
 // element k = l / 16 of the step.  The reduction over the head dim is split so
 // that lane group g = l / 16 walks the contiguous quarter [g*d/4, (g+1)*d/4):
-// every lane loads its quarter row once with wide loads.  The block stages all
-// R*P planes in LDS once (fp32, row stride D+1); each wavefront then takes
-// HASH_TILES tiles of 16 rows against them.  D is the instance's head dim; the
-// rows' own d <= D: elements past d are zero in the rows and the planes.
-constexpr int HASH_TILES = 1;
+// every lane loads its quarter row once with wide loads, and quarter lg of
+// plane 16 t + li straight from global memory into registers (the planes are
+// L2-resident after the first waves): no staging loop and no barrier precede
+// the products.  Each wavefront takes one tile of 16 rows.  D is the
+// instance's head dim; the rows' own d <= D: elements past d are zero in the
+// rows and the planes.
 template <typename T, int D>
 __global__ void __launch_bounds__(256) hash_mfma_kernel(HashP p) {
     constexpr int DQ = D / 4;
+    constexpr int CH = DQ < 32 ? DQ : 32;             // plane elements loaded per group
     extern __shared__ float hs[];
     const int NP = p.R * p.P;
     const int NT = (NP + 15) / 16;
-    float *W = hs;                                    // [NT*16][D+1]
-    float *proj = W + NT * 16 * (D + 1);              // [4 waves][16][NT*16 + 1]
+    float *proj = hs;                                 // [4 waves][16][NT*16 + 1]
     const int pst = NT * 16 + 1;
     hash_clear(p);
     const int wid = threadIdx.x / SSA_WAVE;
     const int lane = lane_id();
-    // plane j (round j / P, hash j % P) is staged by wave j % 4, D / 64 elements a lane
-    for (int j = wid; j < NT * 16; j += 4) {
-        const bool real = j < NP;
-        const float *src = p.planes + (real ? ((int64_t)(j / p.P) * p.maxP + (j % p.P)) * p.d : 0);
-        for (int e = lane; e < D; e += SSA_WAVE) W[j * (D + 1) + e] = (real && e < p.d) ? src[e] : 0.f;
-    }
-    __syncthreads();
     const int li = lane % 16, lg = lane / 16;
-    for (int tile = 0; tile < HASH_TILES; ++tile) {
-        // the block's 4 waves take adjacent 16-row tiles at each step
-        const int64_t row0 = (((int64_t)blockIdx.x * HASH_TILES + tile) * 4 + wid) * 16;
-        if (row0 >= p.rows) break;
+    {
+        // the block's 4 waves take adjacent 16-row tiles
+        const int64_t row0 = ((int64_t)blockIdx.x * 4 + wid) * 16;
+        if (row0 >= p.rows) return;
         const int64_t row = row0 + li;
         float xs[DQ];
         if (row < p.rows) {
@@ -266,12 +261,39 @@ __global__ void __launch_bounds__(256) hash_mfma_kernel(HashP p) {
             if (lane == 0) p.kpart[row0 / 16] = m;
         }
         float *pw = proj + wid * 16 * pst;
+        const int dq = p.d - lg * DQ;                 // this quarter's elements below d
         for (int t = 0; t < NT; ++t) {
+            // plane j = 16 t + li: round j / P, hash j % P; zero past the R*P planes
+            const int j = t * 16 + li;
+            const bool real = j < NP;
+            const float *wr =
+                p.planes + (real ? ((int64_t)(j / p.P) * p.maxP + (j % p.P)) * p.d : 0) + lg * DQ;
             f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-            const float *wr = W + (t * 16 + li) * (D + 1) + lg * DQ;
 #pragma unroll
-            for (int s = 0; s < DQ; ++s)
-                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xs[s], wr[s], acc, 0, 0, 0);
+            for (int s0 = 0; s0 < DQ; s0 += CH) {
+                float wv[CH];
+                bool wide = false;
+                if constexpr (CH % 4 == 0) {
+                    // 16-byte aligned rows of a multiple of 4 floats: a piece
+                    // starting below d lies wholly below it
+                    wide = p.pl16 != 0;
+                    if (wide) {
+#pragma unroll
+                        for (int u = 0; u < CH; u += 4) {
+                            float4 w = make_float4(0.f, 0.f, 0.f, 0.f);
+                            if (real && s0 + u < dq) w = *reinterpret_cast<const float4 *>(wr + s0 + u);
+                            wv[u] = w.x; wv[u + 1] = w.y; wv[u + 2] = w.z; wv[u + 3] = w.w;
+                        }
+                    }
+                }
+                if (!wide) {
+#pragma unroll
+                    for (int u = 0; u < CH; ++u) wv[u] = (real && s0 + u < dq) ? wr[s0 + u] : 0.f;
+                }
+#pragma unroll
+                for (int u = 0; u < CH; ++u)
+                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xs[s0 + u], wv[u], acc, 0, 0, 0);
+            }
 #pragma unroll
             for (int r = 0; r < 4; ++r) pw[(4 * lg + r) * pst + t * 16 + li] = acc[r];
         }
@@ -279,16 +301,18 @@ __global__ void __launch_bounds__(256) hash_mfma_kernel(HashP p) {
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         if (p.key_layout) {
-            if (lane < 16 && row0 + lane < p.rows) {
-                const int64_t rw = row0 + lane;
-                const int i = (int)(rw % p.L);
-                const int64_t bh = rw / p.L;
-                for (int r = 0; r < p.R; ++r) {
-                    const float *pr = pw + lane * pst + r * p.P;
+            // one (round, row) pair per lane, the 16 rows of a round on
+            // consecutive lanes (consecutive ids in the key layout)
+            for (int x0 = 0; x0 < 16 * p.R; x0 += SSA_WAVE) {
+                const int x = x0 + lane;
+                const int r = x / 16, rl = x % 16;
+                const int64_t rw = row0 + rl;
+                if (r < p.R && rw < p.rows) {
+                    const float *pr = pw + rl * pst + r * p.P;
                     int id = 0;
                     for (int j = 0; j < p.P; ++j)
                         if (pr[j] > 0.f) id |= 1 << j;
-                    p.out[(bh * p.R + r) * p.L + i] = (uint16_t)id;
+                    p.out[((rw / p.L) * p.R + r) * p.L + rw % p.L] = (uint16_t)id;
                 }
             }
         } else {
@@ -301,10 +325,6 @@ __global__ void __launch_bounds__(256) hash_mfma_kernel(HashP p) {
                     ssa_write_ids(pw + rl * pst + r * p.P, p.P, p.Tp, p.out + ((row0 + rl) * p.R + r) * p.NS);
             }
         }
-        // this wave's projection rows are rewritten by its next tile
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
 }
 
@@ -3623,15 +3643,15 @@ int make_dims(const ssa_graph_args *a, Dims &D, bool need_q = true, int64_t ws_c
 template <typename T, int Dh>
 int launch_hash_mfma(const HashP &hp, hipStream_t st) {
     const int NT = (hp.R * hp.P + 15) / 16;
-    const size_t lds = ((size_t)NT * 16 * (Dh + 1) + (size_t)4 * 16 * (NT * 16 + 1)) * 4;
+    const size_t lds = (size_t)4 * 16 * (NT * 16 + 1) * 4;
     if (lds > SSA_LDS_BYTES) {
-        ssa_set_error("hash: %d planes x d=%d need %zu bytes of LDS", hp.R * hp.P, Dh, lds);
+        ssa_set_error("hash: %d planes need %zu bytes of LDS", hp.R * hp.P, lds);
         return SSA_E_UNSUP;
     }
     SSA_CHECK_HIP(hipFuncSetAttribute((const void *)hash_mfma_kernel<T, Dh>,
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    hipLaunchKernelGGL((hash_mfma_kernel<T, Dh>), dim3((unsigned)ceil_div(hp.rows, 64 * HASH_TILES)),
-                       dim3(256), lds, st, hp);
+    hipLaunchKernelGGL((hash_mfma_kernel<T, Dh>), dim3((unsigned)ceil_div(hp.rows, 64)), dim3(256),
+                       lds, st, hp);
     SSA_CHECK_LAUNCH();
     return SSA_OK;
 }
@@ -3676,6 +3696,7 @@ int launch_hash(const Dims &D, const ssa_graph_args *a, const Layout &L, char *w
     HashP hp{};
     hp.planes = a->rand_proj;
     hp.R = D.R; hp.maxP = D.maxP; hp.P = D.P; hp.Tp = D.Tp; hp.NS = D.NS; hp.d = D.d;
+    hp.pl16 = (a->rand_proj && (uintptr_t)a->rand_proj % 16 == 0 && D.d % 4 == 0) ? 1 : 0;
     if (keys) {
         hp.x = a->k.ptr; hp.sb = a->k.sb; hp.sh = a->k.sh; hp.sn = a->k.sn;
         hp.nh = D.Hkv; hp.L = D.M; hp.inj = a->k_proj; hp.key_layout = 1;
