@@ -111,6 +111,37 @@ __device__ __forceinline__ float drop_scale_of(const ApplyP &p) {
     return p.fp32w ? p.drop_scale : Cvt<T>::round(p.drop_scale);
 }
 
+// A query row's graph slots j0 + u * 64 + lane (u < NB): the ids (int32 graph,
+// or int64 ids and the mask) of all NB groups are loaded before any is used,
+// so the row pays one memory latency for them instead of one per group.  The
+// loads are unconditional (lanes past the row read its last slot) and the
+// graph's layout is a template parameter, so no branch separates a load from
+// the others.
+constexpr int APPLY_SLOT_BATCH = 4;
+template <int NB, bool I32>
+struct RowSlots {
+    int64_t y[NB];
+    uint8_t v[NB];
+    __device__ __forceinline__ void load(const ApplyP &p, int64_t row, const int64_t *nb,
+                                         const uint8_t *va, int j0, int lane) {
+#pragma unroll
+        for (int u = 0; u < NB; ++u) {
+            const int j = min(j0 + u * SSA_WAVE + lane, p.K - 1);
+            if constexpr (I32) {
+                y[u] = p.nb32[row * p.K + j];
+            } else {
+                y[u] = nb[j];
+                v[u] = va ? va[j] : (uint8_t)1;
+            }
+        }
+    }
+    // the slot is marked invalid: mask false, or a negative id in an int32 graph
+    __device__ __forceinline__ bool marked(int u) const {
+        if constexpr (I32) return y[u] < 0;
+        else return v[u] == 0;
+    }
+};
+
 template <typename T, int D, int U>
 __global__ void __launch_bounds__(WAVES * SSA_WAVE)
 apply_fwd_kernel(ApplyP p) {
@@ -139,28 +170,36 @@ apply_fwd_kernel(ApplyP p) {
     const int64_t *nb = p.nb ? p.nb + row * p.K : nullptr;
     const uint8_t *va = p.valid ? p.valid + row * p.K : nullptr;
 
+    // lanes whose elements lie past the head dim hold zeros and store nothing
+    const bool live = li * VEC < p.d;
+    const int lofs = live ? li * VEC : 0;
+    // the q row is loaded first, beside the row's graph slots below
+    float qf[VEC];
+    load_vec<T, VEC>(qrow + lofs, qf);
+
     // neighbour ids once, as int32 in LDS; masked or out-of-range slots -> -1.
     // The row's padding count is the reference's (sparse_attention.py:1508):
     // slots the graph marks invalid (mask false, or a negative id in an int32
     // graph); an out-of-range id marked valid is skipped here but not counted
     int ninv = 0;
-    for (int j0 = 0; j0 < p.K; j0 += SSA_WAVE) {
-        const int j = j0 + lane;
-        bool o = false, marked = false;
-        if (j < p.K) {
-            const int64_t x = p.nb32 ? (int64_t)p.nb32[row * p.K + j] : nb[j];
-            marked = p.nb32 ? x < 0 : (va ? va[j] == 0 : false);
-            o = !marked && x >= 0 && x < p.M;
-            ix[j] = o ? (int)x : -1;
+    auto slots = [&](auto i32) __attribute__((always_inline)) {
+        for (int j0 = 0; j0 < p.K; j0 += APPLY_SLOT_BATCH * SSA_WAVE) {
+            RowSlots<APPLY_SLOT_BATCH, decltype(i32)::value> rs;
+            rs.load(p, row, nb, va, j0, lane);
+#pragma unroll
+            for (int u = 0; u < APPLY_SLOT_BATCH; ++u) {
+                const int j = j0 + u * SSA_WAVE + lane;
+                const bool in = j < p.K;
+                const bool marked = in && rs.marked(u);
+                const int64_t x = rs.y[u];
+                if (in) ix[j] = (!marked && x >= 0 && x < p.M) ? (int)x : -1;
+                ninv += __popcll(wave_ballot(marked));
+            }
         }
-        ninv += __popcll(wave_ballot(marked));
-    }
+    };
+    if (p.nb32) slots(std::true_type{});
+    else slots(std::false_type{});
     if (p.row_inv && lane == 0) p.row_inv[row] = ninv;
-    // lanes whose elements lie past the head dim hold zeros and store nothing
-    const bool live = li * VEC < p.d;
-    const int lofs = live ? li * VEC : 0;
-    float qf[VEC];
-    load_vec<T, VEC>(qrow + lofs, qf);
 #pragma unroll
     for (int e = 0; e < VEC; ++e) qf[e] = live ? qf[e] : 0.f;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -520,23 +559,31 @@ apply_fwd16_kernel(ApplyP p) {
     const int64_t *nb = p.nb ? p.nb + row * p.K : nullptr;
     const uint8_t *va = p.valid ? p.valid + row * p.K : nullptr;
 
+    // the q row is loaded first, beside the row's graph slots below
+    uint4 q4 = *reinterpret_cast<const uint4 *>(qrow + (live ? li * 8 : 0));
+
     // neighbour ids as int32 in LDS (ids < 2^24, checked at dispatch); the
     // padding count takes the slots the graph marks invalid, as above
     int ninv = 0;
-    for (int j0 = 0; j0 < Kp; j0 += SSA_WAVE) {
-        const int j = j0 + lane;
-        int x = INT32_MIN;
-        bool marked = false;
-        if (j < p.K) {
-            const int64_t y = p.nb32 ? (int64_t)p.nb32[row * p.K + j] : nb[j];
-            marked = p.nb32 ? y < 0 : (va ? va[j] == 0 : false);
-            if (!marked && y >= 0 && y < p.M) x = (int)y;
+    auto slots = [&](auto i32) __attribute__((always_inline)) {
+        for (int j0 = 0; j0 < Kp; j0 += APPLY_SLOT_BATCH * SSA_WAVE) {
+            RowSlots<APPLY_SLOT_BATCH, decltype(i32)::value> rs;
+            rs.load(p, row, nb, va, j0, lane);
+#pragma unroll
+            for (int u = 0; u < APPLY_SLOT_BATCH; ++u) {
+                const int j = j0 + u * SSA_WAVE + lane;
+                const bool in = j < p.K;
+                const bool marked = in && rs.marked(u);
+                const int64_t y = rs.y[u];
+                const int x = (in && !marked && y >= 0 && y < p.M) ? (int)y : INT32_MIN;
+                if (j < Kp) ix[j] = x;
+                ninv += __popcll(wave_ballot(marked));
+            }
         }
-        ix[j] = x;
-        ninv += __popcll(wave_ballot(marked));
-    }
+    };
+    if (p.nb32) slots(std::true_type{});
+    else slots(std::false_type{});
     if (p.row_inv && lane == 0) p.row_inv[row] = ninv;
-    uint4 q4 = *reinterpret_cast<const uint4 *>(qrow + (live ? li * 8 : 0));
     if (!live) q4 = make_uint4(0, 0, 0, 0);
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -575,6 +622,18 @@ apply_fwd16_kernel(ApplyP p) {
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
+    // the first P.V step's V rows (they need only the ids) load while the
+    // softmax runs
+    uint4 vv0[U];
+    {
+        int xi[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) xi[u] = ix[u * RPI + sub];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            vv0[u] = *reinterpret_cast<const uint4 *>(vb + (__umul24((uint32_t)xi[u], vrb) + lio));
+    }
+
     // ---- fp32 softmax; p rounded to the value dtype (inverted dropout on p);
     // padding slots get p = 0
     float m = -INFINITY;
@@ -606,18 +665,10 @@ apply_fwd16_kernel(ApplyP p) {
     float acc[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] = 0.f;
-    for (int j0 = 0; j0 < Kp; j0 += STEP) {
-        int xi[U];
+    auto vstep = [&](int j0, const uint4 (&vv)[U]) __attribute__((always_inline)) {
         float pj[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-            xi[u] = ix[j0 + u * RPI + sub];
-            pj[u] = sc[j0 + u * RPI + sub];
-        }
-        uint4 vv[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-            vv[u] = *reinterpret_cast<const uint4 *>(vb + (__umul24((uint32_t)xi[u], vrb) + lio));
+        for (int u = 0; u < U; ++u) pj[u] = sc[j0 + u * RPI + sub];
 #pragma unroll
         for (int u = 0; u < U; u += 2) {
             const uint32_t pp = Dot2<T>::pack(pj[u], pj[u + 1]);
@@ -631,6 +682,17 @@ apply_fwd16_kernel(ApplyP p) {
                                               acc[2 * r + 1]);
             }
         }
+    };
+    vstep(0, vv0);
+    for (int j0 = STEP; j0 < Kp; j0 += STEP) {
+        int xi[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) xi[u] = ix[j0 + u * RPI + sub];
+        uint4 vv[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            vv[u] = *reinterpret_cast<const uint4 *>(vb + (__umul24((uint32_t)xi[u], vrb) + lio));
+        vstep(j0, vv);
     }
 #pragma unroll
     for (int o = LPR; o < SSA_WAVE; o <<= 1)
