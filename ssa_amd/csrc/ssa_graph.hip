@@ -1958,8 +1958,14 @@ select_kernel(SelP p) {
     const int64_t blk = xcd_logical_block(blockIdx.x, p.nblocks);
     if (blk >= p.nblocks) return;
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / SSA_WAVE);   // wave-uniform
-    const int64_t rloc = blk * SEL_WAVES + wid;
-    if (rloc >= p.rows) return;
+    const int64_t rd = blk * SEL_WAVES + wid;
+    if (rd >= p.rows) return;
+    // causal rows cost more the later their position (more members below the
+    // query): a head's rows go in descending position, so the launch ends on
+    // its cheapest rows instead of its dearest
+    const int64_t rloc =
+        CAUSAL ? (int64_t)((uint32_t)rd / (uint32_t)p.N) * p.N + (p.N - 1 - (int)((uint32_t)rd % (uint32_t)p.N))
+               : rd;
     const int lane = lane_id();
     const int nl = p.nlists;
     int4 *lch = (int4 *)(sel_smem + (int64_t)wid * sel_lds_words(p.words, p.kk, LSH_MODE, nl, CAP));
