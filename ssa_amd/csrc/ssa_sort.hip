@@ -59,6 +59,39 @@ sort_top_kernel(const uint16_t *ids, int n, int NB, int32_t *perm, int32_t *bsta
 // the reference's final insertion pass over the row), and its slice of perm.
 constexpr int SEG_WAVES = 4;
 constexpr int SEG_STACK = SEG_T / (LEAF + 1) + 2;
+constexpr int SEG_PER_LANE = SEG_T / SSA_WAVE;
+
+// A segment whose keys are all equal: libstdc++'s partitions then depend on
+// its length alone.  The median of three (first + 1, middle, last - 1) is the
+// middle element, moved to the front; the unguarded scan stops at every
+// element, so it swaps positions k and n - k for 1 <= k < n / 2 and cuts at
+// ceil(n / 2); both halves recurse the same way down to leaves of LEAF, whose
+// insertion sort moves nothing.  So an element's final slot follows from its
+// position in O(log n) steps, and the subtree is one permutation.
+__device__ __forceinline__ int eq_final_pos(int n, int i) {
+    int base = 0;
+    while (n > LEAF) {
+        const int h = n >> 1;
+        i = i == 0 ? h : (i == h ? 0 : i);
+        if (i != 0 && 2 * i != n) i = n - i;
+        const int c = (n + 1) >> 1;
+        if (i < c) {
+            n = c;
+        } else {
+            base += c;
+            i -= c;
+            n -= c;
+        }
+    }
+    return base + i;
+}
+// partition levels the closed form takes (the larger half each time): the
+// subtree reaches no depth limit when the segment's depth is at least this
+__device__ __forceinline__ int eq_levels(int n) {
+    int l = 0;
+    for (; n > LEAF; n = (n + 1) >> 1) ++l;
+    return l;
+}
 
 template <typename Pos>
 __host__ __device__ constexpr int seg_lds_words() {
@@ -89,10 +122,33 @@ sort_seg_kernel(const typename SortWords<Pos>::W *gkv, int n, const int4 *segs,
         const int4 e = segs[sgi];
         const int row = e.x, f0 = e.y, m = e.z, depth0 = e.w;
         const W *src = gkv + (int64_t)row * n + f0;
-        for (int i = lane; i < m; i += SSA_WAVE) {
-            const W v = src[i];
-            key[i] = (uint16_t)(v & 0xffffu);
-            idx[i] = (Pos)(v >> SH);
+        int32_t *pout = perm + (int64_t)row * n + f0;
+        W rv[SEG_PER_LANE];
+        uint32_t kmin = 0xffffu, kmax = 0u;
+#pragma unroll
+        for (int u = 0; u < SEG_PER_LANE; ++u) {
+            const int i = lane + SSA_WAVE * u;
+            rv[u] = src[min(i, m - 1)];
+            const uint32_t k = (uint32_t)(rv[u] & 0xffffu);
+            kmin = min(kmin, k);
+            kmax = max(kmax, k);
+        }
+        if (wave_min_u(kmin) == wave_max_u(kmax) && depth0 >= eq_levels(m)) {
+            // every key equal: the segment's permutation in closed form
+#pragma unroll
+            for (int u = 0; u < SEG_PER_LANE; ++u) {
+                const int i = lane + SSA_WAVE * u;
+                if (i < m) pout[eq_final_pos(m, i)] = (int32_t)(Pos)(rv[u] >> SH);
+            }
+            continue;
+        }
+#pragma unroll
+        for (int u = 0; u < SEG_PER_LANE; ++u) {
+            const int i = lane + SSA_WAVE * u;
+            if (i < m) {
+                key[i] = (uint16_t)(rv[u] & 0xffffu);
+                idx[i] = (Pos)(rv[u] >> SH);
+            }
         }
         for (int w = lane; w < SEG_T / 32 + 1; w += SSA_WAVE) bits[w] = w == 0 ? 1u : 0u;
         wave_sync_lds();
@@ -106,6 +162,39 @@ sort_seg_kernel(const typename SortWords<Pos>::W *gkv, int n, const int4 *segs,
                 const int a = (int)(se & 0xffffu), b = (int)(se >> 16);
                 const int d = (int)sdep[top];
                 wave_sync_lds();
+                {
+                    // a sub-segment whose keys are all equal: its subtree in
+                    // closed form, each slot then a leaf of its own
+                    uint32_t smin = 0xffffu, smax = 0u;
+#pragma unroll
+                    for (int u = 0; u < SEG_PER_LANE; ++u) {
+                        const int i = a + lane + SSA_WAVE * u;
+                        if (i < b) {
+                            const uint32_t k = key[i];
+                            smin = min(smin, k);
+                            smax = max(smax, k);
+                        }
+                    }
+                    if (wave_min_u(smin) == wave_max_u(smax) && d >= eq_levels(b - a)) {
+                        Pos iv[SEG_PER_LANE];
+#pragma unroll
+                        for (int u = 0; u < SEG_PER_LANE; ++u) {
+                            const int i = a + lane + SSA_WAVE * u;
+                            iv[u] = i < b ? idx[i] : (Pos)0;
+                        }
+                        wave_sync_lds();
+#pragma unroll
+                        for (int u = 0; u < SEG_PER_LANE; ++u) {
+                            const int i = lane + SSA_WAVE * u;
+                            if (a + i < b) {
+                                idx[a + eq_final_pos(b - a, i)] = iv[u];
+                                atomicOr(&bits[(a + i) >> 5], 1u << ((a + i) & 31));
+                            }
+                        }
+                        wave_sync_lds();
+                        continue;
+                    }
+                }
                 if (d == 0) {
                     if (lane == 0) heap_sort_range(key, idx, a, b);
                     wave_sync_lds();
@@ -148,7 +237,6 @@ sort_seg_kernel(const typename SortWords<Pos>::W *gkv, int n, const int4 *segs,
             }
         }
         wave_sync_lds();
-        int32_t *pout = perm + (int64_t)row * n + f0;
         for (int i = lane; i < m; i += SSA_WAVE) pout[i] = (int32_t)idx[i];
         wave_sync_lds();
     }

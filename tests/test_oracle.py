@@ -41,6 +41,38 @@ def test_sort_perm_matches_torch_sort(rows, M, P, dist):
         np.testing.assert_array_equal(oracle.sort_perm(k[r]), ref[r])
 
 
+def _equal_keys_final_slot(n, i):
+    """Final slot of the element at position i of an introsort segment of n
+    equal keys: the closed form the device's segment sort applies to such
+    segments (ssa_sort.hip, eq_final_pos), restated."""
+    base = 0
+    while n > 16:
+        h = n // 2
+        i = h if i == 0 else (0 if i == h else i)       # median of three: first <-> middle
+        if i != 0 and 2 * i != n:                        # the scan swaps k and n - k
+            i = n - i
+        c = (n + 1) // 2                                 # and cuts at ceil(n / 2)
+        if i < c:
+            n = c
+        else:
+            base, i, n = base + c, i - c, n - c
+    return base + i
+
+
+@pytest.mark.parametrize("n", list(range(1, 70)) + [255, 256, 257, 511, 1000, 1023, 1024, 4096,
+                                                     5000, 32768])
+def test_equal_key_segment_permutation_closed_form(n):
+    """A segment of equal keys sorts (torch.sort's introsort) into a
+    permutation fixed by its length alone, which the closed form gives."""
+    # 2-D like the reference's rows (a 1-D sort of 32768+ int keys takes a radix path)
+    ref = torch.sort(torch.zeros((1, n), dtype=torch.int64), dim=-1)[1].numpy()[0]
+    np.testing.assert_array_equal(oracle.sort_perm(np.zeros(n, dtype=np.int64)), ref)
+    mine = np.empty(n, dtype=np.int64)
+    for i in range(n):
+        mine[_equal_keys_final_slot(n, i)] = i
+    np.testing.assert_array_equal(mine, ref)
+
+
 def test_sort_is_not_stable_so_emulation_matters():
     k = RNG.integers(0, 8, (1, 4096)).astype(np.int64)
     uns = torch.sort(torch.from_numpy(k), dim=-1)[1].numpy()
