@@ -397,7 +397,6 @@ struct QbP {
     int32_t *tcnt;          // tiles per instance
     int32_t *kbase;         // first tile of each order key
     int32_t *hcnt;          // per (instance, query block, bucket): count, then first position
-    int32_t *qpos;          // per (instance, query): position in qlist
     int N, R, NS, NB, Hq, Hkv, rep, bh0, ninst, C;
     int64_t heads;          // (kv head, group head) pairs the order keys span
     int rmajor;             // tile order by (round, id set) first (see qb_order_key)
@@ -615,7 +614,75 @@ __device__ void qb_write_tiles(const QbP &p, int inst, int bh, int r, int t, int
     }
 }
 
-__global__ void __launch_bounds__(256) qb_scatter_kernel(QbP p) {
+constexpr int LS_RANK_MIN = 128;   // lists at least this long are ranked through a bitmap
+
+struct CutP {
+    const int32_t *perm, *bstart, *bsize, *sid, *smin;
+    const int64_t *glob;
+    int4 *cut;
+    int32_t *srix;     // per (row, list): offset of the query's score row in its head's
+                       // region of S (lists * N * C elements), in elements
+    const uint2 *ctab; // optional: the list sort's rank table of long lists
+    int N, M, R, NS, NB, C, Cs, Hq, Hkv, rep, bh0, G, causal, nlists;
+    int64_t rows;
+};
+
+// The cut entry of query row rloc (chunk-relative) and list `list` (round,
+// id set), whose bucket is u and whose position in its bucket's query list
+// is pos: written by the query scatter, which has both at hand.
+__device__ void cut_entry(const CutP &p, int64_t rloc, int list, int u, int pos) {
+    const int64_t x = rloc * p.nlists + list;
+    const int n = (int)(rloc % p.N);
+    const int bh = p.bh0 + (int)(rloc / p.N);
+    const int b = bh / p.Hq, h = bh % p.Hq, g = h / p.rep;
+    const int64_t prow = ((int64_t)b * p.Hkv + g) * p.R + list / p.NS;
+    const int st = p.bstart[prow * p.NB + u];
+    const int sz = p.bsize[prow * p.NB + u];
+    const int f = p.perm[prow * p.M + p.M - 1];   // key of the overflow filler slots
+    int cutoff = 0, first = p.C, real = 0;
+    if (sz == 0) {
+        if (p.causal) {
+            const int gl = min(p.G, p.C);
+            for (int j = 0; j < gl; ++j)
+                if ((int)p.glob[j] == n) { first = j; break; }
+            if (first == p.C && n == 0 && p.G < p.C) first = p.G;
+            real = 1;
+        }
+    } else {
+        const int nv = min(sz, p.C);
+        if (p.causal) {
+            if (p.ctab && nv >= LS_RANK_MIN) {
+                // members with id < n: those below n's 32-id word, then its bits
+                const uint2 e = p.ctab[(prow * p.NB + u) * (int64_t)((p.M + 31) / 32) + (n >> 5)];
+                cutoff = (int)e.x + __popc(e.y & ((1u << (n & 31)) - 1u));
+            } else {
+                const int32_t *sd = p.sid + prow * p.M + st;
+                int lo = 0, hi = nv;               // members with id < n
+                while (lo < hi) {
+                    const int mid = (lo + hi) >> 1;
+                    if (sd[mid] < n) lo = mid + 1; else hi = mid;
+                }
+                cutoff = lo;
+            }
+            const int a = cutoff < nv ? p.smin[prow * p.M + st + cutoff] : p.C;
+            const int fb = (sz < p.C && f >= n) ? sz : p.C;
+            first = min(a, fb);
+            real = a < fb ? 1 : 0;
+        } else {
+            cutoff = nv;
+        }
+    }
+    // 16-bit fields, read back as unsigned: the list size capped at C (every
+    // use compares it with 0 and C or takes min(size, C)), the filler key and
+    // the cutoff below 2^16, the bucket start below M <= 65536
+    p.cut[x] = make_int4((int)(prow * p.M) + st,
+                         (int)((uint32_t)min(sz, p.C) | ((uint32_t)f << 16)),
+                         (int)((uint32_t)cutoff | ((uint32_t)st << 16)), first * 2 + real);
+    p.srix[x] = (int32_t)(((int64_t)list * p.N + pos) * p.Cs);
+}
+
+
+__global__ void __launch_bounds__(256) qb_scatter_kernel(QbP p, CutP c) {
     // rank of each query among the block's queries of its bucket, in position
     // order: per wave the lanes of one bucket matched bit by bit (log2 NB
     // ballots), then the waves in order
@@ -647,7 +714,7 @@ __global__ void __launch_bounds__(256) qb_scatter_kernel(QbP p) {
         int pos = p.hcnt[((int64_t)inst * gridDim.x + blockIdx.x) * p.NB + u] + local;
         for (int w = 0; w < wid; ++w) pos += sc_smem[w * p.NB + u];
         p.qlist[(int64_t)inst * p.N + pos] = n;
-        p.qpos[(int64_t)inst * p.N + n] = pos;
+        cut_entry(c, (int64_t)(bh - p.bh0) * p.N + n, r * p.NS + t, u, pos);
     }
 }
 
@@ -1045,7 +1112,6 @@ rescore_mfma_kernel(RsP p) {
 //   rnk[st + c]  sorted index of the member at list slot c
 //   smin[st + i] smallest list slot among sorted members i.. (first future slot)
 //   inv[key]     permutation position of every key
-constexpr int LS_RANK_MIN = 128;   // lists at least this long are ranked through a bitmap
 
 struct LsP {
     const int32_t *perm, *bstart, *bsize;
@@ -1195,75 +1261,6 @@ __global__ void __launch_bounds__(256) list_sort_kernel(LsP p) {
 // {row offset of the bucket (kv-head/round row * M + start), size | filler
 // key << 16, cutoff | start << 16, first slot * 2 + (that slot is valid)};
 // first slot C: none.  Sizes, cutoffs, starts and keys stay below 2^16.
-struct CutP {
-    const uint16_t *qid;
-    const int32_t *perm, *bstart, *bsize, *sid, *smin, *qpos;
-    const int64_t *glob;
-    int4 *cut;
-    int32_t *srix;     // per (row, list): offset of the query's score row in its head's
-                       // region of S (lists * N * C elements), in elements
-    const uint2 *ctab; // optional: the list sort's rank table of long lists
-    int N, M, R, NS, NB, C, Cs, Hq, Hkv, rep, bh0, G, causal, nlists;
-    int64_t rows;
-};
-
-__global__ void __launch_bounds__(256) cut_kernel(CutP p) {
-    const int64_t x = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    if (x >= p.rows * p.nlists) return;
-    const int list = (int)(x % p.nlists);
-    const int64_t rloc = x / p.nlists;
-    const int n = (int)(rloc % p.N);
-    const int bh = p.bh0 + (int)(rloc / p.N);
-    const int b = bh / p.Hq, h = bh % p.Hq, g = h / p.rep;
-    const int64_t row = (int64_t)bh * p.N + n;
-    const int u = p.qid[row * p.R * p.NS + list];
-    const int64_t prow = ((int64_t)b * p.Hkv + g) * p.R + list / p.NS;
-    const int st = p.bstart[prow * p.NB + u];
-    const int sz = p.bsize[prow * p.NB + u];
-    const int f = p.perm[prow * p.M + p.M - 1];   // key of the overflow filler slots
-    int cutoff = 0, first = p.C, real = 0;
-    if (sz == 0) {
-        if (p.causal) {
-            const int gl = min(p.G, p.C);
-            for (int j = 0; j < gl; ++j)
-                if ((int)p.glob[j] == n) { first = j; break; }
-            if (first == p.C && n == 0 && p.G < p.C) first = p.G;
-            real = 1;
-        }
-    } else {
-        const int nv = min(sz, p.C);
-        if (p.causal) {
-            if (p.ctab && nv >= LS_RANK_MIN) {
-                // members with id < n: those below n's 32-id word, then its bits
-                const uint2 e = p.ctab[(prow * p.NB + u) * (int64_t)((p.M + 31) / 32) + (n >> 5)];
-                cutoff = (int)e.x + __popc(e.y & ((1u << (n & 31)) - 1u));
-            } else {
-                const int32_t *sd = p.sid + prow * p.M + st;
-                int lo = 0, hi = nv;               // members with id < n
-                while (lo < hi) {
-                    const int mid = (lo + hi) >> 1;
-                    if (sd[mid] < n) lo = mid + 1; else hi = mid;
-                }
-                cutoff = lo;
-            }
-            const int a = cutoff < nv ? p.smin[prow * p.M + st + cutoff] : p.C;
-            const int fb = (sz < p.C && f >= n) ? sz : p.C;
-            first = min(a, fb);
-            real = a < fb ? 1 : 0;
-        } else {
-            cutoff = nv;
-        }
-    }
-    // 16-bit fields, read back as unsigned: the list size capped at C (every
-    // use compares it with 0 and C or takes min(size, C)), the filler key and
-    // the cutoff below 2^16, the bucket start below M <= 65536
-    p.cut[x] = make_int4((int)(prow * p.M) + st,
-                         (int)((uint32_t)min(sz, p.C) | ((uint32_t)f << 16)),
-                         (int)((uint32_t)cutoff | ((uint32_t)st << 16)), first * 2 + real);
-    const int64_t inst = (rloc / p.N) * p.nlists + list;
-    p.srix[x] = (int32_t)(((int64_t)list * p.N + p.qpos[inst * p.N + n]) * p.Cs);
-}
-
 // ------------------------------------------------------------------ extra scores
 // Per query row: q.k_n (the key that replaces future candidates when causal,
 // :698-709) and q.k_glob[j], q.k_0 (the empty-bucket list, :711-737).  They
@@ -3446,7 +3443,7 @@ int64_t replay_glb_blocks(int W, int words, int64_t budget) {
 }
 
 struct Layout {
-    int64_t kid, qid, perm, bstart, bsize, sorttmp, sid, rnk, smin, inv, cut, srix, qpos, cnt, off,
+    int64_t kid, qid, perm, bstart, bsize, sorttmp, sid, rnk, smin, inv, cut, srix, cnt, off,
         cur,
         qlist, tiles, ntiles, tcnt, kbase, S,
         tie_list, tie_count, aux, psplit, knorm, kpart, rpscr, rpw, ctab, total;
@@ -3472,7 +3469,6 @@ Layout plan(const Dims &D) {
     L.inv = take(D.BK * D.R * D.M * 4);
     L.cut = take(nbh * D.N * D.nlists * 16);
     L.srix = take(nbh * D.N * D.nlists * 4);
-    L.qpos = take(ninst * D.N * 4);
     L.cnt = take(ninst * D.NB * 4);
     L.off = take(ninst * D.NB * 4);
     L.cur = take(ninst * ceil_div(D.N, 256) * D.NB * 4);   // per-block counts / bases
@@ -4140,7 +4136,6 @@ int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char 
         qp.off = (int32_t *)(ws + L.off);
         qp.cur = nullptr;
         qp.hcnt = (int32_t *)(ws + L.cur);
-        qp.qpos = (int32_t *)(ws + L.qpos);
         qp.qlist = (int32_t *)(ws + L.qlist);
         qp.tiles = (int32_t *)(ws + L.tiles);
         qp.ntiles = (int32_t *)(ws + L.ntiles);
@@ -4162,8 +4157,21 @@ int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char 
             hipLaunchKernelGGL(qb_order_kernel, dim3(1), dim3(256), 0, st, qp, nkeys);
             SSA_CHECK_LAUNCH();
         }
+        // the query scatter also writes each (query, list) cut entry: it has
+        // the query's bucket and its position in the bucket's query list
+        CutP cp{};
+        cp.perm = (const int32_t *)(ws + L.perm);
+        cp.bstart = rp.bstart; cp.bsize = rp.bsize; cp.sid = rp.sid;
+        cp.smin = (const int32_t *)(ws + L.smin);
+        cp.glob = a->glob;
+        cp.cut = (int4 *)(ws + L.cut);
+        cp.srix = (int32_t *)(ws + L.srix);
+        cp.ctab = D.ctab ? (const uint2 *)(ws + L.ctab) : nullptr;
+        cp.N = D.N; cp.M = D.M; cp.R = D.R; cp.NS = D.NS; cp.NB = D.NB; cp.C = D.C; cp.Cs = D.Cs;
+        cp.Hq = D.Hq; cp.Hkv = D.Hkv; cp.rep = D.rep; cp.bh0 = (int)bh0; cp.G = D.G;
+        cp.causal = a->causal ? 1 : 0; cp.nlists = D.nlists; cp.rows = (int64_t)nbh * D.N;
         hipLaunchKernelGGL(qb_scatter_kernel, gq, dim3(256), (size_t)std::max(D.NB * 16, 256 * 4),
-                           st, qp);
+                           st, qp, cp);
         SSA_CHECK_LAUNCH();
 
         rp.tiles = qp.tiles; rp.ntiles = qp.ntiles; rp.qlist = qp.qlist;
@@ -4173,23 +4181,6 @@ int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char 
         const int64_t grid = 8 * ceil_div((int64_t)ninst * (ceil_div(D.N, TQ) + D.NB), 8);
         rc = rescore_dispatch<T>(D.d, rp, grid, st);
         if (rc) return rc;
-
-        CutP cp{};
-        cp.qid = qp.qid;
-        cp.perm = (const int32_t *)(ws + L.perm);
-        cp.bstart = rp.bstart; cp.bsize = rp.bsize; cp.sid = rp.sid;
-        cp.smin = (const int32_t *)(ws + L.smin);
-        cp.glob = a->glob;
-        cp.cut = (int4 *)(ws + L.cut);
-        cp.qpos = qp.qpos;
-        cp.srix = (int32_t *)(ws + L.srix);
-        cp.ctab = D.ctab ? (const uint2 *)(ws + L.ctab) : nullptr;
-        cp.N = D.N; cp.M = D.M; cp.R = D.R; cp.NS = D.NS; cp.NB = D.NB; cp.C = D.C; cp.Cs = D.Cs;
-        cp.Hq = D.Hq; cp.Hkv = D.Hkv; cp.rep = D.rep; cp.bh0 = (int)bh0; cp.G = D.G;
-        cp.causal = a->causal ? 1 : 0; cp.nlists = D.nlists; cp.rows = (int64_t)nbh * D.N;
-        hipLaunchKernelGGL(cut_kernel, dim3((unsigned)ceil_div(cp.rows * D.nlists, 256)), dim3(256),
-                           0, st, cp);
-        SSA_CHECK_LAUNCH();
 
         SelP sp{};
         sp.qid = qp.qid; sp.perm = cp.perm; sp.bstart = rp.bstart; sp.bsize = rp.bsize;
