@@ -210,8 +210,9 @@ def _ptr(t):
 
 
 # --------------------------------------------------------------------------- graph build
-# largest key length ssa_build_graph accepts
-MAX_KEYS = 65536
+# largest key length ssa_build_graph accepts (the library refuses some
+# shorter ones whose lists or select rows do not fit its fields or LDS)
+MAX_KEYS = 1 << 20
 
 
 def _graph_args(q, k, rand_proj, *, P, T, C, top_k, window, causal, is_cross, total_k, glob,
@@ -239,8 +240,8 @@ def _graph_args(q, k, rand_proj, *, P, T, C, top_k, window, causal, is_cross, to
         raise RuntimeError(f"ssa_amd.build_graph: k_proj {tuple(k_proj.shape)} is not "
                            f"{(B * Hkv, R, M, P)}")
     if not 1 <= M <= MAX_KEYS:
-        raise RuntimeError(f"ssa_amd.build_graph: key length {M} unsupported (1..{MAX_KEYS}: key "
-                           "ids, bucket starts and list positions travel in 16-bit fields)")
+        raise RuntimeError(f"ssa_amd.build_graph: key length {M} unsupported (1..{MAX_KEYS}: the "
+                           "bucket sort's limit)")
     if glob.numel() > M:
         raise RuntimeError(f"ssa_amd.build_graph: {glob.numel()} global tokens for {M} keys")
     require_device(q, k, rand_proj, glob)

@@ -95,6 +95,8 @@ struct Dims {
     int ctab;          // the list sort writes the cut's rank table (causal only)
     int fused;         // the projections hashed the rows (ssa_project_build_graph): no
                        // hash or aux pass, aux rows for every head, split hyperplanes
+    int cbits;         // width of the cut entries' size and cutoff fields
+    int swaves;        // rows (waves) per select workgroup, as many as its LDS allows
 };
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -615,6 +617,7 @@ __device__ void qb_write_tiles(const QbP &p, int inst, int bh, int r, int t, int
 }
 
 constexpr int LS_RANK_MIN = 128;   // lists at least this long are ranked through a bitmap
+static_assert(LS_RANK_MIN <= 128, "shorter lists pack their slots in 7 bits");
 
 struct CutP {
     const int32_t *perm, *bstart, *bsize, *sid, *smin;
@@ -624,6 +627,8 @@ struct CutP {
                        // region of S (lists * N * C elements), in elements
     const uint2 *ctab; // optional: the list sort's rank table of long lists
     int N, M, R, NS, NB, C, Cs, Hq, Hkv, rep, bh0, G, causal, nlists;
+    int cbits;         // width of a cut entry's size and cutoff fields (the filler
+                       // key and the bucket start take the bits above them)
     int64_t rows;
 };
 
@@ -672,12 +677,14 @@ __device__ void cut_entry(const CutP &p, int64_t rloc, int list, int u, int pos)
             cutoff = nv;
         }
     }
-    // 16-bit fields, read back as unsigned: the list size capped at C (every
-    // use compares it with 0 and C or takes min(size, C)), the filler key and
-    // the cutoff below 2^16, the bucket start below M <= 65536
+    // Packed fields, read back as unsigned: the list size capped at C (every
+    // use compares it with 0 and C or takes min(size, C)) and the cutoff in
+    // the low cbits bits, the filler key and the bucket start (both below M)
+    // above them; cbits is 16 up to 65,536 keys, and the host refuses sizes
+    // whose fields do not fit 32 bits
     p.cut[x] = make_int4((int)(prow * p.M) + st,
-                         (int)((uint32_t)min(sz, p.C) | ((uint32_t)f << 16)),
-                         (int)((uint32_t)cutoff | ((uint32_t)st << 16)), first * 2 + real);
+                         (int)((uint32_t)min(sz, p.C) | ((uint32_t)f << p.cbits)),
+                         (int)((uint32_t)cutoff | ((uint32_t)st << p.cbits)), first * 2 + real);
     p.srix[x] = (int32_t)(((int64_t)list * p.N + pos) * p.Cs);
 }
 
@@ -1214,9 +1221,10 @@ __global__ void __launch_bounds__(256) list_sort_kernel(LsP p) {
         }
         return;
     }
-    // key id << 16 | list slot: ids < 2^15, slots < 2^16
+    // key id << 7 | list slot: lists this short have slots below 128, and
+    // key ids (below M <= 2^20) leave the packed keys below the padding
     for (int i = tid; i < P2; i += 256)
-        ls_key[i] = i < nv ? (((uint32_t)pr[st + i] << 16) | (uint32_t)i) : 0xffffffffu;
+        ls_key[i] = i < nv ? (((uint32_t)pr[st + i] << 7) | (uint32_t)i) : 0xffffffffu;
     __syncthreads();
     for (int k = 2; k <= P2; k <<= 1) {            // bitonic sort, ascending
         for (int j = k >> 1; j > 0; j >>= 1) {
@@ -1232,15 +1240,15 @@ __global__ void __launch_bounds__(256) list_sort_kernel(LsP p) {
     }
     for (int i = tid; i < nv; i += 256) {
         const uint32_t key = ls_key[i];
-        p.sid[base + st + i] = (int32_t)(key >> 16);
-        p.rnk[base + st + (int)(key & 0xffffu)] = i;
+        p.sid[base + st + i] = (int32_t)(key >> 7);
+        p.rnk[base + st + (int)(key & 127u)] = i;
     }
     if (tid < SSA_WAVE) {                          // suffix minimum of the list slots
         const int lane = tid;
         int carry = p.C;
         for (int hi = nv; hi > 0; hi -= SSA_WAVE) {
             const int i = hi - SSA_WAVE + lane;
-            int c = i >= 0 ? (int)(ls_key[i] & 0xffffu) : p.C;
+            int c = i >= 0 ? (int)(ls_key[i] & 127u) : p.C;
 #pragma unroll
             for (int o = 1; o < SSA_WAVE; o <<= 1) {
                 const int y = __shfl_down(c, o, SSA_WAVE);
@@ -1259,8 +1267,8 @@ __global__ void __launch_bounds__(256) list_sort_kernel(LsP p) {
 // an overflow filler (invalid) when the filler key is at or past the query, or
 // an entry of glob ++ 0 for an empty bucket (:711-737) -- as
 // {row offset of the bucket (kv-head/round row * M + start), size | filler
-// key << 16, cutoff | start << 16, first slot * 2 + (that slot is valid)};
-// first slot C: none.  Sizes, cutoffs, starts and keys stay below 2^16.
+// key << cbits, cutoff | start << cbits, first slot * 2 + (that slot is
+// valid)}; first slot C: none.
 // ------------------------------------------------------------------ extra scores
 // Per query row: q.k_n (the key that replaces future candidates when causal,
 // :698-709) and q.k_glob[j], q.k_0 (the empty-bucket list, :711-737).  They
@@ -1491,6 +1499,8 @@ struct SelP {
     const int64_t *glob;
     int N, M, d, R, NS, NB, C, Cs, CPL, nlists, Hq, Hkv, rep, G, kk, window, causal, cross, mode,
         total_k, Kw, Kout, bh0, words;
+    int cbits;             // width of a cut entry's size and cutoff fields
+    int waves;             // rows (one per wave) of a select workgroup
     int64_t Call, rows;
     int64_t rows_all;      // query rows of every head (B * Hq * N): tie rows and output rows
     int64_t *out_idx;
@@ -1946,7 +1956,10 @@ __device__ __forceinline__ void sel_boundary(uint32_t *ckey, int ebits, uint32_t
 //          mode) are handed to the exact replay.  LSH mode writes the selected
 //          keys by descending score, FULL mode merges them with the window and
 //          the globals through a key bitmap.
-template <typename T, bool LSH_MODE, bool CAUSAL, int CAP>
+// WIDE: the cut entries' field width and the rows per workgroup come from
+// p.cbits and p.waves (beyond 65,536 keys, or when fewer than SEL_WAVES rows
+// fit a workgroup's LDS); else they are 16 and SEL_WAVES, as constants.
+template <typename T, bool LSH_MODE, bool CAUSAL, int CAP, bool WIDE>
 // Registers are held to what 8 waves per SIMD allow (the kernel waits on
 // memory and LDS; the bench workload's 5 KB of LDS per wave fits 8 as well).
 __global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) __attribute__((amdgpu_waves_per_eu(8, 8)))
@@ -1955,7 +1968,7 @@ select_kernel(SelP p) {
     const int64_t blk = xcd_logical_block(blockIdx.x, p.nblocks);
     if (blk >= p.nblocks) return;
     const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / SSA_WAVE);   // wave-uniform
-    const int64_t rd = blk * SEL_WAVES + wid;
+    const int64_t rd = blk * (WIDE ? p.waves : SEL_WAVES) + wid;
     if (rd >= p.rows) return;
     // causal rows cost more the later their position (more members below the
     // query): a head's rows go in descending position, so the launch ends on
@@ -2012,8 +2025,10 @@ select_kernel(SelP p) {
         const bool in = list < nl;
         const int4 ct = in ? crow[list] : make_int4(0, 0, 0, 0);
         const int so = in ? xrow[list] : 0;
-        const int sz = ct.y & 0xffff, cutoff = ct.z & 0xffff;
-        const int st = (int)((uint32_t)ct.z >> 16), fk = (int)((uint32_t)ct.y >> 16);
+        const int cb = WIDE ? p.cbits : 16;
+        const uint32_t cmask = (1u << cb) - 1u;
+        const int sz = (int)(ct.y & cmask), cutoff = (int)(ct.z & cmask);
+        const int st = (int)((uint32_t)ct.z >> cb), fk = (int)((uint32_t)ct.y >> cb);
         // a filler that cannot matter (no overflow, or past the query) is -1
         const bool fl = in && sz > 0 && sz < p.C && (!CAUSAL || fk < n);
         if (in) lst[list] = make_int4(st, sz, ct.x - st, fl ? fk : -1);
@@ -2495,11 +2510,16 @@ constexpr int RP_WAVES = 2;
 constexpr uint32_t RP_NEGINF = 0xff800000u;   // rank key of -inf: ~score_key(-inf)
 constexpr int RP_STACK = 64;
 
-// words of one replayed row: rank keys (W), 16-bit payload (key ids below
-// 2^16, or positions), TL/TR (two 16-bit lists), leaf bits, stack, bitmap,
-// glob scores
+// The per-wave replay carries key ids as 16-bit values up to 65,536 keys (a
+// seen bitmap of at most 2,048 words), as 32-bit values beyond
+__host__ __device__ inline bool rp_wide_ids(int words) { return words > 2048; }
+__host__ __device__ inline int rp_cand_words(int W, int words) {
+    return rp_wide_ids(words) ? W : (W + 1) / 2;
+}
+// words of one row of the per-wave replay: rank keys (W), key ids, TL/TR
+// (two 16-bit lists), leaf bits, stack, bitmap, glob scores
 __host__ __device__ inline int rp_lds_words(int W, int words) {
-    return (W + (W + 1) / 2 + W + (W + 31) / 32 + 1 + 3 * RP_STACK + words + 1) & ~1;
+    return (2 * W + rp_cand_words(W, words) + (W + 31) / 32 + 1 + 3 * RP_STACK + words + 1) & ~1;
 }
 
 __device__ __forceinline__ void rp_sync() {
@@ -2509,12 +2529,16 @@ __device__ __forceinline__ void rp_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// CT: 32-bit key ids (the per-wave replay) or 16-bit positions (the
+// workgroup replay, whose rows hold fewer than 2^16 slots)
+template <typename CT>
 struct RpArr {
     uint32_t *key;     // rank keys: smaller = earlier in top-k order
-    uint16_t *cand;    // key ids (or positions) carried along
+    CT *cand;          // key ids (or positions) carried along
 };
 
-__device__ __forceinline__ void rp_swap(const RpArr &a, int i, int j) {
+template <class A>
+__device__ __forceinline__ void rp_swap(const A &a, int i, int j) {
     const uint32_t tk = a.key[i];
     const int32_t tc = a.cand[i];
     a.key[i] = a.key[j]; a.cand[i] = a.cand[j];
@@ -2522,7 +2546,8 @@ __device__ __forceinline__ void rp_swap(const RpArr &a, int i, int j) {
 }
 
 // ---- single-lane heap routines (depth-limit fallbacks, partial_sort)
-__device__ void rp_push_up(const RpArr &a, int base, int hole, int top, uint32_t vk, int32_t vc) {
+template <class A>
+__device__ void rp_push_up(const A &a, int base, int hole, int top, uint32_t vk, int32_t vc) {
     int parent = (hole - 1) / 2;
     while (hole > top && a.key[base + parent] < vk) {
         a.key[base + hole] = a.key[base + parent];
@@ -2534,7 +2559,8 @@ __device__ void rp_push_up(const RpArr &a, int base, int hole, int top, uint32_t
     a.cand[base + hole] = vc;
 }
 
-__device__ void rp_adjust(const RpArr &a, int base, int hole, int len, uint32_t vk, int32_t vc) {
+template <class A>
+__device__ void rp_adjust(const A &a, int base, int hole, int len, uint32_t vk, int32_t vc) {
     const int top = hole;
     int child = hole;
     while (child < (len - 1) / 2) {
@@ -2554,7 +2580,8 @@ __device__ void rp_adjust(const RpArr &a, int base, int hole, int len, uint32_t 
 }
 
 // heap_select(f, mid, l): [f, mid) becomes a max-heap of the mid-f smallest
-__device__ void rp_heap_select(const RpArr &a, int f, int mid, int l) {
+template <class A>
+__device__ void rp_heap_select(const A &a, int f, int mid, int l) {
     const int len = mid - f;
     if (len >= 2) {
         for (int parent = (len - 2) / 2;; --parent) {
@@ -2573,7 +2600,8 @@ __device__ void rp_heap_select(const RpArr &a, int f, int mid, int l) {
     }
 }
 
-__device__ void rp_heap_sort(const RpArr &a, int f, int l) {
+template <class A>
+__device__ void rp_heap_sort(const A &a, int f, int l) {
     while (l - f > 1) {
         --l;
         const uint32_t vk = a.key[l];
@@ -2584,7 +2612,8 @@ __device__ void rp_heap_sort(const RpArr &a, int f, int l) {
     }
 }
 
-__device__ void rp_insertion(const RpArr &a, int f, int l) {
+template <class A>
+__device__ void rp_insertion(const A &a, int f, int l) {
     for (int i = f + 1; i < l; ++i) {
         const uint32_t vk = a.key[i];
         const int32_t vc = a.cand[i];
@@ -2601,7 +2630,8 @@ __device__ void rp_insertion(const RpArr &a, int f, int l) {
 
 // ---- one wavefront partitions [f, l) (median of f+1, middle, l-1 moved to f,
 // then the unguarded Hoare scan, done from the stopper lists); returns the cut
-__device__ int rp_partition(const RpArr &a, uint16_t *TL, uint16_t *TR, int f, int l) {
+template <class A>
+__device__ int rp_partition(const A &a, uint16_t *TL, uint16_t *TR, int f, int l) {
     const int lane = lane_id();
     const int n = l - f;
     const int ia = f + 1, ib = f + n / 2, ic = l - 1;
@@ -2647,7 +2677,8 @@ __device__ int rp_partition(const RpArr &a, uint16_t *TL, uint16_t *TR, int f, i
 __device__ __forceinline__ int rp_log2(int n) { return 31 - __clz(n); }
 
 // std::nth_element(f, nth, l)
-__device__ void rp_nth_element(const RpArr &a, uint16_t *TL, uint16_t *TR, int f, int nth, int l) {
+template <class A>
+__device__ void rp_nth_element(const A &a, uint16_t *TL, uint16_t *TR, int f, int nth, int l) {
     if (f == l || nth == l) return;
     int depth = 2 * rp_log2(l - f);
     while (l - f > 3) {
@@ -2669,7 +2700,8 @@ __device__ void rp_nth_element(const RpArr &a, uint16_t *TL, uint16_t *TR, int f
 
 // std::sort(f, l): introsort loop over an explicit stack, then the final
 // insertion sort, which stops at every partition cut, so it runs per leaf
-__device__ void rp_sort(const RpArr &a, uint16_t *TL, uint16_t *TR, uint32_t *lbits,
+template <class A>
+__device__ void rp_sort(const A &a, uint16_t *TL, uint16_t *TR, uint32_t *lbits,
                         int32_t *stk, int f, int l) {
     const int lane = lane_id();
     if (l - f < 2) return;
@@ -2730,21 +2762,25 @@ __device__ void rp_sort(const RpArr &a, uint16_t *TL, uint16_t *TR, uint32_t *lb
 // Rows are taken only when more than `skip_max` are tied (fewer go to the
 // workgroup replay; skip_max < 0: always).  Six waves per SIMD (80 VGPRs):
 // with many rows the launch runs in rounds of resident rows.
-template <typename T, bool LSH_MODE, bool GLB>
+// CT: the key ids' type, uint32_t exactly when rp_wide_ids(p.words)
+template <typename T, bool LSH_MODE, bool GLB, typename CT>
 __global__ void __launch_bounds__(RP_WAVES * SSA_WAVE) __attribute__((amdgpu_waves_per_eu(6)))
 topk_replay_kernel(SelP p, int chunk, int W, uint32_t *gscr, int skip_max) {
     extern __shared__ uint32_t rp_smem[];
     const int wid = threadIdx.x / SSA_WAVE;
     const int lane = lane_id();
-    const int64_t wave_words = rp_lds_words(W, p.words);
+    // rp_cand_words and rp_lds_words, given that CT is 32-bit exactly when
+    // rp_wide_ids(p.words)
+    const int cw = sizeof(CT) == 4 ? W : (W + 1) / 2;
+    const int64_t wave_words = (2 * W + cw + (W + 31) / 32 + 1 + 3 * RP_STACK + p.words + 1) & ~1;
     uint32_t *base = GLB ? gscr + ((int64_t)blockIdx.x * RP_WAVES + wid) * wave_words
                          : rp_smem + (int64_t)wid * wave_words;
-    RpArr A;
+    RpArr<CT> A;
     A.key = base;
-    A.cand = (uint16_t *)(base + W);
-    uint16_t *TL = (uint16_t *)(base + W + (W + 1) / 2);
+    A.cand = (CT *)(base + W);
+    uint16_t *TL = (uint16_t *)(base + W + cw);
     uint16_t *TR = TL + W;
-    uint32_t *lbits = base + 2 * W + (W + 1) / 2;
+    uint32_t *lbits = base + 2 * W + cw;
     int32_t *stk = (int32_t *)(lbits + (W + 31) / 32 + 1);
     uint32_t *bm = (uint32_t *)(stk + 3 * RP_STACK);
 
@@ -2840,7 +2876,7 @@ topk_replay_kernel(SelP p, int chunk, int W, uint32_t *gscr, int skip_max) {
                 if (in) {
                     const int at = kk + (int)(j0 - s0) + lane;
                     A.key[at] = keep ? ~sk : RP_NEGINF;
-                    A.cand[at] = (uint16_t)v;
+                    A.cand[at] = (CT)v;
                 }
                 rp_sync();
                 j0 += nl;
@@ -3352,7 +3388,7 @@ topk_replay_wg_kernel(SelP p, int chunk, int W, int nsim, uint32_t *gscr, int64_
         // 3. the chunks to replay, replayed as the reference runs them
         const int nmark = misc[1];
         if (wid < nsim) {
-            RpArr A;
+            RpArr<uint16_t> A;
             A.key = slot;
             A.cand = (uint16_t *)(slot + W);
             uint16_t *TL = (uint16_t *)(slot + W + (W + 1) / 2);
@@ -3527,13 +3563,23 @@ int make_dims(const ssa_graph_args *a, Dims &D, bool need_q = true, int64_t ws_c
                       "of %d)", a->d, a->q.dtype == SSA_F32 ? 4 : 8);
         return SSA_E_UNSUP;
     }
-    // key ids, bucket starts and in-list positions travel in 16-bit fields
-    // (the cut entries, the tie replay's payload): M <= 65536, and a list's
-    // size (capped at C) below 2^16
-    if (a->M > 65536 || !ssa_sort_supported(a->M) || (a->M == 65536 && a->C >= 65536)) {
-        ssa_set_error("build_graph: key length %d unsupported (1..65536, with C < 65536 at "
-                      "65536)", a->M);
+    // a cut entry packs a list's size (capped at C) and cutoff, both at most
+    // min(C, M), with a key id and a bucket start, both below M, into 32 bits
+    // each: 16 + 16 bits up to 65,536 keys, else as many bits as min(C, M)
+    // needs for the first two
+    if (!ssa_sort_supported(a->M)) {
+        ssa_set_error("build_graph: key length %d unsupported (1..1048576)", a->M);
         return SSA_E_UNSUP;
+    }
+    {
+        auto width = [](int64_t v) { int b = 0; while (((int64_t)1 << b) <= v) ++b; return b; };
+        const int cb = width(std::min<int64_t>(a->C, a->M)), mb = width(a->M - 1);
+        D.cbits = cb <= 16 && mb <= 16 ? 16 : cb;
+        if (D.cbits + mb > 32) {
+            ssa_set_error("build_graph: %d keys with lists of up to %d members exceed the 32-bit "
+                          "fields of a list cut (%d + %d bits)", a->M, a->C, cb, mb);
+            return SSA_E_UNSUP;
+        }
     }
     SSA_CHECK_ARG((int64_t)a->B * a->Hkv * a->R * a->M < ((int64_t)1 << 29),
                   "build_graph: B*Hkv*R*M must stay below 2^29 (bucket permutation bytes)");
@@ -3577,6 +3623,20 @@ int make_dims(const ssa_graph_args *a, Dims &D, bool need_q = true, int64_t ws_c
         ssa_set_error("build_graph: LSH top-k %d with stream chunks of %d slots exceeds the "
                       "65535 slots the exact tie replay supports", D.kk, D.chunk);
         return SSA_E_UNSUP;
+    }
+    {
+        // one select row (its seen bitmap and buffer grow with the key length)
+        // and the list sort's ranking of a long list must fit a workgroup's LDS
+        const int cap = D.kk > SEL_CAP_LARGE_KK ? SEL_CAP_LARGE : SEL_CAP_SMALL;
+        const int64_t sel = (int64_t)sel_lds_words(sel_bitmap_words(D.M), D.kk,
+                                                   a->mode == SSA_GRAPH_LSH, D.nlists, cap) * 4;
+        const int64_t lsr = (2 * (int64_t)((D.M + 31) / 32) + std::min(D.C, D.M) + 4) * 4;
+        if (sel > SSA_LDS_BYTES || lsr > SSA_LDS_BYTES) {
+            ssa_set_error("build_graph: key length %d unsupported here (a select row needs %lld "
+                          "bytes of LDS, the list ranking %lld; at most %d)", D.M, (long long)sel,
+                          (long long)lsr, SSA_LDS_BYTES);
+            return SSA_E_UNSUP;
+        }
     }
     // chunk the query heads so the score buffer stays near 8 GiB (a chunk's
     // select and rescore grids grow with it: one head of the 32k MQA workload
@@ -3790,21 +3850,34 @@ int rescore_dispatch(int d, const RsP &rp, int64_t grid, hipStream_t st) {
     return SSA_E_UNSUP;
 }
 
-template <typename T, bool LSH, bool CAUSAL, int CAP>
-int launch_select(const SelP &sp, hipStream_t st) {
-    const size_t lds =
-        (size_t)SEL_WAVES * sel_lds_words(sp.words, sp.kk, LSH, sp.nlists, CAP) * 4;
-    if (lds > SSA_LDS_BYTES) {
-        ssa_set_error("build_graph: select needs %zu bytes of LDS", lds);
-        return SSA_E_UNSUP;
-    }
-    SSA_CHECK_HIP(hipFuncSetAttribute((const void *)select_kernel<T, LSH, CAUSAL, CAP>,
+template <typename T, bool LSH, bool CAUSAL, int CAP, bool WIDE>
+int launch_select_w(const SelP &sp, size_t lds, hipStream_t st) {
+    SSA_CHECK_HIP(hipFuncSetAttribute((const void *)select_kernel<T, LSH, CAUSAL, CAP, WIDE>,
                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     const int64_t grid = 8 * ceil_div(sp.nblocks, 8);
-    hipLaunchKernelGGL((select_kernel<T, LSH, CAUSAL, CAP>), dim3((unsigned)grid),
-                       dim3(SEL_WAVES * SSA_WAVE), lds, st, sp);
+    hipLaunchKernelGGL((select_kernel<T, LSH, CAUSAL, CAP, WIDE>), dim3((unsigned)grid),
+                       dim3(sp.waves * SSA_WAVE), lds, st, sp);
     SSA_CHECK_LAUNCH();
     return SSA_OK;
+}
+
+template <typename T, bool LSH, bool CAUSAL, int CAP>
+int launch_select(const SelP &sp0, hipStream_t st) {
+    // SEL_WAVES rows per workgroup, fewer where a row's LDS (its seen bitmap
+    // and buffer grow with the key length) leaves room for fewer
+    const size_t per = (size_t)sel_lds_words(sp0.words, sp0.kk, LSH, sp0.nlists, CAP) * 4;
+    const int waves = (int)std::min<size_t>(SEL_WAVES, SSA_LDS_BYTES / per);
+    if (waves < 1) {
+        ssa_set_error("build_graph: a select row needs %zu bytes of LDS (%d keys)", per, sp0.M);
+        return SSA_E_UNSUP;
+    }
+    SelP sp = sp0;
+    sp.waves = waves;
+    sp.nblocks = ceil_div(sp.rows, waves);
+    const size_t lds = (size_t)waves * per;
+    return sp.cbits != 16 || waves != SEL_WAVES
+               ? launch_select_w<T, LSH, CAUSAL, CAP, true>(sp, lds, st)
+               : launch_select_w<T, LSH, CAUSAL, CAP, false>(sp, lds, st);
 }
 
 // Extra scores with the arithmetic of the rescore kernel rescore_dispatch picks
@@ -3850,6 +3923,30 @@ int aux_dispatch(int d, bool mfma, const AuxP &ap, hipStream_t st) {
 // fit, else in the workspace region `rpscr` (replay_glb_blocks blocks).  Both
 // are launched: each reads the tie count on the device and exits at once when
 // the rows are the other's.
+// the per-wave replay, its arrays in LDS or (when two rows do not fit) in
+// the workspace; CT: the key ids' type
+template <typename T, bool LSH, typename CT>
+int launch_replay_pw(const SelP &sp, const Dims &D, int W, uint32_t *rpscr, int cap,
+                     hipStream_t st) {
+    const int chunk = D.chunk;
+    if (!replay_fits_lds(W, sp.words)) {
+        const int64_t blocks = D.rp_glb_blocks;
+        hipLaunchKernelGGL((topk_replay_kernel<T, LSH, true, CT>), dim3((unsigned)blocks),
+                           dim3(RP_WAVES * SSA_WAVE), 0, st, sp, chunk, W, rpscr, cap);
+        SSA_CHECK_LAUNCH();
+        return SSA_OK;
+    }
+    const size_t lds = (size_t)RP_WAVES * rp_lds_words(W, sp.words) * 4;
+    SSA_CHECK_HIP(hipFuncSetAttribute((const void *)topk_replay_kernel<T, LSH, false, CT>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    // enough blocks for every resident wave to take a row (the rest exit at once)
+    const int64_t blocks = std::min<int64_t>(ceil_div(sp.rows, RP_WAVES), 8192);
+    hipLaunchKernelGGL((topk_replay_kernel<T, LSH, false, CT>), dim3((unsigned)blocks),
+                       dim3(RP_WAVES * SSA_WAVE), lds, st, sp, chunk, W, (uint32_t *)nullptr, cap);
+    SSA_CHECK_LAUNCH();
+    return SSA_OK;
+}
+
 template <typename T, bool LSH>
 int launch_replay(const SelP &sp, const Dims &D, uint32_t *rpscr, uint32_t *rpwscr,
                   hipStream_t st) {
@@ -3878,22 +3975,8 @@ int launch_replay(const SelP &sp, const Dims &D, uint32_t *rpscr, uint32_t *rpws
                            rpw_scratch_words(sp.Call, sp.M, sp.kk, nch), cap);
         SSA_CHECK_LAUNCH();
     }
-    if (!replay_fits_lds(W, sp.words)) {
-        const int64_t blocks = D.rp_glb_blocks;
-        hipLaunchKernelGGL((topk_replay_kernel<T, LSH, true>), dim3((unsigned)blocks),
-                           dim3(RP_WAVES * SSA_WAVE), 0, st, sp, chunk, W, rpscr, cap);
-        SSA_CHECK_LAUNCH();
-        return SSA_OK;
-    }
-    const size_t lds = (size_t)RP_WAVES * rp_lds_words(W, sp.words) * 4;
-    SSA_CHECK_HIP(hipFuncSetAttribute((const void *)topk_replay_kernel<T, LSH, false>,
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    // enough blocks for every resident wave to take a row (the rest exit at once)
-    const int64_t blocks = std::min<int64_t>(ceil_div(sp.rows, RP_WAVES), 8192);
-    hipLaunchKernelGGL((topk_replay_kernel<T, LSH, false>), dim3((unsigned)blocks),
-                       dim3(RP_WAVES * SSA_WAVE), lds, st, sp, chunk, W, (uint32_t *)nullptr, cap);
-    SSA_CHECK_LAUNCH();
-    return SSA_OK;
+    return rp_wide_ids(sp.words) ? launch_replay_pw<T, LSH, uint32_t>(sp, D, W, rpscr, cap, st)
+                                  : launch_replay_pw<T, LSH, uint16_t>(sp, D, W, rpscr, cap, st);
 }
 
 template <typename T, bool LSH>
@@ -4097,6 +4180,11 @@ int keys_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws
         while (p2 < std::min(D.C, D.M)) p2 <<= 1;
         const size_t lds = std::max((size_t)p2 * 4,
                                     (size_t)(2 * ((D.M + 31) / 32) + std::min(D.C, D.M) + 4) * 4);
+        if (lds > SSA_LDS_BYTES) {
+            ssa_set_error("build_graph: ranking lists of up to %d members over %d keys needs %zu "
+                          "bytes of LDS", D.C, D.M, lds);
+            return SSA_E_UNSUP;
+        }
         SSA_CHECK_HIP(hipFuncSetAttribute((const void *)list_sort_kernel,
                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
         hipLaunchKernelGGL(list_sort_kernel, dim3((unsigned)(D.BK * D.R * D.NB)), dim3(256), lds, st,
@@ -4170,6 +4258,7 @@ int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char 
         cp.N = D.N; cp.M = D.M; cp.R = D.R; cp.NS = D.NS; cp.NB = D.NB; cp.C = D.C; cp.Cs = D.Cs;
         cp.Hq = D.Hq; cp.Hkv = D.Hkv; cp.rep = D.rep; cp.bh0 = (int)bh0; cp.G = D.G;
         cp.causal = a->causal ? 1 : 0; cp.nlists = D.nlists; cp.rows = (int64_t)nbh * D.N;
+        cp.cbits = D.cbits;
         hipLaunchKernelGGL(qb_scatter_kernel, gq, dim3(256), (size_t)std::max(D.NB * 16, 256 * 4),
                            st, qp, cp);
         SSA_CHECK_LAUNCH();
@@ -4207,7 +4296,7 @@ int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char 
         sp.aux = ap.out;
         sp.NA = ap.NA;
         sp.perm_bytes = (int)(D.BK * D.R * D.M * 4);
-        sp.nblocks = ceil_div(sp.rows, SEL_WAVES);
+        sp.cbits = D.cbits;
         rc = select_dispatch<T>(sp, st);
         if (rc) return rc;
         last = sp;

@@ -105,7 +105,10 @@ def test_argument_errors_are_reported_without_a_gpu():
 # rows share a workgroup's 160 KiB of LDS (minus 512 bytes of static data).
 def _replay_words(W, M):
     words = ((M + 31) // 32 + 1) & ~1
-    return (W + (W + 1) // 2 + W + (W + 31) // 32 + 1 + 3 * 64 + words + 1) & ~1
+    # rank keys, key ids (16-bit up to 65,536 keys, else 32-bit), two 16-bit
+    # position lists, leaf bits, stack, seen bitmap
+    cand = W if words > 2048 else (W + 1) // 2
+    return (2 * W + cand + (W + 31) // 32 + 1 + 3 * 64 + words + 1) & ~1
 
 
 def _replay_fits(W, M):
@@ -224,11 +227,10 @@ def test_head_dim_rule(d, dtype, ok):
 
 
 # ---------------------------------------------------------------------------- size envelope
-@pytest.mark.parametrize("M", [65537, 100000, 131072])
-def test_key_length_beyond_16_bit_fields_is_refused(M):
-    """Keys beyond 65536 are refused by the library before any launch (key
-    ids, bucket starts and list positions travel in 16-bit fields), and by
-    the Python wrapper before it touches a device."""
+@pytest.mark.parametrize("M", [1048577, 2000000])
+def test_key_length_beyond_the_sort_is_refused(M):
+    """Keys beyond the bucket sort's 2^20 are refused by the library before
+    any launch, and by the Python wrapper before it touches a device."""
     import torch
 
     from ssa_amd import _lib
@@ -242,8 +244,27 @@ def test_key_length_beyond_16_bit_fields_is_refused(M):
                          causal=False, is_cross=True, total_k=64, glob=torch.zeros(2))
 
 
-@pytest.mark.parametrize("M", [32769, 40000, 65536])
-def test_key_lengths_up_to_65536_are_taken(M):
+def test_key_length_refusals_name_their_limit():
+    """Within the sort's range the library refuses, with the reason, what
+    its structures cannot hold: a select row's seen bitmap beyond a
+    workgroup's LDS (about 650,000 keys), and a list cut whose size field
+    (min(C, M)) and key field (M - 1) need more than 32 bits together."""
+    from ssa_amd import _lib
+    L = _lib.lib()
+    a, _ = _full_args(1 << 20, 64)
+    assert L.ssa_graph_workspace_bytes(ctypes.byref(a)) < 0
+    assert b"bytes of LDS" in L.ssa_last_error()
+    a, _ = _full_args(300000, 64)
+    a.N, a.causal, a.is_cross = 64, 0, 1        # 64 queries over the keys
+    a.C = 8192                                  # 14 + 19 bits
+    assert L.ssa_graph_workspace_bytes(ctypes.byref(a)) < 0
+    assert b"32-bit fields" in L.ssa_last_error()
+    a.C = 8191                                  # 13 + 19 bits
+    assert L.ssa_graph_workspace_bytes(ctypes.byref(a)) > 0, L.ssa_last_error()
+
+
+@pytest.mark.parametrize("M", [32769, 40000, 65536, 65537, 100003, 131072, 262144, 600000])
+def test_key_lengths_beyond_16_bits_are_taken(M):
     a, _ = _full_args(M, 64)
     from ssa_amd import _lib
     assert _lib.lib().ssa_graph_workspace_bytes(ctypes.byref(a)) > 0, _lib.lib().ssa_last_error()

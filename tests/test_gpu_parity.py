@@ -39,7 +39,8 @@ def _ints(shape, lo, hi, gen):
 # the workspace (40001: odd, so rows start at unaligned key offsets)
 @pytest.mark.parametrize("rows,n,P", [(3, 17, 1), (2, 1024, 1), (4, 4096, 3), (2, 8192, 4),
                                       (2, 16384, 6), (1, 32768, 5), (2, 300, 12), (5, 16, 2),
-                                      (2, 5, 1), (2, 40001, 7), (2, 65536, 5), (1, 131072, 9)])
+                                      (2, 5, 1), (2, 40001, 7), (2, 65536, 5), (1, 131072, 9),
+                                      (1, 524288, 11), (1, 1048576, 12)])
 @pytest.mark.parametrize("dist", ["uniform", "skewed", "sorted", "reversed", "constant"])
 def test_bucket_sort_is_torch_sort(rows, n, P, dist):
     from ssa_amd import _lib
@@ -97,6 +98,13 @@ GRAPH_CASES = [
     # cut entries' 16-bit fields read unsigned
     ("long_keys_causal", 1, 1, 1, 65536, 65536, 16, 2, 12, 0, 32, 2, 2, True, False),
     ("long_keys_cross", 1, 2, 1, 512, 40000, 16, 2, 6, 1, 32, 2, 2, False, True),
+    # key ids beyond 16 bits: the cut entries' fields split at the width of C
+    # (lists of 224 members ranked through the bitmap and the cut's rank table),
+    # 7-bit slots in the short-list sort, 32-bit ids in the per-wave replay, and
+    # (at 262,144 keys) two select rows per workgroup
+    ("keys_131072_causal", 1, 1, 1, 131072, 131072, 16, 2, 12, 0, 64, 2, 2, True, False),
+    ("keys_100003_cross_probes", 1, 2, 1, 300, 100003, 16, 2, 12, 1, 32, 2, 2, False, True),
+    ("keys_262144_cross", 1, 2, 2, 200, 262144, 16, 2, 12, 0, 64, 2, 2, False, True),
 ]
 
 
