@@ -4083,7 +4083,7 @@ int launch_sort_aux(const Dims &D, const ssa_graph_args *a, const Layout &L, cha
     const int64_t grid = sa.rows + ceil_div(waves, SORT_WAVES);
     const size_t lds = std::max<size_t>((size_t)sa.lds,
                                         (size_t)SORT_WAVES * aux_wave_floats(D.R, D.P) * 4);
-    SSA_CHECK_ARG(lds <= SSA_LDS_BYTES, "build_graph: sort and aux need %zu bytes of LDS", lds);
+    SSA_CHECK_ARG(lds <= SORT_LDS_BYTES, "build_graph: sort and aux need %zu bytes of LDS", lds);
     const void *fn = nullptr;
     switch (mfma_instance(D.d)) {
         case 8: fn = (const void *)sort_aux_kernel<T, 8>; break;

@@ -265,7 +265,7 @@ static void sort_plan(int n, int NB, int *cap, int *tl_in_lds, size_t *lds) {
     const size_t base = ((size_t)4 * n + 15) / 16 * 16 + (size_t)NB * 4 + (size_t)c * 8 +
                         (size_t)c * 2;
     const size_t with_tl = (base + 15) / 16 * 16 + (size_t)4 * n;
-    if (with_tl <= SSA_LDS_BYTES) { *tl_in_lds = 1; *lds = with_tl; }
+    if (with_tl <= SORT_LDS_BYTES) { *tl_in_lds = 1; *lds = with_tl; }
     else { *tl_in_lds = 0; *lds = base; }
 }
 
@@ -290,7 +290,7 @@ int ssa_sort_supported(int n) {
     size_t lds;
     if (n < 1 || n > SORT_MAX_KEYS) return 0;
     sort_plan(n, 4096, &cap, &tl, &lds);
-    return lds <= SSA_LDS_BYTES;
+    return lds <= SORT_LDS_BYTES;
 }
 
 int32_t *ssa_sort_counter(uint16_t *tmp, int rows, int n) {

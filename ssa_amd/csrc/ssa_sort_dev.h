@@ -244,15 +244,26 @@ __device__ void wave_small_sort(uint16_t *key, Pos *idx, uint32_t *bits, int f, 
 // for every listed segment (a segment heap-sorted here keeps these values).
 constexpr int SEG_T = 256;                 // segments handed to kernel B
 constexpr int SORT_NW = SORT_WAVES;
+// A row's segments for kernel B are gathered in LDS (up to SEG_STAGE of them)
+// and appended to the global list with one atomic per row at the end: a
+// device-scope atomic on the list's one counter per segment made the top
+// levels 10% slower.  Segments past SEG_STAGE take that atomic each.
+constexpr int SEG_STAGE = 256;
+// dynamic LDS of kernel A: the static TopShared below takes the rest
+constexpr int SORT_LDS_BYTES = SSA_LDS_BYTES - SEG_STAGE * 16;
 
 struct TopShared {
-    int ncur, nnxt;
+    int ncur, nnxt, nseg, base;
     int piv[SORT_NW], cnt[SORT_NW][2], s[SORT_NW], cut[SORT_NW], nL[SORT_NW], nR[SORT_NW];
+    int4 stage[SEG_STAGE];
 };
 
-__device__ __forceinline__ void emit_segment(int4 *segs, int *segcount, int row, int f, int l,
-                                             int depth) {
-    segs[atomicAdd(segcount, 1)] = make_int4(row, f, l - f, depth);
+__device__ __forceinline__ void emit_segment(TopShared &sh, int4 *segs, int *segcount, int row,
+                                             int f, int l, int depth) {
+    const int4 e = make_int4(row, f, l - f, depth);
+    const int k = atomicAdd(&sh.nseg, 1);
+    if (k < SEG_STAGE) sh.stage[k] = e;
+    else segs[atomicAdd(segcount, 1)] = e;
 }
 
 // Pos: uint16_t (rows of up to 32768 keys, the row in LDS) or uint32_t (longer
@@ -325,12 +336,13 @@ __device__ void sort_top_row(int row, const uint16_t *ids, int n, int NB, int32_
     if (tid == 0) {
         sh.ncur = 0;
         sh.nnxt = 0;
+        sh.nseg = 0;
         if (n > SEG_T) {
             segA[0] = (W)n << SH;
             depA[0] = (uint8_t)depth0;
             sh.ncur = 1;
         } else {
-            emit_segment(segs, segcount, row, 0, n, depth0);
+            emit_segment(sh, segs, segcount, row, 0, n, depth0);
         }
     }
     __syncthreads();
@@ -362,7 +374,7 @@ __device__ void sort_top_row(int row, const uint16_t *ids, int n, int NB, int32_
             nxt[slot] = (W)f | ((W)l << SH);
             dnxt[slot] = (uint8_t)depth;
         } else {
-            emit_segment(segs, segcount, row, f, l, depth);
+            emit_segment(sh, segs, segcount, row, f, l, depth);
         }
     };
     for (int level = 0; level < 64; ++level) {
@@ -493,12 +505,17 @@ __device__ void sort_top_row(int row, const uint16_t *ids, int n, int NB, int32_
         uint8_t *td = dcur; dcur = dnxt; dnxt = td;
     }
     __syncthreads();
+    // the gathered segments into the global list, one atomic for all of them
+    const int ns = min(sh.nseg, SEG_STAGE);
+    if (tid == 0 && ns > 0) sh.base = atomicAdd(segcount, ns);
     W *okv = gkv + (int64_t)row * n;
     int32_t *pout = perm + (int64_t)row * n;
     for (int i = tid; i < n; i += SORT_THREADS) {
         okv[i] = (W)key[i] | ((W)idx[i] << SH);
         pout[i] = (int32_t)idx[i];
     }
+    __syncthreads();
+    for (int i = tid; i < ns; i += SORT_THREADS) segs[sh.base + i] = sh.stage[i];
 }
 
 }  // namespace
