@@ -67,6 +67,7 @@ INT_CASES = [
     ("long_keys", 1, 1, 1, 65536, 65536, 16, 2, 0, 32, 2, 2, True, False, torch.float32),
     ("keys_131072", 1, 1, 1, 131072, 131072, 16, 2, 0, 64, 2, 2, True, False, torch.float32),
     ("keys_262144_cross", 1, 2, 2, 200, 262144, 16, 2, 1, 64, 2, 2, False, True, torch.float32),
+    ("huge_k_wide_ids", 1, 1, 1, 4096, 70000, 16, 2, 0, 1700, 4, 2, False, True, torch.float32),
     ("many_globals", 1, 2, 2, 256, 256, 16, 3, 1, 160, 4, 100, True, False, torch.bfloat16),
 ]
 

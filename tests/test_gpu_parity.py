@@ -186,6 +186,10 @@ HUGE_K = ("huge_k_replay_workspace", 1, 1, 1, 2048, 2048, 16, 2, 3, 0, 1400, 4, 
 # so the per-wave replay runs from its workspace region
 HUGE_K_WAVE = ("huge_k_per_wave_replay_workspace", 1, 1, 1, 4096, 4096, 16, 2, 3, 0, 1700, 4, 2,
                True, False)
+# the same replay with 32-bit key ids: 4,096 queries over 70,000 keys
+# (cross-attention), kk = 1698, cut fields of 13 + 17 bits
+HUGE_K_WAVE_WIDE = ("huge_k_per_wave_replay_wide_ids", 1, 1, 1, 4096, 70000, 16, 2, 3, 0, 1700, 4,
+                    2, False, True)
 
 
 def test_full_graph_exact_tier_huge_k_replay_outside_lds():
@@ -204,6 +208,17 @@ def test_full_graph_exact_tier_huge_k_per_wave_replay_workspace():
     assert ref["n_ties"] > 1024
     win = attn.win_builder(N, M, "cpu").numpy()
     rnb, rva = oracle.merge(win, glob.numpy(), ref["idx"], has_self=True, total_k=K)
+    np.testing.assert_array_equal(got.cpu().numpy().reshape(B * H, N, -1), rnb)
+    np.testing.assert_array_equal(got_v.cpu().numpy().reshape(B * H, N, -1), rva)
+
+
+def test_full_graph_exact_tier_huge_k_per_wave_replay_wide_ids():
+    attn, got, got_v, ref, (B, H, N, M, K, w, cross, causal, glob) = _graph_case(HUGE_K_WAVE_WIDE, 0)
+    print(f"  huge K over {M} keys, per-wave replay: {ref['n_ties']} rows with a tied kk-th score",
+          flush=True)
+    assert ref["n_ties"] > 1024
+    win = np.zeros((N, 0), np.int64)
+    rnb, rva = oracle.merge(win, glob.numpy(), ref["idx"], has_self=False, total_k=K)
     np.testing.assert_array_equal(got.cpu().numpy().reshape(B * H, N, -1), rnb)
     np.testing.assert_array_equal(got_v.cpu().numpy().reshape(B * H, N, -1), rva)
 
