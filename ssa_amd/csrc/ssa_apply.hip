@@ -1171,7 +1171,7 @@ int launch_apply(const ApplyP &p, hipStream_t st, bool bwd) {
 template <typename T>
 int dispatch_d(const ApplyP &p, int d, hipStream_t st, bool bwd) {
     if (!ssa_head_dim_ok(d, std::is_same<T, float>::value ? SSA_F32 : SSA_BF16)) {
-        ssa_set_error("sparse_gather_attention: head dim %d unsupported (4..512: a power of two "
+        ssa_set_error("sparse_gather_attention: head dim %d unsupported (4..1024: a power of two "
                       "or a multiple of %d)", d, std::is_same<T, float>::value ? 4 : 8);
         return SSA_E_UNSUP;
     }
@@ -1184,8 +1184,9 @@ int dispatch_d(const ApplyP &p, int d, hipStream_t st, bool bwd) {
         case 128: return launch_apply<T, 128>(p, st, bwd);
         case 256: return launch_apply<T, 256>(p, st, bwd);
         case 512: return launch_apply<T, 512>(p, st, bwd);
+        case 1024: return launch_apply<T, 1024>(p, st, bwd);
         default:
-            ssa_set_error("sparse_gather_attention: head dim %d unsupported (4..256, power of 2)", d);
+            ssa_set_error("sparse_gather_attention: head dim %d has no kernel instance", d);
             return SSA_E_UNSUP;
     }
 }

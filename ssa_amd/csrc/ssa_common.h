@@ -259,9 +259,9 @@ __host__ __device__ __forceinline__ int64_t ceil_div(int64_t a, int64_t b) { ret
 // and elements past d read zeros and store nothing.
 inline bool ssa_head_dim_ok(int d, int dtype) {
     const int vec = dtype == SSA_F32 ? 4 : 8;
-    return d >= 4 && d <= 512 && ((d & (d - 1)) == 0 || d % vec == 0);
+    return d >= 4 && d <= 1024 && ((d & (d - 1)) == 0 || d % vec == 0);
 }
-// the smallest power-of-two instance (4..512) that covers d
+// the smallest power-of-two instance (4..1024) that covers d
 inline int ssa_pow2_instance(int d) {
     int D = 4;
     while (D < d) D <<= 1;

@@ -3559,7 +3559,7 @@ int make_dims(const ssa_graph_args *a, Dims &D, bool need_q = true, int64_t ws_c
                   "build_graph: q/k dtype");
     SSA_CHECK_ARG(a->G == 0 || a->glob, "build_graph: glob is null");
     if (!ssa_head_dim_ok(a->d, a->q.dtype)) {
-        ssa_set_error("build_graph: head dim %d unsupported (4..512: a power of two or a multiple "
+        ssa_set_error("build_graph: head dim %d unsupported (4..1024: a power of two or a multiple "
                       "of %d)", a->d, a->q.dtype == SSA_F32 ? 4 : 8);
         return SSA_E_UNSUP;
     }
@@ -3736,6 +3736,7 @@ int launch_hash_one(const HashP &hp, int d, hipStream_t st) {
         case 128: return launch_hash_mfma<T, 128>(hp, st);
         case 256: return launch_hash_mfma<T, 256>(hp, st);
         case 512: return launch_hash_mfma<T, 512>(hp, st);
+        case 1024: return launch_hash_mfma<T, 1024>(hp, st);
     }
     ssa_set_error("hash: head dim %d", d);
     return SSA_E_UNSUP;
@@ -3845,6 +3846,7 @@ int rescore_dispatch(int d, const RsP &rp, int64_t grid, hipStream_t st) {
         case 128: return launch_rescore<T, 128>(rp, grid, st);
         case 256: return launch_rescore<T, 256>(rp, grid, st);
         case 512: return launch_rescore<T, 512>(rp, grid, st);
+        case 1024: return launch_rescore<T, 1024>(rp, grid, st);
     }
     ssa_set_error("rescore: head dim %d", d);
     return SSA_E_UNSUP;
@@ -3908,7 +3910,7 @@ int aux_dispatch(int d, bool mfma, const AuxP &ap, hipStream_t st) {
     case DD: hipLaunchKernelGGL((aux_valu_kernel<T, DD>), grid, dim3(256), 0, st, ap); break;
     switch (ssa_pow2_instance(d)) {
         SSA_AUX_VALU(4) SSA_AUX_VALU(8) SSA_AUX_VALU(16) SSA_AUX_VALU(32) SSA_AUX_VALU(64)
-        SSA_AUX_VALU(128) SSA_AUX_VALU(256) SSA_AUX_VALU(512)
+        SSA_AUX_VALU(128) SSA_AUX_VALU(256) SSA_AUX_VALU(512) SSA_AUX_VALU(1024)
         default: ssa_set_error("aux scores: head dim %d", d); return SSA_E_UNSUP;
     }
 #undef SSA_AUX_VALU

@@ -211,9 +211,10 @@ def test_apply_matching_shapes_reach_the_device_check():
 @pytest.mark.parametrize("d,dtype,ok", [(96, 1, True), (80, 1, True), (112, 2, True), (48, 0, True),
                                         (12, 0, True), (12, 1, False), (100, 1, False),
                                         (264, 0, True), (320, 1, True), (512, 0, True),
-                                        (516, 0, False), (1024, 1, False), (2, 0, False)])
+                                        (516, 0, True), (520, 1, True), (1024, 1, True),
+                                        (1028, 0, False), (2048, 1, False), (2, 0, False)])
 def test_head_dim_rule(d, dtype, ok):
-    """Head dims 4..512 that are powers of two or whole 16-byte pieces of the
+    """Head dims 4..1024 that are powers of two or whole 16-byte pieces of the
     element type are taken; others are refused with a message, before any
     launch."""
     from ssa_amd import _lib
