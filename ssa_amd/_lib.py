@@ -283,6 +283,27 @@ def _graph_outputs(a, width, mode, ids32, count_ties, device):
     return out, valid, ties
 
 
+def kernel_head_dim(d: int, dtype: torch.dtype) -> int:
+    """Head dim the kernels run at for rows of d elements: d itself when they
+    take it (a power of two from 4, or whole 16-byte pieces of the element
+    type), else d rounded up to whole pieces.  The added columns hold zeros,
+    which add exact zeros to every dot product: scores, hash projections and
+    outputs are those of the d columns (a zero sum may change sign, and the
+    kernels rank -0 and +0 as one key)."""
+    vec = 4 if dtype == torch.float32 else 8
+    if d >= 4 and (d & (d - 1) == 0 or d % vec == 0):
+        return d
+    dp = (d + vec - 1) // vec * vec
+    return dp if dp <= 1024 else d          # beyond: the library refuses d itself
+
+
+def _pad_cols(t, dp):
+    """t with its last dimension zero-padded to dp (t itself when it has dp)."""
+    if t is None or t.shape[-1] == dp:
+        return t
+    return torch.nn.functional.pad(t, (0, dp - t.shape[-1]))
+
+
 def build_graph(q, k, rand_proj, *, P, T, C, top_k, window, causal, is_cross, total_k, glob,
                 mode=GRAPH_FULL, q_proj=None, k_proj=None, count_ties=False, ids32=False,
                 noalloc=False):
@@ -292,7 +313,13 @@ def build_graph(q, k, rand_proj, *, P, T, C, top_k, window, causal, is_cross, to
     out_idx is int32 with -1 in the invalid slots and out_valid is None.  With
     noalloc the build runs through ssa_build_graph_noalloc: no workspace is
     allocated (the library's fixed scratch array serves instead; the outputs
-    are still allocated here)."""
+    are still allocated here).  Head dims the kernels do not take run
+    zero-padded (kernel_head_dim)."""
+    if q.dim() == 4 and k.dim() == 4 and q.shape[-1] == k.shape[-1]:
+        dp = kernel_head_dim(q.shape[-1], q.dtype)
+        q, k = _pad_cols(q, dp), _pad_cols(k, dp)
+        if rand_proj.dim() == 3 and rand_proj.shape[-1] < dp:
+            rand_proj = _pad_cols(rand_proj, dp)
     a, keep = _graph_args(q, k, rand_proj, P=P, T=T, C=C, top_k=top_k, window=window,
                           causal=causal, is_cross=is_cross, total_k=total_k, glob=glob, mode=mode,
                           q_proj=q_proj, k_proj=k_proj)
@@ -517,6 +544,16 @@ def gather_attention_fwd(q, k, v, neighbors, valid, scale, fp32w=False, dropout_
                                f"contiguous int32 tensor of {B * Hq * N} elements")
     if not (q.dtype == k.dtype == v.dtype):
         raise RuntimeError("ssa_amd.sparse_gather_attention: q, k, v dtypes differ")
+    d = q.shape[-1]
+    dp = kernel_head_dim(d, q.dtype)
+    if dp != d:
+        # head dims the kernels do not take: run zero-padded, keep the d columns
+        o = gather_attention_fwd(_pad_cols(q, dp), _pad_cols(k, dp), _pad_cols(v, dp), neighbors,
+                                 valid, scale, fp32w, dropout_p, seed, None, row_invalid)
+        if out is None:
+            return o[..., :d]
+        out.copy_(o[..., :d])
+        return out
     if out is None:
         B, Hq, N, d = q.shape
         out = torch.empty((B, N, Hq, d), dtype=q.dtype, device=q.device).transpose(1, 2)
@@ -535,6 +572,14 @@ def gather_attention_bwd(q, k, v, neighbors, valid, scale, fp32w, dropout_p, see
     workspace is allocated here); else the fp32-atomic backward."""
     check_apply_shapes(q, k, v, neighbors, valid, dout)
     require_device(q, k, v, neighbors, valid, dout)
+    d = q.shape[-1]
+    dp = kernel_head_dim(d, q.dtype)
+    if dp != d:
+        # head dims the kernels do not take: run zero-padded, keep the d columns
+        dq, dk, dv = gather_attention_bwd(_pad_cols(q, dp), _pad_cols(k, dp), _pad_cols(v, dp),
+                                          neighbors, valid, scale, fp32w, dropout_p, seed,
+                                          _pad_cols(dout, dp), deterministic)
+        return dq[..., :d].contiguous(), dk[..., :d].contiguous(), dv[..., :d].contiguous()
     B, Hq, N, d = q.shape
     _, Hkv, M, _ = k.shape
     do = dout.to(torch.float32).contiguous()

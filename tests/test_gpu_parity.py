@@ -97,6 +97,11 @@ GRAPH_CASES = [
     # beyond 512: the 1024 instances
     ("head_dim_640", 1, 2, 1, 64, 64, 640, 2, 3, 0, 20, 2, 1, True, False),
     ("head_dim_1024_cross", 1, 2, 2, 40, 70, 1024, 2, 3, 1, 20, 2, 1, False, True),
+    # head dims the kernels do not take (neither a power of two nor whole
+    # 16-byte pieces: 6 in every type, 20 in bf16 / f16, 125): run zero-padded
+    ("head_dim_6", 1, 2, 1, 64, 64, 6, 2, 3, 0, 20, 2, 1, True, False),
+    ("head_dim_20", 1, 2, 2, 80, 80, 20, 2, 3, 1, 24, 2, 1, True, False),
+    ("head_dim_125_cross", 1, 2, 1, 40, 70, 125, 2, 3, 1, 20, 2, 1, False, True),
     # key lengths beyond 32768: the bucket sort with 32-bit positions, the
     # cut entries' 16-bit fields read unsigned
     ("long_keys_causal", 1, 1, 1, 65536, 65536, 16, 2, 12, 0, 32, 2, 2, True, False),
@@ -357,6 +362,9 @@ APPLY_CASES = [
     (1, 4, 2, 7, 30, 512, 16),
     (1, 2, 1, 7, 30, 640, 12),
     (1, 2, 2, 5, 20, 1024, 10),
+    (1, 2, 1, 9, 30, 6, 12),
+    (1, 2, 2, 8, 25, 20, 10),
+    (1, 2, 1, 7, 30, 125, 12),
 ]
 
 
@@ -539,8 +547,8 @@ def _check_grad_rows(name, got, exp, dtype):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("case", [(1, 4, 2, 24, 30, 32, 16), (1, 4, 2, 24, 30, 96, 16),
                                   (1, 2, 1, 10, 30, 320, 12), (1, 2, 2, 6, 20, 512, 8),
-                                  (1, 2, 1, 5, 20, 1024, 8)],
-                         ids=["d32", "d96", "d320", "d512", "d1024"])
+                                  (1, 2, 1, 5, 20, 1024, 8), (1, 2, 1, 6, 20, 125, 8)],
+                         ids=["d32", "d96", "d320", "d512", "d1024", "d125"])
 def test_apply_backward_matches_autograd_reference(dtype, case):
     from ssa_amd import sparse_gather_attention
     B, H, nkv, N, M, d, K = case

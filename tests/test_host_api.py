@@ -188,3 +188,20 @@ def test_seeded_model_construction_matches_reference_state_dict(path):
     assert sorted(sd.keys()) == ref_keys
     for key in ref_keys:
         np.testing.assert_array_equal(sd[key].numpy(), z["sd_" + key], err_msg=key)
+
+
+def test_kernel_head_dim_pads_only_what_the_kernels_do_not_take():
+    """Head dims that are powers of two (from 4) or whole 16-byte pieces run
+    as they are; others run zero-padded to whole pieces (at least 4), and
+    beyond 1024 the caller's dim goes to the library, which refuses it."""
+    import torch
+
+    from ssa_amd._lib import kernel_head_dim
+    f32, bf16, f16 = torch.float32, torch.bfloat16, torch.float16
+    cases = [(1, f32, 4), (2, bf16, 8), (3, f32, 4), (4, bf16, 4), (6, f32, 8), (6, bf16, 8),
+             (20, f32, 20), (20, bf16, 24), (96, bf16, 96), (100, f16, 104), (125, f32, 128),
+             (125, bf16, 128), (640, bf16, 640), (1021, bf16, 1024), (1024, f32, 1024),
+             (1025, f32, 1025), (1030, bf16, 1030)]
+    for d, dt, want in cases:
+        assert kernel_head_dim(d, dt) == want, (d, dt)
+
