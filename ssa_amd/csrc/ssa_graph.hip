@@ -1962,7 +1962,10 @@ __device__ __forceinline__ void sel_boundary(uint32_t *ckey, int ebits, uint32_t
 template <typename T, bool LSH_MODE, bool CAUSAL, int CAP, bool WIDE>
 // Registers are held to what 8 waves per SIMD allow (the kernel waits on
 // memory and LDS; the bench workload's 5 KB of LDS per wave fits 8 as well).
-__global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE) __attribute__((amdgpu_waves_per_eu(8, 8)))
+// The 512-key buffer's rows (large kk, whose LDS allows fewer waves anyway)
+// take the register budget of 7, which spills fewer scalar registers.
+__global__ void __launch_bounds__(SEL_WAVES * SSA_WAVE)
+__attribute__((amdgpu_waves_per_eu(CAP >= SEL_CAP_LARGE ? 7 : 8, 8)))
 select_kernel(SelP p) {
     extern __shared__ uint32_t sel_smem[];
     const int64_t blk = xcd_logical_block(blockIdx.x, p.nblocks);
