@@ -1,0 +1,67 @@
+"""A deterministic sweep of graph-build shapes against the oracle.
+
+96 configurations drawn from a seeded generator over batch size, kv heads and
+group size, query and key lengths, head dims (including ones the kernels run
+zero-padded), hash rounds, planes, probes, neighbour counts, window, global
+tokens, causal / cross-attention and fp32 / bf16 / fp16 inputs.  q, k and the
+hyperplanes hold small integers, so every projection and score is exact in
+every type: the merged graph (neighbours and valid mask) must equal the
+oracle's bit for bit, and so must the LSH mode's neighbour lists, in order,
+tied kk-th scores included (the GPU replays the reference's top-k on those
+rows).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import has_gpu
+from test_gpu_parity import _graph_case
+
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skipif(not has_gpu(), reason="needs a ROCm GPU")]
+
+
+def _sweep_cases(n=96, seed=2024):
+    rng = np.random.default_rng(seed)
+    dtypes = [torch.float32, torch.bfloat16, torch.float16]
+    cases = []
+    for i in range(n):
+        cross = bool(rng.random() < 0.3)
+        causal = (not cross) and bool(rng.random() < 0.6)
+        nkv = int(rng.choice([1, 2, 4]))
+        H = nkv * int(rng.choice([1, 2, 4]))
+        B = int(rng.choice([1, 2]))
+        N = int(rng.integers(8, 400))
+        M = int(rng.integers(8, 700)) if cross else N
+        d = int(rng.choice([6, 16, 20, 32, 48, 64, 96, 128]))
+        R = int(rng.integers(1, 5))
+        maxP = int(rng.integers(2, 9))
+        T = int(rng.integers(0, 4))
+        w = int(rng.integers(0, 9))
+        G = int(rng.integers(0, 4))
+        K = int(rng.integers(2 * w + G + 10, 2 * w + G + 80))
+        dt = dtypes[int(rng.integers(0, 3))]
+        cases.append(((f"sweep{i}", B, H, nkv, N, M, d, R, maxP, T, K, w, G, causal, cross), dt))
+    return cases
+
+
+CASES = _sweep_cases()
+
+
+@pytest.mark.parametrize("case,dtype", CASES, ids=[c[0][0] for c in CASES])
+def test_graph_shape_sweep_matches_oracle(case, dtype):
+    attn, got, got_v, ref, (B, H, N, M, K, w, cross, causal, glob) = _graph_case(
+        case, 11, dtype=dtype)
+    win = (np.zeros((N, 0), np.int64) if cross else attn.win_builder(N, M, "cpu").numpy())
+    rnb, rva = oracle.merge(win, glob.numpy(), ref["idx"], has_self=not cross, total_k=K)
+    np.testing.assert_array_equal(got.cpu().numpy().reshape(B * H, N, -1), rnb)
+    np.testing.assert_array_equal(got_v.cpu().numpy().reshape(B * H, N, -1), rva)
+
+
+@pytest.mark.parametrize("case,dtype", CASES[::2], ids=[c[0][0] for c in CASES[::2]])
+def test_lsh_shape_sweep_matches_oracle(case, dtype):
+    attn, got, _, ref, (B, H, N, M, K, w, cross, causal, glob) = _graph_case(
+        case, 13, dtype=dtype, lsh_only=True)
+    np.testing.assert_array_equal(got.cpu().numpy().reshape(B * H, N, -1), ref["idx"])
+
