@@ -1,4 +1,5 @@
-"""A deterministic sweep of graph-build shapes against the oracle.
+"""Deterministic sweeps of graph-build and gather-attention shapes against
+the oracle.
 
 96 configurations drawn from a seeded generator over batch size, kv heads and
 group size, query and key lengths, head dims (including ones the kernels run
@@ -17,6 +18,7 @@ import torch
 import oracle
 from conftest import has_gpu
 from test_gpu_parity import _graph_case
+from test_gpu_parity import test_apply_matches_oracle as _apply_check
 
 pytestmark = [pytest.mark.gpu,
               pytest.mark.skipif(not has_gpu(), reason="needs a ROCm GPU")]
@@ -65,3 +67,37 @@ def test_lsh_shape_sweep_matches_oracle(case, dtype):
         case, 13, dtype=dtype, lsh_only=True)
     np.testing.assert_array_equal(got.cpu().numpy().reshape(B * H, N, -1), ref["idx"])
 
+
+
+
+def _apply_sweep_cases(n=48, seed=77):
+    """(B, Hq, Hkv, N, M, d, K) for the gather attention, with dtype and
+    fp32_attn_weights: random group sizes, head dims 4 to 1024 (including
+    ones run zero-padded), K from 1 to 600."""
+    rng = np.random.default_rng(seed)
+    dtypes = [torch.float32, torch.bfloat16, torch.float16]
+    dims = [4, 6, 8, 16, 20, 24, 32, 40, 64, 72, 96, 128, 160, 256, 320, 512, 640, 1024]
+    cases = []
+    for i in range(n):
+        nkv = int(rng.choice([1, 2, 4]))
+        H = nkv * int(rng.choice([1, 2, 4]))
+        B = int(rng.choice([1, 2]))
+        N = int(rng.integers(1, 40))
+        M = int(rng.integers(1, 300))
+        d = int(rng.choice(dims))
+        K = int(rng.integers(1, 600))
+        cases.append(((B, H, nkv, N, M, d, K), dtypes[int(rng.integers(0, 3))],
+                      bool(rng.random() < 0.3)))
+    return cases
+
+
+APPLY_CASES = _apply_sweep_cases()
+
+
+@pytest.mark.parametrize("case,dtype,fp32w", APPLY_CASES,
+                         ids=[f"apply{i}" for i in range(len(APPLY_CASES))])
+def test_apply_shape_sweep_matches_oracle(case, dtype, fp32w):
+    """Every query row within the per-row bar of the oracle's float64 apply
+    (1e-5 relative in fp32, 2e-2 in bf16 / fp16; 30% of slots masked, slot 0
+    valid)."""
+    _apply_check(case, dtype, fp32w)
