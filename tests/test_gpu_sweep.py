@@ -1,5 +1,5 @@
 """Deterministic sweeps of graph-build and gather-attention shapes against
-the oracle.
+the oracle (and of the backward against float64 autograd).
 
 96 configurations drawn from a seeded generator over batch size, kv heads and
 group size, query and key lengths, head dims (including ones the kernels run
@@ -19,6 +19,7 @@ import oracle
 from conftest import has_gpu
 from test_gpu_parity import _graph_case
 from test_gpu_parity import test_apply_matches_oracle as _apply_check
+from test_gpu_parity import test_apply_backward_matches_autograd_reference as _bwd_check
 
 pytestmark = [pytest.mark.gpu,
               pytest.mark.skipif(not has_gpu(), reason="needs a ROCm GPU")]
@@ -101,3 +102,30 @@ def test_apply_shape_sweep_matches_oracle(case, dtype, fp32w):
     (1e-5 relative in fp32, 2e-2 in bf16 / fp16; 30% of slots masked, slot 0
     valid)."""
     _apply_check(case, dtype, fp32w)
+
+
+def _bwd_sweep_cases(n=24, seed=91):
+    """(B, Hq, Hkv, N, M, d, K) for the backward, small enough for the float64
+    autograd reference (which materialises the gathered rows)."""
+    rng = np.random.default_rng(seed)
+    dims = [4, 6, 16, 20, 32, 48, 64, 96, 128, 200, 256]
+    cases = []
+    for i in range(n):
+        nkv = int(rng.choice([1, 2]))
+        H = nkv * int(rng.choice([1, 2, 4]))
+        cases.append(((int(rng.choice([1, 2])), H, nkv, int(rng.integers(1, 16)),
+                       int(rng.integers(2, 120)), int(rng.choice(dims)),
+                       int(rng.integers(1, 100))),
+                      [torch.float32, torch.bfloat16][int(rng.integers(0, 2))]))
+    return cases
+
+
+BWD_CASES = _bwd_sweep_cases()
+
+
+@pytest.mark.parametrize("case,dtype", BWD_CASES,
+                         ids=[f"bwd{i}" for i in range(len(BWD_CASES))])
+def test_apply_backward_shape_sweep_matches_autograd(case, dtype):
+    """dq, dk, dv per row against float64 autograd of the same function."""
+    _bwd_check(dtype, case)
+
