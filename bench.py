@@ -490,9 +490,9 @@ def main():
                          "5 times, as the reference point for rocprofv3 FETCH_SIZE/WRITE_SIZE")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(the sparse forward shards by kv-head group with no exchange inside attention; "
-              "see the sharding note of the design document).", file=sys.stderr)
+        print(f"bench.py: measures one GPU; --gpus {args.gpus} is not supported (the sparse "
+              "forward would shard by kv-head group, with no exchange inside attention).",
+              file=sys.stderr)
         sys.exit(2)
     import torch
     dev = "cuda:0"
