@@ -100,6 +100,7 @@ GRAPH_CASES = [
     # head dims the kernels do not take (neither a power of two nor whole
     # 16-byte pieces: 6 in every type, 20 in bf16 / f16, 125): run zero-padded
     ("head_dim_6", 1, 2, 1, 64, 64, 6, 2, 3, 0, 20, 2, 1, True, False),
+    ("head_dim_3", 1, 2, 1, 48, 48, 3, 2, 3, 1, 20, 2, 1, True, False),
     ("head_dim_20", 1, 2, 2, 80, 80, 20, 2, 3, 1, 24, 2, 1, True, False),
     ("head_dim_125_cross", 1, 2, 1, 40, 70, 125, 2, 3, 1, 20, 2, 1, False, True),
     # key lengths beyond 32768: the bucket sort with 32-bit positions, the
@@ -363,6 +364,8 @@ APPLY_CASES = [
     (1, 2, 1, 7, 30, 640, 12),
     (1, 2, 2, 5, 20, 1024, 10),
     (1, 2, 1, 9, 30, 6, 12),
+    (1, 2, 1, 9, 30, 2, 12),
+    (1, 2, 2, 8, 25, 3, 10),
     (1, 2, 2, 8, 25, 20, 10),
     (1, 2, 1, 7, 30, 125, 12),
 ]
