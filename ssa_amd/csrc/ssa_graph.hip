@@ -420,33 +420,37 @@ __device__ __forceinline__ void inst_decode(const QbP &p, int inst, int &bh, int
     bh = p.bh0 + inst / (p.NS * p.R);
 }
 
-__global__ void __launch_bounds__(256) qb_hist_kernel(QbP p) {
-    extern __shared__ int32_t hist[];
-    const int inst = blockIdx.y;
+// Query block bx (256 queries) of nbx of instance inst: its count per bucket
+// (hist: NB words of the workgroup's LDS; 256 threads)
+__device__ void qb_hist_block(const QbP &p, int inst, int bx, int nbx, int32_t *hist) {
     int bh, r, t;
     inst_decode(p, inst, bh, r, t);
     for (int u = threadIdx.x; u < p.NB; u += blockDim.x) hist[u] = 0;
     __syncthreads();
-    const int n = blockIdx.x * blockDim.x + threadIdx.x;
+    const int n = bx * (int)blockDim.x + (int)threadIdx.x;
     if (n < p.N) {
         const int u = p.qid[(((int64_t)bh * p.N + n) * p.R + r) * p.NS + t];
         atomicAdd(&hist[u], 1);
     }
     __syncthreads();
-    int32_t *hb = p.hcnt + ((int64_t)inst * gridDim.x + blockIdx.x) * p.NB;
+    int32_t *hb = p.hcnt + ((int64_t)inst * nbx + bx) * p.NB;
     for (int u = threadIdx.x; u < p.NB; u += blockDim.x) hb[u] = hist[u];
+}
+
+__global__ void __launch_bounds__(256) qb_hist_kernel(QbP p) {
+    extern __shared__ int32_t hist[];
+    qb_hist_block(p, (int)blockIdx.y, (int)blockIdx.x, (int)gridDim.x, hist);
 }
 
 // one block per instance: bucket totals and offsets, the first position of
 // each query block's queries in each bucket (so queries stay in position
 // order inside a bucket), and the instance's tile count
-__global__ void __launch_bounds__(256) qb_scan_kernel(QbP p) {
+__device__ void qb_scan_block(const QbP &p, int inst) {
     // thread = (bucket column, query-block group): with NB <= 256 the NB
     // columns are split over 256 / NB groups of query blocks; with more
     // buckets a thread takes NB / 256 columns over every block
     __shared__ int32_t part[256];          // per thread: its sum, then its starting offset
     __shared__ int32_t sq[256], st[256];   // per column: bucket count, tile count (scanned)
-    const int inst = blockIdx.x;
     const int tid = threadIdx.x;
     int bh, r, t;
     inst_decode(p, inst, bh, r, t);
@@ -529,6 +533,8 @@ __global__ void __launch_bounds__(256) qb_scan_kernel(QbP p) {
         }
     }
 }
+
+__global__ void __launch_bounds__(256) qb_scan_kernel(QbP p) { qb_scan_block(p, (int)blockIdx.x); }
 
 // Position of an instance in the tile list: ordered by (kv head, query head
 // within the GQA group, round, id set).  An XCD takes a contiguous range of
@@ -1135,10 +1141,11 @@ struct LsP {
     uint2 *ctab;
 };
 
-__global__ void __launch_bounds__(256) list_sort_kernel(LsP p) {
-    extern __shared__ uint32_t ls_key[];
-    const int64_t prow = blockIdx.x / p.NB;
-    const int u = (int)(blockIdx.x % p.NB);
+// Workgroup blk: list (kv head / round row blk / NB, bucket blk % NB);
+// ls_key: the workgroup's dynamic LDS (256 threads)
+__device__ void list_sort_block(const LsP &p, int64_t blk, uint32_t *ls_key) {
+    const int64_t prow = blk / p.NB;
+    const int u = (int)(blk % p.NB);
     if (p.kpart && u == 0 && prow % p.R == 0) {
         __shared__ uint32_t kred[4];
         const int64_t bk = prow / p.R;
@@ -1259,6 +1266,36 @@ __global__ void __launch_bounds__(256) list_sort_kernel(LsP p) {
             carry = __shfl(c, 0, SSA_WAVE);
         }
     }
+}
+
+__global__ void __launch_bounds__(256) list_sort_kernel(LsP p) {
+    extern __shared__ uint32_t ls_key[];
+    list_sort_block(p, (int64_t)blockIdx.x, ls_key);
+}
+
+// Launches shared by independent work of the first head chunk, whose query
+// ids the launch of the sort's top levels computed: the sort's segment
+// kernel (workgroups [0, nseg)) beside that chunk's query histogram (the
+// rest, nqb per instance), and the list sort (workgroups [0, nls)) beside
+// the chunk's bucket scan (one per instance).  Each pair reads and writes
+// disjoint data, and the segment kernel and the list sort leave most CUs
+// idle on their own.
+__global__ void __launch_bounds__(SEG_WAVES * SSA_WAVE)
+sort_seg_hist_kernel(SortTopArgs s, QbP qp, int nseg, int nqb) {
+    extern __shared__ uint32_t sh_lds[];       // the segment waves' arrays, or NB counts
+    const int blk = (int)blockIdx.x;
+    if (blk < nseg) {
+        sort_seg_blocks<uint16_t>(s.gkv, s.n, s.segs, s.segcount, s.perm, sh_lds, blk, nseg);
+    } else {
+        const int b = blk - nseg;
+        qb_hist_block(qp, b / nqb, b % nqb, nqb, (int32_t *)sh_lds);
+    }
+}
+
+__global__ void __launch_bounds__(256) list_sort_scan_kernel(LsP lp, QbP qp, int nls) {
+    extern __shared__ uint32_t ls_key[];
+    if ((int)blockIdx.x < nls) list_sort_block(lp, (int64_t)blockIdx.x, ls_key);
+    else qb_scan_block(qp, (int)blockIdx.x - nls);
 }
 
 // Per (query row, list): the number of sorted members below the query
@@ -4072,6 +4109,33 @@ AuxP aux_params(const Dims &D, const ssa_graph_args *a, const Layout &L, char *w
     return ap;
 }
 
+// Query bucketing parameters of the head chunk [bh0, bh0 + nbh)
+QbP qb_params(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws, int64_t bh0,
+              int nbh) {
+    QbP qp{};
+    qp.qid = (const uint16_t *)(ws + L.qid);
+    qp.bsize = (const int32_t *)(ws + L.bsize);
+    qp.bstart = (const int32_t *)(ws + L.bstart);
+    qp.cnt = (int32_t *)(ws + L.cnt);
+    qp.off = (int32_t *)(ws + L.off);
+    qp.cur = nullptr;
+    qp.hcnt = (int32_t *)(ws + L.cur);
+    qp.qlist = (int32_t *)(ws + L.qlist);
+    qp.tiles = (int32_t *)(ws + L.tiles);
+    qp.ntiles = (int32_t *)(ws + L.ntiles);
+    qp.tcnt = (int32_t *)(ws + L.tcnt);
+    qp.kbase = (int32_t *)(ws + L.kbase);
+    qp.N = D.N; qp.R = D.R; qp.NS = D.NS; qp.NB = D.NB; qp.Hq = D.Hq; qp.Hkv = D.Hkv;
+    qp.rep = D.rep; qp.bh0 = (int)bh0; qp.ninst = nbh * D.R * D.NS; qp.C = D.C;
+    // round-major tiles when a head's q rows exceed half an XCD's 4 MB L2
+    qp.rmajor = (int64_t)D.N * D.d * (a->q.dtype == SSA_F32 ? 4 : 2) > ((int64_t)2 << 20);
+    return qp;
+}
+
+// Static LDS of the list sort's and the bucket scan's workgroup bodies (kred,
+// part, sq, st), with room to spare
+constexpr size_t LS_SCAN_STATIC_LDS = 4096;
+
 template <typename T>
 int launch_sort_aux(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws,
                     hipStream_t st) {
@@ -4111,7 +4175,20 @@ int launch_sort_aux(const Dims &D, const ssa_graph_args *a, const Layout &L, cha
 #undef SSA_SORT_AUX
     }
     SSA_CHECK_LAUNCH();
-    return ssa_launch_sort_seg(sa, st);
+    // the segments, beside the first chunk's query histogram (its ids came
+    // from the launch above)
+    static_assert(SEG_WAVES * SSA_WAVE == 256, "the query histogram takes 256 queries a block");
+    const QbP qp = qb_params(D, a, L, ws, 0, nbh);
+    const int nseg = ssa_sort_seg_blocks(sa.rows, sa.n);
+    const int nqb = (int)ceil_div(D.N, 256);
+    const size_t hl = std::max<size_t>((size_t)SEG_WAVES * seg_lds_words<uint16_t>() * 4,
+                                       (size_t)D.NB * 4);
+    SSA_CHECK_HIP(hipFuncSetAttribute((const void *)sort_seg_hist_kernel,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)hl));
+    hipLaunchKernelGGL(sort_seg_hist_kernel, dim3((unsigned)(nseg + (int64_t)qp.ninst * nqb)),
+                       dim3(256), hl, st, sa, qp, nseg, nqb);
+    SSA_CHECK_LAUNCH();
+    return SSA_OK;
 }
 
 template <typename T>
@@ -4190,11 +4267,28 @@ int keys_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char *ws
                           "bytes of LDS", D.C, D.M, lds);
             return SSA_E_UNSUP;
         }
+        const int64_t nls = D.BK * D.R * D.NB;
+        if (sort_aux && lds + LS_SCAN_STATIC_LDS <= SSA_LDS_BYTES) {
+            // beside the first chunk's bucket scan (its histogram ran beside
+            // the segments)
+            const QbP qp = qb_params(D, a, L, ws, 0, (int)std::min<int64_t>(D.BH, D.nbh_chunk));
+            SSA_CHECK_HIP(hipFuncSetAttribute((const void *)list_sort_scan_kernel,
+                                              hipFuncAttributeMaxDynamicSharedMemorySize,
+                                              (int)lds));
+            hipLaunchKernelGGL(list_sort_scan_kernel, dim3((unsigned)(nls + qp.ninst)), dim3(256),
+                               lds, st, lp, qp, (int)nls);
+            SSA_CHECK_LAUNCH();
+            return SSA_OK;
+        }
         SSA_CHECK_HIP(hipFuncSetAttribute((const void *)list_sort_kernel,
                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        hipLaunchKernelGGL(list_sort_kernel, dim3((unsigned)(D.BK * D.R * D.NB)), dim3(256), lds, st,
-                           lp);
+        hipLaunchKernelGGL(list_sort_kernel, dim3((unsigned)nls), dim3(256), lds, st, lp);
         SSA_CHECK_LAUNCH();
+        if (sort_aux) {
+            const QbP qp = qb_params(D, a, L, ws, 0, (int)std::min<int64_t>(D.BH, D.nbh_chunk));
+            hipLaunchKernelGGL(qb_scan_kernel, dim3((unsigned)qp.ninst), dim3(256), 0, st, qp);
+            SSA_CHECK_LAUNCH();
+        }
     }
     return SSA_OK;
 }
@@ -4221,28 +4315,15 @@ int queries_typed(const Dims &D, const ssa_graph_args *a, const Layout &L, char 
         const AuxP ap = aux_params(D, a, L, ws, bh0, nbh, fuse_qhash);
         if (!D.fused && !(sort_aux && bh0 == 0)) rc = aux_dispatch<T>(D.d, mfma, ap, st);
         if (rc) return rc;
-        QbP qp{};
-        qp.qid = (const uint16_t *)(ws + L.qid);
-        qp.bsize = (const int32_t *)(ws + L.bsize);
-        qp.bstart = (const int32_t *)(ws + L.bstart);
-        qp.cnt = (int32_t *)(ws + L.cnt);
-        qp.off = (int32_t *)(ws + L.off);
-        qp.cur = nullptr;
-        qp.hcnt = (int32_t *)(ws + L.cur);
-        qp.qlist = (int32_t *)(ws + L.qlist);
-        qp.tiles = (int32_t *)(ws + L.tiles);
-        qp.ntiles = (int32_t *)(ws + L.ntiles);
-        qp.tcnt = (int32_t *)(ws + L.tcnt);
-        qp.kbase = (int32_t *)(ws + L.kbase);
-        qp.N = D.N; qp.R = D.R; qp.NS = D.NS; qp.NB = D.NB; qp.Hq = D.Hq; qp.Hkv = D.Hkv;
-        qp.rep = D.rep; qp.bh0 = (int)bh0; qp.ninst = ninst; qp.C = D.C;
-        // round-major tiles when a head's q rows exceed half an XCD's 4 MB L2
-        qp.rmajor = (int64_t)D.N * D.d * (a->q.dtype == SSA_F32 ? 4 : 2) > ((int64_t)2 << 20);
+        QbP qp = qb_params(D, a, L, ws, bh0, nbh);
         const dim3 gq((unsigned)ceil_div(D.N, 256), (unsigned)ninst);
-        hipLaunchKernelGGL(qb_hist_kernel, gq, dim3(256), (size_t)D.NB * 4, st, qp);
-        SSA_CHECK_LAUNCH();
-        hipLaunchKernelGGL(qb_scan_kernel, dim3((unsigned)ninst), dim3(256), 0, st, qp);
-        SSA_CHECK_LAUNCH();
+        // (the first chunk's histogram and scan ran in the key phase when sort_aux)
+        if (!(sort_aux && bh0 == 0)) {
+            hipLaunchKernelGGL(qb_hist_kernel, gq, dim3(256), (size_t)D.NB * 4, st, qp);
+            SSA_CHECK_LAUNCH();
+            hipLaunchKernelGGL(qb_scan_kernel, dim3((unsigned)ninst), dim3(256), 0, st, qp);
+            SSA_CHECK_LAUNCH();
+        }
         {
             auto bk_of = [&](int64_t bh) { return (bh / D.Hq) * D.Hkv + (bh % D.Hq) / D.rep; };
             qp.heads = (bk_of(bh0 + nbh - 1) - bk_of(bh0) + 1) * D.rep;

@@ -28,6 +28,8 @@ struct SortTopArgs {
 int ssa_sort_top_setup(const uint16_t *ids, int rows, int n, int P, int32_t *perm,
                        int32_t *bstart, int32_t *bsize, uint16_t *tmp, SortTopArgs *a);
 int ssa_launch_sort_seg(const SortTopArgs &a, hipStream_t st);
+// workgroups of the segment launch (SEG_WAVES waves each) for rows x n keys
+int ssa_sort_seg_blocks(int rows, int n);
 int ssa_launch_bucket_sort(const uint16_t *ids, int rows, int n, int P, int32_t *perm,
                            int32_t *bstart, int32_t *bsize, uint16_t *tmp, hipStream_t st,
                            bool counter_clear = true);

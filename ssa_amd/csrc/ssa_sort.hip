@@ -51,195 +51,12 @@ sort_top_kernel(const uint16_t *ids, int n, int NB, int32_t *perm, int32_t *bsta
                       tl_in_lds, cap, smem_raw, sh);
 }
 
-// ---------------------------------------------------------------- segments
-// Kernel B, one wavefront per listed segment (<= SEG_T keys), anywhere on the
-// chip: the segment's remaining introsort subtree (wave partitions above 64
-// keys, the register path below), then the final insertion sort of each leaf
-// (one leaf per lane; partitions leave max(left) <= min(right), so this equals
-// the reference's final insertion pass over the row), and its slice of perm.
-constexpr int SEG_WAVES = 4;
-constexpr int SEG_STACK = SEG_T / (LEAF + 1) + 2;
-constexpr int SEG_PER_LANE = SEG_T / SSA_WAVE;
-
-// A segment whose keys are all equal: libstdc++'s partitions then depend on
-// its length alone.  The median of three (first + 1, middle, last - 1) is the
-// middle element, moved to the front; the unguarded scan stops at every
-// element, so it swaps positions k and n - k for 1 <= k < n / 2 and cuts at
-// ceil(n / 2); both halves recurse the same way down to leaves of LEAF, whose
-// insertion sort moves nothing.  So an element's final slot follows from its
-// position in O(log n) steps, and the subtree is one permutation.
-__device__ __forceinline__ int eq_final_pos(int n, int i) {
-    int base = 0;
-    while (n > LEAF) {
-        const int h = n >> 1;
-        i = i == 0 ? h : (i == h ? 0 : i);
-        if (i != 0 && 2 * i != n) i = n - i;
-        const int c = (n + 1) >> 1;
-        if (i < c) {
-            n = c;
-        } else {
-            base += c;
-            i -= c;
-            n -= c;
-        }
-    }
-    return base + i;
-}
-// partition levels the closed form takes (the larger half each time): the
-// subtree reaches no depth limit when the segment's depth is at least this
-__device__ __forceinline__ int eq_levels(int n) {
-    int l = 0;
-    for (; n > LEAF; n = (n + 1) >> 1) ++l;
-    return l;
-}
-
-template <typename Pos>
-__host__ __device__ constexpr int seg_lds_words() {
-    // key (u16), idx, TL, TR (Pos) x SEG_T each, bits, stack
-    return (SEG_T * (2 + 3 * (int)sizeof(Pos))) / 4 + (SEG_T / 32 + 1) + 2 * SEG_STACK;
-}
-
 template <typename Pos>
 __global__ void __launch_bounds__(SEG_WAVES * SSA_WAVE)
 sort_seg_kernel(const typename SortWords<Pos>::W *gkv, int n, const int4 *segs,
                 const int *segcount, int32_t *perm) {
-    using W = typename SortWords<Pos>::W;
-    constexpr int SH = SortWords<Pos>::SH;
     __shared__ uint32_t lds[SEG_WAVES * seg_lds_words<Pos>()];
-    const int wid = __builtin_amdgcn_readfirstlane(threadIdx.x / SSA_WAVE);
-    const int lane = lane_id();
-    uint32_t *w0 = lds + wid * seg_lds_words<Pos>();
-    Pos *idx = (Pos *)w0;
-    Pos *TL = idx + SEG_T;
-    Pos *TR = TL + SEG_T;
-    uint16_t *key = (uint16_t *)(TR + SEG_T);
-    uint32_t *bits = (uint32_t *)(key + SEG_T);
-    uint32_t *stk = bits + (SEG_T / 32 + 1);
-    uint32_t *sdep = stk + SEG_STACK;
-    const int count = *segcount;
-    const int stride = (int)gridDim.x * SEG_WAVES;
-    for (int sgi = (int)blockIdx.x * SEG_WAVES + wid; sgi < count; sgi += stride) {
-        const int4 e = segs[sgi];
-        const int row = e.x, f0 = e.y, m = e.z, depth0 = e.w;
-        const W *src = gkv + (int64_t)row * n + f0;
-        int32_t *pout = perm + (int64_t)row * n + f0;
-        W rv[SEG_PER_LANE];
-        uint32_t kmin = 0xffffu, kmax = 0u;
-#pragma unroll
-        for (int u = 0; u < SEG_PER_LANE; ++u) {
-            const int i = lane + SSA_WAVE * u;
-            rv[u] = src[min(i, m - 1)];
-            const uint32_t k = (uint32_t)(rv[u] & 0xffffu);
-            kmin = min(kmin, k);
-            kmax = max(kmax, k);
-        }
-        if (wave_min_u(kmin) == wave_max_u(kmax) && depth0 >= eq_levels(m)) {
-            // every key equal: the segment's permutation in closed form
-#pragma unroll
-            for (int u = 0; u < SEG_PER_LANE; ++u) {
-                const int i = lane + SSA_WAVE * u;
-                if (i < m) pout[eq_final_pos(m, i)] = (int32_t)(Pos)(rv[u] >> SH);
-            }
-            continue;
-        }
-#pragma unroll
-        for (int u = 0; u < SEG_PER_LANE; ++u) {
-            const int i = lane + SSA_WAVE * u;
-            if (i < m) {
-                key[i] = (uint16_t)(rv[u] & 0xffffu);
-                idx[i] = (Pos)(rv[u] >> SH);
-            }
-        }
-        for (int w = lane; w < SEG_T / 32 + 1; w += SSA_WAVE) bits[w] = w == 0 ? 1u : 0u;
-        wave_sync_lds();
-        if (m > LEAF) {
-            int top = 1;
-            if (lane == 0) { stk[0] = (uint32_t)m << 16; sdep[0] = (uint32_t)depth0; }
-            wave_sync_lds();
-            while (top > 0) {
-                --top;
-                const uint32_t se = stk[top];
-                const int a = (int)(se & 0xffffu), b = (int)(se >> 16);
-                const int d = (int)sdep[top];
-                wave_sync_lds();
-                {
-                    // a sub-segment whose keys are all equal: its subtree in
-                    // closed form, each slot then a leaf of its own
-                    uint32_t smin = 0xffffu, smax = 0u;
-#pragma unroll
-                    for (int u = 0; u < SEG_PER_LANE; ++u) {
-                        const int i = a + lane + SSA_WAVE * u;
-                        if (i < b) {
-                            const uint32_t k = key[i];
-                            smin = min(smin, k);
-                            smax = max(smax, k);
-                        }
-                    }
-                    if (wave_min_u(smin) == wave_max_u(smax) && d >= eq_levels(b - a)) {
-                        Pos iv[SEG_PER_LANE];
-#pragma unroll
-                        for (int u = 0; u < SEG_PER_LANE; ++u) {
-                            const int i = a + lane + SSA_WAVE * u;
-                            iv[u] = i < b ? idx[i] : (Pos)0;
-                        }
-                        wave_sync_lds();
-#pragma unroll
-                        for (int u = 0; u < SEG_PER_LANE; ++u) {
-                            const int i = lane + SSA_WAVE * u;
-                            if (a + i < b) {
-                                idx[a + eq_final_pos(b - a, i)] = iv[u];
-                                atomicOr(&bits[(a + i) >> 5], 1u << ((a + i) & 31));
-                            }
-                        }
-                        wave_sync_lds();
-                        continue;
-                    }
-                }
-                if (d == 0) {
-                    if (lane == 0) heap_sort_range(key, idx, a, b);
-                    wave_sync_lds();
-                    continue;
-                }
-                if (b - a <= SSA_WAVE) {
-                    wave_small_sort(key, idx, bits, a, b - a, d);
-                    continue;
-                }
-                const int cut = wave_partition(key, idx, TL, TR, a, b);
-                if (lane == 0) {
-                    atomicOr(&bits[cut >> 5], 1u << (cut & 31));
-                    if (cut - a > LEAF) { stk[top] = (uint32_t)a | ((uint32_t)cut << 16); sdep[top] = d - 1; }
-                }
-                if (cut - a > LEAF) ++top;
-                if (lane == 0 && b - cut > LEAF) {
-                    stk[top] = (uint32_t)cut | ((uint32_t)b << 16);
-                    sdep[top] = d - 1;
-                }
-                if (b - cut > LEAF) ++top;
-                wave_sync_lds();
-            }
-        }
-        // final insertion sort, one leaf per lane
-        for (int s0 = lane; s0 < m; s0 += SSA_WAVE) {
-            if (!((bits[s0 >> 5] >> (s0 & 31)) & 1u)) continue;
-            int e1 = s0 + 1;
-            while (e1 < m && !((bits[e1 >> 5] >> (e1 & 31)) & 1u)) ++e1;
-            for (int i = s0 + 1; i < e1; ++i) {
-                const uint16_t vk = key[i];
-                const Pos vi = idx[i];
-                int j = i;
-                while (j > s0 && key[j - 1] > vk) {
-                    key[j] = key[j - 1];
-                    idx[j] = idx[j - 1];
-                    --j;
-                }
-                key[j] = vk;
-                idx[j] = vi;
-            }
-        }
-        wave_sync_lds();
-        for (int i = lane; i < m; i += SSA_WAVE) pout[i] = (int32_t)idx[i];
-        wave_sync_lds();
-    }
+    sort_seg_blocks<Pos>(gkv, n, segs, segcount, perm, lds, (int)blockIdx.x, (int)gridDim.x);
 }
 
 __global__ void sort_zero_kernel(int *p) {
@@ -319,11 +136,15 @@ int ssa_sort_top_setup(const uint16_t *ids, int rows, int n, int P, int32_t *per
     return SSA_OK;
 }
 
+int ssa_sort_seg_blocks(int rows, int n) {
+    const int64_t waves = std::max<int64_t>(1, std::min<int64_t>((int64_t)rows * n / 128, 8192));
+    return (int)ceil_div(waves, SEG_WAVES);
+}
+
 template <typename Pos>
 static int launch_seg(const typename SortWords<Pos>::W *gkv, int rows, int n, const int4 *segs,
                       const int *segcount, int32_t *perm, hipStream_t st) {
-    const int64_t waves = std::max<int64_t>(1, std::min<int64_t>((int64_t)rows * n / 128, 8192));
-    hipLaunchKernelGGL((sort_seg_kernel<Pos>), dim3((unsigned)ceil_div(waves, SEG_WAVES)),
+    hipLaunchKernelGGL((sort_seg_kernel<Pos>), dim3((unsigned)ssa_sort_seg_blocks(rows, n)),
                        dim3(SEG_WAVES * SSA_WAVE), 0, st, gkv, n, segs, segcount, perm);
     SSA_CHECK_LAUNCH();
     return SSA_OK;
