@@ -97,6 +97,9 @@ GRAPH_CASES = [
     # beyond 512: the 1024 instances
     ("head_dim_640", 1, 2, 1, 64, 64, 640, 2, 3, 0, 20, 2, 1, True, False),
     ("head_dim_1024_cross", 1, 2, 2, 40, 70, 1024, 2, 3, 1, 20, 2, 1, False, True),
+    # more than 2048 (head, round, id set) instances in one head chunk: the
+    # tiles ordered by a launch of their own instead of inside the scatter
+    ("many_instances", 10, 32, 8, 32, 32, 8, 8, 3, 0, 16, 2, 1, True, False),
     # head dims the kernels do not take (neither a power of two nor whole
     # 16-byte pieces: 6 in every type, 20 in bf16 / f16, 125): run zero-padded
     ("head_dim_6", 1, 2, 1, 64, 64, 6, 2, 3, 0, 20, 2, 1, True, False),
