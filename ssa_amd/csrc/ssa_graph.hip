@@ -360,7 +360,7 @@ __global__ void __launch_bounds__(256) knorm_kernel(KnP p) {
     if constexpr (SEG > 0) {
         constexpr int RPW = SSA_WAVE / SEG;           // rows per wavefront step
         constexpr int E = 16 / (int)sizeof(T);        // elements per segment
-#pragma unroll 4
+        // (not unrolled: the row sum's lane exchanges sit inside the loop)
         for (int m = m0 + wid * RPW + lane / SEG; m < m1; m += 4 * RPW) {
             T ev[E];
             const uint4 w = *reinterpret_cast<const uint4 *>(kh + (int64_t)m * p.ksn + (lane % SEG) * E);
