@@ -14,7 +14,8 @@ int64_t ssa_sort_tmp_bytes(int rows, int n);
 int32_t *ssa_sort_counter(uint16_t *tmp, int rows, int n);
 // The bucket sort's top levels as a caller launches them itself (rows of at
 // most 32768 keys: 16-bit positions, the row in LDS): sort_top_row's
-// arguments, the dynamic LDS it needs, then kernel B after it.
+// arguments and the dynamic LDS it needs; the caller then runs the segment
+// pass (sort_seg_blocks<uint16_t>) over ssa_sort_seg_blocks() workgroups.
 struct SortTopArgs {
     const uint16_t *ids;
     int rows, n, NB;
@@ -27,7 +28,6 @@ struct SortTopArgs {
 };
 int ssa_sort_top_setup(const uint16_t *ids, int rows, int n, int P, int32_t *perm,
                        int32_t *bstart, int32_t *bsize, uint16_t *tmp, SortTopArgs *a);
-int ssa_launch_sort_seg(const SortTopArgs &a, hipStream_t st);
 // workgroups of the segment launch (SEG_WAVES waves each) for rows x n keys
 int ssa_sort_seg_blocks(int rows, int n);
 int ssa_launch_bucket_sort(const uint16_t *ids, int rows, int n, int P, int32_t *perm,

@@ -150,10 +150,6 @@ static int launch_seg(const typename SortWords<Pos>::W *gkv, int rows, int n, co
     return SSA_OK;
 }
 
-int ssa_launch_sort_seg(const SortTopArgs &a, hipStream_t st) {
-    return launch_seg<uint16_t>(a.gkv, a.rows, a.n, a.segs, a.segcount, a.perm, st);
-}
-
 template <typename Pos>
 static int launch_sort(const uint16_t *ids, int rows, int n, int NB, int32_t *perm,
                        int32_t *bstart, int32_t *bsize, char *t, hipStream_t st) {
