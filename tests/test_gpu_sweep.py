@@ -1,9 +1,9 @@
 """Deterministic sweeps of graph-build and gather-attention shapes against
 the oracle (and of the backward against float64 autograd).
 
-96 configurations drawn from a seeded generator over batch size, kv heads and
-group size, query and key lengths, head dims (including ones the kernels run
-zero-padded), hash rounds, planes, probes, neighbour counts, window, global
+96 configurations (and 24 more over wider ranges) drawn from seeded
+generators over batch size, kv heads and group size, query and key lengths,
+head dims (including ones the kernels run zero-padded), hash rounds, planes, probes, neighbour counts, window, global
 tokens, causal / cross-attention and fp32 / bf16 / fp16 inputs.  q, k and the
 hyperplanes hold small integers, so every projection and score is exact in
 every type: the merged graph (neighbours and valid mask) must equal the
@@ -60,6 +60,40 @@ def test_graph_shape_sweep_matches_oracle(case, dtype):
     rnb, rva = oracle.merge(win, glob.numpy(), ref["idx"], has_self=not cross, total_k=K)
     np.testing.assert_array_equal(got.cpu().numpy().reshape(B * H, N, -1), rnb)
     np.testing.assert_array_equal(got_v.cpu().numpy().reshape(B * H, N, -1), rva)
+
+
+def _wide_cases(n=24, seed=777):
+    """Wider ranges: up to 2,499 queries and 2,999 keys, 8 kv heads, head dims
+    4 to 256, up to 8 rounds, 12 planes, 16-wide windows and 5 globals."""
+    rng = np.random.default_rng(seed)
+    dtypes = [torch.float32, torch.bfloat16, torch.float16]
+    cases = []
+    for i in range(n):
+        cross = bool(rng.random() < 0.3)
+        causal = (not cross) and bool(rng.random() < 0.6)
+        nkv = int(rng.choice([1, 2, 4, 8]))
+        H = nkv * int(rng.choice([1, 2, 4]))
+        B = int(rng.choice([1, 2, 3]))
+        N = int(rng.integers(8, 2500))
+        M = int(rng.integers(8, 3000)) if cross else N
+        d = int(rng.choice([4, 6, 8, 16, 20, 32, 48, 64, 80, 96, 112, 128, 256]))
+        R = int(rng.integers(1, 9))
+        maxP = int(rng.integers(2, 13))
+        T = int(rng.integers(0, 4))
+        w = int(rng.integers(0, 17))
+        G = int(rng.integers(0, 6))
+        K = int(rng.integers(2 * w + G + 10, 2 * w + G + 200))
+        cases.append(((f"wide{i}", B, H, nkv, N, M, d, R, maxP, T, K, w, G, causal, cross),
+                      dtypes[int(rng.integers(0, 3))]))
+    return cases
+
+
+WIDE_CASES = _wide_cases()
+
+
+@pytest.mark.parametrize("case,dtype", WIDE_CASES, ids=[c[0][0] for c in WIDE_CASES])
+def test_graph_wide_sweep_matches_oracle(case, dtype):
+    test_graph_shape_sweep_matches_oracle(case, dtype)
 
 
 @pytest.mark.parametrize("case,dtype", CASES[::2], ids=[c[0][0] for c in CASES[::2]])
